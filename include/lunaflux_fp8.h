@@ -1,0 +1,148 @@
+/*
+ * lunaflux_fp8.h - the FP8 projection path behind LunaFlux's kernel
+ * catalog: the weight-region format that model/device_materialize writes,
+ * the host-side pre-swizzle, the launch geometry a manifest records, and the
+ * gfx950 kernel entry points (symbols in lunaflux_fp8.hsaco) with their
+ * operand lists.
+ *
+ * Operand convention (kernels/launch_contract/paged_admit.mbt:76-107): every
+ * kernel parameter is a device region, in canonical order runtime inputs,
+ * semantic inputs (activation first, then weights in TensorRef order),
+ * outputs, workspace. No scalars cross (kernels/launch_contract/
+ * operands.mbt:1-13): the live row count M is read on the device from the
+ * StepCounts descriptor int32[5] = {prefill_rows, decode_rows, total_rows,
+ * query_tokens, page_entries} (engine/device_step/stage.mbt:59-68), element
+ * 3; N and K are read from the weight region header. The grid is sized for
+ * the profile's max_query_tokens (kernels/launch_contract/
+ * paged_profile.mbt:7-13) and blocks past the live M exit early.
+ */
+#ifndef LUNAFLUX_FP8_H
+#define LUNAFLUX_FP8_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* ---- weight region format ---------------------------------------------- */
+/*
+ * One weight TensorRef = one region (engine/execution_manifest_file/
+ * derive.mbt:163-173), laid out as
+ *   [256-byte header | E x tile block | E x scale block]
+ * Tile block of one expert: the [N, K] e4m3 matrix cut into 16 x 128 tiles,
+ * tile (nt, kt) at ((nt * K/128) + kt) * 2048. Inside a tile the bytes are in
+ * MFMA fragment order: half h (0, 1) holds 64 lanes x 16 bytes, and lane l's
+ * 16 bytes at h*1024 + l*16 are W[16 nt + l%16][128 kt + 32 (l/16) + 16 h +
+ * 0..15]. One wavefront therefore reads a tile with two fully coalesced 1 KiB
+ * loads and each lane ends up holding the 32 consecutive K values one
+ * operand of a 16x16x128 FP8 MFMA (or four 16x16x32 bf16 MFMAs) needs.
+ * Scale block of one expert (fp32, padded to 256 bytes):
+ *   LF_FP8_SCALE_PER_CHANNEL: s[N]
+ *   LF_FP8_SCALE_BLOCK128:    s[N/128][K/128]
+ * The dequantized weight is fp32(q) * s.
+ */
+#define LF_FP8_WEIGHT_MAGIC 0x5738464Cu /* bytes "LF8W" */
+#define LF_FP8_WEIGHT_VERSION 1u
+#define LF_FP8_HEADER_BYTES 256
+#define LF_FP8_TILE_ROWS 16
+#define LF_FP8_TILE_COLUMNS 128
+#define LF_FP8_TILE_BYTES 2048
+#define LF_FP8_LAYOUT_TILE16X128 1u
+
+enum lf_fp8_scale_mode {
+  LF_FP8_SCALE_PER_CHANNEL = 1,
+  LF_FP8_SCALE_BLOCK128 = 2
+};
+
+typedef struct lf_fp8_weight_header {
+  uint32_t magic;
+  uint32_t version;
+  uint32_t layout;
+  uint32_t scale_mode;
+  uint32_t rows;        /* N: output width */
+  uint32_t columns;     /* K: input width */
+  uint32_t experts;     /* 1 for a dense projection */
+  uint32_t reserved;
+  uint64_t tile_offset;     /* = LF_FP8_HEADER_BYTES */
+  uint64_t tile_bytes;      /* per expert: N * K */
+  uint64_t scale_offset;    /* = tile_offset + experts * tile_bytes */
+  uint64_t scale_bytes;     /* per expert, padded to 256 */
+  uint8_t padding[192];
+} lf_fp8_weight_header;
+
+/* Byte size of a weight region; LF_INVALID_ARGUMENT unless N % 16 == 0,
+ * K % 128 == 0 (and N % 128 == 0 for block scales), experts >= 1. */
+int32_t lunaflux_fp8_weight_region_bytes(int32_t scale_mode, int64_t rows,
+                                         int64_t columns, int32_t experts,
+                                         int64_t *byte_count);
+
+/* The pre-swizzle model/device_materialize applies per tensor
+ * (model/device_materialize/layout.mbt:37-93 places tensors; this fills one
+ * placed region). q: E x [N, K] row-major e4m3 codes; scales: E x the scale
+ * block above, unpadded. Writes the whole region (header included). */
+int32_t lunaflux_fp8_pack_weight(int32_t scale_mode, int64_t rows,
+                                 int64_t columns, int32_t experts,
+                                 const uint8_t *q, const float *scales,
+                                 uint8_t *region, int64_t region_bytes);
+/* Inverse of the pack (tests and tooling). */
+int32_t lunaflux_fp8_unpack_weight(const uint8_t *region, int64_t region_bytes,
+                                   uint8_t *q, int64_t q_bytes, float *scales,
+                                   int64_t scale_count);
+
+/* ---- kernel entry points ----------------------------------------------- */
+/*
+ * Families (one catalog AotKernelFamily each; kernels/catalog/entry.mbt:
+ * 161-219):
+ *  W8A16 ("decode"): bf16 activations, e4m3 weights dequantized to bf16 in
+ *    registers (exact), bf16 MFMA, fp32 accumulation, per-channel scale in
+ *    the epilogue. Split-K across the waves of a block; a block owns 16
+ *    output columns. Suffix _m16/_m32/_m64/_m128: the profile's largest M.
+ *  W8A8 ("prefill"): activations quantized per token to e4m3
+ *    (lf_fp8_act_quant_rows), e4m3 x e4m3 MFMA (16x16x128 f8f6f4), fp32
+ *    accumulation, row scale x channel scale epilogue. 128 x 128 block tile.
+ *
+ * Operands (all device regions, in order):
+ *  lf_fp8_act_quant_rows (counts, x, w, xq)   x bf16 [M, K] -> xq; K is read
+ *                                             from the header of w, the
+ *                                             first weight of the op the
+ *                                             quantizer feeds
+ *  *_dense     (counts, x, w, y)              y bf16 [M, N]
+ *  *_qkv       (counts, x, wq, wk, wv, y)     y bf16 [M, Nq+Nk+Nv] = Q|K|V
+ *  *_gate_up   (counts, x, wg, wu, h)         h bf16 [M, I],
+ *                                             h = silu(x Wg^T) * (x Wu^T)
+ * The W8A8 forms take xq (the quantizer's output) in place of x. xq layout:
+ * e4m3 codes [M, K] at offset 0, fp32 row scales at offset
+ * align256(M * K); its size for a profile is lunaflux_fp8_act_quant_bytes.
+ * GatedMlp (model/plan/plan.mbt:47-59) runs as gate_up into the workspace
+ * followed by dense(down) from it.
+ */
+#define LF_FP8_COUNTS_QUERY_TOKENS 3
+#define LF_FP8_COUNTS_BYTES 20
+#define LF_FP8_SYMBOL_BYTES 128
+
+int64_t lunaflux_fp8_act_quant_bytes(int64_t max_rows, int64_t columns);
+
+enum lf_fp8_entry {
+  LF_FP8_ENTRY_ACT_QUANT_ROWS = 1,
+  LF_FP8_ENTRY_W8A16_DENSE = 2,
+  LF_FP8_ENTRY_W8A16_QKV = 3,
+  LF_FP8_ENTRY_W8A16_GATE_UP = 4,
+  LF_FP8_ENTRY_W8A8_DENSE = 5,
+  LF_FP8_ENTRY_W8A8_QKV = 6,
+  LF_FP8_ENTRY_W8A8_GATE_UP = 7
+};
+
+/* Launch geometry a manifest records for (entry, output width N, input width
+ * K, profile max_query_tokens): grid xyz, block xyz, dynamic LDS bytes and
+ * the symbol to load (NUL-terminated, <= 128 bytes). For _QKV, N is the
+ * packed width Nq + Nk + Nv; for _GATE_UP, N is the intermediate width I. */
+int32_t lunaflux_fp8_launch_geometry(int32_t entry, int64_t n, int64_t k,
+                                     int32_t max_tokens, int32_t dims[7],
+                                     char symbol[LF_FP8_SYMBOL_BYTES]);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif

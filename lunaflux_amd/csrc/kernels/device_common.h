@@ -1,0 +1,100 @@
+// device_common.h - gfx950 device helpers shared by the FP8 kernels:
+// vector types for the MFMA operands, the weight-region header as the device
+// sees it, bf16 / e4m3 conversions, and wavefront reductions.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef int i32x8 __attribute__((ext_vector_type(8)));
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+
+#define LF_DEVICE __device__ __forceinline__
+
+// Mirror of lf_fp8_weight_header (include/lunaflux_fp8.h); only the fields
+// the kernels read.
+struct WeightHeader {
+  uint32_t magic, version, layout, scale_mode;
+  uint32_t rows, columns, experts, reserved;
+  uint64_t tile_offset, tile_bytes, scale_offset, scale_bytes;
+};
+
+constexpr uint32_t kWeightMagic = 0x5738464Cu;
+constexpr int kTileBytes = 2048;
+constexpr int kQueryTokensIndex = 3;
+
+LF_DEVICE const WeightHeader &header_of(const uint8_t *region) {
+  return *reinterpret_cast<const WeightHeader *>(region);
+}
+
+LF_DEVICE const uint8_t *expert_tiles(const uint8_t *region, int expert) {
+  const WeightHeader &h = header_of(region);
+  return region + h.tile_offset + static_cast<uint64_t>(expert) * h.tile_bytes;
+}
+
+LF_DEVICE const float *expert_scales(const uint8_t *region, int expert) {
+  const WeightHeader &h = header_of(region);
+  return reinterpret_cast<const float *>(region + h.scale_offset +
+                                         static_cast<uint64_t>(expert) * h.scale_bytes);
+}
+
+LF_DEVICE int live_rows(const int32_t *counts, int capacity) {
+  int m = counts[kQueryTokensIndex];
+  m = m < 0 ? 0 : m;
+  return m > capacity ? capacity : m;
+}
+
+LF_DEVICE uint64_t align256(uint64_t v) { return (v + 255u) & ~uint64_t(255); }
+
+LF_DEVICE float bf16_to_f32(uint32_t bits16) { return __uint_as_float(bits16 << 16); }
+
+// fp32 -> bf16, round to nearest even (finite inputs; NaN stays NaN).
+LF_DEVICE uint32_t f32_to_bf16(float v) {
+  uint32_t u = __float_as_uint(v);
+  if ((u & 0x7fffffffu) > 0x7f800000u) return (u >> 16) | 0x40u;
+  u += 0x7fffu + ((u >> 16) & 1u);
+  return u >> 16;
+}
+
+// OCP E4M3 (bias 7, max 448, no infinities) encode with round to nearest
+// even and saturation to +-448, bit-identical to the host quantizer: the
+// same branch structure and only exact or correctly rounded fp32 operations.
+LF_DEVICE uint32_t e4m3_encode(float value) {
+  uint32_t u = __float_as_uint(value);
+  uint32_t sign = (u >> 24) & 0x80u;
+  uint32_t a = u & 0x7fffffffu;
+  if (a > 0x7f800000u) return sign | 0x7fu;
+  if (a >= 0x43e00000u) return sign | 0x7eu;
+  if (a < 0x3c800000u) {
+    float m = __uint_as_float(a) * 512.0f;  // exact
+    return sign | static_cast<uint32_t>(__builtin_rintf(m));
+  }
+  uint32_t r = a + 0x7ffffu + ((a >> 20) & 1u);
+  r &= 0xfff00000u;
+  uint32_t exponent = (r >> 23) - 120u;  // (e - 127) + 7
+  return sign | (exponent << 3) | ((r >> 20) & 7u);
+}
+
+// Four e4m3 codes (one 32-bit word) -> four bf16 values (two words). The
+// conversion is exact: every e4m3 value is a bf16 value.
+LF_DEVICE void e4m3x4_to_bf16x4(uint32_t word, uint32_t &lo, uint32_t &hi) {
+  bf16x2 a = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(static_cast<int>(word), 1.0f, false);
+  bf16x2 b = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(static_cast<int>(word), 1.0f, true);
+  lo = __builtin_bit_cast(uint32_t, a);
+  hi = __builtin_bit_cast(uint32_t, b);
+}
+
+LF_DEVICE float wave_max(float v) {
+#pragma unroll
+  for (int offset = 32; offset > 0; offset >>= 1) v = fmaxf(v, __shfl_xor(v, offset));
+  return v;
+}
+
+LF_DEVICE float silu_mul(float g, float u) {
+  float denominator = 1.0f + expf(-g);
+  float s = g / denominator;
+  return s * u;
+}

@@ -1,0 +1,3 @@
+// lunaflux_fp8.hip - the one translation unit of the gfx950 code object
+// lunaflux_fp8.hsaco (hipcc --genco --offload-arch=gfx950).
+#include "projection.hip"

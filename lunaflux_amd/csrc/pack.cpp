@@ -1,0 +1,207 @@
+// pack.cpp - host side of include/lunaflux_fp8.h: the weight-region format
+// (header + MFMA-fragment-ordered tiles + fp32 scales), its inverse, and the
+// launch geometry of every kernel entry point. No device code here.
+#include "lunaflux_fp8.h"
+#include "lunaflux_hip.h"
+
+#include <cstdio>
+#include <cstring>
+
+namespace {
+
+constexpr int64_t kMaxDim = int64_t(1) << 30;
+
+int64_t align_up(int64_t v, int64_t a) { return (v + a - 1) / a * a; }
+
+int64_t scale_count(int32_t mode, int64_t rows, int64_t columns) {
+  return mode == LF_FP8_SCALE_PER_CHANNEL ? rows : (rows / 128) * (columns / 128);
+}
+
+bool shape_ok(int32_t mode, int64_t rows, int64_t columns, int32_t experts) {
+  if (rows <= 0 || columns <= 0 || experts <= 0 || rows > kMaxDim ||
+      columns > kMaxDim || experts > 4096) {
+    return false;
+  }
+  if (rows % LF_FP8_TILE_ROWS != 0 || columns % LF_FP8_TILE_COLUMNS != 0) return false;
+  if (mode == LF_FP8_SCALE_BLOCK128) return rows % 128 == 0;
+  return mode == LF_FP8_SCALE_PER_CHANNEL;
+}
+
+void fill_header(lf_fp8_weight_header *h, int32_t mode, int64_t rows,
+                 int64_t columns, int32_t experts) {
+  std::memset(h, 0, sizeof(*h));
+  h->magic = LF_FP8_WEIGHT_MAGIC;
+  h->version = LF_FP8_WEIGHT_VERSION;
+  h->layout = LF_FP8_LAYOUT_TILE16X128;
+  h->scale_mode = static_cast<uint32_t>(mode);
+  h->rows = static_cast<uint32_t>(rows);
+  h->columns = static_cast<uint32_t>(columns);
+  h->experts = static_cast<uint32_t>(experts);
+  h->tile_offset = LF_FP8_HEADER_BYTES;
+  h->tile_bytes = static_cast<uint64_t>(rows * columns);
+  h->scale_offset = h->tile_offset + h->tile_bytes * static_cast<uint64_t>(experts);
+  h->scale_bytes = static_cast<uint64_t>(align_up(scale_count(mode, rows, columns) * 4, 256));
+}
+
+// Byte offset, inside one expert's tile block, of W[n][k].
+inline int64_t swizzled_offset(int64_t n, int64_t k, int64_t columns) {
+  int64_t nt = n / 16, r = n % 16;
+  int64_t kt = k / 128, kk = k % 128;
+  int64_t g = kk / 32, h = (kk % 32) / 16, b = kk % 16;
+  int64_t lane = g * 16 + r;
+  return (nt * (columns / 128) + kt) * LF_FP8_TILE_BYTES + h * 1024 + lane * 16 + b;
+}
+
+}  // namespace
+
+static_assert(sizeof(lf_fp8_weight_header) == LF_FP8_HEADER_BYTES, "header size");
+
+extern "C" {
+
+int32_t lunaflux_fp8_weight_region_bytes(int32_t scale_mode, int64_t rows,
+                                         int64_t columns, int32_t experts,
+                                         int64_t *byte_count) {
+  if (byte_count == nullptr || !shape_ok(scale_mode, rows, columns, experts)) {
+    return LF_INVALID_ARGUMENT;
+  }
+  lf_fp8_weight_header h;
+  fill_header(&h, scale_mode, rows, columns, experts);
+  *byte_count = static_cast<int64_t>(h.scale_offset + h.scale_bytes * static_cast<uint64_t>(experts));
+  return LF_OK;
+}
+
+int32_t lunaflux_fp8_pack_weight(int32_t scale_mode, int64_t rows,
+                                 int64_t columns, int32_t experts,
+                                 const uint8_t *q, const float *scales,
+                                 uint8_t *region, int64_t region_bytes) {
+  int64_t need = 0;
+  int32_t st = lunaflux_fp8_weight_region_bytes(scale_mode, rows, columns, experts, &need);
+  if (st != LF_OK) return st;
+  if (q == nullptr || scales == nullptr || region == nullptr || region_bytes != need) {
+    return LF_INVALID_ARGUMENT;
+  }
+  lf_fp8_weight_header h;
+  fill_header(&h, scale_mode, rows, columns, experts);
+  std::memset(region, 0, static_cast<size_t>(region_bytes));
+  std::memcpy(region, &h, sizeof(h));
+  int64_t sc = scale_count(scale_mode, rows, columns);
+  for (int32_t e = 0; e < experts; e += 1) {
+    const uint8_t *qe = q + e * rows * columns;
+    uint8_t *te = region + h.tile_offset + static_cast<uint64_t>(e) * h.tile_bytes;
+    for (int64_t n = 0; n < rows; n += 1) {
+      for (int64_t k0 = 0; k0 < columns; k0 += 16) {
+        // 16 consecutive k stay contiguous in the swizzled order.
+        std::memcpy(te + swizzled_offset(n, k0, columns), qe + n * columns + k0, 16);
+      }
+    }
+    std::memcpy(region + h.scale_offset + static_cast<uint64_t>(e) * h.scale_bytes,
+                scales + e * sc, static_cast<size_t>(sc) * sizeof(float));
+  }
+  return LF_OK;
+}
+
+int32_t lunaflux_fp8_unpack_weight(const uint8_t *region, int64_t region_bytes,
+                                   uint8_t *q, int64_t q_bytes, float *scales,
+                                   int64_t scale_count_arg) {
+  if (region == nullptr || region_bytes < LF_FP8_HEADER_BYTES) return LF_INVALID_ARGUMENT;
+  lf_fp8_weight_header h;
+  std::memcpy(&h, region, sizeof(h));
+  if (h.magic != LF_FP8_WEIGHT_MAGIC || h.version != LF_FP8_WEIGHT_VERSION ||
+      h.layout != LF_FP8_LAYOUT_TILE16X128) {
+    return LF_INVALID_ARGUMENT;
+  }
+  int32_t mode = static_cast<int32_t>(h.scale_mode);
+  int64_t rows = h.rows, columns = h.columns;
+  int32_t experts = static_cast<int32_t>(h.experts);
+  int64_t need = 0;
+  if (lunaflux_fp8_weight_region_bytes(mode, rows, columns, experts, &need) != LF_OK ||
+      need != region_bytes) {
+    return LF_INVALID_ARGUMENT;
+  }
+  int64_t sc = scale_count(mode, rows, columns);
+  if (q == nullptr || scales == nullptr || q_bytes != experts * rows * columns ||
+      scale_count_arg != experts * sc) {
+    return LF_INVALID_ARGUMENT;
+  }
+  for (int32_t e = 0; e < experts; e += 1) {
+    uint8_t *qe = q + e * rows * columns;
+    const uint8_t *te = region + h.tile_offset + static_cast<uint64_t>(e) * h.tile_bytes;
+    for (int64_t n = 0; n < rows; n += 1) {
+      for (int64_t k0 = 0; k0 < columns; k0 += 16) {
+        std::memcpy(qe + n * columns + k0, te + swizzled_offset(n, k0, columns), 16);
+      }
+    }
+    std::memcpy(scales + e * sc,
+                region + h.scale_offset + static_cast<uint64_t>(e) * h.scale_bytes,
+                static_cast<size_t>(sc) * sizeof(float));
+  }
+  return LF_OK;
+}
+
+int64_t lunaflux_fp8_act_quant_bytes(int64_t max_rows, int64_t columns) {
+  if (max_rows <= 0 || columns <= 0 || max_rows > kMaxDim || columns > kMaxDim) return -1;
+  return align_up(max_rows * columns, 256) + align_up(max_rows * 4, 256);
+}
+
+int32_t lunaflux_fp8_launch_geometry(int32_t entry, int64_t n, int64_t k,
+                                     int32_t max_tokens, int32_t dims[7],
+                                     char symbol[LF_FP8_SYMBOL_BYTES]) {
+  if (dims == nullptr || symbol == nullptr || n <= 0 || k <= 0 ||
+      max_tokens <= 0 || n > kMaxDim || k > kMaxDim || k % 128 != 0) {
+    return LF_INVALID_ARGUMENT;
+  }
+  int32_t gx = 1, gy = 1, bx = 256;
+  const char *name = nullptr;
+  char buffer[LF_FP8_SYMBOL_BYTES];
+  switch (entry) {
+    case LF_FP8_ENTRY_ACT_QUANT_ROWS:
+      name = "lf_fp8_act_quant_rows";
+      gx = max_tokens;
+      bx = 256;
+      break;
+    case LF_FP8_ENTRY_W8A16_DENSE:
+    case LF_FP8_ENTRY_W8A16_QKV:
+    case LF_FP8_ENTRY_W8A16_GATE_UP: {
+      if (n % 16 != 0 || max_tokens > 128) return LF_INVALID_ARGUMENT;
+      int32_t m = max_tokens <= 16 ? 16 : max_tokens <= 32 ? 32 : max_tokens <= 64 ? 64 : 128;
+      const char *op = entry == LF_FP8_ENTRY_W8A16_DENSE ? "dense"
+                       : entry == LF_FP8_ENTRY_W8A16_QKV ? "qkv"
+                                                         : "gate_up";
+      std::snprintf(buffer, sizeof(buffer), "lf_fp8_w8a16_%s_m%d", op, m);
+      name = buffer;
+      gx = static_cast<int32_t>(n / 16);
+      bx = 512;
+      break;
+    }
+    case LF_FP8_ENTRY_W8A8_DENSE:
+    case LF_FP8_ENTRY_W8A8_QKV:
+      if (n % 128 != 0) return LF_INVALID_ARGUMENT;
+      name = entry == LF_FP8_ENTRY_W8A8_DENSE ? "lf_fp8_w8a8_dense" : "lf_fp8_w8a8_qkv";
+      gx = static_cast<int32_t>(n / 128);
+      gy = (max_tokens + 127) / 128;
+      bx = 256;
+      break;
+    case LF_FP8_ENTRY_W8A8_GATE_UP:
+      if (n % 64 != 0) return LF_INVALID_ARGUMENT;
+      name = "lf_fp8_w8a8_gate_up";
+      gx = static_cast<int32_t>(n / 64);
+      gy = (max_tokens + 127) / 128;
+      bx = 256;
+      break;
+    default:
+      return LF_INVALID_ARGUMENT;
+  }
+  if (gy > LF_MAX_GRID_YZ) return LF_INVALID_ARGUMENT;
+  dims[0] = gx;
+  dims[1] = gy;
+  dims[2] = 1;
+  dims[3] = bx;
+  dims[4] = 1;
+  dims[5] = 1;
+  dims[6] = 0;
+  std::memset(symbol, 0, LF_FP8_SYMBOL_BYTES);
+  std::strncpy(symbol, name, LF_FP8_SYMBOL_BYTES - 1);
+  return LF_OK;
+}
+
+}  // extern "C"

@@ -1,0 +1,321 @@
+"""Host side of the FP8 projection path.
+
+The reference executes each plan operation as one AOT entry point with a
+prebuilt operand list (kernels/launch_contract/paged_admit.mbt:76-107,
+engine/device_step/paged_executor_run.mbt:112-143). This module builds those
+launch steps for the FP8 families and offers numpy-level calls named after
+the reference kernels they replace (kernels/reference/basic.mbt:102-153,
+mlp.mbt:4-39), so parity tests read like the reference's own tests:
+
+  dense_projection(x, w)          output / down / LM-head projection
+  qkv_projection(x, wq, wk, wv)   packed Q|K|V
+  gate_up_swiglu(x, wg, wu)       silu(x Wg^T) * (x Wu^T), the first half of
+                                  silu_gated_mlp
+  silu_gated_mlp(x, wg, wu, wd)   the whole GatedMlp operation
+
+Two families (include/lunaflux_fp8.h): "w8a16" (bf16 activations, decode)
+and "w8a8" (per-token e4m3 activations, prefill). Activations and outputs
+are bf16 carried as uint16 bit patterns.
+"""
+from __future__ import annotations
+
+import ctypes
+from dataclasses import dataclass, field
+
+import numpy as np
+
+from . import _abi
+from .device import (Allocation, DeviceError, Function, KernelArgument, KernelArguments,
+                     KernelLaunchDimensions, Stream, open_context)
+
+FAMILIES = ("w8a16", "w8a8")
+PER_CHANNEL = _abi.LF_FP8_SCALE_PER_CHANNEL
+BLOCK128 = _abi.LF_FP8_SCALE_BLOCK128
+W8A16_MAX_TOKENS = 128
+COUNTS_BYTES = 20
+
+
+def _check(operation, status):
+    if status != _abi.LF_OK:
+        raise DeviceError(operation, status)
+
+
+def weight_region_bytes(rows: int, columns: int, experts: int = 1,
+                        scale_mode: int = PER_CHANNEL) -> int:
+    out = ctypes.c_int64(0)
+    _check("weight_region_bytes", _abi.lib().lunaflux_fp8_weight_region_bytes(
+        scale_mode, rows, columns, experts, ctypes.byref(out)))
+    return out.value
+
+
+def pack_weight(q: np.ndarray, scales: np.ndarray, scale_mode: int = PER_CHANNEL) -> np.ndarray:
+    """Pre-swizzles e4m3 codes [N, K] (or [E, N, K]) and their fp32 scales
+    into one weight region (header + MFMA-order tiles + scales)."""
+    q = np.ascontiguousarray(q, np.uint8)
+    if q.ndim == 2:
+        q = q[None]
+    experts, rows, columns = q.shape
+    scales = np.ascontiguousarray(scales, np.float32)
+    size = weight_region_bytes(rows, columns, experts, scale_mode)
+    region = np.empty(size, np.uint8)
+    _check("pack_weight", _abi.lib().lunaflux_fp8_pack_weight(
+        scale_mode, rows, columns, experts,
+        q.ctypes.data_as(ctypes.POINTER(ctypes.c_uint8)),
+        scales.ctypes.data_as(ctypes.POINTER(ctypes.c_float)),
+        region.ctypes.data_as(ctypes.POINTER(ctypes.c_uint8)), size))
+    return region
+
+
+def unpack_weight(region: np.ndarray):
+    """Inverse of pack_weight: (q [E, N, K], scales, header fields)."""
+    region = np.ascontiguousarray(region, np.uint8)
+    head = region[:32].view(np.uint32)
+    scale_mode, rows, columns, experts = int(head[3]), int(head[4]), int(head[5]), int(head[6])
+    per = rows if scale_mode == PER_CHANNEL else (rows // 128) * (columns // 128)
+    q = np.empty((experts, rows, columns), np.uint8)
+    s = np.empty(experts * per, np.float32)
+    _check("unpack_weight", _abi.lib().lunaflux_fp8_unpack_weight(
+        region.ctypes.data_as(ctypes.POINTER(ctypes.c_uint8)), region.size,
+        q.ctypes.data_as(ctypes.POINTER(ctypes.c_uint8)), q.size,
+        s.ctypes.data_as(ctypes.POINTER(ctypes.c_float)), s.size))
+    return q, s.reshape(experts, -1), dict(scale_mode=scale_mode, rows=rows, columns=columns,
+                                           experts=experts)
+
+
+def act_quant_bytes(max_rows: int, columns: int) -> int:
+    n = _abi.lib().lunaflux_fp8_act_quant_bytes(max_rows, columns)
+    if n < 0:
+        raise DeviceError("act_quant_bytes", _abi.LF_INVALID_ARGUMENT)
+    return n
+
+
+def launch_geometry(entry: int, n: int, k: int, max_tokens: int):
+    dims = (ctypes.c_int32 * 7)()
+    symbol = ctypes.create_string_buffer(128)
+    _check("launch_geometry", _abi.lib().lunaflux_fp8_launch_geometry(
+        entry, n, k, max_tokens, dims, symbol))
+    return (KernelLaunchDimensions.new(tuple(dims[0:3]), tuple(dims[3:6]), dims[6]),
+            symbol.value.decode("ascii"))
+
+
+@dataclass
+class Fp8Weight:
+    """One device-resident weight region (a TensorRef's region)."""
+
+    allocation: Allocation
+    rows: int
+    columns: int
+    experts: int
+    scale_mode: int
+
+    @property
+    def region(self) -> KernelArgument:
+        return KernelArgument.device_region(self.allocation, 0, self.allocation.byte_count, 256)
+
+
+@dataclass
+class LaunchStep:
+    """One kernel launch of a plan operation: function, geometry, operands."""
+
+    function: Function
+    dims: KernelLaunchDimensions
+    args: KernelArguments
+    name: str = ""
+
+    def launch(self, stream: Stream, synchronous: bool = True):
+        if synchronous:
+            self.function.launch_synchronous(self.dims, self.args, stream)
+        else:
+            self.function.launch_async(self.dims, self.args, stream)
+
+
+@dataclass
+class BoundOperation:
+    """A plan operation bound to its regions: one or more launch steps run
+    in order on one stream."""
+
+    steps: list
+    workspace: Allocation | None = None
+    keep: list = field(default_factory=list)
+
+    def launch(self, stream: Stream, synchronous: bool = True):
+        for i, step in enumerate(self.steps):
+            step.launch(stream, synchronous and i == len(self.steps) - 1)
+
+
+def _region(alloc: Allocation, byte_count: int | None = None, offset: int = 0,
+            alignment: int = 16) -> KernelArgument:
+    n = alloc.byte_count - offset if byte_count is None else byte_count
+    return KernelArgument.device_region(alloc, offset, n, alignment)
+
+
+class ProjectionRuntime:
+    """A device context with the FP8 code object loaded."""
+
+    def __init__(self, ordinal: int = 0):
+        self.context = open_context(ordinal)
+        self.stream = self.context.create_stream()
+        self.module = self.context.load_module(_abi.code_object_bytes())
+        self._functions = {}
+
+    # -- resources ---------------------------------------------------------
+    def function(self, symbol: str) -> Function:
+        fn = self._functions.get(symbol)
+        if fn is None:
+            fn = self.module.load_function(symbol)
+            self._functions[symbol] = fn
+        return fn
+
+    def upload_weight(self, q: np.ndarray, scales: np.ndarray,
+                      scale_mode: int = PER_CHANNEL) -> Fp8Weight:
+        region = pack_weight(q, scales, scale_mode)
+        q3 = q if q.ndim == 3 else q[None]
+        return Fp8Weight(self.context.upload(region), q3.shape[1], q3.shape[2], q3.shape[0],
+                         scale_mode)
+
+    def weight_from_region(self, region: np.ndarray) -> Fp8Weight:
+        head = np.ascontiguousarray(region[:32]).view(np.uint32)
+        return Fp8Weight(self.context.upload(region), int(head[4]), int(head[5]), int(head[6]),
+                         int(head[3]))
+
+    def step_counts(self, query_tokens: int, decode: bool = True) -> Allocation:
+        """StepCounts int32[5] = {prefill_rows, decode_rows, total_rows,
+        query_tokens, page_entries} (engine/device_step/stage.mbt:59-68)."""
+        rows = query_tokens
+        counts = np.array([0 if decode else 1, rows if decode else 0, rows if decode else 1,
+                           query_tokens, 0], np.int32)
+        return self.context.upload(counts)
+
+    def _step(self, entry: int, n: int, k: int, max_tokens: int, operands) -> LaunchStep:
+        dims, symbol = launch_geometry(entry, n, k, max_tokens)
+        return LaunchStep(self.function(symbol), dims, KernelArguments(operands), symbol)
+
+    # -- binding plan operations to launch steps ---------------------------
+    def bind_act_quant(self, counts: Allocation, x: KernelArgument, w: Fp8Weight,
+                       xq: KernelArgument, max_tokens: int) -> LaunchStep:
+        return self._step(_abi.ENTRY_ACT_QUANT_ROWS, w.rows, w.columns, max_tokens,
+                          [_region(counts, COUNTS_BYTES, alignment=4), x, w.region, xq])
+
+    def bind_dense(self, family: str, counts: Allocation, x: KernelArgument, w: Fp8Weight,
+                   y: KernelArgument, max_tokens: int) -> BoundOperation:
+        _family(family, max_tokens)
+        c = _region(counts, COUNTS_BYTES, alignment=4)
+        if family == "w8a16":
+            return BoundOperation([self._step(_abi.ENTRY_W8A16_DENSE, w.rows, w.columns,
+                                              max_tokens, [c, x, w.region, y])])
+        ws = self.context.allocate(act_quant_bytes(max_tokens, w.columns))
+        xq = _region(ws, alignment=256)
+        return BoundOperation([
+            self.bind_act_quant(counts, x, w, xq, max_tokens),
+            self._step(_abi.ENTRY_W8A8_DENSE, w.rows, w.columns, max_tokens, [c, xq, w.region, y]),
+        ], workspace=ws)
+
+    def bind_qkv(self, family: str, counts: Allocation, x: KernelArgument, wq: Fp8Weight,
+                 wk: Fp8Weight, wv: Fp8Weight, y: KernelArgument, max_tokens: int) -> BoundOperation:
+        _family(family, max_tokens)
+        if not (wq.columns == wk.columns == wv.columns) or wk.rows != wv.rows:
+            raise DeviceError("qkv shapes", _abi.LF_INVALID_ARGUMENT)
+        n = wq.rows + wk.rows + wv.rows
+        c = _region(counts, COUNTS_BYTES, alignment=4)
+        if family == "w8a16":
+            return BoundOperation([self._step(_abi.ENTRY_W8A16_QKV, n, wq.columns, max_tokens,
+                                              [c, x, wq.region, wk.region, wv.region, y])])
+        ws = self.context.allocate(act_quant_bytes(max_tokens, wq.columns))
+        xq = _region(ws, alignment=256)
+        return BoundOperation([
+            self.bind_act_quant(counts, x, wq, xq, max_tokens),
+            self._step(_abi.ENTRY_W8A8_QKV, n, wq.columns, max_tokens,
+                       [c, xq, wq.region, wk.region, wv.region, y]),
+        ], workspace=ws)
+
+    def bind_gate_up(self, family: str, counts: Allocation, x: KernelArgument, wg: Fp8Weight,
+                     wu: Fp8Weight, h: KernelArgument, max_tokens: int) -> BoundOperation:
+        _family(family, max_tokens)
+        if wg.rows != wu.rows or wg.columns != wu.columns:
+            raise DeviceError("gate/up shapes", _abi.LF_INVALID_ARGUMENT)
+        c = _region(counts, COUNTS_BYTES, alignment=4)
+        if family == "w8a16":
+            return BoundOperation([self._step(_abi.ENTRY_W8A16_GATE_UP, wg.rows, wg.columns,
+                                              max_tokens, [c, x, wg.region, wu.region, h])])
+        ws = self.context.allocate(act_quant_bytes(max_tokens, wg.columns))
+        xq = _region(ws, alignment=256)
+        return BoundOperation([
+            self.bind_act_quant(counts, x, wg, xq, max_tokens),
+            self._step(_abi.ENTRY_W8A8_GATE_UP, wg.rows, wg.columns, max_tokens,
+                       [c, xq, wg.region, wu.region, h]),
+        ], workspace=ws)
+
+    def bind_gated_mlp(self, family: str, counts: Allocation, x: KernelArgument, wg: Fp8Weight,
+                       wu: Fp8Weight, wd: Fp8Weight, y: KernelArgument,
+                       max_tokens: int) -> BoundOperation:
+        """GatedMlp (model/plan/plan.mbt:47-59): gate/up + SwiGLU into a bf16
+        intermediate in the workspace, then the down projection from it."""
+        if wd.columns != wg.rows or wd.rows != wg.columns:
+            raise DeviceError("mlp shapes", _abi.LF_INVALID_ARGUMENT)
+        h_bytes = max_tokens * wg.rows * 2
+        h_alloc = self.context.allocate(h_bytes)
+        h = _region(h_alloc, h_bytes, alignment=256)
+        first = self.bind_gate_up(family, counts, x, wg, wu, h, max_tokens)
+        second = self.bind_dense(family, counts, h, wd, y, max_tokens)
+        return BoundOperation(first.steps + second.steps, workspace=h_alloc,
+                              keep=[first.workspace, second.workspace])
+
+    # -- numpy convenience (tests, smoke) -----------------------------------
+    def _run(self, bind, x: np.ndarray, out_shape, max_tokens):
+        x = np.ascontiguousarray(x, np.uint16)
+        m = x.shape[0]
+        max_tokens = max(m, 1) if max_tokens is None else max_tokens
+        if m > max_tokens:
+            raise DeviceError("rows exceed the profile's max_query_tokens", _abi.LF_INVALID_ARGUMENT)
+        # Inputs and outputs are sized for the profile (max_tokens rows), as
+        # the engine's activation regions are.
+        xa = self.context.allocate(max(max_tokens * x.shape[1] * 2, 16))
+        xa.copy_from_host(x)
+        out_bytes = max_tokens * out_shape[1] * 2
+        ya = self.context.allocate(out_bytes)
+        counts = self.step_counts(m)
+        op = bind(counts, _region(xa, alignment=256), _region(ya, alignment=256), max_tokens)
+        op.launch(self.stream, synchronous=True)
+        return ya.read(np.uint16, out_shape) if m else np.zeros(out_shape, np.uint16)
+
+    def dense_projection(self, x, w: Fp8Weight, family="w8a16", max_tokens=None):
+        return self._run(lambda c, xr, yr, mt: self.bind_dense(family, c, xr, w, yr, mt),
+                         x, (x.shape[0], w.rows), max_tokens)
+
+    def qkv_projection(self, x, wq, wk, wv, family="w8a16", max_tokens=None):
+        n = wq.rows + wk.rows + wv.rows
+        return self._run(lambda c, xr, yr, mt: self.bind_qkv(family, c, xr, wq, wk, wv, yr, mt),
+                         x, (x.shape[0], n), max_tokens)
+
+    def gate_up_swiglu(self, x, wg, wu, family="w8a16", max_tokens=None):
+        return self._run(lambda c, xr, yr, mt: self.bind_gate_up(family, c, xr, wg, wu, yr, mt),
+                         x, (x.shape[0], wg.rows), max_tokens)
+
+    def silu_gated_mlp(self, x, wg, wu, wd, family="w8a16", max_tokens=None):
+        return self._run(lambda c, xr, yr, mt: self.bind_gated_mlp(family, c, xr, wg, wu, wd, yr, mt),
+                         x, (x.shape[0], wd.rows), max_tokens)
+
+    def act_quant(self, x, w: Fp8Weight, max_tokens=None):
+        """Runs only the per-token quantizer: (codes [M, K], scales [M])."""
+        x = np.ascontiguousarray(x, np.uint16)
+        m, k = x.shape
+        max_tokens = max(m, 1) if max_tokens is None else max_tokens
+        xa = self.context.allocate(max_tokens * k * 2)
+        xa.copy_from_host(x)
+        ws = self.context.allocate(act_quant_bytes(max_tokens, k))
+        counts = self.step_counts(m)
+        step = self.bind_act_quant(counts, _region(xa, alignment=256), w,
+                                   _region(ws, alignment=256), max_tokens)
+        step.launch(self.stream, synchronous=True)
+        codes = ws.read(np.uint8, (m, k))
+        off = (m * k + 255) // 256 * 256
+        return codes, ws.read(np.float32, (m,), offset=off)
+
+
+def _family(family: str, max_tokens: int):
+    if family not in FAMILIES:
+        raise ValueError(f"unknown family {family!r}; expected one of {FAMILIES}")
+    if max_tokens <= 0:
+        raise DeviceError("max_tokens", _abi.LF_INVALID_ARGUMENT)
+    if family == "w8a16" and max_tokens > W8A16_MAX_TOKENS:
+        raise DeviceError("w8a16 supports at most 128 rows", _abi.LF_INVALID_ARGUMENT)

@@ -170,6 +170,10 @@ float lfo_silu_mul(float g, float u) {
   return s * u;
 }
 
+void lfo_silu_mul_array(const float *g, const float *u, int64_t n, float *out) {
+  for (int64_t i = 0; i < n; i += 1) out[i] = lfo_silu_mul(g[i], u[i]);
+}
+
 /* kernels/reference/mlp.mbt:4-39 */
 int32_t lfo_silu_gated_mlp(const float *x, int32_t rows, int32_t hidden,
                            const float *wg, const float *wu, int32_t inter,

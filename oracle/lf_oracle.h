@@ -93,6 +93,8 @@ int32_t lfo_silu_gated_mlp(const float *x, int32_t rows, int32_t hidden,
                            float *out);
 /* SiLU product for one element: g / (1 + expf(-g)) * u (mlp.mbt:30). */
 float lfo_silu_mul(float g, float u);
+/* out[i] = lfo_silu_mul(g[i], u[i]) for i < n. */
+void lfo_silu_mul_array(const float *g, const float *u, int64_t n, float *out);
 
 /* ---- Part 2: formats and quantizers ------------------------------------ */
 

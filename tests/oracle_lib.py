@@ -31,7 +31,9 @@ class Limits(ctypes.Structure):
 
 
 def _load():
-    if not os.path.exists(LIB_PATH):
+    sources = [os.path.join(ORACLE_DIR, f) for f in ("lf_oracle.c", "lf_oracle.h")]
+    if not os.path.exists(LIB_PATH) or any(
+            os.path.getmtime(f) > os.path.getmtime(LIB_PATH) for f in sources if os.path.exists(f)):
         subprocess.run(["make", "-s", "-C", ORACLE_DIR], check=True)
     lib = ctypes.CDLL(LIB_PATH)
     sig = {
@@ -45,6 +47,7 @@ def _load():
         "lfo_silu_gated_mlp": (_i32, [_f32p, _i32, _i32, _f32p, _f32p, _i32, _f32p, _i32,
                                       ctypes.POINTER(Limits), _f32p, _f32p]),
         "lfo_silu_mul": (ctypes.c_float, [ctypes.c_float, ctypes.c_float]),
+        "lfo_silu_mul_array": (None, [_f32p, _f32p, _i64, _f32p]),
         "lfo_bf16_rne": (ctypes.c_uint16, [ctypes.c_float]),
         "lfo_bf16_to_f32": (ctypes.c_float, [ctypes.c_uint16]),
         "lfo_bf16_round_array": (None, [_f32p, _i64, _u16p]),
@@ -154,6 +157,15 @@ def silu_gated_mlp(x, wg, wu, wd, round_hidden_bf16=False, lim=None, return_hidd
 
 def silu_mul(g: float, u: float) -> float:
     return LIB.lfo_silu_mul(g, u)
+
+
+def silu_mul_array(g: np.ndarray, u: np.ndarray) -> np.ndarray:
+    g = np.ascontiguousarray(g, np.float32)
+    u = np.ascontiguousarray(u, np.float32)
+    assert g.shape == u.shape
+    out = np.zeros(g.shape, np.float32)
+    LIB.lfo_silu_mul_array(_p(g, _f32p), _p(u, _f32p), g.size, _p(out, _f32p))
+    return out
 
 
 def bf16_round(a: np.ndarray) -> np.ndarray:

@@ -1,0 +1,162 @@
+"""CPU tests of the C-ABI library: it loads, exports every function the
+headers declare, and its host-side pieces (weight pre-swizzle, region sizes,
+launch geometry, argument validation) behave as documented. No kernel runs.
+"""
+import ctypes
+import os
+import re
+
+import numpy as np
+import pytest
+
+import oracle_lib as o
+from lunaflux_amd import _abi, fp8, synth
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+
+
+def declared_functions():
+    names = set()
+    for header in ("lunaflux_hip.h", "lunaflux_fp8.h"):
+        text = open(os.path.join(ROOT, "include", header)).read()
+        text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+        names |= set(re.findall(r"\b(lunaflux_\w+)\s*\(", text))
+    return sorted(names)
+
+
+def test_library_exports_every_declared_symbol():
+    lib = ctypes.CDLL(_abi.LIBRARY_PATH)
+    names = declared_functions()
+    assert len(names) >= 38
+    missing = [n for n in names if not hasattr(lib, n)]
+    assert not missing
+    # and the Python binding declares each of them
+    assert set(names) == set(_abi.SIGNATURES)
+
+
+def test_code_object_has_every_entry_point():
+    image = _abi.code_object_bytes()
+    for symbol in ["lf_fp8_act_quant_rows", "lf_fp8_w8a8_dense", "lf_fp8_w8a8_qkv",
+                   "lf_fp8_w8a8_gate_up"] + [f"lf_fp8_w8a16_{op}_m{m}" for op in ("dense", "qkv", "gate_up")
+                                             for m in (16, 32, 64, 128)]:
+        assert symbol.encode() + b"\0" in image, symbol
+
+
+def test_probe_without_gpu_is_an_availability_code():
+    out = (ctypes.c_int64 * 3)()
+    availability = _abi.lib().lunaflux_hip_probe(out)
+    assert availability in range(0, 7)
+    assert out[2] == 0  # no vendor GEMM
+
+
+def test_swizzle_matches_documented_layout():
+    rng = np.random.default_rng(1)
+    n, k = 48, 384
+    q = rng.integers(0, 256, (n, k), dtype=np.uint8)
+    s = rng.random(n, dtype=np.float32)
+    region = fp8.pack_weight(q, s)
+    head = region[:64]
+    h32 = head.view(np.uint32)
+    assert h32[0] == 0x5738464C and bytes(head[:4]) == b"LF8W"
+    assert list(h32[1:8]) == [1, 1, 1, n, k, 1, 0]
+    h64 = head[32:64].view(np.uint64)
+    assert list(h64) == [256, n * k, 256 + n * k, (n * 4 + 255) // 256 * 256]
+    assert region.size == 256 + n * k + (n * 4 + 255) // 256 * 256
+    tiles = region[256:256 + n * k]
+    # W[16 nt + l%16][128 kt + 32 (l/16) + 16 h + b] at tile*2048 + h*1024 + l*16 + b
+    for (row, col) in [(0, 0), (17, 5), (47, 383), (31, 200), (5, 130)]:
+        nt, r = divmod(row, 16)
+        kt, kk = divmod(col, 128)
+        g, rem = divmod(kk, 32)
+        h, b = divmod(rem, 16)
+        lane = g * 16 + r
+        off = (nt * (k // 128) + kt) * 2048 + h * 1024 + lane * 16 + b
+        assert tiles[off] == q[row, col]
+    np.testing.assert_array_equal(region[256 + n * k:256 + n * k + 4 * n].view(np.float32), s)
+    q2, s2, info = fp8.unpack_weight(region)
+    np.testing.assert_array_equal(q2[0], q)
+    np.testing.assert_array_equal(s2[0], s)
+
+
+def test_pack_experts_and_block_scales():
+    rng = np.random.default_rng(2)
+    q = rng.integers(0, 256, (3, 128, 256), dtype=np.uint8)
+    s = rng.random((3, 2), dtype=np.float32)
+    region = fp8.pack_weight(q, s, fp8.BLOCK128)
+    q2, s2, info = fp8.unpack_weight(region)
+    assert info == dict(scale_mode=2, rows=128, columns=256, experts=3)
+    np.testing.assert_array_equal(q2, q)
+    np.testing.assert_array_equal(s2, s)
+
+
+def test_region_size_validation():
+    for rows, cols, mode in [(15, 128, 1), (16, 100, 1), (16, 128, 2), (0, 128, 1), (16, 128, 9)]:
+        with pytest.raises(fp8.DeviceError):
+            fp8.weight_region_bytes(rows, cols, 1, mode)
+
+
+def test_launch_geometry():
+    dims, sym = fp8.launch_geometry(_abi.ENTRY_W8A16_DENSE, 4096, 14336, 32)
+    assert sym == "lf_fp8_w8a16_dense_m32" and dims.grid == (256, 1, 1) and dims.block == (512, 1, 1)
+    dims, sym = fp8.launch_geometry(_abi.ENTRY_W8A16_QKV, 6144, 4096, 1)
+    assert sym == "lf_fp8_w8a16_qkv_m16" and dims.grid == (384, 1, 1)
+    dims, sym = fp8.launch_geometry(_abi.ENTRY_W8A8_GATE_UP, 14336, 4096, 8192)
+    assert sym == "lf_fp8_w8a8_gate_up" and dims.grid == (224, 64, 1) and dims.block == (256, 1, 1)
+    dims, sym = fp8.launch_geometry(_abi.ENTRY_ACT_QUANT_ROWS, 4096, 4096, 2048)
+    assert sym == "lf_fp8_act_quant_rows" and dims.grid == (2048, 1, 1)
+    with pytest.raises(fp8.DeviceError):
+        fp8.launch_geometry(_abi.ENTRY_W8A16_DENSE, 4096, 4096, 129)
+    with pytest.raises(fp8.DeviceError):
+        fp8.launch_geometry(_abi.ENTRY_W8A8_DENSE, 4000, 4096, 64)
+    assert fp8.act_quant_bytes(3, 512) == 1536 + 256
+
+
+def test_closed_and_invalid_handles_without_gpu():
+    lib = _abi.lib()
+    status = ctypes.c_int32(0)
+    ctx = lib.lunaflux_hip_context_create(0, ctypes.byref(status))
+    if status.value == _abi.LF_OK:
+        pytest.skip("a GPU is present")
+    assert status.value in (_abi.LF_UNAVAILABLE, _abi.LF_INVALID_ARGUMENT)
+    assert lib.lunaflux_hip_context_close(ctx) == _abi.LF_OK  # already closed
+    s = lib.lunaflux_hip_stream_create(ctx, ctypes.byref(status))
+    assert status.value == _abi.LF_CLOSED
+    lib.lunaflux_hip_release(s)
+    lib.lunaflux_hip_release(ctx)
+    blas = lib.lunaflux_hip_blas_create(None, ctypes.byref(status))
+    assert status.value == _abi.LF_UNSUPPORTED
+    lib.lunaflux_hip_release(blas)
+    assert lib.lunaflux_hip_bf16_gemm_plan_run(None, None, 0, None, 0, None, 0, None, 0, None) == _abi.LF_UNSUPPORTED
+
+
+def test_numpy_quantizer_matches_oracle():
+    rng = np.random.default_rng(3)
+    raw = rng.integers(0, 2 ** 32, 500_000, dtype=np.uint64).astype(np.uint32).view(np.float32)
+    raw = raw[np.isfinite(raw)]
+    np.testing.assert_array_equal(synth.e4m3_encode(raw), o.e4m3_encode(raw))
+    np.testing.assert_array_equal(synth.bf16_bits(raw), o.bf16_round(raw))
+    w = (rng.standard_normal((96, 512)) * 0.02).astype(np.float32)
+    w[7] = 0
+    for group in (None, 128):
+        q1, s1 = synth.quantize_rows(w, group)
+        q2, s2 = o.quantize_rows(w, group)
+        np.testing.assert_array_equal(q1, q2)
+        np.testing.assert_array_equal(s1, s2)
+    wb = (rng.standard_normal((256, 384)) * 0.02).astype(np.float32)
+    q1, s1 = synth.quantize_blocks(wb)
+    q2, s2 = o.quantize_blocks(wb)
+    np.testing.assert_array_equal(q1, q2)
+    np.testing.assert_array_equal(s1, s2)
+
+
+def test_golden_config1_reproduces_from_seed():
+    g = np.load(os.path.join(ROOT, "tests", "golden", "config1.npz"))
+    rng = np.random.default_rng(int(g["seed"]))
+    x = synth.bf16_bits(rng.standard_normal((4, 512), dtype=np.float32))
+    w = (rng.standard_normal((1536, 512), dtype=np.float32) * np.float32(0.02)).astype(np.float32)
+    q, s = synth.quantize_rows(w)
+    np.testing.assert_array_equal(x, g["x"])
+    np.testing.assert_array_equal(q, g["q"])
+    np.testing.assert_array_equal(s, g["s"])
+    y = o.dense_projection(o.bf16_decode(x), o.dequantize(q, s))
+    np.testing.assert_array_equal(y, g["y32"])
