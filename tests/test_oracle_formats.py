@@ -4,18 +4,21 @@ bfloat16 casts on the CPU), closed-form special cases and invariants. CPU only.
 """
 import numpy as np
 import pytest
-import torch
 
 import oracle_lib as o
 
 
 def torch_e4m3_encode(values: np.ndarray) -> np.ndarray:
+    import torch
+
     # torch returns NaN above 480 instead of saturating; clamp first.
     t = torch.from_numpy(np.clip(values.astype(np.float32), -448.0, 448.0))
     return t.to(torch.float8_e4m3fn).view(torch.uint8).numpy()
 
 
 def test_e4m3_decode_all_codes_match_torch():
+    import torch
+
     codes = np.arange(256, dtype=np.uint8)
     ours = o.e4m3_decode(codes)
     theirs = torch.from_numpy(codes).view(torch.float8_e4m3fn).to(torch.float32).numpy()
@@ -71,6 +74,8 @@ def test_e4m3_roundtrip_is_identity_on_codes():
 
 
 def test_bf16_rne_matches_torch():
+    import torch
+
     rng = np.random.default_rng(12)
     raw = rng.integers(0, 2 ** 32, 1_000_000, dtype=np.uint64).astype(np.uint32)
     values = raw.view(np.float32)
