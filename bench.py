@@ -1,0 +1,276 @@
+"""Benchmark of the FP8 projection hot path on one MI355X.
+
+Metric: FP8 projection GB/s & TFLOP/s (% roofline),
+Llama-3-8B shapes, 1 GPU. Workload of `value`: one
+Llama-3-8B decode layer's four projection calls on the W8A16 family - fused
+QKV (4096 -> 6144), O (4096 -> 4096), gate/up with SwiGLU (4096 -> 2 x 14336
+-> 14336) and down (14336 -> 4096) - at M = 32 tokens, bf16 activations from
+N(0, 1), e4m3 weights from N(0, 0.02) with per-output-channel fp32 scales
+(synthetic, seeded; no checkpoint exists offline). One step = the four calls.
+Weights are rotated over 5 device copies (1.1 GB > the 256 MB MALL) so each
+step streams its weights from HBM.
+
+value = algorithmic bytes of the step / step time, with algorithmic bytes per
+call = N*K (e4m3 weights) + 4*N (scales) + 2*M*K (x) + 2*M*N_out (y), each
+weight byte counted once. The roofline object is the dominant kernel (gate/up)
+timed with HIP events on the launch stream. `detail` holds the other decode
+M values, the prefill (W8A8) GEMMs in TFLOP/s, and the
+act-quant pass. cpu_baseline times the CPU oracle (C restatement of
+kernels/reference over dequantized weights) on the host cores.
+
+Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu] [--quick]
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+
+import numpy as np
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+
+HBM_PEAK_GBS = 8000.0
+FP8_PEAK_TFLOPS = 5000.0
+BF16_PEAK_TFLOPS = 2500.0
+ROTATIONS = 5
+HIDDEN, INTER, NQ, NKV = 4096, 14336, 4096, 1024
+METRIC = "FP8 proj GB/s & TFLOP/s (% roofline), Llama-3-8B shapes M=1..8192, 1 GPU"
+
+
+def log(msg):
+    print(f"[bench] {msg}", file=sys.stderr, flush=True)
+
+
+def call_shapes():
+    """(name, K, N weight rows, N_out) for the four calls of one layer."""
+    return [("qkv", HIDDEN, NQ + 2 * NKV, NQ + 2 * NKV), ("o", HIDDEN, HIDDEN, HIDDEN),
+            ("gate_up", HIDDEN, 2 * INTER, INTER), ("down", INTER, HIDDEN, HIDDEN)]
+
+
+def call_bytes(m, k, n, n_out):
+    return n * k + 4 * n + 2 * m * k + 2 * m * n_out
+
+
+def layer_bytes(m):
+    return sum(call_bytes(m, k, n, no) for _, k, n, no in call_shapes())
+
+
+def call_flops(m, k, n):
+    return 2 * m * n * k
+
+
+class Layer:
+    """Device-resident weights of one layer, ROTATIONS copies each."""
+
+    def __init__(self, rt, seed=1234):
+        from lunaflux_amd import fp8, synth
+        rng = np.random.default_rng(seed)
+        t0 = time.time()
+        self.regions = {}
+        for name, rows, cols in [("q", NQ, HIDDEN), ("k", NKV, HIDDEN), ("v", NKV, HIDDEN),
+                                 ("o", HIDDEN, HIDDEN), ("gate", INTER, HIDDEN),
+                                 ("up", INTER, HIDDEN), ("down", HIDDEN, INTER)]:
+            q, s = synth.weight(rng, rows, cols)
+            region = fp8.pack_weight(q, s)
+            self.regions[name] = [rt.weight_from_region(region) for _ in range(ROTATIONS)]
+        log(f"weights ready ({ROTATIONS} copies of one layer) in {time.time() - t0:.1f}s")
+
+    def w(self, name, r):
+        return self.regions[name][r % ROTATIONS]
+
+
+class Bench:
+    def __init__(self, rt, layer, max_tokens, family):
+        from lunaflux_amd import synth
+        from lunaflux_amd.fp8 import _region
+        self.rt, self.layer, self.family = rt, layer, family
+        ctx = rt.context
+        rng = np.random.default_rng(99 + max_tokens)
+        self.x = ctx.upload(synth.activations(rng, max_tokens, HIDDEN))
+        self.xd = ctx.upload(synth.activations(rng, max_tokens, INTER))
+        self.out = {n: ctx.allocate(max_tokens * no * 2) for n, _, _, no in call_shapes()}
+        self.max_tokens = max_tokens
+        self._region = _region
+        self.ops = {}
+
+    def bind(self, m):
+        rt, L, R = self.rt, self.layer, self._region
+        counts = rt.step_counts(m)
+        ops = []
+        for r in range(ROTATIONS):
+            fam, mt = self.family, self.max_tokens
+            x, xd = R(self.x, alignment=256), R(self.xd, alignment=256)
+            ops.append({
+                "qkv": rt.bind_qkv(fam, counts, x, L.w("q", r), L.w("k", r), L.w("v", r),
+                                   R(self.out["qkv"], alignment=256), mt),
+                "o": rt.bind_dense(fam, counts, x, L.w("o", r), R(self.out["o"], alignment=256), mt),
+                "gate_up": rt.bind_gate_up(fam, counts, x, L.w("gate", r), L.w("up", r),
+                                           R(self.out["gate_up"], alignment=256), mt),
+                "down": rt.bind_dense(fam, counts, xd, L.w("down", r),
+                                      R(self.out["down"], alignment=256), mt),
+            })
+        self.ops[m] = (counts, ops)
+        return ops
+
+    def run(self, m, steps, warmup, calls=("qkv", "o", "gate_up", "down"), probe="gate_up"):
+        """Times `steps` steps of the given calls; returns (total ms, mean ms of
+        each launch step of `probe` (events around it), per-step ms)."""
+        rt = self.rt
+        ops = self.ops.get(m, (None, None))[1] or self.bind(m)
+        stream = rt.stream
+        for i in range(warmup):
+            for c in calls:
+                ops[i % ROTATIONS][c].launch(stream, synchronous=False)
+        stream.synchronize()
+        ctx = rt.context
+        start, stop = ctx.create_event(), ctx.create_event()
+        probe_events = [(ctx.create_event(), ctx.create_event()) for _ in range(steps)]
+        start.record(stream)
+        for i in range(steps):
+            for c in calls:
+                op = ops[i % ROTATIONS][c]
+                if c == probe:
+                    pre = op.steps[:-1]
+                    for s in pre:
+                        s.launch(stream, synchronous=False)
+                    probe_events[i][0].record(stream)
+                    op.steps[-1].launch(stream, synchronous=False)
+                    probe_events[i][1].record(stream)
+                else:
+                    op.launch(stream, synchronous=False)
+        stop.record(stream)
+        stop.synchronize()
+        total = start.elapsed_milliseconds(stop)
+        probe_ms = (sum(a.elapsed_milliseconds(b) for a, b in probe_events) / steps
+                    if probe in calls else None)
+        return total, probe_ms, total / steps
+
+
+def cpu_baseline(m=32, threads=None):
+    """The CPU oracle on this host: the four decode calls of one layer at
+    M=m over dequantized fp32 weights (sequential-K fp32, as the reference),
+    output elements split across threads."""
+    sys.path.insert(0, os.path.join(ROOT, "tests"))
+    import oracle_lib as o
+    from lunaflux_amd import synth
+    threads = threads or min(os.cpu_count() or 1, 16)
+    rng = np.random.default_rng(7)
+    x = o.bf16_decode(synth.activations(rng, m, HIDDEN))
+    xd = o.bf16_decode(synth.activations(rng, m, INTER))
+    weights = []
+    for name, k, n, n_out in call_shapes():
+        q, s = synth.weight(rng, n, k)
+        weights.append((name, n_out, o.dequantize(q, s)))
+    passes, total_s = 0, 0.0
+    # Repeat whole layers until about 20 s of CPU work (wall x threads).
+    while passes == 0 or total_s * threads < 20.0:
+        for name, n_out, w in weights:
+            t0 = time.perf_counter()
+            y = o.project_values_mt(xd if name == "down" else x, w, threads)
+            if name == "gate_up":
+                o.silu_mul_array(y[:, :n_out], y[:, n_out:])
+            total_s += time.perf_counter() - t0
+        passes += 1
+    gbs = passes * layer_bytes(m) / total_s / 1e9
+    return {"value": round(gbs, 4), "unit": "GB/s", "cores": threads, "kind": "port",
+            "sample": f"{passes} decode layers (qkv, o, gate/up+SwiGLU, down) at M={m}, full "
+                      f"shapes: the CPU oracle's sequential-K fp32 project_values over dequantized "
+                      f"weights; {total_s:.2f} s wall on {threads} threads"}
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=50)
+    ap.add_argument("--warmup", type=int, default=10)
+    ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--quick", action="store_true", help="headline only, no detail sweep")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(f"bench.py measures one GPU only: --gpus {args.gpus} is not supported "
+              "(this build has no multi-GPU path; see DESIGN.md on sharding)", file=sys.stderr)
+        sys.exit(2)
+
+    from lunaflux_amd.fp8 import ProjectionRuntime
+    from lunaflux_amd import device
+
+    cap = device.device_info(0)
+    log(f"device: {cap.name} gfx{cap.major}{cap.minor}{0} mem={cap.total_memory / 2**30:.0f} GiB")
+    rt = ProjectionRuntime(0)
+    layer = Layer(rt)
+
+    m = 32
+    decode = Bench(rt, layer, 32, "w8a16")
+    total, probe_ms, step_ms = decode.run(m, args.steps, args.warmup)
+    value = layer_bytes(m) / (step_ms * 1e-3) / 1e9
+    gu_bytes = call_bytes(m, HIDDEN, 2 * INTER, INTER)
+    achieved = gu_bytes / (probe_ms * 1e-3) / 1e9
+    log(f"decode M={m}: {step_ms * 1e3:.1f} us/layer, {value:.0f} GB/s; gate_up {probe_ms * 1e3:.1f} us "
+        f"= {achieved:.0f} GB/s")
+
+    detail = {"decode_w8a16": {}, "prefill_w8a8": {}}
+    if not args.quick:
+        for mm, mt in [(1, 16), (8, 16), (32, 32), (128, 128)]:
+            b = Bench(rt, layer, mt, "w8a16") if mt != 32 else decode
+            row = {}
+            for c, k, n, no in call_shapes():
+                t, p, s_ms = b.run(mm, 20, 5, calls=(c,), probe=c)
+                row[c] = {"us": round(p * 1e3, 2), "GB/s": round(call_bytes(mm, k, n, no) / (p * 1e-3) / 1e9, 1)}
+            t, _, s_ms = b.run(mm, 20, 5)
+            row["layer_us"] = round(s_ms * 1e3, 2)
+            row["layer_GB/s"] = round(layer_bytes(mm) / (s_ms * 1e-3) / 1e9, 1)
+            row["layer_hbm_frac"] = round(row["layer_GB/s"] / HBM_PEAK_GBS, 4)
+            detail["decode_w8a16"][f"M={mm}"] = row
+            log(f"decode M={mm}: {row}")
+        for mm in (2048, 8192):
+            b = Bench(rt, layer, mm, "w8a8")
+            row = {}
+            for c, k, n, no in call_shapes():
+                t, p, s_ms = b.run(mm, 5, 2, calls=(c,), probe=c)
+                tf = call_flops(mm, k, n) / (p * 1e-3) / 1e12
+                row[c] = {"gemm_us": round(p * 1e3, 1), "TFLOP/s": round(tf, 1),
+                          "fp8_frac": round(tf / FP8_PEAK_TFLOPS, 4),
+                          "act_quant_us": round((s_ms - p) * 1e3, 1)}
+            detail["prefill_w8a8"][f"M={mm}"] = row
+            log(f"prefill M={mm}: {row}")
+            del b
+
+    cpu = None
+    if not args.no_cpu:
+        log("timing the CPU oracle baseline ...")
+        cpu = cpu_baseline(32)
+        log(f"cpu baseline: {cpu}")
+
+    line = {
+        "metric": METRIC,
+        "value": round(value, 2),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(step_ms, 5),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "e4m3 weights x bf16 activations, fp32 accumulate (W8A16)",
+        "data": "synthetic (seeded N(0,1) activations, N(0,0.02) weights quantized to e4m3)",
+        "config": {"workload": "llama3-8b decode layer: qkv+o+gate_up(SwiGLU)+down, M=32, W8A16",
+                   "global_batch": m, "seq_len": 1, "parallelism": "single GPU",
+                   "weight_rotations": ROTATIONS},
+        "roofline": {"bound": "hbm", "kernel": "lf_fp8_w8a16_gate_up_m32",
+                     "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
+                     "algorithmic_bytes_per_launch": gu_bytes,
+                     "avg_launch_us": round(probe_ms * 1e3, 2)},
+        "cpu_baseline": cpu,
+        "detail": detail,
+    }
+    print(json.dumps(line), flush=True)
+
+
+if __name__ == "__main__":
+    main()

@@ -418,7 +418,10 @@ int32_t lunaflux_hip_device_info(int32_t ordinal, int64_t numeric[5],
   numeric[3] = prop.major >= 9 ? 1 : 0;
   numeric[4] = 0;
   std::memset(name, 0, LF_DEVICE_NAME_BYTES);
-  std::strncpy(reinterpret_cast<char *>(name), prop.name, LF_DEVICE_NAME_BYTES - 1);
+  // Some drivers report an empty marketing name; the architecture name
+  // (e.g. "gfx950:sramecc+:xnack-") is always set.
+  const char *label = prop.name[0] != '\0' ? prop.name : prop.gcnArchName;
+  std::strncpy(reinterpret_cast<char *>(name), label, LF_DEVICE_NAME_BYTES - 1);
   return LF_OK;
 }
 
