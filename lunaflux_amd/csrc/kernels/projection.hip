@@ -1,6 +1,7 @@
-// projection.hip - gfx950 kernels for the dense FP8 projections (QKV,
-// output, gate/up + SwiGLU, down). Entry points and operand lists are
-// documented in include/lunaflux_fp8.h; every parameter is a device region.
+// projection.hip - gfx950 kernels of the prefill regime: the per-token
+// activation quantizer and the W8A8 FP8 MFMA GEMM (QKV, output/down,
+// gate/up + SwiGLU). Entry points and operand lists are documented in
+// include/lunaflux_fp8.h; every parameter is a device region.
 #include "device_common.h"
 
 namespace {
@@ -56,166 +57,6 @@ __device__ void act_quant_rows(const int32_t *counts, const uint16_t *x,
   if (threadIdx.x == 0) {
     float *scales = reinterpret_cast<float *>(xq + align256(static_cast<uint64_t>(M) * K));
     scales[row] = zero ? 0.0f : amax / 448.0f;
-  }
-}
-
-// ---------------------------------------------------------------------------
-// W8A16: bf16 activations x e4m3 weights (decode regime, M <= 16 * MT).
-// A block (8 waves) owns one 16-column tile of each of its NW weights and
-// splits K across its waves. Each wave streams its weight tiles with two
-// coalesced 1 KiB loads per tile, converts them to bf16 in registers and
-// feeds 16x16x32 bf16 MFMAs whose A operand is the activation read straight
-// from global memory (it is small and L2 resident). The 8 partial tiles are
-// summed in LDS in a fixed order, scaled per channel and stored as bf16.
-// ---------------------------------------------------------------------------
-constexpr int kW16Waves = 8;
-constexpr int kW16Chunk = 4;  // weight tiles loaded ahead per wave
-
-union Frag16 {
-  uint4 u;
-  bf16x8 v;
-};
-
-template <int MT, int NW>
-__device__ void w8a16_accumulate(int M, int K, const uint16_t *__restrict__ x,
-                                 const uint8_t *const (&strip)[NW],
-                                 f32x4 (&acc)[MT][NW]) {
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-  const int KT = K >> 7;
-  const int kt0 = (KT * wave) / kW16Waves, kt1 = (KT * (wave + 1)) / kW16Waves;
-  const int g = lane >> 4, r = lane & 15;
-#pragma unroll
-  for (int mt = 0; mt < MT; ++mt)
-#pragma unroll
-    for (int i = 0; i < NW; ++i) acc[mt][i] = f32x4{0.f, 0.f, 0.f, 0.f};
-
-  for (int base = kt0; base < kt1; base += kW16Chunk) {
-    uint4 b[kW16Chunk][NW][2];
-#pragma unroll
-    for (int c = 0; c < kW16Chunk; ++c) {
-      if (base + c < kt1) {
-#pragma unroll
-        for (int i = 0; i < NW; ++i) {
-          const u32x4 *t = reinterpret_cast<const u32x4 *>(strip[i] + (base + c) * kTileBytes);
-          const u32x4 lo = __builtin_nontemporal_load(t + lane);
-          const u32x4 hi = __builtin_nontemporal_load(t + 64 + lane);
-          b[c][i][0] = make_uint4(lo.x, lo.y, lo.z, lo.w);
-          b[c][i][1] = make_uint4(hi.x, hi.y, hi.z, hi.w);
-        }
-      }
-    }
-#pragma unroll
-    for (int c = 0; c < kW16Chunk; ++c) {
-      if (base + c < kt1) {
-        const int kt = base + c;
-        Frag16 a[MT][4];
-#pragma unroll
-        for (int mt = 0; mt < MT; ++mt) {
-          const int m = mt * 16 + r;
-          if (m < M) {
-            const uint4 *p = reinterpret_cast<const uint4 *>(
-                x + static_cast<uint64_t>(m) * K + kt * 128 + g * 32);
-#pragma unroll
-            for (int j = 0; j < 4; ++j) a[mt][j].u = p[j];
-          } else {
-#pragma unroll
-            for (int j = 0; j < 4; ++j) a[mt][j].u = make_uint4(0u, 0u, 0u, 0u);
-          }
-        }
-#pragma unroll
-        for (int j = 0; j < 4; ++j) {
-#pragma unroll
-          for (int i = 0; i < NW; ++i) {
-            const uint4 &h = b[c][i][j >> 1];
-            uint32_t w0 = (j & 1) ? h.z : h.x;
-            uint32_t w1 = (j & 1) ? h.w : h.y;
-            Frag16 bf;
-            e4m3x4_to_bf16x4(w0, bf.u.x, bf.u.y);
-            e4m3x4_to_bf16x4(w1, bf.u.z, bf.u.w);
-#pragma unroll
-            for (int mt = 0; mt < MT; ++mt) {
-              acc[mt][i] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a[mt][j].v, bf.v,
-                                                                   acc[mt][i], 0, 0, 0);
-            }
-          }
-        }
-      }
-    }
-  }
-}
-
-// MODE 0: dense, 1: qkv, 2: gate/up + SwiGLU.
-template <int MT, int MODE>
-__device__ void w8a16_kernel(const int32_t *counts, const uint16_t *x,
-                             const uint8_t *w0, const uint8_t *w1,
-                             const uint8_t *w2, uint16_t *y) {
-  constexpr int NW = MODE == 2 ? 2 : 1;
-  __shared__ f32x4 red[kW16Waves][MT * NW][64];
-  const WeightHeader &h0 = header_of(w0);
-  if (h0.magic != kWeightMagic) return;
-  const int K = static_cast<int>(h0.columns);
-  const int M = live_rows(counts, 16 * MT);
-  int tile = blockIdx.x;
-  int out_col0, ld;
-  const uint8_t *region[NW];
-  if (MODE == 1) {
-    const int tq = static_cast<int>(h0.rows) >> 4;
-    const int tk = static_cast<int>(header_of(w1).rows) >> 4;
-    ld = static_cast<int>(h0.rows + header_of(w1).rows + header_of(w2).rows);
-    out_col0 = tile * 16;
-    if (tile < tq) {
-      region[0] = w0;
-    } else if (tile < tq + tk) {
-      region[0] = w1;
-      tile -= tq;
-    } else {
-      region[0] = w2;
-      tile -= tq + tk;
-    }
-  } else {
-    ld = static_cast<int>(h0.rows);
-    out_col0 = tile * 16;
-    region[0] = w0;
-    if (NW == 2) region[NW - 1] = w1;
-  }
-  const uint8_t *strip[NW];
-#pragma unroll
-  for (int i = 0; i < NW; ++i) {
-    strip[i] = expert_tiles(region[i], 0) + static_cast<uint64_t>(tile) * (K >> 7) * kTileBytes;
-  }
-  f32x4 acc[MT][NW];
-  w8a16_accumulate<MT, NW>(M, K, x, strip, acc);
-
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-#pragma unroll
-  for (int mt = 0; mt < MT; ++mt)
-#pragma unroll
-    for (int i = 0; i < NW; ++i) red[wave][mt * NW + i][lane] = acc[mt][i];
-  __syncthreads();
-
-  const float *scale0 = expert_scales(region[0], 0);
-  const float *scale1 = expert_scales(region[NW - 1], 0);
-  for (int e = threadIdx.x; e < MT * 256; e += blockDim.x) {
-    const int mt = e >> 8, row16 = (e >> 4) & 15, c = e & 15;
-    const int m = mt * 16 + row16;
-    if (m >= M) continue;
-    const int src_lane = (row16 >> 2) * 16 + c, rr = row16 & 3;
-    float s[NW];
-#pragma unroll
-    for (int i = 0; i < NW; ++i) {
-      float v = 0.0f;
-#pragma unroll
-      for (int wv = 0; wv < kW16Waves; ++wv) v += red[wv][mt * NW + i][src_lane][rr];
-      s[i] = v;
-    }
-    const int n_local = tile * 16 + c;
-    float out;
-    if (MODE == 2) {
-      out = silu_mul(s[0] * scale0[n_local], s[NW - 1] * scale1[n_local]);
-    } else {
-      out = s[0] * scale0[n_local];
-    }
-    y[static_cast<uint64_t>(m) * ld + out_col0 + c] = static_cast<uint16_t>(f32_to_bf16(out));
   }
 }
 
@@ -409,27 +250,6 @@ __global__ __launch_bounds__(256) void lf_fp8_act_quant_rows(const int32_t *coun
                                                              uint8_t *xq) {
   act_quant_rows(counts, x, w, xq);
 }
-
-#define LF_W8A16_ENTRIES(MT, M)                                                        \
-  __global__ __launch_bounds__(512) void lf_fp8_w8a16_dense_m##M(                      \
-      const int32_t *counts, const uint16_t *x, const uint8_t *w, uint16_t *y) {       \
-    w8a16_kernel<MT, 0>(counts, x, w, w, w, y);                                        \
-  }                                                                                    \
-  __global__ __launch_bounds__(512) void lf_fp8_w8a16_qkv_m##M(                        \
-      const int32_t *counts, const uint16_t *x, const uint8_t *wq, const uint8_t *wk,  \
-      const uint8_t *wv, uint16_t *y) {                                                \
-    w8a16_kernel<MT, 1>(counts, x, wq, wk, wv, y);                                     \
-  }                                                                                    \
-  __global__ __launch_bounds__(512) void lf_fp8_w8a16_gate_up_m##M(                    \
-      const int32_t *counts, const uint16_t *x, const uint8_t *wg, const uint8_t *wu,  \
-      uint16_t *h) {                                                                   \
-    w8a16_kernel<MT, 2>(counts, x, wg, wu, wu, h);                                     \
-  }
-
-LF_W8A16_ENTRIES(1, 16)
-LF_W8A16_ENTRIES(2, 32)
-LF_W8A16_ENTRIES(4, 64)
-LF_W8A16_ENTRIES(8, 128)
 
 __global__ __launch_bounds__(256) void lf_fp8_w8a8_dense(const int32_t *counts,
                                                          const uint8_t *xq,

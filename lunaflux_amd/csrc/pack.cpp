@@ -170,7 +170,9 @@ int32_t lunaflux_fp8_launch_geometry(int32_t entry, int64_t n, int64_t k,
       std::snprintf(buffer, sizeof(buffer), "lf_fp8_w8a16_%s_m%d", op, m);
       name = buffer;
       gx = static_cast<int32_t>(n / 16);
-      bx = 512;
+      // gate/up: 4 waves per block (two weights per wave, more blocks per
+      // CU); dense/qkv: 8 waves per block.
+      bx = entry == LF_FP8_ENTRY_W8A16_GATE_UP ? 256 : 512;
       break;
     }
     case LF_FP8_ENTRY_W8A8_DENSE:
