@@ -141,6 +141,81 @@ int32_t lunaflux_fp8_launch_geometry(int32_t entry, int64_t n, int64_t k,
                                      int32_t max_tokens, int32_t dims[7],
                                      char symbol[LF_FP8_SYMBOL_BYTES]);
 
+/* ---- grouped form: MoE expert MLP ---------------------------------------- */
+/*
+ * The reference has no MoE (its plan vocabulary stops at GatedMlp,
+ * model/plan/operations.mbt:4-14), so these entry points define the operand
+ * lists a MoE operation would bind. Expert weights are weight regions with
+ * `experts` = E: gate and up [E][I, H], down [E][H, I]; per-channel scales
+ * with per-token activation quantization (group 0), or 128 x 128 block scales
+ * with per-token-per-128-column activation quantization (group 128).
+ *
+ * The routing descriptor is a 32-byte device region (a model constant, like
+ * a weight) read by every MoE kernel. The workspace is one region whose
+ * layout is a function of the live token count (the counts descriptor) and
+ * the routing descriptor; lunaflux_fp8_moe_workspace_bytes sizes it for a
+ * profile's max_query_tokens.
+ *
+ * Launch sequence and operands (in order):
+ *  lf_moe_route         (counts, desc, logits fp32 [T, E], ws)
+ *  lf_moe_sort          (counts, desc, ws)
+ *  lf_moe_quant_tokens  (counts, desc, x bf16 [T, H], ws)
+ *  lf_moe_gate_up[_b128](counts, desc, wg, wu, ws)
+ *  lf_moe_quant_hidden  (counts, desc, ws)
+ *  lf_moe_down[_b128]   (counts, desc, wd, ws)
+ *  lf_moe_combine       (counts, desc, ws, out bf16 [T, H])
+ * Routing: the k largest logits per token (ties to the lower expert id);
+ * weights are a softmax over the k picked logits (route_mode 0, Mixtral) or
+ * the softmax over all experts at the picked ids (route_mode 1). The sort is
+ * a stable counting sort of assignments a = t*k + j by expert; out[t] =
+ * sum_j w[t, j] * y(t, j) in ascending j, fp32, rounded to bf16.
+ */
+#define LF_FP8_MOE_MAGIC 0x454F4D4Cu /* bytes "LMOE" */
+
+typedef struct lf_fp8_moe_desc {
+  uint32_t magic;
+  int32_t experts;
+  int32_t top_k;
+  int32_t route_mode;
+  int32_t hidden;
+  int32_t inter;
+  int32_t group; /* 0: per token / per channel; 128: 128-wide blocks */
+  int32_t reserved;
+} lf_fp8_moe_desc;
+
+enum lf_fp8_moe_entry {
+  LF_FP8_MOE_ROUTE = 1,
+  LF_FP8_MOE_SORT = 2,
+  LF_FP8_MOE_QUANT_TOKENS = 3,
+  LF_FP8_MOE_GATE_UP = 4,
+  LF_FP8_MOE_QUANT_HIDDEN = 5,
+  LF_FP8_MOE_DOWN = 6,
+  LF_FP8_MOE_COMBINE = 7
+};
+
+/* Validates and fills a descriptor: 1 <= experts <= 256, 1 <= top_k <=
+ * min(experts, 16), route_mode 0 or 1, hidden and inter multiples of 128,
+ * group 0 or 128 (128 also needs hidden, inter <= 4096). */
+int32_t lunaflux_fp8_moe_descriptor(int32_t experts, int32_t top_k,
+                                    int32_t route_mode, int64_t hidden,
+                                    int64_t inter, int32_t group,
+                                    lf_fp8_moe_desc *out);
+/* Workspace bytes for up to max_tokens live tokens; -1 if invalid. */
+int64_t lunaflux_fp8_moe_workspace_bytes(const lf_fp8_moe_desc *desc,
+                                         int32_t max_tokens);
+/* Byte offsets of the workspace arrays for `tokens` live tokens, in order:
+ * top-k ids (int32 [T*k]), top-k weights (fp32 [T*k]), sorted assignments
+ * (int32 [T*k]), position of each assignment (int32 [T*k]), expert row
+ * offsets (int32 [E+1]), expert 128-row tile offsets (int32 [E+1]), e4m3
+ * tokens [T, H], token scales, h bf16 [T*k, I], e4m3 h, h scales, y fp32
+ * [T*k, H], end. */
+int32_t lunaflux_fp8_moe_workspace_layout(const lf_fp8_moe_desc *desc,
+                                          int32_t tokens, int64_t offsets[13]);
+int32_t lunaflux_fp8_moe_launch_geometry(int32_t entry,
+                                         const lf_fp8_moe_desc *desc,
+                                         int32_t max_tokens, int32_t dims[7],
+                                         char symbol[LF_FP8_SYMBOL_BYTES]);
+
 #ifdef __cplusplus
 }
 #endif

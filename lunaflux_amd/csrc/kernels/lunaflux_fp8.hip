@@ -2,3 +2,4 @@
 // lunaflux_fp8.hsaco (hipcc --genco --offload-arch=gfx950).
 #include "projection.hip"
 #include "w8a16.hip"
+#include "moe.hip"

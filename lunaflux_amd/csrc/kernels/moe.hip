@@ -1,0 +1,418 @@
+// moe.hip - the grouped (expert MLP) form of the FP8 projection path.
+//
+// Launch sequence of one MoE expert-MLP operation (all operands are device
+// regions; `desc` is the routing descriptor, `ws` the operation's workspace,
+// whose layout is a function of the live token count T and the descriptor,
+// recomputed identically by every kernel - see MoeLayout):
+//   lf_moe_route          logits [T, E] fp32       -> top-k experts, weights
+//   lf_moe_sort           stable counting sort of the T*k assignments by
+//                         expert -> sorted ids, positions, per-expert row
+//                         offsets and 128-row tile offsets
+//   lf_moe_quant_tokens   x [T, H] bf16            -> e4m3 + scales (per token
+//                         or per token per 128 columns)
+//   lf_moe_gate_up        grouped GEMM over expert gate/up weights with the
+//                         gathered token rows, SwiGLU epilogue -> h [T*k, I]
+//                         bf16 in expert order
+//   lf_moe_quant_hidden   h -> e4m3 + scales
+//   lf_moe_down           grouped GEMM over expert down weights -> y [T*k, H]
+//                         fp32 in expert order
+//   lf_moe_combine        out[t] = sum_j w[t, j] * y[pos(t, j)] (j ascending)
+//                         -> bf16 [T, H]
+#include "w8a8_core.h"
+
+namespace {
+
+constexpr uint32_t kMoeMagic = 0x454F4D4Cu;  // bytes "LMOE"
+
+struct MoeDesc {
+  uint32_t magic;
+  int32_t experts, top_k, route_mode, hidden, inter, group, reserved;
+};
+
+LF_DEVICE uint64_t al256(uint64_t v) { return (v + 255u) & ~uint64_t(255); }
+
+// Byte offsets of the workspace arrays for T live tokens (mirrored on the
+// host by lunaflux_fp8_moe_workspace_bytes).
+struct MoeLayout {
+  uint64_t topk_ids, topk_w, sorted, pos, offsets, tiles, xq, xs, h, hq, hs, y, end;
+  LF_DEVICE MoeLayout(const MoeDesc &d, int T) {
+    const uint64_t A = static_cast<uint64_t>(T) * d.top_k;
+    const uint64_t H = d.hidden, I = d.inter;
+    const uint64_t gx = d.group > 0 ? H / d.group : 1, gh = d.group > 0 ? I / d.group : 1;
+    uint64_t o = 0;
+    topk_ids = o; o = al256(o + A * 4);
+    topk_w = o;   o = al256(o + A * 4);
+    sorted = o;   o = al256(o + A * 4);
+    pos = o;      o = al256(o + A * 4);
+    offsets = o;  o = al256(o + (d.experts + 1) * 4);
+    tiles = o;    o = al256(o + (d.experts + 1) * 4);
+    xq = o;       o = al256(o + static_cast<uint64_t>(T) * H);
+    xs = o;       o = al256(o + static_cast<uint64_t>(T) * gx * 4);
+    h = o;        o = al256(o + A * I * 2);
+    hq = o;       o = al256(o + A * I);
+    hs = o;       o = al256(o + A * gh * 4);
+    y = o;        o = al256(o + A * H * 4);
+    end = o;
+  }
+};
+
+template <typename T>
+LF_DEVICE T *at(uint8_t *ws, uint64_t offset) {
+  return reinterpret_cast<T *>(ws + offset);
+}
+
+LF_DEVICE bool desc_ok(const MoeDesc &d) {
+  return d.magic == kMoeMagic && d.experts > 0 && d.experts <= 256 && d.top_k > 0 &&
+         d.top_k <= d.experts && d.top_k <= 16;
+}
+
+// --- routing ---------------------------------------------------------------
+// One thread per token: the k largest logits in order (ties -> lower expert
+// id, strict comparison), then softmax weights either over the k picked
+// logits (mode 0) or over all experts (mode 1), accumulated in expert order.
+__device__ void route(const int32_t *counts, const MoeDesc &d, const float *logits, uint8_t *ws) {
+  const int T = live_rows(counts, 1 << 30);
+  const int t = blockIdx.x * blockDim.x + threadIdx.x;
+  if (t >= T) return;
+  const MoeLayout L(d, T);
+  const float *l = logits + static_cast<uint64_t>(t) * d.experts;
+  int32_t *ids = at<int32_t>(ws, L.topk_ids) + static_cast<uint64_t>(t) * d.top_k;
+  float *wts = at<float>(ws, L.topk_w) + static_cast<uint64_t>(t) * d.top_k;
+  int picked[16];
+  for (int j = 0; j < d.top_k; ++j) {
+    int best = -1;
+    for (int e = 0; e < d.experts; ++e) {
+      bool taken = false;
+      for (int i = 0; i < j; ++i) taken |= picked[i] == e;
+      if (taken) continue;
+      if (best < 0 || l[e] > l[best]) best = e;
+    }
+    picked[j] = best;
+    ids[j] = best;
+  }
+  const float top = l[picked[0]];
+  float sum = 0.0f;
+  if (d.route_mode == 0) {
+    for (int j = 0; j < d.top_k; ++j) sum += expf(l[picked[j]] - top);
+  } else {
+    for (int e = 0; e < d.experts; ++e) sum += expf(l[e] - top);
+  }
+  for (int j = 0; j < d.top_k; ++j) wts[j] = expf(l[picked[j]] - top) / sum;
+}
+
+// --- stable counting sort ----------------------------------------------------
+// One block of 1024 threads. Pass 1 counts assignments per expert; pass 2
+// walks the assignments in chunks of 1024 in ascending order and gives each
+// its rank among equal experts: within a wave by matching expert ids with
+// ballots over their bits, across the chunk's waves by a prefix over
+// per-wave counts, across chunks by running totals. Positions therefore
+// equal those of a stable sort.
+constexpr int kSortThreads = 1024;
+constexpr int kSortWaves = kSortThreads / 64;
+
+__device__ void sort_assignments(const int32_t *counts, const MoeDesc &d, uint8_t *ws) {
+  __shared__ int32_t cnt[257];
+  __shared__ int32_t running[256];
+  __shared__ int32_t wcnt[kSortWaves][256];
+  const int T = live_rows(counts, 1 << 30);
+  const MoeLayout L(d, T);
+  const int E = d.experts;
+  const int A = T * d.top_k;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int32_t *ids = at<int32_t>(ws, L.topk_ids);
+  int32_t *sorted = at<int32_t>(ws, L.sorted);
+  int32_t *pos = at<int32_t>(ws, L.pos);
+  int32_t *offsets = at<int32_t>(ws, L.offsets);
+  int32_t *tiles = at<int32_t>(ws, L.tiles);
+  for (int e = tid; e < E; e += kSortThreads) {
+    cnt[e] = 0;
+    running[e] = 0;
+  }
+  __syncthreads();
+  for (int a = tid; a < A; a += kSortThreads) atomicAdd(&cnt[ids[a]], 1);
+  __syncthreads();
+  if (tid == 0) {
+    // Exclusive scans: first row and first 128-row tile of each expert;
+    // cnt[e] becomes the first position of expert e.
+    int off = 0, tl = 0;
+    for (int e = 0; e < E; ++e) {
+      const int c = cnt[e];
+      offsets[e] = off;
+      tiles[e] = tl;
+      cnt[e] = off;
+      off += c;
+      tl += (c + w8a8::kBM - 1) / w8a8::kBM;
+    }
+    offsets[E] = off;
+    tiles[E] = tl;
+  }
+  int bits = 0;
+  while ((1 << bits) < E + 1) ++bits;
+  const uint64_t lt_mask = lane == 0 ? 0ull : (~0ull >> (64 - lane));
+  for (int base = 0; base < A; base += kSortThreads) {
+    for (int i = tid; i < kSortWaves * E; i += kSortThreads) wcnt[i / E][i % E] = 0;
+    __syncthreads();
+    const int a = base + tid;
+    const int e = a < A ? ids[a] : E;  // E marks lanes past the end
+    uint64_t same = ~0ull;
+    for (int b = 0; b < bits; ++b) {
+      const uint64_t ones = __ballot((e >> b) & 1);
+      same &= ((e >> b) & 1) ? ones : ~ones;
+    }
+    const int rank = __popcll(same & lt_mask);
+    if (e < E && rank == 0) wcnt[wave][e] = __popcll(same);
+    __syncthreads();
+    if (e < E) {
+      int before = 0;
+      for (int w = 0; w < wave; ++w) before += wcnt[w][e];
+      const int p = cnt[e] + running[e] + before + rank;
+      sorted[p] = a;
+      pos[a] = p;
+    }
+    __syncthreads();
+    for (int x = tid; x < E; x += kSortThreads) {
+      int s = 0;
+      for (int w = 0; w < kSortWaves; ++w) s += wcnt[w][x];
+      running[x] += s;
+    }
+    __syncthreads();
+  }
+}
+
+// --- quantizers --------------------------------------------------------------
+__device__ void quant_rows(const uint16_t *src, int K, int group, uint8_t *dst, float *scales,
+                           int rows) {
+  const int row = blockIdx.x;
+  if (row >= rows) return;
+  const int per_row = group > 0 ? K / group : 1;
+  quantize_row(src + static_cast<uint64_t>(row) * K, K, group, dst + static_cast<uint64_t>(row) * K,
+               scales + static_cast<uint64_t>(row) * per_row);
+}
+
+// --- grouped GEMM -------------------------------------------------------------
+// blockIdx.y enumerates the 128-row tiles of all experts (tiles[] prefix);
+// the expert of a tile is found by binary search.
+LF_DEVICE int expert_of_tile(const int32_t *tiles, int E, int j) {
+  int lo = 0, hi = E;
+  while (hi - lo > 1) {
+    const int mid = (lo + hi) >> 1;
+    if (tiles[mid] <= j) lo = mid; else hi = mid;
+  }
+  return lo;
+}
+
+// STAGE 0: gate/up (x rows gathered by token, SwiGLU, bf16 h);
+// STAGE 1: down (h rows in expert order, fp32 y).
+template <int STAGE, bool BLOCK>
+__device__ void grouped_gemm(const int32_t *counts, const MoeDesc &d, const uint8_t *w0,
+                             const uint8_t *w1, uint8_t *ws) {
+  __shared__ __attribute__((aligned(16))) uint8_t As[2][w8a8::kAStage];
+  // Block-scaled form: activation scales of the block's rows, [kBM][KT],
+  // K <= 4096 (the host rejects larger K for 128-column groups).
+  __shared__ float sa_lds[BLOCK ? w8a8::kBM * 32 : 1];
+  const int T = live_rows(counts, 1 << 30);
+  const MoeLayout L(d, T);
+  const int32_t *tiles = at<int32_t>(ws, L.tiles);
+  const int E = d.experts;
+  const int j = blockIdx.y;
+  if (j >= tiles[E]) return;
+  const int e = expert_of_tile(tiles, E, j);
+  const int32_t *offsets = at<int32_t>(ws, L.offsets);
+  const int p0 = offsets[e] + (j - tiles[e]) * w8a8::kBM;
+  const int pend = offsets[e + 1];
+  const WeightHeader &h0 = header_of(w0);
+  const int K = static_cast<int>(h0.columns);
+  const int KT = K >> 7;
+  const int N = static_cast<int>(h0.rows);
+  if (BLOCK && KT > 32) return;  // sa_lds holds at most 32 scale columns
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int wm = wave >> 1, wn = wave & 1;
+  const int32_t *sorted = at<int32_t>(ws, L.sorted);
+
+  // This thread's activation row.
+  const int trow = tid >> 1;
+  const int p = p0 + trow;
+  const bool live = p < pend;
+  int src_row = 0;
+  if (live) src_row = STAGE == 0 ? sorted[p] / d.top_k : p;
+  const uint8_t *abase = at<uint8_t>(ws, STAGE == 0 ? L.xq : L.hq);
+  const uint4 *asrc = reinterpret_cast<const uint4 *>(abase + static_cast<uint64_t>(src_row) * K + (tid & 1) * 64);
+  const float *ascales = at<float>(ws, STAGE == 0 ? L.xs : L.hs);
+
+  // This wave's weight tiles.
+  const uint8_t *strip[4];
+  const float *wsc[4];
+  const float *sw[4];
+  int col[4];
+  if (STAGE == 0) {
+    const int c0 = blockIdx.x * 64 + wn * 32;
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      const uint8_t *reg = q < 2 ? w0 : w1;
+      col[q] = c0 + (q & 1) * 16;
+      strip[q] = expert_tiles(reg, e) + static_cast<uint64_t>(col[q] >> 4) * KT * kTileBytes;
+      wsc[q] = expert_scales(reg, e);
+    }
+  } else {
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      col[q] = blockIdx.x * 128 + wn * 64 + q * 16;
+      strip[q] = expert_tiles(w0, e) + static_cast<uint64_t>(col[q] >> 4) * KT * kTileBytes;
+      wsc[q] = expert_scales(w0, e);
+    }
+  }
+#pragma unroll
+  for (int q = 0; q < 4; ++q) sw[q] = BLOCK ? wsc[q] + (col[q] >> 7) * KT : nullptr;
+  if constexpr (BLOCK) {
+    // Activation scales of the block's rows: [kBM][KT] (zero for dead rows).
+    for (int i = tid; i < w8a8::kBM * KT; i += blockDim.x) {
+      const int rr = i / KT, kg = i % KT;
+      const int pp = p0 + rr;
+      float s = 0.0f;
+      if (pp < pend) {
+        const int sr = STAGE == 0 ? sorted[pp] / d.top_k : pp;
+        s = ascales[static_cast<uint64_t>(sr) * KT + kg];
+      }
+      sa_lds[i] = s;
+    }
+    __syncthreads();
+  }
+  f32x4 acc[4][4];
+  w8a8::mainloop<BLOCK>(asrc, live, strip, KT, As, sa_lds, sw, acc);
+
+  const int r = lane & 15;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+#pragma unroll
+    for (int rr = 0; rr < 4; ++rr) {
+      const int pp = p0 + w8a8::acc_row(wm, i, lane, rr);
+      if (pp >= pend) continue;
+      float sa = 1.0f;
+      if (!BLOCK) {
+        const int sr = STAGE == 0 ? sorted[pp] / d.top_k : pp;
+        sa = ascales[sr];
+      }
+      if (STAGE == 0) {
+        uint16_t *hrow = at<uint16_t>(ws, L.h) + static_cast<uint64_t>(pp) * N;
+#pragma unroll
+        for (int q = 0; q < 2; ++q) {
+          const int c = col[q] + r;
+          const float gv = BLOCK ? acc[i][q][rr] : acc[i][q][rr] * sa * wsc[q][c];
+          const float uv = BLOCK ? acc[i][q + 2][rr] : acc[i][q + 2][rr] * sa * wsc[q + 2][c];
+          hrow[c] = static_cast<uint16_t>(f32_to_bf16(silu_mul(gv, uv)));
+        }
+      } else {
+        float *yrow = at<float>(ws, L.y) + static_cast<uint64_t>(pp) * N;
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+          const int c = col[q] + r;
+          yrow[c] = BLOCK ? acc[i][q][rr] : acc[i][q][rr] * sa * wsc[q][c];
+        }
+      }
+    }
+  }
+}
+
+// --- combine -------------------------------------------------------------------
+__device__ void combine(const int32_t *counts, const MoeDesc &d, uint8_t *ws, uint16_t *out) {
+  const int T = live_rows(counts, 1 << 30);
+  const int t = blockIdx.x;
+  if (t >= T) return;
+  const MoeLayout L(d, T);
+  const int H = d.hidden;
+  const float *w = at<float>(ws, L.topk_w) + static_cast<uint64_t>(t) * d.top_k;
+  const int32_t *pos = at<int32_t>(ws, L.pos) + static_cast<uint64_t>(t) * d.top_k;
+  const float *y = at<float>(ws, L.y);
+  for (int c = threadIdx.x; c < H; c += blockDim.x) {
+    float acc = 0.0f;
+    for (int j = 0; j < d.top_k; ++j) {
+      const float prod = w[j] * y[static_cast<uint64_t>(pos[j]) * H + c];
+      acc = acc + prod;
+    }
+    out[static_cast<uint64_t>(t) * H + c] = static_cast<uint16_t>(f32_to_bf16(acc));
+  }
+}
+
+LF_DEVICE const MoeDesc &desc_of(const int32_t *desc) { return *reinterpret_cast<const MoeDesc *>(desc); }
+
+}  // namespace
+
+extern "C" {
+
+__global__ __launch_bounds__(256) void lf_moe_route(const int32_t *counts, const int32_t *desc,
+                                                    const float *logits, uint8_t *ws) {
+  const MoeDesc &d = desc_of(desc);
+  if (!desc_ok(d)) return;
+  route(counts, d, logits, ws);
+}
+
+__global__ __launch_bounds__(1024) void lf_moe_sort(const int32_t *counts, const int32_t *desc,
+                                                    uint8_t *ws) {
+  const MoeDesc &d = desc_of(desc);
+  if (!desc_ok(d)) return;
+  sort_assignments(counts, d, ws);
+}
+
+__global__ __launch_bounds__(256) void lf_moe_quant_tokens(const int32_t *counts,
+                                                           const int32_t *desc,
+                                                           const uint16_t *x, uint8_t *ws) {
+  const MoeDesc &d = desc_of(desc);
+  if (!desc_ok(d)) return;
+  const int T = live_rows(counts, 1 << 30);
+  const MoeLayout L(d, T);
+  quant_rows(x, d.hidden, d.group, at<uint8_t>(ws, L.xq), at<float>(ws, L.xs), T);
+}
+
+__global__ __launch_bounds__(256) void lf_moe_quant_hidden(const int32_t *counts,
+                                                           const int32_t *desc, uint8_t *ws) {
+  const MoeDesc &d = desc_of(desc);
+  if (!desc_ok(d)) return;
+  const int T = live_rows(counts, 1 << 30);
+  const MoeLayout L(d, T);
+  quant_rows(at<uint16_t>(ws, L.h), d.inter, d.group, at<uint8_t>(ws, L.hq), at<float>(ws, L.hs),
+             T * d.top_k);
+}
+
+// Per-channel weight scales with per-token activation scales (group 0) ...
+__global__ __launch_bounds__(256) void lf_moe_gate_up(const int32_t *counts, const int32_t *desc,
+                                                      const uint8_t *wg, const uint8_t *wu,
+                                                      uint8_t *ws) {
+  const MoeDesc &d = desc_of(desc);
+  if (!desc_ok(d) || d.group != 0 || header_of(wg).magic != kWeightMagic) return;
+  grouped_gemm<0, false>(counts, d, wg, wu, ws);
+}
+
+__global__ __launch_bounds__(256) void lf_moe_down(const int32_t *counts, const int32_t *desc,
+                                                   const uint8_t *wd, uint8_t *ws) {
+  const MoeDesc &d = desc_of(desc);
+  if (!desc_ok(d) || d.group != 0 || header_of(wd).magic != kWeightMagic) return;
+  grouped_gemm<1, false>(counts, d, wd, wd, ws);
+}
+
+// ... and 128 x 128 block weight scales with per-token-per-128-column
+// activation scales (group 128).
+__global__ __launch_bounds__(256) void lf_moe_gate_up_b128(const int32_t *counts,
+                                                           const int32_t *desc,
+                                                           const uint8_t *wg, const uint8_t *wu,
+                                                           uint8_t *ws) {
+  const MoeDesc &d = desc_of(desc);
+  if (!desc_ok(d) || d.group != 128 || header_of(wg).magic != kWeightMagic) return;
+  grouped_gemm<0, true>(counts, d, wg, wu, ws);
+}
+
+__global__ __launch_bounds__(256) void lf_moe_down_b128(const int32_t *counts,
+                                                        const int32_t *desc, const uint8_t *wd,
+                                                        uint8_t *ws) {
+  const MoeDesc &d = desc_of(desc);
+  if (!desc_ok(d) || d.group != 128 || header_of(wd).magic != kWeightMagic) return;
+  grouped_gemm<1, true>(counts, d, wd, wd, ws);
+}
+
+__global__ __launch_bounds__(256) void lf_moe_combine(const int32_t *counts, const int32_t *desc,
+                                                      uint8_t *ws, uint16_t *out) {
+  const MoeDesc &d = desc_of(desc);
+  if (!desc_ok(d)) return;
+  combine(counts, d, ws, out);
+}
+
+}  // extern "C"

@@ -206,4 +206,112 @@ int32_t lunaflux_fp8_launch_geometry(int32_t entry, int64_t n, int64_t k,
   return LF_OK;
 }
 
+static bool moe_desc_ok(const lf_fp8_moe_desc *d) {
+  return d != nullptr && d->magic == LF_FP8_MOE_MAGIC && d->experts >= 1 && d->experts <= 256 &&
+         d->top_k >= 1 && d->top_k <= d->experts && d->top_k <= 16 &&
+         (d->route_mode == 0 || d->route_mode == 1) && d->hidden > 0 && d->inter > 0 &&
+         d->hidden % 128 == 0 && d->inter % 128 == 0 &&
+         (d->group == 0 || (d->group == 128 && d->hidden <= 4096 && d->inter <= 4096));
+}
+
+int32_t lunaflux_fp8_moe_descriptor(int32_t experts, int32_t top_k, int32_t route_mode,
+                                    int64_t hidden, int64_t inter, int32_t group,
+                                    lf_fp8_moe_desc *out) {
+  if (out == nullptr || hidden > kMaxDim || inter > kMaxDim) return LF_INVALID_ARGUMENT;
+  lf_fp8_moe_desc d;
+  std::memset(&d, 0, sizeof(d));
+  d.magic = LF_FP8_MOE_MAGIC;
+  d.experts = experts;
+  d.top_k = top_k;
+  d.route_mode = route_mode;
+  d.hidden = static_cast<int32_t>(hidden);
+  d.inter = static_cast<int32_t>(inter);
+  d.group = group;
+  if (!moe_desc_ok(&d)) return LF_INVALID_ARGUMENT;
+  *out = d;
+  return LF_OK;
+}
+
+// Mirrors MoeLayout in csrc/kernels/moe.hip.
+int32_t lunaflux_fp8_moe_workspace_layout(const lf_fp8_moe_desc *d, int32_t tokens,
+                                          int64_t offsets[13]) {
+  if (!moe_desc_ok(d) || tokens < 0 || offsets == nullptr) return LF_INVALID_ARGUMENT;
+  const int64_t T = tokens, A = T * d->top_k, H = d->hidden, I = d->inter;
+  const int64_t gx = d->group > 0 ? H / d->group : 1, gh = d->group > 0 ? I / d->group : 1;
+  const int64_t sizes[12] = {
+      A * 4,                  // top-k expert ids
+      A * 4,                  // top-k weights
+      A * 4,                  // sorted assignments
+      A * 4,                  // position of each assignment
+      (d->experts + 1) * 4,   // expert row offsets
+      (d->experts + 1) * 4,   // expert tile offsets
+      T * H,                  // quantized tokens
+      T * gx * 4,             // token scales
+      A * I * 2,              // h (bf16)
+      A * I,                  // quantized h
+      A * gh * 4,             // h scales
+      A * H * 4,              // y (fp32)
+  };
+  int64_t o = 0;
+  for (int i = 0; i < 12; ++i) {
+    offsets[i] = o;
+    o = align_up(o + sizes[i], 256);
+  }
+  offsets[12] = o;
+  return LF_OK;
+}
+
+int64_t lunaflux_fp8_moe_workspace_bytes(const lf_fp8_moe_desc *d, int32_t max_tokens) {
+  int64_t offsets[13];
+  if (max_tokens <= 0 || lunaflux_fp8_moe_workspace_layout(d, max_tokens, offsets) != LF_OK) {
+    return -1;
+  }
+  return offsets[12];
+}
+
+int32_t lunaflux_fp8_moe_launch_geometry(int32_t entry, const lf_fp8_moe_desc *d,
+                                         int32_t max_tokens, int32_t dims[7],
+                                         char symbol[LF_FP8_SYMBOL_BYTES]) {
+  if (!moe_desc_ok(d) || max_tokens <= 0 || dims == nullptr || symbol == nullptr) {
+    return LF_INVALID_ARGUMENT;
+  }
+  const int64_t T = max_tokens, A = T * d->top_k;
+  // Upper bound on the 128-row tiles over all experts: each expert adds at
+  // most one partial tile.
+  const int64_t tiles = A / 128 + d->experts;
+  const bool b128 = d->group == 128;
+  int64_t gx = 1, gy = 1;
+  int32_t bx = 256;
+  const char *name = nullptr;
+  switch (entry) {
+    case LF_FP8_MOE_ROUTE: name = "lf_moe_route"; gx = (T + 255) / 256; break;
+    case LF_FP8_MOE_SORT: name = "lf_moe_sort"; bx = 1024; break;
+    case LF_FP8_MOE_QUANT_TOKENS: name = "lf_moe_quant_tokens"; gx = T; break;
+    case LF_FP8_MOE_GATE_UP:
+      name = b128 ? "lf_moe_gate_up_b128" : "lf_moe_gate_up";
+      gx = d->inter / 64;
+      gy = tiles;
+      break;
+    case LF_FP8_MOE_QUANT_HIDDEN: name = "lf_moe_quant_hidden"; gx = A; break;
+    case LF_FP8_MOE_DOWN:
+      name = b128 ? "lf_moe_down_b128" : "lf_moe_down";
+      gx = d->hidden / 128;
+      gy = tiles;
+      break;
+    case LF_FP8_MOE_COMBINE: name = "lf_moe_combine"; gx = T; break;
+    default: return LF_INVALID_ARGUMENT;
+  }
+  if (gx > INT32_MAX || gy > LF_MAX_GRID_YZ) return LF_INVALID_ARGUMENT;
+  dims[0] = static_cast<int32_t>(gx);
+  dims[1] = static_cast<int32_t>(gy);
+  dims[2] = 1;
+  dims[3] = bx;
+  dims[4] = 1;
+  dims[5] = 1;
+  dims[6] = 0;
+  std::memset(symbol, 0, LF_FP8_SYMBOL_BYTES);
+  std::strncpy(symbol, name, LF_FP8_SYMBOL_BYTES - 1);
+  return LF_OK;
+}
+
 }  // extern "C"

@@ -1,0 +1,156 @@
+"""Host side of the grouped (MoE expert MLP) form of the FP8 path.
+
+The reference has no MoE operation; this module binds the launch sequence
+documented in include/lunaflux_fp8.h (route -> stable sort -> token
+quantization -> grouped gate/up + SwiGLU -> hidden quantization -> grouped
+down -> top-k combine) to device regions, and offers a numpy-level call,
+`moe_expert_mlp`, for tests and tools.
+"""
+from __future__ import annotations
+
+import ctypes
+from dataclasses import dataclass
+
+import numpy as np
+
+from . import _abi
+from .device import DeviceError, KernelArgument, KernelArguments, KernelLaunchDimensions
+from .fp8 import COUNTS_BYTES, BoundOperation, Fp8Weight, LaunchStep, ProjectionRuntime, _region
+
+ROUTE_TOPK_SOFTMAX = 0   # Mixtral: softmax over the k picked logits
+ROUTE_SOFTMAX_TOPK = 1   # softmax over all experts, keep the k picked
+
+
+class MoeDescriptor(ctypes.Structure):
+    _fields_ = [("magic", ctypes.c_uint32), ("experts", ctypes.c_int32), ("top_k", ctypes.c_int32),
+                ("route_mode", ctypes.c_int32), ("hidden", ctypes.c_int32), ("inter", ctypes.c_int32),
+                ("group", ctypes.c_int32), ("reserved", ctypes.c_int32)]
+
+    def as_bytes(self) -> np.ndarray:
+        return np.frombuffer(bytes(self), np.uint8).copy()
+
+
+def _check(operation, status):
+    if status != _abi.LF_OK:
+        raise DeviceError(operation, status)
+
+
+def moe_descriptor(experts: int, top_k: int, route_mode: int, hidden: int, inter: int,
+                   group: int = 0) -> MoeDescriptor:
+    d = MoeDescriptor()
+    _check("moe_descriptor", _abi.lib().lunaflux_fp8_moe_descriptor(
+        experts, top_k, route_mode, hidden, inter, group, ctypes.byref(d)))
+    return d
+
+
+def workspace_bytes(desc: MoeDescriptor, max_tokens: int) -> int:
+    n = _abi.lib().lunaflux_fp8_moe_workspace_bytes(ctypes.byref(desc), max_tokens)
+    if n < 0:
+        raise DeviceError("moe_workspace_bytes", _abi.LF_INVALID_ARGUMENT)
+    return n
+
+
+LAYOUT_FIELDS = ("topk_ids", "topk_w", "sorted", "pos", "offsets", "tiles", "xq", "xs", "h", "hq",
+                 "hs", "y", "end")
+
+
+def workspace_layout(desc: MoeDescriptor, tokens: int) -> dict:
+    out = (ctypes.c_int64 * 13)()
+    _check("moe_workspace_layout", _abi.lib().lunaflux_fp8_moe_workspace_layout(
+        ctypes.byref(desc), tokens, out))
+    return dict(zip(LAYOUT_FIELDS, (int(v) for v in out)))
+
+
+def launch_geometry(entry: int, desc: MoeDescriptor, max_tokens: int):
+    dims = (ctypes.c_int32 * 7)()
+    symbol = ctypes.create_string_buffer(128)
+    _check("moe_launch_geometry", _abi.lib().lunaflux_fp8_moe_launch_geometry(
+        entry, ctypes.byref(desc), max_tokens, dims, symbol))
+    return (KernelLaunchDimensions.new(tuple(dims[0:3]), tuple(dims[3:6]), dims[6]),
+            symbol.value.decode("ascii"))
+
+
+@dataclass
+class BoundMoe(BoundOperation):
+    desc: MoeDescriptor = None
+
+
+def bind_moe(rt: ProjectionRuntime, counts, desc: MoeDescriptor, desc_region: KernelArgument,
+             logits: KernelArgument, x: KernelArgument, wg: Fp8Weight, wu: Fp8Weight,
+             wd: Fp8Weight, out: KernelArgument, max_tokens: int) -> BoundMoe:
+    """Binds one MoE expert-MLP operation to its regions: 7 launch steps."""
+    e, h, i = desc.experts, desc.hidden, desc.inter
+    mode = _abi.LF_FP8_SCALE_BLOCK128 if desc.group == 128 else _abi.LF_FP8_SCALE_PER_CHANNEL
+    for w, rows, cols in ((wg, i, h), (wu, i, h), (wd, h, i)):
+        if (w.experts, w.rows, w.columns, w.scale_mode) != (e, rows, cols, mode):
+            raise DeviceError("moe weight shape", _abi.LF_INVALID_ARGUMENT)
+    ws = rt.context.allocate(workspace_bytes(desc, max_tokens))
+    wsr = _region(ws, alignment=256)
+    c = _region(counts, COUNTS_BYTES, alignment=4)
+
+    def step(entry, operands):
+        dims, symbol = launch_geometry(entry, desc, max_tokens)
+        return LaunchStep(rt.function(symbol), dims, KernelArguments(operands), symbol)
+
+    steps = [
+        step(_abi.MOE_ROUTE, [c, desc_region, logits, wsr]),
+        step(_abi.MOE_SORT, [c, desc_region, wsr]),
+        step(_abi.MOE_QUANT_TOKENS, [c, desc_region, x, wsr]),
+        step(_abi.MOE_GATE_UP, [c, desc_region, wg.region, wu.region, wsr]),
+        step(_abi.MOE_QUANT_HIDDEN, [c, desc_region, wsr]),
+        step(_abi.MOE_DOWN, [c, desc_region, wd.region, wsr]),
+        step(_abi.MOE_COMBINE, [c, desc_region, wsr, out]),
+    ]
+    return BoundMoe(steps=steps, workspace=ws, desc=desc)
+
+
+def moe_expert_mlp(rt: ProjectionRuntime, x: np.ndarray, logits: np.ndarray, wg: Fp8Weight,
+                   wu: Fp8Weight, wd: Fp8Weight, top_k: int, route_mode: int, group: int = 0,
+                   max_tokens: int | None = None, return_workspace: bool = False):
+    """x bf16 bits [T, H], logits fp32 [T, E] -> out bf16 bits [T, H]. With
+    return_workspace, also returns the routing intermediates read back from
+    the device (top-k ids and weights, sorted assignments, positions, expert
+    row and tile offsets)."""
+    x = np.ascontiguousarray(x, np.uint16)
+    logits = np.ascontiguousarray(logits, np.float32)
+    t, hdim = x.shape
+    e = logits.shape[1]
+    desc = moe_descriptor(e, top_k, route_mode, hdim, wg.rows, group)
+    max_tokens = max(t, 1) if max_tokens is None else max_tokens
+    if t > max_tokens:
+        raise DeviceError("tokens exceed max_tokens", _abi.LF_INVALID_ARGUMENT)
+    ctx = rt.context
+    xa = ctx.allocate(max_tokens * hdim * 2)
+    xa.copy_from_host(x)
+    la = ctx.allocate(max_tokens * e * 4)
+    la.copy_from_host(logits)
+    da = ctx.upload(desc.as_bytes())
+    oa = ctx.allocate(max_tokens * hdim * 2)
+    counts = rt.step_counts(t, decode=False)
+    op = bind_moe(rt, counts, desc, _region(da, 32, alignment=4), _region(la, alignment=256),
+                  _region(xa, alignment=256), wg, wu, wd, _region(oa, alignment=256), max_tokens)
+    op.launch(rt.stream, synchronous=True)
+    out = oa.read(np.uint16, (t, hdim)) if t else np.zeros((0, hdim), np.uint16)
+    if not return_workspace:
+        return out
+    lay = workspace_layout(desc, t)
+    a = t * top_k
+    ws = op.workspace
+    i = wg.rows
+    gx = hdim // group if group else 1
+    gh = i // group if group else 1
+    inter = dict(
+        topk_ids=ws.read(np.int32, (t, top_k), lay["topk_ids"]),
+        topk_w=ws.read(np.float32, (t, top_k), lay["topk_w"]),
+        sorted=ws.read(np.int32, (a,), lay["sorted"]),
+        pos=ws.read(np.int32, (a,), lay["pos"]),
+        offsets=ws.read(np.int32, (e + 1,), lay["offsets"]),
+        tiles=ws.read(np.int32, (e + 1,), lay["tiles"]),
+        xq=ws.read(np.uint8, (t, hdim), lay["xq"]),
+        xs=ws.read(np.float32, (t, gx), lay["xs"]),
+        h=ws.read(np.uint16, (a, i), lay["h"]),
+        hq=ws.read(np.uint8, (a, i), lay["hq"]),
+        hs=ws.read(np.float32, (a, gh), lay["hs"]),
+        y=ws.read(np.float32, (a, hdim), lay["y"]),
+    )
+    return out, inter

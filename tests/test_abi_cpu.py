@@ -37,7 +37,9 @@ def test_library_exports_every_declared_symbol():
 def test_code_object_has_every_entry_point():
     image = _abi.code_object_bytes()
     for symbol in ["lf_fp8_act_quant_rows", "lf_fp8_w8a8_dense", "lf_fp8_w8a8_qkv",
-                   "lf_fp8_w8a8_gate_up"] + [f"lf_fp8_w8a16_{op}_m{m}" for op in ("dense", "qkv", "gate_up")
+                   "lf_fp8_w8a8_gate_up", "lf_moe_route", "lf_moe_sort", "lf_moe_quant_tokens",
+                   "lf_moe_gate_up", "lf_moe_gate_up_b128", "lf_moe_quant_hidden", "lf_moe_down",
+                   "lf_moe_down_b128", "lf_moe_combine"] + [f"lf_fp8_w8a16_{op}_m{m}" for op in ("dense", "qkv", "gate_up")
                                              for m in (16, 32, 64, 128)]:
         assert symbol.encode() + b"\0" in image, symbol
 
@@ -160,3 +162,26 @@ def test_golden_config1_reproduces_from_seed():
     np.testing.assert_array_equal(s, g["s"])
     y = o.dense_projection(o.bf16_decode(x), o.dequantize(q, s))
     np.testing.assert_array_equal(y, g["y32"])
+
+
+def test_moe_descriptor_layout_and_geometry():
+    from lunaflux_amd import moe
+    d = moe.moe_descriptor(8, 2, 0, 4096, 14336, 0)
+    raw = d.as_bytes()
+    assert raw.size == 32 and bytes(raw[:4]) == b"LMOE"
+    lay = moe.workspace_layout(d, 1024)
+    assert lay["end"] == moe.workspace_bytes(d, 1024)
+    a = 1024 * 2
+    assert lay["topk_w"] == a * 4 and lay["y"] + a * 4096 * 4 == lay["end"]
+    assert all(v % 256 == 0 for v in lay.values())
+    dims, sym = moe.launch_geometry(4, d, 1024)   # gate/up
+    assert sym == "lf_moe_gate_up" and dims.grid == (14336 // 64, a // 128 + 8, 1)
+    dims, sym = moe.launch_geometry(2, d, 1024)   # sort: one block of 1024
+    assert sym == "lf_moe_sort" and dims.grid == (1, 1, 1) and dims.block == (1024, 1, 1)
+    d5 = moe.moe_descriptor(64, 6, 1, 2048, 1408, 128)
+    dims, sym = moe.launch_geometry(6, d5, 4096)  # down, block scales
+    assert sym == "lf_moe_down_b128" and dims.grid == (2048 // 128, 4096 * 6 // 128 + 64, 1)
+    for bad in [(0, 1, 0, 256, 256, 0), (8, 9, 0, 256, 256, 0), (8, 2, 2, 256, 256, 0),
+                (8, 2, 0, 200, 256, 0), (8, 2, 0, 256, 256, 64), (8, 2, 0, 8192, 256, 128)]:
+        with pytest.raises(fp8.DeviceError):
+            moe.moe_descriptor(*bad)

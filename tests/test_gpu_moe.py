@@ -1,0 +1,157 @@
+"""GPU parity of the MoE expert-MLP path against the CPU oracle.
+
+Bit-exact: routing ids (ties to the lower expert), the stable sort, the
+inverse positions, per-expert row and tile offsets, the token quantizer and
+the hidden-state quantizer (applied to the GPU's h). Routing weights: within
+fp32 rounding of expf. Each GEMM stage meets the BASELINE bar (relative L2
+<= 1e-3, max-abs <= 2e-2 against the bf16-rounded oracle) on that stage's
+actual inputs: gate/up + SwiGLU from the quantized tokens, down from the
+GPU's quantized h, the combine from the GPU's y and routing weights.
+
+End to end from the original inputs the bound is rel-L2 <= 1e-2: h is
+rounded to bf16 and re-quantized to e4m3 between the two GEMMs, so a one-ulp
+difference in h (fp32 summation order) can flip an e4m3 code and move that
+element by up to half an e4m3 step (6% relative); the measured end-to-end
+rel-L2 is 1e-3 .. 4e-3 while every stage is at ~3e-4.
+"""
+import numpy as np
+import pytest
+
+import oracle_lib as o
+from lunaflux_amd import synth
+from parity import parity
+
+pytestmark = pytest.mark.gpu
+
+
+@pytest.fixture(scope="module")
+def rt():
+    from lunaflux_amd.fp8 import ProjectionRuntime
+    return ProjectionRuntime(0)
+
+
+def expert_weights(rng, experts, rows, cols, block):
+    qs, ss = [], []
+    for _ in range(experts):
+        q, s = synth.weight(rng, rows, cols, block=128 if block else None)
+        qs.append(q)
+        ss.append(s)
+    return np.stack(qs), np.stack(ss)
+
+
+def dequant_experts(q, s, block):
+    return np.stack([o.dequantize(q[e], s[e], mode=2 if block else 0, group=128 if block else 0)
+                     for e in range(q.shape[0])])
+
+
+def run_case(rt, rng, t, e, k, hidden, inter, mode, block, logits=None, max_tokens=None):
+    from lunaflux_amd import fp8, moe
+    x = synth.activations(rng, t, hidden)
+    if logits is None:
+        logits = (rng.standard_normal((t, e)) + rng.normal(0, 1.5, e)).astype(np.float32)
+    qg, sg = expert_weights(rng, e, inter, hidden, block)
+    qu, su = expert_weights(rng, e, inter, hidden, block)
+    qd, sd = expert_weights(rng, e, hidden, inter, block)
+    smode = fp8.BLOCK128 if block else fp8.PER_CHANNEL
+    wg, wu, wd = (rt.upload_weight(q, s, smode) for q, s in ((qg, sg), (qu, su), (qd, sd)))
+    out, inter_state = moe.moe_expert_mlp(rt, x, logits, wg, wu, wd, k, mode, 128 if block else 0,
+                                          max_tokens=max_tokens, return_workspace=True)
+    return x, logits, (qg, sg, qu, su, qd, sd), out, inter_state
+
+
+def check_routing(logits, k, mode, st):
+    ex, w = o.route_topk(logits, k, mode)
+    np.testing.assert_array_equal(st["topk_ids"], ex)
+    np.testing.assert_allclose(st["topk_w"], w, rtol=2e-6, atol=1e-7)
+    sorted_a, offsets = o.moe_sort(ex, logits.shape[1])
+    np.testing.assert_array_equal(st["sorted"], sorted_a)
+    np.testing.assert_array_equal(st["offsets"], offsets)
+    inv = np.empty_like(sorted_a)
+    inv[sorted_a] = np.arange(sorted_a.size)
+    np.testing.assert_array_equal(st["pos"], inv)
+    counts = np.diff(offsets)
+    np.testing.assert_array_equal(st["tiles"], np.concatenate([[0], np.cumsum((counts + 127) // 128)]))
+    return ex, w
+
+
+def check_output(x, weights, ex, w, out, block, label, st):
+    """Stage by stage, each against the oracle on the stage's actual inputs
+    (the hidden state is quantized to e4m3 between the two GEMMs, so a one-ulp
+    difference in h can legitimately flip an e4m3 code; the end-to-end
+    comparison is therefore reported with a looser, documented bound)."""
+    qg, sg, qu, su, qd, sd = weights
+    mode, grp = (1, 128) if block else (0, 0)
+    xf = o.bf16_decode(x)
+    xq, xs = o.quantize_rows(xf, group=grp or None)
+    # 1. token quantization: bit-exact
+    np.testing.assert_array_equal(st["xq"], xq)
+    np.testing.assert_array_equal(st["xs"].reshape(xs.shape[0], -1), xs.reshape(xs.shape[0], -1))
+    xr = o.dequantize(xq, xs, mode=mode, group=grp)
+    wg_f, wu_f, wd_f = (dequant_experts(q, s, block) for q, s in ((qg, sg), (qu, su), (qd, sd)))
+    k = ex.shape[1]
+    sorted_a = st["sorted"]
+    experts = ex.reshape(-1)[sorted_a]
+    tokens = sorted_a // k
+    h_ref = np.zeros(st["h"].shape, np.float32)
+    y_ref = np.zeros(st["y"].shape, np.float32)
+    hg = o.bf16_decode(st["h"])
+    hq_ref, hs_ref = o.quantize_rows(hg, group=grp or None)
+    # 3. hidden quantization of the GPU's h: bit-exact
+    np.testing.assert_array_equal(st["hq"], hq_ref)
+    np.testing.assert_array_equal(st["hs"].reshape(hs_ref.shape[0], -1), hs_ref.reshape(hs_ref.shape[0], -1))
+    hr = o.dequantize(hq_ref, hs_ref, mode=mode, group=grp)
+    for e in np.unique(experts):
+        rows = np.flatnonzero(experts == e)
+        xe = xr[tokens[rows]]
+        h_ref[rows] = o.silu_mul_array(o.dense_projection(xe, wg_f[e]), o.dense_projection(xe, wu_f[e]))
+        y_ref[rows] = o.dense_projection(hr[rows], wd_f[e])
+    # 2. grouped gate/up + SwiGLU
+    parity(st["h"], h_ref, label=label + " gate_up")
+    # 4. grouped down on the GPU's quantized h
+    parity(o.bf16_round(st["y"]), y_ref, k=hr.shape[1], s_abs=None, label=label + " down")
+    # 5. combine of the GPU's y with the GPU's routing weights
+    comb = np.zeros(out.shape, np.float32)
+    for j in range(k):
+        comb = (comb + (st["topk_w"][:, j:j + 1] * st["y"][st["pos"].reshape(-1, k)[:, j]]).astype(np.float32)).astype(np.float32)
+    parity(out, comb, label=label + " combine")
+    # end to end against the oracle from the original inputs
+    ref = o.moe_mlp(xr, wg_f, wu_f, wd_f, ex, w, hidden_transform=5 if block else 3, threads=8)
+    parity(out, ref, rel_l2=1e-2, max_abs=0.25, label=label + " end-to-end")
+
+
+@pytest.mark.parametrize("t,e,k,mode", [(100, 8, 2, 0), (37, 64, 6, 1), (1, 8, 2, 0), (300, 16, 4, 0)])
+def test_moe_per_channel(rt, t, e, k, mode):
+    rng = np.random.default_rng(700 + t + e)
+    x, logits, weights, out, st = run_case(rt, rng, t, e, k, 256, 384, mode, block=False)
+    ex, w = check_routing(logits, k, mode, st)
+    check_output(x, weights, ex, w, out, False, f"moe per-channel t={t} e={e} k={k}", st)
+
+
+@pytest.mark.parametrize("t,e,k,mode,max_tokens", [(64, 16, 6, 1, 64), (5, 64, 6, 1, 32),
+                                                   (130, 8, 2, 0, 256)])
+def test_moe_block128(rt, t, e, k, mode, max_tokens):
+    rng = np.random.default_rng(800 + t + e)
+    x, logits, weights, out, st = run_case(rt, rng, t, e, k, 256, 384, mode, block=True,
+                                           max_tokens=max_tokens)
+    ex, w = check_routing(logits, k, mode, st)
+    check_output(x, weights, ex, w, out, True, f"moe block128 t={t} e={e} k={k}", st)
+
+
+def test_moe_all_tokens_one_expert_and_ties(rt):
+    rng = np.random.default_rng(900)
+    t, e = 300, 8
+    logits = np.zeros((t, e), np.float32)   # every logit tied
+    logits[:, 5] = 4.0                      # expert 5 always first
+    x, logits, weights, out, st = run_case(rt, rng, t, e, 2, 256, 256, 0, block=False,
+                                           logits=logits)
+    ex, w = check_routing(logits, 2, 0, st)
+    assert (ex[:, 0] == 5).all() and (ex[:, 1] == 0).all()   # ties go to the lowest id
+    assert st["offsets"].tolist() == [0, 300, 300, 300, 300, 300, 600, 600, 600]
+    check_output(x, weights, ex, w, out, False, "moe one expert", st)
+
+
+def test_moe_zero_tokens(rt):
+    rng = np.random.default_rng(901)
+    x, logits, weights, out, st = run_case(rt, rng, 0, 8, 2, 256, 256, 0, block=False,
+                                           max_tokens=16)
+    assert out.shape == (0, 256)
