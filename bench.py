@@ -150,6 +150,27 @@ class Bench:
         return total, probe_ms, total / steps
 
 
+    def time_kernel(self, m, call, launches, warmup=5):
+        """Average duration of one launch of the last kernel of `call`: HIP
+        events on the launch stream around `launches` back-to-back launches
+        (rotating over the weight copies); earlier steps of the call (the
+        act-quant prologue) run once beforehand, as their output is reused."""
+        ops = self.ops.get(m, (None, None))[1] or self.bind(m)
+        stream, ctx = self.rt.stream, self.rt.context
+        for r in range(ROTATIONS):
+            for s in ops[r][call].steps[:-1]:
+                s.launch(stream, synchronous=False)
+        for i in range(warmup):
+            ops[i % ROTATIONS][call].steps[-1].launch(stream, synchronous=False)
+        start, stop = ctx.create_event(), ctx.create_event()
+        start.record(stream)
+        for i in range(launches):
+            ops[i % ROTATIONS][call].steps[-1].launch(stream, synchronous=False)
+        stop.record(stream)
+        stop.synchronize()
+        return start.elapsed_milliseconds(stop) / launches
+
+
 def cpu_baseline(m=32, threads=None):
     """The CPU oracle on this host: the four decode calls of one layer at
     M=m over dequantized fp32 weights (sequential-K fp32, as the reference),
@@ -182,6 +203,118 @@ def cpu_baseline(m=32, threads=None):
                       f"weights; {total_s:.2f} s wall on {threads} threads"}
 
 
+MOE_CONFIGS = {
+    # Mixtral-style, 8 experts, top-2, per-channel scales.
+    "mixtral_e8_k2_t1024": dict(tokens=1024, experts=8, top_k=2, hidden=4096, inter=14336,
+                                group=0, route_mode=0, popularity="bias"),
+    # 64 experts, top-6, 128x128 block scales, Zipf(1.1).
+    "fine_e64_k6_t4096": dict(tokens=4096, experts=64, top_k=6, hidden=2048, inter=1408,
+                              group=128, route_mode=1, popularity="zipf"),
+    "fine_e64_k6_t32": dict(tokens=32, experts=64, top_k=6, hidden=2048, inter=1408,
+                            group=128, route_mode=1, popularity="zipf"),
+}
+
+
+def moe_flops(c):
+    a = c["tokens"] * c["top_k"]
+    return 2 * a * c["hidden"] * 2 * c["inter"] + 2 * a * c["inter"] * c["hidden"]
+
+
+def moe_bench(rt, c, steps=5, warmup=2, seed=4242):
+    """Times the seven launches of one MoE expert-MLP operation with events
+    between them. Expert weights are E copies of one seeded draw (kernel time
+    does not depend on the values; it keeps setup short)."""
+    from lunaflux_amd import fp8, moe, synth
+    from lunaflux_amd.fp8 import _region
+    rng = np.random.default_rng(seed)
+    e, k, h, i, t = c["experts"], c["top_k"], c["hidden"], c["inter"], c["tokens"]
+    block = 128 if c["group"] else None
+    mode = fp8.BLOCK128 if block else fp8.PER_CHANNEL
+    weights = []
+    for rows, cols in ((i, h), (i, h), (h, i)):
+        q, s = synth.weight(rng, rows, cols, block=block)
+        region = fp8.pack_weight(np.broadcast_to(q, (e,) + q.shape), np.broadcast_to(s, (e,) + s.shape),
+                                 mode)
+        weights.append(rt.weight_from_region(region))
+    logits = rng.standard_normal((t, e)).astype(np.float32)
+    if c["popularity"] == "bias":
+        logits += rng.normal(0.0, 1.5, e).astype(np.float32)
+    else:  # Zipf(1.1) popularity: log-probability bias by expert rank
+        logits += np.log(1.0 / np.arange(1, e + 1) ** 1.1).astype(np.float32)[rng.permutation(e)]
+    desc = moe.moe_descriptor(e, k, c["route_mode"], h, i, c["group"])
+    ctx = rt.context
+    xa = ctx.upload(synth.activations(rng, t, h))
+    la = ctx.upload(logits)
+    da = ctx.upload(desc.as_bytes())
+    oa = ctx.allocate(t * h * 2)
+    counts = rt.step_counts(t, decode=False)
+    op = moe.bind_moe(rt, counts, desc, _region(da, 32, alignment=4), _region(la, alignment=256),
+                      _region(xa, alignment=256), *weights, _region(oa, alignment=256), t)
+    stream = rt.stream
+    for _ in range(warmup):
+        op.launch(stream, synchronous=False)
+    stream.synchronize()
+    events = [[ctx.create_event() for _ in range(len(op.steps) + 1)] for _ in range(steps)]
+    for it in range(steps):
+        events[it][0].record(stream)
+        for s_i, step in enumerate(op.steps):
+            step.launch(stream, synchronous=False)
+            events[it][s_i + 1].record(stream)
+    events[-1][-1].synchronize()
+    per = [sum(events[it][s_i].elapsed_milliseconds(events[it][s_i + 1]) for it in range(steps)) / steps
+           for s_i in range(len(op.steps))]
+    names = [s.name for s in op.steps]
+    total_ms = sum(per)
+    gemm_ms = per[3] + per[5]
+    fl = moe_flops(c)
+    return {"total_us": round(total_ms * 1e3, 1),
+            "steps_us": {n: round(p * 1e3, 1) for n, p in zip(names, per)},
+            "gemm_us": round(gemm_ms * 1e3, 1),
+            "gemm_TFLOP/s": round(fl / (gemm_ms * 1e-3) / 1e12, 1),
+            "gemm_fp8_frac": round(fl / (gemm_ms * 1e-3) / 1e12 / FP8_PEAK_TFLOPS, 4),
+            "total_TFLOP/s": round(fl / (total_ms * 1e-3) / 1e12, 1),
+            "GFLOP": round(fl / 1e9, 1)}
+
+
+def pmc_pass():
+    """Short run for hardware-counter passes: the roofline kernel (W8A16
+    gate/up at M=32) 10 times, then the calibration copy of 512 MiB 3 times."""
+    from lunaflux_amd import _abi, fp8, synth
+    from lunaflux_amd.device import KernelArguments, KernelLaunchDimensions
+    from lunaflux_amd.fp8 import ProjectionRuntime, _region
+    rt = ProjectionRuntime(0)
+    rng = np.random.default_rng(5)
+    ws = [rt.weight_from_region(fp8.pack_weight(*synth.weight(rng, INTER, HIDDEN))) for _ in range(2)]
+    x = rt.context.upload(synth.activations(rng, 32, HIDDEN))
+    h = rt.context.allocate(32 * INTER * 2)
+    counts = rt.step_counts(32)
+    op = rt.bind_gate_up("w8a16", counts, _region(x, alignment=256), ws[0], ws[1],
+                         _region(h, alignment=256), 32)
+    for _ in range(10):
+        op.launch(rt.stream, synchronous=False)
+    n = 512 << 20
+    src, dst = rt.context.allocate(n), rt.context.allocate(n)
+    cnt = rt.context.upload(np.array([n // 16], np.int64))
+    copy = rt.function("lf_calibrate_copy")
+    args = KernelArguments([_region(cnt, 8, alignment=8), _region(src, alignment=256),
+                            _region(dst, alignment=256)])
+    for _ in range(3):
+        copy.launch_async(KernelLaunchDimensions.new((4096,), (256,)), args, rt.stream)
+    rt.stream.synchronize()
+    log(f"pmc pass done (gate_up x10, copy {n} bytes x3)")
+
+
+def measured_traffic():
+    """HBM bytes per launch of the roofline kernel from the committed counter
+    summary (profiles/lf_fp8_w8a16_gate_up_m32.traffic.json), or None."""
+    path = os.path.join(ROOT, "profiles", "lf_fp8_w8a16_gate_up_m32.traffic.json")
+    try:
+        with open(path) as f:
+            return json.load(f).get("bytes_per_launch")
+    except (OSError, ValueError):
+        return None
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -189,11 +322,15 @@ def main():
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--quick", action="store_true", help="headline only, no detail sweep")
+    ap.add_argument("--pmc-pass", action="store_true", help="short run for counter passes")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU only: --gpus {args.gpus} is not supported "
               "(this build has no multi-GPU path; see DESIGN.md on sharding)", file=sys.stderr)
         sys.exit(2)
+    if args.pmc_pass:
+        pmc_pass()
+        return
 
     from lunaflux_amd.fp8 import ProjectionRuntime
     from lunaflux_amd import device
@@ -205,9 +342,10 @@ def main():
 
     m = 32
     decode = Bench(rt, layer, 32, "w8a16")
-    total, probe_ms, step_ms = decode.run(m, args.steps, args.warmup)
+    total, _, step_ms = decode.run(m, args.steps, args.warmup, probe=None)
     value = layer_bytes(m) / (step_ms * 1e-3) / 1e9
     gu_bytes = call_bytes(m, HIDDEN, 2 * INTER, INTER)
+    probe_ms = decode.time_kernel(m, "gate_up", args.steps)
     achieved = gu_bytes / (probe_ms * 1e-3) / 1e9
     log(f"decode M={m}: {step_ms * 1e3:.1f} us/layer, {value:.0f} GB/s; gate_up {probe_ms * 1e3:.1f} us "
         f"= {achieved:.0f} GB/s")
@@ -218,9 +356,9 @@ def main():
             b = Bench(rt, layer, mt, "w8a16") if mt != 32 else decode
             row = {}
             for c, k, n, no in call_shapes():
-                t, p, s_ms = b.run(mm, 20, 5, calls=(c,), probe=c)
+                p = b.time_kernel(mm, c, 20)
                 row[c] = {"us": round(p * 1e3, 2), "GB/s": round(call_bytes(mm, k, n, no) / (p * 1e-3) / 1e9, 1)}
-            t, _, s_ms = b.run(mm, 20, 5)
+            t, _, s_ms = b.run(mm, 20, 5, probe=None)
             row["layer_us"] = round(s_ms * 1e3, 2)
             row["layer_GB/s"] = round(layer_bytes(mm) / (s_ms * 1e-3) / 1e9, 1)
             row["layer_hbm_frac"] = round(row["layer_GB/s"] / HBM_PEAK_GBS, 4)
@@ -230,7 +368,8 @@ def main():
             b = Bench(rt, layer, mm, "w8a8")
             row = {}
             for c, k, n, no in call_shapes():
-                t, p, s_ms = b.run(mm, 5, 2, calls=(c,), probe=c)
+                p = b.time_kernel(mm, c, 5, warmup=2)
+                t, _, s_ms = b.run(mm, 5, 2, calls=(c,), probe=None)
                 tf = call_flops(mm, k, n) / (p * 1e-3) / 1e12
                 row[c] = {"gemm_us": round(p * 1e3, 1), "TFLOP/s": round(tf, 1),
                           "fp8_frac": round(tf / FP8_PEAK_TFLOPS, 4),
@@ -238,6 +377,10 @@ def main():
             detail["prefill_w8a8"][f"M={mm}"] = row
             log(f"prefill M={mm}: {row}")
             del b
+        detail["moe"] = {}
+        for name, c in MOE_CONFIGS.items():
+            detail["moe"][name] = moe_bench(rt, c)
+            log(f"moe {name}: {detail['moe'][name]}")
 
     cpu = None
     if not args.no_cpu:
@@ -263,7 +406,7 @@ def main():
                    "weight_rotations": ROTATIONS},
         "roofline": {"bound": "hbm", "kernel": "lf_fp8_w8a16_gate_up_m32",
                      "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
+                     "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": measured_traffic(),
                      "algorithmic_bytes_per_launch": gu_bytes,
                      "avg_launch_us": round(probe_ms * 1e3, 2)},
         "cpu_baseline": cpu,

@@ -3,3 +3,4 @@
 #include "projection.hip"
 #include "w8a16.hip"
 #include "moe.hip"
+#include "calibrate.hip"
