@@ -2,7 +2,8 @@
 // activation quantizer and the W8A8 FP8 MFMA GEMM (QKV, output/down,
 // gate/up + SwiGLU). Entry points and operand lists are documented in
 // include/lunaflux_fp8.h; every parameter is a device region.
-#include "w8a8_core.h"
+#include "w8a8_v3.h"
+#include "w8a8_v4.h"
 
 namespace {
 
@@ -70,98 +71,225 @@ __device__ void act_quant_rows(const int32_t *counts, const uint16_t *x, const u
 }
 
 // ---------------------------------------------------------------------------
-// Dense W8A8 GEMM: xq [M, K] e4m3 with per-token scales (the quantizer's
-// output) x weights with per-channel scales. MODE 0: dense, 1: qkv (three
-// weights, packed Q|K|V columns), 2: gate/up with the SwiGLU epilogue (each
-// wave takes 32 h-columns: gate and up tiles of the same columns).
+// W8A8 GEMM: xq [M, K] e4m3 with per-token scales (the quantizer's output) x
+// weights with per-channel scales, y = bf16(acc * sa[m] * sw[n]). MODE 0:
+// dense, 1: qkv (three weights, packed Q|K|V columns), 2: gate/up with the
+// SwiGLU epilogue h = silu(g) * u.
+//
+// This form runs the direct-to-LDS main loop of w8a8_v3.h: BM x BN block of
+// WGM x WGN waves, NS LDS stages, 1-D grid in the XCD-aware tile order
+// (tile_of_block, GROUP row blocks per group). Block-local B slot s holds one 16-column weight tile; for
+// gate/up, wave wn's kFN slots are kFN/2 gate tiles followed by the up tiles
+// of the same columns, so the SwiGLU epilogue pairs accumulators inside a
+// lane. Rows past the live M load a valid row (the last live one); their
+// results are never stored.
 // ---------------------------------------------------------------------------
-template <int MODE>
-__device__ void w8a8_kernel(const int32_t *counts, const uint8_t *xq, const uint8_t *w0,
-                            const uint8_t *w1, const uint8_t *w2, uint16_t *y) {
-  __shared__ __attribute__((aligned(16))) uint8_t As[2][w8a8::kAStage];
+template <class T, int GROUP, int MODE>
+__device__ void w8a8_tiled_kernel(const int32_t *counts, const uint8_t *xq, const uint8_t *w0,
+                                  const uint8_t *w1, const uint8_t *w2, uint16_t *y) {
+  constexpr int BM = T::kWaveM * T::kWgm, BN = T::kWaveN * T::kWgn;
+  __shared__ __attribute__((aligned(1024))) uint8_t smem[T::kSmem];
   const WeightHeader &h0 = header_of(w0);
   if (h0.magic != kWeightMagic) return;
   const int K = static_cast<int>(h0.columns);
   const int KT = K >> 7;
   const int M = live_rows(counts, 1 << 30);
-  const int m0 = blockIdx.y * w8a8::kBM;
-  if (m0 >= M) return;
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  const int wm = wave >> 1, wn = wave & 1;
+  const int tq = static_cast<int>(h0.rows) >> 4;
+  const int tk = MODE == 1 ? static_cast<int>(header_of(w1).rows) >> 4 : 0;
+  const int ld = MODE == 1 ? static_cast<int>(h0.rows + header_of(w1).rows + header_of(w2).rows)
+                           : static_cast<int>(h0.rows);
+  const int gx = MODE == 2 ? ld / (BN / 2) : ld / BN;
+  int bx, by;
+  if (!w8a8v3::tile_of_block(gx, (M + BM - 1) / BM, GROUP, bx, by)) return;
+  const int m0 = by * BM;
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int wm = wave / T::kWgn, wn = wave % T::kWgn;
 
-  const uint8_t *strip[4];
-  const float *wscale[4];
-  int scol[4];  // column inside its weight (scale index)
-  int ocol[4];  // output column
-  int ld;
-  if (MODE == 2) {
-    ld = static_cast<int>(h0.rows);
-    const int c0 = blockIdx.x * 64 + wn * 32;
-#pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      const uint8_t *reg = j < 2 ? w0 : w1;
-      const int col = c0 + (j & 1) * 16;
-      strip[j] = expert_tiles(reg, 0) + static_cast<uint64_t>(col >> 4) * KT * kTileBytes;
-      wscale[j] = expert_scales(reg, 0);
-      scol[j] = col;
-      ocol[j] = col;
-    }
-  } else {
-    const int tq = static_cast<int>(h0.rows) >> 4;
-    const int tk = MODE == 1 ? static_cast<int>(header_of(w1).rows) >> 4 : 0;
-    ld = MODE == 1 ? static_cast<int>(h0.rows + header_of(w1).rows + header_of(w2).rows)
-                   : static_cast<int>(h0.rows);
-#pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      int t = blockIdx.x * 8 + wn * 4 + j;
-      ocol[j] = t * 16;
-      const uint8_t *reg = w0;
+  // Weight tile of block slot s: region, tile index inside it, output column.
+  auto slot = [&](int s, const uint8_t *&region, int &t, int &ocol) {
+    if (MODE == 2) {
+      const int sw = s / T::kFN, f = s % T::kFN;
+      const bool up = f >= T::kFN / 2;
+      const int col = bx * (BN / 2) + sw * (T::kWaveN / 2) + 16 * (up ? f - T::kFN / 2 : f);
+      region = up ? w1 : w0;
+      t = col >> 4;
+      ocol = col;
+    } else {
+      t = bx * (BN / 16) + s;
+      ocol = t * 16;
+      region = w0;
       if (MODE == 1) {
         if (t >= tq + tk) {
-          reg = w2;
+          region = w2;
           t -= tq + tk;
         } else if (t >= tq) {
-          reg = w1;
+          region = w1;
           t -= tq;
         }
       }
-      strip[j] = expert_tiles(reg, 0) + static_cast<uint64_t>(t) * KT * kTileBytes;
-      wscale[j] = expert_scales(reg, 0);
-      scol[j] = t * 16;
     }
-  }
+  };
 
-  const int arow = tid >> 1;
-  const bool arow_live = m0 + arow < M;
-  const uint4 *asrc = reinterpret_cast<const uint4 *>(
-      xq + static_cast<uint64_t>(m0 + (arow_live ? arow : 0)) * K + (tid & 1) * 64);
-  const float *const no_scale[4] = {nullptr, nullptr, nullptr, nullptr};
-  f32x4 acc[4][4];
-  w8a8::mainloop<false>(asrc, arow_live, strip, KT, As, nullptr, no_scale, acc);
+  w8a8v3::Plan<T> plan;
+#pragma unroll
+  for (int q = 0; q < T::kAIns; ++q) {
+    const int tr = w8a8v3::a_load_row<T>(wave, q, lane);
+    const int row = m0 + tr < M ? m0 + tr : M - 1;
+    plan.a[q] = xq + static_cast<uint64_t>(row) * K + w8a8v3::a_load_chunk(tr, lane) * 16;
+  }
+#pragma unroll
+  for (int q = 0; q < T::kBIns; ++q) {
+    const int half = w8a8v3::b_load_half<T>(wave, q);
+    const uint8_t *region;
+    int t, ocol;
+    slot(half >> 1, region, t, ocol);
+    plan.b[q] = expert_tiles(region, 0) + static_cast<uint64_t>(t) * KT * kTileBytes +
+                (half & 1) * 1024 + lane * 16;
+  }
+  f32x4 acc[T::kFM][T::kFN];
+  w8a8v3::mainloop<T>(plan, KT, smem, acc);
 
   const float *ascale = reinterpret_cast<const float *>(xq + align256(static_cast<uint64_t>(M) * K));
   const int r = lane & 15;
+  const float *wsc[T::kFN];
+  int ocol[T::kFN];
 #pragma unroll
-  for (int i = 0; i < 4; ++i) {
+  for (int j = 0; j < T::kFN; ++j) {
+    const uint8_t *region;
+    int t;
+    slot(wn * T::kFN + j, region, t, ocol[j]);
+    wsc[j] = expert_scales(region, 0) + t * 16 + r;
+  }
+#pragma unroll
+  for (int i = 0; i < T::kFM; ++i) {
 #pragma unroll
     for (int rr = 0; rr < 4; ++rr) {
-      const int m = m0 + w8a8::acc_row(wm, i, lane, rr);
+      const int m = m0 + w8a8v3::acc_row<T>(wm, i, lane, rr);
       if (m >= M) continue;
       const float sa = ascale[m];
       uint16_t *yrow = y + static_cast<uint64_t>(m) * ld;
       if (MODE == 2) {
 #pragma unroll
-        for (int j = 0; j < 2; ++j) {
-          const int col = scol[j] + r;
-          const float gv = acc[i][j][rr] * sa * wscale[j][col];
-          const float uv = acc[i][j + 2][rr] * sa * wscale[j + 2][col];
+        for (int j = 0; j < T::kFN / 2; ++j) {
+          const float gv = acc[i][j][rr] * sa * *wsc[j];
+          const float uv = acc[i][j + T::kFN / 2][rr] * sa * *wsc[j + T::kFN / 2];
           yrow[ocol[j] + r] = static_cast<uint16_t>(f32_to_bf16(silu_mul(gv, uv)));
         }
       } else {
 #pragma unroll
-        for (int j = 0; j < 4; ++j) {
-          const float v = acc[i][j][rr] * sa * wscale[j][scol[j] + r];
-          yrow[ocol[j] + r] = static_cast<uint16_t>(f32_to_bf16(v));
+        for (int j = 0; j < T::kFN; ++j) {
+          yrow[ocol[j] + r] = static_cast<uint16_t>(f32_to_bf16(acc[i][j][rr] * sa * *wsc[j]));
+        }
+      }
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------
+// W8A8 GEMM on the half-step main loop (w8a8_v4.h, 32 x 32 x 64 MFMA): BM x BN
+// block of WGM x WGN waves, NS LDS stages, 1-D grid in the XCD-aware tile
+// order. Operands and epilogues as w8a8_tiled_kernel. Block-local weight tile s
+// (16 columns) maps to an output column through slot(); for gate/up, wave
+// wn's 2 kFN tiles are kFN gate tiles followed by the up tiles of the same
+// columns, so 32-column fragment j (gate) pairs with j + kFN / 2 (up).
+// ---------------------------------------------------------------------------
+template <class T, int GROUP, int MODE>
+__device__ void w8a8_v4_kernel(const int32_t *counts, const uint8_t *xq, const uint8_t *w0,
+                               const uint8_t *w1, const uint8_t *w2, uint16_t *y) {
+  constexpr int BM = T::kBM, BN = T::kBN;
+  __shared__ __attribute__((aligned(1024))) uint8_t smem[T::kSmem];
+  const WeightHeader &h0 = header_of(w0);
+  if (h0.magic != kWeightMagic) return;
+  const int K = static_cast<int>(h0.columns);
+  const int KT = K >> 7;
+  const int M = live_rows(counts, 1 << 30);
+  const int tq = static_cast<int>(h0.rows) >> 4;
+  const int tk = MODE == 1 ? static_cast<int>(header_of(w1).rows) >> 4 : 0;
+  const int ld = MODE == 1 ? static_cast<int>(h0.rows + header_of(w1).rows + header_of(w2).rows)
+                           : static_cast<int>(h0.rows);
+  const int gx = MODE == 2 ? ld / (BN / 2) : ld / BN;
+  int bx, by;
+  if (!w8a8v3::tile_of_block(gx, (M + BM - 1) / BM, GROUP, bx, by)) return;
+  const int m0 = by * BM;
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int wm = wave / T::kWgn, wn = wave % T::kWgn;
+
+  // Weight tile of block-local tile s: region, tile index inside it, output
+  // column of its first column.
+  auto slot = [&](int s, const uint8_t *&region, int &t, int &ocol) {
+    if (MODE == 2) {
+      const int sw = s / (2 * T::kFN), f = s % (2 * T::kFN);
+      const bool up = f >= T::kFN;
+      const int col = bx * (BN / 2) + sw * (T::kWaveN / 2) + 16 * (up ? f - T::kFN : f);
+      region = up ? w1 : w0;
+      t = col >> 4;
+      ocol = col;
+    } else {
+      t = bx * (BN / 16) + s;
+      ocol = t * 16;
+      region = w0;
+      if (MODE == 1) {
+        if (t >= tq + tk) {
+          region = w2;
+          t -= tq + tk;
+        } else if (t >= tq) {
+          region = w1;
+          t -= tq;
+        }
+      }
+    }
+  };
+
+  w8a8v4::Plan<T> plan;
+#pragma unroll
+  for (int q = 0; q < T::kAIns; ++q) {
+    const int tr = w8a8v4::a_load_row<T>(wave, q, lane);
+    const int row = m0 + tr < M ? m0 + tr : M - 1;
+    plan.a[q] = xq + static_cast<uint64_t>(row) * K + w8a8v4::a_load_slot(tr, lane) * 32;
+  }
+#pragma unroll
+  for (int q = 0; q < T::kBIns; ++q) {
+    const uint8_t *region;
+    int t, ocol;
+    slot(w8a8v4::b_load_tile<T>(wave, q), region, t, ocol);
+    plan.b[q] = expert_tiles(region, 0) + static_cast<uint64_t>(t) * KT * kTileBytes + lane * 16;
+  }
+  w8a8v4::f32x16 acc[T::kFM][T::kFN];
+  w8a8v4::mainloop<T>(plan, KT, smem, acc);
+
+  const float *ascale = reinterpret_cast<const float *>(xq + align256(static_cast<uint64_t>(M) * K));
+  const int c = lane & 31;
+  const float *wsc[T::kFN];
+  int ocol[T::kFN];
+#pragma unroll
+  for (int j = 0; j < T::kFN; ++j) {
+    const uint8_t *region;
+    int t;
+    slot((wn * T::kWaveN) / 16 + 2 * j + (c >> 4), region, t, ocol[j]);
+    ocol[j] += c & 15;
+    wsc[j] = expert_scales(region, 0) + t * 16 + (c & 15);
+  }
+#pragma unroll
+  for (int i = 0; i < T::kFM; ++i) {
+#pragma unroll
+    for (int e = 0; e < 16; ++e) {
+      const int m = m0 + wm * T::kWaveM + w8a8v4::acc_row<T>(i, lane, e);
+      if (m >= M) continue;
+      const float sa = ascale[m];
+      uint16_t *yrow = y + static_cast<uint64_t>(m) * ld;
+      if (MODE == 2) {
+#pragma unroll
+        for (int j = 0; j < T::kFN / 2; ++j) {
+          const float gv = acc[i][j][e] * sa * *wsc[j];
+          const float uv = acc[i][j + T::kFN / 2][e] * sa * *wsc[j + T::kFN / 2];
+          yrow[ocol[j]] = static_cast<uint16_t>(f32_to_bf16(silu_mul(gv, uv)));
+        }
+      } else {
+#pragma unroll
+        for (int j = 0; j < T::kFN; ++j) {
+          yrow[ocol[j]] = static_cast<uint16_t>(f32_to_bf16(acc[i][j][e] * sa * *wsc[j]));
         }
       }
     }
@@ -172,29 +300,48 @@ __device__ void w8a8_kernel(const int32_t *counts, const uint8_t *xq, const uint
 
 extern "C" {
 
+#define LF_W8A8_TILED_ENTRIES(NAME, BM, BN, NS, WGM, WGN, GROUP)                              \
+  __global__ __launch_bounds__(64 * WGM * WGN) void lf_fp8_w8a8_dense_##NAME(                   \
+      const int32_t *counts, const uint8_t *xq, const uint8_t *w, uint16_t *y) {                \
+    w8a8_tiled_kernel<w8a8v3::Tile<BM, BN, NS, WGM, WGN>, GROUP, 0>(counts, xq, w, w, w, y);    \
+  }                                                                                             \
+  __global__ __launch_bounds__(64 * WGM * WGN) void lf_fp8_w8a8_qkv_##NAME(                     \
+      const int32_t *counts, const uint8_t *xq, const uint8_t *wq, const uint8_t *wk,           \
+      const uint8_t *wv, uint16_t *y) {                                                         \
+    w8a8_tiled_kernel<w8a8v3::Tile<BM, BN, NS, WGM, WGN>, GROUP, 1>(counts, xq, wq, wk, wv, y); \
+  }                                                                                             \
+  __global__ __launch_bounds__(64 * WGM * WGN) void lf_fp8_w8a8_gate_up_##NAME(                 \
+      const int32_t *counts, const uint8_t *xq, const uint8_t *wg, const uint8_t *wu,           \
+      uint16_t *h) {                                                                            \
+    w8a8_tiled_kernel<w8a8v3::Tile<BM, BN, NS, WGM, WGN>, GROUP, 2>(counts, xq, wg, wu, wu, h); \
+  }
+
+#define LF_W8A8_V4_ENTRIES(NAME, BM, BN, NS, WGM, WGN, GROUP)                                 \
+  __global__ __launch_bounds__(64 * WGM * WGN) void lf_fp8_w8a8_dense_##NAME(                   \
+      const int32_t *counts, const uint8_t *xq, const uint8_t *w, uint16_t *y) {                \
+    w8a8_v4_kernel<w8a8v4::Tile<BM, BN, NS, WGM, WGN>, GROUP, 0>(counts, xq, w, w, w, y);       \
+  }                                                                                             \
+  __global__ __launch_bounds__(64 * WGM * WGN) void lf_fp8_w8a8_qkv_##NAME(                     \
+      const int32_t *counts, const uint8_t *xq, const uint8_t *wq, const uint8_t *wk,           \
+      const uint8_t *wv, uint16_t *y) {                                                         \
+    w8a8_v4_kernel<w8a8v4::Tile<BM, BN, NS, WGM, WGN>, GROUP, 1>(counts, xq, wq, wk, wv, y);    \
+  }                                                                                             \
+  __global__ __launch_bounds__(64 * WGM * WGN) void lf_fp8_w8a8_gate_up_##NAME(                 \
+      const int32_t *counts, const uint8_t *xq, const uint8_t *wg, const uint8_t *wu,           \
+      uint16_t *h) {                                                                            \
+    w8a8_v4_kernel<w8a8v4::Tile<BM, BN, NS, WGM, WGN>, GROUP, 2>(counts, xq, wg, wu, wu, h);    \
+  }
+
+// Production tiles: 256 x 256 (8 waves, 4-stage half-step ring) wherever a
+// launch has at least one tile per CU, 128 x 128 (4 waves, two blocks per
+// CU) otherwise. lunaflux_fp8_launch_geometry picks between them.
+LF_W8A8_V4_ENTRIES(t256, 256, 256, 4, 4, 2, 4)
+LF_W8A8_TILED_ENTRIES(t128, 128, 128, 2, 2, 2, 4)
+
 __global__ __launch_bounds__(256) void lf_fp8_act_quant_rows(const int32_t *counts,
                                                              const uint16_t *x,
                                                              const uint8_t *w, uint8_t *xq) {
   act_quant_rows(counts, x, w, xq);
-}
-
-__global__ __launch_bounds__(256) void lf_fp8_w8a8_dense(const int32_t *counts,
-                                                         const uint8_t *xq, const uint8_t *w,
-                                                         uint16_t *y) {
-  w8a8_kernel<0>(counts, xq, w, w, w, y);
-}
-
-__global__ __launch_bounds__(256) void lf_fp8_w8a8_qkv(const int32_t *counts,
-                                                       const uint8_t *xq, const uint8_t *wq,
-                                                       const uint8_t *wk, const uint8_t *wv,
-                                                       uint16_t *y) {
-  w8a8_kernel<1>(counts, xq, wq, wk, wv, y);
-}
-
-__global__ __launch_bounds__(256) void lf_fp8_w8a8_gate_up(const int32_t *counts,
-                                                           const uint8_t *xq, const uint8_t *wg,
-                                                           const uint8_t *wu, uint16_t *h) {
-  w8a8_kernel<2>(counts, xq, wg, wu, wu, h);
 }
 
 }  // extern "C"

@@ -1,0 +1,240 @@
+// w8a8_v4.h - e4m3 x e4m3 MFMA main loop: direct global-to-LDS loads in
+// 64-deep K half-steps, v_mfma_scale_f32_32x32x64_f8f6f4 (unit scales),
+// fragments double-buffered in registers.
+//
+// Block tile BM x BN, WGM x WGN waves, wave tile (BM/WGM) x (BN/WGN) of
+// 32 x 32 MFMA blocks. K advances in half-steps of 64: half-step s covers
+// half h = s & 1 of k-tile s >> 1, and "half h" is the set of k with
+// (k / 16) % 2 == h, i.e. 16-byte chunks h, h+2, h+4, h+6 of a 128-byte
+// k-tile row. That set is exactly the h-th 1 KiB half of a packed 16 x 128
+// weight tile (lane l of half h holds column l % 16, k = 32 (l / 16) + 16 h
+// + 0..15), so the packed weight format needs no change. Any permutation of
+// K is valid for a dot product as long as A and B agree, which they do.
+//
+// LDS stage (NS of them, a ring):
+//   A: BM rows x 64 bytes. Row r keeps its 4 chunks (slot j = logical chunk
+//      2 j + h) at physical slot j ^ ((r >> 1) & 3), which makes both the
+//      16-row DMA writes and the 32-row fragment reads bank-conflict free.
+//   B: BN / 16 tile halves of 1 KiB, copied verbatim.
+// MFMA operands (lane l, q = l / 32): A row 32 i + l % 32 and B column
+// 32 j + l % 32, each with slots 2q and 2q+1 (32 bytes).
+//
+// Schedule per half-step s: wait until this wave's loads of stage s + 1 have
+// landed, block barrier (stage s + 1 visible everywhere; the slot being
+// refilled was last read two half-steps ago), issue the loads of stage
+// s + NS - 1, then the MFMAs of stage s interleaved with the LDS reads of
+// stage s + 1's fragments into the other register set.
+#pragma once
+
+#include <type_traits>
+
+#include "w8a8_v3.h"
+
+namespace w8a8v4 {
+
+typedef float f32x16 __attribute__((ext_vector_type(16)));
+
+template <int BM, int BN, int NS, int WGM, int WGN>
+struct Tile {
+  static constexpr int kWaves = WGM * WGN, kThreads = 64 * kWaves;
+  static constexpr int kWaveM = BM / WGM, kWaveN = BN / WGN;
+  static constexpr int kFM = kWaveM / 32, kFN = kWaveN / 32;
+  static constexpr int kABytes = BM * 64, kBBytes = BN * 64;
+  static constexpr int kStage = kABytes + kBBytes;
+  static constexpr int kSmem = NS * kStage;
+  static constexpr int kStages = NS, kWgm = WGM, kWgn = WGN, kBM = BM, kBN = BN;
+  // 1 KiB load instructions per wave and half-step: 16 A rows, or one
+  // weight tile half, each.
+  static constexpr int kAIns = BM / (16 * kWaves), kBIns = BN / (16 * kWaves);
+  static constexpr int kIns = kAIns + kBIns;
+  static_assert(NS == 4, "the main loop's schedule is written for a 4-stage ring");
+  static_assert(kSmem <= 160 * 1024, "LDS budget");
+  static_assert(kAIns * 16 * kWaves == BM && kBIns * 16 * kWaves == BN, "load split");
+  static_assert(kWaveM % 32 == 0 && kWaveN % 32 == 0, "wave tile");
+};
+
+LF_DEVICE int a_phys_slot(int row, int slot) { return slot ^ ((row >> 1) & 3); }
+
+// Tile row written by lane `lane` of this wave's A instruction q, and the
+// logical slot it fetches (its physical slot is lane & 3).
+template <class T>
+LF_DEVICE int a_load_row(int wave, int q, int lane) {
+  return 16 * (wave * T::kAIns + q) + (lane >> 2);
+}
+LF_DEVICE int a_load_slot(int row, int lane) { return a_phys_slot(row, lane & 3); }
+// Block-local weight tile loaded by this wave's B instruction q.
+template <class T>
+LF_DEVICE int b_load_tile(int wave, int q) { return wave * T::kBIns + q; }
+
+template <class T>
+struct Plan {
+  // a[q]: global address of this lane's 16 bytes of A instruction q at
+  // k-tile 0, half 0 (row base + 32 * logical slot); b[q]: global address of
+  // its 16 bytes of B instruction q at k-tile 0, half 0 (tile strip base +
+  // 16 * lane).
+  const uint8_t *a[T::kAIns];
+  const uint8_t *b[T::kBIns];
+};
+
+// Block barrier without the memory fence of __syncthreads (which would make
+// the compiler wait for every outstanding LDS read first). The "memory"
+// clobber keeps the compiler from moving loads or stores across it; the
+// ordering the loop needs is enforced with explicit counter waits.
+LF_DEVICE void block_barrier() { asm volatile("s_barrier" ::: "memory"); }
+
+template <class T>
+__device__ void mainloop(const Plan<T> &plan, int KT, uint8_t *smem,
+                         f32x16 (&acc)[T::kFM][T::kFN]) {
+  constexpr int NS = T::kStages;
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int wm = wave / T::kWgn, wn = wave % T::kWgn;
+  const int q = lane >> 5, c = lane & 31;
+  const int S = 2 * KT;
+
+  const uint32_t smem_base = __builtin_amdgcn_readfirstlane(w8a8v3::lds_offset_of(smem));
+  auto issue = [&](int s) {
+    const int kt = s >> 1, h = s & 1;
+    const uint32_t a = smem_base + (s % NS) * T::kStage;
+    const uint32_t b = a + T::kABytes;
+#pragma unroll
+    for (int i = 0; i < T::kAIns; ++i) {
+      w8a8v3::dma16(plan.a[i] + kt * 128 + h * 16, a + (wave * T::kAIns + i) * 1024);
+    }
+#pragma unroll
+    for (int i = 0; i < T::kBIns; ++i) {
+      w8a8v3::dma16(plan.b[i] + kt * kTileBytes + h * 1024,
+                    b + b_load_tile<T>(wave, i) * 1024);
+    }
+  };
+
+  // LDS byte offsets of this lane's fragment reads inside a stage: A block i
+  // at a_off0 / a_off1 (slots 2q, 2q+1) + 2048 i (32 rows further keep the
+  // same swizzle), B block j at b_off + 2048 j and + 256.
+  const int row0 = wm * T::kWaveM + c;
+  const int a_off0 = row0 * 64 + (a_phys_slot(row0, 2 * q) << 4);
+  const int a_off1 = a_off0 ^ 16;
+  const int b_off = T::kABytes + ((wn * T::kWaveN) / 16 + (c >> 4)) * 1024 + (32 * q + (c & 15)) * 16;
+  auto read_a = [&](w8a8::Frag8 &f, int i, const uint8_t *st) {
+    f.h[0] = *reinterpret_cast<const uint4 *>(st + a_off0 + 2048 * i);
+    f.h[1] = *reinterpret_cast<const uint4 *>(st + a_off1 + 2048 * i);
+  };
+  auto read_b = [&](w8a8::Frag8 &f, int j, const uint8_t *st) {
+    f.h[0] = *reinterpret_cast<const uint4 *>(st + b_off + 2048 * j);
+    f.h[1] = *reinterpret_cast<const uint4 *>(st + b_off + 2048 * j + 256);
+  };
+  // The larger operand set ("outer": kOuter fragments) is refilled in place
+  // for the next half-step right after its last MFMA; the smaller ("inner")
+  // set is double-buffered.
+  constexpr bool kOuterN = T::kFN >= T::kFM;
+  constexpr int kOuter = kOuterN ? T::kFN : T::kFM, kInner = kOuterN ? T::kFM : T::kFN;
+  auto read_outer = [&](w8a8::Frag8 &f, int o, const uint8_t *st) {
+    if (kOuterN) read_b(f, o, st); else read_a(f, o, st);
+  };
+  auto read_inner = [&](w8a8::Frag8 (&f)[kInner], const uint8_t *st) {
+#pragma unroll
+    for (int n = 0; n < kInner; ++n) {
+      if (kOuterN) read_a(f[n], n, st); else read_b(f[n], n, st);
+    }
+  };
+  auto stage_ptr = [&](int s) -> const uint8_t * { return smem + (s % NS) * T::kStage; };
+
+  w8a8::Frag8 outer[kOuter];
+  auto mfma_group = [&](const w8a8::Frag8(&cur)[kInner], int o) {
+#pragma unroll
+    for (int n = 0; n < kInner; ++n) {
+      f32x16 &a = kOuterN ? acc[n][o] : acc[o][n];
+      a = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(
+          kOuterN ? cur[n].v : outer[o].v, kOuterN ? outer[o].v : cur[n].v, a, 0, 0, 0, 127, 0,
+          127);
+    }
+  };
+  // One half-step: compute stage s from outer / cur while stage s + 1's
+  // fragments are read into nxt and, behind each outer fragment's last use,
+  // into outer. The first MFMA group goes ahead of the wait and the block
+  // barrier so the matrix pipe stays busy while waves synchronize.
+  // sched_barrier pins this order (the scheduler would otherwise sink each
+  // outer read to just before its use and stall on it). WAIT: stages whose
+  // loads may stay in flight once stage s + 1 has landed (-1: stage s + 1
+  // does not exist: no wait, barrier or reads); ISSUE: whether stage
+  // s + NS - 1 exists. Both are compile-time so the body has no branches.
+  auto step = [&](auto wait_tag, auto issue_tag, w8a8::Frag8(&cur)[kInner],
+                  w8a8::Frag8(&nxt)[kInner], int s) {
+    constexpr int kWait = decltype(wait_tag)::value;
+    constexpr bool kIssue = decltype(issue_tag)::value;
+    const uint8_t *st = stage_ptr(s + 1);
+    mfma_group(cur, 0);
+    __builtin_amdgcn_sched_barrier(0);
+    if constexpr (kWait >= 0) {
+      w8a8v3::wait_vmcnt<kWait * T::kIns>();
+      block_barrier();
+      if constexpr (kIssue) issue(s + NS - 1);
+      read_inner(nxt, st);
+      read_outer(outer[0], 0, st);
+    }
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int o = 1; o < kOuter; ++o) {
+      mfma_group(cur, o);
+      __builtin_amdgcn_sched_barrier(0);
+      if constexpr (kWait >= 0) read_outer(outer[o], o, st);
+      __builtin_amdgcn_sched_barrier(0);
+    }
+  };
+  using W1 = std::integral_constant<int, 1>;
+  using W0 = std::integral_constant<int, 0>;
+  using WNone = std::integral_constant<int, -1>;
+  using Yes = std::true_type;
+  using No = std::false_type;
+
+#pragma unroll
+  for (int i = 0; i < T::kFM; ++i)
+#pragma unroll
+    for (int j = 0; j < T::kFN; ++j)
+#pragma unroll
+      for (int e = 0; e < 16; ++e) acc[i][j][e] = 0.f;
+
+  // Prologue: stages 0 .. min(2, S - 1) in flight; wait for stage 0.
+  w8a8::Frag8 f0[kInner], f1[kInner];
+  issue(0);
+  issue(1);  // S >= 2 always (K is a multiple of 128)
+  if (S > 2) {
+    issue(2);
+    w8a8v3::wait_vmcnt<2 * T::kIns>();
+  } else {
+    w8a8v3::wait_vmcnt<1 * T::kIns>();
+  }
+  block_barrier();
+  read_inner(f0, stage_ptr(0));
+#pragma unroll
+  for (int o = 0; o < kOuter; ++o) read_outer(outer[o], o, stage_ptr(0));
+  // step(s) refills the slot of stage s - 1, whose fragments every wave had
+  // read (and consumed) before reaching step(s)'s barrier. In step(s) the
+  // stages issued so far end at min(s + 2, S - 1), so stage s + 1 has landed
+  // once at most one stage's loads (s + 2) remain.
+  int s = 0;
+  for (; s + 4 < S; s += 2) {
+    step(W1{}, Yes{}, f0, f1, s);
+    step(W1{}, Yes{}, f1, f0, s + 1);
+  }
+  if (S >= 4) {  // s == S - 4: stage S - 1 is issued last
+    step(W1{}, Yes{}, f0, f1, s);
+    step(W1{}, No{}, f1, f0, s + 1);
+    s += 2;
+  }
+  // s == S - 2: nothing left to issue; wait for the last stage.
+  step(W0{}, No{}, f0, f1, s);
+  step(WNone{}, No{}, f1, f0, s + 1);
+}
+
+// Output coordinates of accumulator element e of lane `lane` in 32 x 32
+// block (i, j): row inside the wave tile and column inside the wave tile.
+template <class T>
+LF_DEVICE int acc_row(int i, int lane, int e) {
+  return 32 * i + 8 * (e >> 2) + 4 * (lane >> 5) + (e & 3);
+}
+template <class T>
+LF_DEVICE int acc_col(int j, int lane) {
+  return 32 * j + (lane & 31);
+}
+
+}  // namespace w8a8v4

@@ -4,6 +4,7 @@
 #include "lunaflux_fp8.h"
 #include "lunaflux_hip.h"
 
+#include <cstdint>
 #include <cstdio>
 #include <cstring>
 
@@ -177,19 +178,27 @@ int32_t lunaflux_fp8_launch_geometry(int32_t entry, int64_t n, int64_t k,
     }
     case LF_FP8_ENTRY_W8A8_DENSE:
     case LF_FP8_ENTRY_W8A8_QKV:
-      if (n % 128 != 0) return LF_INVALID_ARGUMENT;
-      name = entry == LF_FP8_ENTRY_W8A8_DENSE ? "lf_fp8_w8a8_dense" : "lf_fp8_w8a8_qkv";
-      gx = static_cast<int32_t>(n / 128);
-      gy = (max_tokens + 127) / 128;
-      bx = 256;
+    case LF_FP8_ENTRY_W8A8_GATE_UP: {
+      // Output columns per block: BN for dense/qkv, BN / 2 h-columns for
+      // gate/up (each block computes BN / 2 gate and BN / 2 up columns).
+      const bool gate_up = entry == LF_FP8_ENTRY_W8A8_GATE_UP;
+      const int64_t cols256 = gate_up ? 128 : 256, cols128 = gate_up ? 64 : 128;
+      if (n % cols128 != 0) return LF_INVALID_ARGUMENT;
+      // 256 x 256 tiles (512 threads) when the launch has at least one tile
+      // per CU of the 256 on an MI355X and the columns divide; 128 x 128
+      // tiles (256 threads, two blocks per CU) otherwise.
+      const int64_t tiles256 = (n % cols256 == 0) ? ((max_tokens + 255) / 256) * (n / cols256) : 0;
+      const bool big = tiles256 >= 256;
+      const int64_t tiles = big ? tiles256 : ((max_tokens + 127) / 128) * (n / cols128);
+      if (tiles > INT32_MAX) return LF_INVALID_ARGUMENT;
+      const char *op = entry == LF_FP8_ENTRY_W8A8_DENSE ? "dense" : entry == LF_FP8_ENTRY_W8A8_QKV ? "qkv" : "gate_up";
+      std::snprintf(buffer, sizeof(buffer), "lf_fp8_w8a8_%s_%s", op, big ? "t256" : "t128");
+      name = buffer;
+      gx = static_cast<int32_t>(tiles);
+      gy = 1;
+      bx = big ? 512 : 256;
       break;
-    case LF_FP8_ENTRY_W8A8_GATE_UP:
-      if (n % 64 != 0) return LF_INVALID_ARGUMENT;
-      name = "lf_fp8_w8a8_gate_up";
-      gx = static_cast<int32_t>(n / 64);
-      gy = (max_tokens + 127) / 128;
-      bx = 256;
-      break;
+    }
     default:
       return LF_INVALID_ARGUMENT;
   }

@@ -36,8 +36,8 @@ def test_library_exports_every_declared_symbol():
 
 def test_code_object_has_every_entry_point():
     image = _abi.code_object_bytes()
-    for symbol in ["lf_fp8_act_quant_rows", "lf_fp8_w8a8_dense", "lf_fp8_w8a8_qkv",
-                   "lf_fp8_w8a8_gate_up", "lf_moe_route", "lf_moe_sort", "lf_moe_quant_tokens",
+    for symbol in ["lf_fp8_act_quant_rows"] + [f"lf_fp8_w8a8_{op}_{t}" for op in ("dense", "qkv", "gate_up")
+                                               for t in ("t128", "t256")] + ["lf_moe_route", "lf_moe_sort", "lf_moe_quant_tokens",
                    "lf_moe_gate_up", "lf_moe_gate_up_b128", "lf_moe_quant_hidden", "lf_moe_down",
                    "lf_moe_down_b128", "lf_moe_combine"] + [f"lf_fp8_w8a16_{op}_m{m}" for op in ("dense", "qkv", "gate_up")
                                              for m in (16, 32, 64, 128)]:
@@ -102,8 +102,16 @@ def test_launch_geometry():
     assert sym == "lf_fp8_w8a16_dense_m32" and dims.grid == (256, 1, 1) and dims.block == (512, 1, 1)
     dims, sym = fp8.launch_geometry(_abi.ENTRY_W8A16_QKV, 6144, 4096, 1)
     assert sym == "lf_fp8_w8a16_qkv_m16" and dims.grid == (384, 1, 1)
+    # W8A8: 256 x 256 tiles (1-D grid, 512 threads) once there is a tile per
+    # CU, 128 x 128 tiles (256 threads) below that or when N does not divide.
     dims, sym = fp8.launch_geometry(_abi.ENTRY_W8A8_GATE_UP, 14336, 4096, 8192)
-    assert sym == "lf_fp8_w8a8_gate_up" and dims.grid == (224, 64, 1) and dims.block == (256, 1, 1)
+    assert sym == "lf_fp8_w8a8_gate_up_t256" and dims.grid == (32 * 112, 1, 1) and dims.block == (512, 1, 1)
+    dims, sym = fp8.launch_geometry(_abi.ENTRY_W8A8_DENSE, 4096, 14336, 2048)
+    assert sym == "lf_fp8_w8a8_dense_t128" and dims.grid == (16 * 32, 1, 1) and dims.block == (256, 1, 1)
+    dims, sym = fp8.launch_geometry(_abi.ENTRY_W8A8_QKV, 6144, 4096, 8000)
+    assert sym == "lf_fp8_w8a8_qkv_t256" and dims.grid == (32 * 24, 1, 1)
+    dims, sym = fp8.launch_geometry(_abi.ENTRY_W8A8_DENSE, 128 * 33, 4096, 8192)
+    assert sym == "lf_fp8_w8a8_dense_t128" and dims.grid == (64 * 33, 1, 1)
     dims, sym = fp8.launch_geometry(_abi.ENTRY_ACT_QUANT_ROWS, 4096, 4096, 2048)
     assert sym == "lf_fp8_act_quant_rows" and dims.grid == (2048, 1, 1)
     with pytest.raises(fp8.DeviceError):

@@ -121,6 +121,44 @@ def test_dense_w8a8(rt, m, k, n, max_tokens):
     check_projection(y, x_ref(x, "w8a8"), deq(q, s), f"dense w8a8 {m}x{k}x{n}")
 
 
+@pytest.mark.parametrize("op,m,k", [
+    ("dense", 300, 128), ("dense", 1, 256), ("dense", 511, 384), ("qkv", 513, 128),
+    ("qkv", 256, 640), ("gate_up", 257, 256), ("gate_up", 40, 128),
+])
+def test_w8a8_large_tile_edges(rt, op, m, k):
+    """The 256 x 256 tile (chosen for max_query_tokens = 4096 at these
+    widths): ragged live rows, the shortest K loops (K = 128, 256: the
+    4-stage ring's prologue and tail cases), and qkv region boundaries that
+    fall inside a block (Nq = 2176, Nk = Nv = 960)."""
+    from lunaflux_amd import _abi, fp8
+    rng = np.random.default_rng(7000 + m + k)
+    max_tokens = 4096
+    x = synth.activations(rng, m, k)
+    xr = x_ref(x, "w8a8")
+    if op == "dense":
+        n = 4096
+        assert fp8.launch_geometry(_abi.ENTRY_W8A8_DENSE, n, k, max_tokens)[1].endswith("_t256")
+        q, s, w = make_weight(rt, rng, n, k)
+        y = rt.dense_projection(x, w, "w8a8", max_tokens=max_tokens)
+        check_projection(y, xr, deq(q, s), f"t256 dense m={m} k={k}")
+    elif op == "qkv":
+        ns = (2176, 960, 960)
+        assert fp8.launch_geometry(_abi.ENTRY_W8A8_QKV, sum(ns), k, max_tokens)[1].endswith("_t256")
+        ws = [make_weight(rt, rng, n, k) for n in ns]
+        y = rt.qkv_projection(x, *(w for _, _, w in ws), family="w8a8", max_tokens=max_tokens)
+        ref = o.qkv_projection(xr, *(deq(q, s) for q, s, _ in ws))
+        wall = np.concatenate([deq(q, s) for q, s, _ in ws])
+        parity(y, ref, k=k, s_abs=abs_sum(xr, wall), label=f"t256 qkv m={m} k={k}")
+    else:
+        inter = 2048
+        assert fp8.launch_geometry(_abi.ENTRY_W8A8_GATE_UP, inter, k, max_tokens)[1].endswith("_t256")
+        qg, sg, wg = make_weight(rt, rng, inter, k)
+        qu, su, wu = make_weight(rt, rng, inter, k)
+        h = rt.gate_up_swiglu(x, wg, wu, family="w8a8", max_tokens=max_tokens)
+        ref = o.silu_mul_array(o.dense_projection(xr, deq(qg, sg)), o.dense_projection(xr, deq(qu, su)))
+        parity(h, ref, label=f"t256 gate_up m={m} k={k}")
+
+
 @pytest.mark.parametrize("family,m,max_tokens", [("w8a16", 3, 16), ("w8a16", 32, 32),
                                                  ("w8a8", 130, 256), ("w8a8", 5, 128)])
 def test_qkv(rt, family, m, max_tokens):
@@ -168,7 +206,7 @@ def test_silu_gated_mlp(rt, family, m, max_tokens):
 
 @pytest.mark.parametrize("op,m,family", [
     ("qkv", 32, "w8a16"), ("gate_up", 32, "w8a16"), ("down", 32, "w8a16"), ("o", 1, "w8a16"),
-    ("qkv", 2048, "w8a8"), ("down", 2048, "w8a8"),
+    ("qkv", 2048, "w8a8"), ("down", 2048, "w8a8"), ("qkv", 8192, "w8a8"), ("gate_up", 8192, "w8a8"),
 ])
 def test_llama3_8b_shapes_sampled(rt, op, m, family):
     """Full Llama-3-8B projection shapes; the oracle checks a column sample
