@@ -36,7 +36,7 @@ sys.path.insert(0, ROOT)
 HBM_PEAK_GBS = 8000.0
 FP8_PEAK_TFLOPS = 5000.0
 BF16_PEAK_TFLOPS = 2500.0
-ROTATIONS = 5
+ROTATIONS = 24  # weight copies cycled per call: 24 x 218 MB keeps the 256 MB MALL from serving reuse
 HIDDEN, INTER, NQ, NKV = 4096, 14336, 4096, 1024
 METRIC = "FP8 proj GB/s & TFLOP/s (% roofline), Llama-3-8B shapes M=1..8192, 1 GPU"
 

@@ -96,8 +96,10 @@ int32_t lunaflux_fp8_unpack_weight(const uint8_t *region, int64_t region_bytes,
  * 161-219):
  *  W8A16 ("decode"): bf16 activations, e4m3 weights dequantized to bf16 in
  *    registers (exact), bf16 MFMA, fp32 accumulation, per-channel scale in
- *    the epilogue. Split-K across the waves of a block; a block owns 16
- *    output columns. Suffix _m16/_m32/_m64/_m128: the profile's largest M.
+ *    the epilogue. A wave owns 16 output columns, a block 4 such tiles over
+ *    one K-slice; the grid is split-K across blocks, reduced in a fixed
+ *    slice order by the last block of each column group through the
+ *    workspace. Suffix _m16/_m32/_m64/_m128: the profile's largest M.
  *  W8A8 ("prefill"): activations quantized per token to e4m3
  *    (lf_fp8_act_quant_rows), e4m3 x e4m3 MFMA (16x16x128 f8f6f4), fp32
  *    accumulation, row scale x channel scale epilogue. 128 x 128 block tile.
@@ -111,6 +113,10 @@ int32_t lunaflux_fp8_unpack_weight(const uint8_t *region, int64_t region_bytes,
  *  *_qkv       (counts, x, wq, wk, wv, y)     y bf16 [M, Nq+Nk+Nv] = Q|K|V
  *  *_gate_up   (counts, x, wg, wu, h)         h bf16 [M, I],
  *                                             h = silu(x Wg^T) * (x Wu^T)
+ * The W8A16 forms take one more operand, ws (after y / h): the split-K
+ * workspace, lunaflux_fp8_w8a16_workspace_bytes(entry, N, K, max) bytes,
+ * zero-filled once when it is allocated (its arrival counters return to zero
+ * at the end of every launch; launches sharing one ws must not overlap).
  * The W8A8 forms take xq (the quantizer's output) in place of x. xq layout:
  * e4m3 codes [M, K] at offset 0, fp32 row scales at offset
  * align256(M * K); its size for a profile is lunaflux_fp8_act_quant_bytes.
@@ -122,6 +128,11 @@ int32_t lunaflux_fp8_unpack_weight(const uint8_t *region, int64_t region_bytes,
 #define LF_FP8_SYMBOL_BYTES 128
 
 int64_t lunaflux_fp8_act_quant_bytes(int64_t max_rows, int64_t columns);
+/* Split-K workspace of a W8A16 entry for (N, K, max_query_tokens): fp32
+ * partial tiles plus one arrival counter per column group; -1 if the shape
+ * is not supported (N % 16, K % 128, max > 128). */
+int64_t lunaflux_fp8_w8a16_workspace_bytes(int32_t entry, int64_t n, int64_t k,
+                                           int32_t max_tokens);
 
 enum lf_fp8_entry {
   LF_FP8_ENTRY_ACT_QUANT_ROWS = 1,

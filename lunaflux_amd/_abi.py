@@ -96,6 +96,7 @@ SIGNATURES = {
     "lunaflux_fp8_pack_weight": (_i32, [_i32, _i64, _i64, _i32, _u8p, _f32p, _u8p, _i64]),
     "lunaflux_fp8_unpack_weight": (_i32, [_u8p, _i64, _u8p, _i64, _f32p, _i64]),
     "lunaflux_fp8_act_quant_bytes": (_i64, [_i64, _i64]),
+    "lunaflux_fp8_w8a16_workspace_bytes": (_i64, [_i32, _i64, _i64, _i32]),
     "lunaflux_fp8_launch_geometry": (_i32, [_i32, _i64, _i64, _i32, _i32p, ctypes.c_char_p]),
     "lunaflux_fp8_moe_descriptor": (_i32, [_i32, _i32, _i32, _i64, _i64, _i32, _vp]),
     "lunaflux_fp8_moe_workspace_bytes": (_i64, [_vp, _i32]),

@@ -1,22 +1,30 @@
 // w8a16.hip - W8A16 (decode regime): bf16 activations x e4m3 weights.
 //
-// A block owns one 16-column tile of each of its NW weights (NW = 2 for
-// gate/up) and splits K across its WAVES waves. Each wave streams its weight
-// tiles with two coalesced 1 KiB loads per tile, keeping kInFlight tiles of
-// weights outstanding in a register ring so HBM latency is covered, converts
-// them to bf16 in registers (exact) and feeds 16x16x32 bf16 MFMAs. The 8 or
-// 4 partial tiles are summed in LDS in a fixed wave order (deterministic),
-// scaled per channel (plus SwiGLU for gate/up) and stored as bf16.
+// Work split. Each wave owns one 16-column output tile (for gate/up: the
+// gate and the up tile of the same 16 h-columns) and a block of WAVES waves
+// owns WAVES adjacent tiles (a "column group") over one K-slice. The grid is
+// column groups x S K-slices (S, the split-K factor, comes from the launch
+// geometry: gridDim.x = groups * S). Every weight byte is read by exactly one
+// wave; the activation slice x[0:M, slice] streams once per block through a
+// two-buffer LDS ring (D k-tiles per buffer) shared by its waves, so
+// activation traffic is (columns per block) times smaller than with one
+// block per tile.
 //
-// Activations: for M <= 32 each wave copies its 16*MT x 128 activation slice
-// per k-tile into a private LDS slab with coalesced 1 KiB loads (prefetched
-// one k-tile ahead) and reads MFMA fragments from there; for larger M the
-// fragments are read straight from global memory.
+// Per wave: weight k-tiles (two coalesced 1 KiB loads each) are kept D deep
+// in flight in a register ring, converted to bf16 in registers (exact) and
+// fed to 16x16x32 bf16 MFMAs whose A fragments come from the LDS ring. The
+// channel scales and the first activation chunk (global_load_lds straight
+// into LDS) are requested first, then the weight ring, so no global latency
+// sits between the last weight byte and the stores.
+//
+// Split-K (S > 1): each block writes its fp32 partial tile to the workspace,
+// then the last block of the column group to arrive (an atomic counter per
+// group; the last block also resets it to 0 for the next launch) sums the S
+// partials in slice order 0..S-1 -- a fixed order, so results do not depend
+// on which block finishes last -- and runs the epilogue (channel scale, SwiGLU
+// for gate/up, bf16 store). No block ever waits for another.
 #include "device_common.h"
-
-#ifndef LF_W16_DENSE_IN_FLIGHT
-#define LF_W16_DENSE_IN_FLIGHT 4
-#endif
+#include "w8a8_v3.h"
 
 namespace {
 
@@ -24,8 +32,6 @@ union Frag16 {
   uint4 u;
   bf16x8 v;
 };
-
-constexpr int kSlabStride = 272;  // one 256-byte k-slice row + 16 bytes of pad
 
 // Converts the 8 e4m3 codes of sub-chunk j (k = 32g + 8j .. +8 of this lane)
 // to a bf16x8 B fragment.
@@ -49,69 +55,161 @@ LF_DEVICE void load_tiles(const uint8_t *const (&strip)[NW], int kt, int lane, u
   }
 }
 
-LF_DEVICE void wait_lds() { asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory"); }
+// LDS activation ring of a block: two buffers of D k-tiles of 16*MT rows of
+// bf16, k-tile-major (one k-tile = 16*MT rows x 256 bytes); row r keeps its
+// 16-byte chunk c at chunk position c ^ (r & 15), so the 16 rows of an MFMA
+// fragment read fall in distinct banks.
+template <int MT, int D>
+struct XRing {
+  static constexpr int kRows = 16 * MT;
+  static constexpr int kKTileBytes = kRows * 256;
+  static constexpr int kBufferBytes = D * kKTileBytes;
+  static constexpr int kBytes = 2 * kBufferBytes;
+  static_assert(kBytes <= 128 * 1024, "LDS budget");
+};
 
-// M <= 32: activations staged through this wave's LDS slab.
-template <int WAVES, int MT, int NW>
-__device__ void accumulate_staged(int M, int K, const uint16_t *__restrict__ x,
-                                  const uint8_t *const (&strip)[NW], uint8_t *slab,
-                                  f32x4 (&acc)[MT][NW]) {
-  constexpr int kInFlight = NW == 1 ? LF_W16_DENSE_IN_FLIGHT : 2;  // k-tiles of weights outstanding
-  constexpr int kRows = 16 * MT, kXq = kRows / 4;
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+// s_waitcnt vmcnt(n * PER) for a wave-uniform n in [1, N].
+template <int PER, int N>
+LF_DEVICE void wait_vm_multiple(int n) {
+  if constexpr (N <= 1) {
+    w8a8v3::wait_vmcnt<PER>();
+  } else {
+    if (n >= N) {
+      w8a8v3::wait_vmcnt<N * PER>();
+    } else {
+      wait_vm_multiple<PER, N - 1>(n);
+    }
+  }
+}
+
+// MODE 0: dense, 1: qkv (three weights, packed Q|K|V output), 2: gate/up.
+template <int WAVES, int MT, int MODE, int D>
+__device__ void w8a16_kernel(const int32_t *counts, const uint16_t *x, const uint8_t *w0,
+                             const uint8_t *w1, const uint8_t *w2, uint16_t *y, uint8_t *ws) {
+  constexpr int NW = MODE == 2 ? 2 : 1;
+  using X = XRing<MT, D>;
+  __shared__ __attribute__((aligned(1024))) uint8_t ring[X::kBytes];
+  __shared__ int last_block;
+
+  const WeightHeader &h0 = header_of(w0);
+  if (h0.magic != kWeightMagic) return;
+  const int K = static_cast<int>(h0.columns);
   const int KT = K >> 7;
-  const int kt0 = (KT * wave) / WAVES, kt1 = (KT * (wave + 1)) / WAVES;
+  const int tq = static_cast<int>(h0.rows) >> 4;
+  const int tk = MODE == 1 ? static_cast<int>(header_of(w1).rows) >> 4 : 0;
+  const int ld = MODE == 1 ? static_cast<int>(h0.rows + header_of(w1).rows + header_of(w2).rows)
+                           : static_cast<int>(h0.rows);
+  const int tiles = ld >> 4;
+  const int groups = (tiles + WAVES - 1) / WAVES;
+  const int S = static_cast<int>(gridDim.x) / groups;
+  if (S < 1) return;  // the geometry rules this out
+  const int cg = static_cast<int>(blockIdx.x) / S;
+  const int s = static_cast<int>(blockIdx.x) - cg * S;
+  const int kt0 = (KT * s) / S, kt1 = (KT * (s + 1)) / S;
+  const int nkt = kt1 - kt0;
+  if (cg >= groups || nkt < 1) return;
+  const int M = live_rows(counts, X::kRows);
+  if (M == 0) return;
+
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int g = lane >> 4, r = lane & 15;
-  const int xrow = lane >> 4, xcol = (lane & 15) * 8;  // coalesced copy mapping
+  const int out_tile = cg * WAVES + wave;
+  const bool active = out_tile < tiles;  // a partial last group has idle waves
+  int t = active ? out_tile : 0;
+  const uint8_t *region[NW];
+  region[0] = w0;
+  if (MODE == 1) {
+    if (t >= tq + tk) {
+      region[0] = w2;
+      t -= tq + tk;
+    } else if (t >= tq) {
+      region[0] = w1;
+      t -= tq;
+    }
+  }
+  if (NW == 2) region[NW - 1] = w1;
+  const uint8_t *strip[NW];
+#pragma unroll
+  for (int i = 0; i < NW; ++i) {
+    strip[i] = expert_tiles(region[i], 0) + static_cast<uint64_t>(t) * KT * kTileBytes;
+  }
+
+  // 0. Channel scales of this lane's column (first: waits for the activation
+  //    loads below never wait for them).
+  float sc[NW];
+#pragma unroll
+  for (int i = 0; i < NW; ++i) sc[i] = expert_scales(region[i], 0)[t * 16 + r];
+
+  // Activation chunk c (k-tiles c D .. c D + D - 1 of the slice) goes straight
+  // into ring buffer c & 1 with global_load_lds: 1 KiB = 4 rows of one k-tile
+  // per instruction, only the ceil(M / 4) row groups that hold live rows
+  // (rows past M re-read row M - 1; their outputs are never stored).
+  const uint32_t ring_base = __builtin_amdgcn_readfirstlane(w8a8v3::lds_offset_of(ring));
+  const int xins = (M + 3) >> 2;
+  const int chunks = (nkt + D - 1) / D;
+  auto load_chunk = [&](int c) {
+    const int n = (nkt - c * D < D ? nkt - c * D : D) * xins;
+    for (int id = wave; id < n; id += WAVES) {
+      const int kl = id / xins, q = id - kl * xins;
+      const int row = 4 * q + (lane >> 4);
+      const int chunk = (lane & 15) ^ (row & 15);
+      const int src = row < M ? row : M - 1;
+      w8a8v3::dma16(reinterpret_cast<const uint8_t *>(x + static_cast<uint64_t>(src) * K +
+                                                      (kt0 + c * D + kl) * 128 + chunk * 8),
+                    ring_base + (c & 1) * X::kBufferBytes + kl * X::kKTileBytes + q * 1024);
+    }
+  };
+  // Weight loads issued after chunk c's activation loads and before the wait
+  // for them: the refills of chunk c - 1 (one k-tile each while k-tiles
+  // remain), i.e. 2 NW per refilled k-tile.
+  auto refills = [&](int c) {
+    const int n = nkt - D - c * D;
+    return n < 0 ? 0 : n > D ? D : n;
+  };
+
+  load_chunk(0);
+  // Weight ring, D k-tiles deep.
+  uint4 b[D][NW][2];
+#pragma unroll
+  for (int d = 0; d < D; ++d) {
+    if (d < nkt) load_tiles<NW>(strip, kt0 + d, lane, b[d]);
+  }
+  wait_vm_multiple<2 * NW, D>(nkt < D ? nkt : D);
+
+  f32x4 acc[MT][NW];
 #pragma unroll
   for (int mt = 0; mt < MT; ++mt)
 #pragma unroll
     for (int i = 0; i < NW; ++i) acc[mt][i] = f32x4{0.f, 0.f, 0.f, 0.f};
-  if (kt0 >= kt1) return;
-
-  // Activation and weight loads of k-tile kt are issued together, kInFlight
-  // k-tiles ahead of their use. Vector-memory completions are counted in
-  // issue order, so waiting for k-tile kt's data never waits for a later
-  // k-tile's loads. Loads of 4-row groups wholly past the live M are not
-  // issued at all (the branch is wave-uniform).
-  uint4 xr[kInFlight][kXq];
-  auto load_x = [&](int kt, uint4 (&dst)[kXq]) {
-#pragma unroll
-    for (int q = 0; q < kXq; ++q) {
-      const int row = 4 * q + xrow;
-      if (4 * q < M) {
-        dst[q] = row < M ? *reinterpret_cast<const uint4 *>(x + static_cast<uint64_t>(row) * K + kt * 128 + xcol)
-                         : make_uint4(0u, 0u, 0u, 0u);
+  // Rows >= M of the ring hold stale LDS contents; they only feed output
+  // rows >= M, which are never stored (MFMA rows are independent).
+  for (int c = 0; c < chunks; ++c) {
+    if (c > 0) {
+      // This wave's share of chunk c landed: only the refills of chunk c - 1
+      // were issued after it.
+      if (refills(c - 1) == D) {
+        w8a8v3::wait_vmcnt<2 * NW * D>();
       } else {
-        dst[q] = make_uint4(0u, 0u, 0u, 0u);
+        w8a8v3::wait_vmcnt<0>();
       }
     }
-  };
-  uint4 b[kInFlight][NW][2];
+    // Every wave's share of chunk c is in LDS, and every wave is done with
+    // chunk c - 1, whose buffer chunk c + 1 now refills.
+    __syncthreads();
+    if (c + 1 < chunks) load_chunk(c + 1);
+    const uint8_t *buf = ring + (c & 1) * X::kBufferBytes;
 #pragma unroll
-  for (int d = 0; d < kInFlight; ++d) {
-    if (kt0 + d < kt1) {
-      load_x(kt0 + d, xr[d]);
-      load_tiles<NW>(strip, kt0 + d, lane, b[d]);
-    }
-  }
-  for (int base = kt0; base < kt1; base += kInFlight) {
-#pragma unroll
-    for (int d = 0; d < kInFlight; ++d) {
-      const int kt = base + d;
-      if (kt < kt1) {
-        wait_lds();  // the previous k-tile's fragment reads are complete
-#pragma unroll
-        for (int q = 0; q < kXq; ++q) {
-          *reinterpret_cast<uint4 *>(slab + (4 * q + xrow) * kSlabStride + xcol * 2) = xr[d][q];
-        }
-        wait_lds();  // the slab holds k-tile kt
+    for (int d = 0; d < D; ++d) {
+      const int kl = c * D + d;
+      if (kl < nkt) {
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
           Frag16 a[MT];
 #pragma unroll
           for (int mt = 0; mt < MT; ++mt) {
-            a[mt].u = *reinterpret_cast<const uint4 *>(slab + (mt * 16 + r) * kSlabStride + g * 64 + j * 16);
+            const int row = mt * 16 + r;
+            a[mt].u = *reinterpret_cast<const uint4 *>(
+                buf + d * X::kKTileBytes + row * 256 + ((((g << 2) | j) ^ (row & 15)) << 4));
           }
 #pragma unroll
           for (int i = 0; i < NW; ++i) {
@@ -122,173 +220,311 @@ __device__ void accumulate_staged(int M, int K, const uint16_t *__restrict__ x,
             }
           }
         }
-        if (kt + kInFlight < kt1) {
-          load_x(kt + kInFlight, xr[d]);
-          load_tiles<NW>(strip, kt + kInFlight, lane, b[d]);
-        }
+        if (kl + D < nkt) load_tiles<NW>(strip, kt0 + kl + D, lane, b[d]);
       }
     }
   }
-}
 
-// M > 32: activation fragments read straight from global memory (L2).
-template <int WAVES, int MT, int NW>
-__device__ void accumulate_direct(int M, int K, const uint16_t *__restrict__ x,
-                                  const uint8_t *const (&strip)[NW], f32x4 (&acc)[MT][NW]) {
-  constexpr int kChunk = 4;
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-  const int KT = K >> 7;
-  const int kt0 = (KT * wave) / WAVES, kt1 = (KT * (wave + 1)) / WAVES;
-  const int g = lane >> 4, r = lane & 15;
+  // Epilogue. Lane element (mt, rr) is output row mt*16 + 4*g + rr of
+  // column out_tile*16 + r (16x16 MFMA accumulator layout).
+  const int col = out_tile * 16 + r;
+  auto finish = [&](int m, const float (&v)[NW]) {
+    const float out = MODE == 2 ? silu_mul(v[0] * sc[0], v[NW - 1] * sc[NW - 1]) : v[0] * sc[0];
+    y[static_cast<uint64_t>(m) * ld + col] = static_cast<uint16_t>(f32_to_bf16(out));
+  };
+  if (S == 1) {
+    if (!active) return;
 #pragma unroll
-  for (int mt = 0; mt < MT; ++mt)
+    for (int mt = 0; mt < MT; ++mt)
 #pragma unroll
-    for (int i = 0; i < NW; ++i) acc[mt][i] = f32x4{0.f, 0.f, 0.f, 0.f};
-  for (int base = kt0; base < kt1; base += kChunk) {
-    uint4 b[kChunk][NW][2];
+      for (int rr = 0; rr < 4; ++rr) {
+        const int m = mt * 16 + 4 * g + rr;
+        if (m < M) {
+          float v[NW];
 #pragma unroll
-    for (int c = 0; c < kChunk; ++c) {
-      if (base + c < kt1) load_tiles<NW>(strip, base + c, lane, b[c]);
-    }
-#pragma unroll
-    for (int c = 0; c < kChunk; ++c) {
-      if (base + c < kt1) {
-        const int kt = base + c;
-        Frag16 a[MT][4];
-#pragma unroll
-        for (int mt = 0; mt < MT; ++mt) {
-          const int m = mt * 16 + r;
-          const uint4 *p = reinterpret_cast<const uint4 *>(x + static_cast<uint64_t>(m) * K + kt * 128 + g * 32);
-#pragma unroll
-          for (int j = 0; j < 4; ++j) a[mt][j].u = m < M ? p[j] : make_uint4(0u, 0u, 0u, 0u);
+          for (int i = 0; i < NW; ++i) v[i] = acc[mt][i][rr];
+          finish(m, v);
         }
+      }
+    return;
+  }
+
+  // Split-K. The workspace holds, per slice, one fp32 accumulator fragment
+  // (4 values per lane: rows 4g..4g+3 of a 16-row tile) for each (tile,
+  // weight, row tile), fragment index ((s * tiles + out_tile) * NW + i) * MT
+  // + mt, then one arrival counter per column group. Row groups wholly past
+  // M are neither stored nor loaded.
+  //
+  // Partials travel through the device-coherent level without any cache
+  // maintenance: agent-scope atomic stores and loads write through / bypass
+  // the per-XCD L2, and this wave's stores are complete (s_waitcnt vmcnt(0))
+  // before the block's arrival is counted. (A device-scope fence would write
+  // back and invalidate the whole L2 of the XCD, once per block.)
+  // Fragment layout: 256 floats, element e of lane l at e * 64 + l, so each
+  // store or load instruction covers 256 contiguous bytes.
+  float *part = reinterpret_cast<float *>(ws);
+  int *arrivals = reinterpret_cast<int *>(
+      ws + align256(static_cast<uint64_t>(S) * tiles * NW * MT * 256 * sizeof(float)));
+  auto frag_at = [&](int slice, int i, int mt) -> float * {
+    return part + ((static_cast<uint64_t>(slice) * tiles + out_tile) * NW * MT + i * MT + mt) * 256 + lane;
+  };
+  if (active) {
 #pragma unroll
-        for (int j = 0; j < 4; ++j) {
+    for (int mt = 0; mt < MT; ++mt) {
+      if (mt * 16 + 4 * g < M) {
 #pragma unroll
-          for (int i = 0; i < NW; ++i) {
-            const bf16x8 bf = weight_fragment(b[c][i], j);
+        for (int i = 0; i < NW; ++i) {
+          float *p = frag_at(s, i, mt);
 #pragma unroll
-            for (int mt = 0; mt < MT; ++mt) {
-              acc[mt][i] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a[mt][j].v, bf, acc[mt][i], 0, 0, 0);
-            }
+          for (int e = 0; e < 4; ++e) {
+            __hip_atomic_store(p + 64 * e, acc[mt][i][e], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
           }
         }
       }
     }
   }
+  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    const int before =
+        __hip_atomic_fetch_add(arrivals + cg, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    const bool last = before == S - 1;
+    // Every block of the group has arrived: reset for the next launch.
+    if (last) __hip_atomic_store(arrivals + cg, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    last_block = last ? 1 : 0;
+  }
+  __syncthreads();
+  if (last_block == 0 || !active) return;
+  // Sum the S partial fragments in slice order (this block's own from its
+  // registers). Loads of kBatch slices are issued before any is added.
+  constexpr int kBatch = 4;
+  f32x4 sum[MT][NW];
+#pragma unroll
+  for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+    for (int i = 0; i < NW; ++i) sum[mt][i] = f32x4{0.f, 0.f, 0.f, 0.f};
+  for (int s0 = 0; s0 < S; s0 += kBatch) {
+    f32x4 v[kBatch][MT][NW];
+#pragma unroll
+    for (int b = 0; b < kBatch; ++b) {
+      const int slice = s0 + b;
+#pragma unroll
+      for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+        for (int i = 0; i < NW; ++i) {
+          if (slice < S && slice != s && mt * 16 + 4 * g < M) {
+            const float *p = frag_at(slice, i, mt);
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+              v[b][mt][i][e] = __hip_atomic_load(p + 64 * e, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            }
+          } else {
+            v[b][mt][i] = acc[mt][i];
+          }
+        }
+    }
+#pragma unroll
+    for (int b = 0; b < kBatch; ++b) {
+      if (s0 + b < S) {
+#pragma unroll
+        for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+          for (int i = 0; i < NW; ++i) sum[mt][i] += v[b][mt][i];
+      }
+    }
+  }
+#pragma unroll
+  for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+    for (int rr = 0; rr < 4; ++rr) {
+      const int m = mt * 16 + 4 * g + rr;
+      if (m < M) {
+        float v[NW];
+#pragma unroll
+        for (int i = 0; i < NW; ++i) v[i] = sum[mt][i][rr];
+        finish(m, v);
+      }
+    }
 }
 
-template <int WAVES, int MT, int NW, bool STAGED>
-struct W16Shared {
-  static constexpr int kSlabBytes = STAGED ? WAVES * 16 * MT * kSlabStride : 0;
-  static constexpr int kRedBytes = WAVES * MT * NW * 64 * 16;
-  static constexpr int kBytes = kSlabBytes > kRedBytes ? kSlabBytes : kRedBytes;
-};
-
-// MODE 0: dense, 1: qkv (three weights, packed Q|K|V output), 2: gate/up.
-template <int WAVES, int MT, int MODE>
-__device__ void w8a16_kernel(const int32_t *counts, const uint16_t *x, const uint8_t *w0,
-                             const uint8_t *w1, const uint8_t *w2, uint16_t *y) {
+// ---------------------------------------------------------------------------
+// One-tile form: a block owns one 16-column tile (NW weights) and its KS waves
+// split K into contiguous ranges; no workspace, no cross-block reduction.
+// A fragments are read straight from global memory (x is small and stays in
+// L2), DA k-tiles ahead of use; weight k-tiles D ahead. The KS partial tiles
+// are summed in LDS in wave order (deterministic).
+// ---------------------------------------------------------------------------
+template <int KS, int MT, int MODE, int D, int DA>
+__device__ void w8a16_tile_kernel(const int32_t *counts, const uint16_t *x, const uint8_t *w0,
+                                  const uint8_t *w1, const uint8_t *w2, uint16_t *y) {
   constexpr int NW = MODE == 2 ? 2 : 1;
-  constexpr bool STAGED = MT <= 2;
-  using Shared = W16Shared<WAVES, MT, NW, STAGED>;
-  // The activation slabs and the reduction buffer share this storage; a
-  // block barrier separates their lifetimes.
-  __shared__ __attribute__((aligned(16))) uint8_t smem[Shared::kBytes];
+  __shared__ __attribute__((aligned(16))) f32x4 red[KS][MT * NW][64];
   const WeightHeader &h0 = header_of(w0);
   if (h0.magic != kWeightMagic) return;
   const int K = static_cast<int>(h0.columns);
+  const int KT = K >> 7;
+  const int tq = static_cast<int>(h0.rows) >> 4;
+  const int tk = MODE == 1 ? static_cast<int>(header_of(w1).rows) >> 4 : 0;
+  const int ld = MODE == 1 ? static_cast<int>(h0.rows + header_of(w1).rows + header_of(w2).rows)
+                           : static_cast<int>(h0.rows);
+  const int out_tile = blockIdx.x;
+  if (out_tile >= (ld >> 4)) return;
   const int M = live_rows(counts, 16 * MT);
-  int tile = blockIdx.x;
-  const int out_col0 = tile * 16;
-  int ld = static_cast<int>(h0.rows);
+  if (M == 0) return;
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int g = lane >> 4, r = lane & 15;
+  int t = out_tile;
   const uint8_t *region[NW];
   region[0] = w0;
   if (MODE == 1) {
-    const int tq = static_cast<int>(h0.rows) >> 4;
-    const int tk = static_cast<int>(header_of(w1).rows) >> 4;
-    ld = static_cast<int>(h0.rows + header_of(w1).rows + header_of(w2).rows);
-    if (tile >= tq + tk) {
+    if (t >= tq + tk) {
       region[0] = w2;
-      tile -= tq + tk;
-    } else if (tile >= tq) {
+      t -= tq + tk;
+    } else if (t >= tq) {
       region[0] = w1;
-      tile -= tq;
+      t -= tq;
     }
   }
   if (NW == 2) region[NW - 1] = w1;
   const uint8_t *strip[NW];
 #pragma unroll
   for (int i = 0; i < NW; ++i) {
-    strip[i] = expert_tiles(region[i], 0) + static_cast<uint64_t>(tile) * (K >> 7) * kTileBytes;
+    strip[i] = expert_tiles(region[i], 0) + static_cast<uint64_t>(t) * KT * kTileBytes;
   }
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  // Channel scales of the column this thread finishes in the epilogue
+  // ((e >> 2) & 15 for its elements e = threadIdx.x + 64 KS i).
+  const int ec = (threadIdx.x >> 2) & 15;
+  float sc[NW];
+#pragma unroll
+  for (int i = 0; i < NW; ++i) sc[i] = expert_scales(region[i], 0)[t * 16 + ec];
+
+  const int kt0 = (KT * wave) / KS, kt1 = (KT * (wave + 1)) / KS;
+  const int nkt = kt1 - kt0;
+  // This lane's A rows (rows past M re-read row M - 1; their outputs are
+  // never stored).
+  const uint16_t *xrow[MT];
+#pragma unroll
+  for (int mt = 0; mt < MT; ++mt) {
+    const int row = mt * 16 + r;
+    xrow[mt] = x + static_cast<uint64_t>(row < M ? row : M - 1) * K + g * 32;
+  }
+  auto load_a = [&](int kt, uint4 (&dst)[MT][4]) {
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt) {
+      const uint4 *p = reinterpret_cast<const uint4 *>(xrow[mt] + kt * 128);
+#pragma unroll
+      for (int j = 0; j < 4; ++j) dst[mt][j] = p[j];
+    }
+  };
+  uint4 b[D][NW][2];
+  uint4 a[DA][MT][4];
+#pragma unroll
+  for (int d = 0; d < D; ++d) {
+    if (d < nkt) load_tiles<NW>(strip, kt0 + d, lane, b[d]);
+    if (d < DA && d < nkt) load_a(kt0 + d, a[d]);
+  }
   f32x4 acc[MT][NW];
-  if constexpr (STAGED) {
-    accumulate_staged<WAVES, MT, NW>(M, K, x, strip, smem + wave * 16 * MT * kSlabStride, acc);
-    __syncthreads();  // every slab is dead before the reduction buffer reuses it
-  } else {
-    accumulate_direct<WAVES, MT, NW>(M, K, x, strip, acc);
+#pragma unroll
+  for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+    for (int i = 0; i < NW; ++i) acc[mt][i] = f32x4{0.f, 0.f, 0.f, 0.f};
+  static_assert(D % DA == 0, "the A ring divides the weight ring");
+  for (int base = 0; base < nkt; base += D) {
+#pragma unroll
+    for (int d = 0; d < D; ++d) {
+      const int kl = base + d;
+      if (kl < nkt) {
+        uint4(&ad)[MT][4] = a[d % DA];
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+#pragma unroll
+          for (int i = 0; i < NW; ++i) {
+            const bf16x8 bf = weight_fragment(b[d][i], j);
+#pragma unroll
+            for (int mt = 0; mt < MT; ++mt) {
+              Frag16 af;
+              af.u = ad[mt][j];
+              acc[mt][i] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(af.v, bf, acc[mt][i], 0, 0, 0);
+            }
+          }
+        }
+        if (kl + D < nkt) load_tiles<NW>(strip, kt0 + kl + D, lane, b[d]);
+        if (kl + DA < nkt) load_a(kt0 + kl + DA, ad);
+      }
+    }
   }
-  f32x4(*red)[MT * NW][64] = reinterpret_cast<f32x4(*)[MT * NW][64]>(smem);
 #pragma unroll
   for (int mt = 0; mt < MT; ++mt)
 #pragma unroll
     for (int i = 0; i < NW; ++i) red[wave][mt * NW + i][lane] = acc[mt][i];
   __syncthreads();
-
-  const float *scale0 = expert_scales(region[0], 0);
-  const float *scale1 = expert_scales(region[NW - 1], 0);
-  for (int e = threadIdx.x; e < MT * 256; e += blockDim.x) {
-    const int mt = e >> 8, row16 = (e >> 4) & 15, c = e & 15;
-    const int m = mt * 16 + row16;
+  // Element e of the tile: row tile mt, lane l, register rr (16x16 MFMA
+  // accumulator layout: row 4 (l / 16) + rr, column l % 16).
+  for (int e = threadIdx.x; e < MT * 256; e += KS * 64) {
+    const int mt = e >> 8, l = (e >> 2) & 63, rr = e & 3;
+    const int m = mt * 16 + 4 * (l >> 4) + rr;
     if (m >= M) continue;
-    const int src_lane = (row16 >> 2) * 16 + c, rr = row16 & 3;
-    float s[NW];
+    float v[NW];
 #pragma unroll
     for (int i = 0; i < NW; ++i) {
-      float v = 0.0f;
+      float sum = 0.0f;
 #pragma unroll
-      for (int wv = 0; wv < WAVES; ++wv) v += red[wv][mt * NW + i][src_lane][rr];
-      s[i] = v;
+      for (int wv = 0; wv < KS; ++wv) sum += red[wv][mt * NW + i][l][rr];
+      v[i] = sum;
     }
-    const int n_local = tile * 16 + c;
-    const float out = MODE == 2 ? silu_mul(s[0] * scale0[n_local], s[NW - 1] * scale1[n_local])
-                                : s[0] * scale0[n_local];
-    y[static_cast<uint64_t>(m) * ld + out_col0 + c] = static_cast<uint16_t>(f32_to_bf16(out));
+    const float out = MODE == 2 ? silu_mul(v[0] * sc[0], v[NW - 1] * sc[NW - 1]) : v[0] * sc[0];
+    y[static_cast<uint64_t>(m) * ld + out_tile * 16 + ec] = static_cast<uint16_t>(f32_to_bf16(out));
   }
 }
 
 }  // namespace
 
-#ifndef LF_W16_DENSE_WAVES
-#define LF_W16_DENSE_WAVES 8
-#endif
-#ifndef LF_W16_GATE_UP_WAVES
-#define LF_W16_GATE_UP_WAVES 4
+#ifndef LF_W16_WAVES
+#define LF_W16_WAVES 4
 #endif
 
 extern "C" {
 
-#define LF_W8A16_ENTRIES(MT, M)                                                              \
-  __global__ __launch_bounds__(LF_W16_DENSE_WAVES * 64) void lf_fp8_w8a16_dense_m##M(        \
-      const int32_t *counts, const uint16_t *x, const uint8_t *w, uint16_t *y) {             \
-    w8a16_kernel<LF_W16_DENSE_WAVES, MT, 0>(counts, x, w, w, w, y);                          \
+#define LF_W8A16_ENTRIES(MT, M, D)                                                              \
+  __global__ __launch_bounds__(LF_W16_WAVES * 64) void lf_fp8_w8a16_dense_m##M(              \
+      const int32_t *counts, const uint16_t *x, const uint8_t *w, uint16_t *y, uint8_t *ws) { \
+    w8a16_kernel<LF_W16_WAVES, MT, 0, D>(counts, x, w, w, w, y, ws);              \
   }                                                                                          \
-  __global__ __launch_bounds__(LF_W16_DENSE_WAVES * 64) void lf_fp8_w8a16_qkv_m##M(          \
+  __global__ __launch_bounds__(LF_W16_WAVES * 64) void lf_fp8_w8a16_qkv_m##M(                \
       const int32_t *counts, const uint16_t *x, const uint8_t *wq, const uint8_t *wk,        \
-      const uint8_t *wv, uint16_t *y) {                                                      \
-    w8a16_kernel<LF_W16_DENSE_WAVES, MT, 1>(counts, x, wq, wk, wv, y);                       \
+      const uint8_t *wv, uint16_t *y, uint8_t *ws) {                                         \
+    w8a16_kernel<LF_W16_WAVES, MT, 1, D>(counts, x, wq, wk, wv, y, ws);           \
   }                                                                                          \
-  __global__ __launch_bounds__(LF_W16_GATE_UP_WAVES * 64) void lf_fp8_w8a16_gate_up_m##M(    \
+  __global__ __launch_bounds__(LF_W16_WAVES * 64) void lf_fp8_w8a16_gate_up_m##M(            \
       const int32_t *counts, const uint16_t *x, const uint8_t *wg, const uint8_t *wu,        \
-      uint16_t *h) {                                                                         \
-    w8a16_kernel<LF_W16_GATE_UP_WAVES, MT, 2>(counts, x, wg, wu, wu, h);                     \
+      uint16_t *h, uint8_t *ws) {                                                            \
+    w8a16_kernel<LF_W16_WAVES, MT, 2, D>(counts, x, wg, wu, wu, h, ws);           \
   }
 
-LF_W8A16_ENTRIES(1, 16)
-LF_W8A16_ENTRIES(2, 32)
-LF_W8A16_ENTRIES(4, 64)
-LF_W8A16_ENTRIES(8, 128)
+LF_W8A16_ENTRIES(1, 16, 4)
+LF_W8A16_ENTRIES(2, 32, 4)
+LF_W8A16_ENTRIES(4, 64, 4)
+LF_W8A16_ENTRIES(8, 128, 2)
+
+#ifndef LF_W16T_WAVES
+#define LF_W16T_WAVES 8
+#endif
+#define LF_W8A16_TILE_ENTRIES(MT, M, DA)                                                      \
+  __global__ __launch_bounds__(LF_W16T_WAVES * 64) void lf_fp8_w8a16_dense_m##M##_t1(        \
+      const int32_t *counts, const uint16_t *x, const uint8_t *w, uint16_t *y, uint8_t *) {  \
+    w8a16_tile_kernel<LF_W16T_WAVES, MT, 0, 4, DA>(counts, x, w, w, w, y);                    \
+  }                                                                                          \
+  __global__ __launch_bounds__(LF_W16T_WAVES * 64) void lf_fp8_w8a16_qkv_m##M##_t1(          \
+      const int32_t *counts, const uint16_t *x, const uint8_t *wq, const uint8_t *wk,        \
+      const uint8_t *wv, uint16_t *y, uint8_t *) {                                           \
+    w8a16_tile_kernel<LF_W16T_WAVES, MT, 1, 4, DA>(counts, x, wq, wk, wv, y);                 \
+  }                                                                                          \
+  __global__ __launch_bounds__(LF_W16T_WAVES * 64) void lf_fp8_w8a16_gate_up_m##M##_t1(      \
+      const int32_t *counts, const uint16_t *x, const uint8_t *wg, const uint8_t *wu,        \
+      uint16_t *h, uint8_t *) {                                                              \
+    w8a16_tile_kernel<LF_W16T_WAVES, MT, 2, 4, DA>(counts, x, wg, wu, wu, h);                 \
+  }
+
+LF_W8A16_TILE_ENTRIES(1, 16, 1)
 
 }  // extern "C"

@@ -53,6 +53,43 @@ inline int64_t swizzled_offset(int64_t n, int64_t k, int64_t columns) {
   return (nt * (columns / 128) + kt) * LF_FP8_TILE_BYTES + h * 1024 + lane * 16 + b;
 }
 
+
+// W8A16 work split (the kernels are in lunaflux_amd/csrc/kernels/w8a16.hip).
+// Profiles with at most 16 rows use the one-tile form: a block of
+// kW16TileWaves waves per 16-column tile, K split across its waves, one
+// block per tile. Larger profiles use the column-group form: one tile per
+// wave, kW16Waves tiles per block, K cut into `split` slices across blocks
+// (about 512 blocks: two per CU of an MI355X, which is what its 64 KiB LDS
+// ring allows), partial tiles reduced through the workspace. Measured at
+// M = 32 on the Llama-3-8B shapes: 256 or 768+ blocks are slower (fewer
+// bytes in flight, or more partial traffic).
+constexpr int kW16Waves = 4;
+constexpr int kW16TileWaves = 8;
+struct W8a16Split {
+  int mt;
+  bool one_tile;
+  int64_t groups, split;
+};
+bool w8a16_split(int64_t n, int64_t k, int32_t max_tokens, W8a16Split *out) {
+  if (n % 16 != 0 || max_tokens > 128) return false;
+  const int mt = max_tokens <= 16 ? 1 : max_tokens <= 32 ? 2 : max_tokens <= 64 ? 4 : 8;
+  const int64_t kt = k / 128, tiles = n / 16;
+  out->mt = mt;
+  out->one_tile = mt == 1;
+  if (out->one_tile) {
+    out->groups = tiles;
+    out->split = 1;
+    return tiles <= INT32_MAX;
+  }
+  const int64_t groups = (tiles + kW16Waves - 1) / kW16Waves;
+  int64_t split = (512 + groups / 2) / groups;
+  if (split < 1) split = 1;
+  if (split > kt) split = kt;
+  if (groups * split > INT32_MAX) return false;
+  out->groups = groups;
+  out->split = split;
+  return true;
+}
 }  // namespace
 
 static_assert(sizeof(lf_fp8_weight_header) == LF_FP8_HEADER_BYTES, "header size");
@@ -144,6 +181,24 @@ int64_t lunaflux_fp8_act_quant_bytes(int64_t max_rows, int64_t columns) {
   return align_up(max_rows * columns, 256) + align_up(max_rows * 4, 256);
 }
 
+int64_t lunaflux_fp8_w8a16_workspace_bytes(int32_t entry, int64_t n, int64_t k,
+                                           int32_t max_tokens) {
+  if (entry != LF_FP8_ENTRY_W8A16_DENSE && entry != LF_FP8_ENTRY_W8A16_QKV &&
+      entry != LF_FP8_ENTRY_W8A16_GATE_UP) {
+    return -1;
+  }
+  W8a16Split sp;
+  if (n <= 0 || k <= 0 || k % 128 != 0 || max_tokens <= 0 || n > kMaxDim || k > kMaxDim ||
+      !w8a16_split(n, k, max_tokens, &sp)) {
+    return -1;
+  }
+  if (sp.split == 1) return 256;
+  // One 1 KiB fp32 accumulator fragment per (slice, 16-column tile, weight,
+  // 16-row tile), then one arrival counter per column group.
+  const int64_t nw = entry == LF_FP8_ENTRY_W8A16_GATE_UP ? 2 : 1;
+  return align_up(sp.split * (n / 16) * nw * sp.mt * 1024, 256) + align_up(sp.groups * 4, 256);
+}
+
 int32_t lunaflux_fp8_launch_geometry(int32_t entry, int64_t n, int64_t k,
                                      int32_t max_tokens, int32_t dims[7],
                                      char symbol[LF_FP8_SYMBOL_BYTES]) {
@@ -163,17 +218,16 @@ int32_t lunaflux_fp8_launch_geometry(int32_t entry, int64_t n, int64_t k,
     case LF_FP8_ENTRY_W8A16_DENSE:
     case LF_FP8_ENTRY_W8A16_QKV:
     case LF_FP8_ENTRY_W8A16_GATE_UP: {
-      if (n % 16 != 0 || max_tokens > 128) return LF_INVALID_ARGUMENT;
-      int32_t m = max_tokens <= 16 ? 16 : max_tokens <= 32 ? 32 : max_tokens <= 64 ? 64 : 128;
+      W8a16Split sp;
+      if (!w8a16_split(n, k, max_tokens, &sp)) return LF_INVALID_ARGUMENT;
       const char *op = entry == LF_FP8_ENTRY_W8A16_DENSE ? "dense"
                        : entry == LF_FP8_ENTRY_W8A16_QKV ? "qkv"
                                                          : "gate_up";
-      std::snprintf(buffer, sizeof(buffer), "lf_fp8_w8a16_%s_m%d", op, m);
+      std::snprintf(buffer, sizeof(buffer), "lf_fp8_w8a16_%s_m%d%s", op, 16 * sp.mt,
+                    sp.one_tile ? "_t1" : "");
       name = buffer;
-      gx = static_cast<int32_t>(n / 16);
-      // gate/up: 4 waves per block (two weights per wave, more blocks per
-      // CU); dense/qkv: 8 waves per block.
-      bx = entry == LF_FP8_ENTRY_W8A16_GATE_UP ? 256 : 512;
+      gx = static_cast<int32_t>(sp.groups * sp.split);
+      bx = 64 * (sp.one_tile ? kW16TileWaves : kW16Waves);
       break;
     }
     case LF_FP8_ENTRY_W8A8_DENSE:

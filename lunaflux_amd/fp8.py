@@ -89,6 +89,13 @@ def act_quant_bytes(max_rows: int, columns: int) -> int:
     return n
 
 
+def w8a16_workspace_bytes(entry: int, n: int, k: int, max_tokens: int) -> int:
+    nbytes = _abi.lib().lunaflux_fp8_w8a16_workspace_bytes(entry, n, k, max_tokens)
+    if nbytes < 0:
+        raise DeviceError("w8a16_workspace_bytes", _abi.LF_INVALID_ARGUMENT)
+    return nbytes
+
+
 def launch_geometry(entry: int, n: int, k: int, max_tokens: int):
     dims = (ctypes.c_int32 * 7)()
     symbol = ctypes.create_string_buffer(128)
@@ -190,6 +197,15 @@ class ProjectionRuntime:
         dims, symbol = launch_geometry(entry, n, k, max_tokens)
         return LaunchStep(self.function(symbol), dims, KernelArguments(operands), symbol)
 
+    def _w8a16(self, entry: int, n: int, k: int, max_tokens: int, operands) -> BoundOperation:
+        """A W8A16 launch with its split-K workspace (zero-filled once here;
+        the kernels leave its arrival counters at zero after every launch)."""
+        nbytes = w8a16_workspace_bytes(entry, n, k, max_tokens)
+        ws = self.context.allocate(nbytes)
+        ws.copy_from_host(np.zeros(nbytes, np.uint8))
+        step = self._step(entry, n, k, max_tokens, operands + [_region(ws, alignment=256)])
+        return BoundOperation([step], workspace=ws)
+
     # -- binding plan operations to launch steps ---------------------------
     def bind_act_quant(self, counts: Allocation, x: KernelArgument, w: Fp8Weight,
                        xq: KernelArgument, max_tokens: int) -> LaunchStep:
@@ -201,8 +217,8 @@ class ProjectionRuntime:
         _family(family, max_tokens)
         c = _region(counts, COUNTS_BYTES, alignment=4)
         if family == "w8a16":
-            return BoundOperation([self._step(_abi.ENTRY_W8A16_DENSE, w.rows, w.columns,
-                                              max_tokens, [c, x, w.region, y])])
+            return self._w8a16(_abi.ENTRY_W8A16_DENSE, w.rows, w.columns, max_tokens,
+                               [c, x, w.region, y])
         ws = self.context.allocate(act_quant_bytes(max_tokens, w.columns))
         xq = _region(ws, alignment=256)
         return BoundOperation([
@@ -218,8 +234,8 @@ class ProjectionRuntime:
         n = wq.rows + wk.rows + wv.rows
         c = _region(counts, COUNTS_BYTES, alignment=4)
         if family == "w8a16":
-            return BoundOperation([self._step(_abi.ENTRY_W8A16_QKV, n, wq.columns, max_tokens,
-                                              [c, x, wq.region, wk.region, wv.region, y])])
+            return self._w8a16(_abi.ENTRY_W8A16_QKV, n, wq.columns, max_tokens,
+                               [c, x, wq.region, wk.region, wv.region, y])
         ws = self.context.allocate(act_quant_bytes(max_tokens, wq.columns))
         xq = _region(ws, alignment=256)
         return BoundOperation([
@@ -235,8 +251,8 @@ class ProjectionRuntime:
             raise DeviceError("gate/up shapes", _abi.LF_INVALID_ARGUMENT)
         c = _region(counts, COUNTS_BYTES, alignment=4)
         if family == "w8a16":
-            return BoundOperation([self._step(_abi.ENTRY_W8A16_GATE_UP, wg.rows, wg.columns,
-                                              max_tokens, [c, x, wg.region, wu.region, h])])
+            return self._w8a16(_abi.ENTRY_W8A16_GATE_UP, wg.rows, wg.columns, max_tokens,
+                               [c, x, wg.region, wu.region, h])
         ws = self.context.allocate(act_quant_bytes(max_tokens, wg.columns))
         xq = _region(ws, alignment=256)
         return BoundOperation([

@@ -40,7 +40,8 @@ def test_code_object_has_every_entry_point():
                                                for t in ("t128", "t256")] + ["lf_moe_route", "lf_moe_sort", "lf_moe_quant_tokens",
                    "lf_moe_gate_up", "lf_moe_gate_up_b128", "lf_moe_quant_hidden", "lf_moe_down",
                    "lf_moe_down_b128", "lf_moe_combine"] + [f"lf_fp8_w8a16_{op}_m{m}" for op in ("dense", "qkv", "gate_up")
-                                             for m in (16, 32, 64, 128)]:
+                                             for m in (16, 32, 64, 128)] + [
+                   f"lf_fp8_w8a16_{op}_m16_t1" for op in ("dense", "qkv", "gate_up")]:
         assert symbol.encode() + b"\0" in image, symbol
 
 
@@ -98,10 +99,25 @@ def test_region_size_validation():
 
 
 def test_launch_geometry():
+    # W8A16, max rows <= 16: one 16-column tile per 8-wave block, K split
+    # across its waves. Larger profiles: 4 column tiles per 4-wave block, K
+    # cut into about 512 / groups slices across blocks.
     dims, sym = fp8.launch_geometry(_abi.ENTRY_W8A16_DENSE, 4096, 14336, 32)
-    assert sym == "lf_fp8_w8a16_dense_m32" and dims.grid == (256, 1, 1) and dims.block == (512, 1, 1)
+    assert sym == "lf_fp8_w8a16_dense_m32" and dims.grid == (64 * 8, 1, 1) and dims.block == (256, 1, 1)
     dims, sym = fp8.launch_geometry(_abi.ENTRY_W8A16_QKV, 6144, 4096, 1)
-    assert sym == "lf_fp8_w8a16_qkv_m16" and dims.grid == (384, 1, 1)
+    assert sym == "lf_fp8_w8a16_qkv_m16_t1" and dims.grid == (384, 1, 1) and dims.block == (512, 1, 1)
+    dims, sym = fp8.launch_geometry(_abi.ENTRY_W8A16_GATE_UP, 14336, 4096, 32)
+    assert sym == "lf_fp8_w8a16_gate_up_m32" and dims.grid == (224 * 2, 1, 1)
+    dims, sym = fp8.launch_geometry(_abi.ENTRY_W8A16_QKV, 6144, 4096, 128)
+    assert sym == "lf_fp8_w8a16_qkv_m128" and dims.grid == (96 * 5, 1, 1)
+    # split-K workspace: S x (N / 16) x NW x MT 1 KiB fragments + one counter
+    # per column group; 256 bytes (unused) without a split
+    assert fp8.w8a16_workspace_bytes(_abi.ENTRY_W8A16_DENSE, 4096, 14336, 32) == 8 * 256 * 2 * 1024 + 256
+    assert fp8.w8a16_workspace_bytes(_abi.ENTRY_W8A16_QKV, 6144, 4096, 1) == 256
+    assert fp8.w8a16_workspace_bytes(_abi.ENTRY_W8A16_GATE_UP, 14336, 4096, 32) == 2 * 896 * 2 * 2 * 1024 + 1024
+    assert fp8.w8a16_workspace_bytes(_abi.ENTRY_W8A16_QKV, 6144, 4096, 128) == 5 * 384 * 8 * 1024 + 512
+    with pytest.raises(fp8.DeviceError):
+        fp8.w8a16_workspace_bytes(_abi.ENTRY_W8A8_DENSE, 4096, 4096, 16)
     # W8A8: 256 x 256 tiles (1-D grid, 512 threads) once there is a tile per
     # CU, 128 x 128 tiles (256 threads) below that or when N does not divide.
     dims, sym = fp8.launch_geometry(_abi.ENTRY_W8A8_GATE_UP, 14336, 4096, 8192)

@@ -93,7 +93,8 @@ def test_golden_config1(rt):
 @pytest.mark.parametrize("m,k,n,max_tokens", [
     (4, 512, 1536, 16), (1, 4096, 4096, 16), (8, 1024, 2048, 16), (16, 512, 256, 16),
     (32, 2048, 1024, 32), (17, 1024, 512, 32), (50, 512, 256, 64), (128, 1024, 512, 128),
-    (100, 512, 128, 128), (0, 512, 256, 16),
+    (100, 512, 128, 128), (0, 512, 256, 16), (20, 512, 80, 32), (3, 128, 48, 16),
+    (64, 896, 208, 64),
 ])
 def test_dense_w8a16(rt, m, k, n, max_tokens):
     rng = np.random.default_rng(1000 + m * 7 + k + n)
@@ -119,6 +120,44 @@ def test_dense_w8a8(rt, m, k, n, max_tokens):
         assert y.shape == (0, n)
         return
     check_projection(y, x_ref(x, "w8a8"), deq(q, s), f"dense w8a8 {m}x{k}x{n}")
+
+
+@pytest.mark.parametrize("family_op", ["dense", "gate_up"])
+def test_w8a16_split_k_repeated_launches(rt, family_op):
+    """The column-group form reduces split-K partials through the workspace
+    and resets its arrival counters at the end of every launch: three
+    launches of one binding (one workspace) must each match the oracle and
+    be bit-identical to each other (the slice sum order is fixed)."""
+    from lunaflux_amd import _abi, fp8
+    from lunaflux_amd.fp8 import _region
+    rng = np.random.default_rng(7100)
+    m, k, n, max_tokens = 29, 2048, 1024, 32
+    entry = _abi.ENTRY_W8A16_DENSE if family_op == "dense" else _abi.ENTRY_W8A16_GATE_UP
+    dims, sym = fp8.launch_geometry(entry, n, k, max_tokens)
+    assert not sym.endswith("_t1") and dims.grid[0] > (n // 16) // 4  # split across blocks
+    x = synth.activations(rng, m, k)
+    q, s_, w = make_weight(rt, rng, n, k)
+    xa = rt.context.upload(np.concatenate([x, np.zeros((max_tokens - m, k), np.uint16)]))
+    ya = rt.context.allocate(max_tokens * n * 2)
+    counts = rt.step_counts(m)
+    if family_op == "dense":
+        op = rt.bind_dense("w8a16", counts, _region(xa, alignment=256), w, _region(ya, alignment=256),
+                           max_tokens)
+        ref = o.dense_projection(x_ref(x, "w8a16"), deq(q, s_))
+    else:
+        qu, su, wu = make_weight(rt, rng, n, k)
+        op = rt.bind_gate_up("w8a16", counts, _region(xa, alignment=256), w, wu,
+                             _region(ya, alignment=256), max_tokens)
+        xr = x_ref(x, "w8a16")
+        ref = o.silu_mul_array(o.dense_projection(xr, deq(q, s_)), o.dense_projection(xr, deq(qu, su)))
+    outs = []
+    for _ in range(3):
+        op.launch(rt.stream, synchronous=True)
+        outs.append(ya.read(np.uint16, (m, n)))
+    bound = dict(k=k, s_abs=abs_sum(x_ref(x, "w8a16"), deq(q, s_))) if family_op == "dense" else {}
+    for y in outs:
+        parity(y, ref, label=f"split-K {family_op} repeated", **bound)
+    assert np.array_equal(outs[0], outs[1]) and np.array_equal(outs[1], outs[2])
 
 
 @pytest.mark.parametrize("op,m,k", [
