@@ -19,6 +19,7 @@
 //   lf_moe_combine        out[t] = sum_j w[t, j] * y[pos(t, j)] (j ascending)
 //                         -> bf16 [T, H]
 #include "w8a8_core.h"
+#include "w8a8_v3.h"
 
 namespace {
 
@@ -190,8 +191,7 @@ __device__ void quant_rows(const uint16_t *src, int K, int group, uint8_t *dst, 
 }
 
 // --- grouped GEMM -------------------------------------------------------------
-// blockIdx.y enumerates the 128-row tiles of all experts (tiles[] prefix);
-// the expert of a tile is found by binary search.
+// The expert of a 128-row tile (tiles[] prefix) is found by binary search.
 LF_DEVICE int expert_of_tile(const int32_t *tiles, int E, int j) {
   int lo = 0, hi = E;
   while (hi - lo > 1) {
@@ -201,112 +201,153 @@ LF_DEVICE int expert_of_tile(const int32_t *tiles, int E, int j) {
   return lo;
 }
 
-// STAGE 0: gate/up (x rows gathered by token, SwiGLU, bf16 h);
-// STAGE 1: down (h rows in expert order, fp32 y).
+// The grouped GEMMs run the direct-to-LDS main loop (w8a8_v3.h) on 128 x 128
+// blocks of 4 waves, two blocks per CU, over a 1-D grid in the XCD-aware
+// tile order: tile (bx, by) is column block bx of row tile by, where row
+// tiles are the 128-row tiles of all experts (tiles[] prefix).
+using GemmTile = w8a8v3::Tile<128, 128, 2, 2, 2>;
+constexpr int kGemmGroup = 4;
+static_assert(GemmTile::kWaveM * GemmTile::kWgm == w8a8::kBM, "row tiles of the sort");
+
+// Block-scaled fold: each k-tile's products times (activation scale of the
+// row, k-group) x (weight scale of the column's 128-block, k-group).
+struct BlockScaleFold {
+  static constexpr bool kActive = true;
+  const float *sa_lds;  // [128][KT]
+  int KT, wm, lane;
+  const float *sw[GemmTile::kFN];  // slot j: [KT] scales of its 128-column block
+  template <class A>
+  LF_DEVICE void operator()(int kt, const A &step, A &acc) const {
+    float swk[GemmTile::kFN];
+#pragma unroll
+    for (int j = 0; j < GemmTile::kFN; ++j) swk[j] = sw[j][kt];
+#pragma unroll
+    for (int i = 0; i < GemmTile::kFM; ++i) {
+#pragma unroll
+      for (int rr = 0; rr < 4; ++rr) {
+        const float sa = sa_lds[w8a8v3::acc_row<GemmTile>(wm, i, lane, rr) * KT + kt];
+#pragma unroll
+        for (int j = 0; j < GemmTile::kFN; ++j) acc[i][j][rr] += step[i][j][rr] * (sa * swk[j]);
+      }
+    }
+  }
+};
+
+// STAGE 0: gate/up (x rows gathered by token, SwiGLU, bf16 h): a block
+// computes 64 h-columns (wave wn: its kFN / 2 gate tiles, then the up tiles
+// of the same columns). STAGE 1: down (h rows in expert order, fp32 y): a
+// block computes 128 columns.
 template <int STAGE, bool BLOCK>
 __device__ void grouped_gemm(const int32_t *counts, const MoeDesc &d, const uint8_t *w0,
                              const uint8_t *w1, uint8_t *ws) {
-  __shared__ __attribute__((aligned(16))) uint8_t As[2][w8a8::kAStage];
-  // Block-scaled form: activation scales of the block's rows, [kBM][KT],
+  using T = GemmTile;
+  __shared__ __attribute__((aligned(1024))) uint8_t smem[T::kSmem];
+  // Block-scaled form: activation scales of the block's rows, [128][KT],
   // K <= 4096 (the host rejects larger K for 128-column groups).
-  __shared__ float sa_lds[BLOCK ? w8a8::kBM * 32 : 1];
-  const int T = live_rows(counts, 1 << 30);
-  const MoeLayout L(d, T);
+  __shared__ float sa_lds[BLOCK ? 128 * 32 : 1];
+  const int Tn = live_rows(counts, 1 << 30);
+  const MoeLayout L(d, Tn);
   const int32_t *tiles = at<int32_t>(ws, L.tiles);
   const int E = d.experts;
-  const int j = blockIdx.y;
-  if (j >= tiles[E]) return;
-  const int e = expert_of_tile(tiles, E, j);
-  const int32_t *offsets = at<int32_t>(ws, L.offsets);
-  const int p0 = offsets[e] + (j - tiles[e]) * w8a8::kBM;
-  const int pend = offsets[e + 1];
   const WeightHeader &h0 = header_of(w0);
   const int K = static_cast<int>(h0.columns);
   const int KT = K >> 7;
   const int N = static_cast<int>(h0.rows);
   if (BLOCK && KT > 32) return;  // sa_lds holds at most 32 scale columns
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  const int wm = wave >> 1, wn = wave & 1;
+  const int gx = STAGE == 0 ? N / 64 : N / 128;
+  int bx, by;
+  if (!w8a8v3::tile_of_block(gx, tiles[E], kGemmGroup, bx, by)) return;
+  const int e = expert_of_tile(tiles, E, by);
+  const int32_t *offsets = at<int32_t>(ws, L.offsets);
+  const int p0 = offsets[e] + (by - tiles[e]) * 128;
+  const int pend = offsets[e + 1];
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int wm = wave / T::kWgn, wn = wave % T::kWgn;
   const int32_t *sorted = at<int32_t>(ws, L.sorted);
+  auto src_row = [&](int p) { return STAGE == 0 ? sorted[p] / d.top_k : p; };
 
-  // This thread's activation row.
-  const int trow = tid >> 1;
-  const int p = p0 + trow;
-  const bool live = p < pend;
-  int src_row = 0;
-  if (live) src_row = STAGE == 0 ? sorted[p] / d.top_k : p;
+  // Block-local weight tile s (16 columns): region, tile index, column.
+  auto slot = [&](int s, const uint8_t *&region, int &col) {
+    if (STAGE == 0) {
+      const int sw = s / T::kFN, f = s % T::kFN;
+      const bool up = f >= T::kFN / 2;
+      col = bx * 64 + sw * (T::kWaveN / 2) + 16 * (up ? f - T::kFN / 2 : f);
+      region = up ? w1 : w0;
+    } else {
+      col = bx * 128 + 16 * s;
+      region = w0;
+    }
+  };
+
   const uint8_t *abase = at<uint8_t>(ws, STAGE == 0 ? L.xq : L.hq);
-  const uint4 *asrc = reinterpret_cast<const uint4 *>(abase + static_cast<uint64_t>(src_row) * K + (tid & 1) * 64);
   const float *ascales = at<float>(ws, STAGE == 0 ? L.xs : L.hs);
-
-  // This wave's weight tiles.
-  const uint8_t *strip[4];
-  const float *wsc[4];
-  const float *sw[4];
-  int col[4];
-  if (STAGE == 0) {
-    const int c0 = blockIdx.x * 64 + wn * 32;
+  w8a8v3::Plan<T> plan;
 #pragma unroll
-    for (int q = 0; q < 4; ++q) {
-      const uint8_t *reg = q < 2 ? w0 : w1;
-      col[q] = c0 + (q & 1) * 16;
-      strip[q] = expert_tiles(reg, e) + static_cast<uint64_t>(col[q] >> 4) * KT * kTileBytes;
-      wsc[q] = expert_scales(reg, e);
-    }
-  } else {
-#pragma unroll
-    for (int q = 0; q < 4; ++q) {
-      col[q] = blockIdx.x * 128 + wn * 64 + q * 16;
-      strip[q] = expert_tiles(w0, e) + static_cast<uint64_t>(col[q] >> 4) * KT * kTileBytes;
-      wsc[q] = expert_scales(w0, e);
-    }
+  for (int q = 0; q < T::kAIns; ++q) {
+    const int tr = w8a8v3::a_load_row<T>(wave, q, lane);
+    const int p = p0 + tr < pend ? p0 + tr : p0;  // dead rows re-read the first row
+    plan.a[q] = abase + static_cast<uint64_t>(src_row(p)) * K + w8a8v3::a_load_chunk(tr, lane) * 16;
   }
 #pragma unroll
-  for (int q = 0; q < 4; ++q) sw[q] = BLOCK ? wsc[q] + (col[q] >> 7) * KT : nullptr;
+  for (int q = 0; q < T::kBIns; ++q) {
+    const int half = w8a8v3::b_load_half<T>(wave, q);
+    const uint8_t *region;
+    int col;
+    slot(half >> 1, region, col);
+    plan.b[q] = expert_tiles(region, e) + static_cast<uint64_t>(col >> 4) * KT * kTileBytes +
+                (half & 1) * 1024 + lane * 16;
+  }
+  const float *wsc[T::kFN];
+  int col[T::kFN];
+#pragma unroll
+  for (int j = 0; j < T::kFN; ++j) {
+    const uint8_t *region;
+    slot(wn * T::kFN + j, region, col[j]);
+    wsc[j] = expert_scales(region, e);
+  }
+
+  f32x4 acc[T::kFM][T::kFN];
   if constexpr (BLOCK) {
-    // Activation scales of the block's rows: [kBM][KT] (zero for dead rows).
-    for (int i = tid; i < w8a8::kBM * KT; i += blockDim.x) {
+    // Activation scales of the block's rows: [128][KT] (zero for dead rows).
+    for (int i = threadIdx.x; i < 128 * KT; i += blockDim.x) {
       const int rr = i / KT, kg = i % KT;
       const int pp = p0 + rr;
-      float s = 0.0f;
-      if (pp < pend) {
-        const int sr = STAGE == 0 ? sorted[pp] / d.top_k : pp;
-        s = ascales[static_cast<uint64_t>(sr) * KT + kg];
-      }
-      sa_lds[i] = s;
+      sa_lds[i] = pp < pend ? ascales[static_cast<uint64_t>(src_row(pp)) * KT + kg] : 0.0f;
     }
     __syncthreads();
+    BlockScaleFold fold{sa_lds, KT, wm, lane, {}};
+#pragma unroll
+    for (int j = 0; j < T::kFN; ++j) fold.sw[j] = wsc[j] + (col[j] >> 7) * KT;
+    w8a8v3::mainloop<T>(plan, KT, smem, acc, fold);
+  } else {
+    w8a8v3::mainloop<T>(plan, KT, smem, acc);
   }
-  f32x4 acc[4][4];
-  w8a8::mainloop<BLOCK>(asrc, live, strip, KT, As, sa_lds, sw, acc);
 
   const int r = lane & 15;
 #pragma unroll
-  for (int i = 0; i < 4; ++i) {
+  for (int i = 0; i < T::kFM; ++i) {
 #pragma unroll
     for (int rr = 0; rr < 4; ++rr) {
-      const int pp = p0 + w8a8::acc_row(wm, i, lane, rr);
+      const int pp = p0 + w8a8v3::acc_row<T>(wm, i, lane, rr);
       if (pp >= pend) continue;
-      float sa = 1.0f;
-      if (!BLOCK) {
-        const int sr = STAGE == 0 ? sorted[pp] / d.top_k : pp;
-        sa = ascales[sr];
-      }
+      const float sa = BLOCK ? 1.0f : ascales[src_row(pp)];
       if (STAGE == 0) {
         uint16_t *hrow = at<uint16_t>(ws, L.h) + static_cast<uint64_t>(pp) * N;
 #pragma unroll
-        for (int q = 0; q < 2; ++q) {
-          const int c = col[q] + r;
-          const float gv = BLOCK ? acc[i][q][rr] : acc[i][q][rr] * sa * wsc[q][c];
-          const float uv = BLOCK ? acc[i][q + 2][rr] : acc[i][q + 2][rr] * sa * wsc[q + 2][c];
+        for (int j = 0; j < T::kFN / 2; ++j) {
+          const int c = col[j] + r;
+          const float gv = BLOCK ? acc[i][j][rr] : acc[i][j][rr] * sa * wsc[j][c];
+          const float uv = BLOCK ? acc[i][j + T::kFN / 2][rr]
+                                 : acc[i][j + T::kFN / 2][rr] * sa * wsc[j + T::kFN / 2][c];
           hrow[c] = static_cast<uint16_t>(f32_to_bf16(silu_mul(gv, uv)));
         }
       } else {
         float *yrow = at<float>(ws, L.y) + static_cast<uint64_t>(pp) * N;
 #pragma unroll
-        for (int q = 0; q < 4; ++q) {
-          const int c = col[q] + r;
-          yrow[c] = BLOCK ? acc[i][q][rr] : acc[i][q][rr] * sa * wsc[q][c];
+        for (int j = 0; j < T::kFN; ++j) {
+          const int c = col[j] + r;
+          yrow[c] = BLOCK ? acc[i][j][rr] : acc[i][j][rr] * sa * wsc[j][c];
         }
       }
     }

@@ -95,9 +95,20 @@ LF_DEVICE uint32_t lds_offset_of(const uint8_t *p) {
       reinterpret_cast<uintptr_t>((const __attribute__((address_space(3))) uint8_t *)p));
 }
 
-template <class T>
+// Folds of the per-k-tile products into the accumulators. NoFold: the MFMAs
+// accumulate into acc directly (one scale per row and per column, applied
+// in the epilogue). A folding functor (kActive = true) receives each
+// k-tile's products in fresh registers instead and adds them to acc with
+// its own factors (block scales that change with k).
+struct NoFold {
+  static constexpr bool kActive = false;
+  template <class A>
+  LF_DEVICE void operator()(int, const A &, A &) const {}
+};
+
+template <class T, class Fold = NoFold>
 __device__ void mainloop(const Plan<T> &plan, int KT, uint8_t *smem,
-                         f32x4 (&acc)[T::kFM][T::kFN]) {
+                         f32x4 (&acc)[T::kFM][T::kFN], const Fold &fold = Fold{}) {
   constexpr int NS = T::kStages;
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int wm = wave / T::kWgn, wn = wave % T::kWgn;
@@ -147,6 +158,7 @@ __device__ void mainloop(const Plan<T> &plan, int KT, uint8_t *smem,
       bf[j].h[0] = *reinterpret_cast<const uint4 *>(tile + lane * 16);
       bf[j].h[1] = *reinterpret_cast<const uint4 *>(tile + 1024 + lane * 16);
     }
+    f32x4 step[Fold::kActive ? T::kFM : 1][Fold::kActive ? T::kFN : 1];
 #pragma unroll
     for (int i = 0; i < T::kFM; ++i) {
       const int row = wm * T::kWaveM + i * 16 + r;
@@ -155,10 +167,16 @@ __device__ void mainloop(const Plan<T> &plan, int KT, uint8_t *smem,
       af.h[1] = *reinterpret_cast<const uint4 *>(a + w8a8::a_chunk_offset(row, 2 * g + 1));
 #pragma unroll
       for (int j = 0; j < T::kFN; ++j) {
-        acc[i][j] = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(af.v, bf[j].v, acc[i][j], 0,
-                                                                     0, 0, 127, 0, 127);
+        if constexpr (Fold::kActive) {
+          step[i][j] = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(
+              af.v, bf[j].v, f32x4{0.f, 0.f, 0.f, 0.f}, 0, 0, 0, 127, 0, 127);
+        } else {
+          acc[i][j] = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(af.v, bf[j].v, acc[i][j], 0,
+                                                                       0, 0, 127, 0, 127);
+        }
       }
     }
+    if constexpr (Fold::kActive) fold(kt, step, acc);
   }
 }
 

@@ -351,15 +351,15 @@ int32_t lunaflux_fp8_moe_launch_geometry(int32_t entry, const lf_fp8_moe_desc *d
     case LF_FP8_MOE_SORT: name = "lf_moe_sort"; bx = 1024; break;
     case LF_FP8_MOE_QUANT_TOKENS: name = "lf_moe_quant_tokens"; gx = T; break;
     case LF_FP8_MOE_GATE_UP:
+      // 1-D grid over (64 h-column block, 128-row tile); blocks past the
+      // live tile count return.
       name = b128 ? "lf_moe_gate_up_b128" : "lf_moe_gate_up";
-      gx = d->inter / 64;
-      gy = tiles;
+      gx = d->inter / 64 * tiles;
       break;
     case LF_FP8_MOE_QUANT_HIDDEN: name = "lf_moe_quant_hidden"; gx = A; break;
     case LF_FP8_MOE_DOWN:
       name = b128 ? "lf_moe_down_b128" : "lf_moe_down";
-      gx = d->hidden / 128;
-      gy = tiles;
+      gx = d->hidden / 128 * tiles;
       break;
     case LF_FP8_MOE_COMBINE: name = "lf_moe_combine"; gx = T; break;
     default: return LF_INVALID_ARGUMENT;

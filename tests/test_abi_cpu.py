@@ -199,12 +199,13 @@ def test_moe_descriptor_layout_and_geometry():
     assert lay["topk_w"] == a * 4 and lay["y"] + a * 4096 * 4 == lay["end"]
     assert all(v % 256 == 0 for v in lay.values())
     dims, sym = moe.launch_geometry(4, d, 1024)   # gate/up
-    assert sym == "lf_moe_gate_up" and dims.grid == (14336 // 64, a // 128 + 8, 1)
+    # 1-D grid over (64 h-column block, 128-row tile of the tile bound)
+    assert sym == "lf_moe_gate_up" and dims.grid == (14336 // 64 * (a // 128 + 8), 1, 1)
     dims, sym = moe.launch_geometry(2, d, 1024)   # sort: one block of 1024
     assert sym == "lf_moe_sort" and dims.grid == (1, 1, 1) and dims.block == (1024, 1, 1)
     d5 = moe.moe_descriptor(64, 6, 1, 2048, 1408, 128)
     dims, sym = moe.launch_geometry(6, d5, 4096)  # down, block scales
-    assert sym == "lf_moe_down_b128" and dims.grid == (2048 // 128, 4096 * 6 // 128 + 64, 1)
+    assert sym == "lf_moe_down_b128" and dims.grid == (2048 // 128 * (4096 * 6 // 128 + 64), 1, 1)
     for bad in [(0, 1, 0, 256, 256, 0), (8, 9, 0, 256, 256, 0), (8, 2, 2, 256, 256, 0),
                 (8, 2, 0, 200, 256, 0), (8, 2, 0, 256, 256, 64), (8, 2, 0, 8192, 256, 128)]:
         with pytest.raises(fp8.DeviceError):
