@@ -68,37 +68,86 @@ LF_DEVICE bool desc_ok(const MoeDesc &d) {
 }
 
 // --- routing ---------------------------------------------------------------
-// One thread per token: the k largest logits in order (ties -> lower expert
-// id, strict comparison), then softmax weights either over the k picked
-// logits (mode 0) or over all experts (mode 1), accumulated in expert order.
-__device__ void route(const int32_t *counts, const MoeDesc &d, const float *logits, uint8_t *ws) {
+// One wave per token, four tokens per block; lane l holds the logits of
+// experts l, l + 64, ... The k largest logits in order (ties -> lower expert
+// id): k rounds of a wave-wide (value, id) maximum over the experts not yet
+// picked. Softmax weights over the k picked logits (mode 0) or over all
+// experts (mode 1); the sum of exponentials is accumulated in expert order,
+// as the reference loop does.
+LF_DEVICE void route(const int32_t *counts, const MoeDesc &d, const float *logits, uint8_t *ws) {
   const int T = live_rows(counts, 1 << 30);
-  const int t = blockIdx.x * blockDim.x + threadIdx.x;
+  const int t = blockIdx.x * 4 + (threadIdx.x >> 6);
   if (t >= T) return;
+  const int lane = threadIdx.x & 63;
   const MoeLayout L(d, T);
-  const float *l = logits + static_cast<uint64_t>(t) * d.experts;
+  const int E = d.experts;
+  const float *l = logits + static_cast<uint64_t>(t) * E;
   int32_t *ids = at<int32_t>(ws, L.topk_ids) + static_cast<uint64_t>(t) * d.top_k;
   float *wts = at<float>(ws, L.topk_w) + static_cast<uint64_t>(t) * d.top_k;
+  float v[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int e = lane + 64 * i;
+    v[i] = e < E ? l[e] : 0.0f;
+  }
+  uint32_t taken = 0;  // bit i: expert lane + 64 i picked (or absent)
+#pragma unroll
+  for (int i = 0; i < 4; ++i) taken |= (lane + 64 * i < E ? 0u : 1u) << i;
   int picked[16];
+  float pv[16];
   for (int j = 0; j < d.top_k; ++j) {
+    // this lane's candidate: its largest untaken logit, lowest id on ties
     int best = -1;
-    for (int e = 0; e < d.experts; ++e) {
-      bool taken = false;
-      for (int i = 0; i < j; ++i) taken |= picked[i] == e;
-      if (taken) continue;
-      if (best < 0 || l[e] > l[best]) best = e;
+    float bv = 0.0f;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      if (!((taken >> i) & 1u) && (best < 0 || v[i] > bv)) {
+        best = lane + 64 * i;
+        bv = v[i];
+      }
+    }
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) {
+      const int ob = __shfl_xor(best, off);
+      const float ov = __shfl_xor(bv, off);
+      if (ob >= 0 && (best < 0 || ov > bv || (ov == bv && ob < best))) {
+        best = ob;
+        bv = ov;
+      }
     }
     picked[j] = best;
-    ids[j] = best;
+    pv[j] = bv;
+    if ((best & 63) == lane) taken |= 1u << (best >> 6);
   }
-  const float top = l[picked[0]];
+  const float top = pv[0];
   float sum = 0.0f;
   if (d.route_mode == 0) {
-    for (int j = 0; j < d.top_k; ++j) sum += expf(l[picked[j]] - top);
+    for (int j = 0; j < d.top_k; ++j) sum += expf(pv[j] - top);
   } else {
-    for (int e = 0; e < d.experts; ++e) sum += expf(l[e] - top);
+    float ex[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) ex[i] = expf(v[i] - top);
+    for (int e = 0; e < E; ++e) {
+      float te = 0.0f;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        if ((e >> 6) == i) te = __shfl(ex[i], e & 63);
+      }
+      sum += te;
+    }
   }
-  for (int j = 0; j < d.top_k; ++j) wts[j] = expf(l[picked[j]] - top) / sum;
+  if (lane < d.top_k) {
+    float pj = 0.0f;
+    int ij = 0;
+    for (int j = 0; j < d.top_k; ++j) {
+      if (j == lane) {
+        pj = pv[j];
+        ij = picked[j];
+      }
+    }
+    ids[lane] = ij;
+    wts[lane] = expf(pj - top) / sum;
+  }
 }
 
 // --- stable counting sort ----------------------------------------------------
@@ -111,7 +160,7 @@ __device__ void route(const int32_t *counts, const MoeDesc &d, const float *logi
 constexpr int kSortThreads = 1024;
 constexpr int kSortWaves = kSortThreads / 64;
 
-__device__ void sort_assignments(const int32_t *counts, const MoeDesc &d, uint8_t *ws) {
+LF_DEVICE void sort_assignments(const int32_t *counts, const MoeDesc &d, uint8_t *ws) {
   __shared__ int32_t cnt[257];
   __shared__ int32_t running[256];
   __shared__ int32_t wcnt[kSortWaves][256];
@@ -181,13 +230,18 @@ __device__ void sort_assignments(const int32_t *counts, const MoeDesc &d, uint8_
 }
 
 // --- quantizers --------------------------------------------------------------
-__device__ void quant_rows(const uint16_t *src, int K, int group, uint8_t *dst, float *scales,
+// Per token (group 0): one wave per row, four rows per block. Per 128-column
+// group: 16 lanes per group, sixteen groups per block.
+LF_DEVICE void quant_rows(const uint16_t *src, int K, int group, uint8_t *dst, float *scales,
                            int rows) {
-  const int row = blockIdx.x;
-  if (row >= rows) return;
-  const int per_row = group > 0 ? K / group : 1;
-  quantize_row(src + static_cast<uint64_t>(row) * K, K, group, dst + static_cast<uint64_t>(row) * K,
-               scales + static_cast<uint64_t>(row) * per_row);
+  if (group == 0) {
+    const int row = blockIdx.x * 4 + (threadIdx.x >> 6);
+    if (row >= rows) return;
+    quantize_row_wave(src + static_cast<uint64_t>(row) * K, K, dst + static_cast<uint64_t>(row) * K,
+                      scales + row);
+  } else {
+    quantize_groups_wave(src, K, rows, dst, scales, blockIdx.x * 4 + (threadIdx.x >> 6));
+  }
 }
 
 // --- grouped GEMM -------------------------------------------------------------
@@ -355,7 +409,7 @@ __device__ void grouped_gemm(const int32_t *counts, const MoeDesc &d, const uint
 }
 
 // --- combine -------------------------------------------------------------------
-__device__ void combine(const int32_t *counts, const MoeDesc &d, uint8_t *ws, uint16_t *out) {
+LF_DEVICE void combine(const int32_t *counts, const MoeDesc &d, uint8_t *ws, uint16_t *out) {
   const int T = live_rows(counts, 1 << 30);
   const int t = blockIdx.x;
   if (t >= T) return;
@@ -364,13 +418,22 @@ __device__ void combine(const int32_t *counts, const MoeDesc &d, uint8_t *ws, ui
   const float *w = at<float>(ws, L.topk_w) + static_cast<uint64_t>(t) * d.top_k;
   const int32_t *pos = at<int32_t>(ws, L.pos) + static_cast<uint64_t>(t) * d.top_k;
   const float *y = at<float>(ws, L.y);
-  for (int c = threadIdx.x; c < H; c += blockDim.x) {
-    float acc = 0.0f;
+  // four columns per thread (H % 128 == 0); terms added in slot order j
+  for (int c = 4 * threadIdx.x; c < H; c += 4 * blockDim.x) {
+    f32x4 acc = {0.f, 0.f, 0.f, 0.f};
     for (int j = 0; j < d.top_k; ++j) {
-      const float prod = w[j] * y[static_cast<uint64_t>(pos[j]) * H + c];
-      acc = acc + prod;
+      const f32x4 v = *reinterpret_cast<const f32x4 *>(y + static_cast<uint64_t>(pos[j]) * H + c);
+      const float wj = w[j];
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        const float prod = wj * v[q];
+        acc[q] = acc[q] + prod;
+      }
     }
-    out[static_cast<uint64_t>(t) * H + c] = static_cast<uint16_t>(f32_to_bf16(acc));
+    uint2 packed;
+    packed.x = f32_to_bf16(acc[0]) | (f32_to_bf16(acc[1]) << 16);
+    packed.y = f32_to_bf16(acc[2]) | (f32_to_bf16(acc[3]) << 16);
+    *reinterpret_cast<uint2 *>(out + static_cast<uint64_t>(t) * H + c) = packed;
   }
 }
 

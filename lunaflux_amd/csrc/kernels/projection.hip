@@ -8,66 +8,86 @@
 namespace {
 
 // ---------------------------------------------------------------------------
-// Row quantizer: one block per row. For each span of columns (the whole row
-// when group == 0, else `group` columns): amax over the span, ratio = 448 /
-// amax (correctly rounded division), codes = e4m3_rne_sat(x * ratio),
-// scale = amax / 448 (one per span, in order). An all-zero span gets zero
-// codes and scale 0.
+// Activation quantizers. For each span of columns (the whole row, or one
+// 128-column group): amax over the span, ratio = 448 / amax (correctly
+// rounded division), codes = e4m3_rne_sat(x * ratio), scale = amax / 448.
+// An all-zero span gets zero codes and scale 0.
 // ---------------------------------------------------------------------------
-__device__ void quantize_row(const uint16_t *src_row, int K, int group, uint8_t *dst_row,
-                             float *scales_row) {
-  __shared__ float partial[16];
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-  const int span = group > 0 ? group : K;
-  for (int s0 = 0; s0 < K; s0 += span) {
-    const uint4 *src = reinterpret_cast<const uint4 *>(src_row + s0);
-    const int chunks = span >> 3;  // 8 bf16 per 16-byte chunk
-    float amax = 0.0f;
-    for (int c = threadIdx.x; c < chunks; c += blockDim.x) {
-      const uint4 v = src[c];
-      const uint32_t w4[4] = {v.x, v.y, v.z, v.w};
+LF_DEVICE float bf16x8_amax(const uint4 &v, float amax) {
+  const uint32_t w4[4] = {v.x, v.y, v.z, v.w};
 #pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        amax = fmaxf(amax, fabsf(bf16_to_f32(w4[i] & 0xffffu)));
-        amax = fmaxf(amax, fabsf(bf16_to_f32(w4[i] >> 16)));
-      }
-    }
-    amax = wave_max(amax);
-    if (lane == 0) partial[wave] = amax;
-    __syncthreads();
-    amax = partial[0];
-    for (int i = 1; i < static_cast<int>(blockDim.x >> 6); ++i) amax = fmaxf(amax, partial[i]);
-    __syncthreads();  // partial[] is reused by the next span
-    const bool zero = amax == 0.0f;
-    const float ratio = zero ? 0.0f : 448.0f / amax;
-    uint2 *dst = reinterpret_cast<uint2 *>(dst_row + s0);
-    for (int c = threadIdx.x; c < chunks; c += blockDim.x) {
-      const uint4 v = src[c];
-      const uint32_t w4[4] = {v.x, v.y, v.z, v.w};
-      uint32_t out[2] = {0u, 0u};
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const uint32_t lo = zero ? 0u : e4m3_encode(bf16_to_f32(w4[i] & 0xffffu) * ratio);
-        const uint32_t hi = zero ? 0u : e4m3_encode(bf16_to_f32(w4[i] >> 16) * ratio);
-        out[i >> 1] |= (lo | (hi << 8)) << (16 * (i & 1));
-      }
-      dst[c] = make_uint2(out[0], out[1]);
-    }
-    if (threadIdx.x == 0) scales_row[s0 / span] = zero ? 0.0f : amax / 448.0f;
+  for (int i = 0; i < 4; ++i) {
+    amax = fmaxf(amax, fabsf(bf16_to_f32(w4[i] & 0xffffu)));
+    amax = fmaxf(amax, fabsf(bf16_to_f32(w4[i] >> 16)));
   }
+  return amax;
 }
 
+LF_DEVICE uint2 bf16x8_encode(const uint4 &v, float ratio, bool zero) {
+  const uint32_t w4[4] = {v.x, v.y, v.z, v.w};
+  uint32_t out[2] = {0u, 0u};
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const uint32_t lo = zero ? 0u : e4m3_encode(bf16_to_f32(w4[i] & 0xffffu) * ratio);
+    const uint32_t hi = zero ? 0u : e4m3_encode(bf16_to_f32(w4[i] >> 16) * ratio);
+    out[i >> 1] |= (lo | (hi << 8)) << (16 * (i & 1));
+  }
+  return make_uint2(out[0], out[1]);
+}
+
+// Per-token quantizer: one wave per row (no block barriers). Two passes over
+// the row (amax, then encode); the second re-reads it from cache.
+LF_DEVICE void quantize_row_wave(const uint16_t *src_row, int K, uint8_t *dst_row,
+                                 float *scale) {
+  const int lane = threadIdx.x & 63;
+  const int chunks = K >> 3;  // 8 bf16 per 16-byte chunk
+  const uint4 *src = reinterpret_cast<const uint4 *>(src_row);
+  float amax = 0.0f;
+#pragma unroll 8
+  for (int c = lane; c < chunks; c += 64) amax = bf16x8_amax(src[c], amax);
+  amax = wave_max(amax);
+  const bool zero = amax == 0.0f;
+  const float ratio = zero ? 0.0f : 448.0f / amax;
+  uint2 *dst = reinterpret_cast<uint2 *>(dst_row);
+#pragma unroll 8
+  for (int c = lane; c < chunks; c += 64) dst[c] = bf16x8_encode(src[c], ratio, zero);
+  if (lane == 0) *scale = zero ? 0.0f : amax / 448.0f;
+}
+
+// Per-128-column-group quantizer: the 16 lanes 16q..16q+15 of a wave hold
+// one group's 16 chunks; a wave quantizes groups 4 gw .. 4 gw + 3 of the
+// rows x (K / 128) groups (row-major), amax reduced across its 16 lanes.
+LF_DEVICE void quantize_groups_wave(const uint16_t *src, int K, int rows, uint8_t *dst,
+                                    float *scales, int gw) {
+  const int lane = threadIdx.x & 63;
+  const int per_row = K >> 7;
+  const int gid = 4 * gw + (lane >> 4);
+  const bool live = gid < rows * per_row;
+  const int row = live ? gid / per_row : 0, kg = live ? gid - row * per_row : 0;
+  const uint64_t base = static_cast<uint64_t>(row) * K + kg * 128 + (lane & 15) * 8;
+  const uint4 v = live ? *reinterpret_cast<const uint4 *>(src + base) : make_uint4(0u, 0u, 0u, 0u);
+  float amax = bf16x8_amax(v, 0.0f);
+#pragma unroll
+  for (int off = 8; off > 0; off >>= 1) amax = fmaxf(amax, __shfl_xor(amax, off));
+  const bool zero = amax == 0.0f;
+  const float ratio = zero ? 0.0f : 448.0f / amax;
+  if (!live) return;
+  *reinterpret_cast<uint2 *>(dst + base) = bf16x8_encode(v, ratio, zero);
+  if ((lane & 15) == 0) scales[gid] = zero ? 0.0f : amax / 448.0f;
+}
+
+// One wave per row, four rows per block.
 __device__ void act_quant_rows(const int32_t *counts, const uint16_t *x, const uint8_t *w,
                                uint8_t *xq) {
   const WeightHeader &h = header_of(w);
   if (h.magic != kWeightMagic) return;
   const int K = static_cast<int>(h.columns);
   const int M = live_rows(counts, 1 << 30);
-  const int row = blockIdx.x;
+  const int row = blockIdx.x * 4 + (threadIdx.x >> 6);
   if (row >= M) return;
   float *scales = reinterpret_cast<float *>(xq + align256(static_cast<uint64_t>(M) * K));
-  quantize_row(x + static_cast<uint64_t>(row) * K, K, 0, xq + static_cast<uint64_t>(row) * K,
-               scales + row);
+  quantize_row_wave(x + static_cast<uint64_t>(row) * K, K, xq + static_cast<uint64_t>(row) * K,
+                    scales + row);
 }
 
 // ---------------------------------------------------------------------------

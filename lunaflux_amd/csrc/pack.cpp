@@ -211,8 +211,8 @@ int32_t lunaflux_fp8_launch_geometry(int32_t entry, int64_t n, int64_t k,
   char buffer[LF_FP8_SYMBOL_BYTES];
   switch (entry) {
     case LF_FP8_ENTRY_ACT_QUANT_ROWS:
-      name = "lf_fp8_act_quant_rows";
-      gx = max_tokens;
+      name = "lf_fp8_act_quant_rows";  // one wave per row
+      gx = (max_tokens + 3) / 4;
       bx = 256;
       break;
     case LF_FP8_ENTRY_W8A16_DENSE:
@@ -347,16 +347,24 @@ int32_t lunaflux_fp8_moe_launch_geometry(int32_t entry, const lf_fp8_moe_desc *d
   int32_t bx = 256;
   const char *name = nullptr;
   switch (entry) {
-    case LF_FP8_MOE_ROUTE: name = "lf_moe_route"; gx = (T + 255) / 256; break;
+    // Routing and the per-token quantizers: one wave per token (row); the
+    // per-128-column-group quantizers: four groups per wave.
+    case LF_FP8_MOE_ROUTE: name = "lf_moe_route"; gx = (T + 3) / 4; break;
     case LF_FP8_MOE_SORT: name = "lf_moe_sort"; bx = 1024; break;
-    case LF_FP8_MOE_QUANT_TOKENS: name = "lf_moe_quant_tokens"; gx = T; break;
+    case LF_FP8_MOE_QUANT_TOKENS:
+      name = "lf_moe_quant_tokens";
+      gx = b128 ? (T * (d->hidden / 128) + 15) / 16 : (T + 3) / 4;
+      break;
     case LF_FP8_MOE_GATE_UP:
       // 1-D grid over (64 h-column block, 128-row tile); blocks past the
       // live tile count return.
       name = b128 ? "lf_moe_gate_up_b128" : "lf_moe_gate_up";
       gx = d->inter / 64 * tiles;
       break;
-    case LF_FP8_MOE_QUANT_HIDDEN: name = "lf_moe_quant_hidden"; gx = A; break;
+    case LF_FP8_MOE_QUANT_HIDDEN:
+      name = "lf_moe_quant_hidden";
+      gx = b128 ? (A * (d->inter / 128) + 15) / 16 : (A + 3) / 4;
+      break;
     case LF_FP8_MOE_DOWN:
       name = b128 ? "lf_moe_down_b128" : "lf_moe_down";
       gx = d->hidden / 128 * tiles;

@@ -129,7 +129,7 @@ def test_launch_geometry():
     dims, sym = fp8.launch_geometry(_abi.ENTRY_W8A8_DENSE, 128 * 33, 4096, 8192)
     assert sym == "lf_fp8_w8a8_dense_t128" and dims.grid == (64 * 33, 1, 1)
     dims, sym = fp8.launch_geometry(_abi.ENTRY_ACT_QUANT_ROWS, 4096, 4096, 2048)
-    assert sym == "lf_fp8_act_quant_rows" and dims.grid == (2048, 1, 1)
+    assert sym == "lf_fp8_act_quant_rows" and dims.grid == (2048 // 4, 1, 1)  # one wave per row
     with pytest.raises(fp8.DeviceError):
         fp8.launch_geometry(_abi.ENTRY_W8A16_DENSE, 4096, 4096, 129)
     with pytest.raises(fp8.DeviceError):
