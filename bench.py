@@ -304,6 +304,27 @@ def pmc_pass():
     log(f"pmc pass done (gate_up x10, copy {n} bytes x3)")
 
 
+def pmc_pass_prefill():
+    """Short run for the MFMA-utilisation counter pass: the prefill down GEMM
+    (K=14336 -> N=4096) at M=8192 (256 x 256 tiles) and the o GEMM at M=2048
+    (128 x 128 tiles), 5 launches each after one act-quant."""
+    from lunaflux_amd import fp8, synth
+    from lunaflux_amd.fp8 import ProjectionRuntime, _region
+    rt = ProjectionRuntime(0)
+    rng = np.random.default_rng(6)
+    for m, k, n in ((8192, INTER, HIDDEN), (2048, HIDDEN, HIDDEN)):
+        w = rt.weight_from_region(fp8.pack_weight(*synth.weight(rng, n, k)))
+        x = rt.context.upload(synth.activations(rng, m, k))
+        y = rt.context.allocate(m * n * 2)
+        op = rt.bind_dense("w8a8", rt.step_counts(m, decode=False), _region(x, alignment=256), w,
+                           _region(y, alignment=256), m)
+        op.steps[0].launch(rt.stream, synchronous=False)
+        for _ in range(5):
+            op.steps[-1].launch(rt.stream, synchronous=False)
+        rt.stream.synchronize()
+        log(f"pmc prefill pass: {op.steps[-1].name} M={m} K={k} N={n} x5")
+
+
 def measured_traffic():
     """HBM bytes per launch of the roofline kernel from the committed counter
     summary (profiles/lf_fp8_w8a16_gate_up_m32.traffic.json), or None."""
@@ -323,6 +344,8 @@ def main():
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--quick", action="store_true", help="headline only, no detail sweep")
     ap.add_argument("--pmc-pass", action="store_true", help="short run for counter passes")
+    ap.add_argument("--pmc-pass-prefill", action="store_true",
+                    help="short run for the prefill MFMA counter pass")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU only: --gpus {args.gpus} is not supported "
@@ -330,6 +353,9 @@ def main():
         sys.exit(2)
     if args.pmc_pass:
         pmc_pass()
+        return
+    if args.pmc_pass_prefill:
+        pmc_pass_prefill()
         return
 
     from lunaflux_amd.fp8 import ProjectionRuntime

@@ -55,15 +55,15 @@ LF_DEVICE void load_tiles(const uint8_t *const (&strip)[NW], int kt, int lane, u
   }
 }
 
-// LDS activation ring of a block: two buffers of D k-tiles of 16*MT rows of
+// LDS activation ring of a block: two buffers of XC k-tiles of 16*MT rows of
 // bf16, k-tile-major (one k-tile = 16*MT rows x 256 bytes); row r keeps its
 // 16-byte chunk c at chunk position c ^ (r & 15), so the 16 rows of an MFMA
 // fragment read fall in distinct banks.
-template <int MT, int D>
+template <int MT, int XC>
 struct XRing {
   static constexpr int kRows = 16 * MT;
   static constexpr int kKTileBytes = kRows * 256;
-  static constexpr int kBufferBytes = D * kKTileBytes;
+  static constexpr int kBufferBytes = XC * kKTileBytes;
   static constexpr int kBytes = 2 * kBufferBytes;
   static_assert(kBytes <= 128 * 1024, "LDS budget");
 };
@@ -83,11 +83,14 @@ LF_DEVICE void wait_vm_multiple(int n) {
 }
 
 // MODE 0: dense, 1: qkv (three weights, packed Q|K|V output), 2: gate/up.
-template <int WAVES, int MT, int MODE, int D>
+// D: weight k-tiles in flight per wave; XC: k-tiles per activation chunk
+// (D a multiple of XC).
+template <int WAVES, int MT, int MODE, int D, int XC>
 __device__ void w8a16_kernel(const int32_t *counts, const uint16_t *x, const uint8_t *w0,
                              const uint8_t *w1, const uint8_t *w2, uint16_t *y, uint8_t *ws) {
   constexpr int NW = MODE == 2 ? 2 : 1;
-  using X = XRing<MT, D>;
+  static_assert(D % XC == 0, "a weight ring round covers whole activation chunks");
+  using X = XRing<MT, XC>;
   __shared__ __attribute__((aligned(1024))) uint8_t ring[X::kBytes];
   __shared__ int last_block;
 
@@ -140,22 +143,22 @@ __device__ void w8a16_kernel(const int32_t *counts, const uint16_t *x, const uin
 #pragma unroll
   for (int i = 0; i < NW; ++i) sc[i] = expert_scales(region[i], 0)[t * 16 + r];
 
-  // Activation chunk c (k-tiles c D .. c D + D - 1 of the slice) goes straight
+  // Activation chunk c (k-tiles c XC .. c XC + XC - 1 of the slice) goes straight
   // into ring buffer c & 1 with global_load_lds: 1 KiB = 4 rows of one k-tile
   // per instruction, only the ceil(M / 4) row groups that hold live rows
   // (rows past M re-read row M - 1; their outputs are never stored).
   const uint32_t ring_base = __builtin_amdgcn_readfirstlane(w8a8v3::lds_offset_of(ring));
   const int xins = (M + 3) >> 2;
-  const int chunks = (nkt + D - 1) / D;
+  const int chunks = (nkt + XC - 1) / XC;
   auto load_chunk = [&](int c) {
-    const int n = (nkt - c * D < D ? nkt - c * D : D) * xins;
+    const int n = (nkt - c * XC < XC ? nkt - c * XC : XC) * xins;
     for (int id = wave; id < n; id += WAVES) {
       const int kl = id / xins, q = id - kl * xins;
       const int row = 4 * q + (lane >> 4);
       const int chunk = (lane & 15) ^ (row & 15);
       const int src = row < M ? row : M - 1;
       w8a8v3::dma16(reinterpret_cast<const uint8_t *>(x + static_cast<uint64_t>(src) * K +
-                                                      (kt0 + c * D + kl) * 128 + chunk * 8),
+                                                      (kt0 + c * XC + kl) * 128 + chunk * 8),
                     ring_base + (c & 1) * X::kBufferBytes + kl * X::kKTileBytes + q * 1024);
     }
   };
@@ -163,8 +166,8 @@ __device__ void w8a16_kernel(const int32_t *counts, const uint16_t *x, const uin
   // for them: the refills of chunk c - 1 (one k-tile each while k-tiles
   // remain), i.e. 2 NW per refilled k-tile.
   auto refills = [&](int c) {
-    const int n = nkt - D - c * D;
-    return n < 0 ? 0 : n > D ? D : n;
+    const int n = nkt - D - c * XC;
+    return n < 0 ? 0 : n > XC ? XC : n;
   };
 
   load_chunk(0);
@@ -183,45 +186,47 @@ __device__ void w8a16_kernel(const int32_t *counts, const uint16_t *x, const uin
     for (int i = 0; i < NW; ++i) acc[mt][i] = f32x4{0.f, 0.f, 0.f, 0.f};
   // Rows >= M of the ring hold stale LDS contents; they only feed output
   // rows >= M, which are never stored (MFMA rows are independent).
-  for (int c = 0; c < chunks; ++c) {
-    if (c > 0) {
-      // This wave's share of chunk c landed: only the refills of chunk c - 1
-      // were issued after it.
-      if (refills(c - 1) == D) {
-        w8a8v3::wait_vmcnt<2 * NW * D>();
-      } else {
-        w8a8v3::wait_vmcnt<0>();
-      }
-    }
-    // Every wave's share of chunk c is in LDS, and every wave is done with
-    // chunk c - 1, whose buffer chunk c + 1 now refills.
-    __syncthreads();
-    if (c + 1 < chunks) load_chunk(c + 1);
-    const uint8_t *buf = ring + (c & 1) * X::kBufferBytes;
+  for (int base = 0; base < nkt; base += D) {
 #pragma unroll
     for (int d = 0; d < D; ++d) {
-      const int kl = c * D + d;
-      if (kl < nkt) {
-#pragma unroll
-        for (int j = 0; j < 4; ++j) {
-          Frag16 a[MT];
-#pragma unroll
-          for (int mt = 0; mt < MT; ++mt) {
-            const int row = mt * 16 + r;
-            a[mt].u = *reinterpret_cast<const uint4 *>(
-                buf + d * X::kKTileBytes + row * 256 + ((((g << 2) | j) ^ (row & 15)) << 4));
-          }
-#pragma unroll
-          for (int i = 0; i < NW; ++i) {
-            const bf16x8 bf = weight_fragment(b[d][i], j);
-#pragma unroll
-            for (int mt = 0; mt < MT; ++mt) {
-              acc[mt][i] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a[mt].v, bf, acc[mt][i], 0, 0, 0);
-            }
+      const int kl = base + d;
+      if (kl >= nkt) break;
+      if (d % XC == 0) {
+        const int c = kl / XC;
+        if (c > 0) {
+          // This wave's share of chunk c landed: only the refills of chunk
+          // c - 1 were issued after it.
+          if (refills(c - 1) == XC) {
+            w8a8v3::wait_vmcnt<2 * NW * XC>();
+          } else {
+            w8a8v3::wait_vmcnt<0>();
           }
         }
-        if (kl + D < nkt) load_tiles<NW>(strip, kt0 + kl + D, lane, b[d]);
+        // Every wave's share of chunk c is in LDS, and every wave is done
+        // with chunk c - 1, whose buffer chunk c + 1 now refills.
+        __syncthreads();
+        if (c + 1 < chunks) load_chunk(c + 1);
       }
+      const uint8_t *buf = ring + ((kl / XC) & 1) * X::kBufferBytes + (d % XC) * X::kKTileBytes;
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        Frag16 a[MT];
+#pragma unroll
+        for (int mt = 0; mt < MT; ++mt) {
+          const int row = mt * 16 + r;
+          a[mt].u = *reinterpret_cast<const uint4 *>(
+              buf + row * 256 + ((((g << 2) | j) ^ (row & 15)) << 4));
+        }
+#pragma unroll
+        for (int i = 0; i < NW; ++i) {
+          const bf16x8 bf = weight_fragment(b[d][i], j);
+#pragma unroll
+          for (int mt = 0; mt < MT; ++mt) {
+            acc[mt][i] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a[mt].v, bf, acc[mt][i], 0, 0, 0);
+          }
+        }
+      }
+      if (kl + D < nkt) load_tiles<NW>(strip, kt0 + kl + D, lane, b[d]);
     }
   }
 
@@ -485,26 +490,26 @@ __device__ void w8a16_tile_kernel(const int32_t *counts, const uint16_t *x, cons
 
 extern "C" {
 
-#define LF_W8A16_ENTRIES(MT, M, D)                                                              \
+#define LF_W8A16_ENTRIES(MT, M, D, XC)                                                              \
   __global__ __launch_bounds__(LF_W16_WAVES * 64) void lf_fp8_w8a16_dense_m##M(              \
       const int32_t *counts, const uint16_t *x, const uint8_t *w, uint16_t *y, uint8_t *ws) { \
-    w8a16_kernel<LF_W16_WAVES, MT, 0, D>(counts, x, w, w, w, y, ws);              \
+    w8a16_kernel<LF_W16_WAVES, MT, 0, D, XC>(counts, x, w, w, w, y, ws);              \
   }                                                                                          \
   __global__ __launch_bounds__(LF_W16_WAVES * 64) void lf_fp8_w8a16_qkv_m##M(                \
       const int32_t *counts, const uint16_t *x, const uint8_t *wq, const uint8_t *wk,        \
       const uint8_t *wv, uint16_t *y, uint8_t *ws) {                                         \
-    w8a16_kernel<LF_W16_WAVES, MT, 1, D>(counts, x, wq, wk, wv, y, ws);           \
+    w8a16_kernel<LF_W16_WAVES, MT, 1, D, XC>(counts, x, wq, wk, wv, y, ws);           \
   }                                                                                          \
   __global__ __launch_bounds__(LF_W16_WAVES * 64) void lf_fp8_w8a16_gate_up_m##M(            \
       const int32_t *counts, const uint16_t *x, const uint8_t *wg, const uint8_t *wu,        \
       uint16_t *h, uint8_t *ws) {                                                            \
-    w8a16_kernel<LF_W16_WAVES, MT, 2, D>(counts, x, wg, wu, wu, h, ws);           \
+    w8a16_kernel<LF_W16_WAVES, MT, 2, D, XC>(counts, x, wg, wu, wu, h, ws);           \
   }
 
-LF_W8A16_ENTRIES(1, 16, 4)
-LF_W8A16_ENTRIES(2, 32, 4)
-LF_W8A16_ENTRIES(4, 64, 4)
-LF_W8A16_ENTRIES(8, 128, 2)
+LF_W8A16_ENTRIES(1, 16, 4, 4)
+LF_W8A16_ENTRIES(2, 32, 4, 4)
+LF_W8A16_ENTRIES(4, 64, 4, 4)
+LF_W8A16_ENTRIES(8, 128, 2, 2)
 
 #ifndef LF_W16T_WAVES
 #define LF_W16T_WAVES 8
