@@ -9,10 +9,14 @@
 // issued while k-step kt computes, so L2/HBM latency is covered without
 // occupancy. Stage layout:
 //   A: BM rows x 128 bytes; LDS row r holds the row's 16-byte chunk c at
-//      physical chunk c ^ (r & 7) (conflict-free fragment reads). The
-//      swizzle is applied on the global side: lane l of a load instruction
-//      writes LDS row r = 8 (instr) + l / 8, physical chunk l % 8, so it
-//      fetches logical chunk (l % 8) ^ (r & 7).
+//      physical chunk c ^ ((r >> 1) & 7). A ds_read_b128 is served 16 lanes
+//      (256 bytes, all banks) at a time and a fragment read gives those 16
+//      lanes 16 consecutive rows at one logical chunk: rows 2k and 2k+1 fill
+//      the two 128-byte halves of a bank window and (r >> 1) & 7 spreads the
+//      8 row pairs over the 8 chunk positions, so no two lanes of a pass
+//      share a bank. The swizzle is applied on the global side: lane l of a
+//      load instruction writes LDS row r = 8 (instr) + l / 8, physical
+//      chunk l % 8, so it fetches logical chunk (l % 8) ^ ((r >> 1) & 7).
 //   B: BN/16 pre-swizzled 16 x 128 weight tiles copied verbatim, 2 KiB each.
 //
 // The caller provides, per lane, the global row base of each A row it loads
@@ -48,8 +52,12 @@ template <class T>
 LF_DEVICE int a_load_row(int wave, int q, int lane) {
   return 8 * (wave * T::kAIns + q) + (lane >> 3);
 }
+// Physical chunk of logical 16-byte chunk `chunk` of tile row `row`, and the
+// byte offset of that chunk in a stage.
+LF_DEVICE int a_phys_chunk(int row, int chunk) { return chunk ^ ((row >> 1) & 7); }
+LF_DEVICE int a_chunk_offset(int row, int chunk) { return row * 128 + (a_phys_chunk(row, chunk) << 4); }
 // Logical 16-byte chunk of that row this lane fetches.
-LF_DEVICE int a_load_chunk(int row, int lane) { return (lane & 7) ^ (row & 7); }
+LF_DEVICE int a_load_chunk(int row, int lane) { return a_phys_chunk(row, lane & 7); }
 // B half-tile (2 per 16-column slot) of this wave's B instruction q.
 template <class T>
 LF_DEVICE int b_load_half(int wave, int q) { return wave * T::kBIns + q; }
@@ -163,8 +171,8 @@ __device__ void mainloop(const Plan<T> &plan, int KT, uint8_t *smem,
     for (int i = 0; i < T::kFM; ++i) {
       const int row = wm * T::kWaveM + i * 16 + r;
       w8a8::Frag8 af;
-      af.h[0] = *reinterpret_cast<const uint4 *>(a + w8a8::a_chunk_offset(row, 2 * g));
-      af.h[1] = *reinterpret_cast<const uint4 *>(a + w8a8::a_chunk_offset(row, 2 * g + 1));
+      af.h[0] = *reinterpret_cast<const uint4 *>(a + a_chunk_offset(row, 2 * g));
+      af.h[1] = *reinterpret_cast<const uint4 *>(a + a_chunk_offset(row, 2 * g + 1));
 #pragma unroll
       for (int j = 0; j < T::kFN; ++j) {
         if constexpr (Fold::kActive) {

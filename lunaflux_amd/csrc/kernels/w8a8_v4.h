@@ -13,8 +13,11 @@
 //
 // LDS stage (NS of them, a ring):
 //   A: BM rows x 64 bytes. Row r keeps its 4 chunks (slot j = logical chunk
-//      2 j + h) at physical slot j ^ ((r >> 1) & 3), which makes both the
-//      16-row DMA writes and the 32-row fragment reads bank-conflict free.
+//      2 j + h) at physical slot j ^ ((r >> 2) & 3). A ds_read_b128 is served
+//      16 lanes (256 bytes, all banks) at a time; a fragment read gives them
+//      16 consecutive rows at one logical slot: rows 4k..4k+3 fill the four
+//      64-byte quarters of a bank window and (r >> 2) & 3 moves the slot, so
+//      the 16 lanes of a pass hit 16 distinct 16-byte bank groups.
 //   B: BN / 16 tile halves of 1 KiB, copied verbatim.
 // MFMA operands (lane l, q = l / 32): A row 32 i + l % 32 and B column
 // 32 j + l % 32, each with slots 2q and 2q+1 (32 bytes).
@@ -53,7 +56,7 @@ struct Tile {
   static_assert(kWaveM % 32 == 0 && kWaveN % 32 == 0, "wave tile");
 };
 
-LF_DEVICE int a_phys_slot(int row, int slot) { return slot ^ ((row >> 1) & 3); }
+LF_DEVICE int a_phys_slot(int row, int slot) { return slot ^ ((row >> 2) & 3); }
 
 // Tile row written by lane `lane` of this wave's A instruction q, and the
 // logical slot it fetches (its physical slot is lane & 3).
@@ -109,7 +112,8 @@ __device__ void mainloop(const Plan<T> &plan, int KT, uint8_t *smem,
 
   // LDS byte offsets of this lane's fragment reads inside a stage: A block i
   // at a_off0 / a_off1 (slots 2q, 2q+1) + 2048 i (32 rows further keep the
-  // same swizzle), B block j at b_off + 2048 j and + 256.
+  // same swizzle: (r + 32) >> 2 & 3 == r >> 2 & 3), B block j at b_off +
+  // 2048 j and + 256.
   const int row0 = wm * T::kWaveM + c;
   const int a_off0 = row0 * 64 + (a_phys_slot(row0, 2 * q) << 4);
   const int a_off1 = a_off0 ^ 16;
