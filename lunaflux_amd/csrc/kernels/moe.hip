@@ -258,9 +258,12 @@ LF_DEVICE int expert_of_tile(const int32_t *tiles, int E, int j) {
 // The grouped GEMMs run the direct-to-LDS main loop (w8a8_v3.h) on 128 x 128
 // blocks of 4 waves, two blocks per CU, over a 1-D grid in the XCD-aware
 // tile order: tile (bx, by) is column block bx of row tile by, where row
-// tiles are the 128-row tiles of all experts (tiles[] prefix).
+// tiles are the 128-row tiles of all experts (tiles[] prefix). The order is
+// column-major over all row tiles (one group): the expert weights (E x N x K
+// bytes) dwarf the gathered activations, so each XCD takes a range of
+// weight columns and streams every weight strip once, for all row tiles of
+// its expert back to back, while the activations stay in L2/MALL.
 using GemmTile = w8a8v3::Tile<128, 128, 2, 2, 2>;
-constexpr int kGemmGroup = 4;
 static_assert(GemmTile::kWaveM * GemmTile::kWgm == w8a8::kBM, "row tiles of the sort");
 
 // Block-scaled fold: each k-tile's products times (activation scale of the
@@ -310,7 +313,7 @@ __device__ void grouped_gemm(const int32_t *counts, const MoeDesc &d, const uint
   if (BLOCK && KT > 32) return;  // sa_lds holds at most 32 scale columns
   const int gx = STAGE == 0 ? N / 64 : N / 128;
   int bx, by;
-  if (!w8a8v3::tile_of_block(gx, tiles[E], kGemmGroup, bx, by)) return;
+  if (!w8a8v3::tile_of_block(gx, tiles[E], tiles[E], bx, by)) return;
   const int e = expert_of_tile(tiles, E, by);
   const int32_t *offsets = at<int32_t>(ws, L.offsets);
   const int p0 = offsets[e] + (by - tiles[e]) * 128;
