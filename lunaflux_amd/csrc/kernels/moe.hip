@@ -266,6 +266,16 @@ LF_DEVICE int expert_of_tile(const int32_t *tiles, int E, int j) {
 using GemmTile = w8a8v3::Tile<128, 128, 2, 2, 2>;
 static_assert(GemmTile::kWaveM * GemmTile::kWgm == w8a8::kBM, "row tiles of the sort");
 
+// A pointer the compiler can treat as wave-uniform (the caller guarantees it
+// is): both halves through readfirstlane.
+template <typename P>
+LF_DEVICE const P *uniform_ptr(const P *p) {
+  const uint64_t v = reinterpret_cast<uint64_t>(p);
+  const uint32_t lo = __builtin_amdgcn_readfirstlane(static_cast<uint32_t>(v));
+  const uint32_t hi = __builtin_amdgcn_readfirstlane(static_cast<uint32_t>(v >> 32));
+  return reinterpret_cast<const P *>((static_cast<uint64_t>(hi) << 32) | lo);
+}
+
 // Block-scaled fold: each k-tile's products times (activation scale of the
 // row, k-group) x (weight scale of the column's 128-block, k-group).
 struct BlockScaleFold {
@@ -374,8 +384,12 @@ __device__ void grouped_gemm(const int32_t *counts, const MoeDesc &d, const uint
     }
     __syncthreads();
     BlockScaleFold fold{sa_lds, KT, wm, lane, {}};
+    // The weight-scale rows are the same for every lane of the wave; with a
+    // provably uniform address their per-k-tile reads are scalar loads,
+    // counted apart from the vector-memory loads of the stage ring (a vector
+    // load here would make the loop wait for every outstanding stage load).
 #pragma unroll
-    for (int j = 0; j < T::kFN; ++j) fold.sw[j] = wsc[j] + (col[j] >> 7) * KT;
+    for (int j = 0; j < T::kFN; ++j) fold.sw[j] = uniform_ptr(wsc[j] + (col[j] >> 7) * KT);
     w8a8v3::mainloop<T>(plan, KT, smem, acc, fold);
   } else {
     w8a8v3::mainloop<T>(plan, KT, smem, acc);
