@@ -221,7 +221,7 @@ def moe_flops(c):
 
 
 def moe_bench(rt, c, steps=5, warmup=2, seed=4242):
-    """Times the seven launches of one MoE expert-MLP operation with events
+    """Times the launches of one MoE expert-MLP operation with events
     between them. Expert weights are E copies of one seeded draw (kernel time
     does not depend on the values; it keeps setup short)."""
     from lunaflux_amd import fp8, moe, synth
@@ -265,7 +265,8 @@ def moe_bench(rt, c, steps=5, warmup=2, seed=4242):
            for s_i in range(len(op.steps))]
     names = [s.name for s in op.steps]
     total_ms = sum(per)
-    gemm_ms = per[3] + per[5]
+    gemm_ms = sum(p for n, p in zip((s.name for s in op.steps), per)
+                  if n.startswith(("lf_moe_gate_up", "lf_moe_down")))
     fl = moe_flops(c)
     return {"total_us": round(total_ms * 1e3, 1),
             "steps_us": {n: round(p * 1e3, 1) for n, p in zip(names, per)},

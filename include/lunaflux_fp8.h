@@ -169,6 +169,7 @@ int32_t lunaflux_fp8_launch_geometry(int32_t entry, int64_t n, int64_t k,
  *
  * Launch sequence and operands (in order):
  *  lf_moe_route         (counts, desc, logits fp32 [T, E], ws)
+ *  lf_moe_sort_count    (counts, desc, ws)
  *  lf_moe_sort          (counts, desc, ws)
  *  lf_moe_quant_tokens  (counts, desc, x bf16 [T, H], ws)
  *  lf_moe_gate_up[_b128](counts, desc, wg, wu, ws)
@@ -201,7 +202,8 @@ enum lf_fp8_moe_entry {
   LF_FP8_MOE_GATE_UP = 4,
   LF_FP8_MOE_QUANT_HIDDEN = 5,
   LF_FP8_MOE_DOWN = 6,
-  LF_FP8_MOE_COMBINE = 7
+  LF_FP8_MOE_COMBINE = 7,
+  LF_FP8_MOE_SORT_COUNT = 8 /* runs between ROUTE and SORT */
 };
 
 /* Validates and fills a descriptor: 1 <= experts <= 256, 1 <= top_k <=

@@ -105,6 +105,7 @@ SIGNATURES = {
 }
 
 MOE_ROUTE, MOE_SORT, MOE_QUANT_TOKENS, MOE_GATE_UP, MOE_QUANT_HIDDEN, MOE_DOWN, MOE_COMBINE = range(1, 8)
+MOE_SORT_COUNT = 8
 
 
 class NativeLibraryMissing(RuntimeError):

@@ -5,9 +5,10 @@
 // whose layout is a function of the live token count T and the descriptor,
 // recomputed identically by every kernel - see MoeLayout):
 //   lf_moe_route          logits [T, E] fp32       -> top-k experts, weights
-//   lf_moe_sort           stable counting sort of the T*k assignments by
-//                         expert -> sorted ids, positions, per-expert row
-//                         offsets and 128-row tile offsets
+//   lf_moe_sort_count     per-chunk expert counts of the T*k assignments
+//   lf_moe_sort           stable counting sort of the assignments by expert
+//                         -> sorted ids, positions, per-expert row offsets
+//                         and 128-row tile offsets
 //   lf_moe_quant_tokens   x [T, H] bf16            -> e4m3 + scales (per token
 //                         or per token per 128 columns)
 //   lf_moe_gate_up        grouped GEMM over expert gate/up weights with the
@@ -52,7 +53,9 @@ struct MoeLayout {
     h = o;        o = al256(o + A * I * 2);
     hq = o;       o = al256(o + A * I);
     hs = o;       o = al256(o + A * gh * 4);
-    y = o;        o = al256(o + A * H * 4);
+    // y also holds the sort's [chunks][E] count table before the down GEMM
+    const uint64_t table = ((A + 1023) / 1024) * d.experts * 4;
+    y = o;        o = al256(o + (A * H * 4 > table ? A * H * 4 : table));
     end = o;
   }
 };
@@ -151,87 +154,123 @@ LF_DEVICE void route(const int32_t *counts, const MoeDesc &d, const float *logit
 }
 
 // --- stable counting sort ----------------------------------------------------
-// One block of 1024 threads. Pass 1 counts assignments per expert; pass 2
-// walks the assignments in chunks of 1024 in ascending order and gives each
-// its rank among equal experts: within a wave by matching expert ids with
-// ballots over their bits, across the chunk's waves by a prefix over
-// per-wave counts, across chunks by running totals. Positions therefore
-// equal those of a stable sort.
+// Two launches over chunks of 1024 assignments (one 1024-thread block per
+// chunk). lf_moe_sort_count: each block counts its chunk's assignments per
+// expert into a [chunks][E] table. lf_moe_sort: each block sums the table
+// (expert totals, and the counts of the chunks before its own), derives the
+// expert row offsets, and ranks its chunk's assignments among equal experts:
+// within a wave by matching expert ids with ballots over their bits, across
+// the chunk's waves by a prefix over per-wave counts. Positions therefore
+// equal those of a stable sort. The table lives at the start of the y
+// region, which nothing reads before the down GEMM overwrites it.
 constexpr int kSortThreads = 1024;
 constexpr int kSortWaves = kSortThreads / 64;
 
+LF_DEVICE int32_t *chunk_table(uint8_t *ws, const MoeLayout &L) { return at<int32_t>(ws, L.y); }
+
+LF_DEVICE void sort_count(const int32_t *counts, const MoeDesc &d, uint8_t *ws) {
+  __shared__ int32_t cnt[256];
+  const int T = live_rows(counts, 1 << 30);
+  const MoeLayout L(d, T);
+  const int E = d.experts, A = T * d.top_k;
+  const int c = blockIdx.x;
+  if (c * kSortThreads >= A) return;
+  const int tid = threadIdx.x;
+  for (int e = tid; e < E; e += kSortThreads) cnt[e] = 0;
+  __syncthreads();
+  const int a = c * kSortThreads + tid;
+  if (a < A) atomicAdd(&cnt[at<int32_t>(ws, L.topk_ids)[a]], 1);
+  __syncthreads();
+  int32_t *table = chunk_table(ws, L) + static_cast<uint64_t>(c) * E;
+  for (int e = tid; e < E; e += kSortThreads) table[e] = cnt[e];
+}
+
 LF_DEVICE void sort_assignments(const int32_t *counts, const MoeDesc &d, uint8_t *ws) {
-  __shared__ int32_t cnt[257];
-  __shared__ int32_t running[256];
+  __shared__ int32_t base[256];  // first position of expert e's rows of this chunk
   __shared__ int32_t wcnt[kSortWaves][256];
   const int T = live_rows(counts, 1 << 30);
   const MoeLayout L(d, T);
   const int E = d.experts;
   const int A = T * d.top_k;
+  const int c = blockIdx.x;
+  if (A == 0) {
+    // No assignments: every expert is empty (the GEMMs then launch no tile).
+    if (c == 0) {
+      for (int e = threadIdx.x; e <= E; e += kSortThreads) {
+        at<int32_t>(ws, L.offsets)[e] = 0;
+        at<int32_t>(ws, L.tiles)[e] = 0;
+      }
+    }
+    return;
+  }
+  if (c * kSortThreads >= A) return;
+  const int chunks = (A + kSortThreads - 1) / kSortThreads;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int32_t *ids = at<int32_t>(ws, L.topk_ids);
+  const int32_t *table = chunk_table(ws, L);
   int32_t *sorted = at<int32_t>(ws, L.sorted);
   int32_t *pos = at<int32_t>(ws, L.pos);
   int32_t *offsets = at<int32_t>(ws, L.offsets);
   int32_t *tiles = at<int32_t>(ws, L.tiles);
+  // Per expert: total rows and rows in the chunks before this one.
   for (int e = tid; e < E; e += kSortThreads) {
-    cnt[e] = 0;
-    running[e] = 0;
+    int total = 0, before = 0;
+    for (int cc = 0; cc < chunks; ++cc) {
+      const int n = table[static_cast<uint64_t>(cc) * E + e];
+      total += n;
+      before += cc < c ? n : 0;
+    }
+    wcnt[0][e] = total;
+    base[e] = before;
   }
-  __syncthreads();
-  for (int a = tid; a < A; a += kSortThreads) atomicAdd(&cnt[ids[a]], 1);
   __syncthreads();
   if (tid == 0) {
-    // Exclusive scans: first row and first 128-row tile of each expert;
-    // cnt[e] becomes the first position of expert e.
+    // Exclusive scans: first row and first 128-row tile of each expert.
     int off = 0, tl = 0;
     for (int e = 0; e < E; ++e) {
-      const int c = cnt[e];
-      offsets[e] = off;
-      tiles[e] = tl;
-      cnt[e] = off;
-      off += c;
-      tl += (c + w8a8::kBM - 1) / w8a8::kBM;
+      const int n = wcnt[0][e];
+      if (c == 0) {
+        offsets[e] = off;
+        tiles[e] = tl;
+      }
+      base[e] += off;
+      off += n;
+      tl += (n + w8a8::kBM - 1) / w8a8::kBM;
     }
-    offsets[E] = off;
-    tiles[E] = tl;
+    if (c == 0) {
+      offsets[E] = off;
+      tiles[E] = tl;
+    }
   }
+  __syncthreads();
+  for (int i = tid; i < kSortWaves * E; i += kSortThreads) wcnt[i / E][i % E] = 0;
   int bits = 0;
   while ((1 << bits) < E + 1) ++bits;
   const uint64_t lt_mask = lane == 0 ? 0ull : (~0ull >> (64 - lane));
-  for (int base = 0; base < A; base += kSortThreads) {
-    for (int i = tid; i < kSortWaves * E; i += kSortThreads) wcnt[i / E][i % E] = 0;
-    __syncthreads();
-    const int a = base + tid;
-    const int e = a < A ? ids[a] : E;  // E marks lanes past the end
-    uint64_t same = ~0ull;
-    for (int b = 0; b < bits; ++b) {
-      const uint64_t ones = __ballot((e >> b) & 1);
-      same &= ((e >> b) & 1) ? ones : ~ones;
-    }
-    const int rank = __popcll(same & lt_mask);
-    if (e < E && rank == 0) wcnt[wave][e] = __popcll(same);
-    __syncthreads();
-    if (e < E) {
-      int before = 0;
-      for (int w = 0; w < wave; ++w) before += wcnt[w][e];
-      const int p = cnt[e] + running[e] + before + rank;
-      sorted[p] = a;
-      pos[a] = p;
-    }
-    __syncthreads();
-    for (int x = tid; x < E; x += kSortThreads) {
-      int s = 0;
-      for (int w = 0; w < kSortWaves; ++w) s += wcnt[w][x];
-      running[x] += s;
-    }
-    __syncthreads();
+  __syncthreads();
+  const int a = c * kSortThreads + tid;
+  const int e = a < A ? ids[a] : E;  // E marks lanes past the end
+  uint64_t same = ~0ull;
+  for (int b = 0; b < bits; ++b) {
+    const uint64_t ones = __ballot((e >> b) & 1);
+    same &= ((e >> b) & 1) ? ones : ~ones;
+  }
+  const int rank = __popcll(same & lt_mask);
+  if (e < E && rank == 0) wcnt[wave][e] = __popcll(same);
+  __syncthreads();
+  if (e < E) {
+    int before = 0;
+    for (int w = 0; w < wave; ++w) before += wcnt[w][e];
+    const int p = base[e] + before + rank;
+    sorted[p] = a;
+    pos[a] = p;
   }
 }
 
 // --- quantizers --------------------------------------------------------------
 // Per token (group 0): one wave per row, four rows per block. Per 128-column
-// group: 16 lanes per group, sixteen groups per block.
+// group: 16 lanes per group, four groups per wave at a time, the grid's waves
+// striding over all groups.
 LF_DEVICE void quant_rows(const uint16_t *src, int K, int group, uint8_t *dst, float *scales,
                            int rows) {
   if (group == 0) {
@@ -240,7 +279,8 @@ LF_DEVICE void quant_rows(const uint16_t *src, int K, int group, uint8_t *dst, f
     quantize_row_wave(src + static_cast<uint64_t>(row) * K, K, dst + static_cast<uint64_t>(row) * K,
                       scales + row);
   } else {
-    quantize_groups_wave(src, K, rows, dst, scales, blockIdx.x * 4 + (threadIdx.x >> 6));
+    quantize_groups_wave(src, K, rows, dst, scales, blockIdx.x * 4 + (threadIdx.x >> 6),
+                         gridDim.x * 4);
   }
 }
 
@@ -313,6 +353,7 @@ __device__ void grouped_gemm(const int32_t *counts, const MoeDesc &d, const uint
   // K <= 4096 (the host rejects larger K for 128-column groups).
   __shared__ float sa_lds[BLOCK ? 128 * 32 : 1];
   const int Tn = live_rows(counts, 1 << 30);
+  if (Tn == 0) return;
   const MoeLayout L(d, Tn);
   const int32_t *tiles = at<int32_t>(ws, L.tiles);
   const int E = d.experts;
@@ -465,6 +506,13 @@ __global__ __launch_bounds__(256) void lf_moe_route(const int32_t *counts, const
   const MoeDesc &d = desc_of(desc);
   if (!desc_ok(d)) return;
   route(counts, d, logits, ws);
+}
+
+__global__ __launch_bounds__(1024) void lf_moe_sort_count(const int32_t *counts,
+                                                          const int32_t *desc, uint8_t *ws) {
+  const MoeDesc &d = desc_of(desc);
+  if (!desc_ok(d)) return;
+  sort_count(counts, d, ws);
 }
 
 __global__ __launch_bounds__(1024) void lf_moe_sort(const int32_t *counts, const int32_t *desc,

@@ -55,25 +55,42 @@ LF_DEVICE void quantize_row_wave(const uint16_t *src_row, int K, uint8_t *dst_ro
 }
 
 // Per-128-column-group quantizer: the 16 lanes 16q..16q+15 of a wave hold
-// one group's 16 chunks; a wave quantizes groups 4 gw .. 4 gw + 3 of the
-// rows x (K / 128) groups (row-major), amax reduced across its 16 lanes.
+// one group's 16 chunks, so a wave quantizes a quad of four groups (of the
+// rows x (K / 128) groups, row-major) at a time, amax reduced across its 16
+// lanes. Wave gw of nw takes quads gw, gw + nw, ...; the loads of four quads
+// are issued before any of them is encoded.
 LF_DEVICE void quantize_groups_wave(const uint16_t *src, int K, int rows, uint8_t *dst,
-                                    float *scales, int gw) {
+                                    float *scales, int gw, int nw) {
   const int lane = threadIdx.x & 63;
   const int per_row = K >> 7;
-  const int gid = 4 * gw + (lane >> 4);
-  const bool live = gid < rows * per_row;
-  const int row = live ? gid / per_row : 0, kg = live ? gid - row * per_row : 0;
-  const uint64_t base = static_cast<uint64_t>(row) * K + kg * 128 + (lane & 15) * 8;
-  const uint4 v = live ? *reinterpret_cast<const uint4 *>(src + base) : make_uint4(0u, 0u, 0u, 0u);
-  float amax = bf16x8_amax(v, 0.0f);
+  const int groups = rows * per_row;
+  const int quads = (groups + 3) >> 2;
+  constexpr int kBatch = 4;
+  for (int q0 = gw; q0 < quads; q0 += kBatch * nw) {
+    uint4 v[kBatch];
+    uint64_t base[kBatch];
+    int gid[kBatch];
 #pragma unroll
-  for (int off = 8; off > 0; off >>= 1) amax = fmaxf(amax, __shfl_xor(amax, off));
-  const bool zero = amax == 0.0f;
-  const float ratio = zero ? 0.0f : 448.0f / amax;
-  if (!live) return;
-  *reinterpret_cast<uint2 *>(dst + base) = bf16x8_encode(v, ratio, zero);
-  if ((lane & 15) == 0) scales[gid] = zero ? 0.0f : amax / 448.0f;
+    for (int b = 0; b < kBatch; ++b) {
+      gid[b] = 4 * (q0 + b * nw) + (lane >> 4);
+      const bool live = gid[b] < groups;
+      const int row = live ? gid[b] / per_row : 0, kg = live ? gid[b] - row * per_row : 0;
+      base[b] = static_cast<uint64_t>(row) * K + kg * 128 + (lane & 15) * 8;
+      v[b] = live ? *reinterpret_cast<const uint4 *>(src + base[b]) : make_uint4(0u, 0u, 0u, 0u);
+    }
+#pragma unroll
+    for (int b = 0; b < kBatch; ++b) {
+      float amax = bf16x8_amax(v[b], 0.0f);
+#pragma unroll
+      for (int off = 8; off > 0; off >>= 1) amax = fmaxf(amax, __shfl_xor(amax, off));
+      const bool zero = amax == 0.0f;
+      const float ratio = zero ? 0.0f : 448.0f / amax;
+      if (gid[b] < groups) {
+        *reinterpret_cast<uint2 *>(dst + base[b]) = bf16x8_encode(v[b], ratio, zero);
+        if ((lane & 15) == 0) scales[gid[b]] = zero ? 0.0f : amax / 448.0f;
+      }
+    }
+  }
 }
 
 // One wave per row, four rows per block.

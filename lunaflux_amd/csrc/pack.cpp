@@ -4,6 +4,7 @@
 #include "lunaflux_fp8.h"
 #include "lunaflux_hip.h"
 
+#include <algorithm>
 #include <cstdint>
 #include <cstdio>
 #include <cstring>
@@ -269,6 +270,13 @@ int32_t lunaflux_fp8_launch_geometry(int32_t entry, int64_t n, int64_t k,
   return LF_OK;
 }
 
+// Blocks (4 waves, 4 groups per wave per step) for a per-128-group quantizer
+// of `groups` groups: at most 1024 blocks, each wave then loops.
+static int64_t group_quant_blocks(int64_t groups) {
+  const int64_t blocks = (groups + 15) / 16;
+  return blocks < 1024 ? blocks : 1024;
+}
+
 static bool moe_desc_ok(const lf_fp8_moe_desc *d) {
   return d != nullptr && d->magic == LF_FP8_MOE_MAGIC && d->experts >= 1 && d->experts <= 256 &&
          d->top_k >= 1 && d->top_k <= d->experts && d->top_k <= 16 &&
@@ -313,7 +321,9 @@ int32_t lunaflux_fp8_moe_workspace_layout(const lf_fp8_moe_desc *d, int32_t toke
       A * I * 2,              // h (bf16)
       A * I,                  // quantized h
       A * gh * 4,             // h scales
-      A * H * 4,              // y (fp32)
+      // y (fp32); before the down GEMM it holds the sort's [chunks][E]
+      // int32 count table (chunks of 1024 assignments), so it is never smaller
+      std::max<int64_t>(A * H * 4, (A + 1023) / 1024 * d->experts * 4),
   };
   int64_t o = 0;
   for (int i = 0; i < 12; ++i) {
@@ -350,10 +360,12 @@ int32_t lunaflux_fp8_moe_launch_geometry(int32_t entry, const lf_fp8_moe_desc *d
     // Routing and the per-token quantizers: one wave per token (row); the
     // per-128-column-group quantizers: four groups per wave.
     case LF_FP8_MOE_ROUTE: name = "lf_moe_route"; gx = (T + 3) / 4; break;
-    case LF_FP8_MOE_SORT: name = "lf_moe_sort"; bx = 1024; break;
+    // The sort: one 1024-thread block per chunk of 1024 assignments.
+    case LF_FP8_MOE_SORT_COUNT: name = "lf_moe_sort_count"; gx = (A + 1023) / 1024; bx = 1024; break;
+    case LF_FP8_MOE_SORT: name = "lf_moe_sort"; gx = (A + 1023) / 1024; bx = 1024; break;
     case LF_FP8_MOE_QUANT_TOKENS:
       name = "lf_moe_quant_tokens";
-      gx = b128 ? (T * (d->hidden / 128) + 15) / 16 : (T + 3) / 4;
+      gx = b128 ? group_quant_blocks(T * (d->hidden / 128)) : (T + 3) / 4;
       break;
     case LF_FP8_MOE_GATE_UP:
       // 1-D grid over (64 h-column block, 128-row tile); blocks past the
@@ -363,7 +375,7 @@ int32_t lunaflux_fp8_moe_launch_geometry(int32_t entry, const lf_fp8_moe_desc *d
       break;
     case LF_FP8_MOE_QUANT_HIDDEN:
       name = "lf_moe_quant_hidden";
-      gx = b128 ? (A * (d->inter / 128) + 15) / 16 : (A + 3) / 4;
+      gx = b128 ? group_quant_blocks(A * (d->inter / 128)) : (A + 3) / 4;
       break;
     case LF_FP8_MOE_DOWN:
       name = b128 ? "lf_moe_down_b128" : "lf_moe_down";

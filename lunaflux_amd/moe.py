@@ -78,7 +78,7 @@ class BoundMoe(BoundOperation):
 def bind_moe(rt: ProjectionRuntime, counts, desc: MoeDescriptor, desc_region: KernelArgument,
              logits: KernelArgument, x: KernelArgument, wg: Fp8Weight, wu: Fp8Weight,
              wd: Fp8Weight, out: KernelArgument, max_tokens: int) -> BoundMoe:
-    """Binds one MoE expert-MLP operation to its regions: 7 launch steps."""
+    """Binds one MoE expert-MLP operation to its regions: 8 launch steps."""
     e, h, i = desc.experts, desc.hidden, desc.inter
     mode = _abi.LF_FP8_SCALE_BLOCK128 if desc.group == 128 else _abi.LF_FP8_SCALE_PER_CHANNEL
     for w, rows, cols in ((wg, i, h), (wu, i, h), (wd, h, i)):
@@ -94,6 +94,7 @@ def bind_moe(rt: ProjectionRuntime, counts, desc: MoeDescriptor, desc_region: Ke
 
     steps = [
         step(_abi.MOE_ROUTE, [c, desc_region, logits, wsr]),
+        step(_abi.MOE_SORT_COUNT, [c, desc_region, wsr]),
         step(_abi.MOE_SORT, [c, desc_region, wsr]),
         step(_abi.MOE_QUANT_TOKENS, [c, desc_region, x, wsr]),
         step(_abi.MOE_GATE_UP, [c, desc_region, wg.region, wu.region, wsr]),

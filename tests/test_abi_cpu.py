@@ -37,7 +37,7 @@ def test_library_exports_every_declared_symbol():
 def test_code_object_has_every_entry_point():
     image = _abi.code_object_bytes()
     for symbol in ["lf_fp8_act_quant_rows"] + [f"lf_fp8_w8a8_{op}_{t}" for op in ("dense", "qkv", "gate_up")
-                                               for t in ("t128", "t256")] + ["lf_moe_route", "lf_moe_sort", "lf_moe_quant_tokens",
+                                               for t in ("t128", "t256")] + ["lf_moe_route", "lf_moe_sort_count", "lf_moe_sort", "lf_moe_quant_tokens",
                    "lf_moe_gate_up", "lf_moe_gate_up_b128", "lf_moe_quant_hidden", "lf_moe_down",
                    "lf_moe_down_b128", "lf_moe_combine"] + [f"lf_fp8_w8a16_{op}_m{m}" for op in ("dense", "qkv", "gate_up")
                                              for m in (16, 32, 64, 128)] + [
@@ -201,8 +201,10 @@ def test_moe_descriptor_layout_and_geometry():
     dims, sym = moe.launch_geometry(4, d, 1024)   # gate/up
     # 1-D grid over (64 h-column block, 128-row tile of the tile bound)
     assert sym == "lf_moe_gate_up" and dims.grid == (14336 // 64 * (a // 128 + 8), 1, 1)
-    dims, sym = moe.launch_geometry(2, d, 1024)   # sort: one block of 1024
-    assert sym == "lf_moe_sort" and dims.grid == (1, 1, 1) and dims.block == (1024, 1, 1)
+    dims, sym = moe.launch_geometry(2, d, 1024)   # sort: a block per 1024 assignments
+    assert sym == "lf_moe_sort" and dims.grid == (2, 1, 1) and dims.block == (1024, 1, 1)
+    dims, sym = moe.launch_geometry(8, d, 1024)   # sort counts: a block per 1024 assignments
+    assert sym == "lf_moe_sort_count" and dims.grid == (2, 1, 1)
     d5 = moe.moe_descriptor(64, 6, 1, 2048, 1408, 128)
     dims, sym = moe.launch_geometry(6, d5, 4096)  # down, block scales
     assert sym == "lf_moe_down_b128" and dims.grid == (2048 // 128 * (4096 * 6 // 128 + 64), 1, 1)

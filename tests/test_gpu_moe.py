@@ -119,7 +119,8 @@ def check_output(x, weights, ex, w, out, block, label, st):
     parity(out, ref, rel_l2=1e-2, max_abs=0.25, label=label + " end-to-end")
 
 
-@pytest.mark.parametrize("t,e,k,mode", [(100, 8, 2, 0), (37, 64, 6, 1), (1, 8, 2, 0), (300, 16, 4, 0)])
+@pytest.mark.parametrize("t,e,k,mode", [(100, 8, 2, 0), (37, 64, 6, 1), (1, 8, 2, 0), (300, 16, 4, 0),
+                                         (1500, 32, 4, 1)])
 def test_moe_per_channel(rt, t, e, k, mode):
     rng = np.random.default_rng(700 + t + e)
     x, logits, weights, out, st = run_case(rt, rng, t, e, k, 256, 384, mode, block=False)
@@ -148,6 +149,17 @@ def test_moe_all_tokens_one_expert_and_ties(rt):
     assert (ex[:, 0] == 5).all() and (ex[:, 1] == 0).all()   # ties go to the lowest id
     assert st["offsets"].tolist() == [0, 300, 300, 300, 300, 300, 600, 600, 600]
     check_output(x, weights, ex, w, out, False, "moe one expert", st)
+
+
+def test_moe_sort_across_chunks(rt):
+    """The sort ranks assignments in chunks of 1024 across blocks; 3000 x 6
+    assignments over 64 experts (18 chunks) must still give exactly the
+    stable-sort positions, offsets and tile offsets (checked in
+    check_routing against the oracle's sort)."""
+    rng = np.random.default_rng(902)
+    x, logits, weights, out, st = run_case(rt, rng, 3000, 64, 6, 128, 128, 1, block=False)
+    check_routing(logits, 6, 1, st)
+    assert st["offsets"][-1] == 3000 * 6
 
 
 def test_moe_zero_tokens(rt):
