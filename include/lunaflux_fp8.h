@@ -152,6 +152,21 @@ int32_t lunaflux_fp8_launch_geometry(int32_t entry, int64_t n, int64_t k,
                                      int32_t max_tokens, int32_t dims[7],
                                      char symbol[LF_FP8_SYMBOL_BYTES]);
 
+/* W8A16 profiles with max_query_tokens <= 32 select a shape-specialized
+ * entry (K, and for QKV the Q / K-V split, compiled into the symbol, e.g.
+ * lf_fp8_w8a16_gate_up_k4096_m32) where one is built, like an AOT kernel
+ * compiled for one model shape; other shapes use the generic entries. A
+ * specialized entry checks the weight header against its compiled shape and
+ * leaves the output unwritten on a mismatch. The QKV split is not
+ * recoverable from N alone, so QKV operations call these variants with
+ * Nq and Nk = Nv (the catalog records the split of the model's layer); the
+ * plain functions above pick the generic QKV entry. */
+int32_t lunaflux_fp8_qkv_launch_geometry(int32_t entry, int64_t nq, int64_t nkv, int64_t k,
+                                         int32_t max_tokens, int32_t dims[7],
+                                         char symbol[LF_FP8_SYMBOL_BYTES]);
+int64_t lunaflux_fp8_qkv_w8a16_workspace_bytes(int64_t nq, int64_t nkv, int64_t k,
+                                               int32_t max_tokens);
+
 /* ---- grouped form: MoE expert MLP ---------------------------------------- */
 /*
  * The reference has no MoE (its plan vocabulary stops at GatedMlp,

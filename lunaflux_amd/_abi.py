@@ -98,6 +98,9 @@ SIGNATURES = {
     "lunaflux_fp8_act_quant_bytes": (_i64, [_i64, _i64]),
     "lunaflux_fp8_w8a16_workspace_bytes": (_i64, [_i32, _i64, _i64, _i32]),
     "lunaflux_fp8_launch_geometry": (_i32, [_i32, _i64, _i64, _i32, _i32p, ctypes.c_char_p]),
+    "lunaflux_fp8_qkv_launch_geometry": (_i32, [_i32, _i64, _i64, _i64, _i32, _i32p,
+                                                ctypes.c_char_p]),
+    "lunaflux_fp8_qkv_w8a16_workspace_bytes": (_i64, [_i64, _i64, _i64, _i32]),
     "lunaflux_fp8_moe_descriptor": (_i32, [_i32, _i32, _i32, _i64, _i64, _i32, _vp]),
     "lunaflux_fp8_moe_workspace_bytes": (_i64, [_vp, _i32]),
     "lunaflux_fp8_moe_workspace_layout": (_i32, [_vp, _i32, _i64p]),

@@ -6,6 +6,8 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include <utility>
+
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 typedef int i32x8 __attribute__((ext_vector_type(8)));
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
@@ -13,6 +15,18 @@ typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
 
 #define LF_DEVICE __device__ __forceinline__
+
+// Calls f(std::integral_constant<int, i>) for i = 0 .. N-1 in order: a loop
+// whose index is a constant expression in the body, so register arrays
+// indexed by it stay in registers.
+template <class F, int... I>
+LF_DEVICE void static_for_impl(F &&f, std::integer_sequence<int, I...>) {
+  (f(std::integral_constant<int, I>{}), ...);
+}
+template <int N, class F>
+LF_DEVICE void static_for(F &&f) {
+  static_for_impl(f, std::make_integer_sequence<int, N>{});
+}
 
 // Mirror of lf_fp8_weight_header (include/lunaflux_fp8.h); only the fields
 // the kernels read.
@@ -23,6 +37,9 @@ struct WeightHeader {
 };
 
 constexpr uint32_t kWeightMagic = 0x5738464Cu;
+constexpr uint32_t kScalePerChannel = 1u;
+// Header size = tile_offset of every region written by the host pack.
+constexpr uint64_t kWeightHeaderBytes = 256;
 constexpr int kTileBytes = 2048;
 constexpr int kQueryTokensIndex = 3;
 

@@ -33,6 +33,8 @@ union Frag16 {
   bf16x8 v;
 };
 
+LF_DEVICE int wave_index() { return static_cast<int>(threadIdx.x) >> 6; }
+
 // Converts the 8 e4m3 codes of sub-chunk j (k = 32g + 8j .. +8 of this lane)
 // to a bf16x8 B fragment.
 LF_DEVICE bf16x8 weight_fragment(const uint4 (&t)[2], int j) {
@@ -80,6 +82,137 @@ LF_DEVICE void wait_vm_multiple(int n) {
       wait_vm_multiple<PER, N - 1>(n);
     }
   }
+}
+
+// Epilogue of the column-group forms. Lane element (mt, rr) of acc is output
+// row mt*16 + 4g + rr of column out_tile*16 + r (16x16 MFMA accumulator
+// layout). S == 1: scale (+ SwiGLU) and store. S > 1 (split-K): the
+// workspace holds, per slice, one fp32 accumulator fragment (4 values per
+// lane: rows 4g..4g+3 of a 16-row tile) for each (tile, weight, row tile),
+// fragment index ((s * tiles + out_tile) * NW + i) * MT + mt, then one
+// arrival counter per column group. Row groups wholly past M are neither
+// stored nor loaded. The last block of a group to arrive sums the S
+// fragments in slice order 0..S-1 (its own from registers) and stores; it
+// also resets the group's counter for the next launch.
+//
+// Partials travel through the device-coherent level without any cache
+// maintenance: agent-scope atomic stores and loads write through / bypass
+// the per-XCD L2, and this wave's stores are complete (s_waitcnt vmcnt(0))
+// before the block's arrival is counted. (A device-scope fence would write
+// back and invalidate the whole L2 of the XCD, once per block.)
+// Fragment layout: 256 floats, element e of lane l at e * 64 + l, so each
+// store or load instruction covers 256 contiguous bytes.
+template <int MT, int NW, int MODE>
+LF_DEVICE void group_epilogue(const f32x4 (&acc)[MT][NW], const float (&sc)[NW], int M, int S,
+                              int s, int cg, int tiles, int out_tile, bool active, int ld,
+                              uint16_t *y, uint8_t *ws, int &last_block) {
+  const int lane = threadIdx.x & 63;
+  const int g = lane >> 4, r = lane & 15;
+  const int col = out_tile * 16 + r;
+  auto finish = [&](int m, const float (&v)[NW]) {
+    const float out = MODE == 2 ? silu_mul(v[0] * sc[0], v[NW - 1] * sc[NW - 1]) : v[0] * sc[0];
+    y[static_cast<uint64_t>(m) * ld + col] = static_cast<uint16_t>(f32_to_bf16(out));
+  };
+  if (S == 1) {
+    if (!active) return;
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+      for (int rr = 0; rr < 4; ++rr) {
+        const int m = mt * 16 + 4 * g + rr;
+        if (m < M) {
+          float v[NW];
+#pragma unroll
+          for (int i = 0; i < NW; ++i) v[i] = acc[mt][i][rr];
+          finish(m, v);
+        }
+      }
+    return;
+  }
+
+  float *part = reinterpret_cast<float *>(ws);
+  int *arrivals = reinterpret_cast<int *>(
+      ws + align256(static_cast<uint64_t>(S) * tiles * NW * MT * 256 * sizeof(float)));
+  auto frag_at = [&](int slice, int i, int mt) -> float * {
+    return part + ((static_cast<uint64_t>(slice) * tiles + out_tile) * NW * MT + i * MT + mt) * 256 + lane;
+  };
+  if (active) {
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt) {
+      if (mt * 16 + 4 * g < M) {
+#pragma unroll
+        for (int i = 0; i < NW; ++i) {
+          float *p = frag_at(s, i, mt);
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            __hip_atomic_store(p + 64 * e, acc[mt][i][e], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+          }
+        }
+      }
+    }
+  }
+  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    const int before =
+        __hip_atomic_fetch_add(arrivals + cg, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    const bool last = before == S - 1;
+    // Every block of the group has arrived: reset for the next launch.
+    if (last) __hip_atomic_store(arrivals + cg, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    last_block = last ? 1 : 0;
+  }
+  __syncthreads();
+  if (last_block == 0 || !active) return;
+  // Sum the S partial fragments in slice order (this block's own from its
+  // registers). Loads of kBatch slices are issued before any is added.
+  constexpr int kBatch = 4;
+  f32x4 sum[MT][NW];
+#pragma unroll
+  for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+    for (int i = 0; i < NW; ++i) sum[mt][i] = f32x4{0.f, 0.f, 0.f, 0.f};
+  for (int s0 = 0; s0 < S; s0 += kBatch) {
+    f32x4 v[kBatch][MT][NW];
+#pragma unroll
+    for (int b = 0; b < kBatch; ++b) {
+      const int slice = s0 + b;
+#pragma unroll
+      for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+        for (int i = 0; i < NW; ++i) {
+          if (slice < S && slice != s && mt * 16 + 4 * g < M) {
+            const float *p = frag_at(slice, i, mt);
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+              v[b][mt][i][e] = __hip_atomic_load(p + 64 * e, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            }
+          } else {
+            v[b][mt][i] = acc[mt][i];
+          }
+        }
+    }
+#pragma unroll
+    for (int b = 0; b < kBatch; ++b) {
+      if (s0 + b < S) {
+#pragma unroll
+        for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+          for (int i = 0; i < NW; ++i) sum[mt][i] += v[b][mt][i];
+      }
+    }
+  }
+#pragma unroll
+  for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+    for (int rr = 0; rr < 4; ++rr) {
+      const int m = mt * 16 + 4 * g + rr;
+      if (m < M) {
+        float v[NW];
+#pragma unroll
+        for (int i = 0; i < NW; ++i) v[i] = sum[mt][i][rr];
+        finish(m, v);
+      }
+    }
 }
 
 // MODE 0: dense, 1: qkv (three weights, packed Q|K|V output), 2: gate/up.
@@ -230,126 +363,7 @@ __device__ void w8a16_kernel(const int32_t *counts, const uint16_t *x, const uin
     }
   }
 
-  // Epilogue. Lane element (mt, rr) is output row mt*16 + 4*g + rr of
-  // column out_tile*16 + r (16x16 MFMA accumulator layout).
-  const int col = out_tile * 16 + r;
-  auto finish = [&](int m, const float (&v)[NW]) {
-    const float out = MODE == 2 ? silu_mul(v[0] * sc[0], v[NW - 1] * sc[NW - 1]) : v[0] * sc[0];
-    y[static_cast<uint64_t>(m) * ld + col] = static_cast<uint16_t>(f32_to_bf16(out));
-  };
-  if (S == 1) {
-    if (!active) return;
-#pragma unroll
-    for (int mt = 0; mt < MT; ++mt)
-#pragma unroll
-      for (int rr = 0; rr < 4; ++rr) {
-        const int m = mt * 16 + 4 * g + rr;
-        if (m < M) {
-          float v[NW];
-#pragma unroll
-          for (int i = 0; i < NW; ++i) v[i] = acc[mt][i][rr];
-          finish(m, v);
-        }
-      }
-    return;
-  }
-
-  // Split-K. The workspace holds, per slice, one fp32 accumulator fragment
-  // (4 values per lane: rows 4g..4g+3 of a 16-row tile) for each (tile,
-  // weight, row tile), fragment index ((s * tiles + out_tile) * NW + i) * MT
-  // + mt, then one arrival counter per column group. Row groups wholly past
-  // M are neither stored nor loaded.
-  //
-  // Partials travel through the device-coherent level without any cache
-  // maintenance: agent-scope atomic stores and loads write through / bypass
-  // the per-XCD L2, and this wave's stores are complete (s_waitcnt vmcnt(0))
-  // before the block's arrival is counted. (A device-scope fence would write
-  // back and invalidate the whole L2 of the XCD, once per block.)
-  // Fragment layout: 256 floats, element e of lane l at e * 64 + l, so each
-  // store or load instruction covers 256 contiguous bytes.
-  float *part = reinterpret_cast<float *>(ws);
-  int *arrivals = reinterpret_cast<int *>(
-      ws + align256(static_cast<uint64_t>(S) * tiles * NW * MT * 256 * sizeof(float)));
-  auto frag_at = [&](int slice, int i, int mt) -> float * {
-    return part + ((static_cast<uint64_t>(slice) * tiles + out_tile) * NW * MT + i * MT + mt) * 256 + lane;
-  };
-  if (active) {
-#pragma unroll
-    for (int mt = 0; mt < MT; ++mt) {
-      if (mt * 16 + 4 * g < M) {
-#pragma unroll
-        for (int i = 0; i < NW; ++i) {
-          float *p = frag_at(s, i, mt);
-#pragma unroll
-          for (int e = 0; e < 4; ++e) {
-            __hip_atomic_store(p + 64 * e, acc[mt][i][e], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-          }
-        }
-      }
-    }
-  }
-  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-  __syncthreads();
-  if (threadIdx.x == 0) {
-    const int before =
-        __hip_atomic_fetch_add(arrivals + cg, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    const bool last = before == S - 1;
-    // Every block of the group has arrived: reset for the next launch.
-    if (last) __hip_atomic_store(arrivals + cg, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    last_block = last ? 1 : 0;
-  }
-  __syncthreads();
-  if (last_block == 0 || !active) return;
-  // Sum the S partial fragments in slice order (this block's own from its
-  // registers). Loads of kBatch slices are issued before any is added.
-  constexpr int kBatch = 4;
-  f32x4 sum[MT][NW];
-#pragma unroll
-  for (int mt = 0; mt < MT; ++mt)
-#pragma unroll
-    for (int i = 0; i < NW; ++i) sum[mt][i] = f32x4{0.f, 0.f, 0.f, 0.f};
-  for (int s0 = 0; s0 < S; s0 += kBatch) {
-    f32x4 v[kBatch][MT][NW];
-#pragma unroll
-    for (int b = 0; b < kBatch; ++b) {
-      const int slice = s0 + b;
-#pragma unroll
-      for (int mt = 0; mt < MT; ++mt)
-#pragma unroll
-        for (int i = 0; i < NW; ++i) {
-          if (slice < S && slice != s && mt * 16 + 4 * g < M) {
-            const float *p = frag_at(slice, i, mt);
-#pragma unroll
-            for (int e = 0; e < 4; ++e) {
-              v[b][mt][i][e] = __hip_atomic_load(p + 64 * e, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-            }
-          } else {
-            v[b][mt][i] = acc[mt][i];
-          }
-        }
-    }
-#pragma unroll
-    for (int b = 0; b < kBatch; ++b) {
-      if (s0 + b < S) {
-#pragma unroll
-        for (int mt = 0; mt < MT; ++mt)
-#pragma unroll
-          for (int i = 0; i < NW; ++i) sum[mt][i] += v[b][mt][i];
-      }
-    }
-  }
-#pragma unroll
-  for (int mt = 0; mt < MT; ++mt)
-#pragma unroll
-    for (int rr = 0; rr < 4; ++rr) {
-      const int m = mt * 16 + 4 * g + rr;
-      if (m < M) {
-        float v[NW];
-#pragma unroll
-        for (int i = 0; i < NW; ++i) v[i] = sum[mt][i][rr];
-        finish(m, v);
-      }
-    }
+  group_epilogue<MT, NW, MODE>(acc, sc, M, S, s, cg, tiles, out_tile, active, ld, y, ws, last_block);
 }
 
 // ---------------------------------------------------------------------------
@@ -482,6 +496,338 @@ __device__ void w8a16_tile_kernel(const int32_t *counts, const uint16_t *x, cons
   }
 }
 
+// ---------------------------------------------------------------------------
+// Shape-specialized one-tile form. The input width K (and, for QKV, the Q and
+// K/V widths) is a compile-time constant, as in an AOT entry point built for
+// one model shape; the output width comes from the grid (one block per
+// 16-column tile). Nothing on the load path waits for the weight header: the
+// block issues its weight k-tiles the moment it starts, and checks the header
+// against the compiled shape only before it stores.
+//
+// A block of KS waves owns one output tile (NW weights: gate and up for
+// gate/up); wave w owns k-tiles [w KTW, (w + 1) KTW). Each wave keeps DW
+// weight k-tiles and DX activation k-tiles in flight in registers. The loop
+// over its KTW k-tiles is fully unrolled and branch-free, and the loads of
+// step k + DX (activation) and k + DW (weights) are issued right after step
+// k's MFMAs, activations first, so each step waits only for loads issued DX
+// steps earlier: the compiler's s_waitcnt counts are exact and the weight
+// stream never drains between k-tiles. (A rolled loop with conditional
+// refills makes the compiler fall back to vmcnt(0) at every step, which
+// serializes the ring.) The KS partial tiles are summed in LDS in wave order.
+// ---------------------------------------------------------------------------
+template <int K, int KS, int MT, int MODE, int DW, int DX, int NQ = 0, int NKV = 0, int SLOTS = 2>
+__device__ void w8a16_fixed_kernel(const int32_t *counts, const uint16_t *x, const uint8_t *w0,
+                                   const uint8_t *w1, const uint8_t *w2, uint16_t *y) {
+  constexpr int NW = MODE == 2 ? 2 : 1;
+  constexpr int KT = K / 128;
+  static_assert(K % 128 == 0 && KT % KS == 0, "K splits evenly over the waves");
+  constexpr int KTW = KT / KS;
+  constexpr int EW = DW < KTW ? DW : KTW;
+  constexpr int EX = DX < EW ? DX : EW;
+  constexpr int XI = 4 * MT;  // 1 KiB activation loads per k-tile (4 rows each)
+  static_assert(MODE != 1 || (NQ % 16 == 0 && NKV % 16 == 0 && NQ > 0 && NKV > 0), "qkv widths");
+  // Per wave: SLOTS k-tile slots of 16 MT activation rows (256 bytes each;
+  // row r keeps 16-byte chunk c at position c ^ (r & 15), so both the
+  // row-wise writes and the 16-row fragment reads hit distinct banks). With
+  // one slot, step k + 1's writes queue behind step k's fragment reads (a
+  // wave's LDS instructions execute in order). The partial tiles of the K
+  // reduction reuse the same memory after the main loop.
+  static_assert(SLOTS == 1 || SLOTS == 2, "activation slots");
+  constexpr int kSlot = 16 * MT * 16;  // 16-byte chunks per slot
+  constexpr int kXsBytes = KS * SLOTS * kSlot * 16;
+  constexpr int kRedBytes = KS * MT * NW * 64 * 16;
+  __shared__ __attribute__((aligned(16))) u32x4 smem[(kXsBytes > kRedBytes ? kXsBytes : kRedBytes) / 16];
+  u32x4 *xs = smem + wave_index() * SLOTS * kSlot;
+  f32x4 *red = reinterpret_cast<f32x4 *>(smem);
+
+  const int tiles = static_cast<int>(gridDim.x);
+  const int out_tile = static_cast<int>(blockIdx.x);
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int g = lane >> 4, r = lane & 15;
+  const int ld = MODE == 1 ? NQ + 2 * NKV : 16 * tiles;
+
+  int t = out_tile;
+  const uint8_t *region[NW];
+  int region_rows = 16 * tiles;
+  region[0] = w0;
+  if constexpr (MODE == 1) {
+    constexpr int tq = NQ / 16, tk = NKV / 16;
+    region_rows = NQ;
+    if (t >= tq + tk) {
+      region[0] = w2;
+      t -= tq + tk;
+      region_rows = NKV;
+    } else if (t >= tq) {
+      region[0] = w1;
+      t -= tq;
+      region_rows = NKV;
+    }
+  }
+  if constexpr (NW == 2) region[NW - 1] = w1;
+  const uint64_t tile_base = kWeightHeaderBytes + static_cast<uint64_t>(t) * KT * kTileBytes;
+  const uint8_t *strip[NW];
+#pragma unroll
+  for (int i = 0; i < NW; ++i) strip[i] = region[i] + tile_base;
+
+  // Channel scales of the column this thread finishes in the epilogue:
+  // per-channel scales follow the N x K tile block.
+  const int ec = (threadIdx.x >> 2) & 15;
+  float sc[NW];
+#pragma unroll
+  for (int i = 0; i < NW; ++i) {
+    sc[i] = reinterpret_cast<const float *>(
+        region[i] + kWeightHeaderBytes + static_cast<uint64_t>(region_rows) * K)[t * 16 + ec];
+  }
+
+  const int kt0 = wave * KTW;
+  uint4 b[EW][NW][2];
+#pragma unroll
+  for (int d = 0; d < EW; ++d) load_tiles<NW>(strip, kt0 + d, lane, b[d]);
+  // sched_barrier pins the issue order written here: the scheduler would
+  // otherwise sink each load to just before its use to save registers,
+  // which leaves only a k-tile or two in flight.
+  __builtin_amdgcn_sched_barrier(0);
+
+  const int M = live_rows(counts, 16 * MT);
+  // Activation loads are row-coalesced: instruction q gives lane l row
+  // 4 q + l / 16, 16-byte chunk l % 16 of the k-tile (rows past M re-read row
+  // M - 1; their outputs are never stored. M == 0 stores nothing).
+  const uint16_t *xsrc[XI];
+  int xdst[XI];
+#pragma unroll
+  for (int q = 0; q < XI; ++q) {
+    const int row = 4 * q + (lane >> 4);
+    const int src = row < M ? row : (M > 0 ? M - 1 : 0);
+    xsrc[q] = x + static_cast<uint64_t>(src) * K + kt0 * 128 + (lane & 15) * 8;
+    xdst[q] = row * 16 + ((lane & 15) ^ (row & 15));
+  }
+  auto load_a = [&](int k, u32x4 (&dst)[XI]) {
+#pragma unroll
+    for (int q = 0; q < XI; ++q) dst[q] = *reinterpret_cast<const u32x4 *>(xsrc[q] + k * 128);
+  };
+  u32x4 a[EX][XI];
+#pragma unroll
+  for (int d = 0; d < EX; ++d) load_a(d, a[d]);
+  __builtin_amdgcn_sched_barrier(0);
+
+  f32x4 acc[MT][NW];
+#pragma unroll
+  for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+    for (int i = 0; i < NW; ++i) acc[mt][i] = f32x4{0.f, 0.f, 0.f, 0.f};
+  static_for<KTW>([&](auto kc) {
+    constexpr int k = decltype(kc)::value;
+    u32x4 *slot = xs + (k % SLOTS) * kSlot;
+#pragma unroll
+    for (int q = 0; q < XI; ++q) slot[xdst[q]] = a[k % EX][q];
+    __builtin_amdgcn_sched_barrier(0);
+    if constexpr (k + EX < KTW) load_a(k + EX, a[k % EX]);
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      bf16x8 af[MT];
+#pragma unroll
+      for (int mt = 0; mt < MT; ++mt) {
+        af[mt] = __builtin_bit_cast(bf16x8, slot[(16 * mt + r) * 16 + (((g << 2) | j) ^ r)]);
+      }
+#pragma unroll
+      for (int i = 0; i < NW; ++i) {
+        const bf16x8 bf = weight_fragment(b[k % EW][i], j);
+#pragma unroll
+        for (int mt = 0; mt < MT; ++mt) {
+          acc[mt][i] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(af[mt], bf, acc[mt][i], 0, 0, 0);
+        }
+      }
+    }
+    __builtin_amdgcn_sched_barrier(0);
+    if constexpr (k + EW < KTW) load_tiles<NW>(strip, kt0 + k + EW, lane, b[k % EW]);
+    __builtin_amdgcn_sched_barrier(0);
+  });
+
+  __syncthreads();  // every wave is done with its activation slots
+#pragma unroll
+  for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+    for (int i = 0; i < NW; ++i) red[(wave * MT * NW + mt * NW + i) * 64 + lane] = acc[mt][i];
+  __syncthreads();
+
+  // The compiled shape must be the regions' shape; a mismatched region
+  // (wrong weight bound to this entry) leaves the output unwritten.
+  bool ok = true;
+#pragma unroll
+  for (int i = 0; i < NW; ++i) {
+    const WeightHeader &h = header_of(region[i]);
+    ok = ok && h.magic == kWeightMagic && h.columns == static_cast<uint32_t>(K) &&
+         h.rows == static_cast<uint32_t>(region_rows) && h.experts == 1u &&
+         h.scale_mode == kScalePerChannel;
+  }
+  if (!ok) return;
+  // Element e of the tile: row tile mt, lane l, register rr (16x16 MFMA
+  // accumulator layout: row 4 (l / 16) + rr, column l % 16).
+  for (int e = threadIdx.x; e < MT * 256; e += KS * 64) {
+    const int mt = e >> 8, l = (e >> 2) & 63, rr = e & 3;
+    const int m = mt * 16 + 4 * (l >> 4) + rr;
+    if (m >= M) continue;
+    float v[NW];
+#pragma unroll
+    for (int i = 0; i < NW; ++i) {
+      float sum = 0.0f;
+#pragma unroll
+      for (int wv = 0; wv < KS; ++wv) sum += red[(wv * MT * NW + mt * NW + i) * 64 + l][rr];
+      v[i] = sum;
+    }
+    const float out = MODE == 2 ? silu_mul(v[0] * sc[0], v[NW - 1] * sc[NW - 1]) : v[0] * sc[0];
+    y[static_cast<uint64_t>(m) * ld + out_tile * 16 + ec] = static_cast<uint16_t>(f32_to_bf16(out));
+  }
+}
+
+// ---------------------------------------------------------------------------
+// Shape-specialized column-group form: the split-K structure of
+// w8a16_kernel (a block = WAVES adjacent 16-column tiles, one per wave, over
+// one of S K-slices; partials reduced by group_epilogue) with the input
+// width K and S compile-time, so each wave's loop over its K / (128 S)
+// k-tiles is fully unrolled and branch-free and the compiler's s_waitcnt
+// counts are exact (see w8a16_fixed_kernel). The activation k-tile (16 MT
+// rows) is loaded cooperatively with row-coalesced 1 KiB loads into
+// registers (XI / WAVES loads per wave, DX k-tiles ahead), written to one of
+// two LDS slots (chunk c of row r at c ^ (r & 15)), and shared by the block's
+// waves after one barrier per k-tile. The barrier waits only for LDS
+// writes (no memory fence), so the weight ring stays in flight across it.
+// ---------------------------------------------------------------------------
+template <int K, int S, int WAVES, int MT, int MODE, int DW, int DX, int NQ = 0, int NKV = 0>
+__device__ void w8a16_fixed_group_kernel(const int32_t *counts, const uint16_t *x,
+                                         const uint8_t *w0, const uint8_t *w1, const uint8_t *w2,
+                                         uint16_t *y, uint8_t *ws) {
+  constexpr int NW = MODE == 2 ? 2 : 1;
+  constexpr int KT = K / 128;
+  static_assert(K % 128 == 0 && KT % S == 0, "K splits evenly into the slices");
+  constexpr int NKT = KT / S;
+  constexpr int EW = DW < NKT ? DW : NKT;
+  constexpr int EX = DX < EW ? DX : EW;
+  constexpr int XI = 4 * MT;
+  static_assert(XI % WAVES == 0, "activation loads split evenly over the waves");
+  constexpr int XPW = XI / WAVES;
+  static_assert(MODE != 1 || (NQ % 16 == 0 && NKV % 16 == 0 && NQ > 0 && NKV > 0), "qkv widths");
+  constexpr int kSlot = 16 * MT * 16;  // 16-byte chunks per slot
+  __shared__ __attribute__((aligned(16))) u32x4 xs[2 * kSlot];
+  __shared__ int last_block;
+
+  const int groups = static_cast<int>(gridDim.x) / S;
+  const int cg = static_cast<int>(blockIdx.x) / S;
+  const int s = static_cast<int>(blockIdx.x) - cg * S;
+  const int tiles = groups * WAVES;
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int g = lane >> 4, r = lane & 15;
+  const int ld = MODE == 1 ? NQ + 2 * NKV : 16 * tiles;
+  const int out_tile = cg * WAVES + wave;
+
+  int t = out_tile;
+  const uint8_t *region[NW];
+  int region_rows = 16 * tiles;
+  region[0] = w0;
+  if constexpr (MODE == 1) {
+    constexpr int tq = NQ / 16, tk = NKV / 16;
+    region_rows = NQ;
+    if (t >= tq + tk) {
+      region[0] = w2;
+      t -= tq + tk;
+      region_rows = NKV;
+    } else if (t >= tq) {
+      region[0] = w1;
+      t -= tq;
+      region_rows = NKV;
+    }
+  }
+  if constexpr (NW == 2) region[NW - 1] = w1;
+  const int kt0 = s * NKT;
+  const uint64_t tile_base = kWeightHeaderBytes + static_cast<uint64_t>(t) * KT * kTileBytes;
+  const uint8_t *strip[NW];
+#pragma unroll
+  for (int i = 0; i < NW; ++i) strip[i] = region[i] + tile_base;
+  float sc[NW];
+#pragma unroll
+  for (int i = 0; i < NW; ++i) {
+    sc[i] = reinterpret_cast<const float *>(
+        region[i] + kWeightHeaderBytes + static_cast<uint64_t>(region_rows) * K)[t * 16 + r];
+  }
+
+  uint4 b[EW][NW][2];
+#pragma unroll
+  for (int d = 0; d < EW; ++d) load_tiles<NW>(strip, kt0 + d, lane, b[d]);
+  __builtin_amdgcn_sched_barrier(0);
+
+  const int M = live_rows(counts, 16 * MT);
+  const uint16_t *xsrc[XPW];
+  int xdst[XPW];
+#pragma unroll
+  for (int j = 0; j < XPW; ++j) {
+    const int q = wave * XPW + j;
+    const int row = 4 * q + (lane >> 4);
+    const int src = row < M ? row : (M > 0 ? M - 1 : 0);
+    xsrc[j] = x + static_cast<uint64_t>(src) * K + kt0 * 128 + (lane & 15) * 8;
+    xdst[j] = row * 16 + ((lane & 15) ^ (row & 15));
+  }
+  auto load_a = [&](int k, u32x4 (&dst)[XPW]) {
+#pragma unroll
+    for (int j = 0; j < XPW; ++j) dst[j] = *reinterpret_cast<const u32x4 *>(xsrc[j] + k * 128);
+  };
+  u32x4 a[EX][XPW];
+#pragma unroll
+  for (int d = 0; d < EX; ++d) load_a(d, a[d]);
+  __builtin_amdgcn_sched_barrier(0);
+
+  f32x4 acc[MT][NW];
+#pragma unroll
+  for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+    for (int i = 0; i < NW; ++i) acc[mt][i] = f32x4{0.f, 0.f, 0.f, 0.f};
+  static_for<NKT>([&](auto kc) {
+    constexpr int k = decltype(kc)::value;
+    u32x4 *slot = xs + (k & 1) * kSlot;
+#pragma unroll
+    for (int j = 0; j < XPW; ++j) slot[xdst[j]] = a[k % EX][j];
+    __builtin_amdgcn_sched_barrier(0);
+    if constexpr (k + EX < NKT) load_a(k + EX, a[k % EX]);
+    // This wave's rows of k-tile k are in LDS; once every wave's are, the
+    // slot is complete. (The other slot was last read at step k - 1, whose
+    // fragment reads every wave consumed before this barrier.)
+    asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      bf16x8 af[MT];
+#pragma unroll
+      for (int mt = 0; mt < MT; ++mt) {
+        af[mt] = __builtin_bit_cast(bf16x8, slot[(16 * mt + r) * 16 + (((g << 2) | j) ^ r)]);
+      }
+#pragma unroll
+      for (int i = 0; i < NW; ++i) {
+        const bf16x8 bf = weight_fragment(b[k % EW][i], j);
+#pragma unroll
+        for (int mt = 0; mt < MT; ++mt) {
+          acc[mt][i] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(af[mt], bf, acc[mt][i], 0, 0, 0);
+        }
+      }
+    }
+    __builtin_amdgcn_sched_barrier(0);
+    if constexpr (k + EW < NKT) load_tiles<NW>(strip, kt0 + k + EW, lane, b[k % EW]);
+    __builtin_amdgcn_sched_barrier(0);
+  });
+
+  bool ok = true;
+#pragma unroll
+  for (int i = 0; i < NW; ++i) {
+    const WeightHeader &h = header_of(region[i]);
+    ok = ok && h.magic == kWeightMagic && h.columns == static_cast<uint32_t>(K) &&
+         h.rows == static_cast<uint32_t>(region_rows) && h.experts == 1u &&
+         h.scale_mode == kScalePerChannel;
+  }
+  // A mismatched region leaves the output unwritten; every block still takes
+  // part in the arrival count so the counters stay consistent.
+  group_epilogue<MT, NW, MODE>(acc, sc, ok ? M : 0, S, s, cg, tiles, out_tile, true, ld, y, ws,
+                               last_block);
+}
+
 }  // namespace
 
 #ifndef LF_W16_WAVES
@@ -531,5 +877,48 @@ LF_W8A16_ENTRIES(8, 128, 2, 2)
   }
 
 LF_W8A16_TILE_ENTRIES(1, 16, 1)
+
+// Shape-specialized entries for Llama-3-8B (hidden 4096, intermediate
+// 14336, Q 4096, K/V 1024): one-tile (t1) or column-group (g) form, chosen
+// per (shape, profile) by lunaflux_fp8_launch_geometry; the parameters are
+// the measured best of a sweep on MI355X (waves, weight / activation ring
+// depth, LDS slots, K-slices).
+#define LF_W16_FIXED_DENSE_T1(KK, M, MT, KS, DW, DX, SLOTS)                                     \
+  __global__ __launch_bounds__(KS * 64) void lf_fp8_w8a16_dense_k##KK##_m##M(                \
+      const int32_t *counts, const uint16_t *x, const uint8_t *w, uint16_t *y, uint8_t *) {  \
+    w8a16_fixed_kernel<KK, KS, MT, 0, DW, DX, 0, 0, SLOTS>(counts, x, w, w, w, y);            \
+  }
+#define LF_W16_FIXED_GATE_UP_T1(KK, M, MT, KS, DW, DX, SLOTS)                                   \
+  __global__ __launch_bounds__(KS * 64) void lf_fp8_w8a16_gate_up_k##KK##_m##M(              \
+      const int32_t *counts, const uint16_t *x, const uint8_t *wg, const uint8_t *wu,        \
+      uint16_t *h, uint8_t *) {                                                              \
+    w8a16_fixed_kernel<KK, KS, MT, 2, DW, DX, 0, 0, SLOTS>(counts, x, wg, wu, wu, h);         \
+  }
+#define LF_W16_FIXED_QKV_T1(KK, NQ, NKV, M, MT, KS, DW, DX, SLOTS)                              \
+  __global__ __launch_bounds__(KS * 64) void lf_fp8_w8a16_qkv_k##KK##_q##NQ##_kv##NKV##_m##M( \
+      const int32_t *counts, const uint16_t *x, const uint8_t *wq, const uint8_t *wk,        \
+      const uint8_t *wv, uint16_t *y, uint8_t *) {                                           \
+    w8a16_fixed_kernel<KK, KS, MT, 1, DW, DX, NQ, NKV, SLOTS>(counts, x, wq, wk, wv, y);      \
+  }
+#define LF_W16_FIXED_DENSE_G(KK, M, MT, S, W, DW, DX)                                           \
+  __global__ __launch_bounds__(W * 64) void lf_fp8_w8a16_dense_k##KK##_m##M(                 \
+      const int32_t *counts, const uint16_t *x, const uint8_t *w, uint16_t *y, uint8_t *ws) { \
+    w8a16_fixed_group_kernel<KK, S, W, MT, 0, DW, DX>(counts, x, w, w, w, y, ws);             \
+  }
+#define LF_W16_FIXED_GATE_UP_G(KK, M, MT, S, W, DW, DX)                                         \
+  __global__ __launch_bounds__(W * 64) void lf_fp8_w8a16_gate_up_k##KK##_m##M(               \
+      const int32_t *counts, const uint16_t *x, const uint8_t *wg, const uint8_t *wu,        \
+      uint16_t *h, uint8_t *ws) {                                                            \
+    w8a16_fixed_group_kernel<KK, S, W, MT, 2, DW, DX>(counts, x, wg, wu, wu, h, ws);          \
+  }
+
+LF_W16_FIXED_DENSE_T1(4096, 16, 1, 8, 4, 2, 2)
+LF_W16_FIXED_DENSE_T1(4096, 32, 2, 8, 4, 1, 1)
+LF_W16_FIXED_DENSE_T1(14336, 16, 1, 8, 6, 2, 2)
+LF_W16_FIXED_DENSE_G(14336, 32, 2, 4, 4, 6, 2)
+LF_W16_FIXED_QKV_T1(4096, 4096, 1024, 16, 1, 8, 4, 2, 2)
+LF_W16_FIXED_QKV_T1(4096, 4096, 1024, 32, 2, 8, 4, 1, 1)
+LF_W16_FIXED_GATE_UP_T1(4096, 16, 1, 8, 2, 2, 2)
+LF_W16_FIXED_GATE_UP_G(4096, 32, 2, 2, 8, 4, 2)
 
 }  // extern "C"

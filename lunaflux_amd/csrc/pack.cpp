@@ -91,6 +91,64 @@ bool w8a16_split(int64_t n, int64_t k, int32_t max_tokens, W8a16Split *out) {
   out->split = split;
   return true;
 }
+
+// Shape-specialized W8A16 entries (w8a16.hip, "LF_W16_FIXED_*"): compiled for
+// one input width K (and, for QKV, one Q / K-V split), as AOT entry points
+// are compiled for one model shape. Two forms: one-tile (a block of `waves`
+// waves per 16-column tile, K split across its waves, no workspace) and
+// column-group (`waves` tiles per block, K cut into `split` slices across
+// blocks, partials reduced through the workspace). Shapes without an entry
+// here use the generic kernels above.
+struct W8a16Fixed {
+  int32_t entry;
+  int64_t k, nq, nkv;
+  int mt;           // 16-row tiles: the profile's max_query_tokens <= 16 mt
+  bool group;       // column-group form
+  int waves, split;
+  const char *symbol;
+};
+constexpr W8a16Fixed kW8a16Fixed[] = {
+    {LF_FP8_ENTRY_W8A16_DENSE, 4096, 0, 0, 1, false, 8, 1, "lf_fp8_w8a16_dense_k4096_m16"},
+    {LF_FP8_ENTRY_W8A16_DENSE, 4096, 0, 0, 2, false, 8, 1, "lf_fp8_w8a16_dense_k4096_m32"},
+    {LF_FP8_ENTRY_W8A16_DENSE, 14336, 0, 0, 1, false, 8, 1, "lf_fp8_w8a16_dense_k14336_m16"},
+    {LF_FP8_ENTRY_W8A16_DENSE, 14336, 0, 0, 2, true, 4, 4, "lf_fp8_w8a16_dense_k14336_m32"},
+    {LF_FP8_ENTRY_W8A16_QKV, 4096, 4096, 1024, 1, false, 8, 1,
+     "lf_fp8_w8a16_qkv_k4096_q4096_kv1024_m16"},
+    {LF_FP8_ENTRY_W8A16_QKV, 4096, 4096, 1024, 2, false, 8, 1,
+     "lf_fp8_w8a16_qkv_k4096_q4096_kv1024_m32"},
+    {LF_FP8_ENTRY_W8A16_GATE_UP, 4096, 0, 0, 1, false, 8, 1, "lf_fp8_w8a16_gate_up_k4096_m16"},
+    {LF_FP8_ENTRY_W8A16_GATE_UP, 4096, 0, 0, 2, true, 8, 2, "lf_fp8_w8a16_gate_up_k4096_m32"},
+};
+
+// The specialized entry for (entry, N, K, Q / K-V split, profile), or null.
+// nq = nkv = 0 when the split is unknown (QKV then never matches).
+const W8a16Fixed *w8a16_fixed(int32_t entry, int64_t n, int64_t k, int64_t nq, int64_t nkv,
+                              int32_t max_tokens) {
+  if (max_tokens <= 0 || max_tokens > 32 || n <= 0 || n % 16 != 0) return nullptr;
+  const int mt = max_tokens <= 16 ? 1 : 2;
+  for (const W8a16Fixed &f : kW8a16Fixed) {
+    if (f.entry != entry || f.k != k || f.mt != mt) continue;
+    if (entry == LF_FP8_ENTRY_W8A16_QKV && (f.nq != nq || f.nkv != nkv || n != nq + 2 * nkv)) {
+      continue;
+    }
+    if (f.group && (n / 16) % f.waves != 0) continue;
+    return &f;
+  }
+  return nullptr;
+}
+
+int64_t w8a16_fixed_workspace(const W8a16Fixed &f, int64_t n) {
+  if (!f.group || f.split == 1) return 256;
+  const int64_t nw = f.entry == LF_FP8_ENTRY_W8A16_GATE_UP ? 2 : 1;
+  const int64_t groups = n / 16 / f.waves;
+  return align_up(f.split * (n / 16) * nw * f.mt * 1024, 256) + align_up(groups * 4, 256);
+}
+
+void w8a16_fixed_geometry(const W8a16Fixed &f, int64_t n, int32_t *gx, int32_t *bx) {
+  const int64_t tiles = n / 16;
+  *gx = static_cast<int32_t>(f.group ? tiles / f.waves * f.split : tiles);
+  *bx = 64 * f.waves;
+}
 }  // namespace
 
 static_assert(sizeof(lf_fp8_weight_header) == LF_FP8_HEADER_BYTES, "header size");
@@ -182,8 +240,8 @@ int64_t lunaflux_fp8_act_quant_bytes(int64_t max_rows, int64_t columns) {
   return align_up(max_rows * columns, 256) + align_up(max_rows * 4, 256);
 }
 
-int64_t lunaflux_fp8_w8a16_workspace_bytes(int32_t entry, int64_t n, int64_t k,
-                                           int32_t max_tokens) {
+static int64_t w8a16_workspace(int32_t entry, int64_t n, int64_t k, int64_t nq, int64_t nkv,
+                               int32_t max_tokens) {
   if (entry != LF_FP8_ENTRY_W8A16_DENSE && entry != LF_FP8_ENTRY_W8A16_QKV &&
       entry != LF_FP8_ENTRY_W8A16_GATE_UP) {
     return -1;
@@ -193,6 +251,9 @@ int64_t lunaflux_fp8_w8a16_workspace_bytes(int32_t entry, int64_t n, int64_t k,
       !w8a16_split(n, k, max_tokens, &sp)) {
     return -1;
   }
+  if (const W8a16Fixed *f = w8a16_fixed(entry, n, k, nq, nkv, max_tokens)) {
+    return w8a16_fixed_workspace(*f, n);
+  }
   if (sp.split == 1) return 256;
   // One 1 KiB fp32 accumulator fragment per (slice, 16-column tile, weight,
   // 16-row tile), then one arrival counter per column group.
@@ -200,9 +261,20 @@ int64_t lunaflux_fp8_w8a16_workspace_bytes(int32_t entry, int64_t n, int64_t k,
   return align_up(sp.split * (n / 16) * nw * sp.mt * 1024, 256) + align_up(sp.groups * 4, 256);
 }
 
-int32_t lunaflux_fp8_launch_geometry(int32_t entry, int64_t n, int64_t k,
-                                     int32_t max_tokens, int32_t dims[7],
-                                     char symbol[LF_FP8_SYMBOL_BYTES]) {
+int64_t lunaflux_fp8_w8a16_workspace_bytes(int32_t entry, int64_t n, int64_t k,
+                                           int32_t max_tokens) {
+  return w8a16_workspace(entry, n, k, 0, 0, max_tokens);
+}
+
+int64_t lunaflux_fp8_qkv_w8a16_workspace_bytes(int64_t nq, int64_t nkv, int64_t k,
+                                               int32_t max_tokens) {
+  if (nq <= 0 || nkv <= 0 || nq > kMaxDim || nkv > kMaxDim) return -1;
+  return w8a16_workspace(LF_FP8_ENTRY_W8A16_QKV, nq + 2 * nkv, k, nq, nkv, max_tokens);
+}
+
+static int32_t launch_geometry(int32_t entry, int64_t n, int64_t k, int64_t nq, int64_t nkv,
+                               int32_t max_tokens, int32_t dims[7],
+                               char symbol[LF_FP8_SYMBOL_BYTES]) {
   if (dims == nullptr || symbol == nullptr || n <= 0 || k <= 0 ||
       max_tokens <= 0 || n > kMaxDim || k > kMaxDim || k % 128 != 0) {
     return LF_INVALID_ARGUMENT;
@@ -221,6 +293,11 @@ int32_t lunaflux_fp8_launch_geometry(int32_t entry, int64_t n, int64_t k,
     case LF_FP8_ENTRY_W8A16_GATE_UP: {
       W8a16Split sp;
       if (!w8a16_split(n, k, max_tokens, &sp)) return LF_INVALID_ARGUMENT;
+      if (const W8a16Fixed *f = w8a16_fixed(entry, n, k, nq, nkv, max_tokens)) {
+        name = f->symbol;
+        w8a16_fixed_geometry(*f, n, &gx, &bx);
+        break;
+      }
       const char *op = entry == LF_FP8_ENTRY_W8A16_DENSE ? "dense"
                        : entry == LF_FP8_ENTRY_W8A16_QKV ? "qkv"
                                                          : "gate_up";
@@ -268,6 +345,22 @@ int32_t lunaflux_fp8_launch_geometry(int32_t entry, int64_t n, int64_t k,
   std::memset(symbol, 0, LF_FP8_SYMBOL_BYTES);
   std::strncpy(symbol, name, LF_FP8_SYMBOL_BYTES - 1);
   return LF_OK;
+}
+
+int32_t lunaflux_fp8_launch_geometry(int32_t entry, int64_t n, int64_t k,
+                                     int32_t max_tokens, int32_t dims[7],
+                                     char symbol[LF_FP8_SYMBOL_BYTES]) {
+  return launch_geometry(entry, n, k, 0, 0, max_tokens, dims, symbol);
+}
+
+int32_t lunaflux_fp8_qkv_launch_geometry(int32_t entry, int64_t nq, int64_t nkv, int64_t k,
+                                         int32_t max_tokens, int32_t dims[7],
+                                         char symbol[LF_FP8_SYMBOL_BYTES]) {
+  if ((entry != LF_FP8_ENTRY_W8A16_QKV && entry != LF_FP8_ENTRY_W8A8_QKV) || nq <= 0 ||
+      nkv <= 0 || nq > kMaxDim || nkv > kMaxDim) {
+    return LF_INVALID_ARGUMENT;
+  }
+  return launch_geometry(entry, nq + 2 * nkv, k, nq, nkv, max_tokens, dims, symbol);
 }
 
 // Blocks (4 waves, 4 groups per wave per step) for a per-128-group quantizer

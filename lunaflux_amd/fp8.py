@@ -89,18 +89,29 @@ def act_quant_bytes(max_rows: int, columns: int) -> int:
     return n
 
 
-def w8a16_workspace_bytes(entry: int, n: int, k: int, max_tokens: int) -> int:
-    nbytes = _abi.lib().lunaflux_fp8_w8a16_workspace_bytes(entry, n, k, max_tokens)
+def w8a16_workspace_bytes(entry: int, n: int, k: int, max_tokens: int,
+                          qkv_split: tuple[int, int] | None = None) -> int:
+    """Split-K workspace bytes; qkv_split = (Nq, Nkv) lets a QKV operation
+    select its shape-specialized entry."""
+    if qkv_split is not None:
+        nbytes = _abi.lib().lunaflux_fp8_qkv_w8a16_workspace_bytes(*qkv_split, k, max_tokens)
+    else:
+        nbytes = _abi.lib().lunaflux_fp8_w8a16_workspace_bytes(entry, n, k, max_tokens)
     if nbytes < 0:
         raise DeviceError("w8a16_workspace_bytes", _abi.LF_INVALID_ARGUMENT)
     return nbytes
 
 
-def launch_geometry(entry: int, n: int, k: int, max_tokens: int):
+def launch_geometry(entry: int, n: int, k: int, max_tokens: int,
+                    qkv_split: tuple[int, int] | None = None):
     dims = (ctypes.c_int32 * 7)()
     symbol = ctypes.create_string_buffer(128)
-    _check("launch_geometry", _abi.lib().lunaflux_fp8_launch_geometry(
-        entry, n, k, max_tokens, dims, symbol))
+    if qkv_split is not None:
+        _check("launch_geometry", _abi.lib().lunaflux_fp8_qkv_launch_geometry(
+            entry, *qkv_split, k, max_tokens, dims, symbol))
+    else:
+        _check("launch_geometry", _abi.lib().lunaflux_fp8_launch_geometry(
+            entry, n, k, max_tokens, dims, symbol))
     return (KernelLaunchDimensions.new(tuple(dims[0:3]), tuple(dims[3:6]), dims[6]),
             symbol.value.decode("ascii"))
 
@@ -193,17 +204,20 @@ class ProjectionRuntime:
                            query_tokens, 0], np.int32)
         return self.context.upload(counts)
 
-    def _step(self, entry: int, n: int, k: int, max_tokens: int, operands) -> LaunchStep:
-        dims, symbol = launch_geometry(entry, n, k, max_tokens)
+    def _step(self, entry: int, n: int, k: int, max_tokens: int, operands,
+              qkv_split=None) -> LaunchStep:
+        dims, symbol = launch_geometry(entry, n, k, max_tokens, qkv_split)
         return LaunchStep(self.function(symbol), dims, KernelArguments(operands), symbol)
 
-    def _w8a16(self, entry: int, n: int, k: int, max_tokens: int, operands) -> BoundOperation:
+    def _w8a16(self, entry: int, n: int, k: int, max_tokens: int, operands,
+               qkv_split=None) -> BoundOperation:
         """A W8A16 launch with its split-K workspace (zero-filled once here;
         the kernels leave its arrival counters at zero after every launch)."""
-        nbytes = w8a16_workspace_bytes(entry, n, k, max_tokens)
+        nbytes = w8a16_workspace_bytes(entry, n, k, max_tokens, qkv_split)
         ws = self.context.allocate(nbytes)
         ws.copy_from_host(np.zeros(nbytes, np.uint8))
-        step = self._step(entry, n, k, max_tokens, operands + [_region(ws, alignment=256)])
+        step = self._step(entry, n, k, max_tokens, operands + [_region(ws, alignment=256)],
+                          qkv_split)
         return BoundOperation([step], workspace=ws)
 
     # -- binding plan operations to launch steps ---------------------------
@@ -235,7 +249,8 @@ class ProjectionRuntime:
         c = _region(counts, COUNTS_BYTES, alignment=4)
         if family == "w8a16":
             return self._w8a16(_abi.ENTRY_W8A16_QKV, n, wq.columns, max_tokens,
-                               [c, x, wq.region, wk.region, wv.region, y])
+                               [c, x, wq.region, wk.region, wv.region, y],
+                               qkv_split=(wq.rows, wk.rows))
         ws = self.context.allocate(act_quant_bytes(max_tokens, wq.columns))
         xq = _region(ws, alignment=256)
         return BoundOperation([

@@ -41,7 +41,10 @@ def test_code_object_has_every_entry_point():
                    "lf_moe_gate_up", "lf_moe_gate_up_b128", "lf_moe_quant_hidden", "lf_moe_down",
                    "lf_moe_down_b128", "lf_moe_combine"] + [f"lf_fp8_w8a16_{op}_m{m}" for op in ("dense", "qkv", "gate_up")
                                              for m in (16, 32, 64, 128)] + [
-                   f"lf_fp8_w8a16_{op}_m16_t1" for op in ("dense", "qkv", "gate_up")]:
+                   f"lf_fp8_w8a16_{op}_m16_t1" for op in ("dense", "qkv", "gate_up")] + [
+                   f"lf_fp8_w8a16_dense_k{k}_m{m}" for k in (4096, 14336) for m in (16, 32)] + [
+                   f"lf_fp8_w8a16_gate_up_k4096_m{m}" for m in (16, 32)] + [
+                   f"lf_fp8_w8a16_qkv_k4096_q4096_kv1024_m{m}" for m in (16, 32)]:
         assert symbol.encode() + b"\0" in image, symbol
 
 
@@ -99,23 +102,45 @@ def test_region_size_validation():
 
 
 def test_launch_geometry():
-    # W8A16, max rows <= 16: one 16-column tile per 8-wave block, K split
-    # across its waves. Larger profiles: 4 column tiles per 4-wave block, K
-    # cut into about 512 / groups slices across blocks.
-    dims, sym = fp8.launch_geometry(_abi.ENTRY_W8A16_DENSE, 4096, 14336, 32)
+    # W8A16 generic forms, max rows <= 16: one 16-column tile per 8-wave
+    # block, K split across its waves. Larger profiles: 4 column tiles per
+    # 4-wave block, K cut into about 512 / groups slices across blocks.
+    dims, sym = fp8.launch_geometry(_abi.ENTRY_W8A16_DENSE, 4096, 2048, 32)
     assert sym == "lf_fp8_w8a16_dense_m32" and dims.grid == (64 * 8, 1, 1) and dims.block == (256, 1, 1)
     dims, sym = fp8.launch_geometry(_abi.ENTRY_W8A16_QKV, 6144, 4096, 1)
     assert sym == "lf_fp8_w8a16_qkv_m16_t1" and dims.grid == (384, 1, 1) and dims.block == (512, 1, 1)
-    dims, sym = fp8.launch_geometry(_abi.ENTRY_W8A16_GATE_UP, 14336, 4096, 32)
+    dims, sym = fp8.launch_geometry(_abi.ENTRY_W8A16_GATE_UP, 14336, 2048, 32)
     assert sym == "lf_fp8_w8a16_gate_up_m32" and dims.grid == (224 * 2, 1, 1)
     dims, sym = fp8.launch_geometry(_abi.ENTRY_W8A16_QKV, 6144, 4096, 128)
     assert sym == "lf_fp8_w8a16_qkv_m128" and dims.grid == (96 * 5, 1, 1)
     # split-K workspace: S x (N / 16) x NW x MT 1 KiB fragments + one counter
     # per column group; 256 bytes (unused) without a split
-    assert fp8.w8a16_workspace_bytes(_abi.ENTRY_W8A16_DENSE, 4096, 14336, 32) == 8 * 256 * 2 * 1024 + 256
+    assert fp8.w8a16_workspace_bytes(_abi.ENTRY_W8A16_DENSE, 4096, 2048, 32) == 8 * 256 * 2 * 1024 + 256
     assert fp8.w8a16_workspace_bytes(_abi.ENTRY_W8A16_QKV, 6144, 4096, 1) == 256
-    assert fp8.w8a16_workspace_bytes(_abi.ENTRY_W8A16_GATE_UP, 14336, 4096, 32) == 2 * 896 * 2 * 2 * 1024 + 1024
+    assert fp8.w8a16_workspace_bytes(_abi.ENTRY_W8A16_GATE_UP, 14336, 2048, 32) == 2 * 896 * 2 * 2 * 1024 + 1024
     assert fp8.w8a16_workspace_bytes(_abi.ENTRY_W8A16_QKV, 6144, 4096, 128) == 5 * 384 * 8 * 1024 + 512
+    # Shape-specialized (Llama-3-8B) entries for profiles of <= 32 rows.
+    dims, sym = fp8.launch_geometry(_abi.ENTRY_W8A16_DENSE, 4096, 14336, 32)
+    assert sym == "lf_fp8_w8a16_dense_k14336_m32" and dims.grid == (64 * 4, 1, 1)
+    assert dims.block == (256, 1, 1)
+    assert fp8.w8a16_workspace_bytes(_abi.ENTRY_W8A16_DENSE, 4096, 14336, 32) == 4 * 256 * 2 * 1024 + 256
+    dims, sym = fp8.launch_geometry(_abi.ENTRY_W8A16_DENSE, 4096, 4096, 8)
+    assert sym == "lf_fp8_w8a16_dense_k4096_m16" and dims.grid == (256, 1, 1) and dims.block == (512, 1, 1)
+    dims, sym = fp8.launch_geometry(_abi.ENTRY_W8A16_GATE_UP, 14336, 4096, 32)
+    assert sym == "lf_fp8_w8a16_gate_up_k4096_m32" and dims.grid == (112 * 2, 1, 1)
+    assert dims.block == (512, 1, 1)
+    assert fp8.w8a16_workspace_bytes(_abi.ENTRY_W8A16_GATE_UP, 14336, 4096, 32) == 2 * 896 * 2 * 2 * 1024 + 512
+    dims, sym = fp8.launch_geometry(_abi.ENTRY_W8A16_QKV, 6144, 4096, 32, qkv_split=(4096, 1024))
+    assert sym == "lf_fp8_w8a16_qkv_k4096_q4096_kv1024_m32" and dims.grid == (384, 1, 1)
+    assert fp8.w8a16_workspace_bytes(_abi.ENTRY_W8A16_QKV, 6144, 4096, 32, (4096, 1024)) == 256
+    # a QKV split without an entry, or a profile above 32 rows: generic
+    dims, sym = fp8.launch_geometry(_abi.ENTRY_W8A16_QKV, 6144, 4096, 32, qkv_split=(2048, 2048))
+    assert sym == "lf_fp8_w8a16_qkv_m32"
+    dims, sym = fp8.launch_geometry(_abi.ENTRY_W8A16_DENSE, 4096, 4096, 64)
+    assert sym == "lf_fp8_w8a16_dense_m64"
+    # the W8A8 QKV split variant picks the same entry as the plain call
+    assert (fp8.launch_geometry(_abi.ENTRY_W8A8_QKV, 6144, 4096, 2048, qkv_split=(4096, 1024))[1]
+            == fp8.launch_geometry(_abi.ENTRY_W8A8_QKV, 6144, 4096, 2048)[1])
     with pytest.raises(fp8.DeviceError):
         fp8.w8a16_workspace_bytes(_abi.ENTRY_W8A8_DENSE, 4096, 4096, 16)
     # W8A8: 256 x 256 tiles (1-D grid, 512 threads) once there is a tile per

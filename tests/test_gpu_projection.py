@@ -277,3 +277,94 @@ def test_llama3_8b_shapes_sampled(rt, op, m, family):
         parity(y[rows][:, cols], ref, label=label)
     else:
         check_projection(y[rows][:, cols], xr, wr, label)
+
+
+@pytest.mark.parametrize("op,m,max_tokens", [
+    ("o", 1, 16), ("o", 16, 16), ("o", 17, 32), ("o", 32, 32), ("o", 0, 32),
+    ("down", 5, 16), ("down", 20, 32), ("down", 32, 32),
+    ("qkv", 1, 16), ("qkv", 13, 16), ("qkv", 32, 32),
+    ("gate_up", 8, 16), ("gate_up", 25, 32), ("gate_up", 32, 32),
+])
+def test_w8a16_specialized_entries(rt, op, m, max_tokens):
+    """Every shape-specialized W8A16 entry (Llama-3-8B widths, profiles of
+    <= 16 and <= 32 rows) against the oracle on a column sample, with ragged
+    live rows and M = 0; the column-group forms (down, gate_up at 32 rows)
+    run three launches on one workspace, which must be bit-identical."""
+    from lunaflux_amd import _abi, fp8
+    from lunaflux_amd.fp8 import _region
+    rng = np.random.default_rng(8100 + 97 * m + max_tokens + len(op))
+    k = 14336 if op == "down" else 4096
+    x = synth.activations(rng, max(m, 1), k)[:m]
+    xa = rt.context.upload(np.concatenate([x, np.zeros((max_tokens - m, k), np.uint16)]))
+    counts = rt.step_counts(m)
+    # (M = 0: the oracle rejects an empty activation, so one row stands in)
+    xr = x_ref(x if m else synth.activations(rng, 1, k), "w8a16")
+    if op == "qkv":
+        ws = [make_weight(rt, rng, n, k) for n in (4096, 1024, 1024)]
+        n = 6144
+        sym = fp8.launch_geometry(_abi.ENTRY_W8A16_QKV, n, k, max_tokens, qkv_split=(4096, 1024))[1]
+        ya = rt.context.allocate(max_tokens * n * 2)
+        bound = rt.bind_qkv("w8a16", counts, _region(xa, alignment=256), *(w for _, _, w in ws),
+                            _region(ya, alignment=256), max_tokens)
+        cols = np.sort(rng.choice(n, 512, replace=False))
+        wq = np.concatenate([q for q, _, _ in ws])[cols]
+        wsc = np.concatenate([s for _, s, _ in ws])[cols]
+        ref = o.dense_projection(xr, deq(wq, wsc))
+        extra = dict(k=k, s_abs=abs_sum(xr, deq(wq, wsc)))
+    elif op == "gate_up":
+        n = 14336
+        (qg, sg, wg), (qu, su, wu) = make_weight(rt, rng, n, k), make_weight(rt, rng, n, k)
+        sym = fp8.launch_geometry(_abi.ENTRY_W8A16_GATE_UP, n, k, max_tokens)[1]
+        ya = rt.context.allocate(max_tokens * n * 2)
+        bound = rt.bind_gate_up("w8a16", counts, _region(xa, alignment=256), wg, wu,
+                                _region(ya, alignment=256), max_tokens)
+        cols = np.sort(rng.choice(n, 256, replace=False))
+        ref = o.silu_mul_array(o.dense_projection(xr, deq(qg[cols], sg[cols])),
+                               o.dense_projection(xr, deq(qu[cols], su[cols])))
+        extra = {}
+    else:
+        n = 4096
+        q, s, w = make_weight(rt, rng, n, k)
+        sym = fp8.launch_geometry(_abi.ENTRY_W8A16_DENSE, n, k, max_tokens)[1]
+        ya = rt.context.allocate(max_tokens * n * 2)
+        bound = rt.bind_dense("w8a16", counts, _region(xa, alignment=256), w,
+                              _region(ya, alignment=256), max_tokens)
+        cols = np.sort(rng.choice(n, 384, replace=False))
+        ref = o.dense_projection(xr, deq(q[cols], s[cols]))
+        extra = dict(k=k, s_abs=abs_sum(xr, deq(q[cols], s[cols])))
+    assert f"_k{k}_" in sym and sym.endswith(f"_m{16 if max_tokens <= 16 else 32}"), sym
+    sentinel = np.full(max_tokens * n, 0x7FC1, np.uint16)  # a NaN no kernel writes
+    ya.copy_from_host(sentinel)
+    outs = []
+    for _ in range(3):
+        bound.launch(rt.stream, synchronous=True)
+        outs.append(ya.read(np.uint16, (max_tokens, n)))
+    for y in outs:
+        # rows past M stay untouched
+        assert np.all(y[m:] == 0x7FC1), f"{sym}: rows past M written"
+        if m:
+            parity(y[:m][:, cols], ref, label=f"{sym} m={m}", **extra)
+    assert all(np.array_equal(outs[0], y) for y in outs[1:]), f"{sym}: launches differ"
+
+
+def test_w8a16_specialized_entry_rejects_other_shape(rt):
+    """A specialized entry checks the header against its compiled shape: a
+    K = 8192 weight region launched on the K = 4096 dense entry (its reads
+    stay inside the larger region) leaves the output untouched."""
+    from lunaflux_amd.device import KernelArguments
+    from lunaflux_amd.fp8 import _region, COUNTS_BYTES
+    rng = np.random.default_rng(8200)
+    m, k, n = 4, 4096, 4096
+    _, _, w = make_weight(rt, rng, n, 2 * k)
+    x = synth.activations(rng, 16, k)
+    xa = rt.context.upload(x)
+    ya = rt.context.upload(np.full(16 * n, 0x7FC1, np.uint16))
+    ws = rt.context.allocate(256)
+    counts = rt.step_counts(m)
+    from lunaflux_amd import _abi, fp8
+    dims, sym = fp8.launch_geometry(_abi.ENTRY_W8A16_DENSE, n, k, 16)
+    assert sym == "lf_fp8_w8a16_dense_k4096_m16"
+    args = KernelArguments([_region(counts, COUNTS_BYTES, alignment=4), _region(xa, alignment=256),
+                            w.region, _region(ya, alignment=256), _region(ws, alignment=256)])
+    rt.function(sym).launch_synchronous(dims, args, rt.stream)
+    assert np.all(ya.read(np.uint16, (16 * n,)) == 0x7FC1)
