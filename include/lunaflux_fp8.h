@@ -187,9 +187,11 @@ int64_t lunaflux_fp8_qkv_w8a16_workspace_bytes(int64_t nq, int64_t nkv, int64_t 
  *  lf_moe_sort_count    (counts, desc, ws)
  *  lf_moe_sort          (counts, desc, ws)
  *  lf_moe_quant_tokens  (counts, desc, x bf16 [T, H], ws)
- *  lf_moe_gate_up[_b128](counts, desc, wg, wu, ws)
+ *  lf_moe_gate_up[_b128|_t256](counts, desc, wg, wu, ws)
  *  lf_moe_quant_hidden  (counts, desc, ws)
- *  lf_moe_down[_b128]   (counts, desc, wd, ws)
+ *  lf_moe_down[_b128|_t256]   (counts, desc, wd, ws)
+ * (_t256: the per-channel GEMMs on 256 x 256 tiles, chosen by the launch
+ * geometry for profiles that average >= 256 routed rows per expert.)
  *  lf_moe_combine       (counts, desc, ws, out bf16 [T, H])
  * Routing: the k largest logits per token (ties to the lower expert id);
  * weights are a softmax over the k picked logits (route_mode 0, Mixtral) or
@@ -234,7 +236,8 @@ int64_t lunaflux_fp8_moe_workspace_bytes(const lf_fp8_moe_desc *desc,
 /* Byte offsets of the workspace arrays for `tokens` live tokens, in order:
  * top-k ids (int32 [T*k]), top-k weights (fp32 [T*k]), sorted assignments
  * (int32 [T*k]), position of each assignment (int32 [T*k]), expert row
- * offsets (int32 [E+1]), expert 128-row tile offsets (int32 [E+1]), e4m3
+ * offsets (int32 [E+1]), expert 128-row tile offsets (int32 [E+1]) followed
+ * by the 256-row tile offsets (int32 [E+1]), e4m3
  * tokens [T, H], token scales, h bf16 [T*k, I], e4m3 h, h scales, y fp32
  * [T*k, H], end. */
 int32_t lunaflux_fp8_moe_workspace_layout(const lf_fp8_moe_desc *desc,

@@ -21,6 +21,7 @@
 //                         -> bf16 [T, H]
 #include "w8a8_core.h"
 #include "w8a8_v3.h"
+#include "w8a8_v4.h"
 
 namespace {
 
@@ -47,7 +48,8 @@ struct MoeLayout {
     sorted = o;   o = al256(o + A * 4);
     pos = o;      o = al256(o + A * 4);
     offsets = o;  o = al256(o + (d.experts + 1) * 4);
-    tiles = o;    o = al256(o + (d.experts + 1) * 4);
+    // 128-row tile prefix [E + 1], then the 256-row tile prefix [E + 1]
+    tiles = o;    o = al256(o + 2 * (d.experts + 1) * 4);
     xq = o;       o = al256(o + static_cast<uint64_t>(T) * H);
     xs = o;       o = al256(o + static_cast<uint64_t>(T) * gx * 4);
     h = o;        o = al256(o + A * I * 2);
@@ -199,6 +201,7 @@ LF_DEVICE void sort_assignments(const int32_t *counts, const MoeDesc &d, uint8_t
       for (int e = threadIdx.x; e <= E; e += kSortThreads) {
         at<int32_t>(ws, L.offsets)[e] = 0;
         at<int32_t>(ws, L.tiles)[e] = 0;
+        at<int32_t>(ws, L.tiles)[E + 1 + e] = 0;
       }
     }
     return;
@@ -225,21 +228,25 @@ LF_DEVICE void sort_assignments(const int32_t *counts, const MoeDesc &d, uint8_t
   }
   __syncthreads();
   if (tid == 0) {
-    // Exclusive scans: first row and first 128-row tile of each expert.
-    int off = 0, tl = 0;
+    // Exclusive scans: first row, first 128-row tile and first 256-row tile
+    // of each expert.
+    int off = 0, tl = 0, tl2 = 0;
     for (int e = 0; e < E; ++e) {
       const int n = wcnt[0][e];
       if (c == 0) {
         offsets[e] = off;
         tiles[e] = tl;
+        tiles[E + 1 + e] = tl2;
       }
       base[e] += off;
       off += n;
       tl += (n + w8a8::kBM - 1) / w8a8::kBM;
+      tl2 += (n + 2 * w8a8::kBM - 1) / (2 * w8a8::kBM);
     }
     if (c == 0) {
       offsets[E] = off;
       tiles[E] = tl;
+      tiles[E + 1 + E] = tl2;
     }
   }
   __syncthreads();
@@ -466,6 +473,118 @@ __device__ void grouped_gemm(const int32_t *counts, const MoeDesc &d, const uint
   }
 }
 
+// Grouped GEMM on 256 x 256 tiles (the half-step main loop of w8a8_v4.h,
+// 8 waves, one block per CU) for the per-channel form. A weight strip (256
+// columns x K) is streamed once per 256 routed rows of its expert instead of
+// once per 128: with 128-row tiles, the tiles sharing a strip drift apart
+// and miss in L2 (measured: the Mixtral gate/up GEMM fetched twice its
+// weight bytes from HBM). Row tiles are the 256-row tiles of all experts
+// (the second prefix the sort writes); the 1-D tile order is column-major as
+// above. STAGE 0: 128 h-columns per block (each wave column's fragments are
+// its gate tiles, then the up tiles of the same columns); STAGE 1: 256
+// columns per block.
+using GemmTile256 = w8a8v4::Tile<256, 256, 4, 4, 2>;
+
+template <int STAGE>
+__device__ void grouped_gemm_t256(const int32_t *counts, const MoeDesc &d, const uint8_t *w0,
+                                  const uint8_t *w1, uint8_t *ws) {
+  using T = GemmTile256;
+  constexpr int BM = T::kBM;
+  __shared__ __attribute__((aligned(1024))) uint8_t smem[T::kSmem];
+  const int Tn = live_rows(counts, 1 << 30);
+  if (Tn == 0) return;
+  const MoeLayout L(d, Tn);
+  const int E = d.experts;
+  const int32_t *tiles = at<int32_t>(ws, L.tiles) + (E + 1);
+  const WeightHeader &h0 = header_of(w0);
+  const int K = static_cast<int>(h0.columns);
+  const int KT = K >> 7;
+  const int N = static_cast<int>(h0.rows);
+  const int gx = STAGE == 0 ? N / (T::kBN / 2) : N / T::kBN;
+  int bx, by;
+  if (!w8a8v3::tile_of_block(gx, tiles[E], tiles[E], bx, by)) return;
+  const int e = expert_of_tile(tiles, E, by);
+  const int32_t *offsets = at<int32_t>(ws, L.offsets);
+  const int p0 = offsets[e] + (by - tiles[e]) * BM;
+  const int pend = offsets[e + 1];
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int wm = wave / T::kWgn, wn = wave % T::kWgn;
+  const int32_t *sorted = at<int32_t>(ws, L.sorted);
+  auto src_row = [&](int p) { return STAGE == 0 ? sorted[p] / d.top_k : p; };
+
+  auto slot = [&](int s, const uint8_t *&region, int &t, int &ocol) {
+    if (STAGE == 0) {
+      const int sw = s / (2 * T::kFN), f = s % (2 * T::kFN);
+      const bool up = f >= T::kFN;
+      ocol = bx * (T::kBN / 2) + sw * (T::kWaveN / 2) + 16 * (up ? f - T::kFN : f);
+      region = up ? w1 : w0;
+    } else {
+      ocol = bx * T::kBN + 16 * s;
+      region = w0;
+    }
+    t = ocol >> 4;
+  };
+
+  const uint8_t *abase = at<uint8_t>(ws, STAGE == 0 ? L.xq : L.hq);
+  const float *ascales = at<float>(ws, STAGE == 0 ? L.xs : L.hs);
+  w8a8v4::Plan<T> plan;
+#pragma unroll
+  for (int q = 0; q < T::kAIns; ++q) {
+    const int tr = w8a8v4::a_load_row<T>(wave, q, lane);
+    const int p = p0 + tr < pend ? p0 + tr : p0;  // dead rows re-read the first row
+    plan.a[q] = abase + static_cast<uint64_t>(src_row(p)) * K + w8a8v4::a_load_slot(tr, lane) * 32;
+  }
+#pragma unroll
+  for (int q = 0; q < T::kBIns; ++q) {
+    const uint8_t *region;
+    int t, ocol;
+    slot(w8a8v4::b_load_tile<T>(wave, q), region, t, ocol);
+    plan.b[q] = expert_tiles(region, e) + static_cast<uint64_t>(t) * KT * kTileBytes + lane * 16;
+  }
+  w8a8v4::f32x16 acc[T::kFM][T::kFN];
+  // 32-row fragments of this wave with a live row (an expert's last tile is
+  // usually partial, and small experts fill a few rows of one tile).
+  const int live_rows_wave = pend - (p0 + wm * T::kWaveM);
+  const int live_fm = live_rows_wave <= 0 ? 0 : live_rows_wave >= T::kWaveM ? T::kFM
+                                                                           : (live_rows_wave + 31) / 32;
+  w8a8v4::mainloop<T, true>(plan, KT, smem, acc, live_fm);
+
+  const int c = lane & 31;
+  const float *wsc[T::kFN];
+  int ocol[T::kFN];
+#pragma unroll
+  for (int j = 0; j < T::kFN; ++j) {
+    const uint8_t *region;
+    int t;
+    slot((wn * T::kWaveN) / 16 + 2 * j + (c >> 4), region, t, ocol[j]);
+    ocol[j] += c & 15;
+    wsc[j] = expert_scales(region, e) + t * 16 + (c & 15);
+  }
+#pragma unroll
+  for (int i = 0; i < T::kFM; ++i) {
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+      const int pp = p0 + wm * T::kWaveM + w8a8v4::acc_row<T>(i, lane, r);
+      if (pp >= pend) continue;
+      const float sa = ascales[src_row(pp)];
+      if (STAGE == 0) {
+        uint16_t *hrow = at<uint16_t>(ws, L.h) + static_cast<uint64_t>(pp) * N;
+#pragma unroll
+        for (int j = 0; j < T::kFN / 2; ++j) {
+          const float gv = acc[i][j][r] * sa * *wsc[j];
+          const float uv = acc[i][j + T::kFN / 2][r] * sa * *wsc[j + T::kFN / 2];
+          hrow[ocol[j]] = static_cast<uint16_t>(f32_to_bf16(silu_mul(gv, uv)));
+        }
+      } else {
+        float *yrow = at<float>(ws, L.y) + static_cast<uint64_t>(pp) * N;
+#pragma unroll
+        for (int j = 0; j < T::kFN; ++j) yrow[ocol[j]] = acc[i][j][r] * sa * *wsc[j];
+      }
+    }
+  }
+}
+
 // --- combine -------------------------------------------------------------------
 LF_DEVICE void combine(const int32_t *counts, const MoeDesc &d, uint8_t *ws, uint16_t *out) {
   const int T = live_rows(counts, 1 << 30);
@@ -556,6 +675,25 @@ __global__ __launch_bounds__(256) void lf_moe_down(const int32_t *counts, const 
   const MoeDesc &d = desc_of(desc);
   if (!desc_ok(d) || d.group != 0 || header_of(wd).magic != kWeightMagic) return;
   grouped_gemm<1, false>(counts, d, wd, wd, ws);
+}
+
+// The same on 256 x 256 tiles (per-channel form, profiles with >= 256
+// routed rows per expert on average).
+__global__ __launch_bounds__(512) void lf_moe_gate_up_t256(const int32_t *counts,
+                                                           const int32_t *desc,
+                                                           const uint8_t *wg, const uint8_t *wu,
+                                                           uint8_t *ws) {
+  const MoeDesc &d = desc_of(desc);
+  if (!desc_ok(d) || d.group != 0 || header_of(wg).magic != kWeightMagic) return;
+  grouped_gemm_t256<0>(counts, d, wg, wu, ws);
+}
+
+__global__ __launch_bounds__(512) void lf_moe_down_t256(const int32_t *counts,
+                                                        const int32_t *desc, const uint8_t *wd,
+                                                        uint8_t *ws) {
+  const MoeDesc &d = desc_of(desc);
+  if (!desc_ok(d) || d.group != 0 || header_of(wd).magic != kWeightMagic) return;
+  grouped_gemm_t256<1>(counts, d, wd, wd, ws);
 }
 
 // ... and 128 x 128 block weight scales with per-token-per-128-column

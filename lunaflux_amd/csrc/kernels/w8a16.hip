@@ -516,7 +516,7 @@ __device__ void w8a16_tile_kernel(const int32_t *counts, const uint16_t *x, cons
 // serializes the ring.) The KS partial tiles are summed in LDS in wave order.
 // ---------------------------------------------------------------------------
 template <int K, int KS, int MT, int MODE, int DW, int DX, int NQ = 0, int NKV = 0, int SLOTS = 2>
-__device__ void w8a16_fixed_kernel(const int32_t *counts, const uint16_t *x, const uint8_t *w0,
+__device__ __forceinline__ void w8a16_fixed_kernel(const int32_t *counts, const uint16_t *x, const uint8_t *w0,
                                    const uint8_t *w1, const uint8_t *w2, uint16_t *y) {
   constexpr int NW = MODE == 2 ? 2 : 1;
   constexpr int KT = K / 128;
@@ -695,7 +695,7 @@ __device__ void w8a16_fixed_kernel(const int32_t *counts, const uint16_t *x, con
 // writes (no memory fence), so the weight ring stays in flight across it.
 // ---------------------------------------------------------------------------
 template <int K, int S, int WAVES, int MT, int MODE, int DW, int DX, int NQ = 0, int NKV = 0>
-__device__ void w8a16_fixed_group_kernel(const int32_t *counts, const uint16_t *x,
+__device__ __forceinline__ void w8a16_fixed_group_kernel(const int32_t *counts, const uint16_t *x,
                                          const uint8_t *w0, const uint8_t *w1, const uint8_t *w2,
                                          uint16_t *y, uint8_t *ws) {
   constexpr int NW = MODE == 2 ? 2 : 1;
@@ -705,8 +705,10 @@ __device__ void w8a16_fixed_group_kernel(const int32_t *counts, const uint16_t *
   constexpr int EW = DW < NKT ? DW : NKT;
   constexpr int EX = DX < EW ? DX : EW;
   constexpr int XI = 4 * MT;
-  static_assert(XI % WAVES == 0, "activation loads split evenly over the waves");
-  constexpr int XPW = XI / WAVES;
+  static_assert(XI % WAVES == 0 || WAVES % XI == 0, "activation loads split evenly");
+  // With more waves than loads, waves w and w + XI load (and write) the same
+  // rows: identical values, so the duplicate LDS writes are benign.
+  constexpr int XPW = XI >= WAVES ? XI / WAVES : 1;
   static_assert(MODE != 1 || (NQ % 16 == 0 && NKV % 16 == 0 && NQ > 0 && NKV > 0), "qkv widths");
   constexpr int kSlot = 16 * MT * 16;  // 16-byte chunks per slot
   __shared__ __attribute__((aligned(16))) u32x4 xs[2 * kSlot];
@@ -761,7 +763,7 @@ __device__ void w8a16_fixed_group_kernel(const int32_t *counts, const uint16_t *
   int xdst[XPW];
 #pragma unroll
   for (int j = 0; j < XPW; ++j) {
-    const int q = wave * XPW + j;
+    const int q = (wave * XPW + j) % XI;
     const int row = 4 * q + (lane >> 4);
     const int src = row < M ? row : (M > 0 ? M - 1 : 0);
     xsrc[j] = x + static_cast<uint64_t>(src) * K + kt0 * 128 + (lane & 15) * 8;

@@ -85,9 +85,16 @@ struct Plan {
 // ordering the loop needs is enforced with explicit counter waits.
 LF_DEVICE void block_barrier() { asm volatile("s_barrier" ::: "memory"); }
 
-template <class T>
-__device__ void mainloop(const Plan<T> &plan, int KT, uint8_t *smem,
-                         f32x16 (&acc)[T::kFM][T::kFN]) {
+// SKIP: live_fm is how many of this wave's kFM 32-row fragments hold a live
+// row (wave-uniform); the MFMAs of the others are skipped (their
+// accumulators stay zero and are never stored), which frees the matrix pipe
+// of a SIMD for its other wave when a tile is partly past the last row. The
+// branches cost full tiles a few percent (measured on the dense prefill
+// GEMMs, whose only partial tile is the last row tile), so only the grouped
+// GEMMs, where partial tiles are common, use this form.
+template <class T, bool SKIP = false>
+__device__ __forceinline__ void mainloop(const Plan<T> &plan, int KT, uint8_t *smem,
+                         f32x16 (&acc)[T::kFM][T::kFN], int live_fm = T::kFM) {
   constexpr int NS = T::kStages;
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int wm = wave / T::kWgn, wn = wave % T::kWgn;
@@ -143,13 +150,17 @@ __device__ void mainloop(const Plan<T> &plan, int KT, uint8_t *smem,
   auto stage_ptr = [&](int s) -> const uint8_t * { return smem + (s % NS) * T::kStage; };
 
   w8a8::Frag8 outer[kOuter];
+  const int live = __builtin_amdgcn_readfirstlane(live_fm);
   auto mfma_group = [&](const w8a8::Frag8(&cur)[kInner], int o) {
 #pragma unroll
     for (int n = 0; n < kInner; ++n) {
-      f32x16 &a = kOuterN ? acc[n][o] : acc[o][n];
-      a = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(
-          kOuterN ? cur[n].v : outer[o].v, kOuterN ? outer[o].v : cur[n].v, a, 0, 0, 0, 127, 0,
-          127);
+      // row fragment of this product: n (inner = A) or o (outer = A)
+      if (!SKIP || (kOuterN ? n : o) < live) {
+        f32x16 &a = kOuterN ? acc[n][o] : acc[o][n];
+        a = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(
+            kOuterN ? cur[n].v : outer[o].v, kOuterN ? outer[o].v : cur[n].v, a, 0, 0, 0, 127, 0,
+            127);
+      }
     }
   };
   // One half-step: compute stage s from outer / cur while stage s + 1's

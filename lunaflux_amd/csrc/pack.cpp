@@ -408,7 +408,7 @@ int32_t lunaflux_fp8_moe_workspace_layout(const lf_fp8_moe_desc *d, int32_t toke
       A * 4,                  // sorted assignments
       A * 4,                  // position of each assignment
       (d->experts + 1) * 4,   // expert row offsets
-      (d->experts + 1) * 4,   // expert tile offsets
+      2 * (d->experts + 1) * 4,  // expert 128-row, then 256-row tile offsets
       T * H,                  // quantized tokens
       T * gx * 4,             // token scales
       A * I * 2,              // h (bf16)
@@ -446,6 +446,12 @@ int32_t lunaflux_fp8_moe_launch_geometry(int32_t entry, const lf_fp8_moe_desc *d
   // most one partial tile.
   const int64_t tiles = A / 128 + d->experts;
   const bool b128 = d->group == 128;
+  // Per-channel profiles averaging >= 256 routed rows per expert run the
+  // grouped GEMMs on 256 x 256 tiles (8 waves; each weight strip streamed
+  // once per 256 rows), smaller ones on 128 x 128 tiles.
+  const bool t256 = !b128 && A >= 256 * static_cast<int64_t>(d->experts) &&
+                    d->inter % 128 == 0 && d->hidden % 256 == 0;
+  const int64_t tiles256 = A / 256 + d->experts;
   int64_t gx = 1, gy = 1;
   int32_t bx = 256;
   const char *name = nullptr;
@@ -463,6 +469,12 @@ int32_t lunaflux_fp8_moe_launch_geometry(int32_t entry, const lf_fp8_moe_desc *d
     case LF_FP8_MOE_GATE_UP:
       // 1-D grid over (64 h-column block, 128-row tile); blocks past the
       // live tile count return.
+      if (t256) {
+        name = "lf_moe_gate_up_t256";
+        gx = d->inter / 128 * tiles256;
+        bx = 512;
+        break;
+      }
       name = b128 ? "lf_moe_gate_up_b128" : "lf_moe_gate_up";
       gx = d->inter / 64 * tiles;
       break;
@@ -471,6 +483,12 @@ int32_t lunaflux_fp8_moe_launch_geometry(int32_t entry, const lf_fp8_moe_desc *d
       gx = b128 ? group_quant_blocks(A * (d->inter / 128)) : (A + 3) / 4;
       break;
     case LF_FP8_MOE_DOWN:
+      if (t256) {
+        name = "lf_moe_down_t256";
+        gx = d->hidden / 256 * tiles256;
+        bx = 512;
+        break;
+      }
       name = b128 ? "lf_moe_down_b128" : "lf_moe_down";
       gx = d->hidden / 128 * tiles;
       break;

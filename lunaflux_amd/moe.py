@@ -111,7 +111,7 @@ def moe_expert_mlp(rt: ProjectionRuntime, x: np.ndarray, logits: np.ndarray, wg:
     """x bf16 bits [T, H], logits fp32 [T, E] -> out bf16 bits [T, H]. With
     return_workspace, also returns the routing intermediates read back from
     the device (top-k ids and weights, sorted assignments, positions, expert
-    row and tile offsets)."""
+    row offsets and 128- and 256-row tile offsets)."""
     x = np.ascontiguousarray(x, np.uint16)
     logits = np.ascontiguousarray(logits, np.float32)
     t, hdim = x.shape
@@ -147,6 +147,7 @@ def moe_expert_mlp(rt: ProjectionRuntime, x: np.ndarray, logits: np.ndarray, wg:
         pos=ws.read(np.int32, (a,), lay["pos"]),
         offsets=ws.read(np.int32, (e + 1,), lay["offsets"]),
         tiles=ws.read(np.int32, (e + 1,), lay["tiles"]),
+        tiles256=ws.read(np.int32, (e + 1,), lay["tiles"] + 4 * (e + 1)),
         xq=ws.read(np.uint8, (t, hdim), lay["xq"]),
         xs=ws.read(np.float32, (t, gx), lay["xs"]),
         h=ws.read(np.uint16, (a, i), lay["h"]),

@@ -223,9 +223,17 @@ def test_moe_descriptor_layout_and_geometry():
     a = 1024 * 2
     assert lay["topk_w"] == a * 4 and lay["y"] + a * 4096 * 4 == lay["end"]
     assert all(v % 256 == 0 for v in lay.values())
+    assert lay["xq"] - lay["tiles"] == 256  # 128- and 256-row tile prefixes, 2 x 9 int32
     dims, sym = moe.launch_geometry(4, d, 1024)   # gate/up
-    # 1-D grid over (64 h-column block, 128-row tile of the tile bound)
-    assert sym == "lf_moe_gate_up" and dims.grid == (14336 // 64 * (a // 128 + 8), 1, 1)
+    # >= 256 routed rows per expert on average: 256 x 256 tiles, 1-D grid over
+    # (128 h-column block, 256-row tile of the tile bound), 8 waves
+    assert sym == "lf_moe_gate_up_t256" and dims.grid == (14336 // 128 * (a // 256 + 8), 1, 1)
+    assert dims.block == (512, 1, 1)
+    dims, sym = moe.launch_geometry(6, d, 1024)   # down
+    assert sym == "lf_moe_down_t256" and dims.grid == (4096 // 256 * (a // 256 + 8), 1, 1)
+    # fewer rows per expert: 128 x 128 tiles over (64 h-column block, 128-row tile)
+    dims, sym = moe.launch_geometry(4, d, 512)
+    assert sym == "lf_moe_gate_up" and dims.grid == (14336 // 64 * (512 * 2 // 128 + 8), 1, 1)
     dims, sym = moe.launch_geometry(2, d, 1024)   # sort: a block per 1024 assignments
     assert sym == "lf_moe_sort" and dims.grid == (2, 1, 1) and dims.block == (1024, 1, 1)
     dims, sym = moe.launch_geometry(8, d, 1024)   # sort counts: a block per 1024 assignments

@@ -71,6 +71,7 @@ def check_routing(logits, k, mode, st):
     np.testing.assert_array_equal(st["pos"], inv)
     counts = np.diff(offsets)
     np.testing.assert_array_equal(st["tiles"], np.concatenate([[0], np.cumsum((counts + 127) // 128)]))
+    np.testing.assert_array_equal(st["tiles256"], np.concatenate([[0], np.cumsum((counts + 255) // 256)]))
     return ex, w
 
 
@@ -167,3 +168,23 @@ def test_moe_zero_tokens(rt):
     x, logits, weights, out, st = run_case(rt, rng, 0, 8, 2, 256, 256, 0, block=False,
                                            max_tokens=16)
     assert out.shape == (0, 256)
+
+
+@pytest.mark.parametrize("t,e,k,hidden,inter,skew", [
+    (1024, 8, 2, 512, 384, 1.5), (700, 4, 2, 256, 256, 0.0), (1100, 8, 2, 256, 640, 3.0),
+])
+def test_moe_t256(rt, t, e, k, hidden, inter, skew):
+    """Profiles averaging >= 256 routed rows per expert run the grouped GEMMs
+    on 256 x 256 tiles: experts with several 256-row tiles, a partial last
+    tile, skewed load (bias N(0, skew)) and, for the larger skew, experts left
+    with few or no rows."""
+    from lunaflux_amd import _abi, moe
+    desc = moe.moe_descriptor(e, k, 0, hidden, inter, 0)
+    assert moe.launch_geometry(_abi.MOE_GATE_UP, desc, t)[1] == "lf_moe_gate_up_t256"
+    assert moe.launch_geometry(_abi.MOE_DOWN, desc, t)[1] == "lf_moe_down_t256"
+    rng = np.random.default_rng(950 + t + e)
+    logits = (rng.standard_normal((t, e)) + rng.normal(0, skew, e)).astype(np.float32)
+    x, logits, weights, out, st = run_case(rt, rng, t, e, k, hidden, inter, 0, block=False,
+                                           logits=logits)
+    ex, w = check_routing(logits, k, 0, st)
+    check_output(x, weights, ex, w, out, False, f"moe t256 t={t} e={e} skew={skew}", st)
