@@ -39,6 +39,7 @@ BF16_PEAK_TFLOPS = 2500.0
 ROTATIONS = 24  # weight copies cycled per call: 24 x 218 MB keeps the 256 MB MALL from serving reuse
 HIDDEN, INTER, NQ, NKV = 4096, 14336, 4096, 1024
 METRIC = "FP8 proj GB/s & TFLOP/s (% roofline), Llama-3-8B shapes M=1..8192, 1 GPU"
+PMC_COPY_BYTES = 512 << 20  # calibration copy of the counter passes
 
 
 def log(msg):
@@ -61,6 +62,13 @@ def layer_bytes(m):
 
 def call_flops(m, k, n):
     return 2 * m * n * k
+
+
+def roofline_kernel():
+    """Symbol of the dominant kernel of the headline workload: the W8A16
+    gate/up launch of a 32-row profile (host-side geometry, no GPU needed)."""
+    from lunaflux_amd import _abi, fp8
+    return fp8.launch_geometry(_abi.ENTRY_W8A16_GATE_UP, INTER, HIDDEN, 32)[1]
 
 
 class Layer:
@@ -293,7 +301,7 @@ def pmc_pass():
                          _region(h, alignment=256), 32)
     for _ in range(10):
         op.launch(rt.stream, synchronous=False)
-    n = 512 << 20
+    n = PMC_COPY_BYTES
     src, dst = rt.context.allocate(n), rt.context.allocate(n)
     cnt = rt.context.upload(np.array([n // 16], np.int64))
     copy = rt.function("lf_calibrate_copy")
@@ -326,15 +334,71 @@ def pmc_pass_prefill():
         log(f"pmc prefill pass: {op.steps[-1].name} M={m} K={k} N={n} x5")
 
 
-def measured_traffic():
-    """HBM bytes per launch of the roofline kernel from the committed counter
-    summary (profiles/lf_fp8_w8a16_gate_up_m32.traffic.json), or None."""
-    path = os.path.join(ROOT, "profiles", "lf_fp8_w8a16_gate_up_m32.traffic.json")
+def measured_traffic(kernel):
+    """HBM bytes per launch of the roofline kernel from its committed counter
+    summary (profiles/<kernel>.traffic.json, written by --summarize-traffic),
+    or None when there is none for this kernel."""
+    path = os.path.join(ROOT, "profiles", f"{kernel}.traffic.json")
     try:
         with open(path) as f:
-            return json.load(f).get("bytes_per_launch")
+            data = json.load(f)
     except (OSError, ValueError):
         return None
+    return data.get("bytes_per_launch") if data.get("kernel") == kernel else None
+
+
+def summarize_traffic(fetch_csv, write_csv, kernel):
+    """Counter summary of one kernel's HBM traffic from two rocprofv3 --pmc
+    runs of --pmc-pass (FETCH_SIZE, then WRITE_SIZE; KiB per dispatch), each
+    scaled by what the same counter reads for lf_calibrate_copy moving a
+    known number of bytes. Prints the JSON stored under profiles/."""
+    import csv
+
+    def per_dispatch(path, counter):
+        vals = {}
+        for r in csv.DictReader(open(path)):
+            if r["Counter_Name"] == counter:
+                vals.setdefault(r["Kernel_Name"], []).append(float(r["Counter_Value"]))
+        return vals
+
+    fetch, write = per_dispatch(fetch_csv, "FETCH_SIZE"), per_dispatch(write_csv, "WRITE_SIZE")
+    copy_bytes = PMC_COPY_BYTES
+    f_cal = np.mean(fetch["lf_calibrate_copy"])
+    w_cal = np.mean(write["lf_calibrate_copy"])
+    f_factor = copy_bytes / (f_cal * 1024)
+    w_factor = copy_bytes / (w_cal * 1024)
+    f_k = np.mean(fetch[kernel])
+    w_k = np.mean(write[kernel])
+    read_b = int(round(f_k * 1024 * f_factor))
+    write_b = int(round(w_k * 1024 * w_factor))
+    algo = call_bytes(32, HIDDEN, 2 * INTER, INTER)
+    return {
+        "kernel": kernel,
+        "workload": "Llama-3-8B gate/up (4096 -> 2 x 14336, SwiGLU), M=32, one launch",
+        "commands": [
+            "cd /tmp && export TMPDIR=/tmp && timeout -s KILL 120 rocprofv3 --pmc FETCH_SIZE "
+            "--output-format csv -d $GRAFT_REPO_ROOT/gpurun_out/prof_fetch -o fetch -- python3 "
+            "$GRAFT_REPO_ROOT/bench.py --pmc-pass",
+            "cd /tmp && export TMPDIR=/tmp && timeout -s KILL 120 rocprofv3 --pmc WRITE_SIZE "
+            "--output-format csv -d $GRAFT_REPO_ROOT/gpurun_out/prof_write -o write -- python3 "
+            "$GRAFT_REPO_ROOT/bench.py --pmc-pass",
+            "python3 bench.py --summarize-traffic <fetch_counter_collection.csv> "
+            "<write_counter_collection.csv>",
+        ],
+        "fetch_size_kib_per_dispatch": round(f_k, 2),
+        "fetch_dispatches": len(fetch[kernel]),
+        "write_size_kib_per_dispatch": round(w_k, 2),
+        "write_dispatches": len(write[kernel]),
+        "calibration": {"kernel": "lf_calibrate_copy", "bytes_read": copy_bytes,
+                        "bytes_written": copy_bytes, "fetch_size_kib": round(f_cal, 2),
+                        "write_size_kib": round(w_cal, 2), "fetch_factor": round(f_factor, 5),
+                        "write_factor": round(w_factor, 5)},
+        "read_bytes_per_launch": read_b,
+        "write_bytes_per_launch": write_b,
+        "bytes_per_launch": read_b + write_b,
+        "algorithmic_bytes_per_launch": algo,
+        "traffic_over_algorithmic": round((read_b + write_b) / algo, 4),
+    }
 
 
 def main():
@@ -347,7 +411,13 @@ def main():
     ap.add_argument("--pmc-pass", action="store_true", help="short run for counter passes")
     ap.add_argument("--pmc-pass-prefill", action="store_true",
                     help="short run for the prefill MFMA counter pass")
+    ap.add_argument("--summarize-traffic", nargs=2, metavar=("FETCH_CSV", "WRITE_CSV"),
+                    help="print the traffic summary of the roofline kernel from the two "
+                         "--pmc-pass counter CSVs (no GPU needed)")
     args = ap.parse_args()
+    if args.summarize_traffic:
+        print(json.dumps(summarize_traffic(*args.summarize_traffic, roofline_kernel()), indent=1))
+        return
     if args.gpus != 1:
         print(f"bench.py measures one GPU only: --gpus {args.gpus} is not supported "
               "(this build has no multi-GPU path; see DESIGN.md on sharding)", file=sys.stderr)
@@ -372,6 +442,8 @@ def main():
     total, _, step_ms = decode.run(m, args.steps, args.warmup, probe=None)
     value = layer_bytes(m) / (step_ms * 1e-3) / 1e9
     gu_bytes = call_bytes(m, HIDDEN, 2 * INTER, INTER)
+    kernel = decode.ops[m][1][0]["gate_up"].steps[-1].name
+    assert kernel == roofline_kernel(), kernel
     probe_ms = decode.time_kernel(m, "gate_up", args.steps)
     achieved = gu_bytes / (probe_ms * 1e-3) / 1e9
     log(f"decode M={m}: {step_ms * 1e3:.1f} us/layer, {value:.0f} GB/s; gate_up {probe_ms * 1e3:.1f} us "
@@ -431,9 +503,9 @@ def main():
         "config": {"workload": "llama3-8b decode layer: qkv+o+gate_up(SwiGLU)+down, M=32, W8A16",
                    "global_batch": m, "seq_len": 1, "parallelism": "single GPU",
                    "weight_rotations": ROTATIONS},
-        "roofline": {"bound": "hbm", "kernel": "lf_fp8_w8a16_gate_up_m32",
+        "roofline": {"bound": "hbm", "kernel": kernel,
                      "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": measured_traffic(),
+                     "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": measured_traffic(kernel),
                      "algorithmic_bytes_per_launch": gu_bytes,
                      "avg_launch_us": round(probe_ms * 1e3, 2)},
         "cpu_baseline": cpu,
