@@ -884,17 +884,13 @@ LF_W8A16_TILE_ENTRIES(1, 16, 1)
 // 14336, Q 4096, K/V 1024): one-tile (t1) or column-group (g) form, chosen
 // per (shape, profile) by lunaflux_fp8_launch_geometry; the parameters are
 // the measured best of a sweep on MI355X (waves, weight / activation ring
-// depth, LDS slots, K-slices).
+// depth, LDS slots, K-slices). Gate/up has enough tiles (896) to fill the
+// chip with unsplit column groups (2 or 4 tiles per block, S = 1): no
+// exchange, and the activations are read once per group.
 #define LF_W16_FIXED_DENSE_T1(KK, M, MT, KS, DW, DX, SLOTS)                                     \
   __global__ __launch_bounds__(KS * 64) void lf_fp8_w8a16_dense_k##KK##_m##M(                \
       const int32_t *counts, const uint16_t *x, const uint8_t *w, uint16_t *y, uint8_t *) {  \
     w8a16_fixed_kernel<KK, KS, MT, 0, DW, DX, 0, 0, SLOTS>(counts, x, w, w, w, y);            \
-  }
-#define LF_W16_FIXED_GATE_UP_T1(KK, M, MT, KS, DW, DX, SLOTS)                                   \
-  __global__ __launch_bounds__(KS * 64) void lf_fp8_w8a16_gate_up_k##KK##_m##M(              \
-      const int32_t *counts, const uint16_t *x, const uint8_t *wg, const uint8_t *wu,        \
-      uint16_t *h, uint8_t *) {                                                              \
-    w8a16_fixed_kernel<KK, KS, MT, 2, DW, DX, 0, 0, SLOTS>(counts, x, wg, wu, wu, h);         \
   }
 #define LF_W16_FIXED_QKV_T1(KK, NQ, NKV, M, MT, KS, DW, DX, SLOTS)                              \
   __global__ __launch_bounds__(KS * 64) void lf_fp8_w8a16_qkv_k##KK##_q##NQ##_kv##NKV##_m##M( \
@@ -920,7 +916,7 @@ LF_W16_FIXED_DENSE_T1(14336, 16, 1, 8, 6, 2, 2)
 LF_W16_FIXED_DENSE_G(14336, 32, 2, 4, 4, 6, 2)
 LF_W16_FIXED_QKV_T1(4096, 4096, 1024, 16, 1, 8, 4, 2, 2)
 LF_W16_FIXED_QKV_T1(4096, 4096, 1024, 32, 2, 8, 4, 1, 1)
-LF_W16_FIXED_GATE_UP_T1(4096, 16, 1, 8, 2, 2, 2)
-LF_W16_FIXED_GATE_UP_G(4096, 32, 2, 2, 8, 4, 2)
+LF_W16_FIXED_GATE_UP_G(4096, 16, 1, 1, 2, 4, 2)
+LF_W16_FIXED_GATE_UP_G(4096, 32, 2, 1, 4, 3, 2)
 
 }  // extern "C"

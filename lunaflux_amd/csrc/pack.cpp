@@ -116,8 +116,8 @@ constexpr W8a16Fixed kW8a16Fixed[] = {
      "lf_fp8_w8a16_qkv_k4096_q4096_kv1024_m16"},
     {LF_FP8_ENTRY_W8A16_QKV, 4096, 4096, 1024, 2, false, 8, 1,
      "lf_fp8_w8a16_qkv_k4096_q4096_kv1024_m32"},
-    {LF_FP8_ENTRY_W8A16_GATE_UP, 4096, 0, 0, 1, false, 8, 1, "lf_fp8_w8a16_gate_up_k4096_m16"},
-    {LF_FP8_ENTRY_W8A16_GATE_UP, 4096, 0, 0, 2, true, 8, 2, "lf_fp8_w8a16_gate_up_k4096_m32"},
+    {LF_FP8_ENTRY_W8A16_GATE_UP, 4096, 0, 0, 1, true, 2, 1, "lf_fp8_w8a16_gate_up_k4096_m16"},
+    {LF_FP8_ENTRY_W8A16_GATE_UP, 4096, 0, 0, 2, true, 4, 1, "lf_fp8_w8a16_gate_up_k4096_m32"},
 };
 
 // The specialized entry for (entry, N, K, Q / K-V split, profile), or null.

@@ -126,10 +126,14 @@ def test_launch_geometry():
     assert fp8.w8a16_workspace_bytes(_abi.ENTRY_W8A16_DENSE, 4096, 14336, 32) == 4 * 256 * 2 * 1024 + 256
     dims, sym = fp8.launch_geometry(_abi.ENTRY_W8A16_DENSE, 4096, 4096, 8)
     assert sym == "lf_fp8_w8a16_dense_k4096_m16" and dims.grid == (256, 1, 1) and dims.block == (512, 1, 1)
+    # gate/up: unsplit column groups (4 tiles per block at 32 rows, 2 at 16)
     dims, sym = fp8.launch_geometry(_abi.ENTRY_W8A16_GATE_UP, 14336, 4096, 32)
-    assert sym == "lf_fp8_w8a16_gate_up_k4096_m32" and dims.grid == (112 * 2, 1, 1)
-    assert dims.block == (512, 1, 1)
-    assert fp8.w8a16_workspace_bytes(_abi.ENTRY_W8A16_GATE_UP, 14336, 4096, 32) == 2 * 896 * 2 * 2 * 1024 + 512
+    assert sym == "lf_fp8_w8a16_gate_up_k4096_m32" and dims.grid == (224, 1, 1)
+    assert dims.block == (256, 1, 1)
+    assert fp8.w8a16_workspace_bytes(_abi.ENTRY_W8A16_GATE_UP, 14336, 4096, 32) == 256
+    dims, sym = fp8.launch_geometry(_abi.ENTRY_W8A16_GATE_UP, 14336, 4096, 16)
+    assert sym == "lf_fp8_w8a16_gate_up_k4096_m16" and dims.grid == (448, 1, 1)
+    assert dims.block == (128, 1, 1)
     dims, sym = fp8.launch_geometry(_abi.ENTRY_W8A16_QKV, 6144, 4096, 32, qkv_split=(4096, 1024))
     assert sym == "lf_fp8_w8a16_qkv_k4096_q4096_kv1024_m32" and dims.grid == (384, 1, 1)
     assert fp8.w8a16_workspace_bytes(_abi.ENTRY_W8A16_QKV, 6144, 4096, 32, (4096, 1024)) == 256
