@@ -496,6 +496,27 @@ __device__ void w8a16_tile_kernel(const int32_t *counts, const uint16_t *x, cons
   }
 }
 
+// The compiled shape of a specialized entry against a weight region's
+// header. Read together with the live row count, right after the weight
+// prologue is issued, so the scalar loads overlap the weight stream; read
+// after the main loop (where it is used) it put a cold header fetch of
+// about 1 us between the last MFMA and the stores.
+// The first 32 header bytes are read in one go and compared without
+// short-circuits, so the scalar loads issue together (a chain of && made the
+// compiler fetch field by field, each after the previous comparison).
+template <int NW, int K>
+LF_DEVICE bool fixed_shape_ok(const uint8_t *const (&region)[NW], int region_rows) {
+  uint32_t bad = 0;
+#pragma unroll
+  for (int i = 0; i < NW; ++i) {
+    const u32x4 *h = reinterpret_cast<const u32x4 *>(region[i]);
+    const u32x4 a = h[0], b = h[1];  // magic, version, layout, scale_mode | rows, columns, experts
+    bad |= (a.x ^ kWeightMagic) | (a.w ^ kScalePerChannel) |
+           (b.x ^ static_cast<uint32_t>(region_rows)) | (b.y ^ static_cast<uint32_t>(K)) | (b.z ^ 1u);
+  }
+  return bad == 0;
+}
+
 // ---------------------------------------------------------------------------
 // Shape-specialized one-tile form. The input width K (and, for QKV, the Q and
 // K/V widths) is a compile-time constant, as in an AOT entry point built for
@@ -588,7 +609,9 @@ __device__ __forceinline__ void w8a16_fixed_kernel(const int32_t *counts, const 
   // which leaves only a k-tile or two in flight.
   __builtin_amdgcn_sched_barrier(0);
 
-  const int M = live_rows(counts, 16 * MT);
+  // A region whose header disagrees with the compiled shape (a wrong weight
+  // bound to this entry) counts as no live rows: nothing is stored.
+  const int M = live_rows(counts, 16 * MT) & -static_cast<int>(fixed_shape_ok<NW, K>(region, region_rows));
   // Activation loads are row-coalesced: instruction q gives lane l row
   // 4 q + l / 16, 16-byte chunk l % 16 of the k-tile (rows past M re-read row
   // M - 1; their outputs are never stored. M == 0 stores nothing).
@@ -651,17 +674,6 @@ __device__ __forceinline__ void w8a16_fixed_kernel(const int32_t *counts, const 
     for (int i = 0; i < NW; ++i) red[(wave * MT * NW + mt * NW + i) * 64 + lane] = acc[mt][i];
   __syncthreads();
 
-  // The compiled shape must be the regions' shape; a mismatched region
-  // (wrong weight bound to this entry) leaves the output unwritten.
-  bool ok = true;
-#pragma unroll
-  for (int i = 0; i < NW; ++i) {
-    const WeightHeader &h = header_of(region[i]);
-    ok = ok && h.magic == kWeightMagic && h.columns == static_cast<uint32_t>(K) &&
-         h.rows == static_cast<uint32_t>(region_rows) && h.experts == 1u &&
-         h.scale_mode == kScalePerChannel;
-  }
-  if (!ok) return;
   // Element e of the tile: row tile mt, lane l, register rr (16x16 MFMA
   // accumulator layout: row 4 (l / 16) + rr, column l % 16).
   for (int e = threadIdx.x; e < MT * 256; e += KS * 64) {
@@ -758,7 +770,10 @@ __device__ __forceinline__ void w8a16_fixed_group_kernel(const int32_t *counts, 
   for (int d = 0; d < EW; ++d) load_tiles<NW>(strip, kt0 + d, lane, b[d]);
   __builtin_amdgcn_sched_barrier(0);
 
-  const int M = live_rows(counts, 16 * MT);
+  // A region whose header disagrees with the compiled shape counts as no
+  // live rows: nothing is stored, and the block still takes part in the
+  // split-K arrival count, so the counters stay consistent.
+  const int M = live_rows(counts, 16 * MT) & -static_cast<int>(fixed_shape_ok<NW, K>(region, region_rows));
   const uint16_t *xsrc[XPW];
   int xdst[XPW];
 #pragma unroll
@@ -816,17 +831,7 @@ __device__ __forceinline__ void w8a16_fixed_group_kernel(const int32_t *counts, 
     __builtin_amdgcn_sched_barrier(0);
   });
 
-  bool ok = true;
-#pragma unroll
-  for (int i = 0; i < NW; ++i) {
-    const WeightHeader &h = header_of(region[i]);
-    ok = ok && h.magic == kWeightMagic && h.columns == static_cast<uint32_t>(K) &&
-         h.rows == static_cast<uint32_t>(region_rows) && h.experts == 1u &&
-         h.scale_mode == kScalePerChannel;
-  }
-  // A mismatched region leaves the output unwritten; every block still takes
-  // part in the arrival count so the counters stay consistent.
-  group_epilogue<MT, NW, MODE>(acc, sc, ok ? M : 0, S, s, cg, tiles, out_tile, true, ld, y, ws,
+  group_epilogue<MT, NW, MODE>(acc, sc, M, S, s, cg, tiles, out_tile, true, ld, y, ws,
                                last_block);
 }
 
