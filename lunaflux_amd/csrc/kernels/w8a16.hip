@@ -903,6 +903,12 @@ LF_W8A16_TILE_ENTRIES(1, 16, 1)
       const uint8_t *wv, uint16_t *y, uint8_t *) {                                           \
     w8a16_fixed_kernel<KK, KS, MT, 1, DW, DX, NQ, NKV, SLOTS>(counts, x, wq, wk, wv, y);      \
   }
+#define LF_W16_FIXED_QKV_G(KK, NQ, NKV, M, MT, S, W, DW, DX)                                    \
+  __global__ __launch_bounds__(W * 64) void lf_fp8_w8a16_qkv_k##KK##_q##NQ##_kv##NKV##_m##M(  \
+      const int32_t *counts, const uint16_t *x, const uint8_t *wq, const uint8_t *wk,        \
+      const uint8_t *wv, uint16_t *y, uint8_t *ws) {                                         \
+    w8a16_fixed_group_kernel<KK, S, W, MT, 1, DW, DX, NQ, NKV>(counts, x, wq, wk, wv, y, ws);  \
+  }
 #define LF_W16_FIXED_DENSE_G(KK, M, MT, S, W, DW, DX)                                           \
   __global__ __launch_bounds__(W * 64) void lf_fp8_w8a16_dense_k##KK##_m##M(                 \
       const int32_t *counts, const uint16_t *x, const uint8_t *w, uint16_t *y, uint8_t *ws) { \
@@ -920,7 +926,7 @@ LF_W16_FIXED_DENSE_T1(4096, 32, 2, 8, 4, 1, 1)
 LF_W16_FIXED_DENSE_T1(14336, 16, 1, 8, 6, 2, 2)
 LF_W16_FIXED_DENSE_G(14336, 32, 2, 4, 4, 6, 2)
 LF_W16_FIXED_QKV_T1(4096, 4096, 1024, 16, 1, 8, 4, 2, 2)
-LF_W16_FIXED_QKV_T1(4096, 4096, 1024, 32, 2, 8, 4, 1, 1)
+LF_W16_FIXED_QKV_G(4096, 4096, 1024, 32, 2, 4, 8, 4, 2)
 LF_W16_FIXED_GATE_UP_G(4096, 16, 1, 1, 2, 4, 2)
 LF_W16_FIXED_GATE_UP_G(4096, 32, 2, 1, 4, 3, 2)
 

@@ -134,9 +134,15 @@ def test_launch_geometry():
     dims, sym = fp8.launch_geometry(_abi.ENTRY_W8A16_GATE_UP, 14336, 4096, 16)
     assert sym == "lf_fp8_w8a16_gate_up_k4096_m16" and dims.grid == (448, 1, 1)
     assert dims.block == (128, 1, 1)
+    # QKV at 32 rows: 8 tiles per block over 4 K-slices (48 groups x 4)
     dims, sym = fp8.launch_geometry(_abi.ENTRY_W8A16_QKV, 6144, 4096, 32, qkv_split=(4096, 1024))
-    assert sym == "lf_fp8_w8a16_qkv_k4096_q4096_kv1024_m32" and dims.grid == (384, 1, 1)
-    assert fp8.w8a16_workspace_bytes(_abi.ENTRY_W8A16_QKV, 6144, 4096, 32, (4096, 1024)) == 256
+    assert sym == "lf_fp8_w8a16_qkv_k4096_q4096_kv1024_m32" and dims.grid == (192, 1, 1)
+    assert dims.block == (512, 1, 1)
+    assert (fp8.w8a16_workspace_bytes(_abi.ENTRY_W8A16_QKV, 6144, 4096, 32, (4096, 1024))
+            == 4 * 384 * 2 * 1024 + 256)
+    dims, sym = fp8.launch_geometry(_abi.ENTRY_W8A16_QKV, 6144, 4096, 16, qkv_split=(4096, 1024))
+    assert sym == "lf_fp8_w8a16_qkv_k4096_q4096_kv1024_m16" and dims.grid == (384, 1, 1)
+    assert fp8.w8a16_workspace_bytes(_abi.ENTRY_W8A16_QKV, 6144, 4096, 16, (4096, 1024)) == 256
     # a QKV split without an entry, or a profile above 32 rows: generic
     dims, sym = fp8.launch_geometry(_abi.ENTRY_W8A16_QKV, 6144, 4096, 32, qkv_split=(2048, 2048))
     assert sym == "lf_fp8_w8a16_qkv_m32"
