@@ -444,21 +444,39 @@ __device__ void grouped_gemm(const int32_t *counts, const MoeDesc &d, const uint
   }
 
   const int r = lane & 15;
+  // Per-channel form: every scale of this lane before the first store (the
+  // stores share the workspace with the scale arrays, so a load between
+  // stores would wait for them).
+  float swv[T::kFN], sav[T::kFM][4];
+  if constexpr (!BLOCK) {
+#pragma unroll
+    for (int j = 0; j < T::kFN; ++j) swv[j] = wsc[j][col[j] + r];
+    // row scales in expert order: the token quantizer writes the token
+    // scales to the h-scale array by position (stage 0), the hidden
+    // quantizer its own (stage 1)
+    const float *row_scales = at<float>(ws, L.hs);
+#pragma unroll
+    for (int i = 0; i < T::kFM; ++i)
+#pragma unroll
+      for (int rr = 0; rr < 4; ++rr) {
+        const int pp = p0 + w8a8v3::acc_row<T>(wm, i, lane, rr);
+        sav[i][rr] = row_scales[pp < pend ? pp : p0];
+      }
+  }
 #pragma unroll
   for (int i = 0; i < T::kFM; ++i) {
 #pragma unroll
     for (int rr = 0; rr < 4; ++rr) {
       const int pp = p0 + w8a8v3::acc_row<T>(wm, i, lane, rr);
       if (pp >= pend) continue;
-      const float sa = BLOCK ? 1.0f : ascales[src_row(pp)];
       if (STAGE == 0) {
         uint16_t *hrow = at<uint16_t>(ws, L.h) + static_cast<uint64_t>(pp) * N;
 #pragma unroll
         for (int j = 0; j < T::kFN / 2; ++j) {
           const int c = col[j] + r;
-          const float gv = BLOCK ? acc[i][j][rr] : acc[i][j][rr] * sa * wsc[j][c];
+          const float gv = BLOCK ? acc[i][j][rr] : acc[i][j][rr] * sav[i][rr] * swv[j];
           const float uv = BLOCK ? acc[i][j + T::kFN / 2][rr]
-                                 : acc[i][j + T::kFN / 2][rr] * sa * wsc[j + T::kFN / 2][c];
+                                 : acc[i][j + T::kFN / 2][rr] * sav[i][rr] * swv[j + T::kFN / 2];
           hrow[c] = static_cast<uint16_t>(f32_to_bf16(silu_mul(gv, uv)));
         }
       } else {
@@ -466,7 +484,7 @@ __device__ void grouped_gemm(const int32_t *counts, const MoeDesc &d, const uint
 #pragma unroll
         for (int j = 0; j < T::kFN; ++j) {
           const int c = col[j] + r;
-          yrow[c] = BLOCK ? acc[i][j][rr] : acc[i][j][rr] * sa * wsc[j][c];
+          yrow[c] = BLOCK ? acc[i][j][rr] : acc[i][j][rr] * sav[i][rr] * swv[j];
         }
       }
     }
@@ -527,7 +545,14 @@ __device__ void grouped_gemm_t256(const int32_t *counts, const MoeDesc &d, const
   };
 
   const uint8_t *abase = at<uint8_t>(ws, STAGE == 0 ? L.xq : L.hq);
-  const float *ascales = at<float>(ws, STAGE == 0 ? L.xs : L.hs);
+  // Row scales of the tile in expert order (both stages find them in the
+  // h-scale array: the token quantizer writes the token scales there by
+  // position, the hidden quantizer later its own), one per thread of the
+  // first 256, loaded before the main loop and parked in LDS after it.
+  __shared__ float sa_tile[BM];
+  const float *row_scales = at<float>(ws, L.hs);
+  float sa_mine = 0.0f;
+  if (threadIdx.x < BM) sa_mine = row_scales[p0 + static_cast<int>(threadIdx.x) < pend ? p0 + threadIdx.x : p0];
   w8a8v4::Plan<T> plan;
 #pragma unroll
   for (int q = 0; q < T::kAIns; ++q) {
@@ -551,7 +576,7 @@ __device__ void grouped_gemm_t256(const int32_t *counts, const MoeDesc &d, const
   w8a8v4::mainloop<T, true>(plan, KT, smem, acc, live_fm);
 
   const int c = lane & 31;
-  const float *wsc[T::kFN];
+  float swv[T::kFN];
   int ocol[T::kFN];
 #pragma unroll
   for (int j = 0; j < T::kFN; ++j) {
@@ -559,27 +584,60 @@ __device__ void grouped_gemm_t256(const int32_t *counts, const MoeDesc &d, const
     int t;
     slot((wn * T::kWaveN) / 16 + 2 * j + (c >> 4), region, t, ocol[j]);
     ocol[j] += c & 15;
-    wsc[j] = expert_scales(region, e) + t * 16 + (c & 15);
+    swv[j] = expert_scales(region, e)[t * 16 + (c & 15)];
   }
+  if (threadIdx.x < BM) sa_tile[threadIdx.x] = sa_mine;
+  // The output goes through LDS in 16-byte row chunks (w8a8v4::StageTile):
+  // STAGE 0 stages 32 rows x 64 h-columns of bf16 per pass, STAGE 1 16 rows
+  // x 128 columns of fp32 (16 of the 32 rows a fragment row holds).
+  const int col0 = __builtin_amdgcn_readfirstlane(ocol[0] - c);
+  w8a8v4::epilogue_barrier();
+  const int pw = p0 + wm * T::kWaveM;
+  if constexpr (STAGE == 0) {
+    using Stage = w8a8v4::StageTile<uint16_t, 32, T::kWaveN / 2>;
+    static_assert(Stage::kBytes * T::kWaves <= T::kSmem, "staging fits the stage ring");
+    const Stage st{reinterpret_cast<uint16_t *>(smem + wave * Stage::kBytes)};
+    uint16_t *h = at<uint16_t>(ws, L.h);
 #pragma unroll
-  for (int i = 0; i < T::kFM; ++i) {
+    for (int i = 0; i < T::kFM; ++i) {
 #pragma unroll
-    for (int r = 0; r < 16; ++r) {
-      const int pp = p0 + wm * T::kWaveM + w8a8v4::acc_row<T>(i, lane, r);
-      if (pp >= pend) continue;
-      const float sa = ascales[src_row(pp)];
-      if (STAGE == 0) {
-        uint16_t *hrow = at<uint16_t>(ws, L.h) + static_cast<uint64_t>(pp) * N;
+      for (int r = 0; r < 16; ++r) {
+        const float sa = sa_tile[wm * T::kWaveM + w8a8v4::acc_row<T>(i, lane, r)];
 #pragma unroll
         for (int j = 0; j < T::kFN / 2; ++j) {
-          const float gv = acc[i][j][r] * sa * *wsc[j];
-          const float uv = acc[i][j + T::kFN / 2][r] * sa * *wsc[j + T::kFN / 2];
-          hrow[ocol[j]] = static_cast<uint16_t>(f32_to_bf16(silu_mul(gv, uv)));
+          const float gv = acc[i][j][r] * sa * swv[j];
+          const float uv = acc[i][j + T::kFN / 2][r] * sa * swv[j + T::kFN / 2];
+          st.put(w8a8v4::acc_row<T>(0, lane, r), ocol[j] - col0,
+                 static_cast<uint16_t>(f32_to_bf16(silu_mul(gv, uv))));
         }
-      } else {
-        float *yrow = at<float>(ws, L.y) + static_cast<uint64_t>(pp) * N;
+      }
+      const int p_i = pw + 32 * i;
+      st.flush(lane, [&](int row) -> uint16_t * {
+        return p_i + row < pend ? h + static_cast<uint64_t>(p_i + row) * N + col0 : nullptr;
+      });
+    }
+  } else {
+    using Stage = w8a8v4::StageTile<float, 16, T::kWaveN>;
+    static_assert(Stage::kBytes * T::kWaves <= T::kSmem, "staging fits the stage ring");
+    const Stage st{reinterpret_cast<float *>(smem + wave * Stage::kBytes)};
+    float *y = at<float>(ws, L.y);
 #pragma unroll
-        for (int j = 0; j < T::kFN; ++j) yrow[ocol[j]] = acc[i][j][r] * sa * *wsc[j];
+    for (int i = 0; i < T::kFM; ++i) {
+#pragma unroll
+      for (int half = 0; half < 2; ++half) {
+        // accumulator registers 8 half .. 8 half + 7 hold rows 16 half .. + 15
+#pragma unroll
+        for (int r = 8 * half; r < 8 * half + 8; ++r) {
+          const float sa = sa_tile[wm * T::kWaveM + w8a8v4::acc_row<T>(i, lane, r)];
+#pragma unroll
+          for (int j = 0; j < T::kFN; ++j) {
+            st.put(w8a8v4::acc_row<T>(0, lane, r) - 16 * half, ocol[j] - col0, acc[i][j][r] * sa * swv[j]);
+          }
+        }
+        const int p_i = pw + 32 * i + 16 * half;
+        st.flush(lane, [&](int row) -> float * {
+          return p_i + row < pend ? y + static_cast<uint64_t>(p_i + row) * N + col0 : nullptr;
+        });
       }
     }
   }
@@ -648,7 +706,21 @@ __global__ __launch_bounds__(256) void lf_moe_quant_tokens(const int32_t *counts
   if (!desc_ok(d)) return;
   const int T = live_rows(counts, 1 << 30);
   const MoeLayout L(d, T);
-  quant_rows(x, d.hidden, d.group, at<uint8_t>(ws, L.xq), at<float>(ws, L.xs), T);
+  if (d.group != 0) {
+    quant_rows(x, d.hidden, d.group, at<uint8_t>(ws, L.xq), at<float>(ws, L.xs), T);
+    return;
+  }
+  const int row = blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (row >= T) return;
+  const uint64_t off = static_cast<uint64_t>(row) * d.hidden;
+  const float sc = quantize_row_wave(x + off, d.hidden, at<uint8_t>(ws, L.xq) + off,
+                                     at<float>(ws, L.xs) + row);
+  // The per-token scale also in expert order, at the position of each of
+  // the token's k assignments (from the sort), for the gate/up epilogue. It
+  // goes to the h-scale array, which the hidden quantizer only writes after
+  // the gate/up GEMM has consumed it.
+  const int lane = threadIdx.x & 63;
+  if (lane < d.top_k) at<float>(ws, L.hs)[at<int32_t>(ws, L.pos)[row * d.top_k + lane]] = sc;
 }
 
 __global__ __launch_bounds__(256) void lf_moe_quant_hidden(const int32_t *counts,

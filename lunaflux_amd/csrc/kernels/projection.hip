@@ -36,9 +36,10 @@ LF_DEVICE uint2 bf16x8_encode(const uint4 &v, float ratio, bool zero) {
 }
 
 // Per-token quantizer: one wave per row (no block barriers). Two passes over
-// the row (amax, then encode); the second re-reads it from cache.
-LF_DEVICE void quantize_row_wave(const uint16_t *src_row, int K, uint8_t *dst_row,
-                                 float *scale) {
+// the row (amax, then encode); the second re-reads it from cache. Returns the
+// row's scale (in every lane) after lane 0 has stored it.
+LF_DEVICE float quantize_row_wave(const uint16_t *src_row, int K, uint8_t *dst_row,
+                                  float *scale) {
   const int lane = threadIdx.x & 63;
   const int chunks = K >> 3;  // 8 bf16 per 16-byte chunk
   const uint4 *src = reinterpret_cast<const uint4 *>(src_row);
@@ -51,7 +52,9 @@ LF_DEVICE void quantize_row_wave(const uint16_t *src_row, int K, uint8_t *dst_ro
   uint2 *dst = reinterpret_cast<uint2 *>(dst_row);
 #pragma unroll 8
   for (int c = lane; c < chunks; c += 64) dst[c] = bf16x8_encode(src[c], ratio, zero);
-  if (lane == 0) *scale = zero ? 0.0f : amax / 448.0f;
+  const float sc = zero ? 0.0f : amax / 448.0f;
+  if (lane == 0) *scale = sc;
+  return sc;
 }
 
 // Per-128-column-group quantizer: the 16 lanes 16q..16q+15 of a wave hold
@@ -189,34 +192,45 @@ __device__ void w8a8_tiled_kernel(const int32_t *counts, const uint8_t *xq, cons
 
   const float *ascale = reinterpret_cast<const float *>(xq + align256(static_cast<uint64_t>(M) * K));
   const int r = lane & 15;
-  const float *wsc[T::kFN];
+  float swv[T::kFN];
   int ocol[T::kFN];
 #pragma unroll
   for (int j = 0; j < T::kFN; ++j) {
     const uint8_t *region;
     int t;
     slot(wn * T::kFN + j, region, t, ocol[j]);
-    wsc[j] = expert_scales(region, 0) + t * 16 + r;
+    swv[j] = expert_scales(region, 0)[t * 16 + r];
   }
+  // Every scale this lane needs is loaded before the first store (the
+  // stores may alias the scale arrays as far as the compiler knows, so a
+  // load between stores would wait for them: one round trip per row).
+  float sav[T::kFM][4];
+#pragma unroll
+  for (int i = 0; i < T::kFM; ++i)
+#pragma unroll
+    for (int rr = 0; rr < 4; ++rr) {
+      const int m = m0 + w8a8v3::acc_row<T>(wm, i, lane, rr);
+      sav[i][rr] = ascale[m < M ? m : M - 1];
+    }
 #pragma unroll
   for (int i = 0; i < T::kFM; ++i) {
 #pragma unroll
     for (int rr = 0; rr < 4; ++rr) {
       const int m = m0 + w8a8v3::acc_row<T>(wm, i, lane, rr);
       if (m >= M) continue;
-      const float sa = ascale[m];
+      const float sa = sav[i][rr];
       uint16_t *yrow = y + static_cast<uint64_t>(m) * ld;
       if (MODE == 2) {
 #pragma unroll
         for (int j = 0; j < T::kFN / 2; ++j) {
-          const float gv = acc[i][j][rr] * sa * *wsc[j];
-          const float uv = acc[i][j + T::kFN / 2][rr] * sa * *wsc[j + T::kFN / 2];
+          const float gv = acc[i][j][rr] * sa * swv[j];
+          const float uv = acc[i][j + T::kFN / 2][rr] * sa * swv[j + T::kFN / 2];
           yrow[ocol[j] + r] = static_cast<uint16_t>(f32_to_bf16(silu_mul(gv, uv)));
         }
       } else {
 #pragma unroll
         for (int j = 0; j < T::kFN; ++j) {
-          yrow[ocol[j] + r] = static_cast<uint16_t>(f32_to_bf16(acc[i][j][rr] * sa * *wsc[j]));
+          yrow[ocol[j] + r] = static_cast<uint16_t>(f32_to_bf16(acc[i][j][rr] * sa * swv[j]));
         }
       }
     }
@@ -279,6 +293,15 @@ __device__ void w8a8_v4_kernel(const int32_t *counts, const uint8_t *xq, const u
     }
   };
 
+  // Row scales of the tile, one per thread of the first BM, loaded before
+  // the main loop and parked in LDS after it for the epilogue.
+  const float *ascale = reinterpret_cast<const float *>(xq + align256(static_cast<uint64_t>(M) * K));
+  __shared__ float sa_tile[BM];
+  float sa_mine = 0.0f;
+  if (threadIdx.x < BM) {
+    const int m = m0 + static_cast<int>(threadIdx.x);
+    sa_mine = ascale[m < M ? m : M - 1];
+  }
   w8a8v4::Plan<T> plan;
 #pragma unroll
   for (int q = 0; q < T::kAIns; ++q) {
@@ -296,9 +319,9 @@ __device__ void w8a8_v4_kernel(const int32_t *counts, const uint8_t *xq, const u
   w8a8v4::f32x16 acc[T::kFM][T::kFN];
   w8a8v4::mainloop<T>(plan, KT, smem, acc);
 
-  const float *ascale = reinterpret_cast<const float *>(xq + align256(static_cast<uint64_t>(M) * K));
+  if (threadIdx.x < BM) sa_tile[threadIdx.x] = sa_mine;
   const int c = lane & 31;
-  const float *wsc[T::kFN];
+  float swv[T::kFN];
   int ocol[T::kFN];
 #pragma unroll
   for (int j = 0; j < T::kFN; ++j) {
@@ -306,30 +329,42 @@ __device__ void w8a8_v4_kernel(const int32_t *counts, const uint8_t *xq, const u
     int t;
     slot((wn * T::kWaveN) / 16 + 2 * j + (c >> 4), region, t, ocol[j]);
     ocol[j] += c & 15;
-    wsc[j] = expert_scales(region, 0) + t * 16 + (c & 15);
+    swv[j] = expert_scales(region, 0)[t * 16 + (c & 15)];
   }
+  // The wave's output block is contiguous: rows m0 + wm kWaveM + [0, kWaveM),
+  // columns from the first fragment's column (gate/up: kWaveN / 2 h-columns).
+  // Staged one 32-row fragment row at a time (a whole 64-row wave tile with
+  // the bank padding would not fit the 128 KiB ring for 128 columns).
+  constexpr int kCols = MODE == 2 ? T::kWaveN / 2 : T::kWaveN;
+  using Stage = w8a8v4::StageTile<uint16_t, 32, kCols>;
+  static_assert(Stage::kBytes * T::kWaves <= T::kSmem, "staging fits the stage ring");
+  const int col0 = __builtin_amdgcn_readfirstlane(ocol[0] - c);
+  w8a8v4::epilogue_barrier();
+  const Stage st{reinterpret_cast<uint16_t *>(smem + wave * Stage::kBytes)};
 #pragma unroll
   for (int i = 0; i < T::kFM; ++i) {
 #pragma unroll
     for (int e = 0; e < 16; ++e) {
-      const int m = m0 + wm * T::kWaveM + w8a8v4::acc_row<T>(i, lane, e);
-      if (m >= M) continue;
-      const float sa = ascale[m];
-      uint16_t *yrow = y + static_cast<uint64_t>(m) * ld;
+      const int row = w8a8v4::acc_row<T>(0, lane, e);
+      const float sa = sa_tile[wm * T::kWaveM + w8a8v4::acc_row<T>(i, lane, e)];
       if (MODE == 2) {
 #pragma unroll
         for (int j = 0; j < T::kFN / 2; ++j) {
-          const float gv = acc[i][j][e] * sa * *wsc[j];
-          const float uv = acc[i][j + T::kFN / 2][e] * sa * *wsc[j + T::kFN / 2];
-          yrow[ocol[j]] = static_cast<uint16_t>(f32_to_bf16(silu_mul(gv, uv)));
+          const float gv = acc[i][j][e] * sa * swv[j];
+          const float uv = acc[i][j + T::kFN / 2][e] * sa * swv[j + T::kFN / 2];
+          st.put(row, ocol[j] - col0, static_cast<uint16_t>(f32_to_bf16(silu_mul(gv, uv))));
         }
       } else {
 #pragma unroll
         for (int j = 0; j < T::kFN; ++j) {
-          yrow[ocol[j]] = static_cast<uint16_t>(f32_to_bf16(acc[i][j][e] * sa * *wsc[j]));
+          st.put(row, ocol[j] - col0, static_cast<uint16_t>(f32_to_bf16(acc[i][j][e] * sa * swv[j])));
         }
       }
     }
+    const int mw = m0 + wm * T::kWaveM + 32 * i;
+    st.flush(lane, [&](int row) -> uint16_t * {
+      return mw + row < M ? y + static_cast<uint64_t>(mw + row) * ld + col0 : nullptr;
+    });
   }
 }
 

@@ -241,6 +241,40 @@ __device__ __forceinline__ void mainloop(const Plan<T> &plan, int KT, uint8_t *s
   step(WNone{}, No{}, f1, f0, s + 1);
 }
 
+// Epilogue staging. A wave's output tile goes through LDS (the stage ring is
+// free once every wave has left the main loop) so that global memory gets
+// 16-byte row chunks instead of one 2-byte bf16 (or 4-byte fp32) element
+// per lane and accumulator register: 8x (4x) fewer store instructions, each
+// covering whole 128-byte row segments. The tile is ROWS x COLS elements of
+// `Elem`, row pitch COLS + 16 bytes' worth, so the two row groups of one
+// accumulator store (rows r and r + 4) fall in different bank halves.
+template <typename Elem, int ROWS, int COLS>
+struct StageTile {
+  static constexpr int kPitch = COLS + 16 / static_cast<int>(sizeof(Elem));  // elements
+  static constexpr int kBytes = ROWS * kPitch * static_cast<int>(sizeof(Elem));
+  static constexpr int kChunks = ROWS * COLS * static_cast<int>(sizeof(Elem)) / 16;
+  static constexpr int kChunksPerRow = COLS * static_cast<int>(sizeof(Elem)) / 16;
+  Elem *base;
+  LF_DEVICE void put(int row, int col, Elem v) const { base[row * kPitch + col] = v; }
+  // Writes the staged tile: row `row` goes to row_ptr(row) (null: skipped).
+  template <class RowPtr>
+  LF_DEVICE void flush(int lane, RowPtr row_ptr) const {
+#pragma unroll
+    for (int q = 0; q < kChunks / 64; ++q) {
+      const int idx = q * 64 + lane;
+      const int row = idx / kChunksPerRow, chunk = idx % kChunksPerRow;
+      const uint4 v = *reinterpret_cast<const uint4 *>(
+          reinterpret_cast<const uint8_t *>(base + row * kPitch) + chunk * 16);
+      Elem *dst = row_ptr(row);
+      if (dst != nullptr) *reinterpret_cast<uint4 *>(reinterpret_cast<uint8_t *>(dst) + chunk * 16) = v;
+    }
+  }
+};
+
+// All waves have left the main loop (their last fragment reads are done), so
+// the stage ring may be overwritten.
+LF_DEVICE void epilogue_barrier() { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); }
+
 // Output coordinates of accumulator element e of lane `lane` in 32 x 32
 // block (i, j): row inside the wave tile and column inside the wave tile.
 template <class T>
