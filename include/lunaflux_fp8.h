@@ -191,7 +191,10 @@ int64_t lunaflux_fp8_qkv_w8a16_workspace_bytes(int64_t nq, int64_t nkv, int64_t 
  *  lf_moe_quant_hidden  (counts, desc, ws)
  *  lf_moe_down[_b128|_t256]   (counts, desc, wd, ws)
  * (_t256: the per-channel GEMMs on 256 x 256 tiles, chosen by the launch
- * geometry for profiles that average >= 256 routed rows per expert.)
+ * geometry for profiles that average >= 256 routed rows per expert.
+ * With per-token scales lf_moe_quant_tokens reads the sort's positions and
+ * also writes each token's scale in expert order, so it runs after
+ * lf_moe_sort.)
  *  lf_moe_combine       (counts, desc, ws, out bf16 [T, H])
  * Routing: the k largest logits per token (ties to the lower expert id);
  * weights are a softmax over the k picked logits (route_mode 0, Mixtral) or
