@@ -110,8 +110,13 @@ LF_DEVICE float wave_max(float v) {
   return v;
 }
 
+// SiLU(g) * u in the reference's order, g / (1 + e^-g) * u, with the
+// hardware exp2 and reciprocal (each within 1 ulp; e^-g = 2^(-g log2 e)):
+// 5 instructions instead of the 28 of expf and an IEEE division, and within
+// a few fp32 ulp of that form (far inside the bf16 output tolerance).
+// Infinities and NaNs come out as in the IEEE form (-inf: NaN, +inf: +inf).
 LF_DEVICE float silu_mul(float g, float u) {
-  float denominator = 1.0f + expf(-g);
-  float s = g / denominator;
+  const float e = __builtin_amdgcn_exp2f(g * -1.44269504088896341f);
+  const float s = g * __builtin_amdgcn_rcpf(1.0f + e);
   return s * u;
 }
