@@ -76,25 +76,6 @@ LF_DEVICE uint32_t f32_to_bf16(float v) {
   return u >> 16;
 }
 
-// OCP E4M3 (bias 7, max 448, no infinities) encode with round to nearest
-// even and saturation to +-448, bit-identical to the host quantizer: the
-// same branch structure and only exact or correctly rounded fp32 operations.
-LF_DEVICE uint32_t e4m3_encode(float value) {
-  uint32_t u = __float_as_uint(value);
-  uint32_t sign = (u >> 24) & 0x80u;
-  uint32_t a = u & 0x7fffffffu;
-  if (a > 0x7f800000u) return sign | 0x7fu;
-  if (a >= 0x43e00000u) return sign | 0x7eu;
-  if (a < 0x3c800000u) {
-    float m = __uint_as_float(a) * 512.0f;  // exact
-    return sign | static_cast<uint32_t>(__builtin_rintf(m));
-  }
-  uint32_t r = a + 0x7ffffu + ((a >> 20) & 1u);
-  r &= 0xfff00000u;
-  uint32_t exponent = (r >> 23) - 120u;  // (e - 127) + 7
-  return sign | (exponent << 3) | ((r >> 20) & 7u);
-}
-
 // Four e4m3 codes (one 32-bit word) -> four bf16 values (two words). The
 // conversion is exact: every e4m3 value is a bf16 value.
 LF_DEVICE void e4m3x4_to_bf16x4(uint32_t word, uint32_t &lo, uint32_t &hi) {

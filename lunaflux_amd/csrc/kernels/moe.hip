@@ -653,18 +653,26 @@ LF_DEVICE void combine(const int32_t *counts, const MoeDesc &d, uint8_t *ws, uin
   const float *w = at<float>(ws, L.topk_w) + static_cast<uint64_t>(t) * d.top_k;
   const int32_t *pos = at<int32_t>(ws, L.pos) + static_cast<uint64_t>(t) * d.top_k;
   const float *y = at<float>(ws, L.y);
-  // four columns per thread (H % 128 == 0); terms added in slot order j
+  // four columns per thread (H % 128 == 0); the k rows' loads are all issued
+  // before the sum, whose terms are added in slot order j
+  constexpr int kMaxK = 16;  // desc_ok bounds top_k
+  const int k = d.top_k;
   for (int c = 4 * threadIdx.x; c < H; c += 4 * blockDim.x) {
+    f32x4 v[kMaxK];
+    static_for<kMaxK>([&](auto j) {
+      if (j < k) v[j] = *reinterpret_cast<const f32x4 *>(y + static_cast<uint64_t>(pos[j]) * H + c);
+    });
     f32x4 acc = {0.f, 0.f, 0.f, 0.f};
-    for (int j = 0; j < d.top_k; ++j) {
-      const f32x4 v = *reinterpret_cast<const f32x4 *>(y + static_cast<uint64_t>(pos[j]) * H + c);
-      const float wj = w[j];
+    static_for<kMaxK>([&](auto j) {
+      if (j < k) {
+        const float wj = w[j];
 #pragma unroll
-      for (int q = 0; q < 4; ++q) {
-        const float prod = wj * v[q];
-        acc[q] = acc[q] + prod;
+        for (int q = 0; q < 4; ++q) {
+          const float prod = wj * v[j][q];
+          acc[q] = acc[q] + prod;
+        }
       }
-    }
+    });
     uint2 packed;
     packed.x = f32_to_bf16(acc[0]) | (f32_to_bf16(acc[1]) << 16);
     packed.y = f32_to_bf16(acc[2]) | (f32_to_bf16(acc[3]) << 16);

@@ -65,9 +65,12 @@ def test_e4m3_codes_decode_exactly_through_w8a16(rt):
     np.testing.assert_array_equal(o.bf16_decode(y[0]), o.e4m3_decode(codes))
 
 
-def test_act_quant_bit_exact(rt):
-    rng = np.random.default_rng(7)
-    m, k = 37, 1024
+@pytest.mark.parametrize("k", [1024, 6144, 14336, 20480])
+def test_act_quant_bit_exact(rt, k):
+    # k covers each register-resident row form (up to 4096, 8192, 16384
+    # columns) and the two-pass form beyond
+    rng = np.random.default_rng(7 + k)
+    m = 37
     x = synth.activations(rng, m, k)
     x[3] = 0                      # all-zero row: zero codes, zero scale
     x[5, 17] = synth.bf16_bits(np.array([3.0e4], np.float32))[0]   # dominant outlier
@@ -77,6 +80,30 @@ def test_act_quant_bit_exact(rt):
     q_ref, s_ref = o.quantize_rows(o.bf16_decode(x))
     np.testing.assert_array_equal(codes, q_ref)
     np.testing.assert_array_equal(scales, s_ref)
+
+
+def test_act_quant_every_bf16_value(rt):
+    # Rows whose amax is exactly 448 (ratio 1): together they hold every
+    # finite bf16 value of magnitude <= 448 with both signs, so the encode
+    # of each bf16 input (every tie between two e4m3 codes included) is
+    # compared with the oracle's.
+    k = 16384
+    mags = np.arange(0, 0x43E0 + 1, dtype=np.uint32).astype(np.uint16)   # 0 .. 448
+    vals = np.concatenate([mags, mags | np.uint16(0x8000)])
+    per_row = k - 1
+    rows = -(-len(vals) // per_row)
+    x = np.zeros((rows, k), np.uint16)
+    for r in range(rows):
+        chunk = vals[r * per_row:(r + 1) * per_row]
+        x[r, 0] = 0x43E0                     # 448: the row's amax
+        x[r, 1:1 + len(chunk)] = chunk
+    rng = np.random.default_rng(11)
+    _, _, w = make_weight(rt, rng, 16, k)
+    codes, scales = rt.act_quant(x, w, max_tokens=16)
+    q_ref, s_ref = o.quantize_rows(o.bf16_decode(x))
+    np.testing.assert_array_equal(scales, s_ref)
+    assert np.all(s_ref == np.float32(1.0))
+    np.testing.assert_array_equal(codes, q_ref)
 
 
 def test_golden_config1(rt):
