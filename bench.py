@@ -402,6 +402,36 @@ def summarize_traffic(fetch_csv, write_csv, kernel):
     }
 
 
+def summarize_trace(trace_csv, gap=32):
+    """Markdown table of a rocprofv3 kernel-trace CSV: one row per (kernel,
+    blocks, threads) with launches and average / min / max duration in us,
+    plus the average of each segment (dispatches of that key with at most
+    `gap` other dispatches between consecutive ones), which separates the
+    shapes the bench times one after another under the same kernel and grid."""
+    import csv
+    rows = list(csv.DictReader(open(trace_csv)))
+    rows.sort(key=lambda r: int(r["Start_Timestamp"]))
+    groups, last_seen = {}, {}
+    for i, r in enumerate(rows):
+        threads = int(r["Workgroup_Size_X"])
+        key = (r["Kernel_Name"], int(r["Grid_Size_X"]) // threads, threads)
+        us = (int(r["End_Timestamp"]) - int(r["Start_Timestamp"])) / 1000.0
+        segs = groups.setdefault(key, [])
+        if not segs or i - last_seen[key] > gap + 1:
+            segs.append([])
+        segs[-1].append(us)
+        last_seen[key] = i
+    out = ["| Kernel | Blocks | Threads | Launches | Average us | Min us | Max us | Segment averages us |",
+           "|---|---|---|---|---|---|---|---|"]
+    for key in sorted(groups):
+        segs = groups[key]
+        allv = [v for seg in segs for v in seg]
+        seg_avg = ", ".join(f"{sum(seg) / len(seg):.1f} ({len(seg)})" for seg in segs)
+        out.append(f"| {key[0]} | {key[1]} | {key[2]} | {len(allv)} | {sum(allv) / len(allv):.2f} | "
+                   f"{min(allv):.2f} | {max(allv):.2f} | {seg_avg} |")
+    return "\n".join(out)
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -415,7 +445,13 @@ def main():
     ap.add_argument("--summarize-traffic", nargs=2, metavar=("FETCH_CSV", "WRITE_CSV"),
                     help="print the traffic summary of the roofline kernel from the two "
                          "--pmc-pass counter CSVs (no GPU needed)")
+    ap.add_argument("--summarize-trace", metavar="KERNEL_TRACE_CSV",
+                    help="print a per-kernel markdown summary of a rocprofv3 kernel-trace CSV "
+                         "(no GPU needed)")
     args = ap.parse_args()
+    if args.summarize_trace:
+        print(summarize_trace(args.summarize_trace))
+        return
     if args.summarize_traffic:
         print(json.dumps(summarize_traffic(*args.summarize_traffic, roofline_kernel()), indent=1))
         return

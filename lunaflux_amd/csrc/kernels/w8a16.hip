@@ -701,7 +701,7 @@ __device__ __forceinline__ void w8a16_fixed_kernel(const int32_t *counts, const 
 // k-tiles is fully unrolled and branch-free and the compiler's s_waitcnt
 // counts are exact (see w8a16_fixed_kernel). The activation k-tile (16 MT
 // rows) is loaded cooperatively with row-coalesced 1 KiB loads into
-// registers (XI / WAVES loads per wave, DX k-tiles ahead), written to one of
+// registers (ceil(XI / WAVES) loads per wave, DX k-tiles ahead), written to one of
 // two LDS slots (chunk c of row r at c ^ (r & 15)), and shared by the block's
 // waves after one barrier per k-tile. The barrier waits only for LDS
 // writes (no memory fence), so the weight ring stays in flight across it.
@@ -717,10 +717,11 @@ __device__ __forceinline__ void w8a16_fixed_group_kernel(const int32_t *counts, 
   constexpr int EW = DW < NKT ? DW : NKT;
   constexpr int EX = DX < EW ? DX : EW;
   constexpr int XI = 4 * MT;
-  static_assert(XI % WAVES == 0 || WAVES % XI == 0, "activation loads split evenly");
-  // With more waves than loads, waves w and w + XI load (and write) the same
-  // rows: identical values, so the duplicate LDS writes are benign.
-  constexpr int XPW = XI >= WAVES ? XI / WAVES : 1;
+  // XPW = ceil(XI / WAVES) loads per wave, wave w taking loads w XPW .. + XPW
+  // - 1 modulo XI. Where the waves' loads overrun XI (more waves than loads,
+  // or XI not a multiple of WAVES) the later waves repeat the first rows:
+  // identical values, so the duplicate LDS writes are benign.
+  constexpr int XPW = (XI + WAVES - 1) / WAVES;
   static_assert(MODE != 1 || (NQ % 16 == 0 && NKV % 16 == 0 && NQ > 0 && NKV > 0), "qkv widths");
   constexpr int kSlot = 16 * MT * 16;  // 16-byte chunks per slot
   __shared__ __attribute__((aligned(16))) u32x4 xs[2 * kSlot];
