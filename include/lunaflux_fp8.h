@@ -187,11 +187,14 @@ int64_t lunaflux_fp8_qkv_w8a16_workspace_bytes(int64_t nq, int64_t nkv, int64_t 
  *  lf_moe_sort_count    (counts, desc, ws)
  *  lf_moe_sort          (counts, desc, ws)
  *  lf_moe_quant_tokens  (counts, desc, x bf16 [T, H], ws)
- *  lf_moe_gate_up[_b128|_t256](counts, desc, wg, wu, ws)
+ *  lf_moe_gate_up[_b128|_t256|_gemv](counts, desc, wg, wu, ws)
  *  lf_moe_quant_hidden  (counts, desc, ws)
- *  lf_moe_down[_b128|_t256]   (counts, desc, wd, ws)
+ *  lf_moe_down[_b128|_t256|_gemv]   (counts, desc, wd, ws)
  * (_t256: the per-channel GEMMs on 256 x 256 tiles, chosen by the launch
- * geometry for profiles that average >= 256 routed rows per expert.
+ * geometry for profiles that average >= 256 routed rows per expert; _gemv:
+ * either scale mode, chosen for profiles of at most 32 tokens, where the
+ * GEMMs stream the touched experts' weights: a fixed grid whose blocks
+ * loop over (expert with rows, 64-column group) items.
  * With per-token scales lf_moe_quant_tokens reads the sort's positions and
  * also writes each token's scale in expert order, so it runs after
  * lf_moe_sort.)
@@ -240,7 +243,8 @@ int64_t lunaflux_fp8_moe_workspace_bytes(const lf_fp8_moe_desc *desc,
  * top-k ids (int32 [T*k]), top-k weights (fp32 [T*k]), sorted assignments
  * (int32 [T*k]), position of each assignment (int32 [T*k]), expert row
  * offsets (int32 [E+1]), expert 128-row tile offsets (int32 [E+1]) followed
- * by the 256-row tile offsets (int32 [E+1]), e4m3
+ * by the 256-row tile offsets (int32 [E+1]), the number of experts with rows
+ * (int32) and their ids ascending (int32 [E]), e4m3
  * tokens [T, H], token scales, h bf16 [T*k, I], e4m3 h, h scales, y fp32
  * [T*k, H], end. */
 int32_t lunaflux_fp8_moe_workspace_layout(const lf_fp8_moe_desc *desc,

@@ -48,8 +48,9 @@ struct MoeLayout {
     sorted = o;   o = al256(o + A * 4);
     pos = o;      o = al256(o + A * 4);
     offsets = o;  o = al256(o + (d.experts + 1) * 4);
-    // 128-row tile prefix [E + 1], then the 256-row tile prefix [E + 1]
-    tiles = o;    o = al256(o + 2 * (d.experts + 1) * 4);
+    // 128-row tile prefix [E + 1], the 256-row tile prefix [E + 1], the
+    // number of experts with rows, then their ids ascending [E]
+    tiles = o;    o = al256(o + (3 * d.experts + 3) * 4);
     xq = o;       o = al256(o + static_cast<uint64_t>(T) * H);
     xs = o;       o = al256(o + static_cast<uint64_t>(T) * gx * 4);
     h = o;        o = al256(o + A * I * 2);
@@ -203,6 +204,7 @@ LF_DEVICE void sort_assignments(const int32_t *counts, const MoeDesc &d, uint8_t
         at<int32_t>(ws, L.tiles)[e] = 0;
         at<int32_t>(ws, L.tiles)[E + 1 + e] = 0;
       }
+      if (threadIdx.x == 0) at<int32_t>(ws, L.tiles)[2 * E + 2] = 0;  // no expert has rows
     }
     return;
   }
@@ -229,15 +231,17 @@ LF_DEVICE void sort_assignments(const int32_t *counts, const MoeDesc &d, uint8_t
   __syncthreads();
   if (tid == 0) {
     // Exclusive scans: first row, first 128-row tile and first 256-row tile
-    // of each expert.
-    int off = 0, tl = 0, tl2 = 0;
+    // of each expert; and the list of experts with rows.
+    int off = 0, tl = 0, tl2 = 0, live = 0;
     for (int e = 0; e < E; ++e) {
       const int n = wcnt[0][e];
       if (c == 0) {
         offsets[e] = off;
         tiles[e] = tl;
         tiles[E + 1 + e] = tl2;
+        if (n > 0) tiles[2 * E + 3 + live] = e;
       }
+      live += n > 0 ? 1 : 0;
       base[e] += off;
       off += n;
       tl += (n + w8a8::kBM - 1) / w8a8::kBM;
@@ -247,6 +251,7 @@ LF_DEVICE void sort_assignments(const int32_t *counts, const MoeDesc &d, uint8_t
       offsets[E] = off;
       tiles[E] = tl;
       tiles[E + 1 + E] = tl2;
+      tiles[2 * E + 2] = live;
     }
   }
   __syncthreads();
@@ -643,6 +648,223 @@ __device__ void grouped_gemm_t256(const int32_t *counts, const MoeDesc &d, const
   }
 }
 
+// --- grouped GEMV form ------------------------------------------------------------
+// Profiles of at most 32 tokens: every expert holds at most 32 rows (a token
+// picks an expert once), and the GEMMs are bound by streaming the touched
+// experts' weights, not by the matrix pipes. Work items are (expert with
+// rows, group of kGemvWaves consecutive 16-column tiles), from the sort's
+// list of experts with rows; a fixed grid of blocks loops over them (no
+// blocks for empty experts, whose dispatch slots would delay live ones). A
+// wave takes one tile of the item (for gate/up the gate and the up tile of
+// the same 16 h-columns) and streams it over all of K, kGemvRing k-tiles
+// ahead, against the expert's rows in 16-row chunks (an expert of more than
+// 16 rows re-reads its tiles from L2 for each further chunk), with
+// v_mfma_scale_f32_16x16x128_f8f6f4: a 128-deep k-tile is one MFMA and one
+// scale block, and a packed weight tile is its B operand as stored (lane l:
+// column l % 16, k = 32 (l / 16) + 0..31 from the two 1 KiB halves). Lane l
+// holds A row l % 16 of the chunk at the same k bytes, gathered through the
+// sorted ids for gate/up. Block scales: each k-tile's product is folded with
+// s_a[row][kt] (a per-wave LDS table, so no block barrier) and s_w[column
+// block][kt] (scalar loads); per-channel scales multiply the sums in the
+// epilogue. The weight loads of an item are issued first, the dependent
+// chain its activation rows need (offsets, sorted ids, scales) after them.
+constexpr int kGemvWaves = 4;
+constexpr int kGemvRing = 4;
+constexpr int kGemvRows = 16;
+
+// 16 bytes at base + off through a global-address-space pointer: a
+// global_load (vector-memory counter only) rather than a flat load, which
+// the compiler must also count as a possible LDS access and wait for as one.
+LF_DEVICE u32x4 gload16(const uint8_t *base, uint32_t off) {
+  typedef const __attribute__((address_space(1))) uint8_t gbyte;
+  typedef const __attribute__((address_space(1))) u32x4 gvec;
+  return *reinterpret_cast<gvec *>((gbyte *)base + off);
+}
+// A wave-uniform read-only float through the constant address space: a
+// scalar load.
+LF_DEVICE float sload(const float *p, int i) {
+  typedef const __attribute__((address_space(4))) float cfloat;
+  return ((cfloat *)p)[i];
+}
+
+template <int STAGE, bool BLOCK>
+LF_DEVICE void grouped_gemv(const int32_t *counts, const MoeDesc &d, const uint8_t *w0,
+                            const uint8_t *w1, uint8_t *ws) {
+  constexpr int NW = STAGE == 0 ? 2 : 1;
+  constexpr int D = kGemvRing;
+  // Block form: each wave's activation scales of its row chunk, [KT][16],
+  // KT <= 32 (the host rejects larger K for 128-column groups).
+  __shared__ __attribute__((aligned(16))) float sa_lds[BLOCK ? kGemvWaves * kGemvRows * 32 : 4];
+  const int Tn = live_rows(counts, 1 << 30);
+  if (Tn == 0) return;
+  const MoeLayout L(d, Tn);
+  const WeightHeader &h0 = header_of(w0);
+  const int K = static_cast<int>(h0.columns);
+  const int KT = K >> 7;
+  const int N = static_cast<int>(h0.rows);
+  if (BLOCK && KT > 32) return;
+  // Shapes the form is laid out for (the launch geometry only picks it for
+  // them): whole 4-tile column groups, and activation offsets that fit the
+  // 32-bit per-lane offsets of the loads.
+  const uint64_t a_rows = STAGE == 0 ? static_cast<uint64_t>(Tn) : static_cast<uint64_t>(Tn) * d.top_k;
+  if ((N & 63) != 0 || a_rows * static_cast<uint64_t>(K) >= (uint64_t(1) << 32)) return;
+  const int E = d.experts;
+  const int groups = (N >> 4) / kGemvWaves;
+  const int32_t *live = at<int32_t>(ws, L.tiles) + 2 * E + 2;  // [0]: count, then ids
+  const int items = live[0] * groups;
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int g = lane >> 4, r = lane & 15;
+  const int32_t *offsets = at<int32_t>(ws, L.offsets);
+  const int32_t *sorted = at<int32_t>(ws, L.sorted);
+  auto src_row = [&](int p) { return STAGE == 0 ? sorted[p] / d.top_k : p; };
+  const uint8_t *abase = uniform_ptr(at<uint8_t>(ws, STAGE == 0 ? L.xq : L.hq));
+  const float *ascales = at<float>(ws, STAGE == 0 ? L.xs : L.hs);
+  float *sa_wave = sa_lds + (BLOCK ? wave * kGemvRows * 32 : 0);
+
+  for (int item = blockIdx.x; item < items; item += gridDim.x) {
+    const int e = live[1 + item / groups];
+    const int nt = (item % groups) * kGemvWaves + wave;
+    const int col = nt * 16 + (lane & 15);
+    const uint8_t *region[NW];
+    region[0] = w0;
+    if constexpr (NW == 2) region[1] = w1;
+    // Uniform bases (scalar registers) with 32-bit per-lane offsets: the
+    // loads take the base + offset form instead of a 64-bit address each.
+    const uint8_t *strip[NW];
+    const float *wsc[NW], *wsc_blk[NW];
+#pragma unroll
+    for (int i = 0; i < NW; ++i) {
+      strip[i] = uniform_ptr(expert_tiles(region[i], e) + static_cast<uint64_t>(nt) * KT * kTileBytes);
+      wsc[i] = expert_scales(region[i], e);
+      // block form: the [KT] scales of this tile's 128-column block
+      wsc_blk[i] = uniform_ptr(wsc[i] + (BLOCK ? (nt >> 3) * KT : 0));
+    }
+    u32x4 bw[D][NW][2];
+    auto load_b = [&](int slot, int kt) {
+#pragma unroll
+      for (int i = 0; i < NW; ++i) {
+        const uint32_t o = static_cast<uint32_t>(kt) * kTileBytes + lane * 16;
+        bw[slot][i][0] = gload16(strip[i], o);
+        bw[slot][i][1] = gload16(strip[i], o + 1024);
+      }
+    };
+    const int p_first = offsets[e], pend = offsets[e + 1];
+    for (int c0 = p_first; c0 < pend; c0 += kGemvRows) {
+      const int rows = pend - c0 < kGemvRows ? pend - c0 : kGemvRows;
+      // the weight ring's first D k-tiles, then the activation chain
+      static_for<D>([&](auto j) { load_b(j, j < KT ? static_cast<int>(j) : KT - 1); });
+      __builtin_amdgcn_sched_barrier(0);
+      const int my_src = src_row(c0 + (r < rows ? r : 0));  // the source row of lane row r
+      const uint32_t aoff = static_cast<uint32_t>(my_src) * static_cast<uint32_t>(K) + 32 * g;
+      if constexpr (BLOCK) {
+        // This wave's table, [KT][16] (k-major, so a lane's 4 rows of one
+        // k-tile are one 16-byte read), zero for dead rows; the wave alone
+        // reads it, in order after its writes. Lane l fills row l % 16 at
+        // k-tiles l / 16 + 4 m: all its loads are issued together.
+        constexpr int kMaxPer = 8;  // KT <= 32
+        float v[kMaxPer];
+        const float *srow = ascales + static_cast<uint64_t>(my_src) * KT;
+        static_for<kMaxPer>([&](auto m) {
+          const int kg = g + 4 * m;
+          v[m] = srow[kg < KT ? kg : 0];
+        });
+        static_for<kMaxPer>([&](auto m) {
+          const int kg = g + 4 * m;
+          if (kg < KT) sa_wave[kg * 16 + r] = r < rows ? v[m] : 0.0f;
+        });
+      }
+      f32x4 acc[NW];
+#pragma unroll
+      for (int w = 0; w < NW; ++w) acc[w] = f32x4{0.f, 0.f, 0.f, 0.f};
+      // The k loop is branch-free (a branch in it makes the compiler wait
+      // for every outstanding load at each k-tile, which drains the ring).
+      u32x4 av[D][2];
+      auto load_a = [&](int slot, int kt) {
+        const uint32_t o = aoff + kt * 128;
+        av[slot][0] = gload16(abase, o);
+        av[slot][1] = gload16(abase, o + 16);
+      };
+      static_for<D>([&](auto j) { load_a(j, j < KT ? static_cast<int>(j) : KT - 1); });
+      // One k-tile of ring slot j: MFMA(s) on the slot, then its refill D
+      // k-tiles ahead (clamped to the last k-tile, so the loads are issued
+      // unconditionally and the compiler's vmcnt waits stay exact), in this
+      // order: sched_barrier keeps the scheduler from moving the refills,
+      // which would shorten the ring. A k-tile past K (the ring's tail in
+      // the runtime loop) re-reads the last one and contributes nothing: a
+      // select, not a branch.
+      auto k_step = [&](auto jc, int kt) {
+          constexpr int j = decltype(jc)::value;
+          const bool kt_live = kt < KT;
+          const int ktc = kt_live ? kt : KT - 1;
+          float swk[NW];
+          f32x4 sa4;
+          if constexpr (BLOCK) {
+#pragma unroll
+            for (int w = 0; w < NW; ++w) {
+              const float v = sload(wsc_blk[w], ktc);
+              swk[w] = kt_live ? v : 0.0f;
+            }
+            sa4 = *reinterpret_cast<const f32x4 *>(sa_wave + ktc * 16 + 4 * g);
+          }
+          const i32x8 af = __builtin_bit_cast(
+              i32x8, __builtin_shufflevector(av[j][0], av[j][1], 0, 1, 2, 3, 4, 5, 6, 7));
+#pragma unroll
+          for (int w = 0; w < NW; ++w) {
+            const i32x8 bf = __builtin_bit_cast(
+                i32x8, __builtin_shufflevector(bw[j][w][0], bw[j][w][1], 0, 1, 2, 3, 4, 5, 6, 7));
+            if constexpr (BLOCK) {
+              const f32x4 step = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(
+                  af, bf, f32x4{0.f, 0.f, 0.f, 0.f}, 0, 0, 0, 127, 0, 127);
+#pragma unroll
+              for (int q = 0; q < 4; ++q) acc[w][q] += step[q] * (sa4[q] * swk[w]);
+            } else {
+              const f32x4 next = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(
+                  af, bf, acc[w], 0, 0, 0, 127, 0, 127);
+#pragma unroll
+              for (int q = 0; q < 4; ++q) acc[w][q] = kt_live ? next[q] : acc[w][q];
+            }
+          }
+          __builtin_amdgcn_sched_barrier(0);
+          const int nk = kt + D < KT ? kt + D : KT - 1;
+          load_b(j, nk);
+          load_a(j, nk);
+          __builtin_amdgcn_sched_barrier(0);
+      };
+      // A runtime loop of D-step groups: the compiler waits for every
+      // outstanding load at the top of each group. (Unrolled over a
+      // compile-time K it keeps the ring full, but its register use grows
+      // with K: 256 VGPRs and AGPRs with spills at K = 4096.)
+      for (int k0 = 0; k0 < KT; k0 += D) {
+        static_for<D>([&](auto jc) { k_step(jc, k0 + decltype(jc)::value); });
+      }
+      // epilogue: lane holds rows 4 g + q of column col
+      float sw[NW];
+      if constexpr (!BLOCK) {
+#pragma unroll
+        for (int w = 0; w < NW; ++w) sw[w] = wsc[w][col];
+      }
+      const float *row_scales = at<float>(ws, L.hs);  // per-token scales in expert order
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        const int rr = 4 * g + q;
+        if (rr >= rows) continue;
+        const int p = c0 + rr;
+        const float sa = BLOCK ? 1.0f : row_scales[p];
+        if constexpr (STAGE == 0) {
+          const float gv = BLOCK ? acc[0][q] : acc[0][q] * sa * sw[0];
+          const float uv = BLOCK ? acc[1][q] : acc[1][q] * sa * sw[1];
+          at<uint16_t>(ws, L.h)[static_cast<uint64_t>(p) * N + col] =
+              static_cast<uint16_t>(f32_to_bf16(silu_mul(gv, uv)));
+        } else {
+          at<float>(ws, L.y)[static_cast<uint64_t>(p) * N + col] =
+              BLOCK ? acc[0][q] : acc[0][q] * sa * sw[0];
+        }
+      }
+    }
+  }
+}
+
 // --- combine -------------------------------------------------------------------
 LF_DEVICE void combine(const int32_t *counts, const MoeDesc &d, uint8_t *ws, uint16_t *out) {
   const int T = live_rows(counts, 1 << 30);
@@ -774,6 +996,27 @@ __global__ __launch_bounds__(512) void lf_moe_down_t256(const int32_t *counts,
   const MoeDesc &d = desc_of(desc);
   if (!desc_ok(d) || d.group != 0 || header_of(wd).magic != kWeightMagic) return;
   grouped_gemm_t256<1>(counts, d, wd, wd, ws);
+}
+
+// Small profiles (at most 32 tokens): the grouped GEMV form, either scale
+// mode (the descriptor's group).
+__global__ __launch_bounds__(256) void lf_moe_gate_up_gemv(const int32_t *counts,
+                                                           const int32_t *desc,
+                                                           const uint8_t *wg, const uint8_t *wu,
+                                                           uint8_t *ws) {
+  const MoeDesc &d = desc_of(desc);
+  if (!desc_ok(d) || header_of(wg).magic != kWeightMagic) return;
+  if (d.group == 0) grouped_gemv<0, false>(counts, d, wg, wu, ws);
+  else grouped_gemv<0, true>(counts, d, wg, wu, ws);
+}
+
+__global__ __launch_bounds__(256) void lf_moe_down_gemv(const int32_t *counts,
+                                                        const int32_t *desc, const uint8_t *wd,
+                                                        uint8_t *ws) {
+  const MoeDesc &d = desc_of(desc);
+  if (!desc_ok(d) || header_of(wd).magic != kWeightMagic) return;
+  if (d.group == 0) grouped_gemv<1, false>(counts, d, wd, wd, ws);
+  else grouped_gemv<1, true>(counts, d, wd, wd, ws);
 }
 
 // ... and 128 x 128 block weight scales with per-token-per-128-column

@@ -408,7 +408,7 @@ int32_t lunaflux_fp8_moe_workspace_layout(const lf_fp8_moe_desc *d, int32_t toke
       A * 4,                  // sorted assignments
       A * 4,                  // position of each assignment
       (d->experts + 1) * 4,   // expert row offsets
-      2 * (d->experts + 1) * 4,  // expert 128-row, then 256-row tile offsets
+      (3 * d->experts + 3) * 4,  // 128-row, 256-row tile offsets; live expert count, ids
       T * H,                  // quantized tokens
       T * gx * 4,             // token scales
       A * I * 2,              // h (bf16)
@@ -452,6 +452,11 @@ int32_t lunaflux_fp8_moe_launch_geometry(int32_t entry, const lf_fp8_moe_desc *d
   const bool t256 = !b128 && A >= 256 * static_cast<int64_t>(d->experts) &&
                     d->inter % 128 == 0 && d->hidden % 256 == 0;
   const int64_t tiles256 = A / 256 + d->experts;
+  // Profiles of at most 32 tokens (every expert <= 32 rows) run the grouped
+  // GEMV form: a fixed grid (up to 4 blocks per CU) whose blocks loop over
+  // the (expert with rows, 4 consecutive 16-column tiles) items.
+  const bool gemv = T <= 32 && d->inter % 64 == 0 && d->hidden % 64 == 0;
+  const int64_t kGemvBlocks = 1024;
   int64_t gx = 1, gy = 1;
   int32_t bx = 256;
   const char *name = nullptr;
@@ -467,6 +472,11 @@ int32_t lunaflux_fp8_moe_launch_geometry(int32_t entry, const lf_fp8_moe_desc *d
       gx = b128 ? group_quant_blocks(T * (d->hidden / 128)) : (T + 3) / 4;
       break;
     case LF_FP8_MOE_GATE_UP:
+      if (gemv) {
+        name = "lf_moe_gate_up_gemv";
+        gx = std::min<int64_t>(std::min<int64_t>(d->experts, A) * (d->inter / 64), kGemvBlocks);
+        break;
+      }
       // 1-D grid over (64 h-column block, 128-row tile); blocks past the
       // live tile count return.
       if (t256) {
@@ -483,6 +493,11 @@ int32_t lunaflux_fp8_moe_launch_geometry(int32_t entry, const lf_fp8_moe_desc *d
       gx = b128 ? group_quant_blocks(A * (d->inter / 128)) : (A + 3) / 4;
       break;
     case LF_FP8_MOE_DOWN:
+      if (gemv) {
+        name = "lf_moe_down_gemv";
+        gx = std::min<int64_t>(std::min<int64_t>(d->experts, A) * (d->hidden / 64), kGemvBlocks);
+        break;
+      }
       if (t256) {
         name = "lf_moe_down_t256";
         gx = d->hidden / 256 * tiles256;

@@ -148,6 +148,7 @@ def moe_expert_mlp(rt: ProjectionRuntime, x: np.ndarray, logits: np.ndarray, wg:
         offsets=ws.read(np.int32, (e + 1,), lay["offsets"]),
         tiles=ws.read(np.int32, (e + 1,), lay["tiles"]),
         tiles256=ws.read(np.int32, (e + 1,), lay["tiles"] + 4 * (e + 1)),
+        live_experts=ws.read(np.int32, (e + 1,), lay["tiles"] + 8 * (e + 1)),
         xq=ws.read(np.uint8, (t, hdim), lay["xq"]),
         xs=ws.read(np.float32, (t, gx), lay["xs"]),
         h=ws.read(np.uint16, (a, i), lay["h"]),

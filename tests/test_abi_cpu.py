@@ -39,7 +39,7 @@ def test_code_object_has_every_entry_point():
     for symbol in ["lf_fp8_act_quant_rows"] + [f"lf_fp8_w8a8_{op}_{t}" for op in ("dense", "qkv", "gate_up")
                                                for t in ("t128", "t256")] + ["lf_moe_route", "lf_moe_sort_count", "lf_moe_sort", "lf_moe_quant_tokens",
                    "lf_moe_gate_up", "lf_moe_gate_up_b128", "lf_moe_quant_hidden", "lf_moe_down",
-                   "lf_moe_down_b128", "lf_moe_combine"] + [f"lf_fp8_w8a16_{op}_m{m}" for op in ("dense", "qkv", "gate_up")
+                   "lf_moe_down_b128", "lf_moe_combine", "lf_moe_gate_up_gemv", "lf_moe_down_gemv"] + [f"lf_fp8_w8a16_{op}_m{m}" for op in ("dense", "qkv", "gate_up")
                                              for m in (16, 32, 64, 128)] + [
                    f"lf_fp8_w8a16_{op}_m16_t1" for op in ("dense", "qkv", "gate_up")] + [
                    f"lf_fp8_w8a16_dense_k{k}_m{m}" for k in (4096, 14336) for m in (16, 32)] + [
@@ -251,6 +251,19 @@ def test_moe_descriptor_layout_and_geometry():
     d5 = moe.moe_descriptor(64, 6, 1, 2048, 1408, 128)
     dims, sym = moe.launch_geometry(6, d5, 4096)  # down, block scales
     assert sym == "lf_moe_down_b128" and dims.grid == (2048 // 128 * (4096 * 6 // 128 + 64), 1, 1)
+    # profiles of at most 32 tokens: the grouped GEMV form, a block per
+    # (expert, 64 columns), either scale mode
+    # (a fixed grid of at most 1024 blocks looping over the items)
+    dims, sym = moe.launch_geometry(4, d5, 32)
+    assert sym == "lf_moe_gate_up_gemv" and dims.grid == (1024, 1, 1) and dims.block == (256, 1, 1)
+    dims, sym = moe.launch_geometry(6, d5, 32)
+    assert sym == "lf_moe_down_gemv" and dims.grid == (1024, 1, 1)
+    dims, sym = moe.launch_geometry(4, d, 16)
+    assert sym == "lf_moe_gate_up_gemv" and dims.grid == (1024, 1, 1)   # 8 x 224 items, capped
+    dims, sym = moe.launch_geometry(6, moe.moe_descriptor(8, 2, 0, 256, 384, 0), 1)
+    assert sym == "lf_moe_down_gemv" and dims.grid == (2 * 256 // 64, 1, 1)   # at most k experts
+    dims, sym = moe.launch_geometry(4, d5, 33)
+    assert sym == "lf_moe_gate_up_b128"
     for bad in [(0, 1, 0, 256, 256, 0), (8, 9, 0, 256, 256, 0), (8, 2, 2, 256, 256, 0),
                 (8, 2, 0, 200, 256, 0), (8, 2, 0, 256, 256, 64), (8, 2, 0, 8192, 256, 128)]:
         with pytest.raises(fp8.DeviceError):

@@ -72,6 +72,9 @@ def check_routing(logits, k, mode, st):
     counts = np.diff(offsets)
     np.testing.assert_array_equal(st["tiles"], np.concatenate([[0], np.cumsum((counts + 127) // 128)]))
     np.testing.assert_array_equal(st["tiles256"], np.concatenate([[0], np.cumsum((counts + 255) // 256)]))
+    live = np.flatnonzero(counts > 0)
+    assert st["live_experts"][0] == len(live)
+    np.testing.assert_array_equal(st["live_experts"][1:1 + len(live)], live)
     return ex, w
 
 
@@ -137,6 +140,33 @@ def test_moe_block128(rt, t, e, k, mode, max_tokens):
                                            max_tokens=max_tokens)
     ex, w = check_routing(logits, k, mode, st)
     check_output(x, weights, ex, w, out, True, f"moe block128 t={t} e={e} k={k}", st)
+
+
+@pytest.mark.parametrize("t,e,k,hidden,inter,block,one_expert", [
+    (32, 64, 6, 640, 1408, True, False), (32, 64, 6, 640, 1408, True, True),
+    (17, 8, 2, 256, 384, False, False), (32, 8, 2, 384, 256, False, True),
+    (3, 16, 4, 256, 640, True, False), (1, 4, 1, 256, 256, False, False),
+])
+def test_moe_gemv(rt, t, e, k, hidden, inter, block, one_expert):
+    """Profiles of at most 32 tokens run the grouped GEMV entries (either
+    scale mode): ragged expert loads, K of 2, 3, 5 and 11 k-tiles (not
+    multiples of the load ring), and every token on one expert (32 rows:
+    both 16-row fragments)."""
+    from lunaflux_amd import moe
+    d = moe.moe_descriptor(e, k, 1 if block else 0, hidden, inter, 128 if block else 0)
+    assert moe.launch_geometry(4, d, 32)[1] == "lf_moe_gate_up_gemv"
+    rng = np.random.default_rng(950 + t + e + hidden)
+    logits = None
+    if one_expert:
+        logits = rng.standard_normal((t, e)).astype(np.float32)
+        logits[:, 3] = 10.0
+    mode = 1 if block else 0
+    x, logits, weights, out, st = run_case(rt, rng, t, e, k, hidden, inter, mode, block=block,
+                                           logits=logits, max_tokens=32)
+    ex, w = check_routing(logits, k, mode, st)
+    if one_expert:
+        assert (ex[:, 0] == 3).all()
+    check_output(x, weights, ex, w, out, block, f"moe gemv t={t} e={e} k={k} block={block}", st)
 
 
 def test_moe_all_tokens_one_expert_and_ties(rt):
