@@ -336,12 +336,13 @@ struct BlockScaleFold {
   int KT, wm, lane;
   const float *sw[GemmTile::kFN];  // slot j: [KT] scales of its 128-column block
   template <class A>
-  LF_DEVICE void operator()(int kt, const A &step, A &acc) const {
+  LF_DEVICE void operator()(int kt, const A &step, A &acc, int live) const {
     float swk[GemmTile::kFN];
 #pragma unroll
     for (int j = 0; j < GemmTile::kFN; ++j) swk[j] = sw[j][kt];
 #pragma unroll
     for (int i = 0; i < GemmTile::kFM; ++i) {
+      if (i >= live) continue;  // a fragment with no live row
 #pragma unroll
       for (int rr = 0; rr < 4; ++rr) {
         const float sa = sa_lds[w8a8v3::acc_row<GemmTile>(wm, i, lane, rr) * KT + kt];
@@ -428,6 +429,9 @@ __device__ void grouped_gemm(const int32_t *counts, const MoeDesc &d, const uint
   }
 
   f32x4 acc[T::kFM][T::kFN];
+  // 16-row fragments of this wave with a live row (the rest are skipped)
+  const int wave_rows = pend - p0 - wm * T::kWaveM;
+  const int live_fm = wave_rows <= 0 ? 0 : (wave_rows >= T::kWaveM ? T::kFM : (wave_rows + 15) / 16);
   if constexpr (BLOCK) {
     // Activation scales of the block's rows: [128][KT] (zero for dead rows).
     for (int i = threadIdx.x; i < 128 * KT; i += blockDim.x) {
@@ -443,9 +447,9 @@ __device__ void grouped_gemm(const int32_t *counts, const MoeDesc &d, const uint
     // load here would make the loop wait for every outstanding stage load).
 #pragma unroll
     for (int j = 0; j < T::kFN; ++j) fold.sw[j] = uniform_ptr(wsc[j] + (col[j] >> 7) * KT);
-    w8a8v3::mainloop<T>(plan, KT, smem, acc, fold);
+    w8a8v3::mainloop<T, BlockScaleFold, true>(plan, KT, smem, acc, fold, live_fm);
   } else {
-    w8a8v3::mainloop<T>(plan, KT, smem, acc);
+    w8a8v3::mainloop<T, w8a8v3::NoFold, true>(plan, KT, smem, acc, w8a8v3::NoFold{}, live_fm);
   }
 
   const int r = lane & 15;

@@ -111,12 +111,20 @@ LF_DEVICE uint32_t lds_offset_of(const uint8_t *p) {
 struct NoFold {
   static constexpr bool kActive = false;
   template <class A>
-  LF_DEVICE void operator()(int, const A &, A &) const {}
+  LF_DEVICE void operator()(int, const A &, A &, int) const {}
 };
 
-template <class T, class Fold = NoFold>
+// SKIP: live_fm is how many of this wave's kFM 16-row fragments hold a live
+// row (wave-uniform); a wave with none skips its A reads, MFMAs and folds
+// (its accumulators are never stored). Skipping single fragments cost the
+// block-scaled kernel an occupancy step in registers, so the skip is per
+// wave. Only the grouped GEMMs, whose expert tiles are often partly past the
+// expert's last row, use it.
+template <class T, class Fold = NoFold, bool SKIP = false>
 __device__ void mainloop(const Plan<T> &plan, int KT, uint8_t *smem,
-                         f32x4 (&acc)[T::kFM][T::kFN], const Fold &fold = Fold{}) {
+                         f32x4 (&acc)[T::kFM][T::kFN], const Fold &fold = Fold{},
+                         int live_fm = T::kFM) {
+  const int live = __builtin_amdgcn_readfirstlane(live_fm);
   constexpr int NS = T::kStages;
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int wm = wave / T::kWgn, wn = wave % T::kWgn;
@@ -166,6 +174,7 @@ __device__ void mainloop(const Plan<T> &plan, int KT, uint8_t *smem,
       bf[j].h[0] = *reinterpret_cast<const uint4 *>(tile + lane * 16);
       bf[j].h[1] = *reinterpret_cast<const uint4 *>(tile + 1024 + lane * 16);
     }
+    if (SKIP && live == 0) continue;  // wave-uniform; stage bookkeeping is above
     f32x4 step[Fold::kActive ? T::kFM : 1][Fold::kActive ? T::kFN : 1];
 #pragma unroll
     for (int i = 0; i < T::kFM; ++i) {
@@ -184,7 +193,7 @@ __device__ void mainloop(const Plan<T> &plan, int KT, uint8_t *smem,
         }
       }
     }
-    if constexpr (Fold::kActive) fold(kt, step, acc);
+    if constexpr (Fold::kActive) fold(kt, step, acc, T::kFM);
   }
 }
 
