@@ -118,14 +118,20 @@ constexpr W8a16Fixed kW8a16Fixed[] = {
      "lf_fp8_w8a16_qkv_k4096_q4096_kv1024_m32"},
     {LF_FP8_ENTRY_W8A16_GATE_UP, 4096, 0, 0, 1, true, 2, 1, "lf_fp8_w8a16_gate_up_k4096_m16"},
     {LF_FP8_ENTRY_W8A16_GATE_UP, 4096, 0, 0, 2, true, 4, 1, "lf_fp8_w8a16_gate_up_k4096_m32"},
+    {LF_FP8_ENTRY_W8A16_DENSE, 4096, 0, 0, 8, true, 4, 4, "lf_fp8_w8a16_dense_k4096_m128"},
+    {LF_FP8_ENTRY_W8A16_DENSE, 14336, 0, 0, 8, true, 4, 4, "lf_fp8_w8a16_dense_k14336_m128"},
+    {LF_FP8_ENTRY_W8A16_QKV, 4096, 4096, 1024, 8, true, 4, 2,
+     "lf_fp8_w8a16_qkv_k4096_q4096_kv1024_m128"},
+    {LF_FP8_ENTRY_W8A16_GATE_UP, 4096, 0, 0, 8, true, 4, 1, "lf_fp8_w8a16_gate_up_k4096_m128"},
 };
 
 // The specialized entry for (entry, N, K, Q / K-V split, profile), or null.
 // nq = nkv = 0 when the split is unknown (QKV then never matches).
 const W8a16Fixed *w8a16_fixed(int32_t entry, int64_t n, int64_t k, int64_t nq, int64_t nkv,
                               int32_t max_tokens) {
-  if (max_tokens <= 0 || max_tokens > 32 || n <= 0 || n % 16 != 0) return nullptr;
-  const int mt = max_tokens <= 16 ? 1 : 2;
+  if (max_tokens <= 0 || max_tokens > 128 || n <= 0 || n % 16 != 0) return nullptr;
+  // the profile's 16-row fragments (profiles of 33..64 rows have no entries)
+  const int mt = max_tokens <= 16 ? 1 : max_tokens <= 32 ? 2 : max_tokens <= 64 ? 4 : 8;
   for (const W8a16Fixed &f : kW8a16Fixed) {
     if (f.entry != entry || f.k != k || f.mt != mt) continue;
     if (entry == LF_FP8_ENTRY_W8A16_QKV && (f.nq != nq || f.nkv != nkv || n != nq + 2 * nkv)) {

@@ -42,9 +42,9 @@ def test_code_object_has_every_entry_point():
                    "lf_moe_down_b128", "lf_moe_combine", "lf_moe_gate_up_gemv", "lf_moe_down_gemv"] + [f"lf_fp8_w8a16_{op}_m{m}" for op in ("dense", "qkv", "gate_up")
                                              for m in (16, 32, 64, 128)] + [
                    f"lf_fp8_w8a16_{op}_m16_t1" for op in ("dense", "qkv", "gate_up")] + [
-                   f"lf_fp8_w8a16_dense_k{k}_m{m}" for k in (4096, 14336) for m in (16, 32)] + [
-                   f"lf_fp8_w8a16_gate_up_k4096_m{m}" for m in (16, 32)] + [
-                   f"lf_fp8_w8a16_qkv_k4096_q4096_kv1024_m{m}" for m in (16, 32)]:
+                   f"lf_fp8_w8a16_dense_k{k}_m{m}" for k in (4096, 14336) for m in (16, 32, 128)] + [
+                   f"lf_fp8_w8a16_gate_up_k4096_m{m}" for m in (16, 32, 128)] + [
+                   f"lf_fp8_w8a16_qkv_k4096_q4096_kv1024_m{m}" for m in (16, 32, 128)]:
         assert symbol.encode() + b"\0" in image, symbol
 
 
@@ -113,6 +113,8 @@ def test_launch_geometry():
     assert sym == "lf_fp8_w8a16_gate_up_m32" and dims.grid == (224 * 2, 1, 1)
     dims, sym = fp8.launch_geometry(_abi.ENTRY_W8A16_QKV, 6144, 4096, 128)
     assert sym == "lf_fp8_w8a16_qkv_m128" and dims.grid == (96 * 5, 1, 1)
+    dims, sym = fp8.launch_geometry(_abi.ENTRY_W8A16_DENSE, 4096, 2048, 128)
+    assert sym == "lf_fp8_w8a16_dense_m128"   # no entry for this K
     # split-K workspace: S x (N / 16) x NW x MT 1 KiB fragments + one counter
     # per column group; 256 bytes (unused) without a split
     assert fp8.w8a16_workspace_bytes(_abi.ENTRY_W8A16_DENSE, 4096, 2048, 32) == 8 * 256 * 2 * 1024 + 256
@@ -148,6 +150,19 @@ def test_launch_geometry():
     assert sym == "lf_fp8_w8a16_qkv_m32"
     dims, sym = fp8.launch_geometry(_abi.ENTRY_W8A16_DENSE, 4096, 4096, 64)
     assert sym == "lf_fp8_w8a16_dense_m64"
+    # 128-row entries: column groups of 4 tiles over 4 (o, down), 2 (QKV) or
+    # 1 (gate/up) K slices
+    dims, sym = fp8.launch_geometry(_abi.ENTRY_W8A16_DENSE, 4096, 4096, 128)
+    assert sym == "lf_fp8_w8a16_dense_k4096_m128" and dims.grid == (64 * 4, 1, 1)
+    assert dims.block == (256, 1, 1)
+    assert fp8.w8a16_workspace_bytes(_abi.ENTRY_W8A16_DENSE, 4096, 4096, 128) == 4 * 256 * 8 * 1024 + 256
+    dims, sym = fp8.launch_geometry(_abi.ENTRY_W8A16_DENSE, 4096, 14336, 100)
+    assert sym == "lf_fp8_w8a16_dense_k14336_m128" and dims.grid == (64 * 4, 1, 1)
+    dims, sym = fp8.launch_geometry(_abi.ENTRY_W8A16_QKV, 6144, 4096, 128, qkv_split=(4096, 1024))
+    assert sym == "lf_fp8_w8a16_qkv_k4096_q4096_kv1024_m128" and dims.grid == (96 * 2, 1, 1)
+    dims, sym = fp8.launch_geometry(_abi.ENTRY_W8A16_GATE_UP, 14336, 4096, 128)
+    assert sym == "lf_fp8_w8a16_gate_up_k4096_m128" and dims.grid == (224, 1, 1)
+    assert fp8.w8a16_workspace_bytes(_abi.ENTRY_W8A16_GATE_UP, 14336, 4096, 128) == 256
     # the W8A8 QKV split variant picks the same entry as the plain call
     assert (fp8.launch_geometry(_abi.ENTRY_W8A8_QKV, 6144, 4096, 2048, qkv_split=(4096, 1024))[1]
             == fp8.launch_geometry(_abi.ENTRY_W8A8_QKV, 6144, 4096, 2048)[1])

@@ -311,12 +311,14 @@ def test_llama3_8b_shapes_sampled(rt, op, m, family):
     ("down", 5, 16), ("down", 20, 32), ("down", 32, 32),
     ("qkv", 1, 16), ("qkv", 13, 16), ("qkv", 32, 32),
     ("gate_up", 8, 16), ("gate_up", 25, 32), ("gate_up", 32, 32),
+    ("o", 128, 128), ("o", 70, 128), ("down", 128, 128), ("down", 97, 128),
+    ("qkv", 128, 128), ("qkv", 33, 128), ("gate_up", 128, 128), ("gate_up", 111, 128),
 ])
 def test_w8a16_specialized_entries(rt, op, m, max_tokens):
     """Every shape-specialized W8A16 entry (Llama-3-8B widths, profiles of
-    <= 16 and <= 32 rows) against the oracle on a column sample, with ragged
-    live rows and M = 0; the column-group forms (down, gate_up at 32 rows)
-    run three launches on one workspace, which must be bit-identical."""
+    <= 16, <= 32 and <= 128 rows) against the oracle on a column sample, with
+    ragged live rows and M = 0; the column-group forms run three launches on
+    one workspace, which must be bit-identical."""
     from lunaflux_amd import _abi, fp8
     from lunaflux_amd.fp8 import _region
     rng = np.random.default_rng(8100 + 97 * m + max_tokens + len(op))
@@ -359,7 +361,7 @@ def test_w8a16_specialized_entries(rt, op, m, max_tokens):
         cols = np.sort(rng.choice(n, 384, replace=False))
         ref = o.dense_projection(xr, deq(q[cols], s[cols]))
         extra = dict(k=k, s_abs=abs_sum(xr, deq(q[cols], s[cols])))
-    assert f"_k{k}_" in sym and sym.endswith(f"_m{16 if max_tokens <= 16 else 32}"), sym
+    assert f"_k{k}_" in sym and sym.endswith(f"_m{max_tokens}"), sym
     sentinel = np.full(max_tokens * n, 0x7FC1, np.uint16)  # a NaN no kernel writes
     ya.copy_from_host(sentinel)
     outs = []
