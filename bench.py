@@ -180,6 +180,47 @@ class Bench:
         return start.elapsed_milliseconds(stop) / launches
 
 
+VOCAB = 128256
+LM_HEAD_ROTATIONS = 4  # 4 x 525 MB head weights: 8x the MALL
+
+
+def lm_head_bench(rt, launches=20):
+    """The Llama-3 vocabulary head (4096 -> 128,256, the dense entry) at
+    decode sizes on the W8A16 family: average launch time over launches
+    rotating between LM_HEAD_ROTATIONS weight copies, and algorithmic GB/s.
+    The weight is a 2048-row draw tiled down the vocabulary (the values do
+    not change the kernel's time)."""
+    from lunaflux_amd import fp8, synth
+    from lunaflux_amd.fp8 import _region
+    rng = np.random.default_rng(31)
+    q0, s0 = synth.weight(rng, 2048, HIDDEN)
+    reps = VOCAB // 2048 + 1
+    region = fp8.pack_weight(np.tile(q0, (reps, 1))[:VOCAB], np.tile(s0, reps)[:VOCAB])
+    ws = [rt.weight_from_region(region) for _ in range(LM_HEAD_ROTATIONS)]
+    del region
+    ctx, stream = rt.context, rt.stream
+    out = {}
+    for m, mt in [(1, 16), (8, 16), (32, 32), (128, 128)]:
+        x = ctx.upload(synth.activations(rng, mt, HIDDEN))
+        y = ctx.allocate(mt * VOCAB * 2)
+        counts = rt.step_counts(m)
+        ops = [rt.bind_dense("w8a16", counts, _region(x, alignment=256), w,
+                             _region(y, alignment=256), mt) for w in ws]
+        for i in range(5):
+            ops[i % len(ops)].launch(stream, synchronous=False)
+        start, stop = ctx.create_event(), ctx.create_event()
+        start.record(stream)
+        for i in range(launches):
+            ops[i % len(ops)].launch(stream, synchronous=False)
+        stop.record(stream)
+        stop.synchronize()
+        us = start.elapsed_milliseconds(stop) / launches * 1e3
+        gbs = call_bytes(m, HIDDEN, VOCAB, VOCAB) / (us * 1e-6) / 1e9
+        out[f"M={m}"] = {"us": round(us, 2), "GB/s": round(gbs, 1),
+                         "hbm_frac": round(gbs / HBM_PEAK_GBS, 4), "kernel": ops[0].steps[-1].name}
+    return out
+
+
 def cpu_baseline(m=32, threads=None):
     """The CPU oracle on this host: the four decode calls of one layer at
     M=m over dequantized fp32 weights (sequential-K fp32, as the reference),
@@ -500,6 +541,8 @@ def main():
             row["layer_hbm_frac"] = round(row["layer_GB/s"] / HBM_PEAK_GBS, 4)
             detail["decode_w8a16"][f"M={mm}"] = row
             log(f"decode M={mm}: {row}")
+        detail["lm_head_w8a16"] = lm_head_bench(rt)
+        log(f"lm head: {detail['lm_head_w8a16']}")
         for mm in (2048, 8192):
             b = Bench(rt, layer, mm, "w8a8")
             row = {}

@@ -915,6 +915,12 @@ LF_W8A16_TILE_ENTRIES(1, 16, 1)
       const int32_t *counts, const uint16_t *x, const uint8_t *w, uint16_t *y, uint8_t *ws) { \
     w8a16_fixed_group_kernel<KK, S, W, MT, 0, DW, DX>(counts, x, w, w, w, y, ws);             \
   }
+// Wide dense shapes (the vocabulary head): unsplit column groups.
+#define LF_W16_FIXED_DENSE_WIDE_G(KK, M, MT, S, W, DW, DX)                                      \
+  __global__ __launch_bounds__(W * 64) void lf_fp8_w8a16_dense_wide_k##KK##_m##M(            \
+      const int32_t *counts, const uint16_t *x, const uint8_t *w, uint16_t *y, uint8_t *ws) { \
+    w8a16_fixed_group_kernel<KK, S, W, MT, 0, DW, DX>(counts, x, w, w, w, y, ws);             \
+  }
 #define LF_W16_FIXED_GATE_UP_G(KK, M, MT, S, W, DW, DX)                                         \
   __global__ __launch_bounds__(W * 64) void lf_fp8_w8a16_gate_up_k##KK##_m##M(               \
       const int32_t *counts, const uint16_t *x, const uint8_t *wg, const uint8_t *wu,        \
@@ -936,5 +942,10 @@ LF_W16_FIXED_DENSE_G(4096, 128, 8, 4, 4, 2, 1)
 LF_W16_FIXED_DENSE_G(14336, 128, 8, 4, 4, 2, 1)
 LF_W16_FIXED_QKV_G(4096, 4096, 1024, 128, 8, 2, 4, 2, 1)
 LF_W16_FIXED_GATE_UP_G(4096, 128, 8, 1, 4, 2, 1)
+// N >= 16384 (e.g. the 128,256-wide vocabulary head): enough 16-column
+// tiles to fill the chip without a K split, as gate/up.
+LF_W16_FIXED_DENSE_WIDE_G(4096, 16, 1, 1, 2, 4, 2)
+LF_W16_FIXED_DENSE_WIDE_G(4096, 32, 2, 1, 4, 3, 2)
+LF_W16_FIXED_DENSE_WIDE_G(4096, 128, 8, 1, 4, 2, 1)
 
 }  // extern "C"

@@ -106,8 +106,13 @@ struct W8a16Fixed {
   bool group;       // column-group form
   int waves, split;
   const char *symbol;
+  int64_t min_n = 0;  // chosen only for N >= min_n (earlier rows win)
 };
+constexpr int64_t kWideN = 16384;
 constexpr W8a16Fixed kW8a16Fixed[] = {
+    {LF_FP8_ENTRY_W8A16_DENSE, 4096, 0, 0, 1, true, 2, 1, "lf_fp8_w8a16_dense_wide_k4096_m16", kWideN},
+    {LF_FP8_ENTRY_W8A16_DENSE, 4096, 0, 0, 2, true, 4, 1, "lf_fp8_w8a16_dense_wide_k4096_m32", kWideN},
+    {LF_FP8_ENTRY_W8A16_DENSE, 4096, 0, 0, 8, true, 4, 1, "lf_fp8_w8a16_dense_wide_k4096_m128", kWideN},
     {LF_FP8_ENTRY_W8A16_DENSE, 4096, 0, 0, 1, false, 8, 1, "lf_fp8_w8a16_dense_k4096_m16"},
     {LF_FP8_ENTRY_W8A16_DENSE, 4096, 0, 0, 2, false, 8, 1, "lf_fp8_w8a16_dense_k4096_m32"},
     {LF_FP8_ENTRY_W8A16_DENSE, 14336, 0, 0, 1, false, 8, 1, "lf_fp8_w8a16_dense_k14336_m16"},
@@ -133,7 +138,7 @@ const W8a16Fixed *w8a16_fixed(int32_t entry, int64_t n, int64_t k, int64_t nq, i
   // the profile's 16-row fragments (profiles of 33..64 rows have no entries)
   const int mt = max_tokens <= 16 ? 1 : max_tokens <= 32 ? 2 : max_tokens <= 64 ? 4 : 8;
   for (const W8a16Fixed &f : kW8a16Fixed) {
-    if (f.entry != entry || f.k != k || f.mt != mt) continue;
+    if (f.entry != entry || f.k != k || f.mt != mt || n < f.min_n) continue;
     if (entry == LF_FP8_ENTRY_W8A16_QKV && (f.nq != nq || f.nkv != nkv || n != nq + 2 * nkv)) {
       continue;
     }

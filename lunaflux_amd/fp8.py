@@ -313,6 +313,15 @@ class ProjectionRuntime:
         return self._run(lambda c, xr, yr, mt: self.bind_dense(family, c, xr, w, yr, mt),
                          x, (x.shape[0], w.rows), max_tokens)
 
+    def language_model_head(self, x, w: Fp8Weight, family="w8a16", max_tokens=None):
+        """Vocabulary logits [M, vocab] in bf16: the dense projection entry
+        over the head weight [vocab, hidden], as the reference's
+        `language_model_head` is `dense_projection`
+        (kernels/reference/basic.mbt:175-181) and the catalog binds
+        LanguageModelHead to the dense-projection capability
+        (kernels/catalog/entry.mbt:92-93)."""
+        return self.dense_projection(x, w, family, max_tokens)
+
     def qkv_projection(self, x, wq, wk, wv, family="w8a16", max_tokens=None):
         n = wq.rows + wk.rows + wv.rows
         return self._run(lambda c, xr, yr, mt: self.bind_qkv(family, c, xr, wq, wk, wv, yr, mt),

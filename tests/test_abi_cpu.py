@@ -44,7 +44,8 @@ def test_code_object_has_every_entry_point():
                    f"lf_fp8_w8a16_{op}_m16_t1" for op in ("dense", "qkv", "gate_up")] + [
                    f"lf_fp8_w8a16_dense_k{k}_m{m}" for k in (4096, 14336) for m in (16, 32, 128)] + [
                    f"lf_fp8_w8a16_gate_up_k4096_m{m}" for m in (16, 32, 128)] + [
-                   f"lf_fp8_w8a16_qkv_k4096_q4096_kv1024_m{m}" for m in (16, 32, 128)]:
+                   f"lf_fp8_w8a16_qkv_k4096_q4096_kv1024_m{m}" for m in (16, 32, 128)] + [
+                   f"lf_fp8_w8a16_dense_wide_k4096_m{m}" for m in (16, 32, 128)]:
         assert symbol.encode() + b"\0" in image, symbol
 
 
@@ -162,6 +163,13 @@ def test_launch_geometry():
     assert sym == "lf_fp8_w8a16_qkv_k4096_q4096_kv1024_m128" and dims.grid == (96 * 2, 1, 1)
     dims, sym = fp8.launch_geometry(_abi.ENTRY_W8A16_GATE_UP, 14336, 4096, 128)
     assert sym == "lf_fp8_w8a16_gate_up_k4096_m128" and dims.grid == (224, 1, 1)
+    # wide dense shapes (N >= 16384, e.g. the 128,256-column vocabulary head)
+    for mt, w in ((16, 2), (32, 4), (128, 4)):
+        dims, sym = fp8.launch_geometry(_abi.ENTRY_W8A16_DENSE, 128256, 4096, mt)
+        assert sym == f"lf_fp8_w8a16_dense_wide_k4096_m{mt}" and dims.grid == (8016 // w, 1, 1)
+        assert dims.block == (64 * w, 1, 1)
+        assert fp8.w8a16_workspace_bytes(_abi.ENTRY_W8A16_DENSE, 128256, 4096, mt) == 256
+    assert fp8.launch_geometry(_abi.ENTRY_W8A16_DENSE, 16368, 4096, 32)[1] == "lf_fp8_w8a16_dense_k4096_m32"
     assert fp8.w8a16_workspace_bytes(_abi.ENTRY_W8A16_GATE_UP, 14336, 4096, 128) == 256
     # the W8A8 QKV split variant picks the same entry as the plain call
     assert (fp8.launch_geometry(_abi.ENTRY_W8A8_QKV, 6144, 4096, 2048, qkv_split=(4096, 1024))[1]

@@ -376,6 +376,42 @@ def test_w8a16_specialized_entries(rt, op, m, max_tokens):
     assert all(np.array_equal(outs[0], y) for y in outs[1:]), f"{sym}: launches differ"
 
 
+def lm_head_weight(rt, rng, vocab, k):
+    """A [vocab, k] head weight: a 2048-row N(0, 0.02) draw tiled down the
+    vocabulary (drawing 525 M values would take most of the test's time),
+    each copy's scales multiplied by its own factor so tiles differ."""
+    q0, s0 = synth.weight(rng, 2048, k)
+    reps = -(-vocab // 2048)
+    q = np.tile(q0, (reps, 1))[:vocab]
+    s = (np.tile(s0, reps) * np.repeat(np.linspace(0.5, 1.5, reps, dtype=np.float32), 2048))[:vocab]
+    return q, s.astype(np.float32), rt.upload_weight(q, s.astype(np.float32))
+
+
+@pytest.mark.parametrize("m,max_tokens,family", [(1, 16, "w8a16"), (13, 16, "w8a16"),
+                                                (32, 32, "w8a16"), (100, 128, "w8a16"),
+                                                (256, 256, "w8a8")])
+def test_language_model_head(rt, m, max_tokens, family):
+    """Llama-3 vocabulary head (hidden 4096 -> 128,256 logits = 8016
+    16-column tiles, 501 256-column tiles): the dense entry at the widest
+    shape it serves, checked on a column sample that includes the last 64
+    columns, and for W8A16 on the K = 4096 wide-shape entries."""
+    from lunaflux_amd import _abi, fp8
+    vocab, k = 128256, 4096
+    rng = np.random.default_rng(9100 + m)
+    q, s, w = lm_head_weight(rt, rng, vocab, k)
+    x = synth.activations(rng, m, k)
+    if family == "w8a16":
+        sym = fp8.launch_geometry(_abi.ENTRY_W8A16_DENSE, vocab, k, max_tokens)[1]
+        assert sym == f"lf_fp8_w8a16_dense_wide_k4096_m{max_tokens}", sym
+    y = rt.language_model_head(x, w, family=family, max_tokens=max_tokens)
+    assert y.shape == (m, vocab)
+    cols = np.concatenate([np.sort(rng.choice(vocab - 64, 448, replace=False)),
+                           np.arange(vocab - 64, vocab)])
+    rows = np.arange(m) if m <= 128 else np.sort(rng.choice(m, 64, replace=False))
+    check_projection(y[rows][:, cols], x_ref(x, family)[rows], deq(q[cols], s[cols]),
+                     f"lm_head {family} m={m}")
+
+
 def test_w8a16_specialized_entry_rejects_other_shape(rt):
     """A specialized entry checks the header against its compiled shape: a
     K = 8192 weight region launched on the K = 4096 dense entry (its reads
