@@ -180,6 +180,40 @@ class Bench:
         return start.elapsed_milliseconds(stop) / launches
 
 
+def rms_norm_quant_bench(rt, bench, m, launches=20):
+    """The fused RmsNorm + per-token quantizer (eps 1e-5, K = 4096, the input
+    of qkv and gate/up) at prefill size m: average launch time, rotating over
+    enough bf16 input copies (>= 1 GB) that the MALL cannot serve them, and
+    GB/s of algorithmic bytes (2 M K read + 2 K norm weight + M K codes + 4 M
+    scales)."""
+    from lunaflux_amd import synth
+    from lunaflux_amd.fp8 import _region, act_quant_bytes
+    ctx, stream = rt.context, rt.stream
+    rng = np.random.default_rng(55)
+    copies = min(32, max(2, -(-(1 << 30) // (2 * m * HIDDEN))))
+    x0 = synth.activations(rng, m, HIDDEN)
+    xs = [ctx.upload(x0) for _ in range(copies)]
+    g = ctx.upload(synth.bf16_bits(rng.uniform(0.5, 1.5, HIDDEN).astype(np.float32)))
+    xq = ctx.allocate(act_quant_bytes(m, HIDDEN))
+    counts = rt.step_counts(m, decode=False)
+    w = bench.layer.w("q", 0)
+    steps = [rt.bind_rms_norm_quant(counts, _region(x, alignment=256), _region(g), w,
+                                    _region(xq, alignment=256), m, 1e-5) for x in xs]
+    for i in range(3):
+        steps[i % copies].launch(stream, synchronous=False)
+    start, stop = ctx.create_event(), ctx.create_event()
+    start.record(stream)
+    for i in range(launches):
+        steps[i % copies].launch(stream, synchronous=False)
+    stop.record(stream)
+    stop.synchronize()
+    us = start.elapsed_milliseconds(stop) / launches * 1e3
+    nbytes = 3 * m * HIDDEN + 2 * HIDDEN + 4 * m
+    return {"us": round(us, 1), "GB/s": round(nbytes / (us * 1e-6) / 1e9, 1),
+            "hbm_frac": round(nbytes / (us * 1e-6) / 1e9 / HBM_PEAK_GBS, 4),
+            "kernel": steps[0].name}
+
+
 VOCAB = 128256
 LM_HEAD_ROTATIONS = 4  # 4 x 525 MB head weights: 8x the MALL
 
@@ -554,6 +588,7 @@ def main():
                           "fp8_frac": round(tf / FP8_PEAK_TFLOPS, 4),
                           "act_quant_us": round(q * 1e3, 1),
                           "act_quant_GB/s": round(mm * k * 3 / (q * 1e-3) / 1e9, 1)}
+            row["rms_norm_quant_k4096"] = rms_norm_quant_bench(rt, b, mm)
             detail["prefill_w8a8"][f"M={mm}"] = row
             log(f"prefill M={mm}: {row}")
             del b

@@ -141,7 +141,8 @@ enum lf_fp8_entry {
   LF_FP8_ENTRY_W8A16_GATE_UP = 4,
   LF_FP8_ENTRY_W8A8_DENSE = 5,
   LF_FP8_ENTRY_W8A8_QKV = 6,
-  LF_FP8_ENTRY_W8A8_GATE_UP = 7
+  LF_FP8_ENTRY_W8A8_GATE_UP = 7,
+  LF_FP8_ENTRY_RMS_NORM_QUANT_ROWS = 8
 };
 
 /* Launch geometry a manifest records for (entry, output width N, input width
@@ -166,6 +167,29 @@ int32_t lunaflux_fp8_qkv_launch_geometry(int32_t entry, int64_t nq, int64_t nkv,
                                          char symbol[LF_FP8_SYMBOL_BYTES]);
 int64_t lunaflux_fp8_qkv_w8a16_workspace_bytes(int64_t nq, int64_t nkv, int64_t k,
                                                int32_t max_tokens);
+
+/* RmsNorm fused with the per-token quantizer: the RmsNorm operation
+ * (kernels/reference/basic.mbt:32-68; catalog capability rms_norm,
+ * kernels/catalog/entry.mbt:60,79) writing its output as the xq region the
+ * W8A8 projection after it reads, in place of a bf16 activation plus an
+ * lf_fp8_act_quant_rows launch.
+ *  lf_fp8_rms_norm_quant_rows_eps1em5 / _eps1em6
+ *      (counts, x, g, w, xq)   x bf16 [M, K]; g bf16 [K] (the norm weight's
+ *                              TensorRef region); w the first weight of the
+ *                              projection fed (K is read from its header,
+ *                              K <= 8192); xq as for lf_fp8_act_quant_rows.
+ * Per row: inv = 1 / sqrt(sum_k x^2 / K + eps), y = (x * inv) * g in fp32,
+ * then the quantizer's codes and scale of y. The sum of squares is reduced
+ * across a wavefront (not the reference's sequential order), so results
+ * match the reference to fp32 rounding of inv, not bit for bit.
+ * The epsilon is part of the operation shape (model/plan/plan.mbt:146-151),
+ * so each value is its own entry: geometry and symbol for (epsilon, K,
+ * max_rows); LF_UNSUPPORTED for an epsilon with no entry (1e-5 and 1e-6 as
+ * fp32 are built). lunaflux_fp8_launch_geometry rejects this entry
+ * (LF_INVALID_ARGUMENT), as it carries no epsilon. */
+int32_t lunaflux_fp8_rms_norm_quant_geometry(float epsilon, int64_t k, int32_t max_rows,
+                                             int32_t dims[7],
+                                             char symbol[LF_FP8_SYMBOL_BYTES]);
 
 /* ---- grouped form: MoE expert MLP ---------------------------------------- */
 /*

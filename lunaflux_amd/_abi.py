@@ -47,6 +47,7 @@ ENTRY_W8A16_GATE_UP = 4
 ENTRY_W8A8_DENSE = 5
 ENTRY_W8A8_QKV = 6
 ENTRY_W8A8_GATE_UP = 7
+ENTRY_RMS_NORM_QUANT_ROWS = 8
 
 _vp = ctypes.c_void_p
 _i32 = ctypes.c_int32
@@ -101,6 +102,8 @@ SIGNATURES = {
     "lunaflux_fp8_qkv_launch_geometry": (_i32, [_i32, _i64, _i64, _i64, _i32, _i32p,
                                                 ctypes.c_char_p]),
     "lunaflux_fp8_qkv_w8a16_workspace_bytes": (_i64, [_i64, _i64, _i64, _i32]),
+    "lunaflux_fp8_rms_norm_quant_geometry": (_i32, [ctypes.c_float, _i64, _i32, _i32p,
+                                                    ctypes.c_char_p]),
     "lunaflux_fp8_moe_descriptor": (_i32, [_i32, _i32, _i32, _i64, _i64, _i32, _vp]),
     "lunaflux_fp8_moe_workspace_bytes": (_i64, [_vp, _i32]),
     "lunaflux_fp8_moe_workspace_layout": (_i32, [_vp, _i32, _i64p]),

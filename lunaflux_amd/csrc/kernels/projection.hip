@@ -179,6 +179,120 @@ LF_DEVICE void act_quant_rows(const int32_t *counts, const uint16_t *x, const ui
 }
 
 // ---------------------------------------------------------------------------
+// RmsNorm fused with the per-token quantizer (kernels/reference/basic.mbt:
+// 32-68, then the quantizer above on the fp32 result): for row r
+//   ss  = sum_k x[r, k]^2    fp32: each lane sums its own values in column
+//                            order, then a xor butterfly across the wave
+//   inv = 1 / sqrt(ss / K + eps)      correctly rounded sqrt and division, as
+//                                     the reference's fp32 operations
+//   y_k = (x[r, k] * inv) * g[k]      the reference's left-to-right order
+// and the codes and scale of y as the quantizer forms them (amax, ratio =
+// 448 / amax, e4m3_rne_sat(y * ratio), scale = amax / 448). Only the order of
+// the sum of squares differs from the reference's sequential loop. A row whose
+// sum of squares overflows (the reference raises NonFinite) gets inv = 0,
+// hence zero codes and scale 0. One wave per row, register-resident as the
+// quantizer: the row and the norm weight stay in registers (rows of up to
+// 8192 columns).
+// ---------------------------------------------------------------------------
+LF_DEVICE float wave_sum(float v) {
+#pragma unroll
+  for (int offset = 32; offset > 0; offset >>= 1) v += __shfl_xor(v, offset);
+  return v;
+}
+
+LF_DEVICE float rms_scaled(uint32_t xbits, uint32_t gbits, float inv) {
+  return __fmul_rn(__fmul_rn(bf16_to_f32(xbits), inv), bf16_to_f32(gbits));
+}
+
+// Four normalized values (x words x0, x1 and norm-weight words g0, g1) times
+// ratio -> four e4m3 codes, element j in byte j.
+LF_DEVICE uint32_t e4m3x4_from_norm(uint32_t x0, uint32_t x1, uint32_t g0, uint32_t g1, float inv,
+                                    float ratio) {
+  int p = __builtin_amdgcn_cvt_pk_fp8_f32(rms_scaled(x0 & 0xffffu, g0 & 0xffffu, inv) * ratio,
+                                          rms_scaled(x0 >> 16, g0 >> 16, inv) * ratio, 0, false);
+  p = __builtin_amdgcn_cvt_pk_fp8_f32(rms_scaled(x1 & 0xffffu, g1 & 0xffffu, inv) * ratio,
+                                      rms_scaled(x1 >> 16, g1 >> 16, inv) * ratio, p, true);
+  return static_cast<uint32_t>(p);
+}
+
+template <int C>
+LF_DEVICE void rms_norm_quant_row_wave(const uint16_t *x_row, const uint16_t *gamma, int K,
+                                       float eps, uint8_t *dst_row, float *scale) {
+  const int lane = threadIdx.x & 63;
+  const int chunks = K >> 3;
+  const u32x4 *src = reinterpret_cast<const u32x4 *>(x_row);
+  const u32x4 *gsrc = reinterpret_cast<const u32x4 *>(gamma);
+  u32x4 v[C], g[C];
+  static_for<C>([&](auto c) {
+    const int idx = lane + 64 * c;
+    v[c] = idx < chunks ? src[idx] : u32x4{0u, 0u, 0u, 0u};
+    g[c] = idx < chunks ? gsrc[idx] : u32x4{0u, 0u, 0u, 0u};
+  });
+  float ss = 0.0f;
+  static_for<C>([&](auto c) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const float lo = bf16_to_f32(v[c][i] & 0xffffu), hi = bf16_to_f32(v[c][i] >> 16);
+      ss = __fadd_rn(ss, __fmul_rn(lo, lo));
+      ss = __fadd_rn(ss, __fmul_rn(hi, hi));
+    }
+  });
+  static_for<C>([&](auto c) { opaque(v[c]); });  // no x floats kept across passes
+  ss = wave_sum(ss);
+  // __builtin_sqrtf and '/' are the correctly rounded IEEE operations (hipcc's
+  // default fp32 division and sqrt lowering); HIP's __fsqrt_rn is the native
+  // approximate v_sqrt_f32 unless OCML's rounded operations are enabled.
+  const float root = __builtin_sqrtf(__fadd_rn(ss / static_cast<float>(K), eps));
+  const float inv = isinf(ss) ? 0.0f : 1.0f / root;
+  float amax = 0.0f;
+  static_for<C>([&](auto c) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      amax = fmaxf(amax, fabsf(rms_scaled(v[c][i] & 0xffffu, g[c][i] & 0xffffu, inv)));
+      amax = fmaxf(amax, fabsf(rms_scaled(v[c][i] >> 16, g[c][i] >> 16, inv)));
+    }
+  });
+  amax = wave_max(amax);
+  const bool zero = amax == 0.0f;
+  const float ratio = zero ? 0.0f : 448.0f / amax;
+  typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+  u32x2 *dst = reinterpret_cast<u32x2 *>(dst_row);
+  // As in the quantizer, the encode converts the raw words again (the empty
+  // asms keep the compiler from holding the 8 C products).
+  static_for<C>([&](auto c) { opaque(v[c]); });
+  static_for<C>([&](auto c) { opaque(g[c]); });
+  static_for<C>([&](auto c) {
+    const int idx = lane + 64 * c;
+    const uint32_t lo = e4m3x4_from_norm(v[c][0], v[c][1], g[c][0], g[c][1], inv, ratio);
+    const uint32_t hi = e4m3x4_from_norm(v[c][2], v[c][3], g[c][2], g[c][3], inv, ratio);
+    if (idx < chunks) dst[idx] = u32x2{zero ? 0u : lo, zero ? 0u : hi};
+  });
+  if (lane == 0) *scale = zero ? 0.0f : amax / 448.0f;
+}
+
+// One wave per row, four rows per block; K from the header of w (the first
+// weight of the projection the quantized rows feed), at most 8192.
+LF_DEVICE void rms_norm_quant_rows(const int32_t *counts, const uint16_t *x,
+                                   const uint16_t *gamma, const uint8_t *w, uint8_t *xq,
+                                   float eps) {
+  const WeightHeader &h = header_of(w);
+  if (h.magic != kWeightMagic) return;
+  const int K = static_cast<int>(h.columns);
+  if (K > 8192) return;
+  const int M = live_rows(counts, 1 << 30);
+  const int row = blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (row >= M) return;
+  float *scales = reinterpret_cast<float *>(xq + align256(static_cast<uint64_t>(M) * K));
+  const uint16_t *src = x + static_cast<uint64_t>(row) * K;
+  uint8_t *dst = xq + static_cast<uint64_t>(row) * K;
+  if (K <= 4096) {
+    rms_norm_quant_row_wave<8>(src, gamma, K, eps, dst, scales + row);
+  } else {
+    rms_norm_quant_row_wave<16>(src, gamma, K, eps, dst, scales + row);
+  }
+}
+
+// ---------------------------------------------------------------------------
 // W8A8 GEMM: xq [M, K] e4m3 with per-token scales (the quantizer's output) x
 // weights with per-channel scales, y = bf16(acc * sa[m] * sw[n]). MODE 0:
 // dense, 1: qkv (three weights, packed Q|K|V columns), 2: gate/up with the
@@ -482,6 +596,21 @@ __global__ __launch_bounds__(256) void lf_fp8_act_quant_rows(const int32_t *coun
                                                              const uint16_t *x,
                                                              const uint8_t *w, uint8_t *xq) {
   act_quant_rows(counts, x, w, xq);
+}
+
+// RmsNorm + per-token quantizer, one entry per epsilon (the epsilon is part
+// of the operation's NormalizationShape, model/plan/plan.mbt:146-151, so an
+// AOT entry is built per value): 1e-5 (Llama-3) and 1e-6 (the reference
+// spec's default, model/spec/llama.mbt:39).
+__global__ __launch_bounds__(256) void lf_fp8_rms_norm_quant_rows_eps1em5(
+    const int32_t *counts, const uint16_t *x, const uint16_t *gamma, const uint8_t *w,
+    uint8_t *xq) {
+  rms_norm_quant_rows(counts, x, gamma, w, xq, 1e-5f);
+}
+__global__ __launch_bounds__(256) void lf_fp8_rms_norm_quant_rows_eps1em6(
+    const int32_t *counts, const uint16_t *x, const uint16_t *gamma, const uint8_t *w,
+    uint8_t *xq) {
+  rms_norm_quant_rows(counts, x, gamma, w, xq, 1e-6f);
 }
 
 }  // extern "C"

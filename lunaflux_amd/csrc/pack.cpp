@@ -277,6 +277,26 @@ int64_t lunaflux_fp8_w8a16_workspace_bytes(int32_t entry, int64_t n, int64_t k,
   return w8a16_workspace(entry, n, k, 0, 0, max_tokens);
 }
 
+int32_t lunaflux_fp8_rms_norm_quant_geometry(float epsilon, int64_t k, int32_t max_rows,
+                                             int32_t dims[7], char symbol[LF_FP8_SYMBOL_BYTES]) {
+  if (dims == nullptr || symbol == nullptr || k <= 0 || k > 8192 || k % 128 != 0 ||
+      max_rows <= 0) {
+    return LF_INVALID_ARGUMENT;
+  }
+  const char *name = nullptr;
+  if (epsilon == 1e-5f) {
+    name = "lf_fp8_rms_norm_quant_rows_eps1em5";
+  } else if (epsilon == 1e-6f) {
+    name = "lf_fp8_rms_norm_quant_rows_eps1em6";
+  } else {
+    return LF_UNSUPPORTED;
+  }
+  const int32_t values[7] = {(max_rows + 3) / 4, 1, 1, 256, 1, 1, 0};  // one wave per row
+  std::memcpy(dims, values, sizeof(values));
+  std::snprintf(symbol, LF_FP8_SYMBOL_BYTES, "%s", name);
+  return LF_OK;
+}
+
 int64_t lunaflux_fp8_qkv_w8a16_workspace_bytes(int64_t nq, int64_t nkv, int64_t k,
                                                int32_t max_tokens) {
   if (nq <= 0 || nkv <= 0 || nq > kMaxDim || nkv > kMaxDim) return -1;
@@ -294,6 +314,8 @@ static int32_t launch_geometry(int32_t entry, int64_t n, int64_t k, int64_t nq, 
   const char *name = nullptr;
   char buffer[LF_FP8_SYMBOL_BYTES];
   switch (entry) {
+    case LF_FP8_ENTRY_RMS_NORM_QUANT_ROWS:
+      return LF_INVALID_ARGUMENT;  // needs the epsilon: lunaflux_fp8_rms_norm_quant_geometry
     case LF_FP8_ENTRY_ACT_QUANT_ROWS:
       name = "lf_fp8_act_quant_rows";  // one wave per row
       gx = (max_tokens + 3) / 4;

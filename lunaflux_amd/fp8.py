@@ -116,6 +116,18 @@ def launch_geometry(entry: int, n: int, k: int, max_tokens: int,
             symbol.value.decode("ascii"))
 
 
+def rms_norm_quant_geometry(epsilon: float, k: int, max_rows: int):
+    """(dims, symbol) of the fused RmsNorm + quantizer entry for an epsilon
+    (fp32), input width K and profile; DeviceError(UNSUPPORTED) for an
+    epsilon with no built entry."""
+    dims = (ctypes.c_int32 * 7)()
+    symbol = ctypes.create_string_buffer(128)
+    _check("rms_norm_quant_geometry", _abi.lib().lunaflux_fp8_rms_norm_quant_geometry(
+        float(np.float32(epsilon)), k, max_rows, dims, symbol))
+    return (KernelLaunchDimensions.new(tuple(dims[0:3]), tuple(dims[3:6]), dims[6]),
+            symbol.value.decode("ascii"))
+
+
 @dataclass
 class Fp8Weight:
     """One device-resident weight region (a TensorRef's region)."""
@@ -226,6 +238,23 @@ class ProjectionRuntime:
         return self._step(_abi.ENTRY_ACT_QUANT_ROWS, w.rows, w.columns, max_tokens,
                           [_region(counts, COUNTS_BYTES, alignment=4), x, w.region, xq])
 
+    def bind_rms_norm_quant(self, counts: Allocation, x: KernelArgument, gamma: KernelArgument,
+                            w: Fp8Weight, xq: KernelArgument, max_tokens: int,
+                            epsilon: float) -> LaunchStep:
+        """The RmsNorm operation (kernels/reference/basic.mbt:32-68) writing
+        per-token e4m3 rows for the W8A8 projection whose first weight is w
+        (xq: lunaflux_fp8_act_quant_bytes(max_tokens, K) bytes)."""
+        dims, symbol = rms_norm_quant_geometry(epsilon, w.columns, max_tokens)
+        return LaunchStep(self.function(symbol), dims, KernelArguments(
+            [_region(counts, COUNTS_BYTES, alignment=4), x, gamma, w.region, xq]), symbol)
+
+    def bind_dense_quantized(self, counts: Allocation, xq: KernelArgument, w: Fp8Weight,
+                             y: KernelArgument, max_tokens: int) -> LaunchStep:
+        """The W8A8 dense GEMM alone, over rows already quantized (by
+        bind_rms_norm_quant or bind_act_quant)."""
+        return self._step(_abi.ENTRY_W8A8_DENSE, w.rows, w.columns, max_tokens,
+                          [_region(counts, COUNTS_BYTES, alignment=4), xq, w.region, y])
+
     def bind_dense(self, family: str, counts: Allocation, x: KernelArgument, w: Fp8Weight,
                    y: KernelArgument, max_tokens: int) -> BoundOperation:
         _family(family, max_tokens)
@@ -334,6 +363,28 @@ class ProjectionRuntime:
     def silu_gated_mlp(self, x, wg, wu, wd, family="w8a16", max_tokens=None):
         return self._run(lambda c, xr, yr, mt: self.bind_gated_mlp(family, c, xr, wg, wu, wd, yr, mt),
                          x, (x.shape[0], wd.rows), max_tokens)
+
+    def rms_norm_quant(self, x, gamma, w: Fp8Weight, epsilon: float, max_tokens=None):
+        """Runs only the fused RmsNorm + quantizer on bf16 rows x [M, K] with
+        the bf16 norm weight gamma [K]: (codes [M, K], scales [M])."""
+        x = np.ascontiguousarray(x, np.uint16)
+        m, k = x.shape
+        max_tokens = max(m, 1) if max_tokens is None else max_tokens
+        xa = self.context.allocate(max_tokens * k * 2)
+        if m:
+            xa.copy_from_host(x)
+        ga = self.context.upload(np.ascontiguousarray(gamma, np.uint16))
+        ws = self.context.allocate(act_quant_bytes(max_tokens, k))
+        counts = self.step_counts(m)
+        step = self.bind_rms_norm_quant(counts, _region(xa, alignment=256),
+                                        _region(ga, alignment=16), w,
+                                        _region(ws, alignment=256), max_tokens, epsilon)
+        step.launch(self.stream, synchronous=True)
+        if m == 0:
+            return np.zeros((0, k), np.uint8), np.zeros(0, np.float32)
+        codes = ws.read(np.uint8, (m, k))
+        off = (m * k + 255) // 256 * 256
+        return codes, ws.read(np.float32, (m,), offset=off)
 
     def act_quant(self, x, w: Fp8Weight, max_tokens=None):
         """Runs only the per-token quantizer: (codes [M, K], scales [M])."""

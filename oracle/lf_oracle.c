@@ -174,6 +174,43 @@ void lfo_silu_mul_array(const float *g, const float *u, int64_t n, float *out) {
   for (int64_t i = 0; i < n; i += 1) out[i] = lfo_silu_mul(g[i], u[i]);
 }
 
+/* kernels/reference/basic.mbt:32-68: the weight must be one row of the
+ * input's width (InvalidShape(NormalizationWeight)); epsilon must be finite
+ * (NonFinite(Epsilon)) and > 0 (InvalidScalar(Epsilon)); per row the sum of
+ * squares in ascending column order (a non-finite sum is
+ * NonFinite(ComputedValue)), inverse_rms = 1 / sqrt(sum / width + epsilon),
+ * out = x * inverse_rms * w evaluated left to right; a non-finite output is
+ * NonFinite(ComputedValue) (values.mbt:117-133). sqrtf is the correctly
+ * rounded IEEE square root. */
+int32_t lfo_rms_norm(const float *x, int32_t rows, int32_t columns,
+                     const float *w, int32_t w_rows, int32_t w_columns,
+                     float epsilon, const lfo_limits *limits, float *out) {
+  if (w_rows != 1 || w_columns != columns) return LFO_INVALID_SHAPE;
+  if (!finite_f32(epsilon)) return LFO_NON_FINITE;
+  if (epsilon <= 0.0f) return LFO_INVALID_SCALAR;
+  int32_t elements = 0;
+  int32_t st = lfo_checked_element_count(rows, columns, limits, &elements);
+  if (st != LFO_OK) return st;
+  const float width = (float)columns;
+  for (int32_t r = 0; r < rows; r += 1) {
+    const float *xr = x + (int64_t)r * columns;
+    float square_sum = 0.0f;
+    for (int32_t c = 0; c < columns; c += 1) {
+      float square = xr[c] * xr[c];
+      square_sum = square_sum + square;
+    }
+    if (!finite_f32(square_sum)) return LFO_NON_FINITE;
+    float inverse_rms = 1.0f / sqrtf(square_sum / width + epsilon);
+    for (int32_t c = 0; c < columns; c += 1) {
+      float v = xr[c] * inverse_rms;
+      v = v * w[c];
+      if (!finite_f32(v)) return LFO_NON_FINITE;
+      out[(int64_t)r * columns + c] = v;
+    }
+  }
+  return LFO_OK;
+}
+
 /* kernels/reference/mlp.mbt:4-39 */
 int32_t lfo_silu_gated_mlp(const float *x, int32_t rows, int32_t hidden,
                            const float *wg, const float *wu, int32_t inter,

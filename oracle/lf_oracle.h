@@ -13,6 +13,7 @@
  *   lfo_dense_projection     <- kernels/reference/basic.mbt:102-109
  *   lfo_qkv_projection       <- kernels/reference/basic.mbt:113-153
  *   lfo_silu_gated_mlp       <- kernels/reference/mlp.mbt:4-39
+ *   lfo_rms_norm             <- kernels/reference/basic.mbt:32-68
  *   lfo_checked_element_count<- kernels/reference/limits.mbt:47-90
  * Numeric contract (kernels/reference/README.mbt.md:7-18): binary32 values,
  * sequential-K fp32 accumulation with separate multiply and add (this file is
@@ -91,6 +92,11 @@ int32_t lfo_silu_gated_mlp(const float *x, int32_t rows, int32_t hidden,
                            const float *wd, int32_t round_hidden_bf16,
                            const lfo_limits *limits, float *hidden_out,
                            float *out);
+/* Row-wise RMS normalization: w is the [1, columns] norm weight; sequential
+ * fp32 sum of squares, out = x * (1 / sqrt(sum / columns + epsilon)) * w. */
+int32_t lfo_rms_norm(const float *x, int32_t rows, int32_t columns,
+                     const float *w, int32_t w_rows, int32_t w_columns,
+                     float epsilon, const lfo_limits *limits, float *out);
 /* SiLU product for one element: g / (1 + expf(-g)) * u (mlp.mbt:30). */
 float lfo_silu_mul(float g, float u);
 /* out[i] = lfo_silu_mul(g[i], u[i]) for i < n. */

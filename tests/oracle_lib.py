@@ -46,6 +46,8 @@ def _load():
                                       ctypes.POINTER(Limits), _f32p]),
         "lfo_silu_gated_mlp": (_i32, [_f32p, _i32, _i32, _f32p, _f32p, _i32, _f32p, _i32,
                                       ctypes.POINTER(Limits), _f32p, _f32p]),
+        "lfo_rms_norm": (_i32, [_f32p, _i32, _i32, _f32p, _i32, _i32, ctypes.c_float,
+                                ctypes.POINTER(Limits), _f32p]),
         "lfo_silu_mul": (ctypes.c_float, [ctypes.c_float, ctypes.c_float]),
         "lfo_silu_mul_array": (None, [_f32p, _f32p, _i64, _f32p]),
         "lfo_bf16_rne": (ctypes.c_uint16, [ctypes.c_float]),
@@ -153,6 +155,17 @@ def silu_gated_mlp(x, wg, wu, wd, round_hidden_bf16=False, lim=None, return_hidd
                                   inter, _p(wd, _f32p), int(bool(round_hidden_bf16)), _lim(lim),
                                   _p(hidden, _f32p), _p(out, _f32p)))
     return (out, hidden) if return_hidden else out
+
+
+def rms_norm(x: np.ndarray, w: np.ndarray, epsilon: float, lim=None) -> np.ndarray:
+    """x [rows, K] fp32, w the norm weight ([K] or [1, K]) -> fp32 [rows, K]."""
+    x = np.ascontiguousarray(x, np.float32)
+    w = np.ascontiguousarray(w, np.float32)
+    w2 = w.reshape(1, -1) if w.ndim == 1 else w
+    out = np.empty_like(x)
+    _check(LIB.lfo_rms_norm(_p(x, _f32p), x.shape[0], x.shape[1], _p(w2, _f32p), w2.shape[0],
+                            w2.shape[1], float(np.float32(epsilon)), _lim(lim), _p(out, _f32p)))
+    return out
 
 
 def silu_mul(g: float, u: float) -> float:

@@ -45,7 +45,8 @@ def test_code_object_has_every_entry_point():
                    f"lf_fp8_w8a16_dense_k{k}_m{m}" for k in (4096, 14336) for m in (16, 32, 128)] + [
                    f"lf_fp8_w8a16_gate_up_k4096_m{m}" for m in (16, 32, 128)] + [
                    f"lf_fp8_w8a16_qkv_k4096_q4096_kv1024_m{m}" for m in (16, 32, 128)] + [
-                   f"lf_fp8_w8a16_dense_wide_k4096_m{m}" for m in (16, 32, 128)]:
+                   f"lf_fp8_w8a16_dense_wide_k4096_m{m}" for m in (16, 32, 128)] + [
+                   "lf_fp8_rms_norm_quant_rows_eps1em5", "lf_fp8_rms_norm_quant_rows_eps1em6"]:
         assert symbol.encode() + b"\0" in image, symbol
 
 
@@ -291,3 +292,22 @@ def test_moe_descriptor_layout_and_geometry():
                 (8, 2, 0, 200, 256, 0), (8, 2, 0, 256, 256, 64), (8, 2, 0, 8192, 256, 128)]:
         with pytest.raises(fp8.DeviceError):
             moe.moe_descriptor(*bad)
+
+
+def test_rms_norm_quant_geometry():
+    from lunaflux_amd import _abi, fp8
+    from lunaflux_amd.device import DeviceError
+    dims, sym = fp8.rms_norm_quant_geometry(1e-5, 4096, 130)
+    assert sym == "lf_fp8_rms_norm_quant_rows_eps1em5"
+    assert dims.grid == (33, 1, 1) and dims.block == (256, 1, 1)
+    assert fp8.rms_norm_quant_geometry(1e-6, 8192, 4)[1] == "lf_fp8_rms_norm_quant_rows_eps1em6"
+    with pytest.raises(DeviceError) as err:
+        fp8.rms_norm_quant_geometry(1e-4, 4096, 16)
+    assert err.value.status == _abi.LF_UNSUPPORTED
+    for k, rows in ((8320, 16), (4000, 16), (4096, 0)):
+        with pytest.raises(DeviceError) as err:
+            fp8.rms_norm_quant_geometry(1e-5, k, rows)
+        assert err.value.status == _abi.LF_INVALID_ARGUMENT
+    with pytest.raises(DeviceError) as err:
+        fp8.launch_geometry(_abi.ENTRY_RMS_NORM_QUANT_ROWS, 4096, 4096, 16)
+    assert err.value.status == _abi.LF_INVALID_ARGUMENT

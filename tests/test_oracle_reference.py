@@ -174,3 +174,56 @@ def test_multithreaded_projection_is_bit_identical():
     single = o.project_values(x, w)
     for threads in (1, 3, 8):
         np.testing.assert_array_equal(o.project_values_mt(x, w, threads), single)
+
+
+def test_rms_norm_kat():
+    # kernels/reference/operations_test.mbt:38-60: [3, 4], weight [1, 1],
+    # epsilon 1e-5 -> [0.8485277, 1.1313703] within 2e-5
+    out = o.rms_norm(np.array([[3, 4]], np.float32), np.ones((1, 2), np.float32), 1e-5,
+                     ref_limits())
+    np.testing.assert_allclose(out, [[0.8485277, 1.1313703]], atol=2e-5)
+
+
+def test_rms_norm_rejections():
+    # kernels/reference/basic.mbt:38-47 (NormalizationWeight, Epsilon) and
+    # :59-61 (a non-finite sum of squares)
+    x = np.ones((2, 4), np.float32)
+    for w in (np.ones((1, 3), np.float32), np.ones((2, 4), np.float32)):
+        with pytest.raises(o.OracleError) as err:
+            o.rms_norm(x, w, 1e-5)
+        assert err.value.status == o.INVALID_SHAPE
+    for eps, status in ((float("nan"), o.NON_FINITE), (float("inf"), o.NON_FINITE),
+                        (0.0, o.INVALID_SCALAR), (-1e-5, o.INVALID_SCALAR)):
+        with pytest.raises(o.OracleError) as err:
+            o.rms_norm(x, np.ones(4, np.float32), eps)
+        assert err.value.status == status
+    with pytest.raises(o.OracleError) as err:
+        o.rms_norm(np.full((1, 4), 1e20, np.float32), np.ones(4, np.float32), 1e-5)
+    assert err.value.status == o.NON_FINITE
+
+
+def test_rms_norm_sums_squares_in_column_order():
+    # x = [4096, 1 x 1023]: adding 1 to 2^24 is a tie that rounds to even, so
+    # the sequential sum stays 2^24 (any pairwise or blocked order would
+    # reach 2^24 + 1023 or so); then 2^24 / 1024 + 2^-10 = 16384 (another
+    # tie), sqrt 128, inverse 2^-7, all exact: out = x / 128 * w.
+    x = np.ones((1, 1024), np.float32)
+    x[0, 0] = 4096
+    w = np.linspace(0.5, 2.0, 1024, dtype=np.float32)
+    out = o.rms_norm(x, w, 2.0 ** -10)
+    np.testing.assert_array_equal(out, (x / np.float32(128)) * w)
+
+
+def test_rms_norm_closed_form():
+    # against the float64 formula: each row within a few fp32 ulps of
+    # x / sqrt(mean(x^2) + eps) * w, and the weight applied per column
+    rng = np.random.default_rng(77)
+    x = rng.standard_normal((5, 384)).astype(np.float32)
+    w = rng.uniform(0.2, 3.0, 384).astype(np.float32)
+    out = o.rms_norm(x, w, 1e-6)
+    x64 = x.astype(np.float64)
+    ref = x64 / np.sqrt((x64 ** 2).mean(axis=1, keepdims=True) + 1e-6) * w
+    np.testing.assert_allclose(out, ref, rtol=2e-6, atol=0)
+    # a row of equal magnitudes normalizes to +-1 (times w) up to epsilon
+    out = o.rms_norm(np.full((1, 256), -3.0, np.float32), np.ones(256, np.float32), 1e-6)
+    np.testing.assert_allclose(out, -1.0, rtol=1e-6)
