@@ -75,84 +75,88 @@ LF_DEVICE bool desc_ok(const MoeDesc &d) {
 
 // --- routing ---------------------------------------------------------------
 // One wave per token, four tokens per block; lane l holds the logits of
-// experts l, l + 64, ... The k largest logits in order (ties -> lower expert
-// id): k rounds of a wave-wide (value, id) maximum over the experts not yet
-// picked. Softmax weights over the k picked logits (mode 0) or over all
-// experts (mode 1); the sum of exponentials is accumulated in expert order,
-// as the reference loop does.
+// experts l, l + 64, ... (E <= 256) and the wave keeps them in LDS. The k
+// largest logits in order (ties -> lower expert id) by rank: each lane counts
+// the logits that beat each of its own (u_j > v, or u_j == v and j < e), so
+// the expert ranked r < k is the r-th pick, with no serial cross-lane chain.
+// Softmax weights over the k picked logits (mode 0) or over all experts (mode
+// 1); the sum of exponentials is accumulated in expert order, as the
+// reference loop does (every lane reads the exponentials back from LDS and
+// sums them in that order).
+LF_DEVICE void wave_lds_sync() {
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+}
+
 LF_DEVICE void route(const int32_t *counts, const MoeDesc &d, const float *logits, uint8_t *ws) {
+  __shared__ __attribute__((aligned(16))) float sv[4][256];
+  __shared__ int32_t sid[4][16];
+  __shared__ float spv[4][16];
   const int T = live_rows(counts, 1 << 30);
-  const int t = blockIdx.x * 4 + (threadIdx.x >> 6);
+  const int w = threadIdx.x >> 6;
+  const int t = blockIdx.x * 4 + w;
   if (t >= T) return;
   const int lane = threadIdx.x & 63;
   const MoeLayout L(d, T);
-  const int E = d.experts;
+  const int E = d.experts, k = d.top_k;
   const float *l = logits + static_cast<uint64_t>(t) * E;
-  int32_t *ids = at<int32_t>(ws, L.topk_ids) + static_cast<uint64_t>(t) * d.top_k;
-  float *wts = at<float>(ws, L.topk_w) + static_cast<uint64_t>(t) * d.top_k;
+  int32_t *ids = at<int32_t>(ws, L.topk_ids) + static_cast<uint64_t>(t) * k;
+  float *wts = at<float>(ws, L.topk_w) + static_cast<uint64_t>(t) * k;
   float v[4];
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
     const int e = lane + 64 * i;
     v[i] = e < E ? l[e] : 0.0f;
+    if (e < E) sv[w][e] = v[i];
   }
-  uint32_t taken = 0;  // bit i: expert lane + 64 i picked (or absent)
+  wave_lds_sync();
+  const int E4 = E & ~3;
 #pragma unroll
-  for (int i = 0; i < 4; ++i) taken |= (lane + 64 * i < E ? 0u : 1u) << i;
-  int picked[16];
-  float pv[16];
-  for (int j = 0; j < d.top_k; ++j) {
-    // this lane's candidate: its largest untaken logit, lowest id on ties
-    int best = -1;
-    float bv = 0.0f;
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      if (!((taken >> i) & 1u) && (best < 0 || v[i] > bv)) {
-        best = lane + 64 * i;
-        bv = v[i];
-      }
+  for (int i = 0; i < 4; ++i) {
+    const int e = lane + 64 * i;
+    if (e >= E) break;
+    int r = 0;
+    for (int j = 0; j < E4; j += 4) {
+      const float4 u = *reinterpret_cast<const float4 *>(&sv[w][j]);
+      r += (u.x > v[i] || (u.x == v[i] && j < e)) ? 1 : 0;
+      r += (u.y > v[i] || (u.y == v[i] && j + 1 < e)) ? 1 : 0;
+      r += (u.z > v[i] || (u.z == v[i] && j + 2 < e)) ? 1 : 0;
+      r += (u.w > v[i] || (u.w == v[i] && j + 3 < e)) ? 1 : 0;
     }
-#pragma unroll
-    for (int off = 32; off > 0; off >>= 1) {
-      const int ob = __shfl_xor(best, off);
-      const float ov = __shfl_xor(bv, off);
-      if (ob >= 0 && (best < 0 || ov > bv || (ov == bv && ob < best))) {
-        best = ob;
-        bv = ov;
-      }
+    for (int j = E4; j < E; ++j) {
+      const float u = sv[w][j];
+      r += (u > v[i] || (u == v[i] && j < e)) ? 1 : 0;
     }
-    picked[j] = best;
-    pv[j] = bv;
-    if ((best & 63) == lane) taken |= 1u << (best >> 6);
+    if (r < k) {
+      sid[w][r] = e;
+      spv[w][r] = v[i];
+    }
   }
-  const float top = pv[0];
+  wave_lds_sync();
+  const float top = spv[w][0];
   float sum = 0.0f;
   if (d.route_mode == 0) {
-    for (int j = 0; j < d.top_k; ++j) sum += expf(pv[j] - top);
+    for (int j = 0; j < k; ++j) sum += expf(spv[w][j] - top);
   } else {
-    float ex[4];
 #pragma unroll
-    for (int i = 0; i < 4; ++i) ex[i] = expf(v[i] - top);
-    for (int e = 0; e < E; ++e) {
-      float te = 0.0f;
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        if ((e >> 6) == i) te = __shfl(ex[i], e & 63);
-      }
-      sum += te;
+    for (int i = 0; i < 4; ++i) {
+      const int e = lane + 64 * i;
+      if (e < E) sv[w][e] = expf(v[i] - top);
     }
+    wave_lds_sync();
+    for (int j = 0; j < E4; j += 4) {
+      const float4 u = *reinterpret_cast<const float4 *>(&sv[w][j]);
+      sum += u.x;
+      sum += u.y;
+      sum += u.z;
+      sum += u.w;
+    }
+    for (int j = E4; j < E; ++j) sum += sv[w][j];
   }
-  if (lane < d.top_k) {
-    float pj = 0.0f;
-    int ij = 0;
-    for (int j = 0; j < d.top_k; ++j) {
-      if (j == lane) {
-        pj = pv[j];
-        ij = picked[j];
-      }
-    }
-    ids[lane] = ij;
-    wts[lane] = expf(pj - top) / sum;
+  if (lane < k) {
+    ids[lane] = sid[w][lane];
+    wts[lane] = expf(spv[w][lane] - top) / sum;
   }
 }
 
@@ -217,37 +221,69 @@ LF_DEVICE void sort_assignments(const int32_t *counts, const MoeDesc &d, uint8_t
   int32_t *pos = at<int32_t>(ws, L.pos);
   int32_t *offsets = at<int32_t>(ws, L.offsets);
   int32_t *tiles = at<int32_t>(ws, L.tiles);
-  // Per expert: total rows and rows in the chunks before this one.
+  // Per expert: total rows and rows in the chunks before this one, every
+  // (chunk, expert) entry of the table loaded by its own thread and added
+  // into LDS (integer sums: the order does not matter).
   for (int e = tid; e < E; e += kSortThreads) {
-    int total = 0, before = 0;
-    for (int cc = 0; cc < chunks; ++cc) {
-      const int n = table[static_cast<uint64_t>(cc) * E + e];
-      total += n;
-      before += cc < c ? n : 0;
-    }
-    wcnt[0][e] = total;
-    base[e] = before;
+    wcnt[0][e] = 0;
+    base[e] = 0;
   }
   __syncthreads();
-  if (tid == 0) {
-    // Exclusive scans: first row, first 128-row tile and first 256-row tile
-    // of each expert; and the list of experts with rows.
-    int off = 0, tl = 0, tl2 = 0, live = 0;
-    for (int e = 0; e < E; ++e) {
-      const int n = wcnt[0][e];
-      if (c == 0) {
-        offsets[e] = off;
-        tiles[e] = tl;
-        tiles[E + 1 + e] = tl2;
-        if (n > 0) tiles[2 * E + 3 + live] = e;
-      }
-      live += n > 0 ? 1 : 0;
-      base[e] += off;
-      off += n;
-      tl += (n + w8a8::kBM - 1) / w8a8::kBM;
-      tl2 += (n + 2 * w8a8::kBM - 1) / (2 * w8a8::kBM);
+  for (int i = tid; i < chunks * E; i += kSortThreads) {
+    const int cc = i / E, e = i - cc * E;
+    const int n = table[i];
+    atomicAdd(&wcnt[0][e], n);
+    if (cc < c) atomicAdd(&base[e], n);
+  }
+  __syncthreads();
+  if (wave == 0) {
+    // Exclusive scans over the experts (lane l holds experts 4l .. 4l + 3):
+    // first row, first 128-row tile and first 256-row tile of each expert,
+    // and its index in the list of experts with rows.
+    int n4[4], r = 0, t1 = 0, t2 = 0, lv = 0;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int e = 4 * lane + i;
+      n4[i] = e < E ? wcnt[0][e] : 0;
+      r += n4[i];
+      t1 += (n4[i] + w8a8::kBM - 1) / w8a8::kBM;
+      t2 += (n4[i] + 2 * w8a8::kBM - 1) / (2 * w8a8::kBM);
+      lv += n4[i] > 0 ? 1 : 0;
     }
-    if (c == 0) {
+    int off = r, tl = t1, tl2 = t2, live = lv;  // inclusive scans across lanes
+#pragma unroll
+    for (int step = 1; step < 64; step <<= 1) {
+      const int a0 = __shfl_up(off, step), a1 = __shfl_up(tl, step), a2 = __shfl_up(tl2, step),
+                a3 = __shfl_up(live, step);
+      if (lane >= step) {
+        off += a0;
+        tl += a1;
+        tl2 += a2;
+        live += a3;
+      }
+    }
+    off -= r;
+    tl -= t1;
+    tl2 -= t2;
+    live -= lv;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int e = 4 * lane + i;
+      if (e < E) {
+        if (c == 0) {
+          offsets[e] = off;
+          tiles[e] = tl;
+          tiles[E + 1 + e] = tl2;
+          if (n4[i] > 0) tiles[2 * E + 3 + live] = e;
+        }
+        base[e] += off;
+      }
+      off += n4[i];
+      tl += (n4[i] + w8a8::kBM - 1) / w8a8::kBM;
+      tl2 += (n4[i] + 2 * w8a8::kBM - 1) / (2 * w8a8::kBM);
+      live += n4[i] > 0 ? 1 : 0;
+    }
+    if (c == 0 && lane == 63) {  // experts past E count 0: lane 63 holds the totals
       offsets[E] = off;
       tiles[E] = tl;
       tiles[E + 1 + E] = tl2;
