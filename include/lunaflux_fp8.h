@@ -211,11 +211,12 @@ int32_t lunaflux_fp8_rms_norm_quant_geometry(float epsilon, int64_t k, int32_t m
  *  lf_moe_sort_count    (counts, desc, ws)
  *  lf_moe_sort          (counts, desc, ws)
  *  lf_moe_quant_tokens  (counts, desc, x bf16 [T, H], ws)
- *  lf_moe_gate_up[_b128|_t256|_gemv](counts, desc, wg, wu, ws)
+ *  lf_moe_gate_up[_b128|_t256|_t256_b128|_gemv](counts, desc, wg, wu, ws)
  *  lf_moe_quant_hidden  (counts, desc, ws)
- *  lf_moe_down[_b128|_t256|_gemv]   (counts, desc, wd, ws)
- * (_t256: the per-channel GEMMs on 256 x 256 tiles, chosen by the launch
- * geometry for profiles that average >= 256 routed rows per expert; _gemv:
+ *  lf_moe_down[_b128|_t256|_t256_b128|_gemv]   (counts, desc, wd, ws)
+ * (_t256: the GEMMs on 256 x 256 tiles, chosen by the launch geometry for
+ * profiles that average >= 256 routed rows per expert, _t256_b128 with block
+ * scales where both GEMMs have K <= 3072; _gemv:
  * either scale mode, chosen for profiles of at most 32 tokens, where the
  * GEMMs stream the touched experts' weights: a fixed grid whose blocks
  * loop over (expert with rows, 64-column group) items.

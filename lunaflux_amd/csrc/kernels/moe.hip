@@ -548,12 +548,76 @@ __device__ void grouped_gemm(const int32_t *counts, const MoeDesc &d, const uint
 // columns per block.
 using GemmTile256 = w8a8v4::Tile<256, 256, 4, 4, 2>;
 
+// Block scales (128 x 128 weight blocks, per-token-per-128-column activation
+// scales) on the 256 x 256 tile, whose accumulators leave no registers for a
+// fresh set per k-tile: the accumulators hold acc' = (sum so far) / sigma_kt
+// with sigma_kt = a_kt(row) w_kt(column block), so before k-tile kt's MFMAs
+// add its products they are multiplied by sigma_{kt-1} / sigma_kt, and the
+// epilogue multiplies by the last sigma. A zero scale only belongs to an
+// all-zero group, whose products are zero, so each scale sequence carries the
+// last nonzero value forward (any nonzero sigma is then exact) and starts
+// at 1. The row ratios a_{kt-1} / a_kt live in LDS [KT][256]; a wave's
+// column block ratios (gate and up for gate/up, one block for down) in LDS.
+constexpr int kT256MaxKT = 24;  // LDS: 24 KiB of row ratios beside the 128 KiB ring
+
 template <int STAGE>
+struct BlockRescale256 {
+  using T = GemmTile256;
+  static_assert(T::kFN >= T::kFM, "apply(o) rescales column fragment o");
+  typedef const __attribute__((address_space(3))) float *lds_ptr;
+  lds_ptr ra;          // [KT][256]: row ratios
+  lds_ptr rw;          // this wave: [kT256MaxKT] gate (or down) block ratios, then (STAGE 0) up
+  int row0;            // the lane's first accumulator row in the tile
+  f32x4 m[T::kFM][4];  // this k-tile's multipliers of the lane's 32 rows
+  int kt = 0;
+  LF_DEVICE void load(int part) {
+    const float wk = rw[part * kT256MaxKT + kt];
+#pragma unroll
+    for (int i = 0; i < T::kFM; ++i)
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        const f32x4 r = *reinterpret_cast<const __attribute__((address_space(3))) f32x4 *>(
+            ra + kt * 256 + row0 + 32 * i + 8 * q);
+#pragma unroll
+        for (int e = 0; e < 4; ++e) m[i][q][e] = r[e] * wk;
+      }
+  }
+  LF_DEVICE void begin(int k) {
+    kt = k;
+    load(0);
+  }
+  template <class A>
+  LF_DEVICE void apply(int o, A &acc) {
+    // the up fragments (o is a compile-time unrolled index: no runtime branch)
+    if constexpr (STAGE == 0) {
+      if (o == T::kFN / 2) load(1);
+    }
+#pragma unroll
+    for (int i = 0; i < T::kFM; ++i)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) acc[i][o][r] *= m[i][r >> 2][r & 3];
+  }
+};
+
+// Carries the last nonzero scale forward: returns the ratio prev / s for a
+// nonzero s (prev <- s), 1 otherwise.
+LF_DEVICE float carry_ratio(float s, float &prev) {
+  if (s == 0.0f) return 1.0f;
+  const float r = prev / s;
+  prev = s;
+  return r;
+}
+
+template <int STAGE, bool BLOCK = false>
 __device__ void grouped_gemm_t256(const int32_t *counts, const MoeDesc &d, const uint8_t *w0,
                                   const uint8_t *w1, uint8_t *ws) {
   using T = GemmTile256;
   constexpr int BM = T::kBM;
   __shared__ __attribute__((aligned(1024))) uint8_t smem[T::kSmem];
+  __shared__ __attribute__((aligned(16))) float ra_lds[BLOCK ? kT256MaxKT * BM : 1];
+  __shared__ float rw_lds[BLOCK ? T::kWgn * 2 * kT256MaxKT : 1];
+  __shared__ float sw_last[BLOCK ? T::kWgn * 2 : 1];
+
   const int Tn = live_rows(counts, 1 << 30);
   if (Tn == 0) return;
   const MoeLayout L(d, Tn);
@@ -595,9 +659,42 @@ __device__ void grouped_gemm_t256(const int32_t *counts, const MoeDesc &d, const
   // position, the hidden quantizer later its own), one per thread of the
   // first 256, loaded before the main loop and parked in LDS after it.
   __shared__ float sa_tile[BM];
-  const float *row_scales = at<float>(ws, L.hs);
   float sa_mine = 0.0f;
-  if (threadIdx.x < BM) sa_mine = row_scales[p0 + static_cast<int>(threadIdx.x) < pend ? p0 + threadIdx.x : p0];
+  if constexpr (!BLOCK) {
+    const float *row_scales = at<float>(ws, L.hs);
+    if (threadIdx.x < BM) sa_mine = row_scales[p0 + static_cast<int>(threadIdx.x) < pend ? p0 + threadIdx.x : p0];
+  } else {
+    // Ratio tables (see BlockRescale256): threads 0..255 one tile row each
+    // (its activation scales in token order for gate/up, expert order for
+    // down; sa_mine <- the last nonzero one), threads 256.. one (wave
+    // column, weight block) each.
+    if (KT > kT256MaxKT) return;  // the launch geometry never selects this form then
+    const float *ascales = at<float>(ws, STAGE == 0 ? L.xs : L.hs);
+    const int tid = threadIdx.x;
+    if (tid < BM) {
+      const int pp = p0 + tid;
+      float prev = 1.0f;
+      const float *sr = ascales + static_cast<uint64_t>(src_row(pp < pend ? pp : p0)) * KT;
+      for (int kt = 0; kt < KT; ++kt) {
+        const float r = pp < pend ? carry_ratio(sr[kt], prev) : 1.0f;
+        ra_lds[kt * BM + tid] = kt == 0 ? 1.0f : r;
+      }
+      sa_mine = prev;
+    } else if (tid < BM + 2 * T::kWgn) {
+      const int cw = (tid - BM) >> 1, part = (tid - BM) & 1;
+      const uint8_t *region = STAGE == 0 && part ? w1 : w0;
+      const int nb = STAGE == 0 ? (bx * (T::kBN / 2) + cw * (T::kWaveN / 2)) >> 7
+                                : (bx * T::kBN + cw * T::kWaveN) >> 7;
+      const float *sw = expert_scales(region, e) + static_cast<uint64_t>(nb) * KT;
+      float prev = 1.0f;
+      for (int kt = 0; kt < KT; ++kt) {
+        const float r = carry_ratio(sw[kt], prev);
+        rw_lds[(2 * cw + part) * kT256MaxKT + kt] = kt == 0 ? 1.0f : r;
+      }
+      sw_last[2 * cw + part] = prev;
+    }
+    __syncthreads();
+  }
   w8a8v4::Plan<T> plan;
 #pragma unroll
   for (int q = 0; q < T::kAIns; ++q) {
@@ -618,7 +715,14 @@ __device__ void grouped_gemm_t256(const int32_t *counts, const MoeDesc &d, const
   const int live_rows_wave = pend - (p0 + wm * T::kWaveM);
   const int live_fm = live_rows_wave <= 0 ? 0 : live_rows_wave >= T::kWaveM ? T::kFM
                                                                            : (live_rows_wave + 31) / 32;
-  w8a8v4::mainloop<T, true>(plan, KT, smem, acc, live_fm);
+  if constexpr (BLOCK) {
+    typedef const __attribute__((address_space(3))) float *lds_ptr;
+    BlockRescale256<STAGE> rs{(lds_ptr)(ra_lds), (lds_ptr)(rw_lds + 2 * wn * kT256MaxKT),
+                              wm * T::kWaveM + 4 * (lane >> 5), {}, 0};
+    w8a8v4::mainloop<T, true, BlockRescale256<STAGE>>(plan, KT, smem, acc, live_fm, rs);
+  } else {
+    w8a8v4::mainloop<T, true>(plan, KT, smem, acc, live_fm);
+  }
 
   const int c = lane & 31;
   float swv[T::kFN];
@@ -629,7 +733,11 @@ __device__ void grouped_gemm_t256(const int32_t *counts, const MoeDesc &d, const
     int t;
     slot((wn * T::kWaveN) / 16 + 2 * j + (c >> 4), region, t, ocol[j]);
     ocol[j] += c & 15;
-    swv[j] = expert_scales(region, e)[t * 16 + (c & 15)];
+    if constexpr (BLOCK) {
+      swv[j] = sw_last[2 * wn + (STAGE == 0 && j >= T::kFN / 2 ? 1 : 0)];
+    } else {
+      swv[j] = expert_scales(region, e)[t * 16 + (c & 15)];
+    }
   }
   if (threadIdx.x < BM) sa_tile[threadIdx.x] = sa_mine;
   // The output goes through LDS in 16-byte row chunks (w8a8v4::StageTile):
@@ -1036,6 +1144,25 @@ __global__ __launch_bounds__(512) void lf_moe_down_t256(const int32_t *counts,
   const MoeDesc &d = desc_of(desc);
   if (!desc_ok(d) || d.group != 0 || header_of(wd).magic != kWeightMagic) return;
   grouped_gemm_t256<1>(counts, d, wd, wd, ws);
+}
+
+// The same on 128 x 128 block scales (rescaled accumulators, see
+// BlockRescale256); K <= 24 x 128 for both GEMMs.
+__global__ __launch_bounds__(512) void lf_moe_gate_up_t256_b128(const int32_t *counts,
+                                                                const int32_t *desc,
+                                                                const uint8_t *wg,
+                                                                const uint8_t *wu, uint8_t *ws) {
+  const MoeDesc &d = desc_of(desc);
+  if (!desc_ok(d) || d.group != 128 || header_of(wg).magic != kWeightMagic) return;
+  grouped_gemm_t256<0, true>(counts, d, wg, wu, ws);
+}
+
+__global__ __launch_bounds__(512) void lf_moe_down_t256_b128(const int32_t *counts,
+                                                             const int32_t *desc,
+                                                             const uint8_t *wd, uint8_t *ws) {
+  const MoeDesc &d = desc_of(desc);
+  if (!desc_ok(d) || d.group != 128 || header_of(wd).magic != kWeightMagic) return;
+  grouped_gemm_t256<1, true>(counts, d, wd, wd, ws);
 }
 
 // Small profiles (at most 32 tokens): the grouped GEMV form, either scale

@@ -92,9 +92,20 @@ LF_DEVICE void block_barrier() { asm volatile("s_barrier" ::: "memory"); }
 // branches cost full tiles a few percent (measured on the dense prefill
 // GEMMs, whose only partial tile is the last row tile), so only the grouped
 // GEMMs, where partial tiles are common, use this form.
-template <class T, bool SKIP = false>
+// RESCALE (block-scaled operands): before the first half-step of k-tile kt,
+// rescale.begin(kt) loads that k-tile's multipliers and rescale.apply(o, acc)
+// multiplies the accumulators of column fragment o right before their first
+// MFMA of the k-tile (NoRescale: per-channel scales, nothing to do).
+struct NoRescale {
+  LF_DEVICE void begin(int) {}
+  template <class A>
+  LF_DEVICE void apply(int, A &) {}
+};
+
+template <class T, bool SKIP = false, class Rescale = NoRescale>
 __device__ __forceinline__ void mainloop(const Plan<T> &plan, int KT, uint8_t *smem,
-                         f32x16 (&acc)[T::kFM][T::kFN], int live_fm = T::kFM) {
+                         f32x16 (&acc)[T::kFM][T::kFN], int live_fm = T::kFM,
+                         Rescale rescale = Rescale{}) {
   constexpr int NS = T::kStages;
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int wm = wave / T::kWgn, wn = wave % T::kWgn;
@@ -172,11 +183,17 @@ __device__ __forceinline__ void mainloop(const Plan<T> &plan, int KT, uint8_t *s
   // loads may stay in flight once stage s + 1 has landed (-1: stage s + 1
   // does not exist: no wait, barrier or reads); ISSUE: whether stage
   // s + NS - 1 exists. Both are compile-time so the body has no branches.
-  auto step = [&](auto wait_tag, auto issue_tag, w8a8::Frag8(&cur)[kInner],
+  // EVEN: s is the first half-step of its k-tile (the calls come in pairs).
+  auto step = [&](auto wait_tag, auto issue_tag, auto even_tag, w8a8::Frag8(&cur)[kInner],
                   w8a8::Frag8(&nxt)[kInner], int s) {
     constexpr int kWait = decltype(wait_tag)::value;
     constexpr bool kIssue = decltype(issue_tag)::value;
+    constexpr bool kEven = decltype(even_tag)::value;
     const uint8_t *st = stage_ptr(s + 1);
+    if constexpr (kEven) {
+      rescale.begin(s >> 1);
+      rescale.apply(0, acc);
+    }
     mfma_group(cur, 0);
     __builtin_amdgcn_sched_barrier(0);
     if constexpr (kWait >= 0) {
@@ -189,6 +206,7 @@ __device__ __forceinline__ void mainloop(const Plan<T> &plan, int KT, uint8_t *s
     __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
     for (int o = 1; o < kOuter; ++o) {
+      if constexpr (kEven) rescale.apply(o, acc);
       mfma_group(cur, o);
       __builtin_amdgcn_sched_barrier(0);
       if constexpr (kWait >= 0) read_outer(outer[o], o, st);
@@ -228,17 +246,17 @@ __device__ __forceinline__ void mainloop(const Plan<T> &plan, int KT, uint8_t *s
   // once at most one stage's loads (s + 2) remain.
   int s = 0;
   for (; s + 4 < S; s += 2) {
-    step(W1{}, Yes{}, f0, f1, s);
-    step(W1{}, Yes{}, f1, f0, s + 1);
+    step(W1{}, Yes{}, Yes{}, f0, f1, s);
+    step(W1{}, Yes{}, No{}, f1, f0, s + 1);
   }
   if (S >= 4) {  // s == S - 4: stage S - 1 is issued last
-    step(W1{}, Yes{}, f0, f1, s);
-    step(W1{}, No{}, f1, f0, s + 1);
+    step(W1{}, Yes{}, Yes{}, f0, f1, s);
+    step(W1{}, No{}, No{}, f1, f0, s + 1);
     s += 2;
   }
   // s == S - 2: nothing left to issue; wait for the last stage.
-  step(W0{}, No{}, f0, f1, s);
-  step(WNone{}, No{}, f1, f0, s + 1);
+  step(W0{}, No{}, Yes{}, f0, f1, s);
+  step(WNone{}, No{}, No{}, f1, f0, s + 1);
 }
 
 // Epilogue staging. A wave's output tile goes through LDS (the stage ring is

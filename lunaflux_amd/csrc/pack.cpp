@@ -479,11 +479,13 @@ int32_t lunaflux_fp8_moe_launch_geometry(int32_t entry, const lf_fp8_moe_desc *d
   // most one partial tile.
   const int64_t tiles = A / 128 + d->experts;
   const bool b128 = d->group == 128;
-  // Per-channel profiles averaging >= 256 routed rows per expert run the
+  // Profiles averaging >= 256 routed rows per expert run the
   // grouped GEMMs on 256 x 256 tiles (8 waves; each weight strip streamed
   // once per 256 rows), smaller ones on 128 x 128 tiles.
-  const bool t256 = !b128 && A >= 256 * static_cast<int64_t>(d->experts) &&
-                    d->inter % 128 == 0 && d->hidden % 256 == 0;
+  // Block-scaled profiles too, for K <= 3072 in both GEMMs (their row-ratio
+  // table shares the LDS with the stage ring).
+  const bool t256 = A >= 256 * static_cast<int64_t>(d->experts) && d->inter % 128 == 0 &&
+                    d->hidden % 256 == 0 && (!b128 || (d->hidden <= 3072 && d->inter <= 3072));
   const int64_t tiles256 = A / 256 + d->experts;
   // Profiles of at most 32 tokens (every expert <= 32 rows) run the grouped
   // GEMV form: a fixed grid (up to 4 blocks per CU) whose blocks loop over
@@ -513,7 +515,7 @@ int32_t lunaflux_fp8_moe_launch_geometry(int32_t entry, const lf_fp8_moe_desc *d
       // 1-D grid over (64 h-column block, 128-row tile); blocks past the
       // live tile count return.
       if (t256) {
-        name = "lf_moe_gate_up_t256";
+        name = b128 ? "lf_moe_gate_up_t256_b128" : "lf_moe_gate_up_t256";
         gx = d->inter / 128 * tiles256;
         bx = 512;
         break;
@@ -532,7 +534,7 @@ int32_t lunaflux_fp8_moe_launch_geometry(int32_t entry, const lf_fp8_moe_desc *d
         break;
       }
       if (t256) {
-        name = "lf_moe_down_t256";
+        name = b128 ? "lf_moe_down_t256_b128" : "lf_moe_down_t256";
         gx = d->hidden / 256 * tiles256;
         bx = 512;
         break;

@@ -39,7 +39,8 @@ def test_code_object_has_every_entry_point():
     for symbol in ["lf_fp8_act_quant_rows"] + [f"lf_fp8_w8a8_{op}_{t}" for op in ("dense", "qkv", "gate_up")
                                                for t in ("t128", "t256")] + ["lf_moe_route", "lf_moe_sort_count", "lf_moe_sort", "lf_moe_quant_tokens",
                    "lf_moe_gate_up", "lf_moe_gate_up_b128", "lf_moe_quant_hidden", "lf_moe_down",
-                   "lf_moe_down_b128", "lf_moe_combine", "lf_moe_gate_up_gemv", "lf_moe_down_gemv"] + [f"lf_fp8_w8a16_{op}_m{m}" for op in ("dense", "qkv", "gate_up")
+                   "lf_moe_down_b128", "lf_moe_combine", "lf_moe_gate_up_gemv", "lf_moe_down_gemv",
+                   "lf_moe_gate_up_t256_b128", "lf_moe_down_t256_b128"] + [f"lf_fp8_w8a16_{op}_m{m}" for op in ("dense", "qkv", "gate_up")
                                              for m in (16, 32, 64, 128)] + [
                    f"lf_fp8_w8a16_{op}_m16_t1" for op in ("dense", "qkv", "gate_up")] + [
                    f"lf_fp8_w8a16_dense_k{k}_m{m}" for k in (4096, 14336) for m in (16, 32, 128)] + [
@@ -273,8 +274,17 @@ def test_moe_descriptor_layout_and_geometry():
     dims, sym = moe.launch_geometry(8, d, 1024)   # sort counts: a block per 1024 assignments
     assert sym == "lf_moe_sort_count" and dims.grid == (2, 1, 1)
     d5 = moe.moe_descriptor(64, 6, 1, 2048, 1408, 128)
-    dims, sym = moe.launch_geometry(6, d5, 4096)  # down, block scales
-    assert sym == "lf_moe_down_b128" and dims.grid == (2048 // 128 * (4096 * 6 // 128 + 64), 1, 1)
+    # block scales averaging >= 256 rows per expert: 256 x 256 tiles too
+    dims, sym = moe.launch_geometry(6, d5, 4096)  # down
+    assert sym == "lf_moe_down_t256_b128" and dims.grid == (2048 // 256 * (4096 * 6 // 256 + 64), 1, 1)
+    assert dims.block == (512, 1, 1)
+    dims, sym = moe.launch_geometry(4, d5, 4096)  # gate/up
+    assert sym == "lf_moe_gate_up_t256_b128" and dims.grid == (1408 // 128 * (4096 * 6 // 256 + 64), 1, 1)
+    # fewer rows per expert, or K > 3072: 128 x 128 tiles
+    dims, sym = moe.launch_geometry(6, d5, 2048)
+    assert sym == "lf_moe_down_b128" and dims.grid == (2048 // 128 * (2048 * 6 // 128 + 64), 1, 1)
+    d6 = moe.moe_descriptor(8, 2, 1, 4096, 1408, 128)
+    assert moe.launch_geometry(4, d6, 4096)[1] == "lf_moe_gate_up_b128"
     # profiles of at most 32 tokens: the grouped GEMV form, a block per
     # (expert, 64 columns), either scale mode
     # (a fixed grid of at most 1024 blocks looping over the items)

@@ -44,7 +44,11 @@ def dequant_experts(q, s, block):
                      for e in range(q.shape[0])])
 
 
-def run_case(rt, rng, t, e, k, hidden, inter, mode, block, logits=None, max_tokens=None):
+def run_case(rt, rng, t, e, k, hidden, inter, mode, block, logits=None, max_tokens=None,
+             zero_groups=False):
+    """zero_groups (block scales): every third token's second 128-column group
+    of x and the first 128 x 128 block of every gate, up and down weight are
+    zero, so those scales are 0."""
     from lunaflux_amd import fp8, moe
     x = synth.activations(rng, t, hidden)
     if logits is None:
@@ -52,6 +56,11 @@ def run_case(rt, rng, t, e, k, hidden, inter, mode, block, logits=None, max_toke
     qg, sg = expert_weights(rng, e, inter, hidden, block)
     qu, su = expert_weights(rng, e, inter, hidden, block)
     qd, sd = expert_weights(rng, e, hidden, inter, block)
+    if zero_groups:
+        x[::3, 128:256] = 0
+        for q, sc in ((qg, sg), (qu, su), (qd, sd)):
+            q[:, :128, :128] = 0
+            sc.reshape(e, q.shape[1] // 128, q.shape[2] // 128)[:, 0, 0] = 0
     smode = fp8.BLOCK128 if block else fp8.PER_CHANNEL
     wg, wu, wd = (rt.upload_weight(q, s, smode) for q, s in ((qg, sg), (qu, su), (qd, sd)))
     out, inter_state = moe.moe_expert_mlp(rt, x, logits, wg, wu, wd, k, mode, 128 if block else 0,
@@ -201,21 +210,30 @@ def test_moe_zero_tokens(rt):
     assert out.shape == (0, 256)
 
 
-@pytest.mark.parametrize("t,e,k,hidden,inter,skew", [
-    (1024, 8, 2, 512, 384, 1.5), (700, 4, 2, 256, 256, 0.0), (1100, 8, 2, 256, 640, 3.0),
+@pytest.mark.parametrize("t,e,k,hidden,inter,skew,block", [
+    (1024, 8, 2, 512, 384, 1.5, False), (700, 4, 2, 256, 256, 0.0, False),
+    (1100, 8, 2, 256, 640, 3.0, False), (1024, 8, 2, 512, 384, 1.5, True),
+    (700, 4, 2, 256, 256, 0.0, True), (1100, 8, 2, 256, 640, 3.0, True),
+    (1500, 16, 4, 768, 384, 1.0, "zero_groups"),
 ])
-def test_moe_t256(rt, t, e, k, hidden, inter, skew):
+def test_moe_t256(rt, t, e, k, hidden, inter, skew, block):
     """Profiles averaging >= 256 routed rows per expert run the grouped GEMMs
     on 256 x 256 tiles: experts with several 256-row tiles, a partial last
     tile, skewed load (bias N(0, skew)) and, for the larger skew, experts left
-    with few or no rows."""
+    with few or no rows; per-channel and 128 x 128 block scales (rescaled
+    accumulators), the latter also with all-zero activation groups and
+    weight blocks (zero scales carried over)."""
     from lunaflux_amd import _abi, moe
-    desc = moe.moe_descriptor(e, k, 0, hidden, inter, 0)
-    assert moe.launch_geometry(_abi.MOE_GATE_UP, desc, t)[1] == "lf_moe_gate_up_t256"
-    assert moe.launch_geometry(_abi.MOE_DOWN, desc, t)[1] == "lf_moe_down_t256"
-    rng = np.random.default_rng(950 + t + e)
+    zero = block == "zero_groups"
+    block = bool(block)
+    mode = 1 if block else 0
+    desc = moe.moe_descriptor(e, k, mode, hidden, inter, 128 if block else 0)
+    suffix = "_b128" if block else ""
+    assert moe.launch_geometry(_abi.MOE_GATE_UP, desc, t)[1] == "lf_moe_gate_up_t256" + suffix
+    assert moe.launch_geometry(_abi.MOE_DOWN, desc, t)[1] == "lf_moe_down_t256" + suffix
+    rng = np.random.default_rng(950 + t + e + block)
     logits = (rng.standard_normal((t, e)) + rng.normal(0, skew, e)).astype(np.float32)
-    x, logits, weights, out, st = run_case(rt, rng, t, e, k, hidden, inter, 0, block=False,
-                                           logits=logits)
-    ex, w = check_routing(logits, k, 0, st)
-    check_output(x, weights, ex, w, out, False, f"moe t256 t={t} e={e} skew={skew}", st)
+    x, logits, weights, out, st = run_case(rt, rng, t, e, k, hidden, inter, mode, block=block,
+                                           logits=logits, zero_groups=zero)
+    ex, w = check_routing(logits, k, mode, st)
+    check_output(x, weights, ex, w, out, block, f"moe t256 t={t} e={e} skew={skew} block={block}", st)
