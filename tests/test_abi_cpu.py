@@ -178,8 +178,13 @@ def test_launch_geometry():
             == fp8.launch_geometry(_abi.ENTRY_W8A8_QKV, 6144, 4096, 2048)[1])
     with pytest.raises(fp8.DeviceError):
         fp8.w8a16_workspace_bytes(_abi.ENTRY_W8A8_DENSE, 4096, 4096, 16)
-    # W8A8: 256 x 256 tiles (1-D grid, 512 threads) once there is a tile per
-    # CU, 128 x 128 tiles (256 threads) below that or when N does not divide.
+    # W8A8: 256 x 256 tiles (1-D grid, 512 threads) from 192 of them (3/4 of
+    # a tile per CU), 128 x 128 tiles (256 threads) below that or when N does
+    # not divide.
+    dims, sym = fp8.launch_geometry(_abi.ENTRY_W8A8_QKV, 6144, 4096, 2048)
+    assert sym == "lf_fp8_w8a8_qkv_t256" and dims.grid == (8 * 24, 1, 1)
+    dims, sym = fp8.launch_geometry(_abi.ENTRY_W8A8_DENSE, 4096, 4096, 2048)
+    assert sym == "lf_fp8_w8a8_dense_t128" and dims.grid == (16 * 32, 1, 1)
     dims, sym = fp8.launch_geometry(_abi.ENTRY_W8A8_GATE_UP, 14336, 4096, 8192)
     assert sym == "lf_fp8_w8a8_gate_up_t256" and dims.grid == (32 * 112, 1, 1) and dims.block == (512, 1, 1)
     dims, sym = fp8.launch_geometry(_abi.ENTRY_W8A8_DENSE, 4096, 14336, 2048)
