@@ -134,7 +134,7 @@ def check_output(x, weights, ex, w, out, block, label, st):
 
 @pytest.mark.parametrize("t,e,k,mode", [(100, 8, 2, 0), (37, 64, 6, 1), (1, 8, 2, 0), (300, 16, 4, 0),
                                          (1500, 32, 4, 1), (50, 6, 2, 1), (40, 130, 3, 1),
-                                         (60, 130, 5, 0)])
+                                         (60, 130, 5, 0), (80, 16, 10, 1)])
 def test_moe_per_channel(rt, t, e, k, mode):
     rng = np.random.default_rng(700 + t + e)
     x, logits, weights, out, st = run_case(rt, rng, t, e, k, 256, 384, mode, block=False)
