@@ -270,7 +270,7 @@ int64_t lunaflux_fp8_moe_workspace_bytes(const lf_fp8_moe_desc *desc,
  * offsets (int32 [E+1]), expert 128-row tile offsets (int32 [E+1]) followed
  * by the 256-row tile offsets (int32 [E+1]), the number of experts with rows
  * (int32) and their ids ascending (int32 [E]), e4m3
- * tokens [T, H], token scales, h bf16 [T*k, I], e4m3 h, h scales, y fp32
+ * tokens [T, H], token scales, h bf16 [T*k, I], e4m3 h, h scales, y bf16
  * [T*k, H], end. */
 int32_t lunaflux_fp8_moe_workspace_layout(const lf_fp8_moe_desc *desc,
                                           int32_t tokens, int64_t offsets[13]);

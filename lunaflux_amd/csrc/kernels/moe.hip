@@ -16,7 +16,7 @@
 //                         bf16 in expert order
 //   lf_moe_quant_hidden   h -> e4m3 + scales
 //   lf_moe_down           grouped GEMM over expert down weights -> y [T*k, H]
-//                         fp32 in expert order
+//                         bf16 in expert order
 //   lf_moe_combine        out[t] = sum_j w[t, j] * y[pos(t, j)] (j ascending)
 //                         -> bf16 [T, H]
 #include "w8a8_core.h"
@@ -391,7 +391,7 @@ struct BlockScaleFold {
 
 // STAGE 0: gate/up (x rows gathered by token, SwiGLU, bf16 h): a block
 // computes 64 h-columns (wave wn: its kFN / 2 gate tiles, then the up tiles
-// of the same columns). STAGE 1: down (h rows in expert order, fp32 y): a
+// of the same columns). STAGE 1: down (h rows in expert order, bf16 y): a
 // block computes 128 columns.
 template <int STAGE, bool BLOCK>
 __device__ void grouped_gemm(const int32_t *counts, const MoeDesc &d, const uint8_t *w0,
@@ -525,11 +525,12 @@ __device__ void grouped_gemm(const int32_t *counts, const MoeDesc &d, const uint
           hrow[c] = static_cast<uint16_t>(f32_to_bf16(silu_mul(gv, uv)));
         }
       } else {
-        float *yrow = at<float>(ws, L.y) + static_cast<uint64_t>(pp) * N;
+        uint16_t *yrow = at<uint16_t>(ws, L.y) + static_cast<uint64_t>(pp) * N;
 #pragma unroll
         for (int j = 0; j < T::kFN; ++j) {
           const int c = col[j] + r;
-          yrow[c] = BLOCK ? acc[i][j][rr] : acc[i][j][rr] * sav[i][rr] * swv[j];
+          yrow[c] = static_cast<uint16_t>(
+              f32_to_bf16(BLOCK ? acc[i][j][rr] : acc[i][j][rr] * sav[i][rr] * swv[j]));
         }
       }
     }
@@ -741,8 +742,8 @@ __device__ void grouped_gemm_t256(const int32_t *counts, const MoeDesc &d, const
   }
   if (threadIdx.x < BM) sa_tile[threadIdx.x] = sa_mine;
   // The output goes through LDS in 16-byte row chunks (w8a8v4::StageTile):
-  // STAGE 0 stages 32 rows x 64 h-columns of bf16 per pass, STAGE 1 16 rows
-  // x 128 columns of fp32 (16 of the 32 rows a fragment row holds).
+  // STAGE 0 stages 32 rows x 64 h-columns of bf16 per pass, STAGE 1 32 rows
+  // x 128 columns of bf16.
   const int col0 = __builtin_amdgcn_readfirstlane(ocol[0] - c);
   w8a8v4::epilogue_barrier();
   const int pw = p0 + wm * T::kWaveM;
@@ -770,28 +771,25 @@ __device__ void grouped_gemm_t256(const int32_t *counts, const MoeDesc &d, const
       });
     }
   } else {
-    using Stage = w8a8v4::StageTile<float, 16, T::kWaveN>;
+    using Stage = w8a8v4::StageTile<uint16_t, 32, T::kWaveN>;
     static_assert(Stage::kBytes * T::kWaves <= T::kSmem, "staging fits the stage ring");
-    const Stage st{reinterpret_cast<float *>(smem + wave * Stage::kBytes)};
-    float *y = at<float>(ws, L.y);
+    const Stage st{reinterpret_cast<uint16_t *>(smem + wave * Stage::kBytes)};
+    uint16_t *y = at<uint16_t>(ws, L.y);
 #pragma unroll
     for (int i = 0; i < T::kFM; ++i) {
 #pragma unroll
-      for (int half = 0; half < 2; ++half) {
-        // accumulator registers 8 half .. 8 half + 7 hold rows 16 half .. + 15
+      for (int r = 0; r < 16; ++r) {
+        const float sa = sa_tile[wm * T::kWaveM + w8a8v4::acc_row<T>(i, lane, r)];
 #pragma unroll
-        for (int r = 8 * half; r < 8 * half + 8; ++r) {
-          const float sa = sa_tile[wm * T::kWaveM + w8a8v4::acc_row<T>(i, lane, r)];
-#pragma unroll
-          for (int j = 0; j < T::kFN; ++j) {
-            st.put(w8a8v4::acc_row<T>(0, lane, r) - 16 * half, ocol[j] - col0, acc[i][j][r] * sa * swv[j]);
-          }
+        for (int j = 0; j < T::kFN; ++j) {
+          st.put(w8a8v4::acc_row<T>(0, lane, r), ocol[j] - col0,
+                 static_cast<uint16_t>(f32_to_bf16(acc[i][j][r] * sa * swv[j])));
         }
-        const int p_i = pw + 32 * i + 16 * half;
-        st.flush(lane, [&](int row) -> float * {
-          return p_i + row < pend ? y + static_cast<uint64_t>(p_i + row) * N + col0 : nullptr;
-        });
       }
+      const int p_i = pw + 32 * i;
+      st.flush(lane, [&](int row) -> uint16_t * {
+        return p_i + row < pend ? y + static_cast<uint64_t>(p_i + row) * N + col0 : nullptr;
+      });
     }
   }
 }
@@ -1005,8 +1003,8 @@ LF_DEVICE void grouped_gemv(const int32_t *counts, const MoeDesc &d, const uint8
           at<uint16_t>(ws, L.h)[static_cast<uint64_t>(p) * N + col] =
               static_cast<uint16_t>(f32_to_bf16(silu_mul(gv, uv)));
         } else {
-          at<float>(ws, L.y)[static_cast<uint64_t>(p) * N + col] =
-              BLOCK ? acc[0][q] : acc[0][q] * sa * sw[0];
+          at<uint16_t>(ws, L.y)[static_cast<uint64_t>(p) * N + col] =
+              static_cast<uint16_t>(f32_to_bf16(BLOCK ? acc[0][q] : acc[0][q] * sa * sw[0]));
         }
       }
     }
@@ -1022,31 +1020,32 @@ LF_DEVICE void combine(const int32_t *counts, const MoeDesc &d, uint8_t *ws, uin
   const int H = d.hidden;
   const float *w = at<float>(ws, L.topk_w) + static_cast<uint64_t>(t) * d.top_k;
   const int32_t *pos = at<int32_t>(ws, L.pos) + static_cast<uint64_t>(t) * d.top_k;
-  const float *y = at<float>(ws, L.y);
-  // four columns per thread (H % 128 == 0); the k rows' loads are all issued
-  // before the sum, whose terms are added in slot order j
+  const uint16_t *y = at<uint16_t>(ws, L.y);
+  // eight columns per thread (H % 128 == 0); the k rows' loads are all
+  // issued before the sum, whose terms are added in slot order j
   constexpr int kMaxK = 16;  // desc_ok bounds top_k
   const int k = d.top_k;
-  for (int c = 4 * threadIdx.x; c < H; c += 4 * blockDim.x) {
-    f32x4 v[kMaxK];
+  for (int c = 8 * threadIdx.x; c < H; c += 8 * blockDim.x) {
+    u32x4 v[kMaxK];
     static_for<kMaxK>([&](auto j) {
-      if (j < k) v[j] = *reinterpret_cast<const f32x4 *>(y + static_cast<uint64_t>(pos[j]) * H + c);
+      if (j < k) v[j] = *reinterpret_cast<const u32x4 *>(y + static_cast<uint64_t>(pos[j]) * H + c);
     });
-    f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+    float acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
     static_for<kMaxK>([&](auto j) {
       if (j < k) {
         const float wj = w[j];
 #pragma unroll
-        for (int q = 0; q < 4; ++q) {
-          const float prod = wj * v[j][q];
+        for (int q = 0; q < 8; ++q) {
+          const uint32_t word = v[j][q >> 1];
+          const float prod = wj * bf16_to_f32((q & 1) ? word >> 16 : word & 0xffffu);
           acc[q] = acc[q] + prod;
         }
       }
     });
-    uint2 packed;
-    packed.x = f32_to_bf16(acc[0]) | (f32_to_bf16(acc[1]) << 16);
-    packed.y = f32_to_bf16(acc[2]) | (f32_to_bf16(acc[3]) << 16);
-    *reinterpret_cast<uint2 *>(out + static_cast<uint64_t>(t) * H + c) = packed;
+    u32x4 packed;
+#pragma unroll
+    for (int q = 0; q < 4; ++q) packed[q] = f32_to_bf16(acc[2 * q]) | (f32_to_bf16(acc[2 * q + 1]) << 16);
+    *reinterpret_cast<u32x4 *>(out + static_cast<uint64_t>(t) * H + c) = packed;
   }
 }
 

@@ -154,6 +154,6 @@ def moe_expert_mlp(rt: ProjectionRuntime, x: np.ndarray, logits: np.ndarray, wg:
         h=ws.read(np.uint16, (a, i), lay["h"]),
         hq=ws.read(np.uint8, (a, i), lay["hq"]),
         hs=ws.read(np.float32, (a, gh), lay["hs"]),
-        y=ws.read(np.float32, (a, hdim), lay["y"]),
+        y=(ws.read(np.uint16, (a, hdim), lay["y"]).astype(np.uint32) << 16).view(np.float32),
     )
     return out, inter
