@@ -304,7 +304,7 @@ def moe_flops(c):
     return 2 * a * c["hidden"] * 2 * c["inter"] + 2 * a * c["inter"] * c["hidden"]
 
 
-def moe_bench(rt, c, steps=5, warmup=2, seed=4242):
+def moe_bench(rt, c, steps=12, warmup=3, seed=4242):
     """Times the launches of one MoE expert-MLP operation with events
     between them. Expert weights are E copies of one seeded draw (kernel time
     does not depend on the values; it keeps setup short)."""
