@@ -532,7 +532,7 @@ def main():
         return
     if args.gpus != 1:
         print(f"bench.py measures one GPU only: --gpus {args.gpus} is not supported "
-              "(this build has no multi-GPU path; see DESIGN.md on sharding)", file=sys.stderr)
+              "(this build has no multi-GPU path; one GPU runs each kernel at a shard's shape)", file=sys.stderr)
         sys.exit(2)
     if args.pmc_pass:
         pmc_pass()
