@@ -946,6 +946,6 @@ LF_W16_FIXED_GATE_UP_G(4096, 128, 8, 1, 4, 2, 1)
 // tiles to fill the chip without a K split, as gate/up.
 LF_W16_FIXED_DENSE_WIDE_G(4096, 16, 1, 1, 2, 4, 2)
 LF_W16_FIXED_DENSE_WIDE_G(4096, 32, 2, 1, 4, 3, 2)
-LF_W16_FIXED_DENSE_WIDE_G(4096, 128, 8, 1, 4, 2, 1)
+LF_W16_FIXED_DENSE_WIDE_G(4096, 128, 8, 1, 8, 2, 1)
 
 }  // extern "C"

@@ -112,7 +112,7 @@ constexpr int64_t kWideN = 16384;
 constexpr W8a16Fixed kW8a16Fixed[] = {
     {LF_FP8_ENTRY_W8A16_DENSE, 4096, 0, 0, 1, true, 2, 1, "lf_fp8_w8a16_dense_wide_k4096_m16", kWideN},
     {LF_FP8_ENTRY_W8A16_DENSE, 4096, 0, 0, 2, true, 4, 1, "lf_fp8_w8a16_dense_wide_k4096_m32", kWideN},
-    {LF_FP8_ENTRY_W8A16_DENSE, 4096, 0, 0, 8, true, 4, 1, "lf_fp8_w8a16_dense_wide_k4096_m128", kWideN},
+    {LF_FP8_ENTRY_W8A16_DENSE, 4096, 0, 0, 8, true, 8, 1, "lf_fp8_w8a16_dense_wide_k4096_m128", kWideN},
     {LF_FP8_ENTRY_W8A16_DENSE, 4096, 0, 0, 1, false, 8, 1, "lf_fp8_w8a16_dense_k4096_m16"},
     {LF_FP8_ENTRY_W8A16_DENSE, 4096, 0, 0, 2, false, 8, 1, "lf_fp8_w8a16_dense_k4096_m32"},
     {LF_FP8_ENTRY_W8A16_DENSE, 14336, 0, 0, 1, false, 8, 1, "lf_fp8_w8a16_dense_k14336_m16"},

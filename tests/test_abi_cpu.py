@@ -166,7 +166,7 @@ def test_launch_geometry():
     dims, sym = fp8.launch_geometry(_abi.ENTRY_W8A16_GATE_UP, 14336, 4096, 128)
     assert sym == "lf_fp8_w8a16_gate_up_k4096_m128" and dims.grid == (224, 1, 1)
     # wide dense shapes (N >= 16384, e.g. the 128,256-column vocabulary head)
-    for mt, w in ((16, 2), (32, 4), (128, 4)):
+    for mt, w in ((16, 2), (32, 4), (128, 8)):
         dims, sym = fp8.launch_geometry(_abi.ENTRY_W8A16_DENSE, 128256, 4096, mt)
         assert sym == f"lf_fp8_w8a16_dense_wide_k4096_m{mt}" and dims.grid == (8016 // w, 1, 1)
         assert dims.block == (64 * w, 1, 1)
