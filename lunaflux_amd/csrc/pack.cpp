@@ -127,7 +127,7 @@ constexpr W8a16Fixed kW8a16Fixed[] = {
     {LF_FP8_ENTRY_W8A16_DENSE, 14336, 0, 0, 8, true, 4, 4, "lf_fp8_w8a16_dense_k14336_m128"},
     {LF_FP8_ENTRY_W8A16_QKV, 4096, 4096, 1024, 8, true, 4, 2,
      "lf_fp8_w8a16_qkv_k4096_q4096_kv1024_m128"},
-    {LF_FP8_ENTRY_W8A16_GATE_UP, 4096, 0, 0, 8, true, 8, 2, "lf_fp8_w8a16_gate_up_k4096_m128"},
+    {LF_FP8_ENTRY_W8A16_GATE_UP, 4096, 0, 0, 8, true, 4, 1, "lf_fp8_w8a16_gate_up_k4096_m128"},
 };
 
 // The specialized entry for (entry, N, K, Q / K-V split, profile), or null.
