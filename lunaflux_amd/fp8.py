@@ -7,11 +7,15 @@ launch steps for the FP8 families and offers numpy-level calls named after
 the reference kernels they replace (kernels/reference/basic.mbt:102-153,
 mlp.mbt:4-39), so parity tests read like the reference's own tests:
 
-  dense_projection(x, w)          output / down / LM-head projection
+  dense_projection(x, w)          output / down projection
+  language_model_head(x, w)       vocabulary logits (the dense entry)
   qkv_projection(x, wq, wk, wv)   packed Q|K|V
   gate_up_swiglu(x, wg, wu)       silu(x Wg^T) * (x Wu^T), the first half of
                                   silu_gated_mlp
   silu_gated_mlp(x, wg, wu, wd)   the whole GatedMlp operation
+  rms_norm_quant(x, g, w, eps)    RmsNorm (kernels/reference/basic.mbt:32-68)
+                                  written as the per-token e4m3 rows the W8A8
+                                  projection with first weight w reads
 
 Two families (include/lunaflux_fp8.h): "w8a16" (bf16 activations, decode)
 and "w8a8" (per-token e4m3 activations, prefill). Activations and outputs
