@@ -433,3 +433,26 @@ def test_w8a16_specialized_entry_rejects_other_shape(rt):
                             w.region, _region(ya, alignment=256), _region(ws, alignment=256)])
     rt.function(sym).launch_synchronous(dims, args, rt.stream)
     assert np.all(ya.read(np.uint16, (16 * n,)) == 0x7FC1)
+
+
+def test_checkpoint_weight_through_the_dense_entry(rt, tmp_path):
+    """An FP8 weight admitted from a safetensors file (per-channel scales),
+    uploaded and run through the W8A16 and W8A8 dense entries."""
+    import json
+    import struct
+    from lunaflux_amd import checkpoint
+    rng = np.random.default_rng(4321)
+    q, s = synth.weight(rng, 512, 1024)
+    blobs = [q.tobytes(), s.reshape(-1, 1).tobytes()]
+    header = {"proj.weight": {"dtype": "F8_E4M3", "shape": [512, 1024], "data_offsets": [0, len(blobs[0])]},
+              "proj.weight_scale": {"dtype": "F32", "shape": [512, 1],
+                                    "data_offsets": [len(blobs[0]), len(blobs[0]) + len(blobs[1])]}}
+    text = json.dumps(header).encode()
+    path = str(tmp_path / "proj.safetensors")
+    with open(path, "wb") as f:
+        f.write(struct.pack("<Q", len(text)) + text + b"".join(blobs))
+    w = checkpoint.upload_linear(rt, path, "proj")
+    x = synth.activations(rng, 20, 1024)
+    for family in ("w8a16", "w8a8"):
+        y = rt.dense_projection(x, w, family, max_tokens=32)
+        check_projection(y, x_ref(x, family), deq(q, s), f"checkpoint weight {family}")
