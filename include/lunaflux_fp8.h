@@ -79,11 +79,15 @@ int32_t lunaflux_fp8_weight_region_bytes(int32_t scale_mode, int64_t rows,
 
 /* The pre-swizzle model/device_materialize applies per tensor
  * (model/device_materialize/layout.mbt:37-93 places tensors; this fills one
- * placed region). q: E x [N, K] row-major e4m3 codes; scales: E x the scale
- * block above, unpadded. Writes the whole region (header included). */
+ * placed region). q: E x [N, K] row-major e4m3 codes (q_bytes = E N K);
+ * scales: E x the scale block above, unpadded (scale_count = E N for per
+ * channel, E (N/128)(K/128) for blocks). Writes the whole region (header
+ * included); LF_INVALID_ARGUMENT, with nothing read, when a count or the
+ * region size does not match the shape. */
 int32_t lunaflux_fp8_pack_weight(int32_t scale_mode, int64_t rows,
                                  int64_t columns, int32_t experts,
-                                 const uint8_t *q, const float *scales,
+                                 const uint8_t *q, int64_t q_bytes,
+                                 const float *scales, int64_t scale_count,
                                  uint8_t *region, int64_t region_bytes);
 /* Inverse of the pack (tests and tooling). */
 int32_t lunaflux_fp8_unpack_weight(const uint8_t *region, int64_t region_bytes,
@@ -142,8 +146,28 @@ enum lf_fp8_entry {
   LF_FP8_ENTRY_W8A8_DENSE = 5,
   LF_FP8_ENTRY_W8A8_QKV = 6,
   LF_FP8_ENTRY_W8A8_GATE_UP = 7,
-  LF_FP8_ENTRY_RMS_NORM_QUANT_ROWS = 8
+  LF_FP8_ENTRY_RMS_NORM_QUANT_ROWS = 8,
+  LF_FP8_ENTRY_GROUPED = 9 /* admission only: the MoE expert weights */
 };
+
+/* Admission of one weight operand's region before an operation is bound,
+ * the FP8 counterpart of the exact BF16 size check engine/device_plan applies
+ * to every weight region (build.mbt:149-203). region_head: the region's
+ * first LF_FP8_HEADER_BYTES (the header the pack wrote, kept by the
+ * materializer); region_bytes: the TensorRef region's size. The header must
+ * carry the format's magic, version and layout, the shape (rows = N,
+ * columns = K, experts; 1 for the dense families) and the format's own
+ * offsets, and region_bytes must equal lunaflux_fp8_weight_region_bytes for
+ * it. LF_UNSUPPORTED for a valid region with 128 x 128 block scales on a
+ * dense, QKV or gate/up entry (their kernels read one scale per output
+ * channel; only LF_FP8_ENTRY_GROUPED admits block scales);
+ * LF_INVALID_ARGUMENT for anything else that does not hold. The
+ * shape-specialized W8A16 entries start streaming weights before they read
+ * the header, so this check is what bounds their reads. */
+int32_t lunaflux_fp8_admit_weight(int32_t entry, const uint8_t *region_head,
+                                  int64_t head_bytes, int64_t region_bytes,
+                                  int64_t rows, int64_t columns,
+                                  int32_t experts);
 
 /* Launch geometry a manifest records for (entry, output width N, input width
  * K, profile max_query_tokens): grid xyz, block xyz, dynamic LDS bytes and

@@ -48,6 +48,7 @@ ENTRY_W8A8_DENSE = 5
 ENTRY_W8A8_QKV = 6
 ENTRY_W8A8_GATE_UP = 7
 ENTRY_RMS_NORM_QUANT_ROWS = 8
+ENTRY_GROUPED = 9
 
 _vp = ctypes.c_void_p
 _i32 = ctypes.c_int32
@@ -94,7 +95,9 @@ SIGNATURES = {
     "lunaflux_hip_bf16_gemm_plan_close": (_i32, [_vp]),
     "lunaflux_hip_bf16_gemm_plan_run": (_i32, [_vp, _vp, _i64, _vp, _i64, _vp, _i64, _vp, _i64, _vp]),
     "lunaflux_fp8_weight_region_bytes": (_i32, [_i32, _i64, _i64, _i32, _i64p]),
-    "lunaflux_fp8_pack_weight": (_i32, [_i32, _i64, _i64, _i32, _u8p, _f32p, _u8p, _i64]),
+    "lunaflux_fp8_pack_weight": (_i32, [_i32, _i64, _i64, _i32, _u8p, _i64, _f32p, _i64, _u8p,
+                                        _i64]),
+    "lunaflux_fp8_admit_weight": (_i32, [_i32, _u8p, _i64, _i64, _i64, _i64, _i32]),
     "lunaflux_fp8_unpack_weight": (_i32, [_u8p, _i64, _u8p, _i64, _f32p, _i64]),
     "lunaflux_fp8_act_quant_bytes": (_i64, [_i64, _i64]),
     "lunaflux_fp8_w8a16_workspace_bytes": (_i64, [_i32, _i64, _i64, _i32]),

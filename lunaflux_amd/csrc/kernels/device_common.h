@@ -47,6 +47,25 @@ LF_DEVICE const WeightHeader &header_of(const uint8_t *region) {
   return *reinterpret_cast<const WeightHeader *>(region);
 }
 
+// The dense, QKV and gate/up kernels read one fp32 scale per output channel
+// (s[n] for n < N). A 128 x 128 block-scaled region holds (N/128)(K/128)
+// scales, so those kernels refuse it (and a region without the pack's magic)
+// before any other read; the host admission rejects such a binding with
+// LF_UNSUPPORTED. MODE 1 (QKV) checks all three weights.
+template <int MODE>
+LF_DEVICE bool dense_regions_ok(const uint8_t *w0, const uint8_t *w1, const uint8_t *w2) {
+  bool ok = header_of(w0).magic == kWeightMagic && header_of(w0).scale_mode == kScalePerChannel;
+  if (MODE != 0) {
+    ok = ok && header_of(w1).magic == kWeightMagic &&
+         header_of(w1).scale_mode == kScalePerChannel;
+  }
+  if (MODE == 1) {
+    ok = ok && header_of(w2).magic == kWeightMagic &&
+         header_of(w2).scale_mode == kScalePerChannel;
+  }
+  return ok;
+}
+
 LF_DEVICE const uint8_t *expert_tiles(const uint8_t *region, int expert) {
   const WeightHeader &h = header_of(region);
   return region + h.tile_offset + static_cast<uint64_t>(expert) * h.tile_bytes;

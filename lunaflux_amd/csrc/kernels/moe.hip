@@ -89,6 +89,17 @@ LF_DEVICE void wave_lds_sync() {
   __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
 }
 
+// The ranking key of a logit: the logit itself, with NaN as -inf. On these
+// keys "beats" (u > v, or u == v and a lower id) is a strict total order, so
+// the ranks of one token's experts are a permutation of 0 .. E-1 and every
+// pick slot r < k is written once, whatever the logits hold. A NaN logit thus
+// ranks below every finite one (ties by id); a token whose top key is
+// non-finite (+inf, or every logit NaN or -inf) gets NaN weights, and its
+// output row comes out NaN. The reference rejects non-finite values
+// (kernels/reference/basic.mbt:91-93); a kernel cannot raise, so it keeps
+// every index in range and lets the value carry the fault.
+LF_DEVICE float rank_key(float v) { return __builtin_isnan(v) ? -__builtin_inff() : v; }
+
 LF_DEVICE void route(const int32_t *counts, const MoeDesc &d, const float *logits, uint8_t *ws) {
   __shared__ __attribute__((aligned(16))) float sv[4][256];
   __shared__ int32_t sid[4][16];
@@ -107,7 +118,7 @@ LF_DEVICE void route(const int32_t *counts, const MoeDesc &d, const float *logit
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
     const int e = lane + 64 * i;
-    v[i] = e < E ? l[e] : 0.0f;
+    v[i] = e < E ? rank_key(l[e]) : 0.0f;
     if (e < E) sv[w][e] = v[i];
   }
   wave_lds_sync();
@@ -175,6 +186,15 @@ constexpr int kSortWaves = kSortThreads / 64;
 
 LF_DEVICE int32_t *chunk_table(uint8_t *ws, const MoeLayout &L) { return at<int32_t>(ws, L.y); }
 
+// An expert id read back from the workspace, as both sort kernels use it:
+// lf_moe_route writes only ids in [0, E), so this is the identity there; an id
+// outside that range (a workspace written by something else) counts as
+// expert 0 in both kernels alike, so every assignment still gets exactly one
+// position and no count or position index leaves its array.
+LF_DEVICE int sort_expert(int32_t id, int E) {
+  return static_cast<uint32_t>(id) < static_cast<uint32_t>(E) ? id : 0;
+}
+
 LF_DEVICE void sort_count(const int32_t *counts, const MoeDesc &d, uint8_t *ws) {
   __shared__ int32_t cnt[256];
   const int T = live_rows(counts, 1 << 30);
@@ -186,7 +206,7 @@ LF_DEVICE void sort_count(const int32_t *counts, const MoeDesc &d, uint8_t *ws) 
   for (int e = tid; e < E; e += kSortThreads) cnt[e] = 0;
   __syncthreads();
   const int a = c * kSortThreads + tid;
-  if (a < A) atomicAdd(&cnt[at<int32_t>(ws, L.topk_ids)[a]], 1);
+  if (a < A) atomicAdd(&cnt[sort_expert(at<int32_t>(ws, L.topk_ids)[a], E)], 1);
   __syncthreads();
   int32_t *table = chunk_table(ws, L) + static_cast<uint64_t>(c) * E;
   for (int e = tid; e < E; e += kSortThreads) table[e] = cnt[e];
@@ -297,7 +317,7 @@ LF_DEVICE void sort_assignments(const int32_t *counts, const MoeDesc &d, uint8_t
   const uint64_t lt_mask = lane == 0 ? 0ull : (~0ull >> (64 - lane));
   __syncthreads();
   const int a = c * kSortThreads + tid;
-  const int e = a < A ? ids[a] : E;  // E marks lanes past the end
+  const int e = a < A ? sort_expert(ids[a], E) : E;  // E marks lanes past the end
   uint64_t same = ~0ull;
   for (int b = 0; b < bits; ++b) {
     const uint64_t ones = __ballot((e >> b) & 1);
@@ -1032,6 +1052,10 @@ LF_DEVICE void combine(const int32_t *counts, const MoeDesc &d, uint8_t *ws, uin
     });
     float acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
     static_for<kMaxK>([&](auto j) {
+      // product and sum each rounded (no fused multiply-add), as the combine
+      // is defined: the output is then bit-identical to that definition for
+      // the same y and weights
+#pragma clang fp contract(off)
       if (j < k) {
         const float wj = w[j];
 #pragma unroll

@@ -312,7 +312,7 @@ __device__ void w8a8_tiled_kernel(const int32_t *counts, const uint8_t *xq, cons
   constexpr int BM = T::kWaveM * T::kWgm, BN = T::kWaveN * T::kWgn;
   __shared__ __attribute__((aligned(1024))) uint8_t smem[T::kSmem];
   const WeightHeader &h0 = header_of(w0);
-  if (h0.magic != kWeightMagic) return;
+  if (!dense_regions_ok<MODE>(w0, w1, w2)) return;
   const int K = static_cast<int>(h0.columns);
   const int KT = K >> 7;
   const int M = live_rows(counts, 1 << 30);
@@ -433,7 +433,7 @@ __device__ void w8a8_v4_kernel(const int32_t *counts, const uint8_t *xq, const u
   constexpr int BM = T::kBM, BN = T::kBN;
   __shared__ __attribute__((aligned(1024))) uint8_t smem[T::kSmem];
   const WeightHeader &h0 = header_of(w0);
-  if (h0.magic != kWeightMagic) return;
+  if (!dense_regions_ok<MODE>(w0, w1, w2)) return;
   const int K = static_cast<int>(h0.columns);
   const int KT = K >> 7;
   const int M = live_rows(counts, 1 << 30);

@@ -228,7 +228,7 @@ __device__ void w8a16_kernel(const int32_t *counts, const uint16_t *x, const uin
   __shared__ int last_block;
 
   const WeightHeader &h0 = header_of(w0);
-  if (h0.magic != kWeightMagic) return;
+  if (!dense_regions_ok<MODE>(w0, w1, w2)) return;
   const int K = static_cast<int>(h0.columns);
   const int KT = K >> 7;
   const int tq = static_cast<int>(h0.rows) >> 4;
@@ -379,7 +379,7 @@ __device__ void w8a16_tile_kernel(const int32_t *counts, const uint16_t *x, cons
   constexpr int NW = MODE == 2 ? 2 : 1;
   __shared__ __attribute__((aligned(16))) f32x4 red[KS][MT * NW][64];
   const WeightHeader &h0 = header_of(w0);
-  if (h0.magic != kWeightMagic) return;
+  if (!dense_regions_ok<MODE>(w0, w1, w2)) return;
   const int K = static_cast<int>(h0.columns);
   const int KT = K >> 7;
   const int tq = static_cast<int>(h0.rows) >> 4;

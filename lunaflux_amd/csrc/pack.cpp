@@ -180,19 +180,22 @@ int32_t lunaflux_fp8_weight_region_bytes(int32_t scale_mode, int64_t rows,
 
 int32_t lunaflux_fp8_pack_weight(int32_t scale_mode, int64_t rows,
                                  int64_t columns, int32_t experts,
-                                 const uint8_t *q, const float *scales,
+                                 const uint8_t *q, int64_t q_bytes,
+                                 const float *scales, int64_t scale_count_arg,
                                  uint8_t *region, int64_t region_bytes) {
   int64_t need = 0;
   int32_t st = lunaflux_fp8_weight_region_bytes(scale_mode, rows, columns, experts, &need);
   if (st != LF_OK) return st;
-  if (q == nullptr || scales == nullptr || region == nullptr || region_bytes != need) {
+  int64_t sc = scale_count(scale_mode, rows, columns);
+  // Both source spans are checked against the shape before anything is read.
+  if (q == nullptr || scales == nullptr || region == nullptr || region_bytes != need ||
+      q_bytes != experts * rows * columns || scale_count_arg != experts * sc) {
     return LF_INVALID_ARGUMENT;
   }
   lf_fp8_weight_header h;
   fill_header(&h, scale_mode, rows, columns, experts);
   std::memset(region, 0, static_cast<size_t>(region_bytes));
   std::memcpy(region, &h, sizeof(h));
-  int64_t sc = scale_count(scale_mode, rows, columns);
   for (int32_t e = 0; e < experts; e += 1) {
     const uint8_t *qe = q + e * rows * columns;
     uint8_t *te = region + h.tile_offset + static_cast<uint64_t>(e) * h.tile_bytes;
@@ -243,6 +246,44 @@ int32_t lunaflux_fp8_unpack_weight(const uint8_t *region, int64_t region_bytes,
                 region + h.scale_offset + static_cast<uint64_t>(e) * h.scale_bytes,
                 static_cast<size_t>(sc) * sizeof(float));
   }
+  return LF_OK;
+}
+
+int32_t lunaflux_fp8_admit_weight(int32_t entry, const uint8_t *region_head, int64_t head_bytes,
+                                  int64_t region_bytes, int64_t rows, int64_t columns,
+                                  int32_t experts) {
+  const bool dense = entry == LF_FP8_ENTRY_W8A16_DENSE || entry == LF_FP8_ENTRY_W8A16_QKV ||
+                     entry == LF_FP8_ENTRY_W8A16_GATE_UP || entry == LF_FP8_ENTRY_W8A8_DENSE ||
+                     entry == LF_FP8_ENTRY_W8A8_QKV || entry == LF_FP8_ENTRY_W8A8_GATE_UP;
+  const bool grouped = entry == LF_FP8_ENTRY_GROUPED;
+  if ((!dense && !grouped) || region_head == nullptr || head_bytes < LF_FP8_HEADER_BYTES ||
+      (dense && experts != 1)) {
+    return LF_INVALID_ARGUMENT;
+  }
+  lf_fp8_weight_header h;
+  std::memcpy(&h, region_head, sizeof(h));
+  if (h.magic != LF_FP8_WEIGHT_MAGIC || h.version != LF_FP8_WEIGHT_VERSION ||
+      h.layout != LF_FP8_LAYOUT_TILE16X128 || h.rows != rows || h.columns != columns ||
+      h.experts != static_cast<uint32_t>(experts)) {
+    return LF_INVALID_ARGUMENT;
+  }
+  const int32_t mode = static_cast<int32_t>(h.scale_mode);
+  int64_t need = 0;
+  if (lunaflux_fp8_weight_region_bytes(mode, rows, columns, experts, &need) != LF_OK) {
+    return LF_INVALID_ARGUMENT;
+  }
+  // Every offset and size in the header must be the format's own, and the
+  // region exactly the format's size: the specialized entries issue their
+  // weight loads before they read the header, so this check is what keeps
+  // them inside the region.
+  lf_fp8_weight_header want;
+  fill_header(&want, mode, rows, columns, experts);
+  if (region_bytes != need || h.tile_offset != want.tile_offset ||
+      h.tile_bytes != want.tile_bytes || h.scale_offset != want.scale_offset ||
+      h.scale_bytes != want.scale_bytes) {
+    return LF_INVALID_ARGUMENT;
+  }
+  if (dense && mode != LF_FP8_SCALE_PER_CHANNEL) return LF_UNSUPPORTED;
   return LF_OK;
 }
 

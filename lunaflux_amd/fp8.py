@@ -52,9 +52,19 @@ def weight_region_bytes(rows: int, columns: int, experts: int = 1,
     return out.value
 
 
+def scale_count(rows: int, columns: int, experts: int = 1, scale_mode: int = PER_CHANNEL) -> int:
+    """fp32 scales of a weight: N per expert per channel, (N/128)(K/128) per
+    expert for 128 x 128 blocks."""
+    per = rows if scale_mode == PER_CHANNEL else (rows // 128) * (columns // 128)
+    return experts * per
+
+
 def pack_weight(q: np.ndarray, scales: np.ndarray, scale_mode: int = PER_CHANNEL) -> np.ndarray:
     """Pre-swizzles e4m3 codes [N, K] (or [E, N, K]) and their fp32 scales
-    into one weight region (header + MFMA-order tiles + scales)."""
+    into one weight region (header + MFMA-order tiles + scales). The scale
+    array must hold exactly the scale block's count (DeviceError
+    INVALID_ARGUMENT otherwise: the library checks both counts before it
+    reads either array)."""
     q = np.ascontiguousarray(q, np.uint8)
     if q.ndim == 2:
         q = q[None]
@@ -64,10 +74,21 @@ def pack_weight(q: np.ndarray, scales: np.ndarray, scale_mode: int = PER_CHANNEL
     region = np.empty(size, np.uint8)
     _check("pack_weight", _abi.lib().lunaflux_fp8_pack_weight(
         scale_mode, rows, columns, experts,
-        q.ctypes.data_as(ctypes.POINTER(ctypes.c_uint8)),
-        scales.ctypes.data_as(ctypes.POINTER(ctypes.c_float)),
+        q.ctypes.data_as(ctypes.POINTER(ctypes.c_uint8)), q.size,
+        scales.ctypes.data_as(ctypes.POINTER(ctypes.c_float)), scales.size,
         region.ctypes.data_as(ctypes.POINTER(ctypes.c_uint8)), size))
     return region
+
+
+def admit_weight(entry: int, head: np.ndarray, region_bytes: int, rows: int, columns: int,
+                 experts: int = 1):
+    """lunaflux_fp8_admit_weight: raises DeviceError (UNSUPPORTED for a
+    block-scaled region on a dense entry, INVALID_ARGUMENT for a region that
+    is not the format's for this shape)."""
+    head = np.ascontiguousarray(head, np.uint8)
+    _check("admit_weight", _abi.lib().lunaflux_fp8_admit_weight(
+        entry, head.ctypes.data_as(ctypes.POINTER(ctypes.c_uint8)), head.size, region_bytes,
+        rows, columns, experts))
 
 
 def unpack_weight(region: np.ndarray):
@@ -134,17 +155,24 @@ def rms_norm_quant_geometry(epsilon: float, k: int, max_rows: int):
 
 @dataclass
 class Fp8Weight:
-    """One device-resident weight region (a TensorRef's region)."""
+    """One device-resident weight region (a TensorRef's region) and the
+    host copy of its header, which admission checks."""
 
     allocation: Allocation
     rows: int
     columns: int
     experts: int
     scale_mode: int
+    header: np.ndarray = None
 
     @property
     def region(self) -> KernelArgument:
         return KernelArgument.device_region(self.allocation, 0, self.allocation.byte_count, 256)
+
+    def admit(self, entry: int):
+        """Admission for an operand of `entry` (lunaflux_fp8_admit_weight)."""
+        admit_weight(entry, self.header, self.allocation.byte_count, self.rows, self.columns,
+                     self.experts)
 
 
 @dataclass
@@ -202,15 +230,12 @@ class ProjectionRuntime:
 
     def upload_weight(self, q: np.ndarray, scales: np.ndarray,
                       scale_mode: int = PER_CHANNEL) -> Fp8Weight:
-        region = pack_weight(q, scales, scale_mode)
-        q3 = q if q.ndim == 3 else q[None]
-        return Fp8Weight(self.context.upload(region), q3.shape[1], q3.shape[2], q3.shape[0],
-                         scale_mode)
+        return self.weight_from_region(pack_weight(q, scales, scale_mode))
 
     def weight_from_region(self, region: np.ndarray) -> Fp8Weight:
         head = np.ascontiguousarray(region[:32]).view(np.uint32)
         return Fp8Weight(self.context.upload(region), int(head[4]), int(head[5]), int(head[6]),
-                         int(head[3]))
+                         int(head[3]), np.array(region[:_abi.LF_FP8_HEADER_BYTES], np.uint8))
 
     def step_counts(self, query_tokens: int, decode: bool = True) -> Allocation:
         """StepCounts int32[5] = {prefill_rows, decode_rows, total_rows,
@@ -256,12 +281,14 @@ class ProjectionRuntime:
                              y: KernelArgument, max_tokens: int) -> LaunchStep:
         """The W8A8 dense GEMM alone, over rows already quantized (by
         bind_rms_norm_quant or bind_act_quant)."""
+        w.admit(_abi.ENTRY_W8A8_DENSE)
         return self._step(_abi.ENTRY_W8A8_DENSE, w.rows, w.columns, max_tokens,
                           [_region(counts, COUNTS_BYTES, alignment=4), xq, w.region, y])
 
     def bind_dense(self, family: str, counts: Allocation, x: KernelArgument, w: Fp8Weight,
                    y: KernelArgument, max_tokens: int) -> BoundOperation:
         _family(family, max_tokens)
+        w.admit(_abi.ENTRY_W8A16_DENSE if family == "w8a16" else _abi.ENTRY_W8A8_DENSE)
         c = _region(counts, COUNTS_BYTES, alignment=4)
         if family == "w8a16":
             return self._w8a16(_abi.ENTRY_W8A16_DENSE, w.rows, w.columns, max_tokens,
@@ -276,6 +303,8 @@ class ProjectionRuntime:
     def bind_qkv(self, family: str, counts: Allocation, x: KernelArgument, wq: Fp8Weight,
                  wk: Fp8Weight, wv: Fp8Weight, y: KernelArgument, max_tokens: int) -> BoundOperation:
         _family(family, max_tokens)
+        for w in (wq, wk, wv):
+            w.admit(_abi.ENTRY_W8A16_QKV if family == "w8a16" else _abi.ENTRY_W8A8_QKV)
         if not (wq.columns == wk.columns == wv.columns) or wk.rows != wv.rows:
             raise DeviceError("qkv shapes", _abi.LF_INVALID_ARGUMENT)
         n = wq.rows + wk.rows + wv.rows
@@ -295,6 +324,8 @@ class ProjectionRuntime:
     def bind_gate_up(self, family: str, counts: Allocation, x: KernelArgument, wg: Fp8Weight,
                      wu: Fp8Weight, h: KernelArgument, max_tokens: int) -> BoundOperation:
         _family(family, max_tokens)
+        for w in (wg, wu):
+            w.admit(_abi.ENTRY_W8A16_GATE_UP if family == "w8a16" else _abi.ENTRY_W8A8_GATE_UP)
         if wg.rows != wu.rows or wg.columns != wu.columns:
             raise DeviceError("gate/up shapes", _abi.LF_INVALID_ARGUMENT)
         c = _region(counts, COUNTS_BYTES, alignment=4)

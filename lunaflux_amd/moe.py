@@ -84,6 +84,7 @@ def bind_moe(rt: ProjectionRuntime, counts, desc: MoeDescriptor, desc_region: Ke
     for w, rows, cols in ((wg, i, h), (wu, i, h), (wd, h, i)):
         if (w.experts, w.rows, w.columns, w.scale_mode) != (e, rows, cols, mode):
             raise DeviceError("moe weight shape", _abi.LF_INVALID_ARGUMENT)
+        w.admit(_abi.ENTRY_GROUPED)
     ws = rt.context.allocate(workspace_bytes(desc, max_tokens))
     wsr = _region(ws, alignment=256)
     c = _region(counts, COUNTS_BYTES, alignment=4)

@@ -326,3 +326,98 @@ def test_rms_norm_quant_geometry():
     with pytest.raises(DeviceError) as err:
         fp8.launch_geometry(_abi.ENTRY_RMS_NORM_QUANT_ROWS, 4096, 4096, 16)
     assert err.value.status == _abi.LF_INVALID_ARGUMENT
+
+
+def test_pack_rejects_scale_and_code_counts_that_do_not_match_the_shape():
+    rng = np.random.default_rng(3)
+    q = rng.integers(0, 256, (128, 256), dtype=np.uint8)
+    # per channel wants N = 128 scales; block scales want (128/128)(256/128) = 2
+    for scales, mode in [(np.ones(127, np.float32), fp8.PER_CHANNEL),
+                         (np.ones(2, np.float32), fp8.PER_CHANNEL),
+                         (np.ones(129, np.float32), fp8.PER_CHANNEL),
+                         (np.ones(128, np.float32), fp8.BLOCK128),
+                         (np.ones(1, np.float32), fp8.BLOCK128)]:
+        with pytest.raises(fp8.DeviceError) as err:
+            fp8.pack_weight(q, scales, mode)
+        assert err.value.status == _abi.LF_INVALID_ARGUMENT
+    # the C entry checks the code count too (the Python wrapper derives it
+    # from q's shape, so call the library directly with a short count)
+    size = fp8.weight_region_bytes(128, 256)
+    region = np.empty(size, np.uint8)
+    s = np.ones(128, np.float32)
+    u8 = ctypes.POINTER(ctypes.c_uint8)
+    f32 = ctypes.POINTER(ctypes.c_float)
+    for q_bytes, count in [(q.size - 1, 128), (q.size, 127), (q.size + 16, 128)]:
+        st = _abi.lib().lunaflux_fp8_pack_weight(
+            fp8.PER_CHANNEL, 128, 256, 1, q.ctypes.data_as(u8), q_bytes, s.ctypes.data_as(f32),
+            count, region.ctypes.data_as(u8), size)
+        assert st == _abi.LF_INVALID_ARGUMENT
+    assert fp8.scale_count(128, 256, 3, fp8.BLOCK128) == 6
+    assert fp8.scale_count(128, 256, 3, fp8.PER_CHANNEL) == 384
+
+
+DENSE_ENTRIES = (_abi.ENTRY_W8A16_DENSE, _abi.ENTRY_W8A16_QKV, _abi.ENTRY_W8A16_GATE_UP,
+                 _abi.ENTRY_W8A8_DENSE, _abi.ENTRY_W8A8_QKV, _abi.ENTRY_W8A8_GATE_UP)
+
+
+def test_admission_of_weight_regions():
+    rng = np.random.default_rng(4)
+    q = rng.integers(0, 0x7e, (256, 384), dtype=np.uint8)
+    per = fp8.pack_weight(q, np.ones(256, np.float32))
+    blk = fp8.pack_weight(q, np.ones(6, np.float32), fp8.BLOCK128)
+    for entry in DENSE_ENTRIES:
+        fp8.admit_weight(entry, per[:256], per.size, 256, 384)
+        with pytest.raises(fp8.DeviceError) as err:
+            fp8.admit_weight(entry, blk[:256], blk.size, 256, 384)
+        assert err.value.status == _abi.LF_UNSUPPORTED
+    # the grouped (MoE) entries read block scales
+    fp8.admit_weight(_abi.ENTRY_GROUPED, blk[:256], blk.size, 256, 384)
+    fp8.admit_weight(_abi.ENTRY_GROUPED, per[:256], per.size, 256, 384)
+    experts = fp8.pack_weight(np.stack([q, q]), np.ones((2, 6), np.float32), fp8.BLOCK128)
+    fp8.admit_weight(_abi.ENTRY_GROUPED, experts[:256], experts.size, 256, 384, 2)
+
+    def rejected(entry, head, size, rows=256, cols=384, experts=1):
+        with pytest.raises(fp8.DeviceError) as err:
+            fp8.admit_weight(entry, head, size, rows, cols, experts)
+        assert err.value.status == _abi.LF_INVALID_ARGUMENT
+
+    d = _abi.ENTRY_W8A16_DENSE
+    rejected(d, per[:256], per.size - 1)            # region smaller than the format's
+    rejected(d, per[:256], per.size + 256)          # or larger
+    rejected(d, per[:256], per.size, rows=128)      # shape the operation expects differs
+    rejected(d, per[:256], per.size, cols=512)
+    rejected(d, per[:128], per.size)                # header bytes missing
+    rejected(_abi.ENTRY_ACT_QUANT_ROWS, per[:256], per.size)   # not a weight operand
+    rejected(d, experts[:256], experts.size, experts=2)       # dense entries take one expert
+    for field, value in [(0, 0x12345678), (1, 2), (2, 7), (3, 3), (4, 272), (5, 256), (6, 2)]:
+        bad = per[:256].copy()
+        bad[4 * field:4 * field + 4] = np.frombuffer(np.uint32(value).tobytes(), np.uint8)
+        rejected(d, bad, per.size)
+    for field in range(4):                          # tile/scale offsets and sizes
+        bad = per[:256].copy()
+        view = bad[32:64].view(np.uint64)
+        view[field] += 256
+        rejected(d, bad, per.size)
+
+
+def test_dense_binds_refuse_block_scaled_weights_before_any_allocation():
+    """A block-scaled region bound to a dense, QKV or gate/up operation is
+    refused by admission (LF_UNSUPPORTED) before anything is allocated or
+    launched, so no device is needed to see it."""
+    from types import SimpleNamespace
+    rng = np.random.default_rng(12)
+    q = rng.integers(0, 0x7e, (256, 256), dtype=np.uint8)
+    region = fp8.pack_weight(q, np.ones(4, np.float32), fp8.BLOCK128)
+    w = fp8.Fp8Weight(SimpleNamespace(byte_count=region.size), 256, 256, 1, fp8.BLOCK128,
+                      region[:256].copy())
+    binds = [lambda f: fp8.ProjectionRuntime.bind_dense(None, f, None, None, w, None, 16),
+             lambda f: fp8.ProjectionRuntime.bind_qkv(None, f, None, None, w, w, w, None, 16),
+             lambda f: fp8.ProjectionRuntime.bind_gate_up(None, f, None, None, w, w, None, 16)]
+    for bind in binds:
+        for family in fp8.FAMILIES:
+            with pytest.raises(fp8.DeviceError) as err:
+                bind(family)
+            assert err.value.status == _abi.LF_UNSUPPORTED
+    with pytest.raises(fp8.DeviceError) as err:
+        fp8.ProjectionRuntime.bind_dense_quantized(None, None, None, w, None, 16)
+    assert err.value.status == _abi.LF_UNSUPPORTED
