@@ -20,6 +20,11 @@ max-abs bar only when all of these hold:
     between the two.
 Everything else must meet the bar, the relative L2 bar has no exception, and
 the number of excused elements is printed.
+
+For an output that is not a plain dot product (SwiGLU h = silu(g) u) the
+caller passes the bound itself: `midpoint_tol`, the largest distance from
+the exact value that either side's fp32 result may have
+(swiglu_midpoint_tol derives it from the summation bounds of g and u).
 """
 import numpy as np
 
@@ -35,7 +40,28 @@ def abs_sum(x_values: np.ndarray, w_values: np.ndarray) -> np.ndarray:
     return np.abs(x_values.astype(np.float64)) @ np.abs(w_values.astype(np.float64)).T
 
 
-def parity(gpu_bits, ref32, k: int = 0, s_abs=None, rel_l2=REL_L2, max_abs=MAX_ABS, label=""):
+def gamma(k: int) -> float:
+    return k * U32 / (1 - k * U32)
+
+
+def swiglu_midpoint_tol(g, u, s_g, s_u, k: int) -> np.ndarray:
+    """Bound on |computed h - exact h| for h = silu(g) u, where g and u are
+    K-term fp32 dot products with absolute-value sums s_g, s_u: each is
+    within gamma_K S of its exact value in any summation order, |d silu /
+    dg| <= 1.1 and |silu(g)| <= |g| + 0.3, and the silu evaluation itself
+    (expf and a division, or exp2 and a reciprocal) adds at most a few fp32
+    ulp of h, taken as 16 ulp."""
+    g = np.abs(np.asarray(g, np.float64))
+    u = np.abs(np.asarray(u, np.float64))
+    dg = gamma(k) * np.asarray(s_g, np.float64)
+    du = gamma(k) * np.asarray(s_u, np.float64)
+    silu = g + 0.3
+    h = silu * u
+    return 1.1 * (u + du) * dg + (silu + 1.1 * dg) * du + 16 * U32 * h
+
+
+def parity(gpu_bits, ref32, k: int = 0, s_abs=None, rel_l2=REL_L2, max_abs=MAX_ABS, label="",
+           midpoint_tol=None):
     g = o.bf16_decode(gpu_bits).astype(np.float64)
     r16 = o.bf16_round(ref32)
     r = o.bf16_decode(r16).astype(np.float64)
@@ -47,15 +73,19 @@ def parity(gpu_bits, ref32, k: int = 0, s_abs=None, rel_l2=REL_L2, max_abs=MAX_A
     diff = np.abs(g - r)
     over = diff > max_abs
     excused = np.zeros_like(over)
-    if over.any() and s_abs is not None and k > 0:
-        gamma = k * U32 / (1 - k * U32)
+    if over.any() and ((s_abs is not None and k > 0) or midpoint_tol is not None):
+        tol = 0.0
+        if s_abs is not None and k > 0:
+            tol = tol + 2 * gamma(k) * np.asarray(s_abs)
+        if midpoint_tol is not None:
+            tol = tol + 2 * np.asarray(midpoint_tol)
         # one bf16 ulp at the larger magnitude of the two neighbours
         mag = np.maximum(np.abs(g), np.abs(r))
         exponent = np.floor(np.log2(np.where(mag > 0, mag, 1.0)))
         ulp = np.exp2(exponent - 7)
         one_ulp = np.isclose(diff, ulp, rtol=0, atol=0) | np.isclose(diff, ulp / 2, rtol=0, atol=0)
         midpoint = (g + r) / 2
-        near = np.abs(ref32.astype(np.float64) - midpoint) <= 2 * gamma * np.asarray(s_abs)
+        near = np.abs(ref32.astype(np.float64) - midpoint) <= tol
         excused = over & one_ulp & near
     strict = np.where(excused, 0.0, diff)
     mx = float(strict.max())
