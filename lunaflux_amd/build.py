@@ -46,7 +46,7 @@ def build_code_object(out=CODE_OBJECT):
 def build_library(out=LIBRARY):
     sources = [os.path.join(CSRC, "runtime.cpp"), os.path.join(CSRC, "pack.cpp")]
     tmp = out + ".tmp"
-    _run([HIPCC, *HOST_FLAGS, "-shared", "-I", INCLUDE, *sources, "-o", tmp])
+    _run([HIPCC, *HOST_FLAGS, "-shared", "-I", INCLUDE, "-I", CSRC, *sources, "-o", tmp])
     os.replace(tmp, out)
     return out
 

@@ -1,24 +1,58 @@
 // runtime.cpp - implementation of include/lunaflux_hip.h over the HIP
 // runtime (libamdhip64). Host code only; the kernels live in a separate
-// gfx950 code object loaded through lunaflux_hip_module_load.
+// gfx950 code object loaded through lunaflux_hip_module_load. Every HIP call
+// goes through the dispatch table lunaflux::hip() (runtime_internal.h).
 //
 // Lifecycle model (same observable behaviour as internal/cuda/resources.c):
 // each handle carries state (LIVE/CLOSING/CLOSED), an active-operation count
 // and a child count. An operation brackets itself with op_begin/op_end; close
 // moves LIVE -> CLOSING only when nothing is active and no child is open,
-// otherwise it reports LF_BUSY. Memory is reference counted: the creator
-// holds one reference, every open child holds one on its parent, and the
-// object is freed (after closing its device resource) when the count drops
-// to zero.
-#include "lunaflux_hip.h"
-
-#include <hip/hip_runtime.h>
+// otherwise it reports LF_BUSY; a close whose driver call fails leaves the
+// object LIVE, so the close can be retried (resources.c:17-57). Memory is
+// reference counted: the creator holds one reference, every open child holds
+// one on its parent, and the object is freed (after closing its device
+// resource) when the count drops to zero.
+//
+// Asynchronous launches (lunaflux_hip_function_launch_async, an addition to
+// the reference's synchronous ABI) release their hold on the function,
+// module, stream and allocations once the kernel is enqueued. So that a close
+// can never free what a queued kernel still reads, the module and every
+// allocation of such a launch are marked, and closing a marked module or
+// allocation first waits for its device to go idle.
+#include "runtime_internal.h"
 
 #include <atomic>
 #include <cstdlib>
 #include <cstring>
 #include <new>
 #include <vector>
+
+namespace lunaflux {
+
+#ifdef LUNAFLUX_HIP_FAKE
+namespace {
+HipApi g_api{};
+}
+void install_hip_api(const HipApi &api) { g_api = api; }
+const HipApi &hip() { return g_api; }
+#else
+const HipApi &hip() {
+  static const HipApi api = {
+      &hipDriverGetVersion,  &hipGetDeviceCount,       &hipGetDeviceProperties,
+      &hipDeviceTotalMem,    &hipSetDevice,            &hipDeviceSynchronize,
+      &hipMalloc,            &hipFree,                 &hipMemcpy,
+      &hipStreamCreateWithFlags, &hipStreamDestroy,    &hipStreamSynchronize,
+      &hipEventCreate,       &hipEventDestroy,         &hipEventRecord,
+      &hipEventSynchronize,  &hipEventElapsedTime,     &hipModuleLoadData,
+      &hipModuleUnload,      &hipModuleGetFunction,    &hipModuleLaunchKernel,
+  };
+  return api;
+}
+#endif
+
+}  // namespace lunaflux
+
+using lunaflux::hip;
 
 namespace {
 
@@ -45,6 +79,8 @@ struct Object {
   std::atomic<int32_t> state{kClosed};
   std::atomic<int32_t> active{0};
   std::atomic<int32_t> children{0};
+  // set when an asynchronous launch used this object (module, allocation)
+  std::atomic<bool> queued{false};
   Object *parent = nullptr;
   virtual ~Object() { magic = 0; }
   // Releases the device resource; called with the object CLOSING.
@@ -132,13 +168,13 @@ const ApiState &api() {
   static ApiState state = [] {
     ApiState s;
     int version = 0;
-    if (hipDriverGetVersion(&version) != hipSuccess) {
+    if (hip().DriverGetVersion == nullptr || hip().DriverGetVersion(&version) != hipSuccess) {
       s.availability = LF_DRIVER_INITIALIZATION_FAILED;
       return s;
     }
     s.driver_version = version;
     int count = 0;
-    hipError_t e = hipGetDeviceCount(&count);
+    hipError_t e = hip().GetDeviceCount(&count);
     if (e == hipErrorNoDevice || (e == hipSuccess && count == 0)) {
       s.availability = LF_NO_DEVICES;
     } else if (e != hipSuccess) {
@@ -158,12 +194,27 @@ struct lf_context : Object {
   int32_t ordinal = -1;
 };
 
+namespace {
+int32_t set_device_of(Object *child) {
+  lf_context *ctx = static_cast<lf_context *>(child->parent);
+  return map_hip(hip().SetDevice(ctx->ordinal));
+}
+
+// A module or allocation that an asynchronous launch used may still be read
+// by a queued kernel: wait for its device before releasing it.
+int32_t drain_if_queued(Object *o) {
+  if (!o->queued.load()) return LF_OK;
+  int32_t r = map_hip(hip().DeviceSynchronize());
+  if (r == LF_OK) o->queued.store(false);
+  return r;
+}
+}  // namespace
+
 struct lf_stream : Object {
   hipStream_t handle = nullptr;
   int32_t destroy_device() override {
-    lf_context *ctx = static_cast<lf_context *>(parent);
-    int32_t r = map_hip(hipSetDevice(ctx->ordinal));
-    if (r == LF_OK && handle != nullptr) r = map_hip(hipStreamDestroy(handle));
+    int32_t r = set_device_of(this);
+    if (r == LF_OK && handle != nullptr) r = map_hip(hip().StreamDestroy(handle));
     if (r == LF_OK) handle = nullptr;
     return r;
   }
@@ -173,9 +224,8 @@ struct lf_event : Object {
   hipEvent_t handle = nullptr;
   bool recorded = false;
   int32_t destroy_device() override {
-    lf_context *ctx = static_cast<lf_context *>(parent);
-    int32_t r = map_hip(hipSetDevice(ctx->ordinal));
-    if (r == LF_OK && handle != nullptr) r = map_hip(hipEventDestroy(handle));
+    int32_t r = set_device_of(this);
+    if (r == LF_OK && handle != nullptr) r = map_hip(hip().EventDestroy(handle));
     if (r == LF_OK) handle = nullptr;
     return r;
   }
@@ -185,9 +235,9 @@ struct lf_allocation : Object {
   void *base = nullptr;
   size_t size = 0;
   int32_t destroy_device() override {
-    lf_context *ctx = static_cast<lf_context *>(parent);
-    int32_t r = map_hip(hipSetDevice(ctx->ordinal));
-    if (r == LF_OK && base != nullptr) r = map_hip(hipFree(base));
+    int32_t r = set_device_of(this);
+    if (r == LF_OK) r = drain_if_queued(this);
+    if (r == LF_OK && base != nullptr) r = map_hip(hip().Free(base));
     if (r == LF_OK) {
       base = nullptr;
       size = 0;
@@ -215,9 +265,9 @@ struct lf_module : Object {
   hipModule_t handle = nullptr;
   std::vector<uint8_t> image;
   int32_t destroy_device() override {
-    lf_context *ctx = static_cast<lf_context *>(parent);
-    int32_t r = map_hip(hipSetDevice(ctx->ordinal));
-    if (r == LF_OK && handle != nullptr) r = map_hip(hipModuleUnload(handle));
+    int32_t r = set_device_of(this);
+    if (r == LF_OK) r = drain_if_queued(this);
+    if (r == LF_OK && handle != nullptr) r = map_hip(hip().ModuleUnload(handle));
     if (r == LF_OK) {
       handle = nullptr;
       image.clear();
@@ -242,7 +292,7 @@ lf_context *context_of(Object *o) {
 
 int32_t make_current(lf_context *ctx) {
   if (ctx == nullptr || ctx->state.load() != kLive) return LF_CLOSED;
-  return map_hip(hipSetDevice(ctx->ordinal));
+  return map_hip(hip().SetDevice(ctx->ordinal));
 }
 
 // internal/cuda/regions.c:5-32
@@ -265,11 +315,6 @@ int32_t region_address(lf_allocation *a, int64_t offset, int64_t byte_count,
   }
   *out = resolved;
   return LF_OK;
-}
-
-bool host_span_ok(int64_t length, int64_t offset, int64_t count) {
-  return length >= 0 && offset >= 0 && count >= 0 && offset <= length &&
-         count <= length - offset;
 }
 
 // internal/cuda/launch.c:12-38
@@ -298,20 +343,41 @@ T *new_closed(int32_t kind) {
   return o;
 }
 
-int32_t launch(lf_function *fn, lf_stream *stream, int32_t gx, int32_t gy,
-               int32_t gz, int32_t bx, int32_t by, int32_t bz, int32_t lds,
-               int32_t argc, lf_allocation *const *allocs,
-               const int64_t *offsets, const int64_t *bytes,
-               const int64_t *aligns, bool synchronous) {
+}  // namespace
+
+namespace lunaflux {
+
+#ifdef LUNAFLUX_HIP_FAKE
+bool inspect(const void *handle, int32_t out[4]) {
+  const Object *o = static_cast<const Object *>(handle);
+  if (o == nullptr || o->magic != kMagic) return false;
+  out[0] = o->state.load();
+  out[1] = o->active.load();
+  out[2] = o->children.load();
+  out[3] = o->refs.load();
+  return true;
+}
+#endif
+
+int32_t checked_launch(lf_function *fn, lf_stream *stream, int32_t gx, int32_t gy,
+                       int32_t gz, int32_t bx, int32_t by, int32_t bz, int32_t lds,
+                       int32_t argc, lf_allocation *const *allocs,
+                       const int64_t *offsets, const int64_t *bytes,
+                       const int64_t *aligns, bool synchronous,
+                       const LaunchExtra *extra) {
   int32_t status = validate_dims(gx, gy, gz, bx, by, bz, lds);
   if (status != LF_OK) return status;
-  if (argc <= 0 || argc > LF_MAX_KERNEL_ARGUMENTS || allocs == nullptr ||
+  // A trailing argument supplied by the library counts against the cap.
+  const int32_t max_regions = LF_MAX_KERNEL_ARGUMENTS - (extra != nullptr ? 1 : 0);
+  if (argc <= 0 || argc > max_regions || allocs == nullptr ||
       offsets == nullptr || bytes == nullptr || aligns == nullptr) {
     return LF_INVALID_ARGUMENT;
   }
   fn = checked<lf_function>(fn, kFunction);
   stream = checked<lf_stream>(stream, kStream);
   if (fn == nullptr || stream == nullptr) return LF_CLOSED;
+  // Acquire function -> module -> stream -> each allocation, as
+  // internal/cuda/launch.c:75-104 does; release in reverse.
   status = op_begin(fn);
   if (status != LF_OK) return status;
   lf_module *module = static_cast<lf_module *>(fn->parent);
@@ -357,15 +423,24 @@ int32_t launch(lf_function *fn, lf_stream *stream, int32_t gx, int32_t gy,
     params[i] = &values[i];
   }
   if (status == LF_OK) status = make_current(ctx);
+  if (status == LF_OK && extra != nullptr) {
+    // argc < LF_MAX_KERNEL_ARGUMENTS here (checked above), so the slot exists.
+    status = extra->prepare(extra->context, ctx->ordinal, stream->handle, &values[argc]);
+    params[argc] = &values[argc];
+  }
   if (status == LF_OK) {
-    status = map_hip(hipModuleLaunchKernel(
+    status = map_hip(hip().ModuleLaunchKernel(
         fn->handle, static_cast<unsigned>(gx), static_cast<unsigned>(gy),
         static_cast<unsigned>(gz), static_cast<unsigned>(bx),
         static_cast<unsigned>(by), static_cast<unsigned>(bz),
         static_cast<unsigned>(lds), stream->handle, params, nullptr));
   }
   if (status == LF_OK && synchronous) {
-    status = map_hip(hipStreamSynchronize(stream->handle));
+    status = map_hip(hip().StreamSynchronize(stream->handle));
+  }
+  if (status == LF_OK && !synchronous) {
+    module->queued.store(true);
+    for (int32_t i = 0; i < argc; i += 1) allocs[i]->queued.store(true);
   }
   for (int32_t i = acquired; i > 0; i -= 1) op_end(allocs[i - 1]);
   if (stream_acquired) op_end(stream);
@@ -373,6 +448,10 @@ int32_t launch(lf_function *fn, lf_stream *stream, int32_t gx, int32_t gy,
   op_end(fn);
   return status;
 }
+
+}  // namespace lunaflux
+
+namespace {
 
 bool valid_symbol(const uint8_t *name, int64_t length) {
   if (name == nullptr || length <= 0 || length > LF_MAX_SYMBOL_BYTES) return false;
@@ -383,6 +462,50 @@ bool valid_symbol(const uint8_t *name, int64_t length) {
     if (!(alpha || (i > 0 && digit))) return false;
   }
   return true;
+}
+
+// Host <-> device copy of byte_count bytes between host[host_offset..] (a
+// buffer of host_length bytes) and the allocation at device_offset, checked
+// as internal/cuda/transfers.c:6-45 checks: negative offsets or counts are
+// LF_SIZE_OVERFLOW, spans outside either buffer LF_INVALID_ARGUMENT, and an
+// empty copy is valid.
+int32_t copy_host_device(lf_context *context, lf_allocation *allocation,
+                         const uint8_t *source, uint8_t *destination,
+                         int64_t host_length, int64_t host_offset,
+                         int64_t device_offset, int64_t byte_count) {
+  allocation = checked<lf_allocation>(allocation, kAllocation);
+  if (allocation == nullptr) return LF_CLOSED;
+  if (context != nullptr) {
+    context = checked<lf_context>(context, kContext);
+    if (context == nullptr) return LF_CLOSED;
+  }
+  int32_t st = op_begin(allocation);
+  if (st != LF_OK) return st;
+  uintptr_t address = 0;
+  if (source == nullptr && destination == nullptr) {
+    st = LF_INVALID_ARGUMENT;
+  } else if (host_offset < 0 || device_offset < 0 || byte_count < 0 || host_length < 0) {
+    st = LF_SIZE_OVERFLOW;
+  } else if (host_offset > host_length || byte_count > host_length - host_offset) {
+    st = LF_INVALID_ARGUMENT;
+  } else if (context != nullptr && context_of(allocation) != context) {
+    st = LF_INVALID_ARGUMENT;
+  } else {
+    st = region_address(allocation, device_offset, byte_count, 1, true, &address);
+  }
+  if (st == LF_OK) st = make_current(context_of(allocation));
+  if (st == LF_OK && byte_count > 0) {
+    void *device = reinterpret_cast<void *>(address);
+    if (source != nullptr) {
+      st = map_hip(hip().Memcpy(device, source + host_offset,
+                                static_cast<size_t>(byte_count), hipMemcpyHostToDevice));
+    } else {
+      st = map_hip(hip().Memcpy(destination + host_offset, device,
+                                static_cast<size_t>(byte_count), hipMemcpyDeviceToHost));
+    }
+  }
+  op_end(allocation);
+  return st;
 }
 
 }  // namespace
@@ -406,9 +529,10 @@ int32_t lunaflux_hip_device_info(int32_t ordinal, int64_t numeric[5],
   if (numeric == nullptr || name == nullptr) return LF_INVALID_ARGUMENT;
   if (ordinal < 0 || ordinal >= s.device_count) return LF_INVALID_ARGUMENT;
   hipDeviceProp_t prop;
+  std::memset(&prop, 0, sizeof(prop));
   size_t total = 0;
-  if (hipGetDeviceProperties(&prop, ordinal) != hipSuccess ||
-      hipDeviceTotalMem(&total, ordinal) != hipSuccess) {
+  if (hip().GetDeviceProperties(&prop, ordinal) != hipSuccess ||
+      hip().DeviceTotalMem(&total, ordinal) != hipSuccess) {
     return LF_DRIVER_FAILURE;
   }
   numeric[0] = static_cast<int64_t>(total);
@@ -440,7 +564,7 @@ lf_context *lunaflux_hip_context_create(int32_t ordinal, int32_t *status) {
     st = LF_UNAVAILABLE;
   } else if (ordinal < 0 || ordinal >= api().device_count) {
     st = LF_INVALID_ARGUMENT;
-  } else if (hipSetDevice(ordinal) != hipSuccess || hipFree(nullptr) != hipSuccess) {
+  } else if (hip().SetDevice(ordinal) != hipSuccess || hip().Free(nullptr) != hipSuccess) {
     st = LF_DRIVER_FAILURE;
   } else {
     ctx->ordinal = ordinal;
@@ -462,7 +586,9 @@ lf_stream *lunaflux_hip_stream_create(lf_context *context, int32_t *status) {
   int32_t st = s == nullptr ? LF_HOST_ALLOCATION_FAILED : op_begin(context);
   if (s != nullptr && st == LF_OK) {
     st = make_current(context);
-    if (st == LF_OK) st = map_hip(hipStreamCreateWithFlags(&s->handle, hipStreamNonBlocking));
+    if (st == LF_OK) {
+      st = map_hip(hip().StreamCreateWithFlags(&s->handle, hipStreamNonBlocking));
+    }
     if (st == LF_OK) attach(s, context);
     op_end(context);
   }
@@ -482,7 +608,7 @@ int32_t lunaflux_hip_stream_synchronize(lf_stream *stream) {
   int32_t st = op_begin(stream);
   if (st != LF_OK) return st;
   st = make_current(context_of(stream));
-  if (st == LF_OK) st = map_hip(hipStreamSynchronize(stream->handle));
+  if (st == LF_OK) st = map_hip(hip().StreamSynchronize(stream->handle));
   op_end(stream);
   return st;
 }
@@ -493,7 +619,7 @@ lf_event *lunaflux_hip_event_create(lf_context *context, int32_t *status) {
   int32_t st = e == nullptr ? LF_HOST_ALLOCATION_FAILED : op_begin(context);
   if (e != nullptr && st == LF_OK) {
     st = make_current(context);
-    if (st == LF_OK) st = map_hip(hipEventCreate(&e->handle));
+    if (st == LF_OK) st = map_hip(hip().EventCreate(&e->handle));
     if (st == LF_OK) attach(e, context);
     op_end(context);
   }
@@ -519,7 +645,7 @@ int32_t lunaflux_hip_event_record(lf_event *event, lf_stream *stream) {
       st = LF_INVALID_ARGUMENT;
     } else {
       st = make_current(context_of(stream));
-      if (st == LF_OK) st = map_hip(hipEventRecord(event->handle, stream->handle));
+      if (st == LF_OK) st = map_hip(hip().EventRecord(event->handle, stream->handle));
       if (st == LF_OK) event->recorded = true;
     }
     op_end(stream);
@@ -534,7 +660,7 @@ int32_t lunaflux_hip_event_synchronize(lf_event *event) {
   int32_t st = op_begin(event);
   if (st != LF_OK) return st;
   st = make_current(context_of(event));
-  if (st == LF_OK) st = map_hip(hipEventSynchronize(event->handle));
+  if (st == LF_OK) st = map_hip(hip().EventSynchronize(event->handle));
   op_end(event);
   return st;
 }
@@ -553,7 +679,9 @@ double lunaflux_hip_event_elapsed(lf_event *start, lf_event *finish,
         st = LF_INVALID_ARGUMENT;
       } else {
         st = make_current(context_of(start));
-        if (st == LF_OK) st = map_hip(hipEventElapsedTime(&ms, start->handle, finish->handle));
+        if (st == LF_OK) {
+          st = map_hip(hip().EventElapsedTime(&ms, start->handle, finish->handle));
+        }
       }
       op_end(finish);
     }
@@ -579,7 +707,7 @@ lf_allocation *lunaflux_hip_allocation_create(lf_context *context,
     st = op_begin(context);
     if (st == LF_OK) {
       st = make_current(context);
-      if (st == LF_OK) st = map_hip(hipMalloc(&a->base, static_cast<size_t>(byte_count)));
+      if (st == LF_OK) st = map_hip(hip().Malloc(&a->base, static_cast<size_t>(byte_count)));
       if (st == LF_OK) {
         a->size = static_cast<size_t>(byte_count);
         attach(a, context);
@@ -655,50 +783,16 @@ int32_t lunaflux_hip_context_validate_allocation_region(
   return st;
 }
 
-static int32_t copy_host_device(lf_context *context, lf_allocation *allocation,
-                                const uint8_t *source, uint8_t *destination,
-                                int64_t host_length, int64_t host_offset,
-                                int64_t device_offset, int64_t byte_count) {
-  allocation = checked<lf_allocation>(allocation, kAllocation);
-  if (allocation == nullptr) return LF_CLOSED;
-  if (context != nullptr) {
-    context = checked<lf_context>(context, kContext);
-    if (context == nullptr) return LF_CLOSED;
-  }
-  if ((source == nullptr && destination == nullptr) || byte_count <= 0 ||
-      !host_span_ok(host_length, host_offset, byte_count)) {
-    return LF_INVALID_ARGUMENT;
-  }
-  int32_t st = op_begin(allocation);
-  if (st != LF_OK) return st;
-  uintptr_t address = 0;
-  if (context != nullptr && context_of(allocation) != context) {
-    st = LF_INVALID_ARGUMENT;
-  } else {
-    st = region_address(allocation, device_offset, byte_count, 1, false, &address);
-  }
-  if (st == LF_OK) st = make_current(context_of(allocation));
-  if (st == LF_OK) {
-    void *device = reinterpret_cast<void *>(address);
-    if (source != nullptr) {
-      st = map_hip(hipMemcpy(device, source + host_offset,
-                             static_cast<size_t>(byte_count), hipMemcpyHostToDevice));
-    } else {
-      st = map_hip(hipMemcpy(destination + host_offset, device,
-                             static_cast<size_t>(byte_count), hipMemcpyDeviceToHost));
-    }
-  }
-  op_end(allocation);
-  return st;
-}
-
 int32_t lunaflux_hip_copy_to_device(lf_allocation *allocation,
                                     const uint8_t *source,
                                     int64_t source_length,
                                     int64_t source_offset,
                                     int64_t destination_offset,
                                     int64_t byte_count) {
-  if (source == nullptr) return LF_INVALID_ARGUMENT;
+  if (source == nullptr) {
+    return checked<lf_allocation>(allocation, kAllocation) == nullptr ? LF_CLOSED
+                                                                      : LF_INVALID_ARGUMENT;
+  }
   return copy_host_device(nullptr, allocation, source, nullptr, source_length,
                           source_offset, destination_offset, byte_count);
 }
@@ -728,7 +822,10 @@ int32_t lunaflux_hip_copy_to_host(lf_allocation *allocation,
                                   int64_t source_offset, int64_t byte_count,
                                   uint8_t *destination,
                                   int64_t destination_length) {
-  if (destination == nullptr) return LF_INVALID_ARGUMENT;
+  if (destination == nullptr) {
+    return checked<lf_allocation>(allocation, kAllocation) == nullptr ? LF_CLOSED
+                                                                      : LF_INVALID_ARGUMENT;
+  }
   return copy_host_device(nullptr, allocation, nullptr, destination,
                           destination_length, 0, source_offset, byte_count);
 }
@@ -751,7 +848,7 @@ lf_module *lunaflux_hip_module_load(lf_context *context, const uint8_t *image,
         st = LF_HOST_ALLOCATION_FAILED;
       }
       if (st == LF_OK) st = make_current(context);
-      if (st == LF_OK) st = map_hip(hipModuleLoadData(&m->handle, m->image.data()));
+      if (st == LF_OK) st = map_hip(hip().ModuleLoadData(&m->handle, m->image.data()));
       if (st == LF_OK) {
         attach(m, context);
       } else {
@@ -789,7 +886,9 @@ lf_function *lunaflux_hip_function_load(lf_module *module, const uint8_t *name,
       std::memcpy(symbol, name, static_cast<size_t>(name_length));
       symbol[name_length] = '\0';
       st = make_current(context_of(module));
-      if (st == LF_OK) st = map_hip(hipModuleGetFunction(&f->handle, module->handle, symbol));
+      if (st == LF_OK) {
+        st = map_hip(hip().ModuleGetFunction(&f->handle, module->handle, symbol));
+      }
       if (st == LF_OK) {
         attach(f, module);
       } else {
@@ -814,9 +913,9 @@ int32_t lunaflux_hip_function_launch(
     int32_t shared_memory_bytes, int32_t argument_count,
     lf_allocation *const *allocations, const int64_t *offsets,
     const int64_t *byte_counts, const int64_t *alignments) {
-  return launch(function, stream, grid_x, grid_y, grid_z, block_x, block_y,
-                block_z, shared_memory_bytes, argument_count, allocations,
-                offsets, byte_counts, alignments, true);
+  return lunaflux::checked_launch(function, stream, grid_x, grid_y, grid_z, block_x, block_y,
+                                  block_z, shared_memory_bytes, argument_count, allocations,
+                                  offsets, byte_counts, alignments, true, nullptr);
 }
 
 int32_t lunaflux_hip_function_launch_async(
@@ -825,9 +924,9 @@ int32_t lunaflux_hip_function_launch_async(
     int32_t shared_memory_bytes, int32_t argument_count,
     lf_allocation *const *allocations, const int64_t *offsets,
     const int64_t *byte_counts, const int64_t *alignments) {
-  return launch(function, stream, grid_x, grid_y, grid_z, block_x, block_y,
-                block_z, shared_memory_bytes, argument_count, allocations,
-                offsets, byte_counts, alignments, false);
+  return lunaflux::checked_launch(function, stream, grid_x, grid_y, grid_z, block_x, block_y,
+                                  block_z, shared_memory_bytes, argument_count, allocations,
+                                  offsets, byte_counts, alignments, false, nullptr);
 }
 
 lf_blas *lunaflux_hip_blas_create(lf_context *context, int32_t *status) {
