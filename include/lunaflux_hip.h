@@ -202,6 +202,29 @@ int32_t lunaflux_hip_function_launch_async(
   lf_allocation *const *allocations, const int64_t *offsets,
   const int64_t *byte_counts, const int64_t *alignments);
 
+/* No counterpart in the reference. For callers that cannot allocate device
+ * memory (code under HIP graph capture, tight serving loops, harnesses that
+ * forbid hipMalloc): a synchronous launch with every check of
+ * lunaflux_hip_function_launch, whose kernel receives argument_count region
+ * arguments followed by one more: the device address of this library's
+ * scratch array on the stream's device. The array is LF_SCRATCH_MAX_BYTES
+ * (16 MiB), held by each GPU the library launches on until the process ends;
+ * the kernel may use its first scratch_bytes (1 .. LF_SCRATCH_MAX_BYTES,
+ * else LF_INVALID_ARGUMENT, with nothing launched). With clear != 0 those
+ * bytes are zeroed first, by a fill kernel on the same stream. Nothing is
+ * allocated (no hipMalloc, hipFree or allocating library call). Every call on
+ * one GPU shares that GPU's array, which keeps the last call's contents
+ * (clear what must start at zero); calls that overlap on one GPU (several
+ * threads or streams) race. argument_count + 1 <= 32. */
+#define LF_SCRATCH_MAX_BYTES (16 << 20)
+int32_t lunaflux_hip_function_launch_scratch(
+  lf_function *function, lf_stream *stream, int32_t grid_x, int32_t grid_y,
+  int32_t grid_z, int32_t block_x, int32_t block_y, int32_t block_z,
+  int32_t shared_memory_bytes, int32_t argument_count,
+  lf_allocation *const *allocations, const int64_t *offsets,
+  const int64_t *byte_counts, const int64_t *alignments,
+  int64_t scratch_bytes, int32_t clear);
+
 /* Replace lunaflux_cuda_cublas_create/_close and the BF16 vendor GEMM plan
  * (gemm.c:108-397; ffi.mbt:202-240). This ABI ships no vendor GEMM: create
  * returns a CLOSED handle with LF_UNSUPPORTED, matching device_info's

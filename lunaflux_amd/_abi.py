@@ -36,6 +36,9 @@ STATUS_NAMES = {
 LF_AVAILABLE = 0
 LF_NO_DEVICES = 5
 
+# include/lunaflux_hip.h
+LF_SCRATCH_MAX_BYTES = 16 << 20
+
 # include/lunaflux_fp8.h
 LF_FP8_SCALE_PER_CHANNEL = 1
 LF_FP8_SCALE_BLOCK128 = 2
@@ -89,6 +92,9 @@ SIGNATURES = {
                                             _vp, _i64p, _i64p, _i64p]),
     "lunaflux_hip_function_launch_async": (_i32, [_vp, _vp, _i32, _i32, _i32, _i32, _i32, _i32, _i32,
                                                   _i32, _vp, _i64p, _i64p, _i64p]),
+    "lunaflux_hip_function_launch_scratch": (_i32, [_vp, _vp, _i32, _i32, _i32, _i32, _i32, _i32,
+                                                    _i32, _i32, _vp, _i64p, _i64p, _i64p, _i64,
+                                                    _i32]),
     "lunaflux_hip_blas_create": (_vp, [_vp, _i32p]),
     "lunaflux_hip_blas_close": (_i32, [_vp]),
     "lunaflux_hip_bf16_gemm_plan_create": (_vp, [_vp, _i64, _i64, _i64, _i64, _i32p]),

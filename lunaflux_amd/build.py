@@ -1,7 +1,9 @@
 """Builds the native artefacts of lunaflux_amd in-tree:
 
   lunaflux_amd/liblunaflux_hip.so   C-ABI (include/lunaflux_hip.h and
-                                    include/lunaflux_fp8.h), host code only
+                                    include/lunaflux_fp8.h): host code, plus
+                                    the scratch array of the no-allocation
+                                    launch (csrc/scratch.hip)
   lunaflux_amd/lunaflux_fp8.hsaco   gfx950 code object with every kernel
 
 Run ``python -m lunaflux_amd.build``. hipcc cross-compiles for gfx950, so no
@@ -44,9 +46,14 @@ def build_code_object(out=CODE_OBJECT):
 
 
 def build_library(out=LIBRARY):
-    sources = [os.path.join(CSRC, "runtime.cpp"), os.path.join(CSRC, "pack.cpp")]
+    """Host code (runtime.cpp, pack.cpp) plus scratch.hip, the one source with
+    device code of its own: the scratch array and its clearing kernel, built
+    for gfx950 into the library's embedded code object."""
+    sources = [os.path.join(CSRC, "runtime.cpp"), os.path.join(CSRC, "pack.cpp"),
+               os.path.join(CSRC, "scratch.hip")]
     tmp = out + ".tmp"
-    _run([HIPCC, *HOST_FLAGS, "-shared", "-I", INCLUDE, "-I", CSRC, *sources, "-o", tmp])
+    _run([HIPCC, *HOST_FLAGS, f"--offload-arch={ARCH}", "-Xclang", "-target-feature", "-Xclang",
+          "-packed-fp32-ops", "-shared", "-I", INCLUDE, "-I", CSRC, *sources, "-o", tmp])
     os.replace(tmp, out)
     return out
 

@@ -167,6 +167,16 @@ class Function(_Handle):
                      stream: Stream):
         _check(f"launch {self.name}", args._launch(self, dims, stream, False))
 
+    def launch_scratch(self, dims: "KernelLaunchDimensions", args: "KernelArguments",
+                       stream: Stream, scratch_bytes: int, clear: bool = True):
+        """lunaflux_hip_function_launch_scratch: synchronous, allocates
+        nothing; the kernel's last argument is the library's scratch array on
+        this device (the first scratch_bytes of it, zeroed first when clear)."""
+        _check(f"launch_scratch {self.name}", _abi.lib().lunaflux_hip_function_launch_scratch(
+            self._ptr, stream.ptr, *dims.grid, *dims.block, dims.shared_memory_bytes,
+            len(args.arguments), args._allocs, args._offsets, args._bytes, args._aligns,
+            int(scratch_bytes), int(bool(clear))))
+
 
 class Module(_Handle):
     _close_fn = "lunaflux_hip_module_close"
