@@ -5,6 +5,9 @@
                                     the scratch array of the no-allocation
                                     launch (csrc/scratch.hip)
   lunaflux_amd/lunaflux_fp8.hsaco   gfx950 code object with every kernel
+  lunaflux_amd/lunaflux_fp8.manifest.json
+                                    its v1 artifact manifest (SHA-256, device
+                                    target, entry points; lunaflux_amd/manifest.py)
 
 Run ``python -m lunaflux_amd.build``. hipcc cross-compiles for gfx950, so no
 GPU is needed.
@@ -61,6 +64,8 @@ def build_library(out=LIBRARY):
 def build_all():
     build_library()
     build_code_object()
+    from lunaflux_amd import manifest
+    print(manifest.write_manifest(), flush=True)
 
 
 if __name__ == "__main__":
