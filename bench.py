@@ -7,16 +7,17 @@ QKV (4096 -> 6144), O (4096 -> 4096), gate/up with SwiGLU (4096 -> 2 x 14336
 -> 14336) and down (14336 -> 4096) - at M = 32 tokens, bf16 activations from
 N(0, 1), e4m3 weights from N(0, 0.02) with per-output-channel fp32 scales
 (synthetic, seeded; no checkpoint exists offline). One step = the four calls.
-Weights are rotated over 5 device copies (1.1 GB > the 256 MB MALL) so each
-step streams its weights from HBM.
+Weights are rotated over 24 device copies of the layer (5.2 GB, 20x the
+256 MB MALL) so each step streams its weights from HBM.
 
 value = algorithmic bytes of the step / step time, with algorithmic bytes per
 call = N*K (e4m3 weights) + 4*N (scales) + 2*M*K (x) + 2*M*N_out (y), each
 weight byte counted once. The roofline object is the dominant kernel (gate/up)
 timed with HIP events on the launch stream. `detail` holds the other decode
 M values, the prefill (W8A8) GEMMs in TFLOP/s, and the
-act-quant pass. cpu_baseline times the CPU oracle (C restatement of
-kernels/reference over dequantized weights) on the host cores.
+act-quant pass (and each operation's TFLOP/s with it). cpu_baseline times the
+CPU oracle (C restatement of kernels/reference over dequantized weights) on
+the host cores, with one-thread figures for configs 1 and 2 beside it.
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu] [--quick]
 """
@@ -72,23 +73,24 @@ def roofline_kernel():
 
 
 class Layer:
-    """Device-resident weights of one layer, ROTATIONS copies each."""
+    """Device-resident weights of one layer, `rotations` copies each."""
 
-    def __init__(self, rt, seed=1234):
+    def __init__(self, rt, seed=1234, rotations=ROTATIONS):
         from lunaflux_amd import fp8, synth
         rng = np.random.default_rng(seed)
         t0 = time.time()
+        self.rotations = rotations
         self.regions = {}
         for name, rows, cols in [("q", NQ, HIDDEN), ("k", NKV, HIDDEN), ("v", NKV, HIDDEN),
                                  ("o", HIDDEN, HIDDEN), ("gate", INTER, HIDDEN),
                                  ("up", INTER, HIDDEN), ("down", HIDDEN, INTER)]:
             q, s = synth.weight(rng, rows, cols)
             region = fp8.pack_weight(q, s)
-            self.regions[name] = [rt.weight_from_region(region) for _ in range(ROTATIONS)]
-        log(f"weights ready ({ROTATIONS} copies of one layer) in {time.time() - t0:.1f}s")
+            self.regions[name] = [rt.weight_from_region(region) for _ in range(rotations)]
+        log(f"weights ready ({rotations} copies of one layer) in {time.time() - t0:.1f}s")
 
     def w(self, name, r):
-        return self.regions[name][r % ROTATIONS]
+        return self.regions[name][r % self.rotations]
 
 
 class Bench:
@@ -109,7 +111,7 @@ class Bench:
         rt, L, R = self.rt, self.layer, self._region
         counts = rt.step_counts(m)
         ops = []
-        for r in range(ROTATIONS):
+        for r in range(L.rotations):
             fam, mt = self.family, self.max_tokens
             x, xd = R(self.x, alignment=256), R(self.xd, alignment=256)
             ops.append({
@@ -255,6 +257,49 @@ def lm_head_bench(rt, launches=20):
     return out
 
 
+def host_threads():
+    """The host cores this process may use: the CPU affinity set, capped by
+    OMP_NUM_THREADS where the machine sets it (the GPU box gives each GPU a
+    share of its cores and says so there)."""
+    n = len(os.sched_getaffinity(0)) if hasattr(os, "sched_getaffinity") else (os.cpu_count() or 1)
+    cap = os.environ.get("OMP_NUM_THREADS", "")
+    return max(1, min(n, int(cap))) if cap.isdigit() and int(cap) > 0 else n
+
+
+def cpu_single_thread(seconds=4.0):
+    """One-thread figures of the CPU oracle: BASELINE config 1 (M=4, K=512,
+    N=1536) repeated for about `seconds`, and one config-2 decode layer at
+    M=32 (the four calls once)."""
+    sys.path.insert(0, os.path.join(ROOT, "tests"))
+    import oracle_lib as o
+    from lunaflux_amd import synth
+    rng = np.random.default_rng(11)
+    x = o.bf16_decode(synth.activations(rng, 4, 512))
+    q, s = synth.weight(rng, 1536, 512)
+    w = o.dequantize(q, s)
+    reps, t_total = 0, 0.0
+    while t_total < seconds:
+        t0 = time.perf_counter()
+        o.project_values(x, w)
+        t_total += time.perf_counter() - t0
+        reps += 1
+    c1 = reps * call_bytes(4, 512, 1536, 1536) / t_total / 1e9
+    xs = {HIDDEN: o.bf16_decode(synth.activations(rng, 32, HIDDEN)),
+          INTER: o.bf16_decode(synth.activations(rng, 32, INTER))}
+    t_layer = 0.0
+    for name, k, n, n_out in call_shapes():
+        qw, sw = synth.weight(rng, n, k)
+        wd = o.dequantize(qw, sw)
+        t0 = time.perf_counter()
+        y = o.project_values(xs[k], wd)
+        if name == "gate_up":
+            o.silu_mul_array(y[:, :n_out], y[:, n_out:])
+        t_layer += time.perf_counter() - t0
+    return {"config1_GB/s": round(c1, 4), "config1_calls": reps,
+            "config2_m32_layer_GB/s": round(layer_bytes(32) / t_layer / 1e9, 4),
+            "config2_m32_layer_s": round(t_layer, 2), "threads": 1}
+
+
 def cpu_baseline(m=32, threads=None):
     """The CPU oracle on this host: the four decode calls of one layer at
     M=m over dequantized fp32 weights (sequential-K fp32, as the reference),
@@ -262,7 +307,7 @@ def cpu_baseline(m=32, threads=None):
     sys.path.insert(0, os.path.join(ROOT, "tests"))
     import oracle_lib as o
     from lunaflux_amd import synth
-    threads = threads or min(os.cpu_count() or 1, 16)
+    threads = threads or host_threads()
     rng = np.random.default_rng(7)
     x = o.bf16_decode(synth.activations(rng, m, HIDDEN))
     xd = o.bf16_decode(synth.activations(rng, m, INTER))
@@ -284,7 +329,8 @@ def cpu_baseline(m=32, threads=None):
     return {"value": round(gbs, 4), "unit": "GB/s", "cores": threads, "kind": "port",
             "sample": f"{passes} decode layers (qkv, o, gate/up+SwiGLU, down) at M={m}, full "
                       f"shapes: the CPU oracle's sequential-K fp32 project_values over dequantized "
-                      f"weights; {total_s:.2f} s wall on {threads} threads"}
+                      f"weights; {total_s:.2f} s wall on {threads} threads",
+            "single_thread": cpu_single_thread()}
 
 
 MOE_CONFIGS = {
@@ -304,22 +350,28 @@ def moe_flops(c):
     return 2 * a * c["hidden"] * 2 * c["inter"] + 2 * a * c["inter"] * c["hidden"]
 
 
+MOE_ROTATION_BYTES = 1 << 30  # expert weights cycled per step: 4x the 256 MB MALL
+
+
 def moe_bench(rt, c, steps=12, warmup=3, seed=4242):
     """Times the launches of one MoE expert-MLP operation with events
     between them. Expert weights are E copies of one seeded draw (kernel time
-    does not depend on the values; it keeps setup short)."""
+    does not depend on the values; it keeps setup short); enough such weight
+    sets to total MOE_ROTATION_BYTES are cycled over the steps, so no step
+    finds its experts' weights in the MALL from the step before."""
     from lunaflux_amd import fp8, moe, synth
     from lunaflux_amd.fp8 import _region
     rng = np.random.default_rng(seed)
     e, k, h, i, t = c["experts"], c["top_k"], c["hidden"], c["inter"], c["tokens"]
     block = 128 if c["group"] else None
     mode = fp8.BLOCK128 if block else fp8.PER_CHANNEL
-    weights = []
+    regions = []
     for rows, cols in ((i, h), (i, h), (h, i)):
         q, s = synth.weight(rng, rows, cols, block=block)
-        region = fp8.pack_weight(np.broadcast_to(q, (e,) + q.shape), np.broadcast_to(s, (e,) + s.shape),
-                                 mode)
-        weights.append(rt.weight_from_region(region))
+        regions.append(fp8.pack_weight(np.broadcast_to(q, (e,) + q.shape),
+                                       np.broadcast_to(s, (e,) + s.shape), mode))
+    sets = max(1, -(-MOE_ROTATION_BYTES // sum(r.size for r in regions)))
+    weight_sets = [[rt.weight_from_region(r) for r in regions] for _ in range(sets)]
     logits = rng.standard_normal((t, e)).astype(np.float32)
     if c["popularity"] == "bias":
         logits += rng.normal(0.0, 1.5, e).astype(np.float32)
@@ -332,16 +384,18 @@ def moe_bench(rt, c, steps=12, warmup=3, seed=4242):
     da = ctx.upload(desc.as_bytes())
     oa = ctx.allocate(t * h * 2)
     counts = rt.step_counts(t, decode=False)
-    op = moe.bind_moe(rt, counts, desc, _region(da, 32, alignment=4), _region(la, alignment=256),
-                      _region(xa, alignment=256), *weights, _region(oa, alignment=256), t)
+    ops = [moe.bind_moe(rt, counts, desc, _region(da, 32, alignment=4), _region(la, alignment=256),
+                        _region(xa, alignment=256), *weights, _region(oa, alignment=256), t)
+           for weights in weight_sets]
+    op = ops[0]
     stream = rt.stream
-    for _ in range(warmup):
-        op.launch(stream, synchronous=False)
+    for it in range(warmup):
+        ops[it % sets].launch(stream, synchronous=False)
     stream.synchronize()
     events = [[ctx.create_event() for _ in range(len(op.steps) + 1)] for _ in range(steps)]
     for it in range(steps):
         events[it][0].record(stream)
-        for s_i, step in enumerate(op.steps):
+        for s_i, step in enumerate(ops[it % sets].steps):
             step.launch(stream, synchronous=False)
             events[it][s_i + 1].record(stream)
     events[-1][-1].synchronize()
@@ -358,7 +412,7 @@ def moe_bench(rt, c, steps=12, warmup=3, seed=4242):
             "gemm_TFLOP/s": round(fl / (gemm_ms * 1e-3) / 1e12, 1),
             "gemm_fp8_frac": round(fl / (gemm_ms * 1e-3) / 1e12 / FP8_PEAK_TFLOPS, 4),
             "total_TFLOP/s": round(fl / (total_ms * 1e-3) / 1e12, 1),
-            "GFLOP": round(fl / 1e9, 1)}
+            "GFLOP": round(fl / 1e9, 1), "weight_sets": sets}
 
 
 def pmc_pass():
@@ -408,6 +462,89 @@ def pmc_pass_prefill():
             op.steps[-1].launch(rt.stream, synchronous=False)
         rt.stream.synchronize()
         log(f"pmc prefill pass: {op.steps[-1].name} M={m} K={k} N={n} x5")
+
+
+def pmc_pass_all():
+    """Short run for counter passes over the kernels of config 2 and 4-5:
+    the four decode calls at M = 32 and M = 128 (three launches each over two
+    weight copies), one MoE operation of each MoE config (two launches of
+    every step), then the calibration copy of 512 MiB three times."""
+    from lunaflux_amd.device import KernelArguments, KernelLaunchDimensions
+    from lunaflux_amd.fp8 import ProjectionRuntime, _region
+    rt = ProjectionRuntime(0)
+    layer = Layer(rt, rotations=2)
+    for mt in (32, 128):
+        b = Bench(rt, layer, mt, "w8a16")
+        ops = b.bind(mt)
+        for c, _, _, _ in call_shapes():
+            for r in (0, 1, 0):
+                ops[r][c].launch(rt.stream, synchronous=False)
+        rt.stream.synchronize()
+        log(f"pmc pass: decode M={mt} x3")
+    for name, c in MOE_CONFIGS.items():
+        moe_bench(rt, c, steps=2, warmup=0)
+        log(f"pmc pass: moe {name} x2")
+    n = PMC_COPY_BYTES
+    src, dst = rt.context.allocate(n), rt.context.allocate(n)
+    cnt = rt.context.upload(np.array([n // 16], np.int64))
+    copy = rt.function("lf_calibrate_copy")
+    args = KernelArguments([_region(cnt, 8, alignment=8), _region(src, alignment=256),
+                            _region(dst, alignment=256)])
+    for _ in range(3):
+        copy.launch_async(KernelLaunchDimensions.new((4096,), (256,)), args, rt.stream)
+    rt.stream.synchronize()
+    log(f"pmc pass done (copy {n} bytes x3)")
+
+
+def summarize_counters(paths):
+    """Markdown table, one row per (kernel, grid), of rocprofv3 --pmc counter
+    CSVs (any of the passes of --pmc-pass-all; kernel-trace CSVs add the
+    duration): FETCH_SIZE and WRITE_SIZE scaled to bytes by what they read for
+    lf_calibrate_copy moving a known number of bytes, and the MFMA busy
+    fraction SQ_VALU_MFMA_BUSY_CYCLES / (GRBM_GUI_ACTIVE / 8 XCDs x 1024
+    SIMDs) with the clock GRBM_GUI_ACTIVE / 8 / duration."""
+    import csv
+    vals, dur = {}, {}
+    for path in paths:
+        for r in csv.DictReader(open(path)):
+            blocks = int(r.get("Grid_Size_X") or r.get("Grid_Size") or 0) // max(
+                int(r.get("Workgroup_Size_X") or r.get("Workgroup_Size") or 1), 1)
+            key = (r["Kernel_Name"], blocks)
+            if "Counter_Name" in r:
+                vals.setdefault(key, {}).setdefault(r["Counter_Name"], []).append(
+                    float(r["Counter_Value"]))
+            elif "Start_Timestamp" in r:
+                dur.setdefault(key, []).append(
+                    (int(r["End_Timestamp"]) - int(r["Start_Timestamp"])) / 1000.0)
+
+    def mean(key, counter):
+        v = vals.get(key, {}).get(counter)
+        return float(np.mean(v)) if v else None
+
+    cal = [k for k in vals if k[0] == "lf_calibrate_copy"]
+    f_factor = w_factor = None
+    if cal:
+        f_cal, w_cal = mean(cal[0], "FETCH_SIZE"), mean(cal[0], "WRITE_SIZE")
+        f_factor = PMC_COPY_BYTES / (f_cal * 1024) if f_cal else None
+        w_factor = PMC_COPY_BYTES / (w_cal * 1024) if w_cal else None
+    out = [f"Calibration (lf_calibrate_copy, {PMC_COPY_BYTES} B read and written): FETCH_SIZE "
+           f"factor {f_factor and round(f_factor, 4)}, WRITE_SIZE factor {w_factor and round(w_factor, 4)}",
+           "",
+           "| Kernel | Blocks | Duration us | HBM read MB | HBM write MB | MFMA busy | Clock GHz |",
+           "|---|---|---|---|---|---|---|"]
+    for key in sorted(set(vals) | set(dur)):
+        if key[0] == "lf_calibrate_copy":
+            continue
+        f, w = mean(key, "FETCH_SIZE"), mean(key, "WRITE_SIZE")
+        busy, gui = mean(key, "SQ_VALU_MFMA_BUSY_CYCLES"), mean(key, "GRBM_GUI_ACTIVE")
+        d = float(np.mean(dur[key])) if key in dur else None
+        read_mb = f"{f * 1024 * f_factor / 1e6:.1f}" if f is not None and f_factor else "-"
+        write_mb = f"{w * 1024 * w_factor / 1e6:.1f}" if w is not None and w_factor else "-"
+        frac = f"{busy / (gui / 8 * 1024) * 100:.0f} %" if busy is not None and gui else "-"
+        clock = f"{gui / 8 / (d * 1e-6) / 1e9:.2f}" if gui and d else "-"
+        out.append(f"| {key[0]} | {key[1]} | {d and round(d, 1) or '-'} | {read_mb} | {write_mb} | "
+                   f"{frac} | {clock} |")
+    return "\n".join(out)
 
 
 def measured_traffic(kernel):
@@ -520,12 +657,20 @@ def main():
     ap.add_argument("--summarize-traffic", nargs=2, metavar=("FETCH_CSV", "WRITE_CSV"),
                     help="print the traffic summary of the roofline kernel from the two "
                          "--pmc-pass counter CSVs (no GPU needed)")
+    ap.add_argument("--pmc-pass-all", action="store_true",
+                    help="short run of the decode and MoE kernels for counter passes")
+    ap.add_argument("--summarize-counters", nargs="+", metavar="CSV",
+                    help="per-kernel markdown table of --pmc-pass-all counter (and kernel-trace) "
+                         "CSVs (no GPU needed)")
     ap.add_argument("--summarize-trace", metavar="KERNEL_TRACE_CSV",
                     help="print a per-kernel markdown summary of a rocprofv3 kernel-trace CSV "
                          "(no GPU needed)")
     args = ap.parse_args()
     if args.summarize_trace:
         print(summarize_trace(args.summarize_trace))
+        return
+    if args.summarize_counters:
+        print(summarize_counters(args.summarize_counters))
         return
     if args.summarize_traffic:
         print(json.dumps(summarize_traffic(*args.summarize_traffic, roofline_kernel()), indent=1))
@@ -539,6 +684,9 @@ def main():
         return
     if args.pmc_pass_prefill:
         pmc_pass_prefill()
+        return
+    if args.pmc_pass_all:
+        pmc_pass_all()
         return
 
     from lunaflux_amd.fp8 import ProjectionRuntime
@@ -584,10 +732,13 @@ def main():
                 p = b.time_kernel(mm, c, 5, warmup=2)
                 q = b.time_kernel(mm, c, 5, warmup=2, step=0)
                 tf = call_flops(mm, k, n) / (p * 1e-3) / 1e12
+                op_tf = call_flops(mm, k, n) / ((p + q) * 1e-3) / 1e12
                 row[c] = {"gemm_us": round(p * 1e3, 1), "TFLOP/s": round(tf, 1),
                           "fp8_frac": round(tf / FP8_PEAK_TFLOPS, 4),
                           "act_quant_us": round(q * 1e3, 1),
-                          "act_quant_GB/s": round(mm * k * 3 / (q * 1e-3) / 1e9, 1)}
+                          "act_quant_GB/s": round(mm * k * 3 / (q * 1e-3) / 1e9, 1),
+                          "op_us": round((p + q) * 1e3, 1), "op_TFLOP/s": round(op_tf, 1),
+                          "op_fp8_frac": round(op_tf / FP8_PEAK_TFLOPS, 4)}
             row["rms_norm_quant_k4096"] = rms_norm_quant_bench(rt, b, mm)
             detail["prefill_w8a8"][f"M={mm}"] = row
             log(f"prefill M={mm}: {row}")
