@@ -100,13 +100,19 @@ int32_t lunaflux_fp8_unpack_weight(const uint8_t *region, int64_t region_bytes,
  * 161-219):
  *  W8A16 ("decode"): bf16 activations, e4m3 weights dequantized to bf16 in
  *    registers (exact), bf16 MFMA, fp32 accumulation, per-channel scale in
- *    the epilogue. A wave owns 16 output columns, a block 4 such tiles over
- *    one K-slice; the grid is split-K across blocks, reduced in a fixed
- *    slice order by the last block of each column group through the
- *    workspace. Suffix _m16/_m32/_m64/_m128: the profile's largest M.
+ *    the epilogue. Two forms, picked per entry by the launch geometry:
+ *    one-tile (a block of waves owns one 16-column tile and splits K across
+ *    its waves, partials summed in LDS) and column-group (each wave owns one
+ *    16-column tile, a block several adjacent tiles over one K-slice sharing
+ *    the activation slice through LDS; with more than one slice the partials
+ *    are reduced in a fixed slice order by the last block of each column
+ *    group through the workspace). Suffix _m16/_m32/_m64/_m128: the
+ *    profile's largest M; _k<K>...: a shape-specialized entry.
  *  W8A8 ("prefill"): activations quantized per token to e4m3
- *    (lf_fp8_act_quant_rows), e4m3 x e4m3 MFMA (16x16x128 f8f6f4), fp32
- *    accumulation, row scale x channel scale epilogue. 128 x 128 block tile.
+ *    (lf_fp8_act_quant_rows), e4m3 x e4m3 MFMA, fp32 accumulation, row scale
+ *    x channel scale epilogue. _t128: 128 x 128 block tiles of 4 waves
+ *    (16x16x128 f8f6f4 MFMA); _t256: 256 x 256 tiles of 8 waves
+ *    (32x32x64 f8f6f4 MFMA), chosen when a launch has at least 192 of them.
  *
  * Operands (all device regions, in order):
  *  lf_fp8_act_quant_rows (counts, x, w, xq)   x bf16 [M, K] -> xq; K is read
