@@ -936,12 +936,8 @@ LF_W16_FIXED_QKV_T1(4096, 4096, 1024, 16, 1, 8, 4, 2, 2)
 LF_W16_FIXED_QKV_G(4096, 4096, 1024, 32, 2, 4, 8, 4, 2)
 LF_W16_FIXED_GATE_UP_G(4096, 16, 1, 1, 2, 4, 2)
 LF_W16_FIXED_GATE_UP_G(4096, 32, 2, 1, 4, 3, 2)
-// 128 rows (8 fragments per wave): column groups of 4 tiles; K slices
-// measured on the box: o and down 4, QKV 2, gate/up unsplit.
-LF_W16_FIXED_DENSE_G(4096, 128, 8, 4, 4, 2, 1)
-LF_W16_FIXED_DENSE_G(14336, 128, 8, 4, 4, 2, 1)
-LF_W16_FIXED_QKV_G(4096, 4096, 1024, 128, 8, 2, 4, 2, 1)
-LF_W16_FIXED_GATE_UP_G(4096, 128, 8, 1, 4, 2, 1)
+// Profiles of 65..128 rows use the LDS-tiled GEMM (w8a16_gemm.hip), except
+// for these wide shapes.
 // N >= 16384 (e.g. the 128,256-wide vocabulary head): enough 16-column
 // tiles to fill the chip without a K split, as gate/up.
 LF_W16_FIXED_DENSE_WIDE_G(4096, 16, 1, 1, 2, 4, 2)

@@ -123,11 +123,6 @@ constexpr W8a16Fixed kW8a16Fixed[] = {
      "lf_fp8_w8a16_qkv_k4096_q4096_kv1024_m32"},
     {LF_FP8_ENTRY_W8A16_GATE_UP, 4096, 0, 0, 1, true, 2, 1, "lf_fp8_w8a16_gate_up_k4096_m16"},
     {LF_FP8_ENTRY_W8A16_GATE_UP, 4096, 0, 0, 2, true, 4, 1, "lf_fp8_w8a16_gate_up_k4096_m32"},
-    {LF_FP8_ENTRY_W8A16_DENSE, 4096, 0, 0, 8, true, 4, 4, "lf_fp8_w8a16_dense_k4096_m128"},
-    {LF_FP8_ENTRY_W8A16_DENSE, 14336, 0, 0, 8, true, 4, 4, "lf_fp8_w8a16_dense_k14336_m128"},
-    {LF_FP8_ENTRY_W8A16_QKV, 4096, 4096, 1024, 8, true, 4, 2,
-     "lf_fp8_w8a16_qkv_k4096_q4096_kv1024_m128"},
-    {LF_FP8_ENTRY_W8A16_GATE_UP, 4096, 0, 0, 8, true, 4, 1, "lf_fp8_w8a16_gate_up_k4096_m128"},
 };
 
 // The specialized entry for (entry, N, K, Q / K-V split, profile), or null.
@@ -159,6 +154,55 @@ void w8a16_fixed_geometry(const W8a16Fixed &f, int64_t n, int32_t *gx, int32_t *
   const int64_t tiles = n / 16;
   *gx = static_cast<int32_t>(f.group ? tiles / f.waves * f.split : tiles);
   *bx = 64 * f.waves;
+}
+
+// Profiles of 65..128 rows: the LDS-tiled GEMM (kernels/w8a16_gemm.hip,
+// "lf_fp8_w8a16_{op}_m128_n{BN}"), any K, any N its blocks divide. A block
+// (8 waves) computes 128 rows x BN weight columns (gate/up: BN / 2 gate and
+// BN / 2 up columns); BN is 128 when that still gives at least 192 column
+// blocks, else 64. K is cut into S slices so that the launch has about 256
+// blocks, keeping at least 10 k-tiles per slice. Measured at M = 128 on the
+// Llama-3-8B shapes (MI355X, weights rotated past the MALL): o 18.5 -> 15.0
+// us (BN 64, S 3), QKV 23.5 -> 19.1 (64, 2), down 36.8 -> 30.6 (64, 4),
+// gate/up 44.9 -> 43.2 (128, 1), against the column-group form.
+// Vocabulary-wide dense shapes with a column-group entry keep it.
+struct W8a16Gemm {
+  int bn;
+  int64_t blocks_n, split;
+};
+bool w8a16_gemm(int32_t entry, int64_t n, int64_t k, int32_t max_tokens, W8a16Gemm *out) {
+  if (max_tokens <= 64 || max_tokens > 128 || n <= 0 || k % 128 != 0) return false;
+  if (entry == LF_FP8_ENTRY_W8A16_DENSE && n >= kWideN &&
+      w8a16_fixed(entry, n, k, 0, 0, max_tokens) != nullptr) {
+    return false;
+  }
+  const int64_t per128 = entry == LF_FP8_ENTRY_W8A16_GATE_UP ? 64 : 128;
+  const int64_t per64 = per128 / 2;
+  if (n % per128 == 0 && n / per128 >= 192) {
+    out->bn = 128;
+    out->blocks_n = n / per128;
+  } else if (n % per64 == 0) {
+    out->bn = 64;
+    out->blocks_n = n / per64;
+  } else {
+    return false;
+  }
+  const int64_t kt = k / 128;
+  int64_t split = 256 / out->blocks_n;
+  while (split > 1 && kt / split < 10) --split;
+  if (split < 1) split = 1;
+  if (split > kt) split = kt;
+  if (out->blocks_n * split > INT32_MAX) return false;
+  out->split = split;
+  return true;
+}
+
+int64_t w8a16_gemm_workspace(const W8a16Gemm &g) {
+  if (g.split == 1) return 256;
+  // one 1 KiB fp32 fragment per (slice, column block, wave, fragment): 8
+  // waves of 2 x BN / 32 fragments; then one arrival counter per block
+  const int64_t frags = 2 * (g.bn / 32);
+  return align_up(g.split * g.blocks_n * 8 * frags * 1024, 256) + align_up(g.blocks_n * 4, 256);
 }
 }  // namespace
 
@@ -303,6 +347,8 @@ static int64_t w8a16_workspace(int32_t entry, int64_t n, int64_t k, int64_t nq, 
       !w8a16_split(n, k, max_tokens, &sp)) {
     return -1;
   }
+  W8a16Gemm gm;
+  if (w8a16_gemm(entry, n, k, max_tokens, &gm)) return w8a16_gemm_workspace(gm);
   if (const W8a16Fixed *f = w8a16_fixed(entry, n, k, nq, nkv, max_tokens)) {
     return w8a16_fixed_workspace(*f, n);
   }
@@ -367,14 +413,22 @@ static int32_t launch_geometry(int32_t entry, int64_t n, int64_t k, int64_t nq, 
     case LF_FP8_ENTRY_W8A16_GATE_UP: {
       W8a16Split sp;
       if (!w8a16_split(n, k, max_tokens, &sp)) return LF_INVALID_ARGUMENT;
+      const char *op = entry == LF_FP8_ENTRY_W8A16_DENSE ? "dense"
+                       : entry == LF_FP8_ENTRY_W8A16_QKV ? "qkv"
+                                                         : "gate_up";
+      W8a16Gemm gm;
+      if (w8a16_gemm(entry, n, k, max_tokens, &gm)) {
+        std::snprintf(buffer, sizeof(buffer), "lf_fp8_w8a16_%s_m128_n%d", op, gm.bn);
+        name = buffer;
+        gx = static_cast<int32_t>(gm.blocks_n * gm.split);
+        bx = 512;
+        break;
+      }
       if (const W8a16Fixed *f = w8a16_fixed(entry, n, k, nq, nkv, max_tokens)) {
         name = f->symbol;
         w8a16_fixed_geometry(*f, n, &gx, &bx);
         break;
       }
-      const char *op = entry == LF_FP8_ENTRY_W8A16_DENSE ? "dense"
-                       : entry == LF_FP8_ENTRY_W8A16_QKV ? "qkv"
-                                                         : "gate_up";
       std::snprintf(buffer, sizeof(buffer), "lf_fp8_w8a16_%s_m%d%s", op, 16 * sp.mt,
                     sp.one_tile ? "_t1" : "");
       name = buffer;

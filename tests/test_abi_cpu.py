@@ -43,9 +43,10 @@ def test_code_object_has_every_entry_point():
                    "lf_moe_gate_up_t256_b128", "lf_moe_down_t256_b128"] + [f"lf_fp8_w8a16_{op}_m{m}" for op in ("dense", "qkv", "gate_up")
                                              for m in (16, 32, 64, 128)] + [
                    f"lf_fp8_w8a16_{op}_m16_t1" for op in ("dense", "qkv", "gate_up")] + [
-                   f"lf_fp8_w8a16_dense_k{k}_m{m}" for k in (4096, 14336) for m in (16, 32, 128)] + [
-                   f"lf_fp8_w8a16_gate_up_k4096_m{m}" for m in (16, 32, 128)] + [
-                   f"lf_fp8_w8a16_qkv_k4096_q4096_kv1024_m{m}" for m in (16, 32, 128)] + [
+                   f"lf_fp8_w8a16_dense_k{k}_m{m}" for k in (4096, 14336) for m in (16, 32)] + [
+                   f"lf_fp8_w8a16_gate_up_k4096_m{m}" for m in (16, 32)] + [
+                   f"lf_fp8_w8a16_qkv_k4096_q4096_kv1024_m{m}" for m in (16, 32)] + [
+                   f"lf_fp8_w8a16_{op}_m128_n{bn}" for op in ("dense", "qkv", "gate_up") for bn in (64, 128)] + [
                    f"lf_fp8_w8a16_dense_wide_k4096_m{m}" for m in (16, 32, 128)] + [
                    "lf_fp8_rms_norm_quant_rows_eps1em5", "lf_fp8_rms_norm_quant_rows_eps1em6"]:
         assert symbol.encode() + b"\0" in image, symbol
@@ -114,16 +115,15 @@ def test_launch_geometry():
     assert sym == "lf_fp8_w8a16_qkv_m16_t1" and dims.grid == (384, 1, 1) and dims.block == (512, 1, 1)
     dims, sym = fp8.launch_geometry(_abi.ENTRY_W8A16_GATE_UP, 14336, 2048, 32)
     assert sym == "lf_fp8_w8a16_gate_up_m32" and dims.grid == (224 * 2, 1, 1)
-    dims, sym = fp8.launch_geometry(_abi.ENTRY_W8A16_QKV, 6144, 4096, 128)
-    assert sym == "lf_fp8_w8a16_qkv_m128" and dims.grid == (96 * 5, 1, 1)
-    dims, sym = fp8.launch_geometry(_abi.ENTRY_W8A16_DENSE, 4096, 2048, 128)
-    assert sym == "lf_fp8_w8a16_dense_m128"   # no entry for this K
+    # 65..128 rows, N not a multiple of 64: the generic column-group form
+    dims, sym = fp8.launch_geometry(_abi.ENTRY_W8A16_QKV, 6160, 4096, 128)
+    assert sym == "lf_fp8_w8a16_qkv_m128" and dims.grid == (97 * 5, 1, 1)
     # split-K workspace: S x (N / 16) x NW x MT 1 KiB fragments + one counter
     # per column group; 256 bytes (unused) without a split
     assert fp8.w8a16_workspace_bytes(_abi.ENTRY_W8A16_DENSE, 4096, 2048, 32) == 8 * 256 * 2 * 1024 + 256
     assert fp8.w8a16_workspace_bytes(_abi.ENTRY_W8A16_QKV, 6144, 4096, 1) == 256
     assert fp8.w8a16_workspace_bytes(_abi.ENTRY_W8A16_GATE_UP, 14336, 2048, 32) == 2 * 896 * 2 * 2 * 1024 + 1024
-    assert fp8.w8a16_workspace_bytes(_abi.ENTRY_W8A16_QKV, 6144, 4096, 128) == 5 * 384 * 8 * 1024 + 512
+    assert fp8.w8a16_workspace_bytes(_abi.ENTRY_W8A16_QKV, 6144, 4096, 128) == 2 * 96 * 8 * 4 * 1024 + 512
     # Shape-specialized (Llama-3-8B) entries for profiles of <= 32 rows.
     dims, sym = fp8.launch_geometry(_abi.ENTRY_W8A16_DENSE, 4096, 14336, 32)
     assert sym == "lf_fp8_w8a16_dense_k14336_m32" and dims.grid == (64 * 4, 1, 1)
@@ -153,18 +153,22 @@ def test_launch_geometry():
     assert sym == "lf_fp8_w8a16_qkv_m32"
     dims, sym = fp8.launch_geometry(_abi.ENTRY_W8A16_DENSE, 4096, 4096, 64)
     assert sym == "lf_fp8_w8a16_dense_m64"
-    # 128-row entries: column groups of 4 tiles over 4 (o, down), 2 (QKV) or
-    # 1 (gate/up) K slices
+    # 65..128 rows: the LDS-tiled GEMM, 128 x BN tiles (BN 128 with at least
+    # 192 column blocks, else 64; gate/up blocks cover BN / 2 h-columns), K
+    # cut into S slices for about 256 blocks with at least 10 k-tiles each
     dims, sym = fp8.launch_geometry(_abi.ENTRY_W8A16_DENSE, 4096, 4096, 128)
-    assert sym == "lf_fp8_w8a16_dense_k4096_m128" and dims.grid == (64 * 4, 1, 1)
-    assert dims.block == (256, 1, 1)
-    assert fp8.w8a16_workspace_bytes(_abi.ENTRY_W8A16_DENSE, 4096, 4096, 128) == 4 * 256 * 8 * 1024 + 256
+    assert sym == "lf_fp8_w8a16_dense_m128_n64" and dims.grid == (64 * 3, 1, 1)
+    assert dims.block == (512, 1, 1)
+    # S x blocks x 8 waves x (2 x BN / 32) 1 KiB fragments + a counter per block
+    assert fp8.w8a16_workspace_bytes(_abi.ENTRY_W8A16_DENSE, 4096, 4096, 128) == 3 * 64 * 8 * 4 * 1024 + 256
     dims, sym = fp8.launch_geometry(_abi.ENTRY_W8A16_DENSE, 4096, 14336, 100)
-    assert sym == "lf_fp8_w8a16_dense_k14336_m128" and dims.grid == (64 * 4, 1, 1)
+    assert sym == "lf_fp8_w8a16_dense_m128_n64" and dims.grid == (64 * 4, 1, 1)
     dims, sym = fp8.launch_geometry(_abi.ENTRY_W8A16_QKV, 6144, 4096, 128, qkv_split=(4096, 1024))
-    assert sym == "lf_fp8_w8a16_qkv_k4096_q4096_kv1024_m128" and dims.grid == (96 * 2, 1, 1)
+    assert sym == "lf_fp8_w8a16_qkv_m128_n64" and dims.grid == (96 * 2, 1, 1)
     dims, sym = fp8.launch_geometry(_abi.ENTRY_W8A16_GATE_UP, 14336, 4096, 128)
-    assert sym == "lf_fp8_w8a16_gate_up_k4096_m128" and dims.grid == (224, 1, 1)
+    assert sym == "lf_fp8_w8a16_gate_up_m128_n128" and dims.grid == (224, 1, 1)
+    dims, sym = fp8.launch_geometry(_abi.ENTRY_W8A16_DENSE, 4096, 2048, 65)
+    assert sym == "lf_fp8_w8a16_dense_m128_n64" and dims.grid == (64, 1, 1)  # 16 k-tiles: no split
     # wide dense shapes (N >= 16384, e.g. the 128,256-column vocabulary head)
     for mt, w in ((16, 2), (32, 4), (128, 8)):
         dims, sym = fp8.launch_geometry(_abi.ENTRY_W8A16_DENSE, 128256, 4096, mt)

@@ -321,7 +321,8 @@ def test_llama3_8b_shapes_sampled(rt, op, m, family):
 ])
 def test_w8a16_specialized_entries(rt, op, m, max_tokens):
     """Every shape-specialized W8A16 entry (Llama-3-8B widths, profiles of
-    <= 16, <= 32 and <= 128 rows) against the oracle on a column sample, with
+    <= 16 and <= 32 rows) and the LDS-tiled GEMM form at 128 rows against the
+    oracle on a column sample, with
     ragged live rows and M = 0; the column-group forms run three launches on
     one workspace, which must be bit-identical."""
     from lunaflux_amd import _abi, fp8
@@ -366,7 +367,10 @@ def test_w8a16_specialized_entries(rt, op, m, max_tokens):
         cols = np.sort(rng.choice(n, 384, replace=False))
         ref = o.dense_projection(xr, deq(q[cols], s[cols]))
         extra = dict(k=k, s_abs=abs_sum(xr, deq(q[cols], s[cols])))
-    assert f"_k{k}_" in sym and sym.endswith(f"_m{max_tokens}"), sym
+    if max_tokens == 128:  # the LDS-tiled GEMM form
+        assert "_m128_n" in sym, sym
+    else:
+        assert f"_k{k}_" in sym and sym.endswith(f"_m{max_tokens}"), sym
     sentinel = np.full(max_tokens * n, 0x7FC1, np.uint16)  # a NaN no kernel writes
     ya.copy_from_host(sentinel)
     outs = []
@@ -378,6 +382,67 @@ def test_w8a16_specialized_entries(rt, op, m, max_tokens):
         assert np.all(y[m:] == 0x7FC1), f"{sym}: rows past M written"
         if m:
             parity(y[:m][:, cols], ref, label=f"{sym} m={m}", **extra)
+    assert all(np.array_equal(outs[0], y) for y in outs[1:]), f"{sym}: launches differ"
+
+
+@pytest.mark.parametrize("op,n,k,qkv_split,m,max_tokens", [
+    ("dense", 3072, 2048, None, 65, 80),        # BN 64, 48 blocks, 16 k-tiles: no split
+    ("dense", 24576, 1024, None, 128, 128),     # BN 128 (192 blocks), no split
+    ("dense", 1024, 8192, None, 100, 128),      # BN 64, 16 blocks, S 6
+    ("qkv", 3072, 4096, (2048, 512), 77, 128),  # S 3; blocks straddle Q|K|V boundaries
+    ("gate_up", 8192, 2048, None, 128, 128),    # BN 64 (256 blocks)
+    ("gate_up", 12288, 4096, None, 90, 96),     # BN 128 (192 blocks)
+])
+def test_w8a16_gemm_form(rt, op, n, k, qkv_split, m, max_tokens):
+    """The LDS-tiled W8A16 GEMM (profiles of 65..128 rows) on shapes other
+    than Llama-3-8B's: each block width, with and without the K split, QKV
+    blocks across the Q|K|V boundaries, ragged M. Column sample against the
+    oracle; rows past M untouched; three launches on one workspace agree
+    bit for bit."""
+    from lunaflux_amd import _abi, fp8
+    from lunaflux_amd.fp8 import _region
+    rng = np.random.default_rng(9100 + n + k + m)
+    x = synth.activations(rng, m, k)
+    xa = rt.context.upload(np.concatenate([x, np.zeros((max_tokens - m, k), np.uint16)]))
+    counts = rt.step_counts(m)
+    xr = x_ref(x, "w8a16")
+    ya = rt.context.allocate(max_tokens * n * 2)
+    cols = np.sort(rng.choice(n, 384, replace=False))
+    extra = {}
+    if op == "qkv":
+        nq, nkv = qkv_split
+        ws = [make_weight(rt, rng, r, k) for r in (nq, nkv, nkv)]
+        sym = fp8.launch_geometry(_abi.ENTRY_W8A16_QKV, n, k, max_tokens, qkv_split=qkv_split)[1]
+        bound = rt.bind_qkv("w8a16", counts, _region(xa, alignment=256), *(w for _, _, w in ws),
+                            _region(ya, alignment=256), max_tokens)
+        wq = np.concatenate([q for q, _, _ in ws])[cols]
+        wsc = np.concatenate([s for _, s, _ in ws])[cols]
+        ref = o.dense_projection(xr, deq(wq, wsc))
+        extra = dict(k=k, s_abs=abs_sum(xr, deq(wq, wsc)))
+    elif op == "gate_up":
+        (qg, sg, wg), (qu, su, wu) = make_weight(rt, rng, n, k), make_weight(rt, rng, n, k)
+        sym = fp8.launch_geometry(_abi.ENTRY_W8A16_GATE_UP, n, k, max_tokens)[1]
+        bound = rt.bind_gate_up("w8a16", counts, _region(xa, alignment=256), wg, wu,
+                                _region(ya, alignment=256), max_tokens)
+        ref = o.silu_mul_array(o.dense_projection(xr, deq(qg[cols], sg[cols])),
+                               o.dense_projection(xr, deq(qu[cols], su[cols])))
+    else:
+        q, s, w = make_weight(rt, rng, n, k)
+        sym = fp8.launch_geometry(_abi.ENTRY_W8A16_DENSE, n, k, max_tokens)[1]
+        bound = rt.bind_dense("w8a16", counts, _region(xa, alignment=256), w,
+                              _region(ya, alignment=256), max_tokens)
+        ref = o.dense_projection(xr, deq(q[cols], s[cols]))
+        extra = dict(k=k, s_abs=abs_sum(xr, deq(q[cols], s[cols])))
+    assert "_m128_n" in sym, sym
+    sentinel = np.full(max_tokens * n, 0x7FC1, np.uint16)
+    ya.copy_from_host(sentinel)
+    outs = []
+    for _ in range(3):
+        bound.launch(rt.stream, synchronous=True)
+        outs.append(ya.read(np.uint16, (max_tokens, n)))
+    for y in outs:
+        assert np.all(y[m:] == 0x7FC1), f"{sym}: rows past M written"
+        parity(y[:m][:, cols], ref, label=f"{sym} {op} n={n} k={k} m={m}", **extra)
     assert all(np.array_equal(outs[0], y) for y in outs[1:]), f"{sym}: launches differ"
 
 
