@@ -241,12 +241,16 @@ int32_t lunaflux_fp8_rms_norm_quant_geometry(float epsilon, int64_t k, int32_t m
  *  lf_moe_sort_count    (counts, desc, ws)
  *  lf_moe_sort          (counts, desc, ws)
  *  lf_moe_quant_tokens  (counts, desc, x bf16 [T, H], ws)
- *  lf_moe_gate_up[_b128|_t256|_t256_b128|_gemv](counts, desc, wg, wu, ws)
- *  lf_moe_quant_hidden  (counts, desc, ws)
+ *  lf_moe_gate_up[_b128|_t256|_t256_b128_q|_gemv](counts, desc, wg, wu, ws)
+ *  lf_moe_quant_hidden  (counts, desc, ws)    (not with _t256_b128_q)
  *  lf_moe_down[_b128|_t256|_t256_b128|_gemv]   (counts, desc, wd, ws)
  * (_t256: the GEMMs on 256 x 256 tiles, chosen by the launch geometry for
  * profiles that average >= 256 routed rows per expert, _t256_b128 with block
- * scales where both GEMMs have K <= 3072; _gemv:
+ * scales where both GEMMs have K <= 3072, its gate/up as _t256_b128_q, whose
+ * epilogue also runs the hidden quantizer (a block's 128 h-columns are one
+ * scale group): lunaflux_fp8_moe_launch_geometry then returns LF_OK with an
+ * empty symbol and zero dims for LF_FP8_MOE_QUANT_HIDDEN, meaning no launch;
+ * _gemv:
  * either scale mode, chosen for profiles of at most 32 tokens, where the
  * GEMMs stream the touched experts' weights: a fixed grid whose blocks
  * loop over (expert with rows, 64-column group) items.

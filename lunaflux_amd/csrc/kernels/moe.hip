@@ -629,9 +629,13 @@ LF_DEVICE float carry_ratio(float s, float &prev) {
   return r;
 }
 
-template <int STAGE, bool BLOCK = false>
+// QUANT (block-scaled gate/up only): the epilogue also quantizes h, writing
+// the hidden quantizer's e4m3 codes and per-128-column scales instead of
+// bf16 h (see the STAGE 0 epilogue below).
+template <int STAGE, bool BLOCK = false, bool QUANT = false>
 __device__ void grouped_gemm_t256(const int32_t *counts, const MoeDesc &d, const uint8_t *w0,
                                   const uint8_t *w1, uint8_t *ws) {
+  static_assert(!QUANT || (STAGE == 0 && BLOCK), "the fused quantizer is the block-scaled gate/up's");
   using T = GemmTile256;
   constexpr int BM = T::kBM;
   __shared__ __attribute__((aligned(1024))) uint8_t smem[T::kSmem];
@@ -767,7 +771,56 @@ __device__ void grouped_gemm_t256(const int32_t *counts, const MoeDesc &d, const
   const int col0 = __builtin_amdgcn_readfirstlane(ocol[0] - c);
   w8a8v4::epilogue_barrier();
   const int pw = p0 + wm * T::kWaveM;
-  if constexpr (STAGE == 0) {
+  if constexpr (QUANT) {
+    // SwiGLU -> bf16 (the value the unfused path stores as h) -> the hidden
+    // quantizer. The block's 128 h-columns are one scale group (bx): the
+    // whole 256 x 128 bf16 tile is staged in LDS, then each wave quantizes
+    // 32 of its rows as lf_moe_quant_hidden does (16 lanes per row, 8
+    // values each: amax over the 16 lanes, ratio = 448 / amax, codes =
+    // e4m3_rne_sat(h * ratio), scale amax / 448; a zero group gets zero codes
+    // and scale 0), so codes and scales are bit for bit that kernel's.
+    constexpr int kPitch = T::kBN / 2 + 8;  // staged bf16 per row: 128 + pad
+    static_assert(T::kBN / 2 == 128, "a block's h-columns are one 128-column group");
+    static_assert(BM * kPitch * 2 <= T::kSmem, "the h tile fits the stage ring");
+    uint16_t *tile = reinterpret_cast<uint16_t *>(smem);
+#pragma unroll
+    for (int i = 0; i < T::kFM; ++i) {
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const int row = wm * T::kWaveM + w8a8v4::acc_row<T>(i, lane, r);
+        const float sa = sa_tile[row];
+#pragma unroll
+        for (int j = 0; j < T::kFN / 2; ++j) {
+          const float gv = acc[i][j][r] * sa * swv[j];
+          const float uv = acc[i][j + T::kFN / 2][r] * sa * swv[j + T::kFN / 2];
+          tile[row * kPitch + ocol[j] - bx * (T::kBN / 2)] =
+              static_cast<uint16_t>(f32_to_bf16(silu_mul(gv, uv)));
+        }
+      }
+    }
+    __syncthreads();
+    uint8_t *hq = at<uint8_t>(ws, L.hq);
+    float *hs = at<float>(ws, L.hs);
+    const int groups = N >> 7, hcol0 = bx * (T::kBN / 2);
+    const int ch = lane & 15;
+    constexpr int kRowsPerWave = BM / T::kWaves;
+#pragma unroll
+    for (int it = 0; it < kRowsPerWave / 4; ++it) {
+      const int row = wave * kRowsPerWave + 4 * it + (lane >> 4);
+      const uint4 v = *reinterpret_cast<const uint4 *>(tile + row * kPitch + ch * 8);
+      float amax = bf16x8_amax(v, 0.0f);
+#pragma unroll
+      for (int off = 8; off > 0; off >>= 1) amax = fmaxf(amax, __shfl_xor(amax, off));
+      const bool zero = amax == 0.0f;
+      const float ratio = zero ? 0.0f : 448.0f / amax;
+      const int p = p0 + row;
+      if (p < pend) {
+        *reinterpret_cast<uint2 *>(hq + static_cast<uint64_t>(p) * N + hcol0 + ch * 8) =
+            bf16x8_encode(v, ratio, zero);
+        if (ch == 0) hs[static_cast<uint64_t>(p) * groups + bx] = zero ? 0.0f : amax / 448.0f;
+      }
+    }
+  } else if constexpr (STAGE == 0) {
     using Stage = w8a8v4::StageTile<uint16_t, 32, T::kWaveN / 2>;
     static_assert(Stage::kBytes * T::kWaves <= T::kSmem, "staging fits the stage ring");
     const Stage st{reinterpret_cast<uint16_t *>(smem + wave * Stage::kBytes)};
@@ -1178,6 +1231,18 @@ __global__ __launch_bounds__(512) void lf_moe_gate_up_t256_b128(const int32_t *c
   const MoeDesc &d = desc_of(desc);
   if (!desc_ok(d) || d.group != 128 || header_of(wg).magic != kWeightMagic) return;
   grouped_gemm_t256<0, true>(counts, d, wg, wu, ws);
+}
+
+// The same with the hidden quantizer fused into the epilogue: writes h's
+// e4m3 codes and per-128-column scales (the arrays lf_moe_quant_hidden
+// fills), not bf16 h; the plan then has no lf_moe_quant_hidden launch.
+__global__ __launch_bounds__(512) void lf_moe_gate_up_t256_b128_q(const int32_t *counts,
+                                                                  const int32_t *desc,
+                                                                  const uint8_t *wg,
+                                                                  const uint8_t *wu, uint8_t *ws) {
+  const MoeDesc &d = desc_of(desc);
+  if (!desc_ok(d) || d.group != 128 || header_of(wg).magic != kWeightMagic) return;
+  grouped_gemm_t256<0, true, true>(counts, d, wg, wu, ws);
 }
 
 __global__ __launch_bounds__(512) void lf_moe_down_t256_b128(const int32_t *counts,

@@ -611,8 +611,9 @@ int32_t lunaflux_fp8_moe_launch_geometry(int32_t entry, const lf_fp8_moe_desc *d
       }
       // 1-D grid over (64 h-column block, 128-row tile); blocks past the
       // live tile count return.
+      // (block scales: the epilogue also quantizes h, see QUANT_HIDDEN)
       if (t256) {
-        name = b128 ? "lf_moe_gate_up_t256_b128" : "lf_moe_gate_up_t256";
+        name = b128 ? "lf_moe_gate_up_t256_b128_q" : "lf_moe_gate_up_t256";
         gx = d->inter / 128 * tiles256;
         bx = 512;
         break;
@@ -621,6 +622,12 @@ int32_t lunaflux_fp8_moe_launch_geometry(int32_t entry, const lf_fp8_moe_desc *d
       gx = d->inter / 64 * tiles;
       break;
     case LF_FP8_MOE_QUANT_HIDDEN:
+      if (t256 && b128 && !gemv) {
+        // fused into the gate/up epilogue: no launch (empty symbol, zero dims)
+        std::memset(dims, 0, 7 * sizeof(int32_t));
+        std::memset(symbol, 0, LF_FP8_SYMBOL_BYTES);
+        return LF_OK;
+      }
       name = "lf_moe_quant_hidden";
       gx = b128 ? group_quant_blocks(A * (d->inter / 128)) : (A + 3) / 4;
       break;

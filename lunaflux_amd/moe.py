@@ -78,7 +78,9 @@ class BoundMoe(BoundOperation):
 def bind_moe(rt: ProjectionRuntime, counts, desc: MoeDescriptor, desc_region: KernelArgument,
              logits: KernelArgument, x: KernelArgument, wg: Fp8Weight, wu: Fp8Weight,
              wd: Fp8Weight, out: KernelArgument, max_tokens: int) -> BoundMoe:
-    """Binds one MoE expert-MLP operation to its regions: 8 launch steps."""
+    """Binds one MoE expert-MLP operation to its regions: 8 launch steps, 7
+    when the gate/up epilogue runs the hidden quantizer (the geometry gives
+    that step an empty symbol)."""
     e, h, i = desc.experts, desc.hidden, desc.inter
     mode = _abi.LF_FP8_SCALE_BLOCK128 if desc.group == 128 else _abi.LF_FP8_SCALE_PER_CHANNEL
     for w, rows, cols in ((wg, i, h), (wu, i, h), (wd, h, i)):
@@ -91,6 +93,8 @@ def bind_moe(rt: ProjectionRuntime, counts, desc: MoeDescriptor, desc_region: Ke
 
     def step(entry, operands):
         dims, symbol = launch_geometry(entry, desc, max_tokens)
+        if not symbol:
+            return None
         return LaunchStep(rt.function(symbol), dims, KernelArguments(operands), symbol)
 
     steps = [
@@ -103,7 +107,7 @@ def bind_moe(rt: ProjectionRuntime, counts, desc: MoeDescriptor, desc_region: Ke
         step(_abi.MOE_DOWN, [c, desc_region, wd.region, wsr]),
         step(_abi.MOE_COMBINE, [c, desc_region, wsr, out]),
     ]
-    return BoundMoe(steps=steps, workspace=ws, desc=desc)
+    return BoundMoe(steps=[s for s in steps if s is not None], workspace=ws, desc=desc)
 
 
 def moe_expert_mlp(rt: ProjectionRuntime, x: np.ndarray, logits: np.ndarray, wg: Fp8Weight,
@@ -135,6 +139,14 @@ def moe_expert_mlp(rt: ProjectionRuntime, x: np.ndarray, logits: np.ndarray, wg:
     out = oa.read(np.uint16, (t, hdim)) if t else np.zeros((0, hdim), np.uint16)
     if not return_workspace:
         return out
+    gate_up = next(s for s in op.steps if s.name.startswith("lf_moe_gate_up"))
+    if gate_up.name.endswith("_q"):
+        # The plan quantized h in the gate/up epilogue and never stored it;
+        # for inspection the unfused kernel writes the bf16 h (and nothing
+        # else the intermediates below hold).
+        plain = gate_up.name[:-2]
+        LaunchStep(rt.function(plain), gate_up.dims, gate_up.args, plain).launch(
+            rt.stream, synchronous=True)
     lay = workspace_layout(desc, t)
     a = t * top_k
     ws = op.workspace

@@ -287,8 +287,12 @@ def test_moe_descriptor_layout_and_geometry():
     dims, sym = moe.launch_geometry(6, d5, 4096)  # down
     assert sym == "lf_moe_down_t256_b128" and dims.grid == (2048 // 256 * (4096 * 6 // 256 + 64), 1, 1)
     assert dims.block == (512, 1, 1)
-    dims, sym = moe.launch_geometry(4, d5, 4096)  # gate/up
-    assert sym == "lf_moe_gate_up_t256_b128" and dims.grid == (1408 // 128 * (4096 * 6 // 256 + 64), 1, 1)
+    dims, sym = moe.launch_geometry(4, d5, 4096)  # gate/up, quantizing h in its epilogue
+    assert sym == "lf_moe_gate_up_t256_b128_q" and dims.grid == (1408 // 128 * (4096 * 6 // 256 + 64), 1, 1)
+    dims, sym = moe.launch_geometry(5, d5, 4096)  # so no hidden-quantizer launch
+    assert sym == "" and dims.grid == (0, 0, 0) and dims.block == (0, 0, 0)
+    assert moe.launch_geometry(5, d5, 2048)[1] == "lf_moe_quant_hidden"
+    assert moe.launch_geometry(5, d5, 32)[1] == "lf_moe_quant_hidden"
     # fewer rows per expert, or K > 3072: 128 x 128 tiles
     dims, sym = moe.launch_geometry(6, d5, 2048)
     assert sym == "lf_moe_down_b128" and dims.grid == (2048 // 128 * (2048 * 6 // 128 + 64), 1, 1)

@@ -48,7 +48,8 @@ def run_case(rt, rng, t, e, k, hidden, inter, mode, block, logits=None, max_toke
              zero_groups=False):
     """zero_groups (block scales): every third token's second 128-column group
     of x and the first 128 x 128 block of every gate, up and down weight are
-    zero, so those scales are 0."""
+    zero, so those scales are 0; token 5 is all zero (so are its rows of h,
+    whose groups then quantize to zero codes and scale 0)."""
     from lunaflux_amd import fp8, moe
     x = synth.activations(rng, t, hidden)
     if logits is None:
@@ -58,6 +59,7 @@ def run_case(rt, rng, t, e, k, hidden, inter, mode, block, logits=None, max_toke
     qd, sd = expert_weights(rng, e, hidden, inter, block)
     if zero_groups:
         x[::3, 128:256] = 0
+        x[5] = 0
         for q, sc in ((qg, sg), (qu, su), (qd, sd)):
             q[:, :128, :128] = 0
             sc.reshape(e, q.shape[1] // 128, q.shape[2] // 128)[:, 0, 0] = 0
@@ -231,7 +233,11 @@ def test_moe_t256(rt, t, e, k, hidden, inter, skew, block):
     mode = 1 if block else 0
     desc = moe.moe_descriptor(e, k, mode, hidden, inter, 128 if block else 0)
     suffix = "_b128" if block else ""
-    assert moe.launch_geometry(_abi.MOE_GATE_UP, desc, t)[1] == "lf_moe_gate_up_t256" + suffix
+    # block scales: the gate/up epilogue quantizes h (no hidden-quantizer
+    # launch); check_output compares its codes and scales bit for bit with
+    # the quantizer applied to the bf16 h of the unfused kernel
+    assert moe.launch_geometry(_abi.MOE_GATE_UP, desc, t)[1] == "lf_moe_gate_up_t256" + suffix + ("_q" if block else "")
+    assert moe.launch_geometry(_abi.MOE_QUANT_HIDDEN, desc, t)[1] == ("" if block else "lf_moe_quant_hidden")
     assert moe.launch_geometry(_abi.MOE_DOWN, desc, t)[1] == "lf_moe_down_t256" + suffix
     rng = np.random.default_rng(950 + t + e + block)
     logits = (rng.standard_normal((t, e)) + rng.normal(0, skew, e)).astype(np.float32)

@@ -205,7 +205,9 @@ def test_moe_config5_fine_grained_full_shape(rt, t, gemm):
     from lunaflux_amd import _abi, moe
     e, k, hidden, inter = 64, 6, 2048, 1408
     desc = moe.moe_descriptor(e, k, 1, hidden, inter, 128)
-    assert moe.launch_geometry(_abi.MOE_GATE_UP, desc, t)[1] == f"lf_moe_gate_up_{gemm}"
+    # (t256 with block scales: the gate/up epilogue quantizes h)
+    fused = "_q" if gemm == "t256_b128" else ""
+    assert moe.launch_geometry(_abi.MOE_GATE_UP, desc, t)[1] == f"lf_moe_gate_up_{gemm}{fused}"
     assert moe.launch_geometry(_abi.MOE_DOWN, desc, t)[1] == f"lf_moe_down_{gemm}"
     rng = np.random.default_rng(50 + t)
     logits = zipf_logits(rng, t, e)
