@@ -131,7 +131,8 @@ int32_t lunaflux_fp8_unpack_weight(const uint8_t *region, int64_t region_bytes,
  * e4m3 codes [M, K] at offset 0, fp32 row scales at offset
  * align256(M * K); its size for a profile is lunaflux_fp8_act_quant_bytes.
  * GatedMlp (model/plan/plan.mbt:47-59) runs as gate_up into the workspace
- * followed by dense(down) from it.
+ * followed by dense(down) from it, or as one W8A16 launch where an entry is
+ * built (lunaflux_fp8_gated_mlp_geometry).
  */
 #define LF_FP8_COUNTS_QUERY_TOKENS 3
 #define LF_FP8_COUNTS_BYTES 20
@@ -153,7 +154,8 @@ enum lf_fp8_entry {
   LF_FP8_ENTRY_W8A8_QKV = 6,
   LF_FP8_ENTRY_W8A8_GATE_UP = 7,
   LF_FP8_ENTRY_RMS_NORM_QUANT_ROWS = 8,
-  LF_FP8_ENTRY_GROUPED = 9 /* admission only: the MoE expert weights */
+  LF_FP8_ENTRY_GROUPED = 9, /* admission only: the MoE expert weights */
+  LF_FP8_ENTRY_W8A16_GATED_MLP = 10
 };
 
 /* Admission of one weight operand's region before an operation is bound,
@@ -196,6 +198,35 @@ int32_t lunaflux_fp8_qkv_launch_geometry(int32_t entry, int64_t nq, int64_t nkv,
                                          int32_t max_tokens, int32_t dims[7],
                                          char symbol[LF_FP8_SYMBOL_BYTES]);
 int64_t lunaflux_fp8_qkv_w8a16_workspace_bytes(int64_t nq, int64_t nkv, int64_t k,
+                                               int32_t max_tokens);
+
+/* GatedMlp in one launch (model/plan/plan.mbt:47-59: one operation of arity
+ * (4, 1); kernels/reference/mlp.mbt:4-39), W8A16, built for the Llama-3-8B
+ * widths (H = 4096, I = 14336) and profiles of <= 16 and <= 32 rows:
+ *  lf_fp8_w8a16_gated_mlp_h4096_i14336_m16 / _m32
+ *      (counts, x, wg, wu, wd, y, ws)   x, y bf16 [M, H]
+ * The same arithmetic as the W8A16 gate_up launch (h rounded to bf16) then
+ * the dense(down) launch: the grid's first blocks compute h into ws, the
+ * others the down projection, each down K-slice starting once the blocks
+ * writing its h columns have counted themselves done (bounded polls that
+ * cannot hang; a poll that ran out sets the int32 error word at ws + size -
+ * LF_FP8_GATED_MLP_ERROR_OFFSET_FROM_END, never on a correct launch, and
+ * the word stays set). ws: lunaflux_fp8_gated_mlp_workspace_bytes bytes,
+ * zero-filled once when allocated (its counters return to zero at the end
+ * of every launch; launches sharing one ws must not overlap). Geometry and
+ * symbol from lunaflux_fp8_gated_mlp_geometry, which returns LF_UNSUPPORTED
+ * for shapes or profiles without an entry: the operation then runs as the
+ * gate_up and dense launches. Weights are admitted as for the dense entries
+ * (entry LF_FP8_ENTRY_W8A16_GATED_MLP, per-channel scales). On MI355X the
+ * two launches are faster (38.6 vs 44.8 us at M = 32: back-to-back launches
+ * cost little, and the down blocks learn that h is complete 3-5 us after the
+ * last gate/up block counts itself), so this entry is for callers that need
+ * the operation as a single launch. */
+#define LF_FP8_GATED_MLP_ERROR_OFFSET_FROM_END 128
+int32_t lunaflux_fp8_gated_mlp_geometry(int32_t entry, int64_t hidden, int64_t inter,
+                                        int32_t max_tokens, int32_t dims[7],
+                                        char symbol[LF_FP8_SYMBOL_BYTES]);
+int64_t lunaflux_fp8_gated_mlp_workspace_bytes(int32_t entry, int64_t hidden, int64_t inter,
                                                int32_t max_tokens);
 
 /* RmsNorm fused with the per-token quantizer: the RmsNorm operation

@@ -52,6 +52,8 @@ ENTRY_W8A8_QKV = 6
 ENTRY_W8A8_GATE_UP = 7
 ENTRY_RMS_NORM_QUANT_ROWS = 8
 ENTRY_GROUPED = 9
+ENTRY_W8A16_GATED_MLP = 10
+LF_FP8_GATED_MLP_ERROR_OFFSET_FROM_END = 128
 
 _vp = ctypes.c_void_p
 _i32 = ctypes.c_int32
@@ -108,6 +110,8 @@ SIGNATURES = {
     "lunaflux_fp8_act_quant_bytes": (_i64, [_i64, _i64]),
     "lunaflux_fp8_w8a16_workspace_bytes": (_i64, [_i32, _i64, _i64, _i32]),
     "lunaflux_fp8_launch_geometry": (_i32, [_i32, _i64, _i64, _i32, _i32p, ctypes.c_char_p]),
+    "lunaflux_fp8_gated_mlp_geometry": (_i32, [_i32, _i64, _i64, _i32, _i32p, ctypes.c_char_p]),
+    "lunaflux_fp8_gated_mlp_workspace_bytes": (_i64, [_i32, _i64, _i64, _i32]),
     "lunaflux_fp8_qkv_launch_geometry": (_i32, [_i32, _i64, _i64, _i64, _i32, _i32p,
                                                 ctypes.c_char_p]),
     "lunaflux_fp8_qkv_w8a16_workspace_bytes": (_i64, [_i64, _i64, _i64, _i32]),

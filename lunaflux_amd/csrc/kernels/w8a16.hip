@@ -102,7 +102,10 @@ LF_DEVICE void wait_vm_multiple(int n) {
 // back and invalidate the whole L2 of the XCD, once per block.)
 // Fragment layout: 256 floats, element e of lane l at e * 64 + l, so each
 // store or load instruction covers 256 contiguous bytes.
-template <int MT, int NW, int MODE>
+// COHERENT: the outputs are written with agent-scope stores, which write
+// through the XCD's L2, so blocks of the same launch on other XCDs can read
+// them once the writer's stores have completed.
+template <int MT, int NW, int MODE, bool COHERENT = false>
 LF_DEVICE void group_epilogue(const f32x4 (&acc)[MT][NW], const float (&sc)[NW], int M, int S,
                               int s, int cg, int tiles, int out_tile, bool active, int ld,
                               uint16_t *y, uint8_t *ws, int &last_block) {
@@ -111,7 +114,13 @@ LF_DEVICE void group_epilogue(const f32x4 (&acc)[MT][NW], const float (&sc)[NW],
   const int col = out_tile * 16 + r;
   auto finish = [&](int m, const float (&v)[NW]) {
     const float out = MODE == 2 ? silu_mul(v[0] * sc[0], v[NW - 1] * sc[NW - 1]) : v[0] * sc[0];
-    y[static_cast<uint64_t>(m) * ld + col] = static_cast<uint16_t>(f32_to_bf16(out));
+    const uint16_t bits = static_cast<uint16_t>(f32_to_bf16(out));
+    if constexpr (COHERENT) {
+      __hip_atomic_store(y + static_cast<uint64_t>(m) * ld + col, bits, __ATOMIC_RELAXED,
+                         __HIP_MEMORY_SCOPE_AGENT);
+    } else {
+      y[static_cast<uint64_t>(m) * ld + col] = bits;
+    }
   };
   if (S == 1) {
     if (!active) return;
@@ -706,10 +715,21 @@ __device__ __forceinline__ void w8a16_fixed_kernel(const int32_t *counts, const 
 // waves after one barrier per k-tile. The barrier waits only for LDS
 // writes (no memory fence), so the weight ring stays in flight across it.
 // ---------------------------------------------------------------------------
-template <int K, int S, int WAVES, int MT, int MODE, int DW, int DX, int NQ = 0, int NKV = 0>
+// No wait before the activation loads (see the one-launch GatedMlp below).
+struct NoWait {
+  LF_DEVICE void operator()(int) const {}
+};
+
+// bid / nblocks: the block's index and the block count of this kernel's
+// part of the grid (default: blockIdx.x, gridDim.x). wait(s) runs after the
+// weight prologue is in flight and before the first activation load of
+// K-slice s.
+template <int K, int S, int WAVES, int MT, int MODE, int DW, int DX, int NQ = 0, int NKV = 0,
+          class Wait = NoWait, bool COHERENT_OUT = false>
 __device__ __forceinline__ void w8a16_fixed_group_kernel(const int32_t *counts, const uint16_t *x,
                                          const uint8_t *w0, const uint8_t *w1, const uint8_t *w2,
-                                         uint16_t *y, uint8_t *ws) {
+                                         uint16_t *y, uint8_t *ws, int bid = -1, int nblocks = -1,
+                                         const Wait &wait = Wait{}) {
   constexpr int NW = MODE == 2 ? 2 : 1;
   constexpr int KT = K / 128;
   static_assert(K % 128 == 0 && KT % S == 0, "K splits evenly into the slices");
@@ -727,9 +747,11 @@ __device__ __forceinline__ void w8a16_fixed_group_kernel(const int32_t *counts, 
   __shared__ __attribute__((aligned(16))) u32x4 xs[2 * kSlot];
   __shared__ int last_block;
 
-  const int groups = static_cast<int>(gridDim.x) / S;
-  const int cg = static_cast<int>(blockIdx.x) / S;
-  const int s = static_cast<int>(blockIdx.x) - cg * S;
+  const int nb = nblocks < 0 ? static_cast<int>(gridDim.x) : nblocks;
+  const int block = bid < 0 ? static_cast<int>(blockIdx.x) : bid;
+  const int groups = nb / S;
+  const int cg = block / S;
+  const int s = block - cg * S;
   const int tiles = groups * WAVES;
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int g = lane >> 4, r = lane & 15;
@@ -789,6 +811,7 @@ __device__ __forceinline__ void w8a16_fixed_group_kernel(const int32_t *counts, 
 #pragma unroll
     for (int j = 0; j < XPW; ++j) dst[j] = *reinterpret_cast<const u32x4 *>(xsrc[j] + k * 128);
   };
+  wait(s);
   u32x4 a[EX][XPW];
 #pragma unroll
   for (int d = 0; d < EX; ++d) load_a(d, a[d]);
@@ -832,9 +855,111 @@ __device__ __forceinline__ void w8a16_fixed_group_kernel(const int32_t *counts, 
     __builtin_amdgcn_sched_barrier(0);
   });
 
-  group_epilogue<MT, NW, MODE>(acc, sc, M, S, s, cg, tiles, out_tile, true, ld, y, ws,
+  group_epilogue<MT, NW, MODE, COHERENT_OUT>(acc, sc, M, S, s, cg, tiles, out_tile, true, ld, y, ws,
                                last_block);
 }
+
+// ---------------------------------------------------------------------------
+// GatedMlp in one launch (x -> SiLU(x Wg^T) * (x Wu^T) -> h -> h Wd^T): the
+// grid's first G1 blocks run the gate/up column-group kernel (K = H, split
+// 1) into h in the workspace, the next G2 blocks the down column-group
+// kernel (K = I, split DN_S) on h. Down K-slice s needs the h columns of
+// G1 / DN_S gate/up blocks, which write h with agent-scope stores (through
+// the XCD's L2; each 128-byte line of h has one writer) and count
+// themselves into sync[s] once every wave's stores have completed - the
+// pattern of the split-K exchange. A down block starts its weight ring,
+// then one lane polls sync[s] before the block loads h: no block on the down
+// block's XCD has read those lines of h in this launch (each is read only
+// after its slice is complete), so the loads miss to memory and see the
+// written values. (L2-wide write-back and invalidate fences in their place
+// tripled the operation's time.)
+//
+// Measured on MI355X (Llama-3-8B widths, weights rotated past the MALL),
+// this form is slower than the two launches it replaces: 40.2 vs 32.3 us at
+// M = 1 and 44.8 vs 38.6 us at M = 32. Back-to-back launches on one queue
+// cost almost nothing at the boundary, the down part cannot start before
+// the last gate/up block of its slice, and that block's count reaches the
+// polling down blocks 3-5 us after it is issued (per-block timestamps), so
+// the overlap it buys is smaller than the signalling delay. It is built for
+// callers that need the operation as one launch; the plan binds the two
+// launches by default.
+//
+// Blocks are dispatched in index order on each XCD, so every gate/up block
+// has a CU before any down block of its XCD takes one, and gate/up blocks
+// wait for nothing: the polls end. They are bounded all the same (about
+// 2^20 polls, far beyond any real wait): one that runs out sets the error
+// word and goes on, so no launch can hang. The last down block to finish
+// resets the slice counters and its own done counter for the next launch.
+//
+// Workspace: h [16 MT rows][I] bf16 | the down kernel's split-K partials
+// and arrival counters | sync: slice counters [DN_S], done (+64 B), error
+// (+128 B; stays set, 0 on every correct launch).
+constexpr int kGatedSpinLimit = 1 << 20;
+
+struct SliceWait {
+  int *counters;
+  int target;
+  int *error;
+  LF_DEVICE void operator()(int s) const {
+    if (threadIdx.x == 0) {
+      int spins = 0;
+      while (__hip_atomic_load(counters + s, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) < target) {
+        if (++spins > kGatedSpinLimit) {
+          __hip_atomic_store(error, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+          break;
+        }
+        __builtin_amdgcn_s_sleep(1);
+      }
+    }
+    __syncthreads();
+  }
+};
+
+template <int H, int I, int MT, int GU_W, int GU_DW, int GU_DX, int DN_S, int DN_W, int DN_DW,
+          int DN_DX>
+struct GatedMlpFixed {
+  static constexpr int kG1 = I / 16 / GU_W;
+  static constexpr int kG2 = H / 16 / DN_W * DN_S;
+  static constexpr int kSliceCols = I / DN_S;
+  static_assert(kSliceCols % (GU_W * 16) == 0 && kSliceCols % 128 == 0, "slices of whole blocks");
+  static constexpr uint64_t kHBytes = (16ull * MT * I * 2 + 255) & ~255ull;
+  static constexpr uint64_t kDownBytes =
+      ((static_cast<uint64_t>(DN_S) * (H / 16) * MT * 1024 + 255) & ~255ull) +
+      (((H / 16 / DN_W) * 4 + 255) & ~255ull);
+  static constexpr uint64_t kSyncBytes = 256;
+  static_assert(DN_S <= 16, "slice counters fit before the done word");
+
+  LF_DEVICE static void run(const int32_t *counts, const uint16_t *x, const uint8_t *wg,
+                            const uint8_t *wu, const uint8_t *wd, uint16_t *y, uint8_t *ws) {
+    uint16_t *h = reinterpret_cast<uint16_t *>(ws);
+    uint8_t *ws_down = ws + kHBytes;
+    int *sync = reinterpret_cast<int *>(ws + kHBytes + kDownBytes);
+    const int b = static_cast<int>(blockIdx.x);
+    if (b < kG1) {
+      w8a16_fixed_group_kernel<H, 1, GU_W, MT, 2, GU_DW, GU_DX, 0, 0, NoWait, true>(
+          counts, x, wg, wu, wu, h, ws_down, b, kG1);
+      asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+      __syncthreads();
+      if (threadIdx.x == 0) {
+        __hip_atomic_fetch_add(sync + (b * GU_W * 16) / kSliceCols, 1, __ATOMIC_RELAXED,
+                               __HIP_MEMORY_SCOPE_AGENT);
+      }
+      return;
+    }
+    const SliceWait wait{sync, kSliceCols / (GU_W * 16), sync + 32};
+    w8a16_fixed_group_kernel<I, DN_S, DN_W, MT, 0, DN_DW, DN_DX, 0, 0, SliceWait>(
+        counts, h, wd, wd, wd, y, ws_down, b - kG1, kG2, wait);
+    if (threadIdx.x == 0) {
+      const int before = __hip_atomic_fetch_add(sync + 16, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      if (before == kG2 - 1) {
+        for (int s = 0; s < DN_S; ++s) {
+          __hip_atomic_store(sync + s, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        }
+        __hip_atomic_store(sync + 16, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      }
+    }
+  }
+};
 
 }  // namespace
 
@@ -943,5 +1068,20 @@ LF_W16_FIXED_GATE_UP_G(4096, 32, 2, 1, 4, 3, 2)
 LF_W16_FIXED_DENSE_WIDE_G(4096, 16, 1, 1, 2, 4, 2)
 LF_W16_FIXED_DENSE_WIDE_G(4096, 32, 2, 1, 4, 3, 2)
 LF_W16_FIXED_DENSE_WIDE_G(4096, 128, 8, 1, 8, 2, 1)
+
+// One-launch GatedMlp, Llama-3-8B widths (H 4096, I 14336), operands
+// (counts, x, wg, wu, wd, y, ws): the profile's gate/up and down column-group
+// parameters (blocks of GU_W = DN_W waves).
+#define LF_W16_GATED_MLP(M, MT, GU_W, GU_DW, GU_DX, DN_S, DN_W, DN_DW, DN_DX)                     \
+  __global__ __launch_bounds__(64 * GU_W) void lf_fp8_w8a16_gated_mlp_h4096_i14336_m##M(        \
+      const int32_t *counts, const uint16_t *x, const uint8_t *wg, const uint8_t *wu,            \
+      const uint8_t *wd, uint16_t *y, uint8_t *ws) {                                             \
+    static_assert(GU_W == DN_W, "one block size");                                              \
+    GatedMlpFixed<4096, 14336, MT, GU_W, GU_DW, GU_DX, DN_S, DN_W, DN_DW, DN_DX>::run(           \
+        counts, x, wg, wu, wd, y, ws);                                                           \
+  }
+
+LF_W16_GATED_MLP(16, 1, 4, 4, 2, 4, 4, 6, 2)
+LF_W16_GATED_MLP(32, 2, 4, 3, 2, 4, 4, 6, 2)
 
 }  // extern "C"

@@ -197,6 +197,37 @@ bool w8a16_gemm(int32_t entry, int64_t n, int64_t k, int32_t max_tokens, W8a16Ge
   return true;
 }
 
+// One-launch GatedMlp entries (kernels/w8a16.hip, LF_W16_GATED_MLP): the
+// profile's gate/up and down column-group parameters. Workspace: h [16 mt
+// rows][I] bf16, the down kernel's split-K partials and arrival counters,
+// then 256 bytes of slice counters, done counter and error word.
+struct W8a16Gated {
+  int64_t hidden, inter;
+  int mt, waves, down_split;
+  const char *symbol;
+};
+constexpr W8a16Gated kW8a16Gated[] = {
+    {4096, 14336, 1, 4, 4, "lf_fp8_w8a16_gated_mlp_h4096_i14336_m16"},
+    {4096, 14336, 2, 4, 4, "lf_fp8_w8a16_gated_mlp_h4096_i14336_m32"},
+};
+
+const W8a16Gated *w8a16_gated(int32_t entry, int64_t hidden, int64_t inter, int32_t max_tokens) {
+  if (entry != LF_FP8_ENTRY_W8A16_GATED_MLP || max_tokens <= 0 || max_tokens > 32) return nullptr;
+  const int mt = max_tokens <= 16 ? 1 : 2;
+  for (const W8a16Gated &g : kW8a16Gated) {
+    if (g.hidden == hidden && g.inter == inter && g.mt == mt) return &g;
+  }
+  return nullptr;
+}
+
+int64_t w8a16_gated_workspace(const W8a16Gated &g) {
+  const int64_t h = align_up(16 * g.mt * g.inter * 2, 256);
+  const int64_t tiles = g.hidden / 16;
+  const int64_t down = align_up(g.down_split * tiles * g.mt * 1024, 256) +
+                       align_up(tiles / g.waves * 4, 256);
+  return h + down + 256;
+}
+
 int64_t w8a16_gemm_workspace(const W8a16Gemm &g) {
   if (g.split == 1) return 256;
   // one 1 KiB fp32 fragment per (slice, column block, wave, fragment): 8
@@ -298,7 +329,8 @@ int32_t lunaflux_fp8_admit_weight(int32_t entry, const uint8_t *region_head, int
                                   int32_t experts) {
   const bool dense = entry == LF_FP8_ENTRY_W8A16_DENSE || entry == LF_FP8_ENTRY_W8A16_QKV ||
                      entry == LF_FP8_ENTRY_W8A16_GATE_UP || entry == LF_FP8_ENTRY_W8A8_DENSE ||
-                     entry == LF_FP8_ENTRY_W8A8_QKV || entry == LF_FP8_ENTRY_W8A8_GATE_UP;
+                     entry == LF_FP8_ENTRY_W8A8_QKV || entry == LF_FP8_ENTRY_W8A8_GATE_UP ||
+                     entry == LF_FP8_ENTRY_W8A16_GATED_MLP;
   const bool grouped = entry == LF_FP8_ENTRY_GROUPED;
   if ((!dense && !grouped) || region_head == nullptr || head_bytes < LF_FP8_HEADER_BYTES ||
       (dense && experts != 1)) {
@@ -362,6 +394,30 @@ static int64_t w8a16_workspace(int32_t entry, int64_t n, int64_t k, int64_t nq, 
 int64_t lunaflux_fp8_w8a16_workspace_bytes(int32_t entry, int64_t n, int64_t k,
                                            int32_t max_tokens) {
   return w8a16_workspace(entry, n, k, 0, 0, max_tokens);
+}
+
+int64_t lunaflux_fp8_gated_mlp_workspace_bytes(int32_t entry, int64_t hidden, int64_t inter,
+                                               int32_t max_tokens) {
+  const W8a16Gated *g = w8a16_gated(entry, hidden, inter, max_tokens);
+  return g == nullptr ? -1 : w8a16_gated_workspace(*g);
+}
+
+int32_t lunaflux_fp8_gated_mlp_geometry(int32_t entry, int64_t hidden, int64_t inter,
+                                        int32_t max_tokens, int32_t dims[7],
+                                        char symbol[LF_FP8_SYMBOL_BYTES]) {
+  if (dims == nullptr || symbol == nullptr || hidden <= 0 || inter <= 0 || max_tokens <= 0) {
+    return LF_INVALID_ARGUMENT;
+  }
+  const W8a16Gated *g = w8a16_gated(entry, hidden, inter, max_tokens);
+  if (g == nullptr) return LF_UNSUPPORTED;
+  // gate/up blocks (I / 16 / waves, split 1) then down blocks (H / 16 /
+  // waves column groups x the down split)
+  const int64_t blocks = g->inter / 16 / g->waves + g->hidden / 16 / g->waves * g->down_split;
+  const int32_t values[7] = {static_cast<int32_t>(blocks), 1, 1, 64 * g->waves, 1, 1, 0};
+  std::memcpy(dims, values, sizeof(values));
+  std::memset(symbol, 0, LF_FP8_SYMBOL_BYTES);
+  std::snprintf(symbol, LF_FP8_SYMBOL_BYTES, "%s", g->symbol);
+  return LF_OK;
 }
 
 int32_t lunaflux_fp8_rms_norm_quant_geometry(float epsilon, int64_t k, int32_t max_rows,

@@ -141,6 +141,20 @@ def launch_geometry(entry: int, n: int, k: int, max_tokens: int,
             symbol.value.decode("ascii"))
 
 
+def gated_mlp_geometry(hidden: int, inter: int, max_tokens: int):
+    """(dims, symbol) of the one-launch W8A16 GatedMlp entry for the shape and
+    profile, or None where none is built."""
+    dims = (ctypes.c_int32 * 7)()
+    symbol = ctypes.create_string_buffer(128)
+    status = _abi.lib().lunaflux_fp8_gated_mlp_geometry(_abi.ENTRY_W8A16_GATED_MLP, hidden, inter,
+                                                        max_tokens, dims, symbol)
+    if status == _abi.LF_UNSUPPORTED:
+        return None
+    _check("gated_mlp_geometry", status)
+    return (KernelLaunchDimensions.new(tuple(dims[0:3]), tuple(dims[3:6]), dims[6]),
+            symbol.value.decode("ascii"))
+
+
 def rms_norm_quant_geometry(epsilon: float, k: int, max_rows: int):
     """(dims, symbol) of the fused RmsNorm + quantizer entry for an epsilon
     (fp32), input width K and profile; DeviceError(UNSUPPORTED) for an
@@ -342,11 +356,34 @@ class ProjectionRuntime:
 
     def bind_gated_mlp(self, family: str, counts: Allocation, x: KernelArgument, wg: Fp8Weight,
                        wu: Fp8Weight, wd: Fp8Weight, y: KernelArgument,
-                       max_tokens: int) -> BoundOperation:
+                       max_tokens: int, one_launch: bool = False) -> BoundOperation:
         """GatedMlp (model/plan/plan.mbt:47-59): gate/up + SwiGLU into a bf16
-        intermediate in the workspace, then the down projection from it."""
+        intermediate in the workspace, then the down projection from it (two
+        launch steps of one operation). one_launch=True binds the one-launch
+        W8A16 entry instead where one is built for the shape and profile
+        (lunaflux_fp8_gated_mlp_*); it computes the same values and is
+        slower on MI355X (44.8 vs 38.6 us at M = 32), so it is not the
+        default."""
         if wd.columns != wg.rows or wd.rows != wg.columns:
             raise DeviceError("mlp shapes", _abi.LF_INVALID_ARGUMENT)
+        if wg.rows != wu.rows or wg.columns != wu.columns:
+            raise DeviceError("gate/up shapes", _abi.LF_INVALID_ARGUMENT)
+        if family == "w8a16" and one_launch:
+            geometry = gated_mlp_geometry(wg.columns, wg.rows, max_tokens)
+            if geometry is not None:
+                _family(family, max_tokens)
+                for w in (wg, wu, wd):
+                    w.admit(_abi.ENTRY_W8A16_GATED_MLP)
+                dims, symbol = geometry
+                nbytes = _abi.lib().lunaflux_fp8_gated_mlp_workspace_bytes(
+                    _abi.ENTRY_W8A16_GATED_MLP, wg.columns, wg.rows, max_tokens)
+                ws = self.context.allocate(nbytes)
+                ws.copy_from_host(np.zeros(nbytes, np.uint8))
+                c = _region(counts, COUNTS_BYTES, alignment=4)
+                step = LaunchStep(self.function(symbol), dims,
+                                  KernelArguments([c, x, wg.region, wu.region, wd.region, y,
+                                                   _region(ws, alignment=256)]), symbol)
+                return BoundOperation([step], workspace=ws)
         h_bytes = max_tokens * wg.rows * 2
         h_alloc = self.context.allocate(h_bytes)
         h = _region(h_alloc, h_bytes, alignment=256)

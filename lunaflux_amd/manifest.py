@@ -54,6 +54,7 @@ FAMILIES = (
     (7, "lf_fp8_w8a8_qkv_"),
     (8, "lf_fp8_w8a8_gate_up_"),
     (9, "lf_moe_"),
+    (10, "lf_fp8_w8a16_gated_mlp_"),
 )
 
 

@@ -270,6 +270,57 @@ def test_silu_gated_mlp(rt, family, m, max_tokens):
     parity(y, ref, label=f"mlp {family} m={m}")
 
 
+@pytest.mark.parametrize("m,max_tokens", [(1, 16), (13, 16), (16, 16), (17, 32), (32, 32), (0, 32)])
+def test_gated_mlp_one_launch(rt, m, max_tokens):
+    """The one-launch W8A16 GatedMlp at the Llama-3-8B widths (H 4096, I
+    14336): against the oracle on a column sample of y (h rounded to bf16
+    between the GEMMs, as the two-launch form keeps it); bit-identical to
+    the two-launch form where both use the same column-group kernels (the
+    32-row profile); three launches on one workspace agree bit for bit (the
+    slice and done counters return to zero) and leave the error word 0;
+    rows past M untouched."""
+    from lunaflux_amd import _abi
+    from lunaflux_amd.fp8 import _region
+    rng = np.random.default_rng(7300 + m + max_tokens)
+    hidden, inter = 4096, 14336
+    x = synth.activations(rng, max(m, 1), hidden)[:m]
+    qg, sg, wg = make_weight(rt, rng, inter, hidden)
+    qu, su, wu = make_weight(rt, rng, inter, hidden)
+    qd, sd, wd = make_weight(rt, rng, hidden, inter)
+    xa = rt.context.upload(np.concatenate([x, np.zeros((max_tokens - m, hidden), np.uint16)]))
+    counts = rt.step_counts(m)
+    ya = rt.context.allocate(max_tokens * hidden * 2)
+    one = rt.bind_gated_mlp("w8a16", counts, _region(xa, alignment=256), wg, wu, wd,
+                            _region(ya, alignment=256), max_tokens, one_launch=True)
+    assert len(one.steps) == 1 and one.steps[0].name.startswith("lf_fp8_w8a16_gated_mlp_"), one.steps
+    sentinel = np.full(max_tokens * hidden, 0x7FC1, np.uint16)
+    ya.copy_from_host(sentinel)
+    outs = []
+    for _ in range(3):
+        one.launch(rt.stream, synchronous=True)
+        outs.append(ya.read(np.uint16, (max_tokens, hidden)))
+    ws = one.workspace
+    err = ws.read(np.int32, (1,), ws.byte_count - _abi.LF_FP8_GATED_MLP_ERROR_OFFSET_FROM_END)
+    assert err[0] == 0, "a down block's wait for h ran out"
+    assert all(np.array_equal(outs[0], y) for y in outs[1:]), "launches differ"
+    assert np.all(outs[0][m:] == 0x7FC1), "rows past M written"
+    if m:
+        cols = np.sort(rng.choice(hidden, 256, replace=False))
+        xr = x_ref(x, "w8a16")
+        h = o.silu_mul_array(o.dense_projection(xr, deq(qg, sg)), o.dense_projection(xr, deq(qu, su)))
+        hb = o.bf16_decode(o.bf16_round(h))
+        wdc = deq(qd[cols], sd[cols])
+        parity(outs[0][:m][:, cols], o.dense_projection(hb, wdc), k=inter, s_abs=abs_sum(hb, wdc),
+               label=f"gated mlp one launch m={m}")
+    if max_tokens == 32:
+        ya.copy_from_host(sentinel)
+        two = rt.bind_gated_mlp("w8a16", counts, _region(xa, alignment=256), wg, wu, wd,
+                                _region(ya, alignment=256), max_tokens)
+        assert len(two.steps) == 2
+        two.launch(rt.stream, synchronous=True)
+        assert np.array_equal(ya.read(np.uint16, (max_tokens, hidden)), outs[0])
+
+
 @pytest.mark.parametrize("op,m,family", [
     ("qkv", 32, "w8a16"), ("gate_up", 32, "w8a16"), ("down", 32, "w8a16"), ("o", 1, "w8a16"),
     ("qkv", 2048, "w8a8"), ("o", 2048, "w8a8"), ("gate_up", 2048, "w8a8"), ("down", 2048, "w8a8"),
