@@ -159,42 +159,40 @@ void w8a16_fixed_geometry(const W8a16Fixed &f, int64_t n, int32_t *gx, int32_t *
 // Profiles of 65..128 rows: the LDS-tiled GEMM (kernels/w8a16_gemm.hip,
 // "lf_fp8_w8a16_{op}_m128_n{BN}"), any K, any N its blocks divide. A block
 // (8 waves) computes 128 rows x BN weight columns (gate/up: BN / 2 gate and
-// BN / 2 up columns); BN is 128 when that still gives at least 192 column
-// blocks, else 64. K is cut into S slices so that the launch has about 256
-// blocks, keeping at least 10 k-tiles per slice. Measured at M = 128 on the
-// Llama-3-8B shapes (MI355X, weights rotated past the MALL): o 18.5 -> 15.0
-// us (BN 64, S 3), QKV 23.5 -> 19.1 (64, 2), down 36.8 -> 30.6 (64, 4),
-// gate/up 44.9 -> 43.2 (128, 1), against the column-group form.
-// Vocabulary-wide dense shapes with a column-group entry keep it.
+// BN / 2 up columns) over one of S K-slices. BN 128 with the fewest slices
+// that give >= 192 blocks, if each slice keeps >= 8 k-tiles; else BN 64 the
+// same way; else BN 64 with slices of 8 k-tiles. Measured at M = 128 on the
+// Llama-3-8B shapes (MI355X, >= 512 MB of weight copies rotated so the MALL
+// serves none), against the column-group entries this form replaced:
+// gate/up 48.4 -> 44.8 us (BN 128, S 1), QKV 24.2 -> 21.3 (128, 4), o
+// 21.0 -> 17.8 (64, 3), down 38.6 -> 32.5 (128, 6). Vocabulary-wide dense
+// shapes with a column-group entry keep it.
 struct W8a16Gemm {
   int bn;
   int64_t blocks_n, split;
 };
 bool w8a16_gemm(int32_t entry, int64_t n, int64_t k, int32_t max_tokens, W8a16Gemm *out) {
-  if (max_tokens <= 64 || max_tokens > 128 || n <= 0 || k % 128 != 0) return false;
+  if (max_tokens <= 64 || max_tokens > 128 || n <= 0 || k <= 0 || k % 128 != 0) return false;
   if (entry == LF_FP8_ENTRY_W8A16_DENSE && n >= kWideN &&
       w8a16_fixed(entry, n, k, 0, 0, max_tokens) != nullptr) {
     return false;
   }
-  const int64_t per128 = entry == LF_FP8_ENTRY_W8A16_GATE_UP ? 64 : 128;
-  const int64_t per64 = per128 / 2;
-  if (n % per128 == 0 && n / per128 >= 192) {
-    out->bn = 128;
-    out->blocks_n = n / per128;
-  } else if (n % per64 == 0) {
-    out->bn = 64;
-    out->blocks_n = n / per64;
-  } else {
-    return false;
-  }
   const int64_t kt = k / 128;
-  int64_t split = 256 / out->blocks_n;
-  while (split > 1 && kt / split < 10) --split;
-  if (split < 1) split = 1;
-  if (split > kt) split = kt;
-  if (out->blocks_n * split > INT32_MAX) return false;
-  out->split = split;
-  return true;
+  constexpr int64_t kMinBlocks = 192, kMinSliceTiles = 8;
+  for (const int bn : {128, 64}) {
+    const int64_t per = entry == LF_FP8_ENTRY_W8A16_GATE_UP ? bn / 2 : bn;
+    if (n % per != 0) continue;
+    const int64_t blocks = n / per;
+    const int64_t split = std::max<int64_t>(1, (kMinBlocks + blocks - 1) / blocks);
+    if (split <= kt && kt / split >= kMinSliceTiles) {
+      *out = W8a16Gemm{bn, blocks, split};
+      return blocks * split <= INT32_MAX;
+    }
+  }
+  const int64_t per = entry == LF_FP8_ENTRY_W8A16_GATE_UP ? 32 : 64;
+  if (n % per != 0) return false;
+  *out = W8a16Gemm{64, n / per, std::max<int64_t>(1, kt / kMinSliceTiles)};
+  return out->blocks_n * out->split <= INT32_MAX;
 }
 
 // One-launch GatedMlp entries (kernels/w8a16.hip, LF_W16_GATED_MLP): the

@@ -123,7 +123,7 @@ def test_launch_geometry():
     assert fp8.w8a16_workspace_bytes(_abi.ENTRY_W8A16_DENSE, 4096, 2048, 32) == 8 * 256 * 2 * 1024 + 256
     assert fp8.w8a16_workspace_bytes(_abi.ENTRY_W8A16_QKV, 6144, 4096, 1) == 256
     assert fp8.w8a16_workspace_bytes(_abi.ENTRY_W8A16_GATE_UP, 14336, 2048, 32) == 2 * 896 * 2 * 2 * 1024 + 1024
-    assert fp8.w8a16_workspace_bytes(_abi.ENTRY_W8A16_QKV, 6144, 4096, 128) == 2 * 96 * 8 * 4 * 1024 + 512
+    assert fp8.w8a16_workspace_bytes(_abi.ENTRY_W8A16_QKV, 6144, 4096, 128) == 4 * 48 * 8 * 8 * 1024 + 256
     # Shape-specialized (Llama-3-8B) entries for profiles of <= 32 rows.
     dims, sym = fp8.launch_geometry(_abi.ENTRY_W8A16_DENSE, 4096, 14336, 32)
     assert sym == "lf_fp8_w8a16_dense_k14336_m32" and dims.grid == (64 * 4, 1, 1)
@@ -153,22 +153,23 @@ def test_launch_geometry():
     assert sym == "lf_fp8_w8a16_qkv_m32"
     dims, sym = fp8.launch_geometry(_abi.ENTRY_W8A16_DENSE, 4096, 4096, 64)
     assert sym == "lf_fp8_w8a16_dense_m64"
-    # 65..128 rows: the LDS-tiled GEMM, 128 x BN tiles (BN 128 with at least
-    # 192 column blocks, else 64; gate/up blocks cover BN / 2 h-columns), K
-    # cut into S slices for about 256 blocks with at least 10 k-tiles each
+    # 65..128 rows: the LDS-tiled GEMM, 128 x BN tiles (gate/up blocks cover
+    # BN / 2 h-columns): BN 128 with the fewest K slices giving >= 192
+    # blocks if each slice keeps >= 8 k-tiles, else BN 64 the same way, else
+    # BN 64 with 8-k-tile slices
     dims, sym = fp8.launch_geometry(_abi.ENTRY_W8A16_DENSE, 4096, 4096, 128)
     assert sym == "lf_fp8_w8a16_dense_m128_n64" and dims.grid == (64 * 3, 1, 1)
     assert dims.block == (512, 1, 1)
     # S x blocks x 8 waves x (2 x BN / 32) 1 KiB fragments + a counter per block
     assert fp8.w8a16_workspace_bytes(_abi.ENTRY_W8A16_DENSE, 4096, 4096, 128) == 3 * 64 * 8 * 4 * 1024 + 256
     dims, sym = fp8.launch_geometry(_abi.ENTRY_W8A16_DENSE, 4096, 14336, 100)
-    assert sym == "lf_fp8_w8a16_dense_m128_n64" and dims.grid == (64 * 4, 1, 1)
+    assert sym == "lf_fp8_w8a16_dense_m128_n128" and dims.grid == (32 * 6, 1, 1)
     dims, sym = fp8.launch_geometry(_abi.ENTRY_W8A16_QKV, 6144, 4096, 128, qkv_split=(4096, 1024))
-    assert sym == "lf_fp8_w8a16_qkv_m128_n64" and dims.grid == (96 * 2, 1, 1)
+    assert sym == "lf_fp8_w8a16_qkv_m128_n128" and dims.grid == (48 * 4, 1, 1)
     dims, sym = fp8.launch_geometry(_abi.ENTRY_W8A16_GATE_UP, 14336, 4096, 128)
     assert sym == "lf_fp8_w8a16_gate_up_m128_n128" and dims.grid == (224, 1, 1)
     dims, sym = fp8.launch_geometry(_abi.ENTRY_W8A16_DENSE, 4096, 2048, 65)
-    assert sym == "lf_fp8_w8a16_dense_m128_n64" and dims.grid == (64, 1, 1)  # 16 k-tiles: no split
+    assert sym == "lf_fp8_w8a16_dense_m128_n64" and dims.grid == (64 * 2, 1, 1)  # 16 k-tiles
     # wide dense shapes (N >= 16384, e.g. the 128,256-column vocabulary head)
     for mt, w in ((16, 2), (32, 4), (128, 8)):
         dims, sym = fp8.launch_geometry(_abi.ENTRY_W8A16_DENSE, 128256, 4096, mt)

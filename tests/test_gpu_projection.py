@@ -437,11 +437,11 @@ def test_w8a16_specialized_entries(rt, op, m, max_tokens):
 
 
 @pytest.mark.parametrize("op,n,k,qkv_split,m,max_tokens", [
-    ("dense", 3072, 2048, None, 65, 80),        # BN 64, 48 blocks, 16 k-tiles: no split
+    ("dense", 3072, 2048, None, 65, 80),        # BN 64, 48 blocks x 2 slices of 8 k-tiles
     ("dense", 24576, 1024, None, 128, 128),     # BN 128 (192 blocks), no split
-    ("dense", 1024, 8192, None, 100, 128),      # BN 64, 16 blocks, S 6
-    ("qkv", 3072, 4096, (2048, 512), 77, 128),  # S 3; blocks straddle Q|K|V boundaries
-    ("gate_up", 8192, 2048, None, 128, 128),    # BN 64 (256 blocks)
+    ("dense", 1024, 8192, None, 100, 128),      # BN 64, 16 blocks, S 8
+    ("qkv", 3072, 4096, (2048, 512), 77, 128),  # BN 64, S 4; blocks straddle Q|K|V
+    ("gate_up", 8192, 2048, None, 128, 128),    # BN 128, S 2 (256 blocks)
     ("gate_up", 12288, 4096, None, 90, 96),     # BN 128 (192 blocks)
 ])
 def test_w8a16_gemm_form(rt, op, n, k, qkv_split, m, max_tokens):
