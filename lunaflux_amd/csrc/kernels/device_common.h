@@ -85,6 +85,15 @@ LF_DEVICE int live_rows(const int32_t *counts, int capacity) {
 
 LF_DEVICE uint64_t align256(uint64_t v) { return (v + 255u) & ~uint64_t(255); }
 
+// Bank swizzle of 256-byte activation rows (one bf16 k-tile of a row) in
+// LDS: row r keeps 16-byte chunk c at chunk c ^ chunk_swizzle(r & 15), so
+// the 16 lanes that read one logical chunk of 16 consecutive rows (an MFMA
+// fragment) hit distinct banks. Measured on gfx950 with ds_read_b128 (a
+// wave per pattern, 8 waves per CU): XOR with the 2-bit halves of r swapped
+// reads at the contiguous rate, 256 B/clk per CU; XOR with r itself at 2/3
+// of it.
+LF_DEVICE int chunk_swizzle(int r) { return ((r & 3) << 2) | ((r >> 2) & 3); }
+
 LF_DEVICE float bf16_to_f32(uint32_t bits16) { return __uint_as_float(bits16 << 16); }
 
 // fp32 -> bf16, round to nearest even (finite inputs; NaN stays NaN).

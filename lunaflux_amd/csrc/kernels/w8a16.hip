@@ -59,7 +59,7 @@ LF_DEVICE void load_tiles(const uint8_t *const (&strip)[NW], int kt, int lane, u
 
 // LDS activation ring of a block: two buffers of XC k-tiles of 16*MT rows of
 // bf16, k-tile-major (one k-tile = 16*MT rows x 256 bytes); row r keeps its
-// 16-byte chunk c at chunk position c ^ (r & 15), so the 16 rows of an MFMA
+// 16-byte chunk c at chunk position c ^ chunk_swizzle(r), so the 16 rows of an MFMA
 // fragment read fall in distinct banks.
 template <int MT, int XC>
 struct XRing {
@@ -297,7 +297,7 @@ __device__ void w8a16_kernel(const int32_t *counts, const uint16_t *x, const uin
     for (int id = wave; id < n; id += WAVES) {
       const int kl = id / xins, q = id - kl * xins;
       const int row = 4 * q + (lane >> 4);
-      const int chunk = (lane & 15) ^ (row & 15);
+      const int chunk = (lane & 15) ^ chunk_swizzle(row);
       const int src = row < M ? row : M - 1;
       w8a8v3::dma16(reinterpret_cast<const uint8_t *>(x + static_cast<uint64_t>(src) * K +
                                                       (kt0 + c * XC + kl) * 128 + chunk * 8),
@@ -357,7 +357,7 @@ __device__ void w8a16_kernel(const int32_t *counts, const uint16_t *x, const uin
         for (int mt = 0; mt < MT; ++mt) {
           const int row = mt * 16 + r;
           a[mt].u = *reinterpret_cast<const uint4 *>(
-              buf + row * 256 + ((((g << 2) | j) ^ (row & 15)) << 4));
+              buf + row * 256 + ((((g << 2) | j) ^ chunk_swizzle(row)) << 4));
         }
 #pragma unroll
         for (int i = 0; i < NW; ++i) {
@@ -557,7 +557,7 @@ __device__ __forceinline__ void w8a16_fixed_kernel(const int32_t *counts, const 
   constexpr int XI = 4 * MT;  // 1 KiB activation loads per k-tile (4 rows each)
   static_assert(MODE != 1 || (NQ % 16 == 0 && NKV % 16 == 0 && NQ > 0 && NKV > 0), "qkv widths");
   // Per wave: SLOTS k-tile slots of 16 MT activation rows (256 bytes each;
-  // row r keeps 16-byte chunk c at position c ^ (r & 15), so both the
+  // row r keeps 16-byte chunk c at position c ^ chunk_swizzle(r), so both the
   // row-wise writes and the 16-row fragment reads hit distinct banks). With
   // one slot, step k + 1's writes queue behind step k's fragment reads (a
   // wave's LDS instructions execute in order). The partial tiles of the K
@@ -631,7 +631,7 @@ __device__ __forceinline__ void w8a16_fixed_kernel(const int32_t *counts, const 
     const int row = 4 * q + (lane >> 4);
     const int src = row < M ? row : (M > 0 ? M - 1 : 0);
     xsrc[q] = x + static_cast<uint64_t>(src) * K + kt0 * 128 + (lane & 15) * 8;
-    xdst[q] = row * 16 + ((lane & 15) ^ (row & 15));
+    xdst[q] = row * 16 + ((lane & 15) ^ chunk_swizzle(row));
   }
   auto load_a = [&](int k, u32x4 (&dst)[XI]) {
 #pragma unroll
@@ -660,7 +660,7 @@ __device__ __forceinline__ void w8a16_fixed_kernel(const int32_t *counts, const 
       bf16x8 af[MT];
 #pragma unroll
       for (int mt = 0; mt < MT; ++mt) {
-        af[mt] = __builtin_bit_cast(bf16x8, slot[(16 * mt + r) * 16 + (((g << 2) | j) ^ r)]);
+        af[mt] = __builtin_bit_cast(bf16x8, slot[(16 * mt + r) * 16 + (((g << 2) | j) ^ chunk_swizzle(r))]);
       }
 #pragma unroll
       for (int i = 0; i < NW; ++i) {
@@ -711,7 +711,7 @@ __device__ __forceinline__ void w8a16_fixed_kernel(const int32_t *counts, const 
 // counts are exact (see w8a16_fixed_kernel). The activation k-tile (16 MT
 // rows) is loaded cooperatively with row-coalesced 1 KiB loads into
 // registers (ceil(XI / WAVES) loads per wave, DX k-tiles ahead), written to one of
-// two LDS slots (chunk c of row r at c ^ (r & 15)), and shared by the block's
+// two LDS slots (chunk c of row r at c ^ chunk_swizzle(r)), and shared by the block's
 // waves after one barrier per k-tile. The barrier waits only for LDS
 // writes (no memory fence), so the weight ring stays in flight across it.
 // ---------------------------------------------------------------------------
@@ -805,7 +805,7 @@ __device__ __forceinline__ void w8a16_fixed_group_kernel(const int32_t *counts, 
     const int row = 4 * q + (lane >> 4);
     const int src = row < M ? row : (M > 0 ? M - 1 : 0);
     xsrc[j] = x + static_cast<uint64_t>(src) * K + kt0 * 128 + (lane & 15) * 8;
-    xdst[j] = row * 16 + ((lane & 15) ^ (row & 15));
+    xdst[j] = row * 16 + ((lane & 15) ^ chunk_swizzle(row));
   }
   auto load_a = [&](int k, u32x4 (&dst)[XPW]) {
 #pragma unroll
@@ -839,7 +839,7 @@ __device__ __forceinline__ void w8a16_fixed_group_kernel(const int32_t *counts, 
       bf16x8 af[MT];
 #pragma unroll
       for (int mt = 0; mt < MT; ++mt) {
-        af[mt] = __builtin_bit_cast(bf16x8, slot[(16 * mt + r) * 16 + (((g << 2) | j) ^ r)]);
+        af[mt] = __builtin_bit_cast(bf16x8, slot[(16 * mt + r) * 16 + (((g << 2) | j) ^ chunk_swizzle(r))]);
       }
 #pragma unroll
       for (int i = 0; i < NW; ++i) {

@@ -21,10 +21,10 @@
 // the weights to bf16 in registers (exact) and issues 16x16x32 bf16 MFMAs.
 //
 // Activation LDS layout: row r (256 bytes = 16 chunks of 16 bytes) keeps
-// logical chunk c at chunk c ^ (r & 15), so the 16 lanes of a fragment read
-// (16 rows, one logical chunk) hit distinct banks. A load instruction (1 KiB)
-// covers 4 rows; lane l writes row 4q + l / 16, physical chunk l % 16, so it
-// fetches logical chunk (l % 16) ^ (row & 15). Rows past the live M fetch
+// logical chunk c at chunk c ^ chunk_swizzle(r), so the 16 lanes of a
+// fragment read (16 rows, one logical chunk) hit distinct banks. A load
+// instruction (1 KiB) covers 4 rows; lane l writes row 4q + l / 16, physical
+// chunk l % 16, so it fetches logical chunk (l % 16) ^ chunk_swizzle(row). Rows past the live M fetch
 // the last live row (their results are never stored).
 //
 // K order inside a k-step: lane (g, r) of a packed weight tile holds column
@@ -160,7 +160,7 @@ __device__ void w8a16_gemm_kernel(const int32_t *counts, const uint16_t *x, cons
     for (int q = 0; q < T::kAIns; ++q) {
       const int row = 4 * (lw * T::kAIns + q) + (lane >> 4);
       const int src = row < M ? row : M - 1;
-      const int chunk = (lane & 15) ^ (row & 15);
+      const int chunk = (lane & 15) ^ chunk_swizzle(row);
       a_src[q] = reinterpret_cast<const uint8_t *>(x + static_cast<uint64_t>(src) * K) + chunk * 16;
     }
   } else {
@@ -236,7 +236,7 @@ __device__ void w8a16_gemm_kernel(const int32_t *counts, const uint16_t *x, cons
       for (int i = 0; i < T::kFM; ++i) {
         const int row = wm * T::kWaveM + i * 16 + r;
         af[step][i] =
-            *reinterpret_cast<const bf16x8 *>(a + row * 256 + ((((g << 2) | step) ^ r) << 4));
+            *reinterpret_cast<const bf16x8 *>(a + row * 256 + ((((g << 2) | step) ^ chunk_swizzle(r)) << 4));
       }
 #pragma unroll
     for (int step = 0; step < 4; ++step) {
