@@ -9,14 +9,14 @@
 // issued while k-step kt computes, so L2/HBM latency is covered without
 // occupancy. Stage layout:
 //   A: BM rows x 128 bytes; LDS row r holds the row's 16-byte chunk c at
-//      physical chunk c ^ ((r >> 1) & 7). A ds_read_b128 is served 16 lanes
-//      (256 bytes, all banks) at a time and a fragment read gives those 16
-//      lanes 16 consecutive rows at one logical chunk: rows 2k and 2k+1 fill
-//      the two 128-byte halves of a bank window and (r >> 1) & 7 spreads the
-//      8 row pairs over the 8 chunk positions, so no two lanes of a pass
-//      share a bank. The swizzle is applied on the global side: lane l of a
-//      load instruction writes LDS row r = 8 (instr) + l / 8, physical
-//      chunk l % 8, so it fetches logical chunk (l % 8) ^ ((r >> 1) & 7).
+//      physical chunk c ^ (((r & 3) << 1) | ((r >> 2) & 1)). A fragment read
+//      gives 16 lanes 16 consecutive rows at one logical chunk; measured on
+//      gfx950 (ds_read_b128, 8 waves per CU) this swizzle reads at the
+//      contiguous rate, 256 B/clk per CU, where c ^ ((r >> 1) & 7) (row
+//      pairs spread over the chunk positions) ran at 2/3 of it. The swizzle
+//      is applied on the global side: lane l of a load instruction writes LDS
+//      row r = 8 (instr) + l / 8, physical chunk l % 8, so it fetches logical
+//      chunk (l % 8) ^ (((r & 3) << 1) | ((r >> 2) & 1)).
 //   B: BN/16 pre-swizzled 16 x 128 weight tiles copied verbatim, 2 KiB each.
 //
 // The caller provides, per lane, the global row base of each A row it loads
@@ -54,7 +54,7 @@ LF_DEVICE int a_load_row(int wave, int q, int lane) {
 }
 // Physical chunk of logical 16-byte chunk `chunk` of tile row `row`, and the
 // byte offset of that chunk in a stage.
-LF_DEVICE int a_phys_chunk(int row, int chunk) { return chunk ^ ((row >> 1) & 7); }
+LF_DEVICE int a_phys_chunk(int row, int chunk) { return chunk ^ (((row & 3) << 1) | ((row >> 2) & 1)); }
 LF_DEVICE int a_chunk_offset(int row, int chunk) { return row * 128 + (a_phys_chunk(row, chunk) << 4); }
 // Logical 16-byte chunk of that row this lane fetches.
 LF_DEVICE int a_load_chunk(int row, int lane) { return a_phys_chunk(row, lane & 7); }
