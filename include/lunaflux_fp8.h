@@ -106,7 +106,11 @@ int32_t lunaflux_fp8_unpack_weight(const uint8_t *region, int64_t region_bytes,
  *    16-column tile, a block several adjacent tiles over one K-slice sharing
  *    the activation slice through LDS; with more than one slice the partials
  *    are reduced in a fixed slice order by the last block of each column
- *    group through the workspace). Suffix _m16/_m32/_m64/_m128: the
+ *    group through the workspace). Profiles of 65..128 rows use a third,
+ *    LDS-tiled GEMM form (_m128_n64 / _m128_n128: blocks of 8 waves own
+ *    128 rows x BN weight columns over a K-slice; activation and weight
+ *    tiles stream global -> LDS in two rings loaded by different waves),
+ *    except vocabulary-wide dense shapes. Suffix _m16/_m32/_m64/_m128: the
  *    profile's largest M; _k<K>...: a shape-specialized entry.
  *  W8A8 ("prefill"): activations quantized per token to e4m3
  *    (lf_fp8_act_quant_rows), e4m3 x e4m3 MFMA, fp32 accumulation, row scale
