@@ -96,12 +96,18 @@ LF_DEVICE int chunk_swizzle(int r) { return ((r & 3) << 2) | ((r >> 2) & 3); }
 
 LF_DEVICE float bf16_to_f32(uint32_t bits16) { return __uint_as_float(bits16 << 16); }
 
-// fp32 -> bf16, round to nearest even (finite inputs; NaN stays NaN).
+// fp32 -> bf16 bits, round to nearest even; a NaN keeps its sign and top
+// payload bits and becomes quiet: for u = the fp32 bits,
+//   NaN:       (u >> 16) | 0x40
+//   otherwise: (u + 0x7fff + ((u >> 16) & 1)) >> 16   (fp32 denormals kept)
+// One v_cvt_pk_bf16_f32 (the conversion of a float to __bf16 on gfx950).
+// It was compared with the formula above on every one of the 2^32 fp32
+// inputs on MI355X under these kernels' floating-point mode, with no
+// difference. The formula, compiled, is a divergent branch plus five
+// integer operations per value: at 128 values per lane it cost the 256-row
+// GEMM epilogues ~5 us per tile.
 LF_DEVICE uint32_t f32_to_bf16(float v) {
-  uint32_t u = __float_as_uint(v);
-  if ((u & 0x7fffffffu) > 0x7f800000u) return (u >> 16) | 0x40u;
-  u += 0x7fffu + ((u >> 16) & 1u);
-  return u >> 16;
+  return static_cast<uint32_t>(__builtin_bit_cast(uint16_t, static_cast<__bf16>(v)));
 }
 
 // Four e4m3 codes (one 32-bit word) -> four bf16 values (two words). The

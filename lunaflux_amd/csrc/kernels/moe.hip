@@ -414,7 +414,7 @@ struct BlockScaleFold {
 // of the same columns). STAGE 1: down (h rows in expert order, bf16 y): a
 // block computes 128 columns.
 template <int STAGE, bool BLOCK>
-__device__ void grouped_gemm(const int32_t *counts, const MoeDesc &d, const uint8_t *w0,
+__device__ __forceinline__ void grouped_gemm(const int32_t *counts, const MoeDesc &d, const uint8_t *w0,
                              const uint8_t *w1, uint8_t *ws) {
   using T = GemmTile;
   __shared__ __attribute__((aligned(1024))) uint8_t smem[T::kSmem];
@@ -633,7 +633,7 @@ LF_DEVICE float carry_ratio(float s, float &prev) {
 // the hidden quantizer's e4m3 codes and per-128-column scales instead of
 // bf16 h (see the STAGE 0 epilogue below).
 template <int STAGE, bool BLOCK = false, bool QUANT = false>
-__device__ void grouped_gemm_t256(const int32_t *counts, const MoeDesc &d, const uint8_t *w0,
+__device__ __forceinline__ void grouped_gemm_t256(const int32_t *counts, const MoeDesc &d, const uint8_t *w0,
                                   const uint8_t *w1, uint8_t *ws) {
   static_assert(!QUANT || (STAGE == 0 && BLOCK), "the fused quantizer is the block-scaled gate/up's");
   using T = GemmTile256;
@@ -740,13 +740,17 @@ __device__ void grouped_gemm_t256(const int32_t *counts, const MoeDesc &d, const
   const int live_rows_wave = pend - (p0 + wm * T::kWaveM);
   const int live_fm = live_rows_wave <= 0 ? 0 : live_rows_wave >= T::kWaveM ? T::kFM
                                                                            : (live_rows_wave + 31) / 32;
+  // A wave whose 32 A rows are all past the tile's last row issues no A
+  // loads (a tile of a small expert then moves its weights and little
+  // else through the load path).
+  const bool a_loads = p0 + 16 * T::kAIns * wave < pend;
   if constexpr (BLOCK) {
     typedef const __attribute__((address_space(3))) float *lds_ptr;
     BlockRescale256<STAGE> rs{(lds_ptr)(ra_lds), (lds_ptr)(rw_lds + 2 * wn * kT256MaxKT),
                               wm * T::kWaveM + 4 * (lane >> 5), {}, 0};
-    w8a8v4::mainloop<T, true, BlockRescale256<STAGE>>(plan, KT, smem, acc, live_fm, rs);
+    w8a8v4::mainloop<T, true, BlockRescale256<STAGE>>(plan, KT, smem, acc, live_fm, rs, a_loads);
   } else {
-    w8a8v4::mainloop<T, true>(plan, KT, smem, acc, live_fm);
+    w8a8v4::mainloop<T, true>(plan, KT, smem, acc, live_fm, w8a8v4::NoRescale{}, a_loads);
   }
 
   const int c = lane & 31;

@@ -307,7 +307,7 @@ LF_DEVICE void rms_norm_quant_rows(const int32_t *counts, const uint16_t *x,
 // results are never stored.
 // ---------------------------------------------------------------------------
 template <class T, int GROUP, int MODE>
-__device__ void w8a8_tiled_kernel(const int32_t *counts, const uint8_t *xq, const uint8_t *w0,
+__device__ __forceinline__ void w8a8_tiled_kernel(const int32_t *counts, const uint8_t *xq, const uint8_t *w0,
                                   const uint8_t *w1, const uint8_t *w2, uint16_t *y) {
   constexpr int BM = T::kWaveM * T::kWgm, BN = T::kWaveN * T::kWgn;
   __shared__ __attribute__((aligned(1024))) uint8_t smem[T::kSmem];
@@ -428,7 +428,7 @@ __device__ void w8a8_tiled_kernel(const int32_t *counts, const uint8_t *xq, cons
 // columns, so 32-column fragment j (gate) pairs with j + kFN / 2 (up).
 // ---------------------------------------------------------------------------
 template <class T, int GROUP, int MODE>
-__device__ void w8a8_v4_kernel(const int32_t *counts, const uint8_t *xq, const uint8_t *w0,
+__device__ __forceinline__ void w8a8_v4_kernel(const int32_t *counts, const uint8_t *xq, const uint8_t *w0,
                                const uint8_t *w1, const uint8_t *w2, uint16_t *y) {
   constexpr int BM = T::kBM, BN = T::kBN;
   __shared__ __attribute__((aligned(1024))) uint8_t smem[T::kSmem];

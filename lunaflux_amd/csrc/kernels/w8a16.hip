@@ -383,7 +383,7 @@ __device__ void w8a16_kernel(const int32_t *counts, const uint16_t *x, const uin
 // are summed in LDS in wave order (deterministic).
 // ---------------------------------------------------------------------------
 template <int KS, int MT, int MODE, int D, int DA>
-__device__ void w8a16_tile_kernel(const int32_t *counts, const uint16_t *x, const uint8_t *w0,
+__device__ __forceinline__ void w8a16_tile_kernel(const int32_t *counts, const uint16_t *x, const uint8_t *w0,
                                   const uint8_t *w1, const uint8_t *w2, uint16_t *y) {
   constexpr int NW = MODE == 2 ? 2 : 1;
   __shared__ __attribute__((aligned(16))) f32x4 red[KS][MT * NW][64];

@@ -83,7 +83,7 @@ LF_DEVICE void wait_ring(int later) {
 // (each wave column's fragments: kFN / 2 gate tiles, then the up tiles of the
 // same h-columns, so SwiGLU pairs fragment j with j + kFN / 2 in a lane).
 template <int BN, int WGM, int WGN, int NSA, int NSB, int MODE>
-__device__ void w8a16_gemm_kernel(const int32_t *counts, const uint16_t *x, const uint8_t *w0,
+__device__ __forceinline__ void w8a16_gemm_kernel(const int32_t *counts, const uint16_t *x, const uint8_t *w0,
                                   const uint8_t *w1, const uint8_t *w2, uint16_t *y,
                                   uint8_t *ws) {
   using T = Tile<BN, WGM, WGN, NSA, NSB>;

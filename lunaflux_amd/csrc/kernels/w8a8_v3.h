@@ -121,7 +121,7 @@ struct NoFold {
 // wave. Only the grouped GEMMs, whose expert tiles are often partly past the
 // expert's last row, use it.
 template <class T, class Fold = NoFold, bool SKIP = false>
-__device__ void mainloop(const Plan<T> &plan, int KT, uint8_t *smem,
+__device__ __forceinline__ void mainloop(const Plan<T> &plan, int KT, uint8_t *smem,
                          f32x4 (&acc)[T::kFM][T::kFN], const Fold &fold = Fold{},
                          int live_fm = T::kFM) {
   const int live = __builtin_amdgcn_readfirstlane(live_fm);

@@ -96,6 +96,15 @@ LF_DEVICE void block_barrier() { asm volatile("s_barrier" ::: "memory"); }
 // rescale.begin(kt) loads that k-tile's multipliers and rescale.apply(o, acc)
 // multiplies the accumulators of column fragment o right before their first
 // MFMA of the k-tile (NoRescale: per-channel scales, nothing to do).
+// a_loads (wave-uniform): whether this wave issues its A loads. A wave loads
+// A rows 16 kAIns wave .. + 16 kAIns - 1; when all of them are past the last
+// live row the caller passes false and the wave issues only its B loads.
+// Every fragment an MFMA reads then still comes from a loading wave,
+// provided the caller's live_fm skips each fragment whose rows are all dead
+// and the fragments line up with the loaders' row ranges (kAIns = 2: 32 rows
+// per loader and per fragment). The rows such a wave would have written keep
+// whatever the LDS held; no MFMA reads them. Each wave counts its own loads
+// (vmcnt), so the waits use kBIns loads per stage for such a wave.
 struct NoRescale {
   LF_DEVICE void begin(int) {}
   template <class A>
@@ -105,21 +114,34 @@ struct NoRescale {
 template <class T, bool SKIP = false, class Rescale = NoRescale>
 __device__ __forceinline__ void mainloop(const Plan<T> &plan, int KT, uint8_t *smem,
                          f32x16 (&acc)[T::kFM][T::kFN], int live_fm = T::kFM,
-                         Rescale rescale = Rescale{}) {
+                         Rescale rescale = Rescale{}, bool a_loads = true) {
+  static_assert(!SKIP || T::kAIns * 16 == 32, "a loader's rows are one 32-row fragment");
   constexpr int NS = T::kStages;
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int wm = wave / T::kWgn, wn = wave % T::kWgn;
   const int q = lane >> 5, c = lane & 31;
   const int S = 2 * KT;
+  const bool a_on = !SKIP || __builtin_amdgcn_readfirstlane(static_cast<int>(a_loads)) != 0;
 
+  // Wait until at most N stages of this wave's loads are outstanding.
+  auto wait_stages = [&](auto n_tag) {
+    constexpr int N = decltype(n_tag)::value;
+    if (a_on) {
+      w8a8v3::wait_vmcnt<N * T::kIns>();
+    } else {
+      w8a8v3::wait_vmcnt<N * T::kBIns>();
+    }
+  };
   const uint32_t smem_base = __builtin_amdgcn_readfirstlane(w8a8v3::lds_offset_of(smem));
   auto issue = [&](int s) {
     const int kt = s >> 1, h = s & 1;
     const uint32_t a = smem_base + (s % NS) * T::kStage;
     const uint32_t b = a + T::kABytes;
+    if (a_on) {
 #pragma unroll
-    for (int i = 0; i < T::kAIns; ++i) {
-      w8a8v3::dma16(plan.a[i] + kt * 128 + h * 16, a + (wave * T::kAIns + i) * 1024);
+      for (int i = 0; i < T::kAIns; ++i) {
+        w8a8v3::dma16(plan.a[i] + kt * 128 + h * 16, a + (wave * T::kAIns + i) * 1024);
+      }
     }
 #pragma unroll
     for (int i = 0; i < T::kBIns; ++i) {
@@ -197,7 +219,7 @@ __device__ __forceinline__ void mainloop(const Plan<T> &plan, int KT, uint8_t *s
     mfma_group(cur, 0);
     __builtin_amdgcn_sched_barrier(0);
     if constexpr (kWait >= 0) {
-      w8a8v3::wait_vmcnt<kWait * T::kIns>();
+      wait_stages(std::integral_constant<int, kWait>{});
       block_barrier();
       if constexpr (kIssue) issue(s + NS - 1);
       read_inner(nxt, st);
@@ -232,9 +254,9 @@ __device__ __forceinline__ void mainloop(const Plan<T> &plan, int KT, uint8_t *s
   issue(1);  // S >= 2 always (K is a multiple of 128)
   if (S > 2) {
     issue(2);
-    w8a8v3::wait_vmcnt<2 * T::kIns>();
+    wait_stages(std::integral_constant<int, 2>{});
   } else {
-    w8a8v3::wait_vmcnt<1 * T::kIns>();
+    wait_stages(std::integral_constant<int, 1>{});
   }
   block_barrier();
   read_inner(f0, stage_ptr(0));
