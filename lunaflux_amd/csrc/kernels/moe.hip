@@ -353,14 +353,40 @@ LF_DEVICE void quant_rows(const uint16_t *src, int K, int group, uint8_t *dst, f
 }
 
 // --- grouped GEMM -------------------------------------------------------------
-// The expert of a 128-row tile (tiles[] prefix) is found by binary search.
-LF_DEVICE int expert_of_tile(const int32_t *tiles, int E, int j) {
-  int lo = 0, hi = E;
-  while (hi - lo > 1) {
-    const int mid = (lo + hi) >> 1;
-    if (tiles[mid] <= j) lo = mid; else hi = mid;
+// The expert owning row tile j of a tile prefix (tiles[0] = 0, nondecreasing,
+// j < tiles[E]), with its first tile and its routed-row range, found by the
+// whole block in one round of loads: thread t < E tests tiles[t] <= j <
+// tiles[t + 1], which exactly one expert satisfies (an expert without tiles
+// has tiles[t] == tiles[t + 1]), and publishes t, tiles[t], offsets[t] and
+// offsets[t + 1] in LDS. A binary search instead costs log2(E) dependent
+// global loads per block. Every thread of the block calls it (barriers
+// inside); E <= blockDim.x. The slots start as expert 0 with no rows, so an
+// inconsistent prefix yields an in-range expert and an empty row range.
+struct TileExpert {
+  int e, first_tile, row_begin, row_end;
+};
+LF_DEVICE TileExpert find_tile_expert(const int32_t *tiles, const int32_t *offsets, int E, int j) {
+  __shared__ int found[4];
+  const int t = threadIdx.x;
+  if (t == 0) {
+    found[0] = 0;
+    found[1] = j;
+    found[2] = 0;
+    found[3] = 0;
   }
-  return lo;
+  __syncthreads();
+  if (t < E) {
+    const int lo = tiles[t], hi = tiles[t + 1];
+    const int o0 = offsets[t], o1 = offsets[t + 1];
+    if (lo <= j && j < hi) {
+      found[0] = t;
+      found[1] = lo;
+      found[2] = o0;
+      found[3] = o1;
+    }
+  }
+  __syncthreads();
+  return {found[0], found[1], found[2], found[3]};
 }
 
 // The grouped GEMMs run the direct-to-LDS main loop (w8a8_v3.h) on 128 x 128
@@ -434,10 +460,10 @@ __device__ __forceinline__ void grouped_gemm(const int32_t *counts, const MoeDes
   const int gx = STAGE == 0 ? N / 64 : N / 128;
   int bx, by;
   if (!w8a8v3::tile_of_block(gx, tiles[E], tiles[E], bx, by)) return;
-  const int e = expert_of_tile(tiles, E, by);
-  const int32_t *offsets = at<int32_t>(ws, L.offsets);
-  const int p0 = offsets[e] + (by - tiles[e]) * 128;
-  const int pend = offsets[e + 1];
+  const TileExpert te = find_tile_expert(tiles, at<int32_t>(ws, L.offsets), E, by);
+  const int e = te.e;
+  const int p0 = te.row_begin + (by - te.first_tile) * 128;
+  const int pend = te.row_end;
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int wm = wave / T::kWgn, wn = wave % T::kWgn;
@@ -655,10 +681,10 @@ __device__ __forceinline__ void grouped_gemm_t256(const int32_t *counts, const M
   const int gx = STAGE == 0 ? N / (T::kBN / 2) : N / T::kBN;
   int bx, by;
   if (!w8a8v3::tile_of_block(gx, tiles[E], tiles[E], bx, by)) return;
-  const int e = expert_of_tile(tiles, E, by);
-  const int32_t *offsets = at<int32_t>(ws, L.offsets);
-  const int p0 = offsets[e] + (by - tiles[e]) * BM;
-  const int pend = offsets[e + 1];
+  const TileExpert te = find_tile_expert(tiles, at<int32_t>(ws, L.offsets), E, by);
+  const int e = te.e;
+  const int p0 = te.row_begin + (by - te.first_tile) * BM;
+  const int pend = te.row_end;
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int wm = wave / T::kWgn, wn = wave % T::kWgn;
@@ -696,13 +722,22 @@ __device__ __forceinline__ void grouped_gemm_t256(const int32_t *counts, const M
     if (KT > kT256MaxKT) return;  // the launch geometry never selects this form then
     const float *ascales = at<float>(ws, STAGE == 0 ? L.xs : L.hs);
     const int tid = threadIdx.x;
+    // Each thread issues all of its scale loads before the first use (one
+    // memory latency instead of one per k-tile).
+    float sv[kT256MaxKT];
     if (tid < BM) {
       const int pp = p0 + tid;
+      const bool live = pp < pend;
+      const float *sr = ascales + static_cast<uint64_t>(src_row(live ? pp : p0)) * KT;
+#pragma unroll
+      for (int kt = 0; kt < kT256MaxKT; ++kt) sv[kt] = kt < KT ? sr[kt] : 0.0f;
       float prev = 1.0f;
-      const float *sr = ascales + static_cast<uint64_t>(src_row(pp < pend ? pp : p0)) * KT;
-      for (int kt = 0; kt < KT; ++kt) {
-        const float r = pp < pend ? carry_ratio(sr[kt], prev) : 1.0f;
-        ra_lds[kt * BM + tid] = kt == 0 ? 1.0f : r;
+#pragma unroll
+      for (int kt = 0; kt < kT256MaxKT; ++kt) {
+        if (kt < KT) {
+          const float r = live ? carry_ratio(sv[kt], prev) : 1.0f;
+          ra_lds[kt * BM + tid] = kt == 0 ? 1.0f : r;
+        }
       }
       sa_mine = prev;
     } else if (tid < BM + 2 * T::kWgn) {
@@ -711,10 +746,15 @@ __device__ __forceinline__ void grouped_gemm_t256(const int32_t *counts, const M
       const int nb = STAGE == 0 ? (bx * (T::kBN / 2) + cw * (T::kWaveN / 2)) >> 7
                                 : (bx * T::kBN + cw * T::kWaveN) >> 7;
       const float *sw = expert_scales(region, e) + static_cast<uint64_t>(nb) * KT;
+#pragma unroll
+      for (int kt = 0; kt < kT256MaxKT; ++kt) sv[kt] = kt < KT ? sw[kt] : 0.0f;
       float prev = 1.0f;
-      for (int kt = 0; kt < KT; ++kt) {
-        const float r = carry_ratio(sw[kt], prev);
-        rw_lds[(2 * cw + part) * kT256MaxKT + kt] = kt == 0 ? 1.0f : r;
+#pragma unroll
+      for (int kt = 0; kt < kT256MaxKT; ++kt) {
+        if (kt < KT) {
+          const float r = carry_ratio(sv[kt], prev);
+          rw_lds[(2 * cw + part) * kT256MaxKT + kt] = kt == 0 ? 1.0f : r;
+        }
       }
       sw_last[2 * cw + part] = prev;
     }
