@@ -245,3 +245,28 @@ def test_moe_t256(rt, t, e, k, hidden, inter, skew, block):
                                            logits=logits, zero_groups=zero)
     ex, w = check_routing(logits, k, mode, st)
     check_output(x, weights, ex, w, out, block, f"moe t256 t={t} e={e} skew={skew} block={block}", st)
+
+
+@pytest.mark.parametrize("block", [False, True])
+def test_moe_t256_row_boundaries(rt, block):
+    """256-row tiles whose live rows end exactly at or just past the 32-row
+    boundaries of the loading waves (a wave loads the A rows of one 32-row
+    fragment and skips its loads when all of them are past the tile's last
+    row): experts routed 288 (a 32-row last tile), 33, 64, 65, 31, 1, 352
+    and 1214 rows, top-1 over one-hot logits, both scale modes."""
+    from lunaflux_amd import _abi, moe
+    rows = [288, 33, 64, 65, 31, 1, 352, 1214]
+    e, k, hidden, inter = len(rows), 1, 256, 256
+    t = sum(rows)
+    mode = 1 if block else 0
+    desc = moe.moe_descriptor(e, k, mode, hidden, inter, 128 if block else 0)
+    assert moe.launch_geometry(_abi.MOE_DOWN, desc, t)[1].startswith("lf_moe_down_t256")
+    rng = np.random.default_rng(960 + block)
+    assign = rng.permutation(np.repeat(np.arange(e), rows))
+    logits = (0.1 * rng.standard_normal((t, e))).astype(np.float32)
+    logits[np.arange(t), assign] = 5.0
+    x, logits, weights, out, st = run_case(rt, rng, t, e, k, hidden, inter, mode, block=block,
+                                           logits=logits)
+    ex, w = check_routing(logits, k, mode, st)
+    assert np.diff(st["offsets"]).tolist() == rows
+    check_output(x, weights, ex, w, out, block, f"moe t256 row boundaries block={block}", st)
