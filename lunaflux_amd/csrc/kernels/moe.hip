@@ -971,14 +971,50 @@ LF_DEVICE void grouped_gemv(const int32_t *counts, const MoeDesc &d, const uint8
   // 32-bit per-lane offsets of the loads.
   const uint64_t a_rows = STAGE == 0 ? static_cast<uint64_t>(Tn) : static_cast<uint64_t>(Tn) * d.top_k;
   if ((N & 63) != 0 || a_rows * static_cast<uint64_t>(K) >= (uint64_t(1) << 32)) return;
+  if (blockDim.x != 64 * kGemvWaves) return;  // the item layout's block (the geometry's)
   const int E = d.experts;
   const int groups = (N >> 4) / kGemvWaves;
   const int32_t *live = at<int32_t>(ws, L.tiles) + 2 * E + 2;  // [0]: count, then ids
-  const int items = live[0] * groups;
+  const int nlive = live[0];
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int g = lane >> 4, r = lane & 15;
   const int32_t *offsets = at<int32_t>(ws, L.offsets);
+  // Row chunks are items of their own: expert j of the live list has
+  // ceil(rows_j / 16) chunks; items (j, chunk 0, group) come first, j-major,
+  // then the further chunks, numbered by extra[j] = sum over i < j of
+  // (chunks_i - 1): item nlive * groups + x * groups + group is chunk
+  // 1 + x - extra[j] of the expert j with extra[j] <= x < extra[j + 1]. A
+  // further chunk then streams its tiles in another block beside the first
+  // chunk, not after it in the same block (with 17-32 rows that sequence set
+  // the kernel's length). One thread per live expert (E <= 256 = blockDim.x)
+  // and a wave scan build the prefix in LDS.
+  __shared__ int extra[257];
+  __shared__ int wave_extra[kGemvWaves];
+  {
+    const int t = static_cast<int>(threadIdx.x);
+    int mine = 0;
+    if (t < nlive) {
+      const int ex = live[1 + t];
+      mine = (offsets[ex + 1] - offsets[ex] + kGemvRows - 1) / kGemvRows - 1;
+      mine = mine < 0 ? 0 : mine;
+    }
+    int incl = mine;
+#pragma unroll
+    for (int off = 1; off < 64; off <<= 1) {
+      const int v = __shfl_up(incl, off);
+      if (lane >= off) incl += v;
+    }
+    if (lane == 63) wave_extra[wave] = incl;
+    __syncthreads();
+    int before = 0;
+    for (int w = 0; w < wave; ++w) before += wave_extra[w];
+    extra[t + 1] = before + incl;
+    if (t == 0) extra[0] = 0;
+    __syncthreads();
+  }
+  const int first_items = nlive * groups;
+  const int items = (nlive + extra[nlive]) * groups;
   const int32_t *sorted = at<int32_t>(ws, L.sorted);
   auto src_row = [&](int p) { return STAGE == 0 ? sorted[p] / d.top_k : p; };
   const uint8_t *abase = uniform_ptr(at<uint8_t>(ws, STAGE == 0 ? L.xq : L.hq));
@@ -986,7 +1022,18 @@ LF_DEVICE void grouped_gemv(const int32_t *counts, const MoeDesc &d, const uint8
   float *sa_wave = sa_lds + (BLOCK ? wave * kGemvRows * 32 : 0);
 
   for (int item = blockIdx.x; item < items; item += gridDim.x) {
-    const int e = live[1 + item / groups];
+    int j = item / groups, chunk = 0;
+    if (item >= first_items) {
+      const int x = (item - first_items) / groups;
+      int lo = 0, hi = nlive;  // extra[lo] <= x < extra[hi]
+      while (hi - lo > 1) {
+        const int mid = (lo + hi) >> 1;
+        if (extra[mid] <= x) lo = mid; else hi = mid;
+      }
+      j = lo;
+      chunk = 1 + x - extra[lo];
+    }
+    const int e = live[1 + j];
     const int nt = (item % groups) * kGemvWaves + wave;
     const int col = nt * 16 + (lane & 15);
     const uint8_t *region[NW];
@@ -1012,8 +1059,9 @@ LF_DEVICE void grouped_gemv(const int32_t *counts, const MoeDesc &d, const uint8
         bw[slot][i][1] = gload16(strip[i], o + 1024);
       }
     };
-    const int p_first = offsets[e], pend = offsets[e + 1];
-    for (int c0 = p_first; c0 < pend; c0 += kGemvRows) {
+    const int pend = offsets[e + 1];
+    const int c0 = offsets[e] + kGemvRows * chunk;
+    if (c0 < pend) {
       const int rows = pend - c0 < kGemvRows ? pend - c0 : kGemvRows;
       // the weight ring's first D k-tiles, then the activation chain
       static_for<D>([&](auto j) { load_b(j, j < KT ? static_cast<int>(j) : KT - 1); });
