@@ -100,16 +100,11 @@ LF_DEVICE void wave_lds_sync() {
 // every index in range and lets the value carry the fault.
 LF_DEVICE float rank_key(float v) { return __builtin_isnan(v) ? -__builtin_inff() : v; }
 
-LF_DEVICE void route(const int32_t *counts, const MoeDesc &d, const float *logits, uint8_t *ws) {
-  __shared__ __attribute__((aligned(16))) float sv[4][256];
-  __shared__ int32_t sid[4][16];
-  __shared__ float spv[4][16];
-  const int T = live_rows(counts, 1 << 30);
-  const int w = threadIdx.x >> 6;
-  const int t = blockIdx.x * 4 + w;
-  if (t >= T) return;
+// Routes token t with the calling wave; sv (E floats, 16-byte aligned), sid
+// and spv (16 each) are this wave's LDS scratch.
+LF_DEVICE void route_token(const MoeDesc &d, const MoeLayout &L, const float *logits, uint8_t *ws,
+                           int t, float *sv, int32_t *sid, float *spv) {
   const int lane = threadIdx.x & 63;
-  const MoeLayout L(d, T);
   const int E = d.experts, k = d.top_k;
   const float *l = logits + static_cast<uint64_t>(t) * E;
   int32_t *ids = at<int32_t>(ws, L.topk_ids) + static_cast<uint64_t>(t) * k;
@@ -119,7 +114,7 @@ LF_DEVICE void route(const int32_t *counts, const MoeDesc &d, const float *logit
   for (int i = 0; i < 4; ++i) {
     const int e = lane + 64 * i;
     v[i] = e < E ? rank_key(l[e]) : 0.0f;
-    if (e < E) sv[w][e] = v[i];
+    if (e < E) sv[e] = v[i];
   }
   wave_lds_sync();
   const int E4 = E & ~3;
@@ -129,46 +124,60 @@ LF_DEVICE void route(const int32_t *counts, const MoeDesc &d, const float *logit
     if (e >= E) break;
     int r = 0;
     for (int j = 0; j < E4; j += 4) {
-      const float4 u = *reinterpret_cast<const float4 *>(&sv[w][j]);
+      const float4 u = *reinterpret_cast<const float4 *>(&sv[j]);
       r += (u.x > v[i] || (u.x == v[i] && j < e)) ? 1 : 0;
       r += (u.y > v[i] || (u.y == v[i] && j + 1 < e)) ? 1 : 0;
       r += (u.z > v[i] || (u.z == v[i] && j + 2 < e)) ? 1 : 0;
       r += (u.w > v[i] || (u.w == v[i] && j + 3 < e)) ? 1 : 0;
     }
     for (int j = E4; j < E; ++j) {
-      const float u = sv[w][j];
+      const float u = sv[j];
       r += (u > v[i] || (u == v[i] && j < e)) ? 1 : 0;
     }
     if (r < k) {
-      sid[w][r] = e;
-      spv[w][r] = v[i];
+      sid[r] = e;
+      spv[r] = v[i];
     }
   }
   wave_lds_sync();
-  const float top = spv[w][0];
+  const float top = spv[0];
   float sum = 0.0f;
   if (d.route_mode == 0) {
-    for (int j = 0; j < k; ++j) sum += expf(spv[w][j] - top);
+    for (int j = 0; j < k; ++j) sum += expf(spv[j] - top);
   } else {
+    // the ranking above has read sv for the last time
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
       const int e = lane + 64 * i;
-      if (e < E) sv[w][e] = expf(v[i] - top);
+      if (e < E) sv[e] = expf(v[i] - top);
     }
     wave_lds_sync();
     for (int j = 0; j < E4; j += 4) {
-      const float4 u = *reinterpret_cast<const float4 *>(&sv[w][j]);
+      const float4 u = *reinterpret_cast<const float4 *>(&sv[j]);
       sum += u.x;
       sum += u.y;
       sum += u.z;
       sum += u.w;
     }
-    for (int j = E4; j < E; ++j) sum += sv[w][j];
+    for (int j = E4; j < E; ++j) sum += sv[j];
   }
   if (lane < k) {
-    ids[lane] = sid[w][lane];
-    wts[lane] = expf(spv[w][lane] - top) / sum;
+    ids[lane] = sid[lane];
+    wts[lane] = expf(spv[lane] - top) / sum;
   }
+  // the next token of this wave overwrites sv, sid and spv
+  wave_lds_sync();
+}
+
+LF_DEVICE void route(const int32_t *counts, const MoeDesc &d, const float *logits, uint8_t *ws) {
+  __shared__ __attribute__((aligned(16))) float sv[4][256];
+  __shared__ int32_t sid[4][16];
+  __shared__ float spv[4][16];
+  const int T = live_rows(counts, 1 << 30);
+  const int w = threadIdx.x >> 6;
+  const int t = blockIdx.x * 4 + w;
+  if (t >= T) return;
+  route_token(d, MoeLayout(d, T), logits, ws, t, sv[w], sid[w], spv[w]);
 }
 
 // --- stable counting sort ----------------------------------------------------
@@ -212,105 +221,95 @@ LF_DEVICE void sort_count(const int32_t *counts, const MoeDesc &d, uint8_t *ws) 
   for (int e = tid; e < E; e += kSortThreads) table[e] = cnt[e];
 }
 
-LF_DEVICE void sort_assignments(const int32_t *counts, const MoeDesc &d, uint8_t *ws) {
-  __shared__ int32_t base[256];  // first position of expert e's rows of this chunk
-  __shared__ int32_t wcnt[kSortWaves][256];
-  const int T = live_rows(counts, 1 << 30);
-  const MoeLayout L(d, T);
+// Writes an empty routing result: every expert without rows (the GEMMs then
+// launch no tile).
+LF_DEVICE void sort_write_empty(const MoeDesc &d, const MoeLayout &L, uint8_t *ws) {
   const int E = d.experts;
-  const int A = T * d.top_k;
-  const int c = blockIdx.x;
-  if (A == 0) {
-    // No assignments: every expert is empty (the GEMMs then launch no tile).
-    if (c == 0) {
-      for (int e = threadIdx.x; e <= E; e += kSortThreads) {
-        at<int32_t>(ws, L.offsets)[e] = 0;
-        at<int32_t>(ws, L.tiles)[e] = 0;
-        at<int32_t>(ws, L.tiles)[E + 1 + e] = 0;
-      }
-      if (threadIdx.x == 0) at<int32_t>(ws, L.tiles)[2 * E + 2] = 0;  // no expert has rows
-    }
-    return;
+  for (int e = threadIdx.x; e <= E; e += blockDim.x) {
+    at<int32_t>(ws, L.offsets)[e] = 0;
+    at<int32_t>(ws, L.tiles)[e] = 0;
+    at<int32_t>(ws, L.tiles)[E + 1 + e] = 0;
   }
-  if (c * kSortThreads >= A) return;
-  const int chunks = (A + kSortThreads - 1) / kSortThreads;
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  const int32_t *ids = at<int32_t>(ws, L.topk_ids);
-  const int32_t *table = chunk_table(ws, L);
-  int32_t *sorted = at<int32_t>(ws, L.sorted);
-  int32_t *pos = at<int32_t>(ws, L.pos);
+  if (threadIdx.x == 0) at<int32_t>(ws, L.tiles)[2 * E + 2] = 0;  // no expert has rows
+}
+
+// Exclusive scans over the experts by wave 0 (lane l holds experts 4l ..
+// 4l + 3), from the expert totals in wcnt[0]: first row, first 128-row tile
+// and first 256-row tile of each expert, and its index in the list of
+// experts with rows; written to the workspace when write_global, and the
+// first row added to base[e]. The caller synchronizes the block before and
+// after.
+LF_DEVICE void sort_scan_experts(const MoeDesc &d, const MoeLayout &L, uint8_t *ws, bool write_global,
+                                 int32_t *base, int32_t (*wcnt)[256]) {
+  const int E = d.experts;
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  if (wave != 0) return;
   int32_t *offsets = at<int32_t>(ws, L.offsets);
   int32_t *tiles = at<int32_t>(ws, L.tiles);
-  // Per expert: total rows and rows in the chunks before this one, every
-  // (chunk, expert) entry of the table loaded by its own thread and added
-  // into LDS (integer sums: the order does not matter).
-  for (int e = tid; e < E; e += kSortThreads) {
-    wcnt[0][e] = 0;
-    base[e] = 0;
-  }
-  __syncthreads();
-  for (int i = tid; i < chunks * E; i += kSortThreads) {
-    const int cc = i / E, e = i - cc * E;
-    const int n = table[i];
-    atomicAdd(&wcnt[0][e], n);
-    if (cc < c) atomicAdd(&base[e], n);
-  }
-  __syncthreads();
-  if (wave == 0) {
-    // Exclusive scans over the experts (lane l holds experts 4l .. 4l + 3):
-    // first row, first 128-row tile and first 256-row tile of each expert,
-    // and its index in the list of experts with rows.
-    int n4[4], r = 0, t1 = 0, t2 = 0, lv = 0;
+  int n4[4], r = 0, t1 = 0, t2 = 0, lv = 0;
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const int e = 4 * lane + i;
-      n4[i] = e < E ? wcnt[0][e] : 0;
-      r += n4[i];
-      t1 += (n4[i] + w8a8::kBM - 1) / w8a8::kBM;
-      t2 += (n4[i] + 2 * w8a8::kBM - 1) / (2 * w8a8::kBM);
-      lv += n4[i] > 0 ? 1 : 0;
+  for (int i = 0; i < 4; ++i) {
+    const int e = 4 * lane + i;
+    n4[i] = e < E ? wcnt[0][e] : 0;
+    r += n4[i];
+    t1 += (n4[i] + w8a8::kBM - 1) / w8a8::kBM;
+    t2 += (n4[i] + 2 * w8a8::kBM - 1) / (2 * w8a8::kBM);
+    lv += n4[i] > 0 ? 1 : 0;
+  }
+  int off = r, tl = t1, tl2 = t2, live = lv;  // inclusive scans across lanes
+#pragma unroll
+  for (int step = 1; step < 64; step <<= 1) {
+    const int a0 = __shfl_up(off, step), a1 = __shfl_up(tl, step), a2 = __shfl_up(tl2, step),
+              a3 = __shfl_up(live, step);
+    if (lane >= step) {
+      off += a0;
+      tl += a1;
+      tl2 += a2;
+      live += a3;
     }
-    int off = r, tl = t1, tl2 = t2, live = lv;  // inclusive scans across lanes
+  }
+  off -= r;
+  tl -= t1;
+  tl2 -= t2;
+  live -= lv;
 #pragma unroll
-    for (int step = 1; step < 64; step <<= 1) {
-      const int a0 = __shfl_up(off, step), a1 = __shfl_up(tl, step), a2 = __shfl_up(tl2, step),
-                a3 = __shfl_up(live, step);
-      if (lane >= step) {
-        off += a0;
-        tl += a1;
-        tl2 += a2;
-        live += a3;
+  for (int i = 0; i < 4; ++i) {
+    const int e = 4 * lane + i;
+    if (e < E) {
+      if (write_global) {
+        offsets[e] = off;
+        tiles[e] = tl;
+        tiles[E + 1 + e] = tl2;
+        if (n4[i] > 0) tiles[2 * E + 3 + live] = e;
       }
+      base[e] += off;
     }
-    off -= r;
-    tl -= t1;
-    tl2 -= t2;
-    live -= lv;
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const int e = 4 * lane + i;
-      if (e < E) {
-        if (c == 0) {
-          offsets[e] = off;
-          tiles[e] = tl;
-          tiles[E + 1 + e] = tl2;
-          if (n4[i] > 0) tiles[2 * E + 3 + live] = e;
-        }
-        base[e] += off;
-      }
-      off += n4[i];
-      tl += (n4[i] + w8a8::kBM - 1) / w8a8::kBM;
-      tl2 += (n4[i] + 2 * w8a8::kBM - 1) / (2 * w8a8::kBM);
-      live += n4[i] > 0 ? 1 : 0;
-    }
-    if (c == 0 && lane == 63) {  // experts past E count 0: lane 63 holds the totals
-      offsets[E] = off;
-      tiles[E] = tl;
-      tiles[E + 1 + E] = tl2;
-      tiles[2 * E + 2] = live;
-    }
+    off += n4[i];
+    tl += (n4[i] + w8a8::kBM - 1) / w8a8::kBM;
+    tl2 += (n4[i] + 2 * w8a8::kBM - 1) / (2 * w8a8::kBM);
+    live += n4[i] > 0 ? 1 : 0;
   }
-  __syncthreads();
+  if (write_global && lane == 63) {  // experts past E count 0: lane 63 holds the totals
+    offsets[E] = off;
+    tiles[E] = tl;
+    tiles[E + 1 + E] = tl2;
+    tiles[2 * E + 2] = live;
+  }
+}
+
+// Positions of chunk c's assignments (a = c * kSortThreads + thread < A)
+// from base[e], the first position of expert e's rows of this chunk: ranks
+// among equal experts within a wave by matching expert ids with ballots over
+// their bits, across the chunk's waves by a prefix over per-wave counts
+// (left in wcnt[wave][e] on return). Every thread of a kSortThreads-thread
+// block calls it; it synchronizes the block inside.
+LF_DEVICE void sort_rank_chunk(const MoeDesc &d, const MoeLayout &L, uint8_t *ws, int A, int c,
+                               const int32_t *base, int32_t (*wcnt)[256]) {
+  const int E = d.experts;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int32_t *ids = at<int32_t>(ws, L.topk_ids);
+  int32_t *sorted = at<int32_t>(ws, L.sorted);
+  int32_t *pos = at<int32_t>(ws, L.pos);
   for (int i = tid; i < kSortWaves * E; i += kSortThreads) wcnt[i / E][i % E] = 0;
   int bits = 0;
   while ((1 << bits) < E + 1) ++bits;
@@ -332,6 +331,93 @@ LF_DEVICE void sort_assignments(const int32_t *counts, const MoeDesc &d, uint8_t
     const int p = base[e] + before + rank;
     sorted[p] = a;
     pos[a] = p;
+  }
+}
+
+LF_DEVICE void sort_assignments(const int32_t *counts, const MoeDesc &d, uint8_t *ws) {
+  __shared__ int32_t base[256];  // first position of expert e's rows of this chunk
+  __shared__ int32_t wcnt[kSortWaves][256];
+  const int T = live_rows(counts, 1 << 30);
+  const MoeLayout L(d, T);
+  const int E = d.experts;
+  const int A = T * d.top_k;
+  const int c = blockIdx.x;
+  if (A == 0) {
+    if (c == 0) sort_write_empty(d, L, ws);
+    return;
+  }
+  if (c * kSortThreads >= A) return;
+  const int chunks = (A + kSortThreads - 1) / kSortThreads;
+  const int tid = threadIdx.x;
+  const int32_t *table = chunk_table(ws, L);
+  // Per expert: total rows and rows in the chunks before this one, every
+  // (chunk, expert) entry of the table loaded by its own thread and added
+  // into LDS (integer sums: the order does not matter).
+  for (int e = tid; e < E; e += kSortThreads) {
+    wcnt[0][e] = 0;
+    base[e] = 0;
+  }
+  __syncthreads();
+  for (int i = tid; i < chunks * E; i += kSortThreads) {
+    const int cc = i / E, e = i - cc * E;
+    const int n = table[i];
+    atomicAdd(&wcnt[0][e], n);
+    if (cc < c) atomicAdd(&base[e], n);
+  }
+  __syncthreads();
+  sort_scan_experts(d, L, ws, c == 0, base, wcnt);
+  __syncthreads();
+  sort_rank_chunk(d, L, ws, A, c, base, wcnt);
+}
+
+// Routing and the whole sort in one block of kSortThreads threads, for
+// profiles with few assignments (the launch geometry picks it when
+// max_tokens * top_k <= kSortThreads, where lf_moe_route, lf_moe_sort_count
+// and lf_moe_sort are three launches of a few microseconds each): the waves
+// route the tokens (route_token, as lf_moe_route), then the block counts the
+// assignments per expert, scans as lf_moe_sort, and ranks the chunks of
+// kSortThreads assignments in order, each chunk's positions starting where
+// the previous chunk's rows of each expert ended. Outputs equal those of the
+// three launches for any number of tokens.
+LF_DEVICE void route_sort_block(const int32_t *counts, const MoeDesc &d, const float *logits,
+                                uint8_t *ws) {
+  __shared__ __attribute__((aligned(16))) float sv[kSortWaves][256];
+  __shared__ int32_t sid[kSortWaves][16];
+  __shared__ float spv[kSortWaves][16];
+  __shared__ int32_t base[256];
+  __shared__ int32_t wcnt[kSortWaves][256];
+  const int T = live_rows(counts, 1 << 30);
+  const MoeLayout L(d, T);
+  const int E = d.experts;
+  const int A = T * d.top_k;
+  const int tid = threadIdx.x, wave = tid >> 6;
+  for (int t = wave; t < T; t += kSortWaves) route_token(d, L, logits, ws, t, sv[wave], sid[wave], spv[wave]);
+  // the ids written above are visible to the whole block after the barrier
+  __syncthreads();
+  if (A == 0) {
+    sort_write_empty(d, L, ws);
+    return;
+  }
+  for (int e = tid; e < E; e += kSortThreads) {
+    wcnt[0][e] = 0;
+    base[e] = 0;
+  }
+  __syncthreads();
+  const int32_t *ids = at<int32_t>(ws, L.topk_ids);
+  for (int a = tid; a < A; a += kSortThreads) atomicAdd(&wcnt[0][sort_expert(ids[a], E)], 1);
+  __syncthreads();
+  sort_scan_experts(d, L, ws, true, base, wcnt);
+  __syncthreads();
+  for (int c = 0; c * kSortThreads < A; ++c) {
+    sort_rank_chunk(d, L, ws, A, c, base, wcnt);
+    __syncthreads();
+    // the next chunk's rows of expert e start after this chunk's
+    for (int e = tid; e < E; e += kSortThreads) {
+      int n = 0;
+      for (int w = 0; w < kSortWaves; ++w) n += wcnt[w][e];
+      base[e] += n;
+    }
+    __syncthreads();
   }
 }
 
@@ -1243,6 +1329,13 @@ __global__ __launch_bounds__(1024) void lf_moe_sort(const int32_t *counts, const
   const MoeDesc &d = desc_of(desc);
   if (!desc_ok(d)) return;
   sort_assignments(counts, d, ws);
+}
+
+__global__ __launch_bounds__(1024) void lf_moe_route_sort(const int32_t *counts, const int32_t *desc,
+                                                         const float *logits, uint8_t *ws) {
+  const MoeDesc &d = desc_of(desc);
+  if (!desc_ok(d) || blockDim.x != kSortThreads) return;
+  route_sort_block(counts, d, logits, ws);
 }
 
 __global__ __launch_bounds__(256) void lf_moe_quant_tokens(const int32_t *counts,

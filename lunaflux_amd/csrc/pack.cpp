@@ -649,10 +649,30 @@ int32_t lunaflux_fp8_moe_launch_geometry(int32_t entry, const lf_fp8_moe_desc *d
   switch (entry) {
     // Routing and the per-token quantizers: one wave per token (row); the
     // per-128-column-group quantizers: four groups per wave.
-    case LF_FP8_MOE_ROUTE: name = "lf_moe_route"; gx = (T + 3) / 4; break;
+    // Profiles of at most 1024 assignments route and sort in one launch
+    // (lf_moe_route_sort, one 1024-thread block); the two sort steps then
+    // launch nothing (empty symbol, zero dims).
+    case LF_FP8_MOE_ROUTE:
+      if (A <= 1024) {
+        name = "lf_moe_route_sort";
+        bx = 1024;
+        break;
+      }
+      name = "lf_moe_route";
+      gx = (T + 3) / 4;
+      break;
     // The sort: one 1024-thread block per chunk of 1024 assignments.
-    case LF_FP8_MOE_SORT_COUNT: name = "lf_moe_sort_count"; gx = (A + 1023) / 1024; bx = 1024; break;
-    case LF_FP8_MOE_SORT: name = "lf_moe_sort"; gx = (A + 1023) / 1024; bx = 1024; break;
+    case LF_FP8_MOE_SORT_COUNT:
+    case LF_FP8_MOE_SORT:
+      if (A <= 1024) {
+        std::memset(dims, 0, 7 * sizeof(int32_t));
+        std::memset(symbol, 0, LF_FP8_SYMBOL_BYTES);
+        return LF_OK;
+      }
+      name = entry == LF_FP8_MOE_SORT ? "lf_moe_sort" : "lf_moe_sort_count";
+      gx = (A + 1023) / 1024;
+      bx = 1024;
+      break;
     case LF_FP8_MOE_QUANT_TOKENS:
       name = "lf_moe_quant_tokens";
       gx = b128 ? group_quant_blocks(T * (d->hidden / 128)) : (T + 3) / 4;

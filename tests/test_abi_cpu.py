@@ -37,7 +37,7 @@ def test_library_exports_every_declared_symbol():
 def test_code_object_has_every_entry_point():
     image = _abi.code_object_bytes()
     for symbol in ["lf_fp8_act_quant_rows"] + [f"lf_fp8_w8a8_{op}_{t}" for op in ("dense", "qkv", "gate_up")
-                                               for t in ("t128", "t256")] + ["lf_moe_route", "lf_moe_sort_count", "lf_moe_sort", "lf_moe_quant_tokens",
+                                               for t in ("t128", "t256")] + ["lf_moe_route", "lf_moe_route_sort", "lf_moe_sort_count", "lf_moe_sort", "lf_moe_quant_tokens",
                    "lf_moe_gate_up", "lf_moe_gate_up_b128", "lf_moe_quant_hidden", "lf_moe_down",
                    "lf_moe_down_b128", "lf_moe_combine", "lf_moe_gate_up_gemv", "lf_moe_down_gemv",
                    "lf_moe_gate_up_t256_b128", "lf_moe_down_t256_b128"] + [f"lf_fp8_w8a16_{op}_m{m}" for op in ("dense", "qkv", "gate_up")
@@ -283,6 +283,18 @@ def test_moe_descriptor_layout_and_geometry():
     assert sym == "lf_moe_sort" and dims.grid == (2, 1, 1) and dims.block == (1024, 1, 1)
     dims, sym = moe.launch_geometry(8, d, 1024)   # sort counts: a block per 1024 assignments
     assert sym == "lf_moe_sort_count" and dims.grid == (2, 1, 1)
+    dims, sym = moe.launch_geometry(1, d, 1024)   # route: a wave per token
+    assert sym == "lf_moe_route" and dims.grid == (256, 1, 1) and dims.block == (256, 1, 1)
+    # at most 1024 assignments: routing and the whole sort in one block, and
+    # no sort launches (empty symbol, zero dims)
+    for tokens in (512, 1):
+        dims, sym = moe.launch_geometry(1, d, tokens)
+        assert sym == "lf_moe_route_sort" and dims.grid == (1, 1, 1) and dims.block == (1024, 1, 1)
+        for entry in (8, 2):
+            dims, sym = moe.launch_geometry(entry, d, tokens)
+            assert sym == "" and dims.grid == (0, 0, 0) and dims.block == (0, 0, 0)
+    assert moe.launch_geometry(1, d, 513)[1] == "lf_moe_route"
+    assert moe.launch_geometry(2, d, 513)[1] == "lf_moe_sort"
     d5 = moe.moe_descriptor(64, 6, 1, 2048, 1408, 128)
     # block scales averaging >= 256 rows per expert: 256 x 256 tiles too
     dims, sym = moe.launch_geometry(6, d5, 4096)  # down
