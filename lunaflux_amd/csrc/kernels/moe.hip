@@ -698,22 +698,16 @@ struct BlockRescale256 {
   using T = GemmTile256;
   static_assert(T::kFN >= T::kFM, "apply(o) rescales column fragment o");
   typedef const __attribute__((address_space(3))) float *lds_ptr;
-  lds_ptr ra;          // [KT][256]: row ratios
-  lds_ptr rw;          // this wave: [kT256MaxKT] gate (or down) block ratios, then (STAGE 0) up
-  int row0;            // the lane's first accumulator row in the tile
-  f32x4 m[T::kFM][4];  // this k-tile's multipliers of the lane's 32 rows
+  lds_ptr ra;       // [KT][256]: row ratios
+  lds_ptr rw;       // this wave: [kT256MaxKT] gate (or down) block ratios, then (STAGE 0) up
+  int row0;         // the lane's row of fragment 0 in the tile (swapped layout: one row per
+                    // lane and fragment)
+  float m[T::kFM];  // this k-tile's multipliers of the lane's rows
   int kt = 0;
   LF_DEVICE void load(int part) {
     const float wk = rw[part * kT256MaxKT + kt];
 #pragma unroll
-    for (int i = 0; i < T::kFM; ++i)
-#pragma unroll
-      for (int q = 0; q < 4; ++q) {
-        const f32x4 r = *reinterpret_cast<const __attribute__((address_space(3))) f32x4 *>(
-            ra + kt * 256 + row0 + 32 * i + 8 * q);
-#pragma unroll
-        for (int e = 0; e < 4; ++e) m[i][q][e] = r[e] * wk;
-      }
+    for (int i = 0; i < T::kFM; ++i) m[i] = ra[kt * 256 + row0 + 32 * i] * wk;
   }
   LF_DEVICE void begin(int k) {
     kt = k;
@@ -728,7 +722,7 @@ struct BlockRescale256 {
 #pragma unroll
     for (int i = 0; i < T::kFM; ++i)
 #pragma unroll
-      for (int r = 0; r < 16; ++r) acc[i][o][r] *= m[i][r >> 2][r & 3];
+      for (int r = 0; r < 16; ++r) acc[i][o][r] *= m[i];
   }
 };
 
@@ -870,35 +864,52 @@ __device__ __forceinline__ void grouped_gemm_t256(const int32_t *counts, const M
   // loads (a tile of a small expert then moves its weights and little
   // else through the load path).
   const bool a_loads = p0 + 16 * T::kAIns * wave < pend;
+  // Per-channel column scales of the block, one per thread of the first 256
+  // (STAGE 1: its 256 output columns; STAGE 0: its 128 gate, then 128 up
+  // columns), loaded before the main loop and parked in LDS after it.
+  float sw_mine = 0.0f;
+  if constexpr (!BLOCK) {
+    const int n = static_cast<int>(threadIdx.x);
+    if (n < T::kBN) {
+      sw_mine = STAGE == 0 ? expert_scales(n < T::kBN / 2 ? w0 : w1, e)[bx * (T::kBN / 2) + (n & (T::kBN / 2 - 1))]
+                           : expert_scales(w0, e)[bx * T::kBN + n];
+    }
+  }
+  // The MFMAs run with swapped operands (mainloop SWAP): lane l holds tile
+  // row wm * 64 + 32 i + l % 32 of fragment i and, for element 4 g + q of
+  // fragment j, wave-tile column 32 j + 8 g + 4 (l / 32) + q. One row scale
+  // (and block-scale multiplier) per lane and fragment instead of 16 keeps
+  // registers free for the loop, and the epilogue stages 4 columns (8 bytes)
+  // per LDS write.
   if constexpr (BLOCK) {
     typedef const __attribute__((address_space(3))) float *lds_ptr;
     BlockRescale256<STAGE> rs{(lds_ptr)(ra_lds), (lds_ptr)(rw_lds + 2 * wn * kT256MaxKT),
-                              wm * T::kWaveM + 4 * (lane >> 5), {}, 0};
-    w8a8v4::mainloop<T, true, BlockRescale256<STAGE>>(plan, KT, smem, acc, live_fm, rs, a_loads);
+                              wm * T::kWaveM + (lane & 31), {}, 0};
+    w8a8v4::mainloop<T, true, BlockRescale256<STAGE>, true>(plan, KT, smem, acc, live_fm, rs, a_loads);
   } else {
-    w8a8v4::mainloop<T, true>(plan, KT, smem, acc, live_fm, w8a8v4::NoRescale{}, a_loads);
+    w8a8v4::mainloop<T, true, w8a8v4::NoRescale, true>(plan, KT, smem, acc, live_fm,
+                                                        w8a8v4::NoRescale{}, a_loads);
   }
 
-  const int c = lane & 31;
-  float swv[T::kFN];
-  int ocol[T::kFN];
-#pragma unroll
-  for (int j = 0; j < T::kFN; ++j) {
-    const uint8_t *region;
-    int t;
-    slot((wn * T::kWaveN) / 16 + 2 * j + (c >> 4), region, t, ocol[j]);
-    ocol[j] += c & 15;
-    if constexpr (BLOCK) {
-      swv[j] = sw_last[2 * wn + (STAGE == 0 && j >= T::kFN / 2 ? 1 : 0)];
-    } else {
-      swv[j] = expert_scales(region, e)[t * 16 + (c & 15)];
-    }
-  }
+  __shared__ float sw_tile[BLOCK ? 1 : T::kBN];
   if (threadIdx.x < BM) sa_tile[threadIdx.x] = sa_mine;
+  if constexpr (!BLOCK) {
+    if (threadIdx.x < T::kBN) sw_tile[threadIdx.x] = sw_mine;
+  }
+  // Column scale of wave-tile column cc of part `part` (0: gate or down
+  // columns, 1: up columns).
+  auto col_scale = [&](int part, int cc) -> float {
+    if constexpr (BLOCK) {
+      return sw_last[2 * wn + part];
+    } else {
+      return STAGE == 0 ? sw_tile[part * (T::kBN / 2) + wn * (T::kWaveN / 2) + cc]
+                        : sw_tile[wn * T::kWaveN + cc];
+    }
+  };
+  const int rl = lane & 31, c4 = 4 * (lane >> 5);
   // The output goes through LDS in 16-byte row chunks (w8a8v4::StageTile):
   // STAGE 0 stages 32 rows x 64 h-columns of bf16 per pass, STAGE 1 32 rows
-  // x 128 columns of bf16.
-  const int col0 = __builtin_amdgcn_readfirstlane(ocol[0] - c);
+  // x 128 columns of bf16; each lane writes 4 consecutive columns at a time.
   w8a8v4::epilogue_barrier();
   const int pw = p0 + wm * T::kWaveM;
   if constexpr (QUANT) {
@@ -915,18 +926,23 @@ __device__ __forceinline__ void grouped_gemm_t256(const int32_t *counts, const M
     uint16_t *tile = reinterpret_cast<uint16_t *>(smem);
 #pragma unroll
     for (int i = 0; i < T::kFM; ++i) {
+      const int row = wm * T::kWaveM + w8a8v4::acc_row_t<T>(i, lane);
+      const float sa = sa_tile[row];
 #pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        const int row = wm * T::kWaveM + w8a8v4::acc_row<T>(i, lane, r);
-        const float sa = sa_tile[row];
+      for (int j = 0; j < T::kFN / 2; ++j)
 #pragma unroll
-        for (int j = 0; j < T::kFN / 2; ++j) {
-          const float gv = acc[i][j][r] * sa * swv[j];
-          const float uv = acc[i][j + T::kFN / 2][r] * sa * swv[j + T::kFN / 2];
-          tile[row * kPitch + ocol[j] - bx * (T::kBN / 2)] =
-              static_cast<uint16_t>(f32_to_bf16(silu_mul(gv, uv)));
+        for (int g = 0; g < 4; ++g) {
+          const int cc = 32 * j + 8 * g + c4;
+          uint32_t b[4];
+#pragma unroll
+          for (int q = 0; q < 4; ++q) {
+            const float gv = acc[i][j][4 * g + q] * sa * col_scale(0, cc + q);
+            const float uv = acc[i][j + T::kFN / 2][4 * g + q] * sa * col_scale(1, cc + q);
+            b[q] = f32_to_bf16(silu_mul(gv, uv));
+          }
+          *reinterpret_cast<uint2 *>(tile + row * kPitch + wn * (T::kWaveN / 2) + cc) =
+              uint2{b[0] | (b[1] << 16), b[2] | (b[3] << 16)};
         }
-      }
     }
     __syncthreads();
     uint8_t *hq = at<uint8_t>(ws, L.hq);
@@ -955,19 +971,24 @@ __device__ __forceinline__ void grouped_gemm_t256(const int32_t *counts, const M
     static_assert(Stage::kBytes * T::kWaves <= T::kSmem, "staging fits the stage ring");
     const Stage st{reinterpret_cast<uint16_t *>(smem + wave * Stage::kBytes)};
     uint16_t *h = at<uint16_t>(ws, L.h);
+    const int col0 = bx * (T::kBN / 2) + wn * (T::kWaveN / 2);
 #pragma unroll
     for (int i = 0; i < T::kFM; ++i) {
+      const float sa = sa_tile[wm * T::kWaveM + w8a8v4::acc_row_t<T>(i, lane)];
 #pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        const float sa = sa_tile[wm * T::kWaveM + w8a8v4::acc_row<T>(i, lane, r)];
+      for (int j = 0; j < T::kFN / 2; ++j)
 #pragma unroll
-        for (int j = 0; j < T::kFN / 2; ++j) {
-          const float gv = acc[i][j][r] * sa * swv[j];
-          const float uv = acc[i][j + T::kFN / 2][r] * sa * swv[j + T::kFN / 2];
-          st.put(w8a8v4::acc_row<T>(0, lane, r), ocol[j] - col0,
-                 static_cast<uint16_t>(f32_to_bf16(silu_mul(gv, uv))));
+        for (int g = 0; g < 4; ++g) {
+          const int cc = 32 * j + 8 * g + c4;
+          uint32_t b[4];
+#pragma unroll
+          for (int q = 0; q < 4; ++q) {
+            const float gv = acc[i][j][4 * g + q] * sa * col_scale(0, cc + q);
+            const float uv = acc[i][j + T::kFN / 2][4 * g + q] * sa * col_scale(1, cc + q);
+            b[q] = f32_to_bf16(silu_mul(gv, uv));
+          }
+          st.put4(rl, cc, b);
         }
-      }
       const int p_i = pw + 32 * i;
       st.flush(lane, [&](int row) -> uint16_t * {
         return p_i + row < pend ? h + static_cast<uint64_t>(p_i + row) * N + col0 : nullptr;
@@ -978,17 +999,20 @@ __device__ __forceinline__ void grouped_gemm_t256(const int32_t *counts, const M
     static_assert(Stage::kBytes * T::kWaves <= T::kSmem, "staging fits the stage ring");
     const Stage st{reinterpret_cast<uint16_t *>(smem + wave * Stage::kBytes)};
     uint16_t *y = at<uint16_t>(ws, L.y);
+    const int col0 = bx * T::kBN + wn * T::kWaveN;
 #pragma unroll
     for (int i = 0; i < T::kFM; ++i) {
+      const float sa = sa_tile[wm * T::kWaveM + w8a8v4::acc_row_t<T>(i, lane)];
 #pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        const float sa = sa_tile[wm * T::kWaveM + w8a8v4::acc_row<T>(i, lane, r)];
+      for (int j = 0; j < T::kFN; ++j)
 #pragma unroll
-        for (int j = 0; j < T::kFN; ++j) {
-          st.put(w8a8v4::acc_row<T>(0, lane, r), ocol[j] - col0,
-                 static_cast<uint16_t>(f32_to_bf16(acc[i][j][r] * sa * swv[j])));
+        for (int g = 0; g < 4; ++g) {
+          const int cc = 32 * j + 8 * g + c4;
+          uint32_t b[4];
+#pragma unroll
+          for (int q = 0; q < 4; ++q) b[q] = f32_to_bf16(acc[i][j][4 * g + q] * sa * col_scale(0, cc + q));
+          st.put4(rl, cc, b);
         }
-      }
       const int p_i = pw + 32 * i;
       st.flush(lane, [&](int row) -> uint16_t * {
         return p_i + row < pend ? y + static_cast<uint64_t>(p_i + row) * N + col0 : nullptr;

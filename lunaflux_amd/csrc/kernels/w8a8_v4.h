@@ -105,13 +105,19 @@ LF_DEVICE void block_barrier() { asm volatile("s_barrier" ::: "memory"); }
 // per loader and per fragment). The rows such a wave would have written keep
 // whatever the LDS held; no MFMA reads them. Each wave counts its own loads
 // (vmcnt), so the waits use kBIns loads per stage for such a wave.
+// SWAP: the MFMAs take the weight fragment as their first operand and the
+// activation fragment as the second, so each accumulator block holds the
+// transposed product: lane l keeps tile row 32 i + l % 32 of fragment i and,
+// for element 4 g + q of fragment j, column 32 j + 8 g + 4 (l / 32) + q (one
+// row per lane and fragment, runs of 4 consecutive columns; acc_row_t and
+// acc_col_t). The sums are the same, element by element.
 struct NoRescale {
   LF_DEVICE void begin(int) {}
   template <class A>
   LF_DEVICE void apply(int, A &) {}
 };
 
-template <class T, bool SKIP = false, class Rescale = NoRescale>
+template <class T, bool SKIP = false, class Rescale = NoRescale, bool SWAP = false>
 __device__ __forceinline__ void mainloop(const Plan<T> &plan, int KT, uint8_t *smem,
                          f32x16 (&acc)[T::kFM][T::kFN], int live_fm = T::kFM,
                          Rescale rescale = Rescale{}, bool a_loads = true) {
@@ -190,9 +196,10 @@ __device__ __forceinline__ void mainloop(const Plan<T> &plan, int KT, uint8_t *s
       // row fragment of this product: n (inner = A) or o (outer = A)
       if (!SKIP || (kOuterN ? n : o) < live) {
         f32x16 &a = kOuterN ? acc[n][o] : acc[o][n];
-        a = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(
-            kOuterN ? cur[n].v : outer[o].v, kOuterN ? outer[o].v : cur[n].v, a, 0, 0, 0, 127, 0,
-            127);
+        const auto &fa = kOuterN ? cur[n].v : outer[o].v;  // activation rows
+        const auto &fb = kOuterN ? outer[o].v : cur[n].v;  // weight columns
+        a = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(SWAP ? fb : fa, SWAP ? fa : fb, a, 0, 0,
+                                                            0, 127, 0, 127);
       }
     }
   };
@@ -296,6 +303,12 @@ struct StageTile {
   static constexpr int kChunksPerRow = COLS * static_cast<int>(sizeof(Elem)) / 16;
   Elem *base;
   LF_DEVICE void put(int row, int col, Elem v) const { base[row * kPitch + col] = v; }
+  // Four consecutive 16-bit elements from column col (a multiple of 4): one
+  // 8-byte write.
+  LF_DEVICE void put4(int row, int col, const uint32_t (&b)[4]) const {
+    static_assert(sizeof(Elem) == 2, "four 16-bit elements");
+    *reinterpret_cast<uint2 *>(base + row * kPitch + col) = uint2{b[0] | (b[1] << 16), b[2] | (b[3] << 16)};
+  }
   // Writes the staged tile: row `row` goes to row_ptr(row) (null: skipped).
   template <class RowPtr>
   LF_DEVICE void flush(int lane, RowPtr row_ptr) const {
@@ -324,6 +337,15 @@ LF_DEVICE int acc_row(int i, int lane, int e) {
 template <class T>
 LF_DEVICE int acc_col(int j, int lane) {
   return 32 * j + (lane & 31);
+}
+// The same with SWAP: the row is the lane's, the columns run in groups of 4.
+template <class T>
+LF_DEVICE int acc_row_t(int i, int lane) {
+  return 32 * i + (lane & 31);
+}
+template <class T>
+LF_DEVICE int acc_col_t(int j, int lane, int e) {
+  return 32 * j + 8 * (e >> 2) + 4 * (lane >> 5) + (e & 3);
 }
 
 }  // namespace w8a8v4
