@@ -724,8 +724,17 @@ struct NoWait {
 // part of the grid (default: blockIdx.x, gridDim.x). wait(s) runs after the
 // weight prologue is in flight and before the first activation load of
 // K-slice s.
+// KROT: each block walks its k-tiles starting at ((block / 8) mod NKT) and
+// wrapping around, instead of at 0. Blocks are dispatched to the 8 XCDs in
+// turn, so the blocks sharing one L2 start at different k-tiles. Unsplit
+// forms (every block reads all of x) otherwise all read the same k-tile of
+// x at the same moment from the same few L2 channels: gate/up at 32 rows
+// 21.6 -> 20.5 us. The split-K forms read disjoint slices and were slower
+// with it (down 17.8 -> 18.4 us), so they keep the plain order. The sums
+// run in a different k order, so results differ from the plain order by
+// fp32 rounding.
 template <int K, int S, int WAVES, int MT, int MODE, int DW, int DX, int NQ = 0, int NKV = 0,
-          class Wait = NoWait, bool COHERENT_OUT = false>
+          class Wait = NoWait, bool COHERENT_OUT = false, bool KROT = false>
 __device__ __forceinline__ void w8a16_fixed_group_kernel(const int32_t *counts, const uint16_t *x,
                                          const uint8_t *w0, const uint8_t *w1, const uint8_t *w2,
                                          uint16_t *y, uint8_t *ws, int bid = -1, int nblocks = -1,
@@ -777,6 +786,12 @@ __device__ __forceinline__ void w8a16_fixed_group_kernel(const int32_t *counts, 
   }
   if constexpr (NW == 2) region[NW - 1] = w1;
   const int kt0 = s * NKT;
+  // k-tile index of step k (KROT: rotated by the block's position on its XCD)
+  const int rot = KROT ? __builtin_amdgcn_readfirstlane((block >> 3) % NKT) : 0;
+  auto kr = [&](int k) {
+    const int kk = k + rot;
+    return kk < NKT ? kk : kk - NKT;
+  };
   const uint64_t tile_base = kWeightHeaderBytes + static_cast<uint64_t>(t) * KT * kTileBytes;
   const uint8_t *strip[NW];
 #pragma unroll
@@ -790,7 +805,7 @@ __device__ __forceinline__ void w8a16_fixed_group_kernel(const int32_t *counts, 
 
   uint4 b[EW][NW][2];
 #pragma unroll
-  for (int d = 0; d < EW; ++d) load_tiles<NW>(strip, kt0 + d, lane, b[d]);
+  for (int d = 0; d < EW; ++d) load_tiles<NW>(strip, kt0 + kr(d), lane, b[d]);
   __builtin_amdgcn_sched_barrier(0);
 
   // A region whose header disagrees with the compiled shape counts as no
@@ -809,7 +824,7 @@ __device__ __forceinline__ void w8a16_fixed_group_kernel(const int32_t *counts, 
   }
   auto load_a = [&](int k, u32x4 (&dst)[XPW]) {
 #pragma unroll
-    for (int j = 0; j < XPW; ++j) dst[j] = *reinterpret_cast<const u32x4 *>(xsrc[j] + k * 128);
+    for (int j = 0; j < XPW; ++j) dst[j] = *reinterpret_cast<const u32x4 *>(xsrc[j] + kr(k) * 128);
   };
   wait(s);
   u32x4 a[EX][XPW];
@@ -851,7 +866,7 @@ __device__ __forceinline__ void w8a16_fixed_group_kernel(const int32_t *counts, 
       }
     }
     __builtin_amdgcn_sched_barrier(0);
-    if constexpr (k + EW < NKT) load_tiles<NW>(strip, kt0 + k + EW, lane, b[k % EW]);
+    if constexpr (k + EW < NKT) load_tiles<NW>(strip, kt0 + kr(k + EW), lane, b[k % EW]);
     __builtin_amdgcn_sched_barrier(0);
   });
 
@@ -936,7 +951,7 @@ struct GatedMlpFixed {
     int *sync = reinterpret_cast<int *>(ws + kHBytes + kDownBytes);
     const int b = static_cast<int>(blockIdx.x);
     if (b < kG1) {
-      w8a16_fixed_group_kernel<H, 1, GU_W, MT, 2, GU_DW, GU_DX, 0, 0, NoWait, true>(
+      w8a16_fixed_group_kernel<H, 1, GU_W, MT, 2, GU_DW, GU_DX, 0, 0, NoWait, true, true>(
           counts, x, wg, wu, wu, h, ws_down, b, kG1);
       asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
       __syncthreads();
@@ -1044,13 +1059,15 @@ LF_W8A16_TILE_ENTRIES(1, 16, 1)
 #define LF_W16_FIXED_DENSE_WIDE_G(KK, M, MT, S, W, DW, DX)                                      \
   __global__ __launch_bounds__(W * 64) void lf_fp8_w8a16_dense_wide_k##KK##_m##M(            \
       const int32_t *counts, const uint16_t *x, const uint8_t *w, uint16_t *y, uint8_t *ws) { \
-    w8a16_fixed_group_kernel<KK, S, W, MT, 0, DW, DX>(counts, x, w, w, w, y, ws);             \
+    w8a16_fixed_group_kernel<KK, S, W, MT, 0, DW, DX, 0, 0, NoWait, false, S == 1>(            \
+        counts, x, w, w, w, y, ws);                                                          \
   }
 #define LF_W16_FIXED_GATE_UP_G(KK, M, MT, S, W, DW, DX)                                         \
   __global__ __launch_bounds__(W * 64) void lf_fp8_w8a16_gate_up_k##KK##_m##M(               \
       const int32_t *counts, const uint16_t *x, const uint8_t *wg, const uint8_t *wu,        \
       uint16_t *h, uint8_t *ws) {                                                            \
-    w8a16_fixed_group_kernel<KK, S, W, MT, 2, DW, DX>(counts, x, wg, wu, wu, h, ws);          \
+    w8a16_fixed_group_kernel<KK, S, W, MT, 2, DW, DX, 0, 0, NoWait, false, S == 1>(            \
+        counts, x, wg, wu, wu, h, ws);                                                       \
   }
 
 LF_W16_FIXED_DENSE_T1(4096, 16, 1, 8, 4, 2, 2)
