@@ -272,15 +272,16 @@ int32_t lunaflux_fp8_rms_norm_quant_geometry(float epsilon, int64_t k, int32_t m
  * profile's max_query_tokens.
  *
  * Launch sequence and operands (in order):
- *  lf_moe_route[_sort]  (counts, desc, logits fp32 [T, E], ws)
+ *  lf_moe_route[_sort]  (counts, desc, logits fp32 [T, E], x bf16 [T, H], ws)
  *  lf_moe_sort_count    (counts, desc, ws)    (not after lf_moe_route_sort)
  *  lf_moe_sort          (counts, desc, ws)    (not after lf_moe_route_sort)
- * (lf_moe_route_sort: routing and the whole sort in one 1024-thread block,
- * chosen for profiles of max_tokens * top_k <= 1024; the geometry then
- * returns LF_OK with an empty symbol and zero dims for
- * LF_FP8_MOE_SORT_COUNT and LF_FP8_MOE_SORT, meaning no launch. Its outputs
- * equal those of the three launches.)
- *  lf_moe_quant_tokens  (counts, desc, x bf16 [T, H], ws)
+ *  lf_moe_quant_tokens  (counts, desc, x bf16 [T, H], ws)  (not after lf_moe_route_sort)
+ * (lf_moe_route_sort: routing, the whole sort and the token quantizer in one
+ * 1024-thread block, chosen for profiles of max_tokens * top_k <= 1024; the
+ * geometry then returns LF_OK with an empty symbol and zero dims for
+ * LF_FP8_MOE_SORT_COUNT, LF_FP8_MOE_SORT and LF_FP8_MOE_QUANT_TOKENS,
+ * meaning no launch. Its outputs equal those of the four launches.
+ * lf_moe_route does not read x.)
  *  lf_moe_gate_up[_b128|_t256|_t256_b128_q|_gemv](counts, desc, wg, wu, ws)
  *  lf_moe_quant_hidden  (counts, desc, ws)    (not with _t256_b128_q)
  *  lf_moe_down[_b128|_t256|_t256_b128|_gemv]   (counts, desc, wd, ws)

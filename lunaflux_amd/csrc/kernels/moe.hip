@@ -370,17 +370,21 @@ LF_DEVICE void sort_assignments(const int32_t *counts, const MoeDesc &d, uint8_t
   sort_rank_chunk(d, L, ws, A, c, base, wcnt);
 }
 
-// Routing and the whole sort in one block of kSortThreads threads, for
-// profiles with few assignments (the launch geometry picks it when
-// max_tokens * top_k <= kSortThreads, where lf_moe_route, lf_moe_sort_count
-// and lf_moe_sort are three launches of a few microseconds each): the waves
-// route the tokens (route_token, as lf_moe_route), then the block counts the
-// assignments per expert, scans as lf_moe_sort, and ranks the chunks of
-// kSortThreads assignments in order, each chunk's positions starting where
-// the previous chunk's rows of each expert ended. Outputs equal those of the
-// three launches for any number of tokens.
+// Routing, the whole sort and the token quantizer in one block of
+// kSortThreads threads, for profiles with few assignments (the launch
+// geometry picks it when max_tokens * top_k <= kSortThreads, where
+// lf_moe_route, lf_moe_sort_count, lf_moe_sort and lf_moe_quant_tokens are
+// four launches of a few microseconds each): the waves route the tokens
+// (route_token, as lf_moe_route), then the block counts the assignments per
+// expert, scans as lf_moe_sort, and ranks the chunks of kSortThreads
+// assignments in order, each chunk's positions starting where the previous
+// chunk's rows of each expert ended; then the waves quantize the tokens as
+// lf_moe_quant_tokens does (the per-token form with the two-pass row
+// quantizer, whose codes and scales equal the register-resident one's: a
+// 1024-thread block leaves a wave 128 registers). Outputs equal those of the
+// four launches for any number of tokens.
 LF_DEVICE void route_sort_block(const int32_t *counts, const MoeDesc &d, const float *logits,
-                                uint8_t *ws) {
+                                const uint16_t *x, uint8_t *ws) {
   __shared__ __attribute__((aligned(16))) float sv[kSortWaves][256];
   __shared__ int32_t sid[kSortWaves][16];
   __shared__ float spv[kSortWaves][16];
@@ -418,6 +422,20 @@ LF_DEVICE void route_sort_block(const int32_t *counts, const MoeDesc &d, const f
       base[e] += n;
     }
     __syncthreads();
+  }
+  // The token quantizer; the per-token form reads the positions written
+  // above (visible to the block after the last barrier).
+  if (d.group != 0) {
+    quantize_groups_wave(x, d.hidden, T, at<uint8_t>(ws, L.xq), at<float>(ws, L.xs), wave,
+                         kSortWaves);
+    return;
+  }
+  const int lane = tid & 63;
+  for (int t = wave; t < T; t += kSortWaves) {
+    const uint64_t off = static_cast<uint64_t>(t) * d.hidden;
+    const float sc = quantize_row_wave_2pass(x + off, d.hidden, at<uint8_t>(ws, L.xq) + off,
+                                             at<float>(ws, L.xs) + t);
+    if (lane < d.top_k) at<float>(ws, L.hs)[at<int32_t>(ws, L.pos)[t * d.top_k + lane]] = sc;
   }
 }
 
@@ -1334,8 +1352,11 @@ LF_DEVICE const MoeDesc &desc_of(const int32_t *desc) { return *reinterpret_cast
 
 extern "C" {
 
+// The route step's operands carry the tokens x for both of its kernels
+// (lf_moe_route does not read them; lf_moe_route_sort quantizes them).
 __global__ __launch_bounds__(256) void lf_moe_route(const int32_t *counts, const int32_t *desc,
-                                                    const float *logits, uint8_t *ws) {
+                                                    const float *logits, const uint16_t *,
+                                                    uint8_t *ws) {
   const MoeDesc &d = desc_of(desc);
   if (!desc_ok(d)) return;
   route(counts, d, logits, ws);
@@ -1356,10 +1377,11 @@ __global__ __launch_bounds__(1024) void lf_moe_sort(const int32_t *counts, const
 }
 
 __global__ __launch_bounds__(1024) void lf_moe_route_sort(const int32_t *counts, const int32_t *desc,
-                                                         const float *logits, uint8_t *ws) {
+                                                         const float *logits, const uint16_t *x,
+                                                         uint8_t *ws) {
   const MoeDesc &d = desc_of(desc);
   if (!desc_ok(d) || blockDim.x != kSortThreads) return;
-  route_sort_block(counts, d, logits, ws);
+  route_sort_block(counts, d, logits, x, ws);
 }
 
 __global__ __launch_bounds__(256) void lf_moe_quant_tokens(const int32_t *counts,

@@ -649,9 +649,10 @@ int32_t lunaflux_fp8_moe_launch_geometry(int32_t entry, const lf_fp8_moe_desc *d
   switch (entry) {
     // Routing and the per-token quantizers: one wave per token (row); the
     // per-128-column-group quantizers: four groups per wave.
-    // Profiles of at most 1024 assignments route and sort in one launch
-    // (lf_moe_route_sort, one 1024-thread block); the two sort steps then
-    // launch nothing (empty symbol, zero dims).
+    // Profiles of at most 1024 assignments route, sort and quantize the
+    // tokens in one launch (lf_moe_route_sort, one 1024-thread block); the
+    // two sort steps and the token quantizer then launch nothing (empty
+    // symbol, zero dims).
     case LF_FP8_MOE_ROUTE:
       if (A <= 1024) {
         name = "lf_moe_route_sort";
@@ -674,6 +675,11 @@ int32_t lunaflux_fp8_moe_launch_geometry(int32_t entry, const lf_fp8_moe_desc *d
       bx = 1024;
       break;
     case LF_FP8_MOE_QUANT_TOKENS:
+      if (A <= 1024) {  // quantized by lf_moe_route_sort
+        std::memset(dims, 0, 7 * sizeof(int32_t));
+        std::memset(symbol, 0, LF_FP8_SYMBOL_BYTES);
+        return LF_OK;
+      }
       name = "lf_moe_quant_tokens";
       gx = b128 ? group_quant_blocks(T * (d->hidden / 128)) : (T + 3) / 4;
       break;

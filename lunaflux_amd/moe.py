@@ -78,9 +78,12 @@ class BoundMoe(BoundOperation):
 def bind_moe(rt: ProjectionRuntime, counts, desc: MoeDescriptor, desc_region: KernelArgument,
              logits: KernelArgument, x: KernelArgument, wg: Fp8Weight, wu: Fp8Weight,
              wd: Fp8Weight, out: KernelArgument, max_tokens: int) -> BoundMoe:
-    """Binds one MoE expert-MLP operation to its regions: 8 launch steps, 7
-    when the gate/up epilogue runs the hidden quantizer (the geometry gives
-    that step an empty symbol)."""
+    """Binds one MoE expert-MLP operation to its regions: 8 launch steps,
+    fewer where the geometry gives a step an empty symbol (no launch): the
+    hidden quantizer when the gate/up epilogue runs it, and the two sort
+    steps and the token quantizer when the route step's kernel
+    (lf_moe_route_sort, profiles of at most 1024 assignments) does their
+    work."""
     e, h, i = desc.experts, desc.hidden, desc.inter
     mode = _abi.LF_FP8_SCALE_BLOCK128 if desc.group == 128 else _abi.LF_FP8_SCALE_PER_CHANNEL
     for w, rows, cols in ((wg, i, h), (wu, i, h), (wd, h, i)):
@@ -98,7 +101,7 @@ def bind_moe(rt: ProjectionRuntime, counts, desc: MoeDescriptor, desc_region: Ke
         return LaunchStep(rt.function(symbol), dims, KernelArguments(operands), symbol)
 
     steps = [
-        step(_abi.MOE_ROUTE, [c, desc_region, logits, wsr]),
+        step(_abi.MOE_ROUTE, [c, desc_region, logits, x, wsr]),
         step(_abi.MOE_SORT_COUNT, [c, desc_region, wsr]),
         step(_abi.MOE_SORT, [c, desc_region, wsr]),
         step(_abi.MOE_QUANT_TOKENS, [c, desc_region, x, wsr]),

@@ -290,11 +290,12 @@ def test_moe_descriptor_layout_and_geometry():
     for tokens in (512, 1):
         dims, sym = moe.launch_geometry(1, d, tokens)
         assert sym == "lf_moe_route_sort" and dims.grid == (1, 1, 1) and dims.block == (1024, 1, 1)
-        for entry in (8, 2):
+        for entry in (8, 2, 3):  # sort count, sort, token quantizer
             dims, sym = moe.launch_geometry(entry, d, tokens)
             assert sym == "" and dims.grid == (0, 0, 0) and dims.block == (0, 0, 0)
     assert moe.launch_geometry(1, d, 513)[1] == "lf_moe_route"
     assert moe.launch_geometry(2, d, 513)[1] == "lf_moe_sort"
+    assert moe.launch_geometry(3, d, 513)[1] == "lf_moe_quant_tokens"
     d5 = moe.moe_descriptor(64, 6, 1, 2048, 1408, 128)
     # block scales averaging >= 256 rows per expert: 256 x 256 tiles too
     dims, sym = moe.launch_geometry(6, d5, 4096)  # down

@@ -272,46 +272,59 @@ def test_moe_t256_row_boundaries(rt, block):
     check_output(x, weights, ex, w, out, block, f"moe t256 row boundaries block={block}", st)
 
 
-@pytest.mark.parametrize("t,e,k,mode", [(32, 64, 6, 1), (100, 8, 2, 0), (1, 8, 2, 0), (0, 8, 2, 0),
-                                        (600, 16, 4, 0), (3000, 64, 6, 1)])
-def test_moe_route_sort_one_block(rt, t, e, k, mode):
-    """lf_moe_route_sort (routing and the whole stable sort in one block, the
-    plan's route step for profiles of at most 1024 assignments, with no sort
-    launches) writes the routing outputs of lf_moe_route + lf_moe_sort_count +
-    lf_moe_sort bit for bit: top-k ids and weights, sorted assignments,
-    positions, expert offsets, 128- and 256-row tile prefixes and the list of
-    experts with rows. Launched directly at 2400 and 18000 assignments it also
+@pytest.mark.parametrize("t,e,k,mode,group", [(32, 64, 6, 1, 128), (32, 64, 6, 1, 0), (100, 8, 2, 0, 0),
+                                              (1, 8, 2, 0, 128), (0, 8, 2, 0, 0), (600, 16, 4, 0, 0),
+                                              (3000, 64, 6, 1, 128)])
+def test_moe_route_sort_one_block(rt, t, e, k, mode, group):
+    """lf_moe_route_sort (routing, the whole stable sort and the token
+    quantizer in one block: the plan's route step for profiles of at most 1024
+    assignments, with no sort or token-quantizer launches) writes the outputs
+    of lf_moe_route + lf_moe_sort_count + lf_moe_sort + lf_moe_quant_tokens bit
+    for bit: top-k ids and weights, sorted assignments, positions, expert
+    offsets, 128- and 256-row tile prefixes, the list of experts with rows,
+    the e4m3 tokens and their scales (per token, also in expert order, or per
+    128-column group). Launched directly at 2400 and 18000 assignments it also
     runs its loop over 1024-assignment chunks."""
     from lunaflux_amd import _abi, moe
     from lunaflux_amd.fp8 import _region, COUNTS_BYTES
     from lunaflux_amd.device import KernelArguments, KernelLaunchDimensions
-    rng = np.random.default_rng(970 + t + e)
+    hidden = 256
+    rng = np.random.default_rng(970 + t + e + group)
     logits = (rng.standard_normal((max(t, 1), e)) + rng.normal(0, 1.5, e)).astype(np.float32)
     logits[::7, :3] = 0.5  # ties, broken by the lower expert id
-    desc = moe.moe_descriptor(e, k, mode, 256, 256, 0)
+    x = synth.activations(rng, max(t, 1), hidden)
+    x[::5, 128:] = 0  # all-zero groups (scale 0)
+    desc = moe.moe_descriptor(e, k, mode, hidden, 256, group)
     ctx = rt.context
-    big = max(t, 1024 // k + 1)  # a profile whose plan has the three launches
+    big = max(t, 1024 // k + 1)  # a profile whose plan has the four launches
     assert moe.launch_geometry(_abi.MOE_ROUTE, desc, big)[1] == "lf_moe_route"
     if t * k <= 1024:
         assert moe.launch_geometry(_abi.MOE_ROUTE, desc, max(t, 1))[1] == "lf_moe_route_sort"
-        assert moe.launch_geometry(_abi.MOE_SORT, desc, max(t, 1))[1] == ""
-        assert moe.launch_geometry(_abi.MOE_SORT_COUNT, desc, max(t, 1))[1] == ""
-    la, da = ctx.upload(logits), ctx.upload(desc.as_bytes())
+        for entry in (_abi.MOE_SORT, _abi.MOE_SORT_COUNT, _abi.MOE_QUANT_TOKENS):
+            assert moe.launch_geometry(entry, desc, max(t, 1))[1] == ""
+    la, da, xa = ctx.upload(logits), ctx.upload(desc.as_bytes()), ctx.upload(x)
     counts = rt.step_counts(t, decode=False)
     nbytes = moe.workspace_bytes(desc, big)
-    c, dr, lr = _region(counts, COUNTS_BYTES, alignment=4), _region(da, 32, alignment=4), _region(la, alignment=256)
+    c, dr = _region(counts, COUNTS_BYTES, alignment=4), _region(da, 32, alignment=4)
+    lr, xr = _region(la, alignment=256), _region(xa, alignment=256)
 
-    def routing(ws):
+    def outputs(ws):
         lay = moe.workspace_layout(desc, t)
         a = t * k
         tiles = ws.read(np.int32, (3 * e + 3,), lay["tiles"])
         nlive = int(tiles[2 * e + 2])
-        return dict(ids=ws.read(np.int32, (a,), lay["topk_ids"]),
-                    w=ws.read(np.uint32, (a,), lay["topk_w"]),
-                    sorted=ws.read(np.int32, (a,), lay["sorted"]),
-                    pos=ws.read(np.int32, (a,), lay["pos"]),
-                    offsets=ws.read(np.int32, (e + 1,), lay["offsets"]),
-                    tiles=tiles[:2 * e + 3 + nlive])
+        gx = hidden // group if group else 1
+        out = dict(ids=ws.read(np.int32, (a,), lay["topk_ids"]),
+                   w=ws.read(np.uint32, (a,), lay["topk_w"]),
+                   sorted=ws.read(np.int32, (a,), lay["sorted"]),
+                   pos=ws.read(np.int32, (a,), lay["pos"]),
+                   offsets=ws.read(np.int32, (e + 1,), lay["offsets"]),
+                   tiles=tiles[:2 * e + 3 + nlive],
+                   xq=ws.read(np.uint8, (t * hidden,), lay["xq"]),
+                   xs=ws.read(np.uint32, (t * gx,), lay["xs"]))
+        if group == 0:
+            out["hs"] = ws.read(np.uint32, (a,), lay["hs"])  # token scales in expert order
+        return out
 
     results = []
     for fused in (False, True):
@@ -319,18 +332,21 @@ def test_moe_route_sort_one_block(rt, t, e, k, mode):
         ws.copy_from_host(np.full(nbytes, 0xA5, np.uint8))
         wr = _region(ws, alignment=256)
         if fused:
-            steps = [("lf_moe_route_sort", KernelLaunchDimensions.new((1,), (1024,)), [c, dr, lr, wr])]
+            steps = [("lf_moe_route_sort", KernelLaunchDimensions.new((1,), (1024,)), [c, dr, lr, xr, wr])]
         else:
             steps = [(moe.launch_geometry(entry, desc, big)[1], moe.launch_geometry(entry, desc, big)[0], ops)
-                     for entry, ops in ((_abi.MOE_ROUTE, [c, dr, lr, wr]), (_abi.MOE_SORT_COUNT, [c, dr, wr]),
-                                        (_abi.MOE_SORT, [c, dr, wr]))]
+                     for entry, ops in ((_abi.MOE_ROUTE, [c, dr, lr, xr, wr]), (_abi.MOE_SORT_COUNT, [c, dr, wr]),
+                                        (_abi.MOE_SORT, [c, dr, wr]), (_abi.MOE_QUANT_TOKENS, [c, dr, xr, wr]))]
         for name, dims, ops in steps:
             rt.function(name).launch_async(dims, KernelArguments(ops), rt.stream)
         rt.stream.synchronize()
-        results.append(routing(ws))
+        results.append(outputs(ws))
     for key in results[0]:
         np.testing.assert_array_equal(results[1][key], results[0][key], err_msg=key)
     if t:
         ex, _ = o.route_topk(logits[:t], k, mode)
         np.testing.assert_array_equal(results[1]["ids"].reshape(t, k), ex)
+        q, sc = o.quantize_rows(o.bf16_decode(x[:t]), group=group or None)
+        np.testing.assert_array_equal(results[1]["xq"].reshape(t, hidden), q)
+        np.testing.assert_array_equal(results[1]["xs"].view(np.float32).ravel(), np.asarray(sc, np.float32).ravel())
     assert results[1]["offsets"][-1] == t * k
