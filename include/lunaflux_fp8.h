@@ -115,8 +115,9 @@ int32_t lunaflux_fp8_unpack_weight(const uint8_t *region, int64_t region_bytes,
  *  W8A8 ("prefill"): activations quantized per token to e4m3
  *    (lf_fp8_act_quant_rows), e4m3 x e4m3 MFMA, fp32 accumulation, row scale
  *    x channel scale epilogue. _t128: 128 x 128 block tiles of 4 waves
- *    (16x16x128 f8f6f4 MFMA); _t256: 256 x 256 tiles of 8 waves
- *    (32x32x64 f8f6f4 MFMA), chosen when a launch has at least 192 of them.
+ *    (16x16x128 f8f6f4 MFMA); _t256: 256 x 256 tiles of 4 waves
+ *    (16x16x128 f8f6f4 MFMA, 128 x 128 outputs per wave), chosen when a
+ *    launch has at least 192 of them.
  *
  * Operands (all device regions, in order):
  *  lf_fp8_act_quant_rows (counts, x, w, xq)   x bf16 [M, K] -> xq; K is read

@@ -4,6 +4,7 @@
 // include/lunaflux_fp8.h; every parameter is a device region.
 #include "w8a8_v3.h"
 #include "w8a8_v4.h"
+#include "w8a8_v5.h"
 
 namespace {
 
@@ -550,6 +551,151 @@ __device__ __forceinline__ void w8a8_v4_kernel(const int32_t *counts, const uint
   }
 }
 
+// ---------------------------------------------------------------------------
+// W8A8 GEMM on the four-wave 256 x 256 loop (w8a8_v5.h, 16 x 16 x 128 MFMA
+// with the weight fragment first): 1-D grid in the XCD-aware tile order,
+// operands as w8a8_tiled_kernel (block-local weight tile s = 8 wn + j is
+// wave wn's fragment j; for gate/up, fragments 0-3 are gate tiles and 4-7
+// the up tiles of the same columns). Each lane holds one output row and four
+// consecutive columns per accumulator, so the epilogue stages a wave's
+// output through LDS with one 8-byte write per accumulator and stores whole
+// 16-byte row chunks.
+// ---------------------------------------------------------------------------
+template <int GROUP, int MODE>
+__device__ __forceinline__ void w8a8_v5_kernel(const int32_t *counts, const uint8_t *xq, const uint8_t *w0,
+                                               const uint8_t *w1, const uint8_t *w2, uint16_t *y) {
+  using T = w8a8v5::Tile;
+  constexpr int BM = 256, BN = 256;
+  __shared__ __attribute__((aligned(1024))) uint8_t smem[T::kSmem];
+  const WeightHeader &h0 = header_of(w0);
+  if (!dense_regions_ok<MODE>(w0, w1, w2)) return;
+  const int K = static_cast<int>(h0.columns);
+  const int KT = K >> 7;
+  const int M = live_rows(counts, 1 << 30);
+  const int tq = static_cast<int>(h0.rows) >> 4;
+  const int tk = MODE == 1 ? static_cast<int>(header_of(w1).rows) >> 4 : 0;
+  const int ld = MODE == 1 ? static_cast<int>(h0.rows + header_of(w1).rows + header_of(w2).rows)
+                           : static_cast<int>(h0.rows);
+  const int gx = MODE == 2 ? ld / (BN / 2) : ld / BN;
+  int bx, by;
+  if (!w8a8v3::tile_of_block(gx, (M + BM - 1) / BM, GROUP, bx, by)) return;
+  const int m0 = by * BM;
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int wm = wave / T::kWgn, wn = wave % T::kWgn;
+
+  // Weight tile of block-local tile s: region, tile index inside it, output
+  // column of its first column.
+  auto slot = [&](int s, const uint8_t *&region, int &t, int &ocol) {
+    if (MODE == 2) {
+      const int sw = s / T::kFN, f = s % T::kFN;
+      const bool up = f >= T::kFN / 2;
+      const int col = bx * (BN / 2) + sw * (T::kWaveN / 2) + 16 * (up ? f - T::kFN / 2 : f);
+      region = up ? w1 : w0;
+      t = col >> 4;
+      ocol = col;
+    } else {
+      t = bx * (BN / 16) + s;
+      ocol = t * 16;
+      region = w0;
+      if (MODE == 1) {
+        if (t >= tq + tk) {
+          region = w2;
+          t -= tq + tk;
+        } else if (t >= tq) {
+          region = w1;
+          t -= tq;
+        }
+      }
+    }
+  };
+
+  // Row scales of the tile, one per thread, loaded before the main loop and
+  // parked in LDS after it for the epilogue.
+  const float *ascale = reinterpret_cast<const float *>(xq + align256(static_cast<uint64_t>(M) * K));
+  __shared__ float sa_tile[BM];
+  float sa_mine;
+  {
+    const int m = m0 + static_cast<int>(threadIdx.x);
+    sa_mine = ascale[m < M ? m : M - 1];
+  }
+  w8a8v3::Plan<T> plan;
+#pragma unroll
+  for (int q = 0; q < T::kAIns; ++q) {
+    const int tr = w8a8v3::a_load_row<T>(wave, q, lane);
+    const int row = m0 + tr < M ? m0 + tr : M - 1;
+    plan.a[q] = xq + static_cast<uint64_t>(row) * K + w8a8v3::a_load_chunk(tr, lane) * 16;
+  }
+#pragma unroll
+  for (int q = 0; q < T::kBIns; ++q) {
+    const int half = w8a8v3::b_load_half<T>(wave, q);
+    const uint8_t *region;
+    int t, ocol;
+    slot(half >> 1, region, t, ocol);
+    plan.b[q] = expert_tiles(region, 0) + static_cast<uint64_t>(t) * KT * kTileBytes +
+                (half & 1) * 1024 + lane * 16;
+  }
+  f32x4 acc[T::kFM][T::kFN];
+  w8a8v5::mainloop<T, true>(plan, KT, smem, acc);
+
+  sa_tile[threadIdx.x] = sa_mine;
+  // Column scales: four consecutive columns of each fragment per lane.
+  float4 swv[T::kFN];
+  int ocol[T::kFN];
+#pragma unroll
+  for (int j = 0; j < T::kFN; ++j) {
+    const uint8_t *region;
+    int t;
+    slot(wn * T::kFN + j, region, t, ocol[j]);
+    swv[j] = *reinterpret_cast<const float4 *>(expert_scales(region, 0) + t * 16 + 4 * (lane >> 4));
+  }
+  // A wave's output block is rows m0 + wm 128 + [0, 128) and kCols
+  // consecutive columns from its first fragment's column (gate/up: 64
+  // h-columns), staged kRows rows at a time.
+  constexpr int kCols = MODE == 2 ? T::kWaveN / 2 : T::kWaveN;
+  constexpr int kRows = MODE == 2 ? 128 : 64;
+  using Stage = w8a8v4::StageTile<uint16_t, kRows, kCols>;
+  static_assert(Stage::kBytes * T::kWaves <= T::kSmem, "staging fits the stage ring");
+  const int col0 = __builtin_amdgcn_readfirstlane(ocol[0]);
+  w8a8v4::epilogue_barrier();
+  const Stage st{reinterpret_cast<uint16_t *>(smem + wave * Stage::kBytes)};
+  constexpr int kPassRows = kRows / 16;
+#pragma unroll
+  for (int p = 0; p < T::kFM / kPassRows; ++p) {
+#pragma unroll
+    for (int ii = 0; ii < kPassRows; ++ii) {
+      const int i = p * kPassRows + ii;
+      const int row = w8a8v5::acc_row(ii, lane);
+      const float sa = sa_tile[wm * T::kWaveM + w8a8v5::acc_row(i, lane)];
+      if (MODE == 2) {
+#pragma unroll
+        for (int j = 0; j < T::kFN / 2; ++j) {
+          uint32_t b[4];
+#pragma unroll
+          for (int q = 0; q < 4; ++q) {
+            const float gv = acc[i][j][q] * sa * swv[j][q];
+            const float uv = acc[i][j + T::kFN / 2][q] * sa * swv[j + T::kFN / 2][q];
+            b[q] = f32_to_bf16(silu_mul(gv, uv));
+          }
+          st.put4(row, ocol[j] - col0 + 4 * (lane >> 4), b);
+        }
+      } else {
+#pragma unroll
+        for (int j = 0; j < T::kFN; ++j) {
+          uint32_t b[4];
+#pragma unroll
+          for (int q = 0; q < 4; ++q) b[q] = f32_to_bf16(acc[i][j][q] * sa * swv[j][q]);
+          st.put4(row, ocol[j] - col0 + 4 * (lane >> 4), b);
+        }
+      }
+    }
+    const int mw = m0 + wm * T::kWaveM + kRows * p;
+    st.flush(lane, [&](int row) -> uint16_t * {
+      return mw + row < M ? y + static_cast<uint64_t>(mw + row) * ld + col0 : nullptr;
+    });
+  }
+}
+
 }  // namespace
 
 extern "C" {
@@ -586,10 +732,31 @@ extern "C" {
     w8a8_v4_kernel<w8a8v4::Tile<BM, BN, NS, WGM, WGN>, GROUP, 2>(counts, xq, wg, wu, wu, h);    \
   }
 
-// Production tiles: 256 x 256 (8 waves, 4-stage half-step ring) wherever a
-// launch has at least one tile per CU, 128 x 128 (4 waves, two blocks per
-// CU) otherwise. lunaflux_fp8_launch_geometry picks between them.
-LF_W8A8_V4_ENTRIES(t256, 256, 256, 4, 4, 2, 4)
+#define LF_W8A8_V5_ENTRIES(NAME, GROUP)                                                        \
+  __global__ __launch_bounds__(256) void lf_fp8_w8a8_dense_##NAME(                                \
+      const int32_t *counts, const uint8_t *xq, const uint8_t *w, uint16_t *y) {                  \
+    w8a8_v5_kernel<GROUP, 0>(counts, xq, w, w, w, y);                                             \
+  }                                                                                               \
+  __global__ __launch_bounds__(256) void lf_fp8_w8a8_qkv_##NAME(                                  \
+      const int32_t *counts, const uint8_t *xq, const uint8_t *wq, const uint8_t *wk,             \
+      const uint8_t *wv, uint16_t *y) {                                                           \
+    w8a8_v5_kernel<GROUP, 1>(counts, xq, wq, wk, wv, y);                                          \
+  }                                                                                               \
+  __global__ __launch_bounds__(256) void lf_fp8_w8a8_gate_up_##NAME(                              \
+      const int32_t *counts, const uint8_t *xq, const uint8_t *wg, const uint8_t *wu,             \
+      uint16_t *h) {                                                                              \
+    w8a8_v5_kernel<GROUP, 2>(counts, xq, wg, wu, wu, h);                                          \
+  }
+
+// Production tiles (lunaflux_fp8_launch_geometry picks): 256 x 256 on four
+// waves (_t256) wherever a launch has at least one tile per CU; 256 x 256 on
+// eight waves with the 4-stage half-step ring (_t256w8) from three quarters
+// of a tile per CU up to that, where a CU runs a single tile and two waves
+// per SIMD hide its load latency better (QKV at M = 2048, 192 tiles: 52.3
+// against 57.5 us; from 512 tiles the four-wave form is 3-7 % faster);
+// 128 x 128 (4 waves, two blocks per CU) below.
+LF_W8A8_V5_ENTRIES(t256, 4)
+LF_W8A8_V4_ENTRIES(t256w8, 256, 256, 4, 4, 2, 4)
 LF_W8A8_TILED_ENTRIES(t128, 128, 128, 2, 2, 2, 4)
 
 __global__ __launch_bounds__(256) void lf_fp8_act_quant_rows(const int32_t *counts,

@@ -498,21 +498,24 @@ static int32_t launch_geometry(int32_t entry, int64_t n, int64_t k, int64_t nq, 
       const bool gate_up = entry == LF_FP8_ENTRY_W8A8_GATE_UP;
       const int64_t cols256 = gate_up ? 128 : 256, cols128 = gate_up ? 64 : 128;
       if (n % cols128 != 0) return LF_INVALID_ARGUMENT;
-      // 256 x 256 tiles (512 threads) when the launch has at least 192 of
-      // them (three quarters of a tile per CU of the 256 on an MI355X) and
-      // the columns divide; 128 x 128 tiles (256 threads, two blocks per CU)
+      // 256 x 256 tiles when the launch has at least 192 of them (three
+      // quarters of a tile per CU of the 256 on an MI355X) and the columns
+      // divide: on 4 waves (_t256) from 256 tiles, on 8 waves (_t256w8, a
+      // single tile per CU, whose load latency two waves per SIMD hide
+      // better) below that; 128 x 128 tiles (4 waves, two blocks per CU)
       // otherwise. Measured at M = 2048: QKV (192 large tiles) 71.2 -> 59.5
       // us on the large tiles; o and down (128) were 30-40 % slower on them.
       const int64_t tiles256 = (n % cols256 == 0) ? ((max_tokens + 255) / 256) * (n / cols256) : 0;
-      const bool big = tiles256 >= 192;
+      const bool big = tiles256 >= 192, four_wave = tiles256 >= 256;
       const int64_t tiles = big ? tiles256 : ((max_tokens + 127) / 128) * (n / cols128);
       if (tiles > INT32_MAX) return LF_INVALID_ARGUMENT;
       const char *op = entry == LF_FP8_ENTRY_W8A8_DENSE ? "dense" : entry == LF_FP8_ENTRY_W8A8_QKV ? "qkv" : "gate_up";
-      std::snprintf(buffer, sizeof(buffer), "lf_fp8_w8a8_%s_%s", op, big ? "t256" : "t128");
+      std::snprintf(buffer, sizeof(buffer), "lf_fp8_w8a8_%s_%s", op,
+                    !big ? "t128" : four_wave ? "t256" : "t256w8");
       name = buffer;
       gx = static_cast<int32_t>(tiles);
       gy = 1;
-      bx = big ? 512 : 256;
+      bx = big && !four_wave ? 512 : 256;
       break;
     }
     default:

@@ -187,42 +187,44 @@ def test_w8a16_split_k_repeated_launches(rt, family_op):
     assert np.array_equal(outs[0], outs[1]) and np.array_equal(outs[1], outs[2])
 
 
+@pytest.mark.parametrize("form,max_tokens", [("_t256", 4096), ("_t256w8", 3072)])
 @pytest.mark.parametrize("op,m,k", [
-    ("dense", 300, 128), ("dense", 1, 256), ("dense", 511, 384), ("qkv", 513, 128),
-    ("qkv", 256, 640), ("gate_up", 257, 256), ("gate_up", 40, 128),
+    ("dense", 300, 128), ("dense", 1, 256), ("dense", 511, 384), ("dense", 257, 1408),
+    ("qkv", 513, 128), ("qkv", 256, 640), ("gate_up", 257, 256), ("gate_up", 40, 128),
 ])
-def test_w8a8_large_tile_edges(rt, op, m, k):
-    """The 256 x 256 tile (chosen for max_query_tokens = 4096 at these
-    widths): ragged live rows, the shortest K loops (K = 128, 256: the
-    4-stage ring's prologue and tail cases), and qkv region boundaries that
-    fall inside a block (Nq = 2176, Nk = Nv = 960)."""
+def test_w8a8_large_tile_edges(rt, op, m, k, form, max_tokens):
+    """The 256 x 256 tiles at these widths: the four-wave form for
+    max_query_tokens = 4096 (256 tiles) and the eight-wave form for 3072
+    (192 tiles). Ragged live rows, the shortest K loops (K = 128: one k-tile,
+    K = 256: the two-stage prologue with nothing left to load; the eight-wave
+    ring's prologue and tail cases), an odd k-tile count (K = 1408), and qkv
+    region boundaries that fall inside a block (Nq = 2176, Nk = Nv = 960)."""
     from lunaflux_amd import _abi, fp8
     rng = np.random.default_rng(7000 + m + k)
-    max_tokens = 4096
     x = synth.activations(rng, m, k)
     xr = x_ref(x, "w8a8")
     if op == "dense":
         n = 4096
-        assert fp8.launch_geometry(_abi.ENTRY_W8A8_DENSE, n, k, max_tokens)[1].endswith("_t256")
+        assert fp8.launch_geometry(_abi.ENTRY_W8A8_DENSE, n, k, max_tokens)[1].endswith(form)
         q, s, w = make_weight(rt, rng, n, k)
         y = rt.dense_projection(x, w, "w8a8", max_tokens=max_tokens)
-        check_projection(y, xr, deq(q, s), f"t256 dense m={m} k={k}")
+        check_projection(y, xr, deq(q, s), f"{form} dense m={m} k={k}")
     elif op == "qkv":
         ns = (2176, 960, 960)
-        assert fp8.launch_geometry(_abi.ENTRY_W8A8_QKV, sum(ns), k, max_tokens)[1].endswith("_t256")
+        assert fp8.launch_geometry(_abi.ENTRY_W8A8_QKV, sum(ns), k, max_tokens)[1].endswith(form)
         ws = [make_weight(rt, rng, n, k) for n in ns]
         y = rt.qkv_projection(x, *(w for _, _, w in ws), family="w8a8", max_tokens=max_tokens)
         ref = o.qkv_projection(xr, *(deq(q, s) for q, s, _ in ws))
         wall = np.concatenate([deq(q, s) for q, s, _ in ws])
-        parity(y, ref, k=k, s_abs=abs_sum(xr, wall), label=f"t256 qkv m={m} k={k}")
+        parity(y, ref, k=k, s_abs=abs_sum(xr, wall), label=f"{form} qkv m={m} k={k}")
     else:
         inter = 2048
-        assert fp8.launch_geometry(_abi.ENTRY_W8A8_GATE_UP, inter, k, max_tokens)[1].endswith("_t256")
+        assert fp8.launch_geometry(_abi.ENTRY_W8A8_GATE_UP, inter, k, max_tokens)[1].endswith(form)
         qg, sg, wg = make_weight(rt, rng, inter, k)
         qu, su, wu = make_weight(rt, rng, inter, k)
         h = rt.gate_up_swiglu(x, wg, wu, family="w8a8", max_tokens=max_tokens)
         ref = o.silu_mul_array(o.dense_projection(xr, deq(qg, sg)), o.dense_projection(xr, deq(qu, su)))
-        parity(h, ref, label=f"t256 gate_up m={m} k={k}")
+        parity(h, ref, label=f"{form} gate_up m={m} k={k}")
 
 
 @pytest.mark.parametrize("family,m,max_tokens", [("w8a16", 3, 16), ("w8a16", 32, 32),
