@@ -139,21 +139,20 @@ __device__ __forceinline__ void mainloop(const Plan<T> &plan, int KT, uint8_t *s
     }
   };
   const uint32_t smem_base = __builtin_amdgcn_readfirstlane(w8a8v3::lds_offset_of(smem));
-  auto issue = [&](int s) {
+  // Load q of stage s: this wave's A instructions first, then its B ones.
+  auto issue_one = [&](int s, int q) {
     const int kt = s >> 1, h = s & 1;
     const uint32_t a = smem_base + (s % NS) * T::kStage;
-    const uint32_t b = a + T::kABytes;
-    if (a_on) {
-#pragma unroll
-      for (int i = 0; i < T::kAIns; ++i) {
-        w8a8v3::dma16(plan.a[i] + kt * 128 + h * 16, a + (wave * T::kAIns + i) * 1024);
-      }
+    if (q < T::kAIns) {
+      if (a_on) w8a8v3::dma16(plan.a[q] + kt * 128 + h * 16, a + (wave * T::kAIns + q) * 1024);
+    } else {
+      w8a8v3::dma16(plan.b[q - T::kAIns] + kt * kTileBytes + h * 1024,
+                    a + T::kABytes + b_load_tile<T>(wave, q - T::kAIns) * 1024);
     }
+  };
+  auto issue = [&](int s) {
 #pragma unroll
-    for (int i = 0; i < T::kBIns; ++i) {
-      w8a8v3::dma16(plan.b[i] + kt * kTileBytes + h * 1024,
-                    b + b_load_tile<T>(wave, i) * 1024);
-    }
+    for (int q = 0; q < T::kIns; ++q) issue_one(s, q);
   };
 
   // LDS byte offsets of this lane's fragment reads inside a stage: A block i
@@ -223,12 +222,21 @@ __device__ __forceinline__ void mainloop(const Plan<T> &plan, int KT, uint8_t *s
       rescale.begin(s >> 1);
       rescale.apply(0, acc);
     }
+    // Loads of stage s + NS - 1 issued after group o: q in [o kIns / kOuter,
+    // (o + 1) kIns / kOuter), so they reach the vector memory path spread
+    // over the half-step instead of in one run.
+    auto issue_after = [&](int o) {
+      if constexpr (kIssue) {
+#pragma unroll
+        for (int q = o * T::kIns / kOuter; q < (o + 1) * T::kIns / kOuter; ++q) issue_one(s + NS - 1, q);
+      }
+    };
     mfma_group(cur, 0);
     __builtin_amdgcn_sched_barrier(0);
     if constexpr (kWait >= 0) {
       wait_stages(std::integral_constant<int, kWait>{});
       block_barrier();
-      if constexpr (kIssue) issue(s + NS - 1);
+      issue_after(0);
       read_inner(nxt, st);
       read_outer(outer[0], 0, st);
     }
@@ -238,7 +246,10 @@ __device__ __forceinline__ void mainloop(const Plan<T> &plan, int KT, uint8_t *s
       if constexpr (kEven) rescale.apply(o, acc);
       mfma_group(cur, o);
       __builtin_amdgcn_sched_barrier(0);
-      if constexpr (kWait >= 0) read_outer(outer[o], o, st);
+      if constexpr (kWait >= 0) {
+        read_outer(outer[o], o, st);
+        issue_after(o);
+      }
       __builtin_amdgcn_sched_barrier(0);
     }
   };
