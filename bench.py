@@ -443,15 +443,21 @@ def pmc_pass():
     log(f"pmc pass done (gate_up x10, copy {n} bytes x3)")
 
 
+# (M, K, N) of the dense GEMMs pmc_pass_prefill launches, in order.
+PREFILL_PASS_SHAPES = ((8192, INTER, HIDDEN), (8192, HIDDEN, HIDDEN), (3072, HIDDEN, HIDDEN),
+                       (2048, HIDDEN, HIDDEN))
+
+
 def pmc_pass_prefill():
     """Short run for the MFMA-utilisation counter pass: the prefill down GEMM
-    (K=14336 -> N=4096) at M=8192 (256 x 256 tiles) and the o GEMM at M=2048
-    (128 x 128 tiles), 5 launches each after one act-quant."""
+    (K=14336 -> N=4096) and o GEMM at M=8192 (256 x 256 tiles, four waves),
+    the o GEMM at M=3072 (192 tiles of 256 x 256: the eight-wave form) and at
+    M=2048 (128 x 128 tiles), 5 launches each after one act-quant."""
     from lunaflux_amd import fp8, synth
     from lunaflux_amd.fp8 import ProjectionRuntime, _region
     rt = ProjectionRuntime(0)
     rng = np.random.default_rng(6)
-    for m, k, n in ((8192, INTER, HIDDEN), (2048, HIDDEN, HIDDEN)):
+    for m, k, n in PREFILL_PASS_SHAPES:
         w = rt.weight_from_region(fp8.pack_weight(*synth.weight(rng, n, k)))
         x = rt.context.upload(synth.activations(rng, m, k))
         y = rt.context.allocate(m * n * 2)
@@ -614,6 +620,48 @@ def summarize_traffic(fetch_csv, write_csv, kernel):
     }
 
 
+def summarize_mfma(counter_csv, trace_csv):
+    """Markdown table of the --pmc-pass-prefill MFMA counter pass (counter CSV
+    of SQ_VALU_MFMA_BUSY_CYCLES, SQ_INSTS_VALU_MFMA_MOPS_F8, SQ_INSTS_VALU_MFMA_F8,
+    SQ_INSTS_VALU_MFMA_F6F4, GRBM_GUI_ACTIVE) with durations from a kernel
+    trace of the same pass: per shape the mean over its 5 GEMM launches. MFMA
+    busy = busy cycles / (GRBM_GUI_ACTIVE / 8 XCDs x 1024 SIMDs); clock =
+    GRBM_GUI_ACTIVE / 8 / duration."""
+    import csv
+    gemm = lambda name: name.startswith("lf_fp8_w8a8_dense")
+    disp = {}
+    for r in csv.DictReader(open(counter_csv)):
+        if gemm(r["Kernel_Name"]):
+            d = disp.setdefault(int(r["Dispatch_Id"]), {"name": r["Kernel_Name"], "wg": int(r["Workgroup_Size"])})
+            d[r["Counter_Name"]] = float(r["Counter_Value"])
+    ids = sorted(disp)
+    trace = [r for r in csv.DictReader(open(trace_csv)) if gemm(r["Kernel_Name"])]
+    shapes = PREFILL_PASS_SHAPES
+    if len(ids) != 5 * len(shapes) or len(trace) != 5 * len(shapes):
+        raise SystemExit(f"expected {5 * len(shapes)} GEMM dispatches, got {len(ids)} / {len(trace)}")
+    lines = ["| Kernel | Shape | Threads | MFMA instructions | MFMA flops (MOPS_F8 x 512) | MFMA busy cycles "
+             "| GRBM_GUI_ACTIVE | Duration (trace) | Clock | MFMA busy | Achieved |",
+             "|---|---|---|---|---|---|---|---|---|---|---|"]
+    for s, (m, k, n) in enumerate(shapes):
+        ds = [disp[i] for i in ids[5 * s:5 * s + 5]]
+        ts = trace[5 * s:5 * s + 5]
+        name = ds[0]["name"]
+        if any(d["name"] != name for d in ds) or any(t["Kernel_Name"] != name for t in ts):
+            raise SystemExit(f"dispatch order does not match the pass at shape {s}")
+        mean = lambda c: sum(d[c] for d in ds) / len(ds)
+        dur = sum(int(t["End_Timestamp"]) - int(t["Start_Timestamp"]) for t in ts) / len(ts) / 1e3
+        ins = mean("SQ_INSTS_VALU_MFMA_F8") + mean("SQ_INSTS_VALU_MFMA_F6F4")
+        mops = mean("SQ_INSTS_VALU_MFMA_MOPS_F8") * 512
+        busy, gui = mean("SQ_VALU_MFMA_BUSY_CYCLES"), mean("GRBM_GUI_ACTIVE")
+        flops = 2 * m * n * k
+        op = "down" if k == INTER else "o"
+        lines.append(f"| {name} | {op}, M={m}, K={k}, N={n} | {ds[0]['wg']} | {ins:.0f} | {mops:.4g} "
+                     f"(= 2MNK {flops:.4g}) | {busy:.4g} | {gui:.4g} | {dur:.1f} us | "
+                     f"{gui / 8 / (dur * 1e-6) / 1e9:.2f} GHz | {100 * busy / (gui / 8 * 1024):.0f} % | "
+                     f"{flops / dur / 1e6:.0f} TFLOP/s |")
+    return "\n".join(lines)
+
+
 def summarize_trace(trace_csv, gap=32):
     """Markdown table of a rocprofv3 kernel-trace CSV: one row per (kernel,
     blocks, threads) with launches and average / min / max duration in us,
@@ -662,12 +710,17 @@ def main():
     ap.add_argument("--summarize-counters", nargs="+", metavar="CSV",
                     help="per-kernel markdown table of --pmc-pass-all counter (and kernel-trace) "
                          "CSVs (no GPU needed)")
+    ap.add_argument("--summarize-mfma", nargs=2, metavar=("COUNTER_CSV", "KERNEL_TRACE_CSV"),
+                    help="markdown table of the --pmc-pass-prefill MFMA counter pass (no GPU needed)")
     ap.add_argument("--summarize-trace", metavar="KERNEL_TRACE_CSV",
                     help="print a per-kernel markdown summary of a rocprofv3 kernel-trace CSV "
                          "(no GPU needed)")
     args = ap.parse_args()
     if args.summarize_trace:
         print(summarize_trace(args.summarize_trace))
+        return
+    if args.summarize_mfma:
+        print(summarize_mfma(*args.summarize_mfma))
         return
     if args.summarize_counters:
         print(summarize_counters(args.summarize_counters))
