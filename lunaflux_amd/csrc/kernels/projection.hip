@@ -552,20 +552,20 @@ __device__ __forceinline__ void w8a8_v4_kernel(const int32_t *counts, const uint
 }
 
 // ---------------------------------------------------------------------------
-// W8A8 GEMM on the four-wave 256 x 256 loop (w8a8_v5.h, 16 x 16 x 128 MFMA
-// with the weight fragment first): 1-D grid in the XCD-aware tile order,
-// operands as w8a8_tiled_kernel (block-local weight tile s = 8 wn + j is
-// wave wn's fragment j; for gate/up, fragments 0-3 are gate tiles and 4-7
-// the up tiles of the same columns). Each lane holds one output row and four
+// W8A8 GEMM on the four-wave 256-row loop (w8a8_v5.h, 16 x 16 x 128 MFMA
+// with the weight fragment first; T: 256 x 256 or 256 x 128 tiles): 1-D grid
+// in the XCD-aware tile order, operands as w8a8_tiled_kernel (block-local
+// weight tile s = kFN wn + j is wave wn's fragment j; for gate/up, the first
+// kFN / 2 fragments are gate tiles and the rest the up tiles of the same
+// columns). Each lane holds one output row and four
 // consecutive columns per accumulator, so the epilogue stages a wave's
 // output through LDS with one 8-byte write per accumulator and stores whole
 // 16-byte row chunks.
 // ---------------------------------------------------------------------------
-template <int GROUP, int MODE>
+template <class T, int GROUP, int MODE>
 __device__ __forceinline__ void w8a8_v5_kernel(const int32_t *counts, const uint8_t *xq, const uint8_t *w0,
                                                const uint8_t *w1, const uint8_t *w2, uint16_t *y) {
-  using T = w8a8v5::Tile;
-  constexpr int BM = 256, BN = 256;
+  constexpr int BM = 256, BN = T::kWaveN * T::kWgn;
   __shared__ __attribute__((aligned(1024))) uint8_t smem[T::kSmem];
   const WeightHeader &h0 = header_of(w0);
   if (!dense_regions_ok<MODE>(w0, w1, w2)) return;
@@ -653,7 +653,7 @@ __device__ __forceinline__ void w8a8_v5_kernel(const int32_t *counts, const uint
   // consecutive columns from its first fragment's column (gate/up: 64
   // h-columns), staged kRows rows at a time.
   constexpr int kCols = MODE == 2 ? T::kWaveN / 2 : T::kWaveN;
-  constexpr int kRows = MODE == 2 ? 128 : 64;
+  constexpr int kRows = kCols <= 64 ? 128 : 64;
   using Stage = w8a8v4::StageTile<uint16_t, kRows, kCols>;
   static_assert(Stage::kBytes * T::kWaves <= T::kSmem, "staging fits the stage ring");
   const int col0 = __builtin_amdgcn_readfirstlane(ocol[0]);
@@ -732,20 +732,20 @@ extern "C" {
     w8a8_v4_kernel<w8a8v4::Tile<BM, BN, NS, WGM, WGN>, GROUP, 2>(counts, xq, wg, wu, wu, h);    \
   }
 
-#define LF_W8A8_V5_ENTRIES(NAME, GROUP)                                                        \
+#define LF_W8A8_V5_ENTRIES(NAME, TILE, GROUP)                                                  \
   __global__ __launch_bounds__(256) void lf_fp8_w8a8_dense_##NAME(                                \
       const int32_t *counts, const uint8_t *xq, const uint8_t *w, uint16_t *y) {                  \
-    w8a8_v5_kernel<GROUP, 0>(counts, xq, w, w, w, y);                                             \
+    w8a8_v5_kernel<TILE, GROUP, 0>(counts, xq, w, w, w, y);                                       \
   }                                                                                               \
   __global__ __launch_bounds__(256) void lf_fp8_w8a8_qkv_##NAME(                                  \
       const int32_t *counts, const uint8_t *xq, const uint8_t *wq, const uint8_t *wk,             \
       const uint8_t *wv, uint16_t *y) {                                                           \
-    w8a8_v5_kernel<GROUP, 1>(counts, xq, wq, wk, wv, y);                                          \
+    w8a8_v5_kernel<TILE, GROUP, 1>(counts, xq, wq, wk, wv, y);                                    \
   }                                                                                               \
   __global__ __launch_bounds__(256) void lf_fp8_w8a8_gate_up_##NAME(                              \
       const int32_t *counts, const uint8_t *xq, const uint8_t *wg, const uint8_t *wu,             \
       uint16_t *h) {                                                                              \
-    w8a8_v5_kernel<GROUP, 2>(counts, xq, wg, wu, wu, h);                                          \
+    w8a8_v5_kernel<TILE, GROUP, 2>(counts, xq, wg, wu, wu, h);                                    \
   }
 
 // Production tiles (lunaflux_fp8_launch_geometry picks): 256 x 256 on four
@@ -754,8 +754,13 @@ extern "C" {
 // of a tile per CU up to that, where a CU runs a single tile and two waves
 // per SIMD hide its load latency better (QKV at M = 2048, 192 tiles: 52.3
 // against 57.5 us; from 512 tiles the four-wave form is 3-7 % faster);
-// 128 x 128 (4 waves, two blocks per CU) below.
-LF_W8A8_V5_ENTRIES(t256, 4)
+// below, for QKV / dense, 256 x 128 on four waves (_t256x128, three stages)
+// where that gives 128-256 tiles (o and down at M = 2048: 35.3 / 108.5
+// against 38.9 / 121.0 us on 128 x 128; QKV at M = 1024 34.0 against 38.5;
+// gate/up ran 10-18 % slower on it than on 256 x 256); 128 x 128 (4 waves,
+// two blocks per CU) otherwise.
+LF_W8A8_V5_ENTRIES(t256, w8a8v5::Tile, 4)
+LF_W8A8_V5_ENTRIES(t256x128, w8a8v5::TileN128, 4)
 LF_W8A8_V4_ENTRIES(t256w8, 256, 256, 4, 4, 2, 4)
 LF_W8A8_TILED_ENTRIES(t128, 128, 128, 2, 2, 2, 4)
 

@@ -502,16 +502,21 @@ static int32_t launch_geometry(int32_t entry, int64_t n, int64_t k, int64_t nq, 
       // quarters of a tile per CU of the 256 on an MI355X) and the columns
       // divide: on 4 waves (_t256) from 256 tiles, on 8 waves (_t256w8, a
       // single tile per CU, whose load latency two waves per SIMD hide
-      // better) below that; 128 x 128 tiles (4 waves, two blocks per CU)
-      // otherwise. Measured at M = 2048: QKV (192 large tiles) 71.2 -> 59.5
-      // us on the large tiles; o and down (128) were 30-40 % slower on them.
+      // better) below that. Fewer: QKV and dense on 256 x 128 tiles (4
+      // waves, _t256x128) when those number 128-256 (at most one per CU);
+      // otherwise 128 x 128 tiles (4 waves, two blocks per CU). Measured at
+      // M = 2048: QKV (192 large tiles) 71.2 -> 59.5 us on the large tiles;
+      // o and down (128) were 30-40 % slower on them and 9-10 % faster on
+      // 256 x 128 than on 128 x 128.
       const int64_t tiles256 = (n % cols256 == 0) ? ((max_tokens + 255) / 256) * (n / cols256) : 0;
+      const int64_t tiles256x128 = !gate_up ? ((max_tokens + 255) / 256) * (n / cols128) : 0;
       const bool big = tiles256 >= 192, four_wave = tiles256 >= 256;
-      const int64_t tiles = big ? tiles256 : ((max_tokens + 127) / 128) * (n / cols128);
+      const bool wide128 = !big && tiles256x128 >= 128 && tiles256x128 <= 256;
+      const int64_t tiles = big ? tiles256 : wide128 ? tiles256x128 : ((max_tokens + 127) / 128) * (n / cols128);
       if (tiles > INT32_MAX) return LF_INVALID_ARGUMENT;
       const char *op = entry == LF_FP8_ENTRY_W8A8_DENSE ? "dense" : entry == LF_FP8_ENTRY_W8A8_QKV ? "qkv" : "gate_up";
       std::snprintf(buffer, sizeof(buffer), "lf_fp8_w8a8_%s_%s", op,
-                    !big ? "t128" : four_wave ? "t256" : "t256w8");
+                    big ? (four_wave ? "t256" : "t256w8") : wide128 ? "t256x128" : "t128");
       name = buffer;
       gx = static_cast<int32_t>(tiles);
       gy = 1;

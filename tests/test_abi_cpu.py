@@ -37,7 +37,7 @@ def test_library_exports_every_declared_symbol():
 def test_code_object_has_every_entry_point():
     image = _abi.code_object_bytes()
     for symbol in ["lf_fp8_act_quant_rows"] + [f"lf_fp8_w8a8_{op}_{t}" for op in ("dense", "qkv", "gate_up")
-                                               for t in ("t128", "t256", "t256w8")] + ["lf_moe_route", "lf_moe_route_sort", "lf_moe_sort_count", "lf_moe_sort", "lf_moe_quant_tokens",
+                                               for t in ("t128", "t256", "t256w8", "t256x128")] + ["lf_moe_route", "lf_moe_route_sort", "lf_moe_sort_count", "lf_moe_sort", "lf_moe_quant_tokens",
                    "lf_moe_gate_up", "lf_moe_gate_up_b128", "lf_moe_quant_hidden", "lf_moe_down",
                    "lf_moe_down_b128", "lf_moe_combine", "lf_moe_gate_up_gemv", "lf_moe_down_gemv",
                    "lf_moe_gate_up_t256_b128", "lf_moe_down_t256_b128"] + [f"lf_fp8_w8a16_{op}_m{m}" for op in ("dense", "qkv", "gate_up")
@@ -184,8 +184,9 @@ def test_launch_geometry():
     with pytest.raises(fp8.DeviceError):
         fp8.w8a16_workspace_bytes(_abi.ENTRY_W8A8_DENSE, 4096, 4096, 16)
     # W8A8: 256 x 256 tiles (1-D grid) from 192 of them (3/4 of a tile per
-    # CU), on 8 waves below 256 tiles and on 4 waves from there; 128 x 128
-    # tiles (4 waves) below 192 or when N does not divide.
+    # CU), on 8 waves below 256 tiles and on 4 waves from there; below 192,
+    # QKV and dense on 256 x 128 tiles when they number 128-256, else 128 x
+    # 128 tiles (4 waves), as when N does not divide.
     dims, sym = fp8.launch_geometry(_abi.ENTRY_W8A8_QKV, 6144, 4096, 2048)
     assert sym == "lf_fp8_w8a8_qkv_t256w8" and dims.grid == (8 * 24, 1, 1) and dims.block == (512, 1, 1)
     dims, sym = fp8.launch_geometry(_abi.ENTRY_W8A8_QKV, 6144, 4096, 2560)
@@ -193,11 +194,19 @@ def test_launch_geometry():
     dims, sym = fp8.launch_geometry(_abi.ENTRY_W8A8_QKV, 8192, 4096, 2048)
     assert sym == "lf_fp8_w8a8_qkv_t256" and dims.grid == (8 * 32, 1, 1) and dims.block == (256, 1, 1)
     dims, sym = fp8.launch_geometry(_abi.ENTRY_W8A8_DENSE, 4096, 4096, 2048)
-    assert sym == "lf_fp8_w8a8_dense_t128" and dims.grid == (16 * 32, 1, 1)
+    assert sym == "lf_fp8_w8a8_dense_t256x128" and dims.grid == (8 * 32, 1, 1) and dims.block == (256, 1, 1)
+    dims, sym = fp8.launch_geometry(_abi.ENTRY_W8A8_QKV, 6144, 4096, 1024)
+    assert sym == "lf_fp8_w8a8_qkv_t256x128" and dims.grid == (4 * 48, 1, 1)
+    dims, sym = fp8.launch_geometry(_abi.ENTRY_W8A8_QKV, 6144, 4096, 1536)   # 288 such tiles
+    assert sym == "lf_fp8_w8a8_qkv_t128" and dims.grid == (12 * 48, 1, 1)
+    dims, sym = fp8.launch_geometry(_abi.ENTRY_W8A8_DENSE, 4096, 4096, 512)    # 64 such tiles
+    assert sym == "lf_fp8_w8a8_dense_t128" and dims.grid == (4 * 32, 1, 1)
+    dims, sym = fp8.launch_geometry(_abi.ENTRY_W8A8_GATE_UP, 14336, 4096, 256)  # never on 256 x 128
+    assert sym == "lf_fp8_w8a8_gate_up_t128" and dims.grid == (2 * 224, 1, 1)
     dims, sym = fp8.launch_geometry(_abi.ENTRY_W8A8_GATE_UP, 14336, 4096, 8192)
     assert sym == "lf_fp8_w8a8_gate_up_t256" and dims.grid == (32 * 112, 1, 1) and dims.block == (256, 1, 1)
     dims, sym = fp8.launch_geometry(_abi.ENTRY_W8A8_DENSE, 4096, 14336, 2048)
-    assert sym == "lf_fp8_w8a8_dense_t128" and dims.grid == (16 * 32, 1, 1) and dims.block == (256, 1, 1)
+    assert sym == "lf_fp8_w8a8_dense_t256x128" and dims.grid == (8 * 32, 1, 1) and dims.block == (256, 1, 1)
     dims, sym = fp8.launch_geometry(_abi.ENTRY_W8A8_QKV, 6144, 4096, 8000)
     assert sym == "lf_fp8_w8a8_qkv_t256" and dims.grid == (32 * 24, 1, 1)
     dims, sym = fp8.launch_geometry(_abi.ENTRY_W8A8_DENSE, 128 * 33, 4096, 8192)

@@ -187,18 +187,25 @@ def test_w8a16_split_k_repeated_launches(rt, family_op):
     assert np.array_equal(outs[0], outs[1]) and np.array_equal(outs[1], outs[2])
 
 
-@pytest.mark.parametrize("form,max_tokens", [("_t256", 4096), ("_t256w8", 3072)])
-@pytest.mark.parametrize("op,m,k", [
+_LARGE_TILE_CASES = [
     ("dense", 300, 128), ("dense", 1, 256), ("dense", 511, 384), ("dense", 257, 1408),
     ("qkv", 513, 128), ("qkv", 256, 640), ("gate_up", 257, 256), ("gate_up", 40, 128),
-])
+]
+
+
+@pytest.mark.parametrize("op,m,k,form,max_tokens", [
+    c + f for f in (("_t256", 4096), ("_t256w8", 3072), ("_t256x128", 2048))
+    for c in _LARGE_TILE_CASES if not (f[0] == "_t256x128" and c[0] == "gate_up")
+] + [("dense", 2048, 384, "_t256x128", 2048), ("qkv", 700, 512, "_t256x128", 2048)])
 def test_w8a8_large_tile_edges(rt, op, m, k, form, max_tokens):
-    """The 256 x 256 tiles at these widths: the four-wave form for
-    max_query_tokens = 4096 (256 tiles) and the eight-wave form for 3072
-    (192 tiles). Ragged live rows, the shortest K loops (K = 128: one k-tile,
-    K = 256: the two-stage prologue with nothing left to load; the eight-wave
-    ring's prologue and tail cases), an odd k-tile count (K = 1408), and qkv
-    region boundaries that fall inside a block (Nq = 2176, Nk = Nv = 960)."""
+    """The 256-row tiles at these widths: 256 x 256 on four waves for
+    max_query_tokens = 4096 (256 tiles), on eight waves for 3072 (192
+    tiles), and (QKV and dense) 256 x 128 on four waves with three stages for
+    2048. Ragged live rows, the shortest K loops (K = 128: one k-tile, K =
+    256: the prologue with nothing left to load, K = 384: three stages and
+    nothing left; the eight-wave ring's prologue and tail cases), an odd
+    k-tile count (K = 1408), full tiles, and qkv region boundaries that fall
+    inside a block (Nq = 2176, Nk = Nv = 960)."""
     from lunaflux_amd import _abi, fp8
     rng = np.random.default_rng(7000 + m + k)
     x = synth.activations(rng, m, k)
