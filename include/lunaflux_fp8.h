@@ -114,10 +114,12 @@ int32_t lunaflux_fp8_unpack_weight(const uint8_t *region, int64_t region_bytes,
  *    profile's largest M; _k<K>...: a shape-specialized entry.
  *  W8A8 ("prefill"): activations quantized per token to e4m3
  *    (lf_fp8_act_quant_rows), e4m3 x e4m3 MFMA, fp32 accumulation, row scale
- *    x channel scale epilogue. _t128: 128 x 128 block tiles of 4 waves
- *    (16x16x128 f8f6f4 MFMA); _t256: 256 x 256 tiles of 4 waves
- *    (16x16x128 f8f6f4 MFMA, 128 x 128 outputs per wave), chosen when a
- *    launch has at least 192 of them.
+ *    x channel scale epilogue. _t256: 256 x 256 tiles of 4 waves
+ *    (16x16x128 f8f6f4 MFMA, 128 x 128 outputs per wave) for launches of at
+ *    least 256 such tiles; _t256w8: the same tiles on 8 waves (32x32x64
+ *    f8f6f4 MFMA, 512-thread blocks) for 192-255; _t256x128 (QKV, dense):
+ *    256 x 128 tiles of 4 waves when those number 128-256; _t128: 128 x 128
+ *    tiles of 4 waves otherwise.
  *
  * Operands (all device regions, in order):
  *  lf_fp8_act_quant_rows (counts, x, w, xq)   x bf16 [M, K] -> xq; K is read
