@@ -75,10 +75,14 @@ LF_DEVICE bool desc_ok(const MoeDesc &d) {
 
 // --- routing ---------------------------------------------------------------
 // One wave per token, four tokens per block; lane l holds the logits of
-// experts l, l + 64, ... (E <= 256) and the wave keeps them in LDS. The k
-// largest logits in order (ties -> lower expert id) by rank: each lane counts
-// the logits that beat each of its own (u_j > v, or u_j == v and j < e), so
-// the expert ranked r < k is the r-th pick, with no serial cross-lane chain.
+// experts l, l + 64, ... (E <= 256) and the wave keeps their ranking keys in
+// LDS. The k largest logits in order (ties -> lower expert id) by rank: each
+// lane counts the keys that beat each of its own, so the expert ranked r < k
+// is the r-th pick, with no serial cross-lane chain. A key is one 64-bit
+// integer (rank_key64) that orders as the logit and then the lower id does,
+// so "beats" is one integer compare (a compare and a carry-add per key; the
+// float form, u > v or u == v and j < e, cost boolean mask logic on the
+// scalar unit per key: 2.5 us per token at E = 64 against 0.8 us measured).
 // Softmax weights over the k picked logits (mode 0) or over all experts (mode
 // 1); the sum of exponentials is accumulated in expert order, as the
 // reference loop does (every lane reads the exponentials back from LDS and
@@ -100,39 +104,66 @@ LF_DEVICE void wave_lds_sync() {
 // every index in range and lets the value carry the fault.
 LF_DEVICE float rank_key(float v) { return __builtin_isnan(v) ? -__builtin_inff() : v; }
 
-// Routes token t with the calling wave; sv (E floats, 16-byte aligned), sid
-// and spv (16 each) are this wave's LDS scratch.
-LF_DEVICE void route_token(const MoeDesc &d, const MoeLayout &L, const float *logits, uint8_t *ws,
-                           int t, float *sv, int32_t *sid, float *spv) {
-  const int lane = threadIdx.x & 63;
-  const int E = d.experts, k = d.top_k;
-  const float *l = logits + static_cast<uint64_t>(t) * E;
-  int32_t *ids = at<int32_t>(ws, L.topk_ids) + static_cast<uint64_t>(t) * k;
-  float *wts = at<float>(ws, L.topk_w) + static_cast<uint64_t>(t) * k;
+// rank_key as a 64-bit integer with the expert id below it: the key's bits
+// mapped to a signed integer in float order (negative floats have their
+// magnitude bits flipped; -0 is first made +0, which compares equal to it),
+// times 256, plus 255 - e. Key a > key b exactly when a's logit ranks above
+// b's or they are equal and a's id is lower. Slots past E hold INT64_MIN,
+// below every key.
+LF_DEVICE int64_t rank_key64(float v, int e) {
+  const int32_t b = __float_as_int(rank_key(v) + 0.0f);
+  const int32_t o = b >= 0 ? b : b ^ 0x7fffffff;
+  return static_cast<int64_t>(o) * 256 + (255 - e);
+}
+typedef int64_t i64x2 __attribute__((ext_vector_type(2)));
+
+// This lane's logits of token t (experts lane, lane + 64, lane + 128,
+// lane + 192; 0 past E).
+struct TokenLogits {
   float v[4];
+};
+LF_DEVICE TokenLogits route_load(const MoeDesc &d, const float *logits, int t) {
+  const int lane = threadIdx.x & 63;
+  const int E = d.experts;
+  const float *l = logits + static_cast<uint64_t>(t) * E;
+  TokenLogits r;
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
     const int e = lane + 64 * i;
-    v[i] = e < E ? rank_key(l[e]) : 0.0f;
-    if (e < E) sv[e] = v[i];
+    r.v[i] = e < E ? l[e] : 0.0f;
+  }
+  return r;
+}
+
+// Routes token t, whose logits lg holds, with the calling wave; sk (256
+// keys, 16-byte aligned), sid and spv (16 each) are this wave's LDS scratch.
+LF_DEVICE void route_ranked(const MoeDesc &d, const MoeLayout &L, uint8_t *ws, int t,
+                            const TokenLogits &lg, int64_t *sk, int32_t *sid, float *spv) {
+  const int lane = threadIdx.x & 63;
+  const int E = d.experts, k = d.top_k;
+  int32_t *ids = at<int32_t>(ws, L.topk_ids) + static_cast<uint64_t>(t) * k;
+  float *wts = at<float>(ws, L.topk_w) + static_cast<uint64_t>(t) * k;
+  float v[4];
+  int64_t key[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int e = lane + 64 * i;
+    v[i] = e < E ? rank_key(lg.v[i]) : 0.0f;
+    key[i] = e < E ? rank_key64(lg.v[i], e) : INT64_MIN;
+    sk[e] = key[i];
   }
   wave_lds_sync();
-  const int E4 = E & ~3;
+  const int E2 = (E + 1) & ~1;  // an odd E reads the INT64_MIN slot E too
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
     const int e = lane + 64 * i;
     if (e >= E) break;
     int r = 0;
-    for (int j = 0; j < E4; j += 4) {
-      const float4 u = *reinterpret_cast<const float4 *>(&sv[j]);
-      r += (u.x > v[i] || (u.x == v[i] && j < e)) ? 1 : 0;
-      r += (u.y > v[i] || (u.y == v[i] && j + 1 < e)) ? 1 : 0;
-      r += (u.z > v[i] || (u.z == v[i] && j + 2 < e)) ? 1 : 0;
-      r += (u.w > v[i] || (u.w == v[i] && j + 3 < e)) ? 1 : 0;
-    }
-    for (int j = E4; j < E; ++j) {
-      const float u = sv[j];
-      r += (u > v[i] || (u == v[i] && j < e)) ? 1 : 0;
+#pragma unroll 8
+    for (int j = 0; j < E2; j += 2) {
+      const i64x2 u = *reinterpret_cast<const i64x2 *>(&sk[j]);
+      r += u.x > key[i] ? 1 : 0;
+      r += u.y > key[i] ? 1 : 0;
     }
     if (r < k) {
       sid[r] = e;
@@ -145,13 +176,17 @@ LF_DEVICE void route_token(const MoeDesc &d, const MoeLayout &L, const float *lo
   if (d.route_mode == 0) {
     for (int j = 0; j < k; ++j) sum += expf(spv[j] - top);
   } else {
-    // the ranking above has read sv for the last time
+    // the ranking above has read sk for the last time; the exponentials
+    // take its first E floats
+    float *sv = reinterpret_cast<float *>(sk);
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
       const int e = lane + 64 * i;
       if (e < E) sv[e] = expf(v[i] - top);
     }
     wave_lds_sync();
+    const int E4 = E & ~3;
+#pragma unroll 8
     for (int j = 0; j < E4; j += 4) {
       const float4 u = *reinterpret_cast<const float4 *>(&sv[j]);
       sum += u.x;
@@ -165,19 +200,24 @@ LF_DEVICE void route_token(const MoeDesc &d, const MoeLayout &L, const float *lo
     ids[lane] = sid[lane];
     wts[lane] = expf(spv[lane] - top) / sum;
   }
-  // the next token of this wave overwrites sv, sid and spv
+  // the next token of this wave overwrites sk, sid and spv
   wave_lds_sync();
 }
 
+LF_DEVICE void route_token(const MoeDesc &d, const MoeLayout &L, const float *logits, uint8_t *ws,
+                           int t, int64_t *sk, int32_t *sid, float *spv) {
+  route_ranked(d, L, ws, t, route_load(d, logits, t), sk, sid, spv);
+}
+
 LF_DEVICE void route(const int32_t *counts, const MoeDesc &d, const float *logits, uint8_t *ws) {
-  __shared__ __attribute__((aligned(16))) float sv[4][256];
+  __shared__ __attribute__((aligned(16))) int64_t sk[4][256];
   __shared__ int32_t sid[4][16];
   __shared__ float spv[4][16];
   const int T = live_rows(counts, 1 << 30);
   const int w = threadIdx.x >> 6;
   const int t = blockIdx.x * 4 + w;
   if (t >= T) return;
-  route_token(d, MoeLayout(d, T), logits, ws, t, sv[w], sid[w], spv[w]);
+  route_token(d, MoeLayout(d, T), logits, ws, t, sk[w], sid[w], spv[w]);
 }
 
 // --- stable counting sort ----------------------------------------------------
@@ -374,18 +414,18 @@ LF_DEVICE void sort_assignments(const int32_t *counts, const MoeDesc &d, uint8_t
 // kSortThreads threads, for profiles with few assignments (the launch
 // geometry picks it when max_tokens * top_k <= kSortThreads, where
 // lf_moe_route, lf_moe_sort_count, lf_moe_sort and lf_moe_quant_tokens are
-// four launches of a few microseconds each): the waves route the tokens
-// (route_token, as lf_moe_route), then the block counts the assignments per
-// expert, scans as lf_moe_sort, and ranks the chunks of kSortThreads
-// assignments in order, each chunk's positions starting where the previous
-// chunk's rows of each expert ended; then the waves quantize the tokens as
-// lf_moe_quant_tokens does (the per-token form with the two-pass row
+// four launches of a few microseconds each): half of the waves route the
+// tokens (route_ranked, as lf_moe_route) while the other half quantize them
+// as lf_moe_quant_tokens does (the per-token form with the two-pass row
 // quantizer, whose codes and scales equal the register-resident one's: a
-// 1024-thread block leaves a wave 128 registers). Outputs equal those of the
+// 1024-thread block leaves a wave 128 registers); then the block counts the
+// assignments per expert, scans as lf_moe_sort, and ranks the chunks of
+// kSortThreads assignments in order, each chunk's positions starting where
+// the previous chunk's rows of each expert ended. Outputs equal those of the
 // four launches for any number of tokens.
 LF_DEVICE void route_sort_block(const int32_t *counts, const MoeDesc &d, const float *logits,
                                 const uint16_t *x, uint8_t *ws) {
-  __shared__ __attribute__((aligned(16))) float sv[kSortWaves][256];
+  __shared__ __attribute__((aligned(16))) int64_t sk[kSortWaves][256];
   __shared__ int32_t sid[kSortWaves][16];
   __shared__ float spv[kSortWaves][16];
   __shared__ int32_t base[256];
@@ -395,8 +435,39 @@ LF_DEVICE void route_sort_block(const int32_t *counts, const MoeDesc &d, const f
   const int E = d.experts;
   const int A = T * d.top_k;
   const int tid = threadIdx.x, wave = tid >> 6;
-  for (int t = wave; t < T; t += kSortWaves) route_token(d, L, logits, ws, t, sv[wave], sid[wave], spv[wave]);
-  // the ids written above are visible to the whole block after the barrier
+  // The first half of the waves routes the tokens while the second half
+  // runs the token quantizer (codes and token scales need no routing; the
+  // per-token form's expert-order copies of the scales are written after the
+  // sort).
+  constexpr int kRouteWaves = kSortWaves / 2;
+  if (wave < kRouteWaves) {
+    // A wave's tokens are taken in batches of 4 whose logits are all loaded
+    // before the first is ranked (one load latency per batch, not per token).
+    constexpr int kBatch = 4;
+    for (int t0 = wave; t0 < T; t0 += kBatch * kRouteWaves) {
+      TokenLogits lg[kBatch];
+#pragma unroll
+      for (int b = 0; b < kBatch; ++b) {
+        const int t = t0 + b * kRouteWaves;
+        lg[b] = route_load(d, logits, t < T ? t : t0);
+      }
+#pragma unroll
+      for (int b = 0; b < kBatch; ++b) {
+        const int t = t0 + b * kRouteWaves;
+        if (t < T) route_ranked(d, L, ws, t, lg[b], sk[wave], sid[wave], spv[wave]);
+      }
+    }
+  } else if (d.group != 0) {
+    quantize_groups_wave(x, d.hidden, T, at<uint8_t>(ws, L.xq), at<float>(ws, L.xs), wave - kRouteWaves,
+                         kSortWaves - kRouteWaves);
+  } else {
+    for (int t = wave - kRouteWaves; t < T; t += kSortWaves - kRouteWaves) {
+      const uint64_t off = static_cast<uint64_t>(t) * d.hidden;
+      quantize_row_wave_2pass(x + off, d.hidden, at<uint8_t>(ws, L.xq) + off, at<float>(ws, L.xs) + t);
+    }
+  }
+  // the ids and token scales written above are visible to the whole block
+  // after the barrier
   __syncthreads();
   if (A == 0) {
     sort_write_empty(d, L, ws);
@@ -423,19 +494,14 @@ LF_DEVICE void route_sort_block(const int32_t *counts, const MoeDesc &d, const f
     }
     __syncthreads();
   }
-  // The token quantizer; the per-token form reads the positions written
-  // above (visible to the block after the last barrier).
-  if (d.group != 0) {
-    quantize_groups_wave(x, d.hidden, T, at<uint8_t>(ws, L.xq), at<float>(ws, L.xs), wave,
-                         kSortWaves);
-    return;
-  }
-  const int lane = tid & 63;
-  for (int t = wave; t < T; t += kSortWaves) {
-    const uint64_t off = static_cast<uint64_t>(t) * d.hidden;
-    const float sc = quantize_row_wave_2pass(x + off, d.hidden, at<uint8_t>(ws, L.xq) + off,
-                                             at<float>(ws, L.xs) + t);
-    if (lane < d.top_k) at<float>(ws, L.hs)[at<int32_t>(ws, L.pos)[t * d.top_k + lane]] = sc;
+  // Per-token form: each token's scale also goes to its assignments'
+  // positions in expert order (the positions written above are visible to
+  // the block after the last barrier).
+  if (d.group == 0) {
+    const float *xs = at<float>(ws, L.xs);
+    const int32_t *pos = at<int32_t>(ws, L.pos);
+    float *hs = at<float>(ws, L.hs);
+    for (int a = tid; a < A; a += kSortThreads) hs[pos[a]] = xs[a / d.top_k];
   }
 }
 
@@ -1346,7 +1412,10 @@ LF_DEVICE void combine(const int32_t *counts, const MoeDesc &d, uint8_t *ws, uin
   }
 }
 
-LF_DEVICE const MoeDesc &desc_of(const int32_t *desc) { return *reinterpret_cast<const MoeDesc *>(desc); }
+// The descriptor by value: held in registers for the whole kernel. A
+// reference into the descriptor buffer would be read again from memory after
+// every fence and barrier (each a load latency in the routing and sort loops).
+LF_DEVICE MoeDesc desc_of(const int32_t *desc) { return *reinterpret_cast<const MoeDesc *>(desc); }
 
 }  // namespace
 
@@ -1357,21 +1426,21 @@ extern "C" {
 __global__ __launch_bounds__(256) void lf_moe_route(const int32_t *counts, const int32_t *desc,
                                                     const float *logits, const uint16_t *,
                                                     uint8_t *ws) {
-  const MoeDesc &d = desc_of(desc);
+  const MoeDesc d = desc_of(desc);
   if (!desc_ok(d)) return;
   route(counts, d, logits, ws);
 }
 
 __global__ __launch_bounds__(1024) void lf_moe_sort_count(const int32_t *counts,
                                                           const int32_t *desc, uint8_t *ws) {
-  const MoeDesc &d = desc_of(desc);
+  const MoeDesc d = desc_of(desc);
   if (!desc_ok(d)) return;
   sort_count(counts, d, ws);
 }
 
 __global__ __launch_bounds__(1024) void lf_moe_sort(const int32_t *counts, const int32_t *desc,
                                                     uint8_t *ws) {
-  const MoeDesc &d = desc_of(desc);
+  const MoeDesc d = desc_of(desc);
   if (!desc_ok(d)) return;
   sort_assignments(counts, d, ws);
 }
@@ -1379,7 +1448,7 @@ __global__ __launch_bounds__(1024) void lf_moe_sort(const int32_t *counts, const
 __global__ __launch_bounds__(1024) void lf_moe_route_sort(const int32_t *counts, const int32_t *desc,
                                                          const float *logits, const uint16_t *x,
                                                          uint8_t *ws) {
-  const MoeDesc &d = desc_of(desc);
+  const MoeDesc d = desc_of(desc);
   if (!desc_ok(d) || blockDim.x != kSortThreads) return;
   route_sort_block(counts, d, logits, x, ws);
 }
@@ -1387,7 +1456,7 @@ __global__ __launch_bounds__(1024) void lf_moe_route_sort(const int32_t *counts,
 __global__ __launch_bounds__(256) void lf_moe_quant_tokens(const int32_t *counts,
                                                            const int32_t *desc,
                                                            const uint16_t *x, uint8_t *ws) {
-  const MoeDesc &d = desc_of(desc);
+  const MoeDesc d = desc_of(desc);
   if (!desc_ok(d)) return;
   const int T = live_rows(counts, 1 << 30);
   const MoeLayout L(d, T);
@@ -1410,7 +1479,7 @@ __global__ __launch_bounds__(256) void lf_moe_quant_tokens(const int32_t *counts
 
 __global__ __launch_bounds__(256) void lf_moe_quant_hidden(const int32_t *counts,
                                                            const int32_t *desc, uint8_t *ws) {
-  const MoeDesc &d = desc_of(desc);
+  const MoeDesc d = desc_of(desc);
   if (!desc_ok(d)) return;
   const int T = live_rows(counts, 1 << 30);
   const MoeLayout L(d, T);
@@ -1422,14 +1491,14 @@ __global__ __launch_bounds__(256) void lf_moe_quant_hidden(const int32_t *counts
 __global__ __launch_bounds__(256) void lf_moe_gate_up(const int32_t *counts, const int32_t *desc,
                                                       const uint8_t *wg, const uint8_t *wu,
                                                       uint8_t *ws) {
-  const MoeDesc &d = desc_of(desc);
+  const MoeDesc d = desc_of(desc);
   if (!desc_ok(d) || d.group != 0 || header_of(wg).magic != kWeightMagic) return;
   grouped_gemm<0, false>(counts, d, wg, wu, ws);
 }
 
 __global__ __launch_bounds__(256) void lf_moe_down(const int32_t *counts, const int32_t *desc,
                                                    const uint8_t *wd, uint8_t *ws) {
-  const MoeDesc &d = desc_of(desc);
+  const MoeDesc d = desc_of(desc);
   if (!desc_ok(d) || d.group != 0 || header_of(wd).magic != kWeightMagic) return;
   grouped_gemm<1, false>(counts, d, wd, wd, ws);
 }
@@ -1440,7 +1509,7 @@ __global__ __launch_bounds__(512) void lf_moe_gate_up_t256(const int32_t *counts
                                                            const int32_t *desc,
                                                            const uint8_t *wg, const uint8_t *wu,
                                                            uint8_t *ws) {
-  const MoeDesc &d = desc_of(desc);
+  const MoeDesc d = desc_of(desc);
   if (!desc_ok(d) || d.group != 0 || header_of(wg).magic != kWeightMagic) return;
   grouped_gemm_t256<0>(counts, d, wg, wu, ws);
 }
@@ -1448,7 +1517,7 @@ __global__ __launch_bounds__(512) void lf_moe_gate_up_t256(const int32_t *counts
 __global__ __launch_bounds__(512) void lf_moe_down_t256(const int32_t *counts,
                                                         const int32_t *desc, const uint8_t *wd,
                                                         uint8_t *ws) {
-  const MoeDesc &d = desc_of(desc);
+  const MoeDesc d = desc_of(desc);
   if (!desc_ok(d) || d.group != 0 || header_of(wd).magic != kWeightMagic) return;
   grouped_gemm_t256<1>(counts, d, wd, wd, ws);
 }
@@ -1459,7 +1528,7 @@ __global__ __launch_bounds__(512) void lf_moe_gate_up_t256_b128(const int32_t *c
                                                                 const int32_t *desc,
                                                                 const uint8_t *wg,
                                                                 const uint8_t *wu, uint8_t *ws) {
-  const MoeDesc &d = desc_of(desc);
+  const MoeDesc d = desc_of(desc);
   if (!desc_ok(d) || d.group != 128 || header_of(wg).magic != kWeightMagic) return;
   grouped_gemm_t256<0, true>(counts, d, wg, wu, ws);
 }
@@ -1471,7 +1540,7 @@ __global__ __launch_bounds__(512) void lf_moe_gate_up_t256_b128_q(const int32_t 
                                                                   const int32_t *desc,
                                                                   const uint8_t *wg,
                                                                   const uint8_t *wu, uint8_t *ws) {
-  const MoeDesc &d = desc_of(desc);
+  const MoeDesc d = desc_of(desc);
   if (!desc_ok(d) || d.group != 128 || header_of(wg).magic != kWeightMagic) return;
   grouped_gemm_t256<0, true, true>(counts, d, wg, wu, ws);
 }
@@ -1479,7 +1548,7 @@ __global__ __launch_bounds__(512) void lf_moe_gate_up_t256_b128_q(const int32_t 
 __global__ __launch_bounds__(512) void lf_moe_down_t256_b128(const int32_t *counts,
                                                              const int32_t *desc,
                                                              const uint8_t *wd, uint8_t *ws) {
-  const MoeDesc &d = desc_of(desc);
+  const MoeDesc d = desc_of(desc);
   if (!desc_ok(d) || d.group != 128 || header_of(wd).magic != kWeightMagic) return;
   grouped_gemm_t256<1, true>(counts, d, wd, wd, ws);
 }
@@ -1490,7 +1559,7 @@ __global__ __launch_bounds__(256) void lf_moe_gate_up_gemv(const int32_t *counts
                                                            const int32_t *desc,
                                                            const uint8_t *wg, const uint8_t *wu,
                                                            uint8_t *ws) {
-  const MoeDesc &d = desc_of(desc);
+  const MoeDesc d = desc_of(desc);
   if (!desc_ok(d) || header_of(wg).magic != kWeightMagic) return;
   if (d.group == 0) grouped_gemv<0, false>(counts, d, wg, wu, ws);
   else grouped_gemv<0, true>(counts, d, wg, wu, ws);
@@ -1499,7 +1568,7 @@ __global__ __launch_bounds__(256) void lf_moe_gate_up_gemv(const int32_t *counts
 __global__ __launch_bounds__(256) void lf_moe_down_gemv(const int32_t *counts,
                                                         const int32_t *desc, const uint8_t *wd,
                                                         uint8_t *ws) {
-  const MoeDesc &d = desc_of(desc);
+  const MoeDesc d = desc_of(desc);
   if (!desc_ok(d) || header_of(wd).magic != kWeightMagic) return;
   if (d.group == 0) grouped_gemv<1, false>(counts, d, wd, wd, ws);
   else grouped_gemv<1, true>(counts, d, wd, wd, ws);
@@ -1511,7 +1580,7 @@ __global__ __launch_bounds__(256) void lf_moe_gate_up_b128(const int32_t *counts
                                                            const int32_t *desc,
                                                            const uint8_t *wg, const uint8_t *wu,
                                                            uint8_t *ws) {
-  const MoeDesc &d = desc_of(desc);
+  const MoeDesc d = desc_of(desc);
   if (!desc_ok(d) || d.group != 128 || header_of(wg).magic != kWeightMagic) return;
   grouped_gemm<0, true>(counts, d, wg, wu, ws);
 }
@@ -1519,14 +1588,14 @@ __global__ __launch_bounds__(256) void lf_moe_gate_up_b128(const int32_t *counts
 __global__ __launch_bounds__(256) void lf_moe_down_b128(const int32_t *counts,
                                                         const int32_t *desc, const uint8_t *wd,
                                                         uint8_t *ws) {
-  const MoeDesc &d = desc_of(desc);
+  const MoeDesc d = desc_of(desc);
   if (!desc_ok(d) || d.group != 128 || header_of(wd).magic != kWeightMagic) return;
   grouped_gemm<1, true>(counts, d, wd, wd, ws);
 }
 
 __global__ __launch_bounds__(256) void lf_moe_combine(const int32_t *counts, const int32_t *desc,
                                                       uint8_t *ws, uint16_t *out) {
-  const MoeDesc &d = desc_of(desc);
+  const MoeDesc d = desc_of(desc);
   if (!desc_ok(d)) return;
   combine(counts, d, ws, out);
 }

@@ -196,6 +196,27 @@ def test_moe_all_tokens_one_expert_and_ties(rt):
     check_output(x, weights, ex, w, out, False, "moe one expert", st)
 
 
+@pytest.mark.parametrize("t,e,k,mode", [(40, 7, 3, 1), (33, 129, 5, 0), (600, 7, 2, 0)])
+def test_moe_route_signed_zero_ties_odd_experts(rt, t, e, k, mode):
+    """Routing ranks integer keys ordered as the logits, -0 equal to +0, the
+    lower id first among equals; with an odd expert count the key slot past
+    the last expert is read too and must rank below every expert. Rows of
+    signed zeros, rows of many equal values and rows won by the last expert
+    route as the oracle does (600 tokens: the multi-block route kernel)."""
+    rng = np.random.default_rng(990 + e + t)
+    logits = rng.standard_normal((t, e)).astype(np.float32)
+    logits[::3] = 0.0
+    logits[::3, 1::2] = -0.0              # -0 ties +0: lower id first
+    logits[1::3, :e // 2 + 1] = logits[1::3, :1]   # many equal values
+    logits[2::3, -1] = 50.0               # the last expert wins
+    x, logits, weights, out, st = run_case(rt, rng, t, e, k, 256, 384, mode, block=False,
+                                           logits=logits)
+    ex, w = check_routing(logits, k, mode, st)
+    assert (ex[::3] == np.arange(k)).all()
+    assert (ex[2::3, 0] == e - 1).all()
+    check_output(x, weights, ex, w, out, False, f"moe signed zeros t={t} e={e} k={k}", st)
+
+
 def test_moe_sort_across_chunks(rt):
     """The sort ranks assignments in chunks of 1024 across blocks; 3000 x 6
     assignments over 64 experts (18 chunks) must still give exactly the
