@@ -7,7 +7,12 @@
 //
 // Stage layout, load plan and fragment reads are those of w8a8_v3.h's loop
 // (A rows with the chunk swizzle that reads conflict-free, B as verbatim
-// 2 KiB weight tiles), on w8a8v3 tiles of 2 x 2 waves.
+// 2 KiB weight tiles), on w8a8v3 tiles of 2 x 2 waves. The load addresses
+// are held as wave-uniform 64-bit bases in scalar registers plus 32-bit
+// per-lane offsets (Plan): the A rows of the tile from one base (tile row
+// offset times K plus the chunk: K < 2^24 keeps it in 32 bits), each B
+// half-tile's base with the lane's 16 bytes as the one shared offset. This
+// takes 9 vector registers where 64-bit per-lane addresses took 32.
 //
 // Against the 8-wave half-step loop (w8a8_v4.h) a wave keeps its 128 x 128
 // block of outputs (256 x 256 tiles), so a k-tile reads 64 KiB of fragments
@@ -61,13 +66,44 @@ using TileN128 = w8a8v3::Tile<256, 128, 3, 2, 2>;
 // / 35.4 / 35.4 / 35.8 us and down 108.7 / 109.2 / 108.5 / 109.3 us at M =
 // 2048, QKV 34.0 / 34.7 / 34.8 / 35.3 us and down 93.9 / 94.5 / 95.4 / 97.3
 // us at M = 1024.
+// Load plan: A instruction q of this wave at k-tile kt fetches a_base +
+// kt * 128 + a_off[q]; B instruction q fetches b_base[q] + kt * kTileBytes +
+// b_lane.
+template <class T>
+struct Plan {
+  const uint8_t *a_base;
+  uint32_t a_off[T::kAIns];
+  const uint8_t *b_base[T::kBIns];
+  uint32_t b_lane;
+};
+
+// A pointer every lane of the wave holds, moved to scalar registers.
+LF_DEVICE const uint8_t *uniform_ptr(const uint8_t *p) {
+  const uint64_t v = reinterpret_cast<uint64_t>(p);
+  const uint32_t lo = __builtin_amdgcn_readfirstlane(static_cast<uint32_t>(v));
+  const uint32_t hi = __builtin_amdgcn_readfirstlane(static_cast<uint32_t>(v >> 32));
+  return reinterpret_cast<const uint8_t *>((static_cast<uint64_t>(hi) << 32) | lo);
+}
+
+// global_load_lds_dwordx4 with a scalar base and a 32-bit lane offset; the
+// wave writes LDS at lds_offset + 16 * lane (as w8a8v3::dma16).
+#pragma clang diagnostic push
+#pragma clang diagnostic ignored "-Winline-asm"  // M0 is listed as clobbered on purpose
+LF_DEVICE void dma16(const uint8_t *base, uint32_t offset, uint32_t lds_offset) {
+  asm volatile("s_mov_b32 m0, %2\n\tglobal_load_lds_dwordx4 %0, %1"
+               :
+               : "v"(offset), "s"(base), "s"(__builtin_amdgcn_readfirstlane(lds_offset))
+               : "memory", "m0");
+}
+#pragma clang diagnostic pop
+
 template <class T>
 constexpr int barrier_row() {
   return T::kStages == 3 ? 1 : 3;
 }
 
 template <class T, bool SWAP, int P = barrier_row<T>()>
-__device__ __forceinline__ void mainloop(const w8a8v3::Plan<T> &plan, int KT, uint8_t *smem,
+__device__ __forceinline__ void mainloop(const Plan<T> &plan, int KT, uint8_t *smem,
                                          f32x4 (&acc)[T::kFM][T::kFN]) {
   constexpr int NS = T::kStages, FM = T::kFM, FN = T::kFN;
   static_assert((NS == 2 || NS == 3) && FM == 8 && T::kWaves == 4, "4-wave 256-row tile");
@@ -83,10 +119,10 @@ __device__ __forceinline__ void mainloop(const w8a8v3::Plan<T> &plan, int KT, ui
   auto dma = [&](int kt, int q) {
     const uint32_t a = smem_base + (kt % NS) * T::kStage;
     if (q < T::kAIns) {
-      w8a8v3::dma16(plan.a[q] + kt * 128, a + (wave * T::kAIns + q) * 1024);
+      dma16(plan.a_base + kt * 128, plan.a_off[q], a + (wave * T::kAIns + q) * 1024);
     } else {
-      w8a8v3::dma16(plan.b[q - T::kAIns] + kt * kTileBytes,
-                    a + T::kABytes + w8a8v3::b_load_half<T>(wave, q - T::kAIns) * 1024);
+      dma16(plan.b_base[q - T::kAIns] + kt * kTileBytes, plan.b_lane,
+            a + T::kABytes + w8a8v3::b_load_half<T>(wave, q - T::kAIns) * 1024);
     }
   };
   auto stage = [&](int kt) -> const uint8_t * { return smem + (kt % NS) * T::kStage; };

@@ -508,9 +508,13 @@ static int32_t launch_geometry(int32_t entry, int64_t n, int64_t k, int64_t nq, 
       // M = 2048: QKV (192 large tiles) 71.2 -> 59.5 us on the large tiles;
       // o and down (128) were 30-40 % slower on them and 9-10 % faster on
       // 256 x 128 than on 128 x 128.
+      // The four-wave forms (_t256, _t256x128) address a tile's activation
+      // rows with 32-bit offsets from its first row, which needs 256 K <
+      // 2^32; wider K takes the eight-wave or 128 x 128 forms.
+      const bool offsets32 = k < (int64_t(1) << 24);
       const int64_t tiles256 = (n % cols256 == 0) ? ((max_tokens + 255) / 256) * (n / cols256) : 0;
-      const int64_t tiles256x128 = !gate_up ? ((max_tokens + 255) / 256) * (n / cols128) : 0;
-      const bool big = tiles256 >= 192, four_wave = tiles256 >= 256;
+      const int64_t tiles256x128 = !gate_up && offsets32 ? ((max_tokens + 255) / 256) * (n / cols128) : 0;
+      const bool big = tiles256 >= 192, four_wave = tiles256 >= 256 && offsets32;
       const bool wide128 = !big && tiles256x128 >= 128 && tiles256x128 <= 256;
       const int64_t tiles = big ? tiles256 : wide128 ? tiles256x128 : ((max_tokens + 127) / 128) * (n / cols128);
       if (tiles > INT32_MAX) return LF_INVALID_ARGUMENT;

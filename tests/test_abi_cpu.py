@@ -211,6 +211,13 @@ def test_launch_geometry():
     assert sym == "lf_fp8_w8a8_qkv_t256" and dims.grid == (32 * 24, 1, 1)
     dims, sym = fp8.launch_geometry(_abi.ENTRY_W8A8_DENSE, 128 * 33, 4096, 8192)
     assert sym == "lf_fp8_w8a8_dense_t128" and dims.grid == (64 * 33, 1, 1)
+    # the four-wave forms take 32-bit activation offsets from a tile's first
+    # row (256 K < 2^32): from K = 2^24 the eight-wave or 128 x 128 forms
+    big_k = 1 << 24
+    assert fp8.launch_geometry(_abi.ENTRY_W8A8_DENSE, 8192, big_k - 128, 2048)[1] == "lf_fp8_w8a8_dense_t256"
+    dims, sym = fp8.launch_geometry(_abi.ENTRY_W8A8_DENSE, 8192, big_k, 2048)
+    assert sym == "lf_fp8_w8a8_dense_t256w8" and dims.block == (512, 1, 1)
+    assert fp8.launch_geometry(_abi.ENTRY_W8A8_DENSE, 4096, big_k, 2048)[1] == "lf_fp8_w8a8_dense_t128"
     dims, sym = fp8.launch_geometry(_abi.ENTRY_ACT_QUANT_ROWS, 4096, 4096, 2048)
     assert sym == "lf_fp8_act_quant_rows" and dims.grid == (2048 // 4, 1, 1)  # one wave per row
     with pytest.raises(fp8.DeviceError):
