@@ -842,6 +842,10 @@ __device__ __forceinline__ void grouped_gemm_t256(const int32_t *counts, const M
   const int K = static_cast<int>(h0.columns);
   const int KT = K >> 7;
   const int N = static_cast<int>(h0.rows);
+  // the 32-bit activation offsets of the load plan (the launch geometry
+  // picks this form only when they fit)
+  const uint64_t a_rows = STAGE == 0 ? static_cast<uint64_t>(Tn) : static_cast<uint64_t>(Tn) * d.top_k;
+  if (a_rows * static_cast<uint64_t>(K) >= (uint64_t(1) << 32)) return;
   const int gx = STAGE == 0 ? N / (T::kBN / 2) : N / T::kBN;
   int bx, by;
   if (!w8a8v3::tile_of_block(gx, tiles[E], tiles[E], bx, by)) return;
@@ -924,20 +928,25 @@ __device__ __forceinline__ void grouped_gemm_t256(const int32_t *counts, const M
     }
     __syncthreads();
   }
+  // A offsets from the token (or assignment) array: rows x K < 2^32 (the
+  // launch geometry picks this form only then).
   w8a8v4::Plan<T> plan;
+  plan.a_base = w8a8v3::uniform_ptr(abase);
 #pragma unroll
   for (int q = 0; q < T::kAIns; ++q) {
     const int tr = w8a8v4::a_load_row<T>(wave, q, lane);
     const int p = p0 + tr < pend ? p0 + tr : p0;  // dead rows re-read the first row
-    plan.a[q] = abase + static_cast<uint64_t>(src_row(p)) * K + w8a8v4::a_load_slot(tr, lane) * 32;
+    plan.a_off[q] = static_cast<uint32_t>(src_row(p)) * static_cast<uint32_t>(K) +
+                    w8a8v4::a_load_slot(tr, lane) * 32;
   }
 #pragma unroll
   for (int q = 0; q < T::kBIns; ++q) {
     const uint8_t *region;
     int t, ocol;
     slot(w8a8v4::b_load_tile<T>(wave, q), region, t, ocol);
-    plan.b[q] = expert_tiles(region, e) + static_cast<uint64_t>(t) * KT * kTileBytes + lane * 16;
+    plan.b_base[q] = w8a8v3::uniform_ptr(expert_tiles(region, e) + static_cast<uint64_t>(t) * KT * kTileBytes);
   }
+  plan.b_lane = lane * 16;
   w8a8v4::f32x16 acc[T::kFM][T::kFN];
   // 32-row fragments of this wave with a live row (an expert's last tile is
   // usually partial, and small experts fill a few rows of one tile).

@@ -485,20 +485,24 @@ __device__ __forceinline__ void w8a8_v4_kernel(const int32_t *counts, const uint
     const int m = m0 + static_cast<int>(threadIdx.x);
     sa_mine = ascale[m < M ? m : M - 1];
   }
+  // A offsets from the tile's first row: below 256 K < 2^32 for K < 2^24
+  // (the launch geometry picks this form only then).
   w8a8v4::Plan<T> plan;
+  plan.a_base = w8a8v3::uniform_ptr(xq + static_cast<uint64_t>(m0) * K);
 #pragma unroll
   for (int q = 0; q < T::kAIns; ++q) {
     const int tr = w8a8v4::a_load_row<T>(wave, q, lane);
-    const int row = m0 + tr < M ? m0 + tr : M - 1;
-    plan.a[q] = xq + static_cast<uint64_t>(row) * K + w8a8v4::a_load_slot(tr, lane) * 32;
+    const int row = m0 + tr < M ? tr : M - 1 - m0;
+    plan.a_off[q] = static_cast<uint32_t>(row) * static_cast<uint32_t>(K) + w8a8v4::a_load_slot(tr, lane) * 32;
   }
 #pragma unroll
   for (int q = 0; q < T::kBIns; ++q) {
     const uint8_t *region;
     int t, ocol;
     slot(w8a8v4::b_load_tile<T>(wave, q), region, t, ocol);
-    plan.b[q] = expert_tiles(region, 0) + static_cast<uint64_t>(t) * KT * kTileBytes + lane * 16;
+    plan.b_base[q] = w8a8v3::uniform_ptr(expert_tiles(region, 0) + static_cast<uint64_t>(t) * KT * kTileBytes);
   }
+  plan.b_lane = lane * 16;
   w8a8v4::f32x16 acc[T::kFM][T::kFN];
   w8a8v4::mainloop<T>(plan, KT, smem, acc);
 
@@ -622,7 +626,7 @@ __device__ __forceinline__ void w8a8_v5_kernel(const int32_t *counts, const uint
   // A offsets from the tile's first row: below 256 K + K < 2^32 for K <
   // 2^24 (the launch geometry picks this form only then).
   w8a8v5::Plan<T> plan;
-  plan.a_base = w8a8v5::uniform_ptr(xq + static_cast<uint64_t>(m0) * K);
+  plan.a_base = w8a8v3::uniform_ptr(xq + static_cast<uint64_t>(m0) * K);
 #pragma unroll
   for (int q = 0; q < T::kAIns; ++q) {
     const int tr = w8a8v3::a_load_row<T>(wave, q, lane);
@@ -636,7 +640,7 @@ __device__ __forceinline__ void w8a8_v5_kernel(const int32_t *counts, const uint
     const uint8_t *region;
     int t, ocol;
     slot(half >> 1, region, t, ocol);
-    plan.b_base[q] = w8a8v5::uniform_ptr(expert_tiles(region, 0) +
+    plan.b_base[q] = w8a8v3::uniform_ptr(expert_tiles(region, 0) +
                                          static_cast<uint64_t>(t) * KT * kTileBytes + (half & 1) * 1024);
   }
   plan.b_lane = lane * 16;

@@ -94,6 +94,24 @@ LF_DEVICE void dma16(const uint8_t *src, uint32_t lds_offset) {
                : "v"(src), "s"(__builtin_amdgcn_readfirstlane(lds_offset))
                : "memory", "m0");
 }
+// A pointer every lane of the wave holds, moved to scalar registers.
+LF_DEVICE const uint8_t *uniform_ptr(const uint8_t *p) {
+  const uint64_t v = reinterpret_cast<uint64_t>(p);
+  const uint32_t lo = __builtin_amdgcn_readfirstlane(static_cast<uint32_t>(v));
+  const uint32_t hi = __builtin_amdgcn_readfirstlane(static_cast<uint32_t>(v >> 32));
+  return reinterpret_cast<const uint8_t *>((static_cast<uint64_t>(hi) << 32) | lo);
+}
+
+// The same load with a wave-uniform base in scalar registers and a 32-bit
+// lane offset (address base + offset): the loops keep one base per
+// instruction group and a 32-bit register per lane instead of a 64-bit
+// address per lane and instruction.
+LF_DEVICE void dma16(const uint8_t *base, uint32_t offset, uint32_t lds_offset) {
+  asm volatile("s_mov_b32 m0, %2\n\tglobal_load_lds_dwordx4 %0, %1"
+               :
+               : "v"(offset), "s"(base), "s"(__builtin_amdgcn_readfirstlane(lds_offset))
+               : "memory", "m0");
+}
 #pragma clang diagnostic pop
 
 // LDS byte offset of a pointer into a __shared__ array (an address-space

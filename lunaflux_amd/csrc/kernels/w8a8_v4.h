@@ -69,14 +69,17 @@ LF_DEVICE int a_load_slot(int row, int lane) { return a_phys_slot(row, lane & 3)
 template <class T>
 LF_DEVICE int b_load_tile(int wave, int q) { return wave * T::kBIns + q; }
 
+// Load plan, wave-uniform bases (scalar registers) plus 32-bit lane offsets:
+// A instruction q at k-tile kt, half h fetches a_base + kt * 128 + h * 16 +
+// a_off[q] (a_off: the row's offset from a_base + 32 * logical slot); B
+// instruction q fetches b_base[q] + kt * kTileBytes + h * 1024 + b_lane
+// (b_base: the tile strip; b_lane = 16 * lane).
 template <class T>
 struct Plan {
-  // a[q]: global address of this lane's 16 bytes of A instruction q at
-  // k-tile 0, half 0 (row base + 32 * logical slot); b[q]: global address of
-  // its 16 bytes of B instruction q at k-tile 0, half 0 (tile strip base +
-  // 16 * lane).
-  const uint8_t *a[T::kAIns];
-  const uint8_t *b[T::kBIns];
+  const uint8_t *a_base;
+  uint32_t a_off[T::kAIns];
+  const uint8_t *b_base[T::kBIns];
+  uint32_t b_lane;
 };
 
 // Block barrier without the memory fence of __syncthreads (which would make
@@ -144,9 +147,11 @@ __device__ __forceinline__ void mainloop(const Plan<T> &plan, int KT, uint8_t *s
     const int kt = s >> 1, h = s & 1;
     const uint32_t a = smem_base + (s % NS) * T::kStage;
     if (q < T::kAIns) {
-      if (a_on) w8a8v3::dma16(plan.a[q] + kt * 128 + h * 16, a + (wave * T::kAIns + q) * 1024);
+      if (a_on) {
+        w8a8v3::dma16(plan.a_base + kt * 128 + h * 16, plan.a_off[q], a + (wave * T::kAIns + q) * 1024);
+      }
     } else {
-      w8a8v3::dma16(plan.b[q - T::kAIns] + kt * kTileBytes + h * 1024,
+      w8a8v3::dma16(plan.b_base[q - T::kAIns] + kt * kTileBytes + h * 1024, plan.b_lane,
                     a + T::kABytes + b_load_tile<T>(wave, q - T::kAIns) * 1024);
     }
   };

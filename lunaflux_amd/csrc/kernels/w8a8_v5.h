@@ -77,25 +77,6 @@ struct Plan {
   uint32_t b_lane;
 };
 
-// A pointer every lane of the wave holds, moved to scalar registers.
-LF_DEVICE const uint8_t *uniform_ptr(const uint8_t *p) {
-  const uint64_t v = reinterpret_cast<uint64_t>(p);
-  const uint32_t lo = __builtin_amdgcn_readfirstlane(static_cast<uint32_t>(v));
-  const uint32_t hi = __builtin_amdgcn_readfirstlane(static_cast<uint32_t>(v >> 32));
-  return reinterpret_cast<const uint8_t *>((static_cast<uint64_t>(hi) << 32) | lo);
-}
-
-// global_load_lds_dwordx4 with a scalar base and a 32-bit lane offset; the
-// wave writes LDS at lds_offset + 16 * lane (as w8a8v3::dma16).
-#pragma clang diagnostic push
-#pragma clang diagnostic ignored "-Winline-asm"  // M0 is listed as clobbered on purpose
-LF_DEVICE void dma16(const uint8_t *base, uint32_t offset, uint32_t lds_offset) {
-  asm volatile("s_mov_b32 m0, %2\n\tglobal_load_lds_dwordx4 %0, %1"
-               :
-               : "v"(offset), "s"(base), "s"(__builtin_amdgcn_readfirstlane(lds_offset))
-               : "memory", "m0");
-}
-#pragma clang diagnostic pop
 
 template <class T>
 constexpr int barrier_row() {
@@ -119,10 +100,10 @@ __device__ __forceinline__ void mainloop(const Plan<T> &plan, int KT, uint8_t *s
   auto dma = [&](int kt, int q) {
     const uint32_t a = smem_base + (kt % NS) * T::kStage;
     if (q < T::kAIns) {
-      dma16(plan.a_base + kt * 128, plan.a_off[q], a + (wave * T::kAIns + q) * 1024);
+      w8a8v3::dma16(plan.a_base + kt * 128, plan.a_off[q], a + (wave * T::kAIns + q) * 1024);
     } else {
-      dma16(plan.b_base[q - T::kAIns] + kt * kTileBytes, plan.b_lane,
-            a + T::kABytes + w8a8v3::b_load_half<T>(wave, q - T::kAIns) * 1024);
+      w8a8v3::dma16(plan.b_base[q - T::kAIns] + kt * kTileBytes, plan.b_lane,
+                    a + T::kABytes + w8a8v3::b_load_half<T>(wave, q - T::kAIns) * 1024);
     }
   };
   auto stage = [&](int kt) -> const uint8_t * { return smem + (kt % NS) * T::kStage; };

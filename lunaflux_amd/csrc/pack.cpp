@@ -508,13 +508,13 @@ static int32_t launch_geometry(int32_t entry, int64_t n, int64_t k, int64_t nq, 
       // M = 2048: QKV (192 large tiles) 71.2 -> 59.5 us on the large tiles;
       // o and down (128) were 30-40 % slower on them and 9-10 % faster on
       // 256 x 128 than on 128 x 128.
-      // The four-wave forms (_t256, _t256x128) address a tile's activation
-      // rows with 32-bit offsets from its first row, which needs 256 K <
-      // 2^32; wider K takes the eight-wave or 128 x 128 forms.
+      // The 256-row forms (_t256, _t256w8, _t256x128) address a tile's
+      // activation rows with 32-bit offsets from its first row, which needs
+      // 256 K < 2^32; wider K takes the 128 x 128 form.
       const bool offsets32 = k < (int64_t(1) << 24);
-      const int64_t tiles256 = (n % cols256 == 0) ? ((max_tokens + 255) / 256) * (n / cols256) : 0;
+      const int64_t tiles256 = (n % cols256 == 0 && offsets32) ? ((max_tokens + 255) / 256) * (n / cols256) : 0;
       const int64_t tiles256x128 = !gate_up && offsets32 ? ((max_tokens + 255) / 256) * (n / cols128) : 0;
-      const bool big = tiles256 >= 192, four_wave = tiles256 >= 256 && offsets32;
+      const bool big = tiles256 >= 192, four_wave = tiles256 >= 256;
       const bool wide128 = !big && tiles256x128 >= 128 && tiles256x128 <= 256;
       const int64_t tiles = big ? tiles256 : wide128 ? tiles256x128 : ((max_tokens + 127) / 128) * (n / cols128);
       if (tiles > INT32_MAX) return LF_INVALID_ARGUMENT;
@@ -647,8 +647,11 @@ int32_t lunaflux_fp8_moe_launch_geometry(int32_t entry, const lf_fp8_moe_desc *d
   // once per 256 rows), smaller ones on 128 x 128 tiles.
   // Block-scaled profiles too, for K <= 3072 in both GEMMs (their row-ratio
   // table shares the LDS with the stage ring).
+  // Their activation rows are addressed by 32-bit offsets into the token
+  // and assignment arrays: A rows x max(H, I) < 2^32.
   const bool t256 = A >= 256 * static_cast<int64_t>(d->experts) && d->inter % 128 == 0 &&
-                    d->hidden % 256 == 0 && (!b128 || (d->hidden <= 3072 && d->inter <= 3072));
+                    d->hidden % 256 == 0 && (!b128 || (d->hidden <= 3072 && d->inter <= 3072)) &&
+                    A * std::max<int64_t>(d->hidden, d->inter) < (int64_t(1) << 32);
   const int64_t tiles256 = A / 256 + d->experts;
   // Profiles of at most 32 tokens (every expert <= 32 rows) run the grouped
   // GEMV form: a fixed grid (up to 4 blocks per CU) whose blocks loop over

@@ -212,12 +212,13 @@ def test_launch_geometry():
     dims, sym = fp8.launch_geometry(_abi.ENTRY_W8A8_DENSE, 128 * 33, 4096, 8192)
     assert sym == "lf_fp8_w8a8_dense_t128" and dims.grid == (64 * 33, 1, 1)
     # the four-wave forms take 32-bit activation offsets from a tile's first
-    # row (256 K < 2^32): from K = 2^24 the eight-wave or 128 x 128 forms
+    # row (256 K < 2^32), as does the eight-wave form: from K = 2^24 the
+    # 128 x 128 form
     big_k = 1 << 24
     assert fp8.launch_geometry(_abi.ENTRY_W8A8_DENSE, 8192, big_k - 128, 2048)[1] == "lf_fp8_w8a8_dense_t256"
-    dims, sym = fp8.launch_geometry(_abi.ENTRY_W8A8_DENSE, 8192, big_k, 2048)
-    assert sym == "lf_fp8_w8a8_dense_t256w8" and dims.block == (512, 1, 1)
-    assert fp8.launch_geometry(_abi.ENTRY_W8A8_DENSE, 4096, big_k, 2048)[1] == "lf_fp8_w8a8_dense_t128"
+    assert fp8.launch_geometry(_abi.ENTRY_W8A8_DENSE, 8192, big_k - 128, 1536)[1] == "lf_fp8_w8a8_dense_t256w8"
+    for n, m in ((8192, 2048), (8192, 1536), (4096, 2048)):
+        assert fp8.launch_geometry(_abi.ENTRY_W8A8_DENSE, n, big_k, m)[1] == "lf_fp8_w8a8_dense_t128"
     dims, sym = fp8.launch_geometry(_abi.ENTRY_ACT_QUANT_ROWS, 4096, 4096, 2048)
     assert sym == "lf_fp8_act_quant_rows" and dims.grid == (2048 // 4, 1, 1)  # one wave per row
     with pytest.raises(fp8.DeviceError):
@@ -296,6 +297,11 @@ def test_moe_descriptor_layout_and_geometry():
     assert dims.block == (512, 1, 1)
     dims, sym = moe.launch_geometry(6, d, 1024)   # down
     assert sym == "lf_moe_down_t256" and dims.grid == (4096 // 256 * (a // 256 + 8), 1, 1)
+    # the 256-row forms take 32-bit activation offsets: assignments x max(H, I)
+    # must stay below 2^32 (here from 149,797 tokens at k = 2, I = 14336)
+    for t, t256 in ((149796, True), (149797, False)):
+        name = moe.launch_geometry(4, d, t)[1]
+        assert (name == "lf_moe_gate_up_t256") == t256, (t, name)
     # fewer rows per expert: 128 x 128 tiles over (64 h-column block, 128-row tile)
     dims, sym = moe.launch_geometry(4, d, 512)
     assert sym == "lf_moe_gate_up" and dims.grid == (14336 // 64 * (512 * 2 // 128 + 8), 1, 1)
