@@ -437,6 +437,7 @@ __device__ __forceinline__ void w8a8_v4_kernel(const int32_t *counts, const uint
   if (!dense_regions_ok<MODE>(w0, w1, w2)) return;
   const int K = static_cast<int>(h0.columns);
   const int KT = K >> 7;
+  if (K >= (1 << 24)) return;  // 32-bit activation offsets (the geometry never picks this form)
   const int M = live_rows(counts, 1 << 30);
   const int tq = static_cast<int>(h0.rows) >> 4;
   const int tk = MODE == 1 ? static_cast<int>(header_of(w1).rows) >> 4 : 0;
@@ -575,6 +576,7 @@ __device__ __forceinline__ void w8a8_v5_kernel(const int32_t *counts, const uint
   if (!dense_regions_ok<MODE>(w0, w1, w2)) return;
   const int K = static_cast<int>(h0.columns);
   const int KT = K >> 7;
+  if (K >= (1 << 24)) return;  // 32-bit activation offsets (the geometry never picks this form)
   const int M = live_rows(counts, 1 << 30);
   const int tq = static_cast<int>(h0.rows) >> 4;
   const int tk = MODE == 1 ? static_cast<int>(header_of(w1).rows) >> 4 : 0;
