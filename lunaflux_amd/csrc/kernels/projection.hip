@@ -126,6 +126,13 @@ LF_DEVICE float quantize_row_wave(const uint16_t *src_row, int K, uint8_t *dst_r
   return quantize_row_wave_2pass(src_row, K, dst_row, scale);
 }
 
+// v of the lane that DPP control CTRL selects within this lane's row of 16
+// (every lane of the wave active).
+template <int CTRL>
+LF_DEVICE float dpp_f32(float v) {
+  return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, 0xf, 0xf, false));
+}
+
 // Per-128-column-group quantizer: the 16 lanes 16q..16q+15 of a wave hold
 // one group's 16 chunks, so a wave quantizes a quad of four groups (of the
 // rows x (K / 128) groups, row-major) at a time, amax reduced across its 16
@@ -153,8 +160,14 @@ LF_DEVICE void quantize_groups_wave(const uint16_t *src, int K, int rows, uint8_
 #pragma unroll
     for (int b = 0; b < kBatch; ++b) {
       float amax = bf16x8_amax(v[b], 0.0f);
-#pragma unroll
-      for (int off = 8; off > 0; off >>= 1) amax = fmaxf(amax, __shfl_xor(amax, off));
+      // maximum over the 16 lanes of the DPP row: swaps within quads, then
+      // the other quad of the half-row (mirror), then the other half-row
+      // (mirror); register-to-register, where a shuffle goes through LDS.
+      // The maximum is the same in any order.
+      amax = fmaxf(amax, dpp_f32<0xB1>(amax));   // quad_perm [1, 0, 3, 2]
+      amax = fmaxf(amax, dpp_f32<0x4E>(amax));   // quad_perm [2, 3, 0, 1]
+      amax = fmaxf(amax, dpp_f32<0x141>(amax));  // row_half_mirror
+      amax = fmaxf(amax, dpp_f32<0x140>(amax));  // row_mirror
       const bool zero = amax == 0.0f;
       const float ratio = zero ? 0.0f : 448.0f / amax;
       if (gid[b] < groups) {
