@@ -137,9 +137,11 @@ int32_t lunaflux_fp8_unpack_weight(const uint8_t *region, int64_t region_bytes,
  * The W8A8 forms take xq (the quantizer's output) in place of x. xq layout:
  * e4m3 codes [M, K] at offset 0, fp32 row scales at offset
  * align256(M * K); its size for a profile is lunaflux_fp8_act_quant_bytes.
- * GatedMlp (model/plan/plan.mbt:47-59) runs as gate_up into the workspace
- * followed by dense(down) from it, or as one W8A16 launch where an entry is
- * built (lunaflux_fp8_gated_mlp_geometry).
+ * The _aq forms (below) take x and quantize it inside the same launch.
+ * GatedMlp (model/plan/plan.mbt:47-59) runs as one launch
+ * (lunaflux_fp8_gated_mlp_geometry: W8A16 at the Llama-3-8B widths, W8A8
+ * for any width), or as gate_up into the workspace followed by dense(down)
+ * from it.
  */
 #define LF_FP8_COUNTS_QUERY_TOKENS 3
 #define LF_FP8_COUNTS_BYTES 20
@@ -162,8 +164,36 @@ enum lf_fp8_entry {
   LF_FP8_ENTRY_W8A8_GATE_UP = 7,
   LF_FP8_ENTRY_RMS_NORM_QUANT_ROWS = 8,
   LF_FP8_ENTRY_GROUPED = 9, /* admission only: the MoE expert weights */
-  LF_FP8_ENTRY_W8A16_GATED_MLP = 10
+  LF_FP8_ENTRY_W8A16_GATED_MLP = 10,
+  /* W8A8 operations as one launch each, the per-token quantizer inside */
+  LF_FP8_ENTRY_W8A8_DENSE_AQ = 11,
+  LF_FP8_ENTRY_W8A8_QKV_AQ = 12,
+  LF_FP8_ENTRY_W8A8_GATE_UP_AQ = 13,
+  LF_FP8_ENTRY_W8A8_GATED_MLP = 14
 };
+
+/* One launch per W8A8 operation (the plan binds one AOT entry point per
+ * operation, kernels/launch_contract/types.mbt:16-27, and rejects a second
+ * contract for the same (profile, operation), paged_admit.mbt:275-279):
+ *  lf_fp8_w8a8_{dense,qkv,gate_up}_{t256,t256x128,t256w8,t128}_aq
+ *      (counts, x, w..., y, ws)   operands as the W8A16 forms: x bf16 [M, K]
+ * The grid's first 256 blocks quantize x per token (the codes and scales of
+ * lf_fp8_act_quant_rows) into ws; the GEMM's tiles follow, each starting
+ * once every row of its band is quantized (counted, bounded waits: see the
+ * error word below). Same outputs as the act-quant launch followed by the
+ * GEMM-only entry of the same tile form. Geometry and symbol from
+ * lunaflux_fp8_launch_geometry / lunaflux_fp8_qkv_launch_geometry with the
+ * _AQ entry; ws: lunaflux_fp8_w8a8_workspace_bytes bytes (-1 if the shape
+ * has no form), zero-filled once when allocated.
+ * Workspace of every one-launch entry with counted waits (these and the
+ * W8A8 GatedMlp): it starts with a sync area whose first int32 is the error
+ * word, 0 after every correct launch; 1 if a wait ran out (never on a
+ * correct launch; the polls are bounded, so no launch hangs). Once it is
+ * set, launches on that workspace store nothing until the caller
+ * zero-fills the workspace again (its counters are then not at rest).
+ * Launches sharing one ws must not overlap. */
+#define LF_FP8_AQ_ERROR_OFFSET 0
+int64_t lunaflux_fp8_w8a8_workspace_bytes(int32_t entry, int64_t n, int64_t k, int32_t max_tokens);
 
 /* Admission of one weight operand's region before an operation is bound,
  * the FP8 counterpart of the exact BF16 size check engine/device_plan applies
@@ -230,6 +260,15 @@ int64_t lunaflux_fp8_qkv_w8a16_workspace_bytes(int64_t nq, int64_t nkv, int64_t 
  * last gate/up block counts itself), so this entry is for callers that need
  * the operation as a single launch. */
 #define LF_FP8_GATED_MLP_ERROR_OFFSET_FROM_END 128
+/* With entry LF_FP8_ENTRY_W8A8_GATED_MLP (any H, I that are multiples of
+ * 128, any profile): the W8A8 GatedMlp in one launch,
+ *  lf_fp8_w8a8_gated_mlp_{t256_t256,t256_t256x128,t128_t128}
+ *      (counts, x, wg, wu, wd, y, ws)   x, y bf16 [M, H]
+ * the act-quant, gate/up (SwiGLU, h rounded to bf16), act-quant of h and
+ * down launches as four counted steps of one grid (gate/up and down tile
+ * forms in the name), with the same outputs. ws as for the _AQ entries
+ * (error word at offset LF_FP8_AQ_ERROR_OFFSET), sized by
+ * lunaflux_fp8_gated_mlp_workspace_bytes with this entry. */
 int32_t lunaflux_fp8_gated_mlp_geometry(int32_t entry, int64_t hidden, int64_t inter,
                                         int32_t max_tokens, int32_t dims[7],
                                         char symbol[LF_FP8_SYMBOL_BYTES]);

@@ -53,7 +53,12 @@ ENTRY_W8A8_GATE_UP = 7
 ENTRY_RMS_NORM_QUANT_ROWS = 8
 ENTRY_GROUPED = 9
 ENTRY_W8A16_GATED_MLP = 10
+ENTRY_W8A8_DENSE_AQ = 11
+ENTRY_W8A8_QKV_AQ = 12
+ENTRY_W8A8_GATE_UP_AQ = 13
+ENTRY_W8A8_GATED_MLP = 14
 LF_FP8_GATED_MLP_ERROR_OFFSET_FROM_END = 128
+LF_FP8_AQ_ERROR_OFFSET = 0
 
 _vp = ctypes.c_void_p
 _i32 = ctypes.c_int32
@@ -109,6 +114,7 @@ SIGNATURES = {
     "lunaflux_fp8_unpack_weight": (_i32, [_u8p, _i64, _u8p, _i64, _f32p, _i64]),
     "lunaflux_fp8_act_quant_bytes": (_i64, [_i64, _i64]),
     "lunaflux_fp8_w8a16_workspace_bytes": (_i64, [_i32, _i64, _i64, _i32]),
+    "lunaflux_fp8_w8a8_workspace_bytes": (_i64, [_i32, _i64, _i64, _i32]),
     "lunaflux_fp8_launch_geometry": (_i32, [_i32, _i64, _i64, _i32, _i32p, ctypes.c_char_p]),
     "lunaflux_fp8_gated_mlp_geometry": (_i32, [_i32, _i64, _i64, _i32, _i32p, ctypes.c_char_p]),
     "lunaflux_fp8_gated_mlp_workspace_bytes": (_i64, [_i32, _i64, _i64, _i32]),

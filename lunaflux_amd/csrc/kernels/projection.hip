@@ -55,7 +55,27 @@ LF_DEVICE void opaque(u32x4 &x) { asm volatile("" : "+v"(x)); }
 // 16-byte chunks l, l + 64, ..., l + 64 (C - 1) (rows of up to 512 C
 // columns), so the row is read from memory once with all of its loads in
 // flight; then the wave's amax and the encode from registers.
-template <int C>
+// THROUGH: codes and scale are stored through the XCD's L2 (agent-scope
+// atomic stores, phases.h), for rows that blocks of the same launch read.
+template <bool THROUGH>
+LF_DEVICE void store_codes8(uint8_t *p, uint32_t lo, uint32_t hi) {
+  if constexpr (THROUGH) {
+    __hip_atomic_store(reinterpret_cast<uint64_t *>(p), (static_cast<uint64_t>(hi) << 32) | lo,
+                       __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  } else {
+    *reinterpret_cast<uint2 *>(p) = make_uint2(lo, hi);
+  }
+}
+template <bool THROUGH>
+LF_DEVICE void store_scale(float *p, float v) {
+  if constexpr (THROUGH) {
+    __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  } else {
+    *p = v;
+  }
+}
+
+template <int C, bool THROUGH = false>
 LF_DEVICE float quantize_row_wave_regs(const uint16_t *src_row, int K, uint8_t *dst_row,
                                        float *scale) {
   const int lane = threadIdx.x & 63;
@@ -77,8 +97,6 @@ LF_DEVICE float quantize_row_wave_regs(const uint16_t *src_row, int K, uint8_t *
   amax = wave_max(amax);
   const bool zero = amax == 0.0f;
   const float ratio = zero ? 0.0f : 448.0f / amax;
-  typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
-  u32x2 *dst = reinterpret_cast<u32x2 *>(dst_row);
   // The encode converts the raw chunks again rather than keeping the 8 C
   // floats of the amax pass alive (an empty asm that "redefines" each chunk
   // keeps the compiler from reusing them; 8 C floats would not fit).
@@ -87,15 +105,16 @@ LF_DEVICE float quantize_row_wave_regs(const uint16_t *src_row, int K, uint8_t *
     const int idx = lane + 64 * c;
     const uint32_t lo = e4m3x4_from_bf16(v[c][0], v[c][1], ratio);
     const uint32_t hi = e4m3x4_from_bf16(v[c][2], v[c][3], ratio);
-    if (idx < chunks) dst[idx] = u32x2{zero ? 0u : lo, zero ? 0u : hi};
+    if (idx < chunks) store_codes8<THROUGH>(dst_row + 8 * idx, zero ? 0u : lo, zero ? 0u : hi);
   });
   const float sc = zero ? 0.0f : amax / 448.0f;
-  if (lane == 0) *scale = sc;
+  if (lane == 0) store_scale<THROUGH>(scale, sc);
   return sc;
 }
 
 // Per-token quantizer for rows longer than the register-resident forms: two
 // passes over the row (amax, then encode); the second re-reads it from cache.
+template <bool THROUGH = false>
 LF_DEVICE float quantize_row_wave_2pass(const uint16_t *src_row, int K, uint8_t *dst_row,
                                         float *scale) {
   const int lane = threadIdx.x & 63;
@@ -107,23 +126,28 @@ LF_DEVICE float quantize_row_wave_2pass(const uint16_t *src_row, int K, uint8_t 
   amax = wave_max(amax);
   const bool zero = amax == 0.0f;
   const float ratio = zero ? 0.0f : 448.0f / amax;
-  uint2 *dst = reinterpret_cast<uint2 *>(dst_row);
 #pragma unroll 8
-  for (int c = lane; c < chunks; c += 64) dst[c] = bf16x8_encode(src[c], ratio, zero);
+  for (int c = lane; c < chunks; c += 64) {
+    const uint2 e = bf16x8_encode(src[c], ratio, zero);
+    store_codes8<THROUGH>(dst_row + 8 * c, e.x, e.y);
+  }
   const float sc = zero ? 0.0f : amax / 448.0f;
-  if (lane == 0) *scale = sc;
+  if (lane == 0) store_scale<THROUGH>(scale, sc);
   return sc;
 }
 
 // One wave per row, the register-resident form sized for the row (K is
 // wave-uniform, so the branch is too). Returns the row's scale in every
 // lane after lane 0 has stored it. Same arithmetic in every form.
+// MAXC: the widest register-resident form (chunks per lane) the caller's
+// register budget allows; wider rows take the two-pass form.
+template <bool THROUGH = false, int MAXC = 32>
 LF_DEVICE float quantize_row_wave(const uint16_t *src_row, int K, uint8_t *dst_row,
                                   float *scale) {
-  if (K <= 4096) return quantize_row_wave_regs<8>(src_row, K, dst_row, scale);
-  if (K <= 8192) return quantize_row_wave_regs<16>(src_row, K, dst_row, scale);
-  if (K <= 16384) return quantize_row_wave_regs<32>(src_row, K, dst_row, scale);
-  return quantize_row_wave_2pass(src_row, K, dst_row, scale);
+  if (K <= 4096) return quantize_row_wave_regs<8, THROUGH>(src_row, K, dst_row, scale);
+  if (MAXC >= 16 && K <= 8192) return quantize_row_wave_regs<16, THROUGH>(src_row, K, dst_row, scale);
+  if (MAXC >= 32 && K <= 16384) return quantize_row_wave_regs<32, THROUGH>(src_row, K, dst_row, scale);
+  return quantize_row_wave_2pass<THROUGH>(src_row, K, dst_row, scale);
 }
 
 // v of the lane that DPP control CTRL selects within this lane's row of 16
@@ -307,6 +331,39 @@ LF_DEVICE void rms_norm_quant_rows(const int32_t *counts, const uint16_t *x,
 }
 
 // ---------------------------------------------------------------------------
+// Pieces shared by the W8A8 GEMM bodies below.
+// ---------------------------------------------------------------------------
+// Gate of a GEMM tile: called with the tile's first row before any of its
+// activation rows or row scales is read; false means the tile is not
+// computed and nothing is stored (Open: every tile runs).
+struct Open {
+  LF_DEVICE bool operator()(int) const { return true; }
+};
+
+// Output row width: N (dense, gate/up: I) or Nq + Nk + Nv (QKV).
+template <int MODE>
+LF_DEVICE int dense_ld(const uint8_t *w0, const uint8_t *w1, const uint8_t *w2) {
+  return MODE == 1 ? static_cast<int>(header_of(w0).rows + header_of(w1).rows + header_of(w2).rows)
+                   : static_cast<int>(header_of(w0).rows);
+}
+// Column blocks of a BN-wide tile (gate/up: BN / 2 h-columns per block).
+template <int MODE, int BN>
+LF_DEVICE int dense_gx(int ld) {
+  return MODE == 2 ? ld / (BN / 2) : ld / BN;
+}
+
+// Writes bf16 NaN over the live rows of output tile (m0, bx): a 256-row
+// form bound to a weight it cannot address (K >= 2^24).
+template <int MODE, int BN>
+LF_DEVICE void poison_tile(uint16_t *y, int ld, int M, int m0, int BM, int bx) {
+  constexpr int cols = MODE == 2 ? BN / 2 : BN;
+  const int rows = M - m0 < BM ? M - m0 : BM;
+  for (int e = threadIdx.x; e < rows * cols; e += blockDim.x) {
+    y[static_cast<uint64_t>(m0 + e / cols) * ld + bx * cols + e % cols] = 0x7FC0u;
+  }
+}
+
+// ---------------------------------------------------------------------------
 // W8A8 GEMM: xq [M, K] e4m3 with per-token scales (the quantizer's output) x
 // weights with per-channel scales, y = bf16(acc * sa[m] * sw[n]). MODE 0:
 // dense, 1: qkv (three weights, packed Q|K|V columns), 2: gate/up with the
@@ -320,24 +377,28 @@ LF_DEVICE void rms_norm_quant_rows(const int32_t *counts, const uint16_t *x,
 // lane. Rows past the live M load a valid row (the last live one); their
 // results are never stored.
 // ---------------------------------------------------------------------------
-template <class T, int GROUP, int MODE>
-__device__ __forceinline__ void w8a8_tiled_kernel(const int32_t *counts, const uint8_t *xq, const uint8_t *w0,
-                                  const uint8_t *w1, const uint8_t *w2, uint16_t *y) {
+template <class T, int GROUP, int MODE, bool THROUGH = false, class Gate = Open>
+__device__ __forceinline__ int w8a8_tiled_kernel(uint8_t *smem, const int32_t *counts, const uint8_t *xq,
+                                                 const uint8_t *w0, const uint8_t *w1, const uint8_t *w2,
+                                                 uint16_t *y, int bid = -1, int capacity = 1 << 30,
+                                                 const Gate &gate = Gate{}) {
   constexpr int BM = T::kWaveM * T::kWgm, BN = T::kWaveN * T::kWgn;
-  __shared__ __attribute__((aligned(1024))) uint8_t smem[T::kSmem];
   const WeightHeader &h0 = header_of(w0);
-  if (!dense_regions_ok<MODE>(w0, w1, w2)) return;
+  if (!dense_regions_ok<MODE>(w0, w1, w2)) return -1;
   const int K = static_cast<int>(h0.columns);
   const int KT = K >> 7;
-  const int M = live_rows(counts, 1 << 30);
+  const int M = live_rows(counts, capacity);
   const int tq = static_cast<int>(h0.rows) >> 4;
   const int tk = MODE == 1 ? static_cast<int>(header_of(w1).rows) >> 4 : 0;
-  const int ld = MODE == 1 ? static_cast<int>(h0.rows + header_of(w1).rows + header_of(w2).rows)
-                           : static_cast<int>(h0.rows);
-  const int gx = MODE == 2 ? ld / (BN / 2) : ld / BN;
+  const int ld = dense_ld<MODE>(w0, w1, w2);
+  const int gx = dense_gx<MODE, BN>(ld);
   int bx, by;
-  if (!w8a8v3::tile_of_block(gx, (M + BM - 1) / BM, GROUP, bx, by)) return;
+  if (!w8a8v3::tile_of_block(bid < 0 ? static_cast<int>(blockIdx.x) : bid, gx, (M + BM - 1) / BM, GROUP,
+                             bx, by)) {
+    return -1;
+  }
   const int m0 = by * BM;
+  if (!gate(m0)) return -1;
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int wm = wave / T::kWgn, wn = wave % T::kWgn;
@@ -416,21 +477,28 @@ __device__ __forceinline__ void w8a8_tiled_kernel(const int32_t *counts, const u
       if (m >= M) continue;
       const float sa = sav[i][rr];
       uint16_t *yrow = y + static_cast<uint64_t>(m) * ld;
+      auto put = [&](int col, float v) {
+        const uint16_t bits = static_cast<uint16_t>(f32_to_bf16(v));
+        if constexpr (THROUGH) {
+          __hip_atomic_store(yrow + col, bits, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        } else {
+          yrow[col] = bits;
+        }
+      };
       if (MODE == 2) {
 #pragma unroll
         for (int j = 0; j < T::kFN / 2; ++j) {
           const float gv = acc[i][j][rr] * sa * swv[j];
           const float uv = acc[i][j + T::kFN / 2][rr] * sa * swv[j + T::kFN / 2];
-          yrow[ocol[j] + r] = static_cast<uint16_t>(f32_to_bf16(silu_mul(gv, uv)));
+          put(ocol[j] + r, silu_mul(gv, uv));
         }
       } else {
 #pragma unroll
-        for (int j = 0; j < T::kFN; ++j) {
-          yrow[ocol[j] + r] = static_cast<uint16_t>(f32_to_bf16(acc[i][j][rr] * sa * swv[j]));
-        }
+        for (int j = 0; j < T::kFN; ++j) put(ocol[j] + r, acc[i][j][rr] * sa * swv[j]);
       }
     }
   }
+  return by;
 }
 
 // ---------------------------------------------------------------------------
@@ -441,25 +509,35 @@ __device__ __forceinline__ void w8a8_tiled_kernel(const int32_t *counts, const u
 // wn's 2 kFN tiles are kFN gate tiles followed by the up tiles of the same
 // columns, so 32-column fragment j (gate) pairs with j + kFN / 2 (up).
 // ---------------------------------------------------------------------------
-template <class T, int GROUP, int MODE>
-__device__ __forceinline__ void w8a8_v4_kernel(const int32_t *counts, const uint8_t *xq, const uint8_t *w0,
-                               const uint8_t *w1, const uint8_t *w2, uint16_t *y) {
+template <class T, int GROUP, int MODE, bool THROUGH = false, class Gate = Open>
+__device__ __forceinline__ int w8a8_v4_kernel(uint8_t *smem, const int32_t *counts, const uint8_t *xq,
+                                              const uint8_t *w0, const uint8_t *w1, const uint8_t *w2,
+                                              uint16_t *y, int bid = -1, int capacity = 1 << 30,
+                                              const Gate &gate = Gate{}) {
   constexpr int BM = T::kBM, BN = T::kBN;
-  __shared__ __attribute__((aligned(1024))) uint8_t smem[T::kSmem];
   const WeightHeader &h0 = header_of(w0);
-  if (!dense_regions_ok<MODE>(w0, w1, w2)) return;
+  if (!dense_regions_ok<MODE>(w0, w1, w2)) return -1;
   const int K = static_cast<int>(h0.columns);
   const int KT = K >> 7;
-  if (K >= (1 << 24)) return;  // 32-bit activation offsets (the geometry never picks this form)
-  const int M = live_rows(counts, 1 << 30);
+  const int M = live_rows(counts, capacity);
   const int tq = static_cast<int>(h0.rows) >> 4;
   const int tk = MODE == 1 ? static_cast<int>(header_of(w1).rows) >> 4 : 0;
-  const int ld = MODE == 1 ? static_cast<int>(h0.rows + header_of(w1).rows + header_of(w2).rows)
-                           : static_cast<int>(h0.rows);
-  const int gx = MODE == 2 ? ld / (BN / 2) : ld / BN;
+  const int ld = dense_ld<MODE>(w0, w1, w2);
+  const int gx = dense_gx<MODE, BN>(ld);
   int bx, by;
-  if (!w8a8v3::tile_of_block(gx, (M + BM - 1) / BM, GROUP, bx, by)) return;
+  if (!w8a8v3::tile_of_block(bid < 0 ? static_cast<int>(blockIdx.x) : bid, gx, (M + BM - 1) / BM, GROUP,
+                             bx, by)) {
+    return -1;
+  }
   const int m0 = by * BM;
+  // 32-bit activation offsets need K < 2^24 (the geometry never picks this
+  // form for wider K); a tile bound to such a weight anyway is filled with
+  // NaN rather than left stale.
+  if (K >= (1 << 24)) {
+    poison_tile<MODE, BN>(y, ld, M, m0, BM, bx);
+    return by;
+  }
+  if (!gate(m0)) return -1;
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int wm = wave / T::kWgn, wn = wave % T::kWgn;
@@ -563,10 +641,11 @@ __device__ __forceinline__ void w8a8_v4_kernel(const int32_t *counts, const uint
       }
     }
     const int mw = m0 + wm * T::kWaveM + 32 * i;
-    st.flush(lane, [&](int row) -> uint16_t * {
+    st.template flush<THROUGH>(lane, [&](int row) -> uint16_t * {
       return mw + row < M ? y + static_cast<uint64_t>(mw + row) * ld + col0 : nullptr;
     });
   }
+  return by;
 }
 
 // ---------------------------------------------------------------------------
@@ -580,25 +659,33 @@ __device__ __forceinline__ void w8a8_v4_kernel(const int32_t *counts, const uint
 // output through LDS with one 8-byte write per accumulator and stores whole
 // 16-byte row chunks.
 // ---------------------------------------------------------------------------
-template <class T, int GROUP, int MODE>
-__device__ __forceinline__ void w8a8_v5_kernel(const int32_t *counts, const uint8_t *xq, const uint8_t *w0,
-                                               const uint8_t *w1, const uint8_t *w2, uint16_t *y) {
+template <class T, int GROUP, int MODE, bool THROUGH = false, class Gate = Open>
+__device__ __forceinline__ int w8a8_v5_kernel(uint8_t *smem, const int32_t *counts, const uint8_t *xq,
+                                              const uint8_t *w0, const uint8_t *w1, const uint8_t *w2,
+                                              uint16_t *y, int bid = -1, int capacity = 1 << 30,
+                                              const Gate &gate = Gate{}) {
   constexpr int BM = 256, BN = T::kWaveN * T::kWgn;
-  __shared__ __attribute__((aligned(1024))) uint8_t smem[T::kSmem];
   const WeightHeader &h0 = header_of(w0);
-  if (!dense_regions_ok<MODE>(w0, w1, w2)) return;
+  if (!dense_regions_ok<MODE>(w0, w1, w2)) return -1;
   const int K = static_cast<int>(h0.columns);
   const int KT = K >> 7;
-  if (K >= (1 << 24)) return;  // 32-bit activation offsets (the geometry never picks this form)
-  const int M = live_rows(counts, 1 << 30);
+  const int M = live_rows(counts, capacity);
   const int tq = static_cast<int>(h0.rows) >> 4;
   const int tk = MODE == 1 ? static_cast<int>(header_of(w1).rows) >> 4 : 0;
-  const int ld = MODE == 1 ? static_cast<int>(h0.rows + header_of(w1).rows + header_of(w2).rows)
-                           : static_cast<int>(h0.rows);
-  const int gx = MODE == 2 ? ld / (BN / 2) : ld / BN;
+  const int ld = dense_ld<MODE>(w0, w1, w2);
+  const int gx = dense_gx<MODE, BN>(ld);
   int bx, by;
-  if (!w8a8v3::tile_of_block(gx, (M + BM - 1) / BM, GROUP, bx, by)) return;
+  if (!w8a8v3::tile_of_block(bid < 0 ? static_cast<int>(blockIdx.x) : bid, gx, (M + BM - 1) / BM, GROUP,
+                             bx, by)) {
+    return -1;
+  }
   const int m0 = by * BM;
+  // 32-bit activation offsets need K < 2^24 (as in w8a8_v4_kernel)
+  if (K >= (1 << 24)) {
+    poison_tile<MODE, BN>(y, ld, M, m0, BM, bx);
+    return by;
+  }
+  if (!gate(m0)) return -1;
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int wm = wave / T::kWgn, wn = wave % T::kWgn;
@@ -714,63 +801,58 @@ __device__ __forceinline__ void w8a8_v5_kernel(const int32_t *counts, const uint
       }
     }
     const int mw = m0 + wm * T::kWaveM + kRows * p;
-    st.flush(lane, [&](int row) -> uint16_t * {
+    st.template flush<THROUGH>(lane, [&](int row) -> uint16_t * {
       return mw + row < M ? y + static_cast<uint64_t>(mw + row) * ld + col0 : nullptr;
     });
   }
+  return by;
 }
 
-}  // namespace
-
-extern "C" {
-
-#define LF_W8A8_TILED_ENTRIES(NAME, BM, BN, NS, WGM, WGN, GROUP)                              \
-  __global__ __launch_bounds__(64 * WGM * WGN) void lf_fp8_w8a8_dense_##NAME(                   \
-      const int32_t *counts, const uint8_t *xq, const uint8_t *w, uint16_t *y) {                \
-    w8a8_tiled_kernel<w8a8v3::Tile<BM, BN, NS, WGM, WGN>, GROUP, 0>(counts, xq, w, w, w, y);    \
-  }                                                                                             \
-  __global__ __launch_bounds__(64 * WGM * WGN) void lf_fp8_w8a8_qkv_##NAME(                     \
-      const int32_t *counts, const uint8_t *xq, const uint8_t *wq, const uint8_t *wk,           \
-      const uint8_t *wv, uint16_t *y) {                                                         \
-    w8a8_tiled_kernel<w8a8v3::Tile<BM, BN, NS, WGM, WGN>, GROUP, 1>(counts, xq, wq, wk, wv, y); \
-  }                                                                                             \
-  __global__ __launch_bounds__(64 * WGM * WGN) void lf_fp8_w8a8_gate_up_##NAME(                 \
-      const int32_t *counts, const uint8_t *xq, const uint8_t *wg, const uint8_t *wu,           \
-      uint16_t *h) {                                                                            \
-    w8a8_tiled_kernel<w8a8v3::Tile<BM, BN, NS, WGM, WGN>, GROUP, 2>(counts, xq, wg, wu, wu, h); \
+// ---------------------------------------------------------------------------
+// The W8A8 GEMM forms the launch geometry picks: tile height, block size and
+// LDS of each, and its body.
+// ---------------------------------------------------------------------------
+template <class T, int GROUP>
+struct FormT128 {  // 128 x 128 tiles, 4 waves, two blocks per CU
+  static constexpr int kBM = T::kWaveM * T::kWgm, kBN = T::kWaveN * T::kWgn;
+  static constexpr int kThreads = T::kThreads, kSmem = T::kSmem;
+  // widest register-resident row of an in-launch quantizer (quantize_row_wave):
+  // wider ones would cost this form its second wave per SIMD
+  static constexpr int kQuantChunks = 8;
+  template <int MODE, bool THROUGH = false, class Gate = Open>
+  LF_DEVICE static int run(uint8_t *smem, const int32_t *counts, const uint8_t *xq, const uint8_t *w0,
+                           const uint8_t *w1, const uint8_t *w2, uint16_t *y, int bid = -1,
+                           int capacity = 1 << 30, const Gate &gate = Gate{}) {
+    return w8a8_tiled_kernel<T, GROUP, MODE, THROUGH, Gate>(smem, counts, xq, w0, w1, w2, y, bid, capacity,
+                                                           gate);
   }
-
-#define LF_W8A8_V4_ENTRIES(NAME, BM, BN, NS, WGM, WGN, GROUP)                                 \
-  __global__ __launch_bounds__(64 * WGM * WGN) void lf_fp8_w8a8_dense_##NAME(                   \
-      const int32_t *counts, const uint8_t *xq, const uint8_t *w, uint16_t *y) {                \
-    w8a8_v4_kernel<w8a8v4::Tile<BM, BN, NS, WGM, WGN>, GROUP, 0>(counts, xq, w, w, w, y);       \
-  }                                                                                             \
-  __global__ __launch_bounds__(64 * WGM * WGN) void lf_fp8_w8a8_qkv_##NAME(                     \
-      const int32_t *counts, const uint8_t *xq, const uint8_t *wq, const uint8_t *wk,           \
-      const uint8_t *wv, uint16_t *y) {                                                         \
-    w8a8_v4_kernel<w8a8v4::Tile<BM, BN, NS, WGM, WGN>, GROUP, 1>(counts, xq, wq, wk, wv, y);    \
-  }                                                                                             \
-  __global__ __launch_bounds__(64 * WGM * WGN) void lf_fp8_w8a8_gate_up_##NAME(                 \
-      const int32_t *counts, const uint8_t *xq, const uint8_t *wg, const uint8_t *wu,           \
-      uint16_t *h) {                                                                            \
-    w8a8_v4_kernel<w8a8v4::Tile<BM, BN, NS, WGM, WGN>, GROUP, 2>(counts, xq, wg, wu, wu, h);    \
+};
+template <class T, int GROUP>
+struct FormW8 {  // 256 x 256 tiles on 8 waves, 4-stage half-step ring
+  static constexpr int kBM = T::kBM, kBN = T::kBN;
+  static constexpr int kThreads = T::kThreads, kSmem = T::kSmem;
+  static constexpr int kQuantChunks = 32;
+  template <int MODE, bool THROUGH = false, class Gate = Open>
+  LF_DEVICE static int run(uint8_t *smem, const int32_t *counts, const uint8_t *xq, const uint8_t *w0,
+                           const uint8_t *w1, const uint8_t *w2, uint16_t *y, int bid = -1,
+                           int capacity = 1 << 30, const Gate &gate = Gate{}) {
+    return w8a8_v4_kernel<T, GROUP, MODE, THROUGH, Gate>(smem, counts, xq, w0, w1, w2, y, bid, capacity,
+                                                        gate);
   }
-
-#define LF_W8A8_V5_ENTRIES(NAME, TILE, GROUP)                                                  \
-  __global__ __launch_bounds__(256) void lf_fp8_w8a8_dense_##NAME(                                \
-      const int32_t *counts, const uint8_t *xq, const uint8_t *w, uint16_t *y) {                  \
-    w8a8_v5_kernel<TILE, GROUP, 0>(counts, xq, w, w, w, y);                                       \
-  }                                                                                               \
-  __global__ __launch_bounds__(256) void lf_fp8_w8a8_qkv_##NAME(                                  \
-      const int32_t *counts, const uint8_t *xq, const uint8_t *wq, const uint8_t *wk,             \
-      const uint8_t *wv, uint16_t *y) {                                                           \
-    w8a8_v5_kernel<TILE, GROUP, 1>(counts, xq, wq, wk, wv, y);                                    \
-  }                                                                                               \
-  __global__ __launch_bounds__(256) void lf_fp8_w8a8_gate_up_##NAME(                              \
-      const int32_t *counts, const uint8_t *xq, const uint8_t *wg, const uint8_t *wu,             \
-      uint16_t *h) {                                                                              \
-    w8a8_v5_kernel<TILE, GROUP, 2>(counts, xq, wg, wu, wu, h);                                    \
+};
+template <class T, int GROUP>
+struct FormV5 {  // 256 x 256 / 256 x 128 tiles on 4 waves
+  static constexpr int kBM = 256, kBN = T::kWaveN * T::kWgn;
+  static constexpr int kThreads = T::kThreads, kSmem = T::kSmem;
+  static constexpr int kQuantChunks = 32;
+  template <int MODE, bool THROUGH = false, class Gate = Open>
+  LF_DEVICE static int run(uint8_t *smem, const int32_t *counts, const uint8_t *xq, const uint8_t *w0,
+                           const uint8_t *w1, const uint8_t *w2, uint16_t *y, int bid = -1,
+                           int capacity = 1 << 30, const Gate &gate = Gate{}) {
+    return w8a8_v5_kernel<T, GROUP, MODE, THROUGH, Gate>(smem, counts, xq, w0, w1, w2, y, bid, capacity,
+                                                        gate);
   }
+};
 
 // Production tiles (lunaflux_fp8_launch_geometry picks): 256 x 256 on four
 // waves (_t256) wherever a launch has at least one tile per CU; 256 x 256 on
@@ -783,10 +865,219 @@ extern "C" {
 // against 38.9 / 121.0 us on 128 x 128; QKV at M = 1024 34.0 against 38.5;
 // gate/up ran 10-18 % slower on it than on 256 x 256); 128 x 128 (4 waves,
 // two blocks per CU) otherwise.
-LF_W8A8_V5_ENTRIES(t256, w8a8v5::Tile, 4)
-LF_W8A8_V5_ENTRIES(t256x128, w8a8v5::TileN128, 4)
-LF_W8A8_V4_ENTRIES(t256w8, 256, 256, 4, 4, 2, 4)
-LF_W8A8_TILED_ENTRIES(t128, 128, 128, 2, 2, 2, 4)
+using GemmT256 = FormV5<w8a8v5::Tile, 4>;
+using GemmT256x128 = FormV5<w8a8v5::TileN128, 4>;
+using GemmT256w8 = FormW8<w8a8v4::Tile<256, 256, 4, 4, 2>, 4>;
+using GemmT128 = FormT128<w8a8v3::Tile<128, 128, 2, 2, 2>, 4>;
+
+// ---------------------------------------------------------------------------
+// One launch per W8A8 operation. The plan binds each operation to one AOT
+// entry point (kernels/launch_contract/types.mbt:16-27), and the operation's
+// input is the bf16 activation, so the per-token quantizer runs inside the
+// launch: the grid is kQuantBlocks quantizer blocks followed by the GEMM's
+// blocks, and a GEMM tile starts its loads once every 16-row chunk of its
+// row band is quantized (phases.h). Quantizer block q takes chunks q,
+// q + kQuantBlocks, ...; each wave of it quantizes 16 / waves rows of a
+// chunk with the standalone quantizer's code (same codes and scales), its
+// stores written through to memory, then the block counts the chunk into
+// its band's counter.
+// Workspace: the sync area (phases.h, one step of bands = ceil(max_tokens /
+// BM) counters) followed by the quantized rows in the layout of
+// lf_fp8_act_quant_rows' output (codes [M, K], fp32 scales at
+// align256(M K)); bands = (gridDim.x - kQuantBlocks) / column blocks.
+// ---------------------------------------------------------------------------
+constexpr int kQuantBlocks = 256;
+constexpr int kChunkRows = 16;
+
+LF_DEVICE int chunks_in_band(int M, int band, int BM) {
+  const int rows = M - band * BM < BM ? M - band * BM : BM;
+  return rows <= 0 ? 0 : (rows + kChunkRows - 1) / kChunkRows;
+}
+
+template <class F>
+LF_DEVICE void quantize_chunk(const uint16_t *x, int K, int M, int c, uint8_t *xq, float *scales) {
+  constexpr int R = kChunkRows / (F::kThreads / 64);
+  const int wave = static_cast<int>(threadIdx.x) >> 6;
+#pragma unroll 1
+  for (int i = 0; i < R; ++i) {
+    const int row = c * kChunkRows + wave * R + i;
+    if (row < M) {
+      quantize_row_wave<true, F::kQuantChunks>(x + static_cast<uint64_t>(row) * K, K,
+                                               xq + static_cast<uint64_t>(row) * K, scales + row);
+    }
+  }
+}
+
+template <class F, int MODE>
+LF_DEVICE void w8a8_one_launch(const int32_t *counts, const uint16_t *x, const uint8_t *w0,
+                               const uint8_t *w1, const uint8_t *w2, uint16_t *y, uint8_t *ws) {
+  __shared__ __attribute__((aligned(1024))) uint8_t smem[F::kSmem];
+  __shared__ phase::Flag flag;
+  if (!dense_regions_ok<MODE>(w0, w1, w2)) return;
+  const int K = static_cast<int>(header_of(w0).columns);
+  const int gx = dense_gx<MODE, F::kBN>(dense_ld<MODE>(w0, w1, w2));
+  const int blocks = static_cast<int>(gridDim.x) - kQuantBlocks;
+  if (gx <= 0 || blocks <= 0 || blocks % gx != 0) return;  // not a grid of this entry's geometry
+  const int bands = blocks / gx;
+  const phase::Sync sync{reinterpret_cast<int *>(ws), bands};
+  uint8_t *xq = ws + phase::sync_bytes(1, bands);
+  const int cap = bands * F::kBM;
+  const int M = live_rows(counts, cap);
+  if (phase::failed(sync, flag)) return;
+  const int b = static_cast<int>(blockIdx.x);
+  if (b < kQuantBlocks) {
+    float *scales = reinterpret_cast<float *>(xq + align256(static_cast<uint64_t>(M) * K));
+    const int chunks = (M + kChunkRows - 1) / kChunkRows;
+    for (int c = b; c < chunks; c += kQuantBlocks) {
+      quantize_chunk<F>(x, K, M, c, xq, scales);
+      phase::signal(sync.band(0, c * kChunkRows / F::kBM));
+    }
+    return;
+  }
+  const auto gate = [&](int m0) {
+    const int band = m0 / F::kBM;
+    return phase::wait_for(sync, sync.band(0, band), chunks_in_band(M, band, F::kBM), flag);
+  };
+  F::template run<MODE>(smem, counts, xq, w0, w1, w2, y, b - kQuantBlocks, cap, gate);
+  phase::finish(sync, blocks, 1, flag);
+}
+
+// ---------------------------------------------------------------------------
+// W8A8 GatedMlp in one launch (model/plan/plan.mbt:47-59;
+// kernels/reference/mlp.mbt:4-39): x -> xq (per token) -> gate/up + SwiGLU ->
+// h (bf16) -> hq (per token) -> down -> y, the same arithmetic as the
+// act-quant, gate/up, act-quant and dense launches, as four steps of one
+// grid: [kQuantBlocks x quantizer][gate/up tiles][kQuantBlocks h quantizer]
+// [down tiles]. Gate/up tiles wait for their band's x chunks and write h
+// through to memory; an h-quantizer chunk waits for every gate/up tile of its
+// band; down tiles wait for their band's h chunks. Both GEMMs use the same
+// band height and block size (GU::kBM, kThreads).
+// Workspace: sync area (three steps of bands counters), xq for cap = bands
+// BM rows (act-quant layout, K = H), h bf16 [cap, I], hq (act-quant layout,
+// K = I); bands = (gridDim.x - 2 kQuantBlocks) / (gate/up + down column
+// blocks).
+// ---------------------------------------------------------------------------
+template <class GU, class DN>
+LF_DEVICE void w8a8_gated_mlp(const int32_t *counts, const uint16_t *x, const uint8_t *wg,
+                              const uint8_t *wu, const uint8_t *wd, uint16_t *y, uint8_t *ws) {
+  static_assert(GU::kBM == DN::kBM && GU::kThreads == DN::kThreads, "one band height, one block size");
+  constexpr int BM = GU::kBM;
+  constexpr int kSmem = GU::kSmem > DN::kSmem ? GU::kSmem : DN::kSmem;
+  __shared__ __attribute__((aligned(1024))) uint8_t smem[kSmem];
+  __shared__ phase::Flag flag;
+  if (!dense_regions_ok<2>(wg, wu, wu) || !dense_regions_ok<0>(wd, wd, wd)) return;
+  const int H = static_cast<int>(header_of(wg).columns), I = static_cast<int>(header_of(wg).rows);
+  if (static_cast<int>(header_of(wd).columns) != I || static_cast<int>(header_of(wd).rows) != H) return;
+  const int gx1 = dense_gx<2, GU::kBN>(I), gx2 = dense_gx<0, DN::kBN>(H);
+  const int blocks = static_cast<int>(gridDim.x) - 2 * kQuantBlocks;
+  if (gx1 <= 0 || gx2 <= 0 || blocks <= 0 || blocks % (gx1 + gx2) != 0) return;
+  const int bands = blocks / (gx1 + gx2);
+  const phase::Sync sync{reinterpret_cast<int *>(ws), bands};
+  const int cap = bands * BM;
+  const uint64_t xq_bytes = align256(static_cast<uint64_t>(cap) * H) + align256(static_cast<uint64_t>(cap) * 4);
+  const uint64_t h_bytes = align256(static_cast<uint64_t>(cap) * I * 2);
+  uint8_t *xq = ws + phase::sync_bytes(3, bands);
+  uint16_t *h = reinterpret_cast<uint16_t *>(xq + xq_bytes);
+  uint8_t *hq = xq + xq_bytes + h_bytes;
+  const int M = live_rows(counts, cap);
+  if (phase::failed(sync, flag)) return;
+  const int chunks = (M + kChunkRows - 1) / kChunkRows;
+  int b = static_cast<int>(blockIdx.x);
+  if (b < kQuantBlocks) {  // step 0: x -> xq
+    float *scales = reinterpret_cast<float *>(xq + align256(static_cast<uint64_t>(M) * H));
+    for (int c = b; c < chunks; c += kQuantBlocks) {
+      quantize_chunk<GU>(x, H, M, c, xq, scales);
+      phase::signal(sync.band(0, c * kChunkRows / BM));
+    }
+    return;
+  }
+  b -= kQuantBlocks;
+  if (b < gx1 * bands) {  // step 1: gate/up + SwiGLU -> h
+    const auto gate = [&](int m0) {
+      const int band = m0 / BM;
+      return phase::wait_for(sync, sync.band(0, band), chunks_in_band(M, band, BM), flag);
+    };
+    const int band = GU::template run<2, true>(smem, counts, xq, wg, wu, wu, h, b, cap, gate);
+    if (band >= 0) phase::signal(sync.band(1, band));
+    return;
+  }
+  b -= gx1 * bands;
+  if (b < kQuantBlocks) {  // step 2: h -> hq
+    float *scales = reinterpret_cast<float *>(hq + align256(static_cast<uint64_t>(M) * I));
+    for (int c = b; c < chunks; c += kQuantBlocks) {
+      const int band = c * kChunkRows / BM;
+      if (!phase::wait_for(sync, sync.band(1, band), gx1, flag)) return;
+      quantize_chunk<GU>(h, I, M, c, hq, scales);
+      phase::signal(sync.band(2, band));
+    }
+    return;
+  }
+  b -= kQuantBlocks;
+  const auto gate = [&](int m0) {  // step 3: down
+    const int band = m0 / BM;
+    return phase::wait_for(sync, sync.band(2, band), chunks_in_band(M, band, BM), flag);
+  };
+  DN::template run<0>(smem, counts, hq, wd, wd, wd, y, b, cap, gate);
+  phase::finish(sync, gx2 * bands, 3, flag);
+}
+
+}  // namespace
+
+extern "C" {
+
+// GEMM alone over rows already quantized (lf_fp8_act_quant_rows or the fused
+// RmsNorm quantizer): (counts, xq, w..., y). One launch with the quantizer
+// (_aq): (counts, x, w..., y, ws).
+#define LF_W8A8_ENTRIES(NAME, FORM)                                                             \
+  __global__ __launch_bounds__(FORM::kThreads) void lf_fp8_w8a8_dense_##NAME(                  \
+      const int32_t *counts, const uint8_t *xq, const uint8_t *w, uint16_t *y) {                \
+    __shared__ __attribute__((aligned(1024))) uint8_t smem[FORM::kSmem];                        \
+    FORM::template run<0>(smem, counts, xq, w, w, w, y);                                        \
+  }                                                                                             \
+  __global__ __launch_bounds__(FORM::kThreads) void lf_fp8_w8a8_qkv_##NAME(                    \
+      const int32_t *counts, const uint8_t *xq, const uint8_t *wq, const uint8_t *wk,           \
+      const uint8_t *wv, uint16_t *y) {                                                         \
+    __shared__ __attribute__((aligned(1024))) uint8_t smem[FORM::kSmem];                        \
+    FORM::template run<1>(smem, counts, xq, wq, wk, wv, y);                                     \
+  }                                                                                             \
+  __global__ __launch_bounds__(FORM::kThreads) void lf_fp8_w8a8_gate_up_##NAME(                \
+      const int32_t *counts, const uint8_t *xq, const uint8_t *wg, const uint8_t *wu,           \
+      uint16_t *h) {                                                                            \
+    __shared__ __attribute__((aligned(1024))) uint8_t smem[FORM::kSmem];                        \
+    FORM::template run<2>(smem, counts, xq, wg, wu, wu, h);                                     \
+  }                                                                                             \
+  __global__ __launch_bounds__(FORM::kThreads) void lf_fp8_w8a8_dense_##NAME##_aq(             \
+      const int32_t *counts, const uint16_t *x, const uint8_t *w, uint16_t *y, uint8_t *ws) {   \
+    w8a8_one_launch<FORM, 0>(counts, x, w, w, w, y, ws);                                        \
+  }                                                                                             \
+  __global__ __launch_bounds__(FORM::kThreads) void lf_fp8_w8a8_qkv_##NAME##_aq(               \
+      const int32_t *counts, const uint16_t *x, const uint8_t *wq, const uint8_t *wk,           \
+      const uint8_t *wv, uint16_t *y, uint8_t *ws) {                                            \
+    w8a8_one_launch<FORM, 1>(counts, x, wq, wk, wv, y, ws);                                     \
+  }                                                                                             \
+  __global__ __launch_bounds__(FORM::kThreads) void lf_fp8_w8a8_gate_up_##NAME##_aq(           \
+      const int32_t *counts, const uint16_t *x, const uint8_t *wg, const uint8_t *wu,           \
+      uint16_t *h, uint8_t *ws) {                                                               \
+    w8a8_one_launch<FORM, 2>(counts, x, wg, wu, wu, h, ws);                                     \
+  }
+
+LF_W8A8_ENTRIES(t256, GemmT256)
+LF_W8A8_ENTRIES(t256x128, GemmT256x128)
+LF_W8A8_ENTRIES(t256w8, GemmT256w8)
+LF_W8A8_ENTRIES(t128, GemmT128)
+
+// W8A8 GatedMlp in one launch: (counts, x, wg, wu, wd, y, ws), gate/up form
+// then down form in the name.
+#define LF_W8A8_GATED_MLP(NAME, GU, DN)                                                        \
+  __global__ __launch_bounds__(GU::kThreads) void lf_fp8_w8a8_gated_mlp_##NAME(                \
+      const int32_t *counts, const uint16_t *x, const uint8_t *wg, const uint8_t *wu,          \
+      const uint8_t *wd, uint16_t *y, uint8_t *ws) {                                           \
+    w8a8_gated_mlp<GU, DN>(counts, x, wg, wu, wd, y, ws);                                      \
+  }
+
+LF_W8A8_GATED_MLP(t256_t256, GemmT256, GemmT256)
+LF_W8A8_GATED_MLP(t256_t256x128, GemmT256, GemmT256x128)
+LF_W8A8_GATED_MLP(t128_t128, GemmT128, GemmT128)
 
 __global__ __launch_bounds__(256) void lf_fp8_act_quant_rows(const int32_t *counts,
                                                              const uint16_t *x,

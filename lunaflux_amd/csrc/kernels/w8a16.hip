@@ -24,6 +24,7 @@
 // on which block finishes last -- and runs the epilogue (channel scale, SwiGLU
 // for gate/up, bf16 store). No block ever waits for another.
 #include "device_common.h"
+#include "phases.h"
 #include "w8a8_v3.h"
 
 namespace {
@@ -716,14 +717,17 @@ __device__ __forceinline__ void w8a16_fixed_kernel(const int32_t *counts, const 
 // writes (no memory fence), so the weight ring stays in flight across it.
 // ---------------------------------------------------------------------------
 // No wait before the activation loads (see the one-launch GatedMlp below).
+// A wait returns false when the block must not go on (it then loads no
+// activation and stores nothing).
 struct NoWait {
-  LF_DEVICE void operator()(int) const {}
+  LF_DEVICE bool operator()(int) const { return true; }
 };
 
 // bid / nblocks: the block's index and the block count of this kernel's
 // part of the grid (default: blockIdx.x, gridDim.x). wait(s) runs after the
 // weight prologue is in flight and before the first activation load of
-// K-slice s.
+// K-slice s; if it returns false the block returns there (no activation
+// load, no store, no split-K arrival).
 // KROT: each block walks its k-tiles starting at ((block / 8) mod NKT) and
 // wrapping around, instead of at 0. Blocks are dispatched to the 8 XCDs in
 // turn, so the blocks sharing one L2 start at different k-tiles. Unsplit
@@ -826,7 +830,7 @@ __device__ __forceinline__ void w8a16_fixed_group_kernel(const int32_t *counts, 
 #pragma unroll
     for (int j = 0; j < XPW; ++j) dst[j] = *reinterpret_cast<const u32x4 *>(xsrc[j] + kr(k) * 128);
   };
-  wait(s);
+  if (!wait(s)) return;
   u32x4 a[EX][XPW];
 #pragma unroll
   for (int d = 0; d < EX; ++d) load_a(d, a[d]);
@@ -901,33 +905,25 @@ __device__ __forceinline__ void w8a16_fixed_group_kernel(const int32_t *counts, 
 //
 // Blocks are dispatched in index order on each XCD, so every gate/up block
 // has a CU before any down block of its XCD takes one, and gate/up blocks
-// wait for nothing: the polls end. They are bounded all the same (about
-// 2^20 polls, far beyond any real wait): one that runs out sets the error
-// word and goes on, so no launch can hang. The last down block to finish
-// resets the slice counters and its own done counter for the next launch.
+// wait for nothing: the polls end. They are bounded all the same
+// (phases.h: about 2^20 polls, far beyond any real wait): one that runs out
+// sets the error word, and its block returns without loading h or storing
+// anything. The last down block to finish resets the slice counters and its
+// own done counter for the next launch, unless the error word is set; every
+// block of a launch that finds the word set returns at once, so a workspace
+// whose counters are not at rest produces no output until the caller
+// zero-fills it (the host binding does so when it reads the word after a
+// synchronous launch).
 //
 // Workspace: h [16 MT rows][I] bf16 | the down kernel's split-K partials
 // and arrival counters | sync: slice counters [DN_S], done (+64 B), error
-// (+128 B; stays set, 0 on every correct launch).
-constexpr int kGatedSpinLimit = 1 << 20;
-
+// (+128 B; 0 after every correct launch).
 struct SliceWait {
   int *counters;
   int target;
   int *error;
-  LF_DEVICE void operator()(int s) const {
-    if (threadIdx.x == 0) {
-      int spins = 0;
-      while (__hip_atomic_load(counters + s, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) < target) {
-        if (++spins > kGatedSpinLimit) {
-          __hip_atomic_store(error, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-          break;
-        }
-        __builtin_amdgcn_s_sleep(1);
-      }
-    }
-    __syncthreads();
-  }
+  phase::Flag *flag;
+  LF_DEVICE bool operator()(int s) const { return phase::wait_for(counters + s, target, error, *flag); }
 };
 
 template <int H, int I, int MT, int GU_W, int GU_DW, int GU_DX, int DN_S, int DN_W, int DN_DW,
@@ -946,9 +942,12 @@ struct GatedMlpFixed {
 
   LF_DEVICE static void run(const int32_t *counts, const uint16_t *x, const uint8_t *wg,
                             const uint8_t *wu, const uint8_t *wd, uint16_t *y, uint8_t *ws) {
+    __shared__ phase::Flag flag;
     uint16_t *h = reinterpret_cast<uint16_t *>(ws);
     uint8_t *ws_down = ws + kHBytes;
     int *sync = reinterpret_cast<int *>(ws + kHBytes + kDownBytes);
+    int *error = sync + 32;
+    if (phase::failed(error, flag)) return;
     const int b = static_cast<int>(blockIdx.x);
     if (b < kG1) {
       w8a16_fixed_group_kernel<H, 1, GU_W, MT, 2, GU_DW, GU_DX, 0, 0, NoWait, true, true>(
@@ -961,16 +960,14 @@ struct GatedMlpFixed {
       }
       return;
     }
-    const SliceWait wait{sync, kSliceCols / (GU_W * 16), sync + 32};
+    const SliceWait wait{sync, kSliceCols / (GU_W * 16), error, &flag};
     w8a16_fixed_group_kernel<I, DN_S, DN_W, MT, 0, DN_DW, DN_DX, 0, 0, SliceWait>(
         counts, h, wd, wd, wd, y, ws_down, b - kG1, kG2, wait);
     if (threadIdx.x == 0) {
       const int before = __hip_atomic_fetch_add(sync + 16, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-      if (before == kG2 - 1) {
-        for (int s = 0; s < DN_S; ++s) {
-          __hip_atomic_store(sync + s, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        }
-        __hip_atomic_store(sync + 16, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      if (before == kG2 - 1 && phase::load_agent(error) == 0) {
+        for (int s = 0; s < DN_S; ++s) phase::store_agent(sync + s, 0);
+        phase::store_agent(sync + 16, 0);
       }
     }
   }

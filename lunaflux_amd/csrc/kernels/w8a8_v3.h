@@ -227,9 +227,11 @@ LF_DEVICE int acc_row(int wm, int i, int lane, int rr) {
 // `group` row blocks column by column, so the blocks resident on an XCD at
 // one time share few A row strips and weight column strips in its L2.
 // Returns false for blocks with no tile.
-LF_DEVICE bool tile_of_block(int gx, int gy, int group, int &bx, int &by) {
+// b: the block's index in the GEMM's part of the grid (blockIdx.x when the
+// GEMM is the whole grid; a one-launch operation puts other steps' blocks
+// first, in a multiple of 8 so that b % 8 is still the XCD).
+LF_DEVICE bool tile_of_block(int b, int gx, int gy, int group, int &bx, int &by) {
   const int tiles = gx * gy;
-  const int b = blockIdx.x;
   if (b >= tiles) return false;
   const int xcd = b & 7, local = b >> 3;
   const int base = tiles >> 3, extra = tiles & 7;
@@ -241,6 +243,9 @@ LF_DEVICE bool tile_of_block(int gx, int gy, int group, int &bx, int &by) {
   by = first + in % rows;
   bx = in / rows;
   return true;
+}
+LF_DEVICE bool tile_of_block(int gx, int gy, int group, int &bx, int &by) {
+  return tile_of_block(static_cast<int>(blockIdx.x), gx, gy, group, bx, by);
 }
 
 }  // namespace w8a8v3

@@ -31,6 +31,7 @@
 
 #include <type_traits>
 
+#include "phases.h"
 #include "w8a8_v3.h"
 
 namespace w8a8v4 {
@@ -326,16 +327,25 @@ struct StageTile {
     *reinterpret_cast<uint2 *>(base + row * kPitch + col) = uint2{b[0] | (b[1] << 16), b[2] | (b[3] << 16)};
   }
   // Writes the staged tile: row `row` goes to row_ptr(row) (null: skipped).
-  template <class RowPtr>
+  // THROUGH: the stores write through the XCD's L2 (phases.h), for a tile
+  // that blocks of the same launch read.
+  template <bool THROUGH = false, class RowPtr>
   LF_DEVICE void flush(int lane, RowPtr row_ptr) const {
 #pragma unroll
     for (int q = 0; q < kChunks / 64; ++q) {
       const int idx = q * 64 + lane;
       const int row = idx / kChunksPerRow, chunk = idx % kChunksPerRow;
-      const uint4 v = *reinterpret_cast<const uint4 *>(
+      const u32x4 v = *reinterpret_cast<const u32x4 *>(
           reinterpret_cast<const uint8_t *>(base + row * kPitch) + chunk * 16);
       Elem *dst = row_ptr(row);
-      if (dst != nullptr) *reinterpret_cast<uint4 *>(reinterpret_cast<uint8_t *>(dst) + chunk * 16) = v;
+      if (dst != nullptr) {
+        uint8_t *p = reinterpret_cast<uint8_t *>(dst) + chunk * 16;
+        if constexpr (THROUGH) {
+          phase::store16_through(p, v);
+        } else {
+          *reinterpret_cast<u32x4 *>(p) = v;
+        }
+      }
     }
   }
 };

@@ -226,6 +226,98 @@ int64_t w8a16_gated_workspace(const W8a16Gated &g) {
   return h + down + 256;
 }
 
+// W8A8 tile forms (kernels/projection.hip). Output columns per block: BN
+// for dense / QKV, BN / 2 h-columns for gate/up (a block computes BN / 2
+// gate and BN / 2 up columns). 256 x 256 tiles when the launch has at least
+// 192 of them (three quarters of a tile per CU of the 256 on an MI355X) and
+// the columns divide: on 4 waves (t256) from 256 tiles, on 8 waves (t256w8,
+// a single tile per CU, whose load latency two waves per SIMD hide better)
+// below that. Fewer: QKV and dense on 256 x 128 tiles (4 waves, t256x128)
+// when those number 128-256 (at most one per CU); otherwise 128 x 128 tiles
+// (4 waves, two blocks per CU). Measured at M = 2048: QKV (192 large tiles)
+// 71.2 -> 59.5 us on the large tiles; o and down (128) were 30-40 % slower
+// on them and 9-10 % faster on 256 x 128 than on 128 x 128.
+// The 256-row forms address a tile's activation rows with 32-bit offsets
+// from its first row, which needs 256 K < 2^32; wider K takes 128 x 128.
+enum class W8a8Form { kT256, kT256w8, kT256x128, kT128 };
+struct W8a8Tiles {
+  W8a8Form form;
+  int bm, bn, threads;
+  int64_t gx, bands;  // column blocks, row bands (of bm rows) for the profile
+};
+const char *w8a8_form_name(W8a8Form f) {
+  switch (f) {
+    case W8a8Form::kT256: return "t256";
+    case W8a8Form::kT256w8: return "t256w8";
+    case W8a8Form::kT256x128: return "t256x128";
+    default: return "t128";
+  }
+}
+W8a8Tiles w8a8_tiles_of(W8a8Form f, bool gate_up, int64_t n, int32_t max_tokens) {
+  W8a8Tiles t{f, 256, 256, 256, 0, 0};
+  if (f == W8a8Form::kT256w8) t.threads = 512;
+  if (f == W8a8Form::kT256x128) t.bn = 128;
+  if (f == W8a8Form::kT128) t.bm = t.bn = 128;
+  t.gx = n / (gate_up ? t.bn / 2 : t.bn);
+  t.bands = (max_tokens + t.bm - 1) / t.bm;
+  return t;
+}
+// false if no form takes the shape (n not a multiple of the 128-column form's
+// block width).
+bool w8a8_tiles(bool gate_up, int64_t n, int64_t k, int32_t max_tokens, W8a8Tiles *out) {
+  const int64_t cols256 = gate_up ? 128 : 256, cols128 = gate_up ? 64 : 128;
+  if (n % cols128 != 0) return false;
+  const bool offsets32 = k < (int64_t(1) << 24);
+  const int64_t bands256 = (max_tokens + 255) / 256;
+  const int64_t tiles256 = (n % cols256 == 0 && offsets32) ? bands256 * (n / cols256) : 0;
+  const int64_t tiles256x128 = !gate_up && offsets32 ? bands256 * (n / cols128) : 0;
+  const bool big = tiles256 >= 192, four_wave = tiles256 >= 256;
+  const bool wide128 = !big && tiles256x128 >= 128 && tiles256x128 <= 256;
+  const W8a8Form f = big ? (four_wave ? W8a8Form::kT256 : W8a8Form::kT256w8)
+                         : wide128 ? W8a8Form::kT256x128 : W8a8Form::kT128;
+  *out = w8a8_tiles_of(f, gate_up, n, max_tokens);
+  return true;
+}
+
+// One-launch W8A8 entries (_aq, and the GatedMlp): 256 quantizer blocks
+// per quantizer step ahead of the GEMM blocks (kQuantBlocks in
+// kernels/projection.hip), and the sync area of kernels/phases.h at the
+// start of the workspace.
+constexpr int64_t kQuantBlocks = 256;
+int64_t sync_bytes(int64_t steps, int64_t bands) { return align_up(128 + 4 * steps * bands, 256); }
+int64_t quantized_rows_bytes(int64_t rows, int64_t k) {
+  return align_up(rows * k, 256) + align_up(rows * 4, 256);
+}
+
+// W8A8 GatedMlp in one launch: both GEMMs on 4-wave blocks of one band
+// height. Gate/up on 256 x 256 tiles where its own launch would take 256-row
+// tiles (down then on 256 x 256, or 256 x 128 where its own launch would
+// not take 256 x 256), else both on 128 x 128.
+struct W8a8Gated {
+  W8a8Tiles gu, dn;
+};
+bool w8a8_gated(int64_t hidden, int64_t inter, int32_t max_tokens, W8a8Gated *out) {
+  W8a8Tiles gu, dn;
+  if (!w8a8_tiles(true, inter, hidden, max_tokens, &gu) || !w8a8_tiles(false, hidden, inter, max_tokens, &dn)) {
+    return false;
+  }
+  const bool offsets32 = hidden < (int64_t(1) << 24) && inter < (int64_t(1) << 24);
+  if (gu.form != W8a8Form::kT128 && offsets32 && hidden % 128 == 0) {
+    out->gu = w8a8_tiles_of(W8a8Form::kT256, true, inter, max_tokens);
+    const bool dn256 = (dn.form == W8a8Form::kT256 || dn.form == W8a8Form::kT256w8) && hidden % 256 == 0;
+    out->dn = w8a8_tiles_of(dn256 ? W8a8Form::kT256 : W8a8Form::kT256x128, false, hidden, max_tokens);
+  } else {
+    out->gu = w8a8_tiles_of(W8a8Form::kT128, true, inter, max_tokens);
+    out->dn = w8a8_tiles_of(W8a8Form::kT128, false, hidden, max_tokens);
+  }
+  return true;
+}
+int64_t w8a8_gated_workspace(const W8a8Gated &g, int64_t hidden, int64_t inter) {
+  const int64_t cap = g.gu.bands * g.gu.bm;
+  return sync_bytes(3, g.gu.bands) + quantized_rows_bytes(cap, hidden) + align_up(cap * inter * 2, 256) +
+         quantized_rows_bytes(cap, inter);
+}
+
 int64_t w8a16_gemm_workspace(const W8a16Gemm &g) {
   if (g.split == 1) return 256;
   // one 1 KiB fp32 fragment per (slice, column block, wave, fragment): 8
@@ -328,7 +420,9 @@ int32_t lunaflux_fp8_admit_weight(int32_t entry, const uint8_t *region_head, int
   const bool dense = entry == LF_FP8_ENTRY_W8A16_DENSE || entry == LF_FP8_ENTRY_W8A16_QKV ||
                      entry == LF_FP8_ENTRY_W8A16_GATE_UP || entry == LF_FP8_ENTRY_W8A8_DENSE ||
                      entry == LF_FP8_ENTRY_W8A8_QKV || entry == LF_FP8_ENTRY_W8A8_GATE_UP ||
-                     entry == LF_FP8_ENTRY_W8A16_GATED_MLP;
+                     entry == LF_FP8_ENTRY_W8A16_GATED_MLP || entry == LF_FP8_ENTRY_W8A8_DENSE_AQ ||
+                     entry == LF_FP8_ENTRY_W8A8_QKV_AQ || entry == LF_FP8_ENTRY_W8A8_GATE_UP_AQ ||
+                     entry == LF_FP8_ENTRY_W8A8_GATED_MLP;
   const bool grouped = entry == LF_FP8_ENTRY_GROUPED;
   if ((!dense && !grouped) || region_head == nullptr || head_bytes < LF_FP8_HEADER_BYTES ||
       (dense && experts != 1)) {
@@ -396,8 +490,27 @@ int64_t lunaflux_fp8_w8a16_workspace_bytes(int32_t entry, int64_t n, int64_t k,
 
 int64_t lunaflux_fp8_gated_mlp_workspace_bytes(int32_t entry, int64_t hidden, int64_t inter,
                                                int32_t max_tokens) {
+  if (entry == LF_FP8_ENTRY_W8A8_GATED_MLP) {
+    W8a8Gated g;
+    if (hidden <= 0 || inter <= 0 || max_tokens <= 0 || hidden > kMaxDim || inter > kMaxDim ||
+        hidden % 128 != 0 || !w8a8_gated(hidden, inter, max_tokens, &g)) {
+      return -1;
+    }
+    return w8a8_gated_workspace(g, hidden, inter);
+  }
   const W8a16Gated *g = w8a16_gated(entry, hidden, inter, max_tokens);
   return g == nullptr ? -1 : w8a16_gated_workspace(*g);
+}
+
+int64_t lunaflux_fp8_w8a8_workspace_bytes(int32_t entry, int64_t n, int64_t k, int32_t max_tokens) {
+  if ((entry != LF_FP8_ENTRY_W8A8_DENSE_AQ && entry != LF_FP8_ENTRY_W8A8_QKV_AQ &&
+       entry != LF_FP8_ENTRY_W8A8_GATE_UP_AQ) ||
+      n <= 0 || k <= 0 || k % 128 != 0 || max_tokens <= 0 || n > kMaxDim || k > kMaxDim) {
+    return -1;
+  }
+  W8a8Tiles t;
+  if (!w8a8_tiles(entry == LF_FP8_ENTRY_W8A8_GATE_UP_AQ, n, k, max_tokens, &t)) return -1;
+  return sync_bytes(1, t.bands) + quantized_rows_bytes(t.bands * t.bm, k);
 }
 
 int32_t lunaflux_fp8_gated_mlp_geometry(int32_t entry, int64_t hidden, int64_t inter,
@@ -405,6 +518,22 @@ int32_t lunaflux_fp8_gated_mlp_geometry(int32_t entry, int64_t hidden, int64_t i
                                         char symbol[LF_FP8_SYMBOL_BYTES]) {
   if (dims == nullptr || symbol == nullptr || hidden <= 0 || inter <= 0 || max_tokens <= 0) {
     return LF_INVALID_ARGUMENT;
+  }
+  if (entry == LF_FP8_ENTRY_W8A8_GATED_MLP) {
+    W8a8Gated g;
+    if (hidden > kMaxDim || inter > kMaxDim || hidden % 128 != 0 || inter % 128 != 0 ||
+        !w8a8_gated(hidden, inter, max_tokens, &g)) {
+      return LF_INVALID_ARGUMENT;
+    }
+    // x quantizer, gate/up tiles, h quantizer, down tiles
+    const int64_t blocks = 2 * kQuantBlocks + (g.gu.gx + g.dn.gx) * g.gu.bands;
+    if (blocks > INT32_MAX) return LF_INVALID_ARGUMENT;
+    const int32_t values[7] = {static_cast<int32_t>(blocks), 1, 1, g.gu.threads, 1, 1, 0};
+    std::memcpy(dims, values, sizeof(values));
+    std::memset(symbol, 0, LF_FP8_SYMBOL_BYTES);
+    std::snprintf(symbol, LF_FP8_SYMBOL_BYTES, "lf_fp8_w8a8_gated_mlp_%s_%s", w8a8_form_name(g.gu.form),
+                  w8a8_form_name(g.dn.form));
+    return LF_OK;
   }
   const W8a16Gated *g = w8a16_gated(entry, hidden, inter, max_tokens);
   if (g == nullptr) return LF_UNSUPPORTED;
@@ -492,39 +621,24 @@ static int32_t launch_geometry(int32_t entry, int64_t n, int64_t k, int64_t nq, 
     }
     case LF_FP8_ENTRY_W8A8_DENSE:
     case LF_FP8_ENTRY_W8A8_QKV:
-    case LF_FP8_ENTRY_W8A8_GATE_UP: {
-      // Output columns per block: BN for dense/qkv, BN / 2 h-columns for
-      // gate/up (each block computes BN / 2 gate and BN / 2 up columns).
-      const bool gate_up = entry == LF_FP8_ENTRY_W8A8_GATE_UP;
-      const int64_t cols256 = gate_up ? 128 : 256, cols128 = gate_up ? 64 : 128;
-      if (n % cols128 != 0) return LF_INVALID_ARGUMENT;
-      // 256 x 256 tiles when the launch has at least 192 of them (three
-      // quarters of a tile per CU of the 256 on an MI355X) and the columns
-      // divide: on 4 waves (_t256) from 256 tiles, on 8 waves (_t256w8, a
-      // single tile per CU, whose load latency two waves per SIMD hide
-      // better) below that. Fewer: QKV and dense on 256 x 128 tiles (4
-      // waves, _t256x128) when those number 128-256 (at most one per CU);
-      // otherwise 128 x 128 tiles (4 waves, two blocks per CU). Measured at
-      // M = 2048: QKV (192 large tiles) 71.2 -> 59.5 us on the large tiles;
-      // o and down (128) were 30-40 % slower on them and 9-10 % faster on
-      // 256 x 128 than on 128 x 128.
-      // The 256-row forms (_t256, _t256w8, _t256x128) address a tile's
-      // activation rows with 32-bit offsets from its first row, which needs
-      // 256 K < 2^32; wider K takes the 128 x 128 form.
-      const bool offsets32 = k < (int64_t(1) << 24);
-      const int64_t tiles256 = (n % cols256 == 0 && offsets32) ? ((max_tokens + 255) / 256) * (n / cols256) : 0;
-      const int64_t tiles256x128 = !gate_up && offsets32 ? ((max_tokens + 255) / 256) * (n / cols128) : 0;
-      const bool big = tiles256 >= 192, four_wave = tiles256 >= 256;
-      const bool wide128 = !big && tiles256x128 >= 128 && tiles256x128 <= 256;
-      const int64_t tiles = big ? tiles256 : wide128 ? tiles256x128 : ((max_tokens + 127) / 128) * (n / cols128);
-      if (tiles > INT32_MAX) return LF_INVALID_ARGUMENT;
-      const char *op = entry == LF_FP8_ENTRY_W8A8_DENSE ? "dense" : entry == LF_FP8_ENTRY_W8A8_QKV ? "qkv" : "gate_up";
-      std::snprintf(buffer, sizeof(buffer), "lf_fp8_w8a8_%s_%s", op,
-                    big ? (four_wave ? "t256" : "t256w8") : wide128 ? "t256x128" : "t128");
+    case LF_FP8_ENTRY_W8A8_GATE_UP:
+    case LF_FP8_ENTRY_W8A8_DENSE_AQ:
+    case LF_FP8_ENTRY_W8A8_QKV_AQ:
+    case LF_FP8_ENTRY_W8A8_GATE_UP_AQ: {
+      const bool aq = entry == LF_FP8_ENTRY_W8A8_DENSE_AQ || entry == LF_FP8_ENTRY_W8A8_QKV_AQ ||
+                      entry == LF_FP8_ENTRY_W8A8_GATE_UP_AQ;
+      const bool gate_up = entry == LF_FP8_ENTRY_W8A8_GATE_UP || entry == LF_FP8_ENTRY_W8A8_GATE_UP_AQ;
+      const bool qkv = entry == LF_FP8_ENTRY_W8A8_QKV || entry == LF_FP8_ENTRY_W8A8_QKV_AQ;
+      W8a8Tiles t;
+      if (!w8a8_tiles(gate_up, n, k, max_tokens, &t)) return LF_INVALID_ARGUMENT;
+      const int64_t blocks = t.gx * t.bands + (aq ? kQuantBlocks : 0);
+      if (blocks > INT32_MAX) return LF_INVALID_ARGUMENT;
+      std::snprintf(buffer, sizeof(buffer), "lf_fp8_w8a8_%s_%s%s", qkv ? "qkv" : gate_up ? "gate_up" : "dense",
+                    w8a8_form_name(t.form), aq ? "_aq" : "");
       name = buffer;
-      gx = static_cast<int32_t>(tiles);
+      gx = static_cast<int32_t>(blocks);
       gy = 1;
-      bx = big && !four_wave ? 512 : 256;
+      bx = t.threads;
       break;
     }
     default:
@@ -552,7 +666,8 @@ int32_t lunaflux_fp8_launch_geometry(int32_t entry, int64_t n, int64_t k,
 int32_t lunaflux_fp8_qkv_launch_geometry(int32_t entry, int64_t nq, int64_t nkv, int64_t k,
                                          int32_t max_tokens, int32_t dims[7],
                                          char symbol[LF_FP8_SYMBOL_BYTES]) {
-  if ((entry != LF_FP8_ENTRY_W8A16_QKV && entry != LF_FP8_ENTRY_W8A8_QKV) || nq <= 0 ||
+  if ((entry != LF_FP8_ENTRY_W8A16_QKV && entry != LF_FP8_ENTRY_W8A8_QKV &&
+       entry != LF_FP8_ENTRY_W8A8_QKV_AQ) || nq <= 0 ||
       nkv <= 0 || nq > kMaxDim || nkv > kMaxDim) {
     return LF_INVALID_ARGUMENT;
   }

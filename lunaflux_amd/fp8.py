@@ -127,6 +127,15 @@ def w8a16_workspace_bytes(entry: int, n: int, k: int, max_tokens: int,
     return nbytes
 
 
+def w8a8_workspace_bytes(entry: int, n: int, k: int, max_tokens: int) -> int:
+    """Workspace of a one-launch W8A8 entry (_AQ): the sync area, then the
+    quantized rows for the profile."""
+    nbytes = _abi.lib().lunaflux_fp8_w8a8_workspace_bytes(entry, n, k, max_tokens)
+    if nbytes < 0:
+        raise DeviceError("w8a8_workspace_bytes", _abi.LF_INVALID_ARGUMENT)
+    return nbytes
+
+
 def launch_geometry(entry: int, n: int, k: int, max_tokens: int,
                     qkv_split: tuple[int, int] | None = None):
     dims = (ctypes.c_int32 * 7)()
@@ -141,13 +150,13 @@ def launch_geometry(entry: int, n: int, k: int, max_tokens: int,
             symbol.value.decode("ascii"))
 
 
-def gated_mlp_geometry(hidden: int, inter: int, max_tokens: int):
-    """(dims, symbol) of the one-launch W8A16 GatedMlp entry for the shape and
-    profile, or None where none is built."""
+def gated_mlp_geometry(hidden: int, inter: int, max_tokens: int,
+                       entry: int = _abi.ENTRY_W8A16_GATED_MLP):
+    """(dims, symbol) of the one-launch GatedMlp entry (W8A16 or W8A8) for the
+    shape and profile, or None where none is built."""
     dims = (ctypes.c_int32 * 7)()
     symbol = ctypes.create_string_buffer(128)
-    status = _abi.lib().lunaflux_fp8_gated_mlp_geometry(_abi.ENTRY_W8A16_GATED_MLP, hidden, inter,
-                                                        max_tokens, dims, symbol)
+    status = _abi.lib().lunaflux_fp8_gated_mlp_geometry(entry, hidden, inter, max_tokens, dims, symbol)
     if status == _abi.LF_UNSUPPORTED:
         return None
     _check("gated_mlp_geometry", status)
@@ -208,15 +217,47 @@ class LaunchStep:
 @dataclass
 class BoundOperation:
     """A plan operation bound to its regions: one or more launch steps run
-    in order on one stream."""
+    in order on one stream.
+
+    error_offset: byte offset in the workspace of the int32 error word of an
+    entry with counted waits (kernels/phases.h), or None. A synchronous
+    launch reads it back; a set word (a wait ran out: never on a correct
+    launch) zero-fills the workspace, which puts its counters back at rest,
+    and raises DeviceError(LF_DRIVER_FAILURE). check() does the same after
+    asynchronous launches."""
 
     steps: list
     workspace: Allocation | None = None
     keep: list = field(default_factory=list)
+    error_offset: int | None = None
 
     def launch(self, stream: Stream, synchronous: bool = True):
         for i, step in enumerate(self.steps):
             step.launch(stream, synchronous and i == len(self.steps) - 1)
+        if synchronous:
+            self.check()
+
+    def check(self):
+        """Raises DeviceError if a counted wait of an earlier launch ran out
+        (the caller synchronizes the stream first)."""
+        if self.error_offset is None:
+            return
+        word = self.workspace.read(np.int32, (1,), self.error_offset)[0]
+        if word != 0:
+            self.workspace.copy_from_host(np.zeros(self.workspace.byte_count, np.uint8))
+            raise DeviceError("a counted wait of a one-launch entry ran out", _abi.LF_DRIVER_FAILURE)
+
+
+@dataclass
+class _Chain(BoundOperation):
+    """An operation bound as the steps of several bound operations in order
+    (their workspaces kept alive); check() checks each part's error word."""
+
+    parts: list = field(default_factory=list)
+
+    def check(self):
+        for part in self.parts:
+            part.check()
 
 
 def _region(alloc: Allocation, byte_count: int | None = None, offset: int = 0,
@@ -275,6 +316,17 @@ class ProjectionRuntime:
                           qkv_split)
         return BoundOperation([step], workspace=ws)
 
+    def _w8a8_one_launch(self, entry: int, n: int, k: int, max_tokens: int, operands,
+                         qkv_split=None) -> BoundOperation:
+        """A one-launch W8A8 operation (_AQ entry): bf16 x in, the quantizer
+        and the GEMM as counted steps of one grid; its workspace (sync area,
+        quantized rows) zero-filled once here."""
+        nbytes = w8a8_workspace_bytes(entry, n, k, max_tokens)
+        ws = self.context.allocate(nbytes)
+        ws.copy_from_host(np.zeros(nbytes, np.uint8))
+        step = self._step(entry, n, k, max_tokens, operands + [_region(ws, alignment=256)], qkv_split)
+        return BoundOperation([step], workspace=ws, error_offset=_abi.LF_FP8_AQ_ERROR_OFFSET)
+
     # -- binding plan operations to launch steps ---------------------------
     def bind_act_quant(self, counts: Allocation, x: KernelArgument, w: Fp8Weight,
                        xq: KernelArgument, max_tokens: int) -> LaunchStep:
@@ -300,13 +352,20 @@ class ProjectionRuntime:
                           [_region(counts, COUNTS_BYTES, alignment=4), xq, w.region, y])
 
     def bind_dense(self, family: str, counts: Allocation, x: KernelArgument, w: Fp8Weight,
-                   y: KernelArgument, max_tokens: int) -> BoundOperation:
+                   y: KernelArgument, max_tokens: int, one_launch: bool = True) -> BoundOperation:
+        """OutputProjection / down / the vocabulary head. W8A8: one launch
+        (the _aq entry quantizes x inside it); one_launch=False binds the
+        act-quant launch and the GEMM-only launch instead (same outputs)."""
         _family(family, max_tokens)
         w.admit(_abi.ENTRY_W8A16_DENSE if family == "w8a16" else _abi.ENTRY_W8A8_DENSE)
         c = _region(counts, COUNTS_BYTES, alignment=4)
         if family == "w8a16":
             return self._w8a16(_abi.ENTRY_W8A16_DENSE, w.rows, w.columns, max_tokens,
                                [c, x, w.region, y])
+        if one_launch:
+            w.admit(_abi.ENTRY_W8A8_DENSE_AQ)
+            return self._w8a8_one_launch(_abi.ENTRY_W8A8_DENSE_AQ, w.rows, w.columns, max_tokens,
+                                         [c, x, w.region, y])
         ws = self.context.allocate(act_quant_bytes(max_tokens, w.columns))
         xq = _region(ws, alignment=256)
         return BoundOperation([
@@ -315,7 +374,8 @@ class ProjectionRuntime:
         ], workspace=ws)
 
     def bind_qkv(self, family: str, counts: Allocation, x: KernelArgument, wq: Fp8Weight,
-                 wk: Fp8Weight, wv: Fp8Weight, y: KernelArgument, max_tokens: int) -> BoundOperation:
+                 wk: Fp8Weight, wv: Fp8Weight, y: KernelArgument, max_tokens: int,
+                 one_launch: bool = True) -> BoundOperation:
         _family(family, max_tokens)
         for w in (wq, wk, wv):
             w.admit(_abi.ENTRY_W8A16_QKV if family == "w8a16" else _abi.ENTRY_W8A8_QKV)
@@ -327,6 +387,10 @@ class ProjectionRuntime:
             return self._w8a16(_abi.ENTRY_W8A16_QKV, n, wq.columns, max_tokens,
                                [c, x, wq.region, wk.region, wv.region, y],
                                qkv_split=(wq.rows, wk.rows))
+        if one_launch:
+            return self._w8a8_one_launch(_abi.ENTRY_W8A8_QKV_AQ, n, wq.columns, max_tokens,
+                                         [c, x, wq.region, wk.region, wv.region, y],
+                                         qkv_split=(wq.rows, wk.rows))
         ws = self.context.allocate(act_quant_bytes(max_tokens, wq.columns))
         xq = _region(ws, alignment=256)
         return BoundOperation([
@@ -336,7 +400,8 @@ class ProjectionRuntime:
         ], workspace=ws)
 
     def bind_gate_up(self, family: str, counts: Allocation, x: KernelArgument, wg: Fp8Weight,
-                     wu: Fp8Weight, h: KernelArgument, max_tokens: int) -> BoundOperation:
+                     wu: Fp8Weight, h: KernelArgument, max_tokens: int,
+                     one_launch: bool = True) -> BoundOperation:
         _family(family, max_tokens)
         for w in (wg, wu):
             w.admit(_abi.ENTRY_W8A16_GATE_UP if family == "w8a16" else _abi.ENTRY_W8A8_GATE_UP)
@@ -346,6 +411,9 @@ class ProjectionRuntime:
         if family == "w8a16":
             return self._w8a16(_abi.ENTRY_W8A16_GATE_UP, wg.rows, wg.columns, max_tokens,
                                [c, x, wg.region, wu.region, h])
+        if one_launch:
+            return self._w8a8_one_launch(_abi.ENTRY_W8A8_GATE_UP_AQ, wg.rows, wg.columns, max_tokens,
+                                         [c, x, wg.region, wu.region, h])
         ws = self.context.allocate(act_quant_bytes(max_tokens, wg.columns))
         xq = _region(ws, alignment=256)
         return BoundOperation([
@@ -356,41 +424,46 @@ class ProjectionRuntime:
 
     def bind_gated_mlp(self, family: str, counts: Allocation, x: KernelArgument, wg: Fp8Weight,
                        wu: Fp8Weight, wd: Fp8Weight, y: KernelArgument,
-                       max_tokens: int, one_launch: bool = False) -> BoundOperation:
-        """GatedMlp (model/plan/plan.mbt:47-59): gate/up + SwiGLU into a bf16
-        intermediate in the workspace, then the down projection from it (two
-        launch steps of one operation). one_launch=True binds the one-launch
-        W8A16 entry instead where one is built for the shape and profile
-        (lunaflux_fp8_gated_mlp_*); it computes the same values and is
-        slower on MI355X (44.8 vs 38.6 us at M = 32), so it is not the
-        default."""
+                       max_tokens: int, one_launch: bool = True) -> BoundOperation:
+        """GatedMlp (model/plan/plan.mbt:47-59) as one launch, the plan's one
+        AOT entry point for the operation (lunaflux_fp8_gated_mlp_geometry):
+        W8A8 for any width (x quantizer, gate/up + SwiGLU, h quantizer and
+        down as counted steps of one grid), W8A16 where a one-launch entry is
+        built for the shape and profile. Elsewhere, or with one_launch=False,
+        two launch steps: gate/up + SwiGLU into a bf16 intermediate, then the
+        down projection from it (each W8A8 step then quantizes its input
+        inside its own launch, or, with one_launch=False, in a launch of its
+        own). Every form computes the same values."""
         if wd.columns != wg.rows or wd.rows != wg.columns:
             raise DeviceError("mlp shapes", _abi.LF_INVALID_ARGUMENT)
         if wg.rows != wu.rows or wg.columns != wu.columns:
             raise DeviceError("gate/up shapes", _abi.LF_INVALID_ARGUMENT)
-        if family == "w8a16" and one_launch:
-            geometry = gated_mlp_geometry(wg.columns, wg.rows, max_tokens)
-            if geometry is not None:
-                _family(family, max_tokens)
-                for w in (wg, wu, wd):
-                    w.admit(_abi.ENTRY_W8A16_GATED_MLP)
-                dims, symbol = geometry
-                nbytes = _abi.lib().lunaflux_fp8_gated_mlp_workspace_bytes(
-                    _abi.ENTRY_W8A16_GATED_MLP, wg.columns, wg.rows, max_tokens)
-                ws = self.context.allocate(nbytes)
-                ws.copy_from_host(np.zeros(nbytes, np.uint8))
-                c = _region(counts, COUNTS_BYTES, alignment=4)
-                step = LaunchStep(self.function(symbol), dims,
-                                  KernelArguments([c, x, wg.region, wu.region, wd.region, y,
-                                                   _region(ws, alignment=256)]), symbol)
-                return BoundOperation([step], workspace=ws)
+        _family(family, max_tokens)
+        entry = _abi.ENTRY_W8A16_GATED_MLP if family == "w8a16" else _abi.ENTRY_W8A8_GATED_MLP
+        geometry = gated_mlp_geometry(wg.columns, wg.rows, max_tokens, entry) if one_launch else None
+        if geometry is not None:
+            for w in (wg, wu, wd):
+                w.admit(entry)
+            dims, symbol = geometry
+            nbytes = _abi.lib().lunaflux_fp8_gated_mlp_workspace_bytes(entry, wg.columns, wg.rows,
+                                                                        max_tokens)
+            if nbytes < 0:
+                raise DeviceError("gated_mlp_workspace_bytes", _abi.LF_INVALID_ARGUMENT)
+            ws = self.context.allocate(nbytes)
+            ws.copy_from_host(np.zeros(nbytes, np.uint8))
+            c = _region(counts, COUNTS_BYTES, alignment=4)
+            step = LaunchStep(self.function(symbol), dims,
+                              KernelArguments([c, x, wg.region, wu.region, wd.region, y,
+                                               _region(ws, alignment=256)]), symbol)
+            error_offset = (nbytes - _abi.LF_FP8_GATED_MLP_ERROR_OFFSET_FROM_END if family == "w8a16"
+                            else _abi.LF_FP8_AQ_ERROR_OFFSET)
+            return BoundOperation([step], workspace=ws, error_offset=error_offset)
         h_bytes = max_tokens * wg.rows * 2
         h_alloc = self.context.allocate(h_bytes)
         h = _region(h_alloc, h_bytes, alignment=256)
-        first = self.bind_gate_up(family, counts, x, wg, wu, h, max_tokens)
-        second = self.bind_dense(family, counts, h, wd, y, max_tokens)
-        return BoundOperation(first.steps + second.steps, workspace=h_alloc,
-                              keep=[first.workspace, second.workspace])
+        first = self.bind_gate_up(family, counts, x, wg, wu, h, max_tokens, one_launch=one_launch)
+        second = self.bind_dense(family, counts, h, wd, y, max_tokens, one_launch=one_launch)
+        return _Chain(first.steps + second.steps, workspace=h_alloc, parts=[first, second])
 
     # -- numpy convenience (tests, smoke) -----------------------------------
     def _run(self, bind, x: np.ndarray, out_shape, max_tokens):

@@ -43,8 +43,13 @@ MAX_MODULE_BYTES = 1 << 30
 MAX_SYMBOL_BYTES = 128  # the C ABI's bound (include/lunaflux_hip.h)
 
 # Stable family ids (the integer a catalog AotKernelFamily names within the
-# module), by symbol prefix; first match wins.
+# module), by symbol prefix and suffix; first match wins. The one-launch W8A8
+# forms (_aq: x and a workspace in place of the quantized rows) are families
+# of their own, since their operand lists differ.
 FAMILIES = (
+    (12, "lf_fp8_w8a8_dense_", "_aq"),
+    (13, "lf_fp8_w8a8_qkv_", "_aq"),
+    (14, "lf_fp8_w8a8_gate_up_", "_aq"),
     (1, "lf_fp8_act_quant_rows"),
     (2, "lf_fp8_rms_norm_quant_rows_"),
     (3, "lf_fp8_w8a16_dense_"),
@@ -55,6 +60,7 @@ FAMILIES = (
     (8, "lf_fp8_w8a8_gate_up_"),
     (9, "lf_moe_"),
     (10, "lf_fp8_w8a16_gated_mlp_"),
+    (11, "lf_fp8_w8a8_gated_mlp_"),
 )
 
 
@@ -80,8 +86,8 @@ def kernel_symbols(image: bytes) -> list:
 
 
 def family_of(symbol: str):
-    for family, prefix in FAMILIES:
-        if symbol.startswith(prefix):
+    for family, prefix, *suffix in FAMILIES:
+        if symbol.startswith(prefix) and (not suffix or symbol.endswith(suffix[0])):
             return family
     return None
 

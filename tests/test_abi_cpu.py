@@ -228,6 +228,89 @@ def test_launch_geometry():
     assert fp8.act_quant_bytes(3, 512) == 1536 + 256
 
 
+def test_one_launch_w8a8_geometry_and_workspace():
+    """The _aq entries: the GEMM-only entry's tile form, 256 quantizer blocks
+    ahead of its tiles, workspace = sync area (128 B + one counter per row
+    band, 256-aligned) + the quantized rows of ceil(max / BM) BM-row bands.
+    The W8A8 GatedMlp: both GEMMs on 4-wave blocks of one band height."""
+    for entry, plain, n, k, m in [
+        (_abi.ENTRY_W8A8_DENSE_AQ, _abi.ENTRY_W8A8_DENSE, 4096, 4096, 8192),
+        (_abi.ENTRY_W8A8_DENSE_AQ, _abi.ENTRY_W8A8_DENSE, 4096, 14336, 2048),
+        (_abi.ENTRY_W8A8_GATE_UP_AQ, _abi.ENTRY_W8A8_GATE_UP, 14336, 4096, 8192),
+        (_abi.ENTRY_W8A8_GATE_UP_AQ, _abi.ENTRY_W8A8_GATE_UP, 14336, 4096, 256),
+        (_abi.ENTRY_W8A8_DENSE_AQ, _abi.ENTRY_W8A8_DENSE, 4096, 4096, 3),
+    ]:
+        d0, s0 = fp8.launch_geometry(plain, n, k, m)
+        d1, s1 = fp8.launch_geometry(entry, n, k, m)
+        assert s1 == s0 + "_aq" and d1.grid == (d0.grid[0] + 256, 1, 1) and d1.block == d0.block
+        bm = 128 if s0.endswith("_t128") else 256
+        bands = -(-m // bm)
+        sync = -(-(128 + 4 * bands) // 256) * 256
+        cap = bands * bm
+        assert fp8.w8a8_workspace_bytes(entry, n, k, m) == sync + fp8.act_quant_bytes(cap, k)
+    d, s = fp8.launch_geometry(_abi.ENTRY_W8A8_QKV_AQ, 6144, 4096, 2048, qkv_split=(4096, 1024))
+    assert s == "lf_fp8_w8a8_qkv_t256w8_aq" and d.grid == (8 * 24 + 256, 1, 1) and d.block == (512, 1, 1)
+    with pytest.raises(fp8.DeviceError):
+        fp8.w8a8_workspace_bytes(_abi.ENTRY_W8A8_DENSE, 4096, 4096, 16)    # the GEMM-only entry
+    lib = _abi.lib()
+    for h, i, m, sym, bands, gx in [
+        (4096, 14336, 8192, "lf_fp8_w8a8_gated_mlp_t256_t256", 32, 112 + 16),
+        (4096, 14336, 2048, "lf_fp8_w8a8_gated_mlp_t256_t256x128", 8, 112 + 32),
+        (4096, 14336, 3072, "lf_fp8_w8a8_gated_mlp_t256_t256", 12, 112 + 16),    # down t256w8 alone
+        (4096, 14336, 512, "lf_fp8_w8a8_gated_mlp_t256_t256x128", 2, 112 + 32),  # gate/up t256w8 alone
+        (4096, 14336, 256, "lf_fp8_w8a8_gated_mlp_t128_t128", 2, 224 + 32),
+    ]:
+        d, s = fp8.gated_mlp_geometry(h, i, m, _abi.ENTRY_W8A8_GATED_MLP)
+        assert s == sym and d.grid == (512 + gx * bands, 1, 1) and d.block == (256, 1, 1), (s, d.grid)
+        bm = 128 if "t128" in sym else 256
+        cap = bands * bm
+        sync = -(-(128 + 12 * bands) // 256) * 256
+        want = sync + fp8.act_quant_bytes(cap, h) + cap * i * 2 + fp8.act_quant_bytes(cap, i)
+        assert lib.lunaflux_fp8_gated_mlp_workspace_bytes(_abi.ENTRY_W8A8_GATED_MLP, h, i, m) == want
+    assert lib.lunaflux_fp8_gated_mlp_workspace_bytes(_abi.ENTRY_W8A8_GATED_MLP, 4000, 14336, 64) == -1
+
+
+class _FakeWorkspace:
+    """The two calls BoundOperation.check makes on its workspace."""
+
+    def __init__(self, nbytes):
+        self.data = np.zeros(nbytes, np.uint8)
+        self.byte_count = nbytes
+
+    def read(self, dtype, shape, offset=0):
+        n = int(np.prod(shape)) * np.dtype(dtype).itemsize
+        return self.data[offset:offset + n].view(dtype).reshape(shape).copy()
+
+    def copy_from_host(self, data, offset=0):
+        raw = np.ascontiguousarray(data).view(np.uint8).ravel()
+        self.data[offset:offset + raw.size] = raw
+
+
+def test_bound_operation_error_word():
+    """A set error word (a counted wait ran out) raises LF_DRIVER_FAILURE and
+    zero-fills the workspace, which puts its counters back at rest; a clear
+    word passes; an operation without counted waits never reads."""
+    ws = _FakeWorkspace(1024)
+    op = fp8.BoundOperation([], workspace=ws, error_offset=0)
+    op.check()
+    ws.data[:4] = np.array([1], np.int32).view(np.uint8)
+    ws.data[200] = 7                       # a counter left mid-count
+    with pytest.raises(fp8.DeviceError) as err:
+        op.check()
+    assert err.value.status == _abi.LF_DRIVER_FAILURE
+    assert not ws.data.any()
+    op.check()
+    ws2 = _FakeWorkspace(512)
+    ws2.data[512 - _abi.LF_FP8_GATED_MLP_ERROR_OFFSET_FROM_END] = 1
+    with pytest.raises(fp8.DeviceError):
+        fp8.BoundOperation([], workspace=ws2, error_offset=512 - _abi.LF_FP8_GATED_MLP_ERROR_OFFSET_FROM_END).check()
+    fp8.BoundOperation([], workspace=None).check()
+    chain = fp8._Chain([], parts=[fp8.BoundOperation([], workspace=ws, error_offset=0), op])
+    ws.data[:4] = np.array([1], np.int32).view(np.uint8)
+    with pytest.raises(fp8.DeviceError):
+        chain.check()
+
+
 def test_closed_and_invalid_handles_without_gpu():
     lib = _abi.lib()
     status = ctypes.c_int32(0)

@@ -300,7 +300,7 @@ def test_gated_mlp_one_launch(rt, m, max_tokens):
     counts = rt.step_counts(m)
     ya = rt.context.allocate(max_tokens * hidden * 2)
     one = rt.bind_gated_mlp("w8a16", counts, _region(xa, alignment=256), wg, wu, wd,
-                            _region(ya, alignment=256), max_tokens, one_launch=True)
+                            _region(ya, alignment=256), max_tokens)
     assert len(one.steps) == 1 and one.steps[0].name.startswith("lf_fp8_w8a16_gated_mlp_"), one.steps
     sentinel = np.full(max_tokens * hidden, 0x7FC1, np.uint16)
     ya.copy_from_host(sentinel)
@@ -324,10 +324,19 @@ def test_gated_mlp_one_launch(rt, m, max_tokens):
     if max_tokens == 32:
         ya.copy_from_host(sentinel)
         two = rt.bind_gated_mlp("w8a16", counts, _region(xa, alignment=256), wg, wu, wd,
-                                _region(ya, alignment=256), max_tokens)
+                                _region(ya, alignment=256), max_tokens, one_launch=False)
         assert len(two.steps) == 2
         two.launch(rt.stream, synchronous=True)
         assert np.array_equal(ya.read(np.uint16, (max_tokens, hidden)), outs[0])
+        # new inputs on the same workspace: each launch starts from counters
+        # at rest (a stale count would let down read h early)
+        for _ in range(2):
+            x2 = synth.activations(rng, max(m, 1), hidden)[:m]
+            xa.copy_from_host(np.concatenate([x2, np.zeros((max_tokens - m, hidden), np.uint16)]))
+            one.launch(rt.stream, synchronous=True)
+            y1 = ya.read(np.uint16, (max_tokens, hidden))
+            two.launch(rt.stream, synchronous=True)
+            assert np.array_equal(y1, ya.read(np.uint16, (max_tokens, hidden)))
 
 
 @pytest.mark.parametrize("op,m,family", [

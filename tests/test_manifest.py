@@ -40,7 +40,10 @@ def test_manifest_describes_every_kernel_of_the_code_object(image):
                          ("lf_fp8_w8a16_gate_up_k4096_m32", 5), ("lf_fp8_w8a16_dense_m128", 3),
                          ("lf_fp8_w8a16_qkv_k4096_q4096_kv1024_m32", 4),
                          ("lf_fp8_w8a8_dense_t256", 6), ("lf_fp8_w8a8_gate_up_t128", 8),
-                         ("lf_moe_route", 9), ("lf_moe_down_t256_b128", 9)]:
+                         ("lf_moe_route", 9), ("lf_moe_down_t256_b128", 9),
+                         ("lf_fp8_w8a16_gated_mlp_h4096_i14336_m32", 10),
+                         ("lf_fp8_w8a8_gated_mlp_t256_t256", 11), ("lf_fp8_w8a8_dense_t256_aq", 12),
+                         ("lf_fp8_w8a8_qkv_t128_aq", 13), ("lf_fp8_w8a8_gate_up_t256x128_aq", 14)]:
         assert symbols[name][0] == family, name
     assert "lf_calibrate_copy" not in symbols          # a benchmark tool, not a plan kernel
     pairs = [(e["family_id"], e["entry_point_id"]) for e in module["entry_points"]]
