@@ -14,8 +14,10 @@ value = algorithmic bytes of the step / step time, with algorithmic bytes per
 call = N*K (e4m3 weights) + 4*N (scales) + 2*M*K (x) + 2*M*N_out (y), each
 weight byte counted once. The roofline object is the dominant kernel (gate/up)
 timed with HIP events on the launch stream. `detail` holds the other decode
-M values, the prefill (W8A8) GEMMs in TFLOP/s, and the
-act-quant pass (and each operation's TFLOP/s with it). cpu_baseline times the
+M values (and the GatedMlp operation as one launch against two), the
+prefill (W8A8) GEMMs in TFLOP/s, the act-quant pass, each
+operation's TFLOP/s with it as two launches and as the plan's one launch
+(act-quant inside), and the W8A8 GatedMlp as one launch against four. cpu_baseline times the
 CPU oracle (C restatement of kernels/reference over dequantized weights) on
 the host cores, with one-thread figures for configs 1 and 2 beside it.
 
@@ -94,18 +96,28 @@ class Layer:
 
 
 class Bench:
-    def __init__(self, rt, layer, max_tokens, family):
+    """One profile's bound calls over the rotated weights. one_launch: the
+    plan's binding, one launch per operation (the W8A8 calls quantize their
+    input inside the launch); False: the W8A8 calls as an act-quant launch
+    plus a GEMM-only launch. `share`: another Bench of the same profile whose
+    activation and output buffers this one reuses."""
+
+    def __init__(self, rt, layer, max_tokens, family, one_launch=True, share=None):
         from lunaflux_amd import synth
         from lunaflux_amd.fp8 import _region
-        self.rt, self.layer, self.family = rt, layer, family
+        self.rt, self.layer, self.family, self.one_launch = rt, layer, family, one_launch
         ctx = rt.context
-        rng = np.random.default_rng(99 + max_tokens)
-        self.x = ctx.upload(synth.activations(rng, max_tokens, HIDDEN))
-        self.xd = ctx.upload(synth.activations(rng, max_tokens, INTER))
-        self.out = {n: ctx.allocate(max_tokens * no * 2) for n, _, _, no in call_shapes()}
+        if share is not None:
+            self.x, self.xd, self.out = share.x, share.xd, share.out
+        else:
+            rng = np.random.default_rng(99 + max_tokens)
+            self.x = ctx.upload(synth.activations(rng, max_tokens, HIDDEN))
+            self.xd = ctx.upload(synth.activations(rng, max_tokens, INTER))
+            self.out = {n: ctx.allocate(max_tokens * no * 2) for n, _, _, no in call_shapes()}
         self.max_tokens = max_tokens
         self._region = _region
         self.ops = {}
+        self.mlp_ops = {}
 
     def bind(self, m):
         rt, L, R = self.rt, self.layer, self._region
@@ -114,17 +126,50 @@ class Bench:
         for r in range(L.rotations):
             fam, mt = self.family, self.max_tokens
             x, xd = R(self.x, alignment=256), R(self.xd, alignment=256)
+            one = self.one_launch
             ops.append({
                 "qkv": rt.bind_qkv(fam, counts, x, L.w("q", r), L.w("k", r), L.w("v", r),
-                                   R(self.out["qkv"], alignment=256), mt),
-                "o": rt.bind_dense(fam, counts, x, L.w("o", r), R(self.out["o"], alignment=256), mt),
+                                   R(self.out["qkv"], alignment=256), mt, one_launch=one),
+                "o": rt.bind_dense(fam, counts, x, L.w("o", r), R(self.out["o"], alignment=256), mt,
+                                   one_launch=one),
                 "gate_up": rt.bind_gate_up(fam, counts, x, L.w("gate", r), L.w("up", r),
-                                           R(self.out["gate_up"], alignment=256), mt),
+                                           R(self.out["gate_up"], alignment=256), mt, one_launch=one),
                 "down": rt.bind_dense(fam, counts, xd, L.w("down", r),
-                                      R(self.out["down"], alignment=256), mt),
+                                      R(self.out["down"], alignment=256), mt, one_launch=one),
             })
         self.ops[m] = (counts, ops)
         return ops
+
+    def bind_mlp(self, m, one_launch):
+        """The GatedMlp operation (gate/up + SwiGLU + down, x [M, 4096] ->
+        y [M, 4096]) for each weight rotation."""
+        key = (m, one_launch)
+        if key not in self.mlp_ops:
+            rt, L, R = self.rt, self.layer, self._region
+            counts = rt.step_counts(m)
+            self.mlp_ops[key] = [
+                rt.bind_gated_mlp(self.family, counts, R(self.x, alignment=256), L.w("gate", r),
+                                  L.w("up", r), L.w("down", r), R(self.out["o"], alignment=256),
+                                  self.max_tokens, one_launch=one_launch)
+                for r in range(L.rotations)]
+        return self.mlp_ops[key]
+
+    def time_ops(self, ops, launches, warmup=3):
+        """Average time of one whole bound operation (all of its launch steps),
+        `launches` back to back over the rotations: HIP events on the launch
+        stream. Checks the counted waits' error words afterwards."""
+        stream, ctx = self.rt.stream, self.rt.context
+        for i in range(warmup):
+            ops[i % len(ops)].launch(stream, synchronous=False)
+        start, stop = ctx.create_event(), ctx.create_event()
+        start.record(stream)
+        for i in range(launches):
+            ops[i % len(ops)].launch(stream, synchronous=False)
+        stop.record(stream)
+        stop.synchronize()
+        for op in ops:
+            op.check()
+        return start.elapsed_milliseconds(stop) / launches
 
     def run(self, m, steps, warmup, calls=("qkv", "o", "gate_up", "down"), probe="gate_up"):
         """Times `steps` steps of the given calls; returns (total ms, mean ms of
@@ -764,6 +809,8 @@ def main():
 
     detail = {"decode_w8a16": {}, "prefill_w8a8": {}}
     if not args.quick:
+        mlp_bytes = lambda mm: (call_bytes(mm, HIDDEN, 2 * INTER, INTER) +
+                                call_bytes(mm, INTER, HIDDEN, HIDDEN) - 4 * mm * INTER)
         for mm, mt in [(1, 16), (8, 16), (32, 32), (128, 128)]:
             b = Bench(rt, layer, mt, "w8a16") if mt != 32 else decode
             row = {}
@@ -774,28 +821,50 @@ def main():
             row["layer_us"] = round(s_ms * 1e3, 2)
             row["layer_GB/s"] = round(layer_bytes(mm) / (s_ms * 1e-3) / 1e9, 1)
             row["layer_hbm_frac"] = round(row["layer_GB/s"] / HBM_PEAK_GBS, 4)
+            # GatedMlp as the plan binds it (one launch where an entry is
+            # built) against its two launches; bytes without h's round trip
+            one = b.bind_mlp(mm, True)
+            two = b.bind_mlp(mm, False)
+            t1, t2 = b.time_ops(one, 20), b.time_ops(two, 20)
+            row["gated_mlp"] = {"launches": len(one[0].steps), "us": round(t1 * 1e3, 2),
+                                "GB/s": round(mlp_bytes(mm) / (t1 * 1e-3) / 1e9, 1),
+                                "two_launch_us": round(t2 * 1e3, 2)}
+            # the drop-in layer: qkv, o and the GatedMlp operation, one launch each
+            row["layer_one_launch_us"] = round((row["qkv"]["us"] + row["o"]["us"]) + t1 * 1e3, 2)
             detail["decode_w8a16"][f"M={mm}"] = row
             log(f"decode M={mm}: {row}")
         detail["lm_head_w8a16"] = lm_head_bench(rt)
         log(f"lm head: {detail['lm_head_w8a16']}")
         for mm in (2048, 8192):
-            b = Bench(rt, layer, mm, "w8a8")
+            b = Bench(rt, layer, mm, "w8a8", one_launch=False)
+            b1 = Bench(rt, layer, mm, "w8a8", one_launch=True, share=b)
             row = {}
             for c, k, n, no in call_shapes():
                 p = b.time_kernel(mm, c, 5, warmup=2)
                 q = b.time_kernel(mm, c, 5, warmup=2, step=0)
+                p1 = b1.time_kernel(mm, c, 5, warmup=2)
                 tf = call_flops(mm, k, n) / (p * 1e-3) / 1e12
                 op_tf = call_flops(mm, k, n) / ((p + q) * 1e-3) / 1e12
+                one_tf = call_flops(mm, k, n) / (p1 * 1e-3) / 1e12
                 row[c] = {"gemm_us": round(p * 1e3, 1), "TFLOP/s": round(tf, 1),
                           "fp8_frac": round(tf / FP8_PEAK_TFLOPS, 4),
                           "act_quant_us": round(q * 1e3, 1),
                           "act_quant_GB/s": round(mm * k * 3 / (q * 1e-3) / 1e9, 1),
                           "op_us": round((p + q) * 1e3, 1), "op_TFLOP/s": round(op_tf, 1),
-                          "op_fp8_frac": round(op_tf / FP8_PEAK_TFLOPS, 4)}
+                          "op_fp8_frac": round(op_tf / FP8_PEAK_TFLOPS, 4),
+                          # the plan's binding: one launch, act-quant inside
+                          "one_launch_us": round(p1 * 1e3, 1), "one_launch_TFLOP/s": round(one_tf, 1),
+                          "one_launch_fp8_frac": round(one_tf / FP8_PEAK_TFLOPS, 4)}
+            mlp_flops = call_flops(mm, HIDDEN, 2 * INTER) + call_flops(mm, INTER, HIDDEN)
+            t1, t4 = b1.time_ops(b1.bind_mlp(mm, True), 5), b.time_ops(b.bind_mlp(mm, False), 5)
+            row["gated_mlp"] = {"launches": 1, "us": round(t1 * 1e3, 1),
+                                "TFLOP/s": round(mlp_flops / (t1 * 1e-3) / 1e12, 1),
+                                "fp8_frac": round(mlp_flops / (t1 * 1e-3) / 1e12 / FP8_PEAK_TFLOPS, 4),
+                                "four_launch_us": round(t4 * 1e3, 1)}
             row["rms_norm_quant_k4096"] = rms_norm_quant_bench(rt, b, mm)
             detail["prefill_w8a8"][f"M={mm}"] = row
             log(f"prefill M={mm}: {row}")
-            del b
+            del b, b1
         detail["moe"] = {}
         for name, c in MOE_CONFIGS.items():
             detail["moe"][name] = moe_bench(rt, c)

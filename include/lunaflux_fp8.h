@@ -189,8 +189,9 @@ enum lf_fp8_entry {
  * W8A8 GatedMlp): it starts with a sync area whose first int32 is the error
  * word, 0 after every correct launch; 1 if a wait ran out (never on a
  * correct launch; the polls are bounded, so no launch hangs). Once it is
- * set, launches on that workspace store nothing until the caller
- * zero-fills the workspace again (its counters are then not at rest).
+ * set, launches on that workspace leave their outputs unwritten until the
+ * caller zero-fills the workspace again (its counters are then not at
+ * rest).
  * Launches sharing one ws must not overlap. */
 #define LF_FP8_AQ_ERROR_OFFSET 0
 int64_t lunaflux_fp8_w8a8_workspace_bytes(int32_t entry, int64_t n, int64_t k, int32_t max_tokens);

@@ -24,9 +24,11 @@
 // 2^20 polls, ~30 ms): a poll that runs out sets the error word, and the
 // block stores nothing and returns.
 // After an error: the last block does not reset the counters, and every
-// block of a later launch that finds the error word set returns before it
-// reads or writes anything else; the host reads the word after a
-// synchronous launch, zero-fills the workspace and reports the failure.
+// wait of a later launch reads the error word with its first poll and fails,
+// so no block that depends on a wait stores an output (blocks of a first
+// step, which wait for nothing, may still rewrite their part of the
+// workspace); the host reads the word after a synchronous launch,
+// zero-fills the workspace and reports the failure.
 //
 // Visibility. The stores a later step reads go through the XCD's L2 to
 // memory (agent-scope atomic stores and write-through stores: the sc1
@@ -70,17 +72,6 @@ struct Flag {
   int value;
 };
 
-// True if an earlier wait of this or a previous launch ran out (read by
-// thread 0, broadcast to the block).
-LF_DEVICE bool failed(const int *error, Flag &flag) {
-  if (threadIdx.x == 0) flag.value = load_agent(error);
-  __syncthreads();
-  const bool f = flag.value != 0;
-  __syncthreads();
-  return f;
-}
-LF_DEVICE bool failed(const Sync &s, Flag &flag) { return failed(s.error(), flag); }
-
 // Counts this block into `counter` once the stores of all its waves have
 // completed.
 LF_DEVICE void signal(int *counter) {
@@ -92,20 +83,29 @@ LF_DEVICE void signal(int *counter) {
 // Waits until *counter >= target. False if the poll ran out (the error word
 // is then set) or another block's had: the caller loads nothing that
 // depends on the wait and stores nothing.
+// Each poll is one device-scope round trip (the counter); the error word is
+// read every 32nd poll only (measured: a second, dependent load per poll
+// put the wait's end 2.5-5 us after the last count).
+// The first poll also reads the error word (both loads in flight at once),
+// so a launch on a failed workspace stores nothing without a separate check.
 LF_DEVICE bool wait_for(const int *counter, int target, int *error, Flag &flag) {
   if (threadIdx.x == 0) {
     int ok = 1, spins = 0;
-    while (load_agent(counter) < target) {
-      if (load_agent(error) != 0) {
-        ok = 0;
-        break;
+    const int first = load_agent(counter);
+    if (load_agent(error) != 0) ok = 0;
+    for (int c = first; ok && c < target; c = load_agent(counter)) {
+      if ((++spins & 31) == 0) {
+        if (load_agent(error) != 0) {
+          ok = 0;
+          break;
+        }
+        if (spins > kSpinLimit) {
+          store_agent(error, 1);
+          ok = 0;
+          break;
+        }
       }
-      if (++spins > kSpinLimit) {
-        store_agent(error, 1);
-        ok = 0;
-        break;
-      }
-      __builtin_amdgcn_s_sleep(2);
+      __builtin_amdgcn_s_sleep(1);
     }
     flag.value = ok;
   }

@@ -75,41 +75,58 @@ LF_DEVICE void store_scale(float *p, float v) {
   }
 }
 
+// RB consecutive rows at once (rows row0 .. row0 + live - 1 of x, live <=
+// RB): every load of the batch is issued before the first row is reduced,
+// so a wave keeps RB rows in flight (RB C 16 bytes per lane). Returns the
+// scale of the batch's first row.
+template <int C, int RB, bool THROUGH = false>
+LF_DEVICE float quantize_rows_wave_regs(const uint16_t *x, int K, int row0, int live, uint8_t *xq,
+                                        float *scales) {
+  const int lane = threadIdx.x & 63;
+  const int chunks = K >> 3;
+  u32x4 v[RB][C];
+  static_for<RB>([&](auto b) {
+    const u32x4 *src = reinterpret_cast<const u32x4 *>(x + static_cast<uint64_t>(row0 + b) * K);
+    static_for<C>([&](auto c) {
+      const int idx = lane + 64 * c;
+      v[b][c] = (b < live && idx < chunks) ? src[idx] : u32x4{0u, 0u, 0u, 0u};
+    });
+  });
+  float first = 0.0f;
+  static_for<RB>([&](auto b) {
+    float amax = 0.0f;
+    static_for<C>([&](auto c) {
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        amax = fmaxf(amax, fabsf(bf16_to_f32(v[b][c][i] & 0xffffu)));
+        amax = fmaxf(amax, fabsf(bf16_to_f32(v[b][c][i] >> 16)));
+      }
+    });
+    amax = wave_max(amax);
+    const bool zero = amax == 0.0f;
+    const float ratio = zero ? 0.0f : 448.0f / amax;
+    // The encode converts the raw chunks again rather than keeping the 8 C
+    // floats of the amax pass alive (an empty asm that "redefines" each
+    // chunk keeps the compiler from reusing them; 8 C floats would not fit).
+    static_for<C>([&](auto c) { opaque(v[b][c]); });
+    uint8_t *dst = xq + static_cast<uint64_t>(row0 + b) * K;
+    static_for<C>([&](auto c) {
+      const int idx = lane + 64 * c;
+      const uint32_t lo = e4m3x4_from_bf16(v[b][c][0], v[b][c][1], ratio);
+      const uint32_t hi = e4m3x4_from_bf16(v[b][c][2], v[b][c][3], ratio);
+      if (b < live && idx < chunks) store_codes8<THROUGH>(dst + 8 * idx, zero ? 0u : lo, zero ? 0u : hi);
+    });
+    const float sc = zero ? 0.0f : amax / 448.0f;
+    if (b < live && lane == 0) store_scale<THROUGH>(scales + row0 + b, sc);
+    if (b == 0) first = sc;
+  });
+  return first;
+}
+
 template <int C, bool THROUGH = false>
 LF_DEVICE float quantize_row_wave_regs(const uint16_t *src_row, int K, uint8_t *dst_row,
                                        float *scale) {
-  const int lane = threadIdx.x & 63;
-  const int chunks = K >> 3;
-  const u32x4 *src = reinterpret_cast<const u32x4 *>(src_row);
-  u32x4 v[C];
-  static_for<C>([&](auto c) {
-    const int idx = lane + 64 * c;
-    v[c] = idx < chunks ? src[idx] : u32x4{0u, 0u, 0u, 0u};
-  });
-  float amax = 0.0f;
-  static_for<C>([&](auto c) {
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      amax = fmaxf(amax, fabsf(bf16_to_f32(v[c][i] & 0xffffu)));
-      amax = fmaxf(amax, fabsf(bf16_to_f32(v[c][i] >> 16)));
-    }
-  });
-  amax = wave_max(amax);
-  const bool zero = amax == 0.0f;
-  const float ratio = zero ? 0.0f : 448.0f / amax;
-  // The encode converts the raw chunks again rather than keeping the 8 C
-  // floats of the amax pass alive (an empty asm that "redefines" each chunk
-  // keeps the compiler from reusing them; 8 C floats would not fit).
-  static_for<C>([&](auto c) { opaque(v[c]); });
-  static_for<C>([&](auto c) {
-    const int idx = lane + 64 * c;
-    const uint32_t lo = e4m3x4_from_bf16(v[c][0], v[c][1], ratio);
-    const uint32_t hi = e4m3x4_from_bf16(v[c][2], v[c][3], ratio);
-    if (idx < chunks) store_codes8<THROUGH>(dst_row + 8 * idx, zero ? 0u : lo, zero ? 0u : hi);
-  });
-  const float sc = zero ? 0.0f : amax / 448.0f;
-  if (lane == 0) store_scale<THROUGH>(scale, sc);
-  return sc;
+  return quantize_rows_wave_regs<C, 1, THROUGH>(src_row, K, 0, 1, dst_row, scale);
 }
 
 // Per-token quantizer for rows longer than the register-resident forms: two
@@ -875,10 +892,11 @@ using GemmT128 = FormT128<w8a8v3::Tile<128, 128, 2, 2, 2>, 4>;
 // entry point (kernels/launch_contract/types.mbt:16-27), and the operation's
 // input is the bf16 activation, so the per-token quantizer runs inside the
 // launch: the grid is kQuantBlocks quantizer blocks followed by the GEMM's
-// blocks, and a GEMM tile starts its loads once every 16-row chunk of its
-// row band is quantized (phases.h). Quantizer block q takes chunks q,
-// q + kQuantBlocks, ...; each wave of it quantizes 16 / waves rows of a
-// chunk with the standalone quantizer's code (same codes and scales), its
+// blocks, and a GEMM tile starts its loads once every chunk (kChunkRows
+// rows) of its row band is quantized (phases.h). Quantizer block q takes
+// chunks q, q + kQuantBlocks, ...; each wave of it quantizes kChunkRows /
+// waves rows of a chunk with the standalone quantizer's code (same codes
+// and scales), its
 // stores written through to memory, then the block counts the chunk into
 // its band's counter.
 // Workspace: the sync area (phases.h, one step of bands = ceil(max_tokens /
@@ -887,23 +905,49 @@ using GemmT128 = FormT128<w8a8v3::Tile<128, 128, 2, 2, 2>, 4>;
 // align256(M K)); bands = (gridDim.x - kQuantBlocks) / column blocks.
 // ---------------------------------------------------------------------------
 constexpr int kQuantBlocks = 256;
-constexpr int kChunkRows = 16;
+// 8-row chunks: at M = 2048 every quantizer block has one (16-row chunks left
+// half of them idle and the other half ended 5-10 us into the launch).
+constexpr int kChunkRows = 8;
 
 LF_DEVICE int chunks_in_band(int M, int band, int BM) {
   const int rows = M - band * BM < BM ? M - band * BM : BM;
   return rows <= 0 ? 0 : (rows + kChunkRows - 1) / kChunkRows;
 }
 
+// The R = kChunkRows / waves rows of chunk c that this wave quantizes (at
+// least one: an 8-wave block leaves waves past the chunk idle), in batches
+// of register-resident rows (128 VGPRs of row data: 4 rows of <= 4096
+// columns, 2 of <= 8192, 1 of <= 16384; F::kQuantChunks caps the row width
+// of that form, wider rows take the two-pass form one at a time).
 template <class F>
 LF_DEVICE void quantize_chunk(const uint16_t *x, int K, int M, int c, uint8_t *xq, float *scales) {
-  constexpr int R = kChunkRows / (F::kThreads / 64);
+  constexpr int kWaves = F::kThreads / 64;
+  constexpr int R = kChunkRows / kWaves > 0 ? kChunkRows / kWaves : 1;
   const int wave = static_cast<int>(threadIdx.x) >> 6;
+  if (wave * R >= kChunkRows) return;
+  const int row0 = c * kChunkRows + wave * R;
+  const int live = M - row0 < R ? M - row0 : R;
+  if (live <= 0) return;
+  auto batches = [&](auto chunks_tag, auto rows_tag) {
+    constexpr int C = decltype(chunks_tag)::value, RB = decltype(rows_tag)::value;
 #pragma unroll 1
-  for (int i = 0; i < R; ++i) {
-    const int row = c * kChunkRows + wave * R + i;
-    if (row < M) {
-      quantize_row_wave<true, F::kQuantChunks>(x + static_cast<uint64_t>(row) * K, K,
-                                               xq + static_cast<uint64_t>(row) * K, scales + row);
+    for (int i = 0; i < live; i += RB) {
+      quantize_rows_wave_regs<C, RB, true>(x, K, row0 + i, live - i, xq, scales);
+    }
+  };
+  using std::integral_constant;
+  constexpr int RB8 = R < 4 ? R : 4, RB16 = R < 2 ? R : 2;
+  if (K <= 4096) {
+    batches(integral_constant<int, 8>{}, integral_constant<int, RB8>{});
+  } else if (F::kQuantChunks >= 16 && K <= 8192) {
+    batches(integral_constant<int, 16>{}, integral_constant<int, RB16>{});
+  } else if (F::kQuantChunks >= 32 && K <= 16384) {
+    batches(integral_constant<int, 32>{}, integral_constant<int, 1>{});
+  } else {
+#pragma unroll 1
+    for (int i = 0; i < live; ++i) {
+      const uint64_t off = static_cast<uint64_t>(row0 + i) * K;
+      quantize_row_wave_2pass<true>(x + off, K, xq + off, scales + row0 + i);
     }
   }
 }
@@ -923,7 +967,6 @@ LF_DEVICE void w8a8_one_launch(const int32_t *counts, const uint16_t *x, const u
   uint8_t *xq = ws + phase::sync_bytes(1, bands);
   const int cap = bands * F::kBM;
   const int M = live_rows(counts, cap);
-  if (phase::failed(sync, flag)) return;
   const int b = static_cast<int>(blockIdx.x);
   if (b < kQuantBlocks) {
     float *scales = reinterpret_cast<float *>(xq + align256(static_cast<uint64_t>(M) * K));
@@ -980,7 +1023,6 @@ LF_DEVICE void w8a8_gated_mlp(const int32_t *counts, const uint16_t *x, const ui
   uint16_t *h = reinterpret_cast<uint16_t *>(xq + xq_bytes);
   uint8_t *hq = xq + xq_bytes + h_bytes;
   const int M = live_rows(counts, cap);
-  if (phase::failed(sync, flag)) return;
   const int chunks = (M + kChunkRows - 1) / kChunkRows;
   int b = static_cast<int>(blockIdx.x);
   if (b < kQuantBlocks) {  // step 0: x -> xq

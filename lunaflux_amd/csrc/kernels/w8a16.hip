@@ -910,10 +910,10 @@ __device__ __forceinline__ void w8a16_fixed_group_kernel(const int32_t *counts, 
 // sets the error word, and its block returns without loading h or storing
 // anything. The last down block to finish resets the slice counters and its
 // own done counter for the next launch, unless the error word is set; every
-// block of a launch that finds the word set returns at once, so a workspace
-// whose counters are not at rest produces no output until the caller
-// zero-fills it (the host binding does so when it reads the word after a
-// synchronous launch).
+// down block's wait reads the word with its first poll and fails while it
+// is set, so a workspace whose counters are not at rest produces no output
+// until the caller zero-fills it (the host binding does so when it reads
+// the word after a synchronous launch).
 //
 // Workspace: h [16 MT rows][I] bf16 | the down kernel's split-K partials
 // and arrival counters | sync: slice counters [DN_S], done (+64 B), error
@@ -947,7 +947,6 @@ struct GatedMlpFixed {
     uint8_t *ws_down = ws + kHBytes;
     int *sync = reinterpret_cast<int *>(ws + kHBytes + kDownBytes);
     int *error = sync + 32;
-    if (phase::failed(error, flag)) return;
     const int b = static_cast<int>(blockIdx.x);
     if (b < kG1) {
       w8a16_fixed_group_kernel<H, 1, GU_W, MT, 2, GU_DW, GU_DX, 0, 0, NoWait, true, true>(
