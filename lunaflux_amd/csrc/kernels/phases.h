@@ -8,11 +8,15 @@
 // and a block of a later step waits, with a bounded poll, for a counter
 // that the blocks of the earlier step add to once their stores are
 // complete. All counters live in the operation's workspace (the sync area,
-// at its start):
-//   int32 [0]      error word: 0, or 1 once a wait ran out (sticky)
-//   int32 [16]     done counter of the last step's blocks
-//   int32 [32 ..]  band counters: step s, row band b at 32 + s * bands + b
-// sized sync_bytes(steps, bands). The binding zero-fills it once; the last
+// at its start), each in a 128-byte line of its own:
+//   byte 0                     error word: 0, or 1 once a wait ran out (sticky)
+//   byte 128                   done counter of the last step's blocks
+//   byte 256 + 128 (s bands + b)  band counter of step s, row band b
+// sized sync_bytes(steps, bands). (Counters sharing a line with the ones
+// hundreds of blocks poll reached those blocks ~8 us late: the W8A16
+// one-launch GatedMlp's four slice counts in one line, polled by 256 blocks,
+// became visible 4-8 us after their last add; one line each, ~1 us.) The
+// binding zero-fills the area once; the last
 // block of the last step to finish puts every counter back to zero, so every
 // launch starts from zeros.
 //
@@ -55,16 +59,19 @@ LF_DEVICE void store_agent(int *p, int v) {
   __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
+// Ints per 128-byte line: counters polled by many blocks get a line each.
+constexpr int kLineInts = 32;
+
 struct Sync {
   int *base;
   int bands;
   LF_DEVICE int *error() const { return base; }
-  LF_DEVICE int *done() const { return base + 16; }
-  LF_DEVICE int *band(int step, int b) const { return base + 32 + step * bands + b; }
+  LF_DEVICE int *done() const { return base + kLineInts; }
+  LF_DEVICE int *band(int step, int b) const { return base + kLineInts * (2 + step * bands + b); }
 };
 
 LF_DEVICE uint64_t sync_bytes(int steps, int bands) {
-  return align256(128 + 4ull * static_cast<uint64_t>(steps) * static_cast<uint64_t>(bands));
+  return 256 + 128ull * static_cast<uint64_t>(steps) * static_cast<uint64_t>(bands);
 }
 
 // The flag word every block keeps in LDS to broadcast thread 0's decisions.
@@ -129,7 +136,7 @@ LF_DEVICE void finish(const Sync &s, int total, int steps, Flag &flag) {
   }
   __syncthreads();
   if (flag.value != 0) {
-    for (int i = threadIdx.x; i < steps * s.bands; i += blockDim.x) store_agent(s.band(0, 0) + i, 0);
+    for (int i = threadIdx.x; i < steps * s.bands; i += blockDim.x) store_agent(s.band(0, 0) + kLineInts * i, 0);
     if (threadIdx.x == 0) store_agent(s.done(), 0);
   }
 }

@@ -916,14 +916,17 @@ __device__ __forceinline__ void w8a16_fixed_group_kernel(const int32_t *counts, 
 // the word after a synchronous launch).
 //
 // Workspace: h [16 MT rows][I] bf16 | the down kernel's split-K partials
-// and arrival counters | sync: slice counters [DN_S], done (+64 B), error
-// (+128 B; 0 after every correct launch).
+// and arrival counters | sync (768 bytes): slice counter s at +128 s (a line
+// each: phases.h), done (+512 B), error (+640 B, the last line but one; 0
+// after every correct launch).
 struct SliceWait {
   int *counters;
   int target;
   int *error;
   phase::Flag *flag;
-  LF_DEVICE bool operator()(int s) const { return phase::wait_for(counters + s, target, error, *flag); }
+  LF_DEVICE bool operator()(int s) const {
+    return phase::wait_for(counters + phase::kLineInts * s, target, error, *flag);
+  }
 };
 
 template <int H, int I, int MT, int GU_W, int GU_DW, int GU_DX, int DN_S, int DN_W, int DN_DW,
@@ -937,16 +940,21 @@ struct GatedMlpFixed {
   static constexpr uint64_t kDownBytes =
       ((static_cast<uint64_t>(DN_S) * (H / 16) * MT * 1024 + 255) & ~255ull) +
       (((H / 16 / DN_W) * 4 + 255) & ~255ull);
-  static constexpr uint64_t kSyncBytes = 256;
-  static_assert(DN_S <= 16, "slice counters fit before the done word");
+  static constexpr uint64_t kSyncBytes = 768;
+  static_assert(DN_S <= 4, "slice counters fit before the done word");
 
   LF_DEVICE static void run(const int32_t *counts, const uint16_t *x, const uint8_t *wg,
                             const uint8_t *wu, const uint8_t *wd, uint16_t *y, uint8_t *ws) {
     __shared__ phase::Flag flag;
     uint16_t *h = reinterpret_cast<uint16_t *>(ws);
     uint8_t *ws_down = ws + kHBytes;
+    // The block ranges and tile indices below are compiled for a grid of
+    // kG1 + kG2 blocks (the geometry's); any other grid stores and loads
+    // nothing (a larger one would address tiles past the weight regions).
+    if (static_cast<int>(gridDim.x) != kG1 + kG2) return;
     int *sync = reinterpret_cast<int *>(ws + kHBytes + kDownBytes);
-    int *error = sync + 32;
+    int *done = sync + 4 * phase::kLineInts;
+    int *error = sync + 5 * phase::kLineInts;
     const int b = static_cast<int>(blockIdx.x);
     if (b < kG1) {
       w8a16_fixed_group_kernel<H, 1, GU_W, MT, 2, GU_DW, GU_DX, 0, 0, NoWait, true, true>(
@@ -954,8 +962,8 @@ struct GatedMlpFixed {
       asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
       __syncthreads();
       if (threadIdx.x == 0) {
-        __hip_atomic_fetch_add(sync + (b * GU_W * 16) / kSliceCols, 1, __ATOMIC_RELAXED,
-                               __HIP_MEMORY_SCOPE_AGENT);
+        __hip_atomic_fetch_add(sync + phase::kLineInts * ((b * GU_W * 16) / kSliceCols), 1,
+                               __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
       }
       return;
     }
@@ -963,10 +971,10 @@ struct GatedMlpFixed {
     w8a16_fixed_group_kernel<I, DN_S, DN_W, MT, 0, DN_DW, DN_DX, 0, 0, SliceWait>(
         counts, h, wd, wd, wd, y, ws_down, b - kG1, kG2, wait);
     if (threadIdx.x == 0) {
-      const int before = __hip_atomic_fetch_add(sync + 16, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      const int before = __hip_atomic_fetch_add(done, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
       if (before == kG2 - 1 && phase::load_agent(error) == 0) {
-        for (int s = 0; s < DN_S; ++s) phase::store_agent(sync + s, 0);
-        phase::store_agent(sync + 16, 0);
+        for (int s = 0; s < DN_S; ++s) phase::store_agent(sync + phase::kLineInts * s, 0);
+        phase::store_agent(done, 0);
       }
     }
   }

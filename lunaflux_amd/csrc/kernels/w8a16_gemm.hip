@@ -41,6 +41,7 @@
 //
 // Included after w8a16.hip (its weight_fragment), in the one translation unit.
 #include "device_common.h"
+#include "phases.h"
 #include "w8a8_v3.h"
 
 namespace w16g {
@@ -82,12 +83,20 @@ LF_DEVICE void wait_ring(int later) {
 // MODE 0: dense, 1: QKV (three weights, packed Q|K|V output), 2: gate/up
 // (each wave column's fragments: kFN / 2 gate tiles, then the up tiles of the
 // same h-columns, so SwiGLU pairs fragment j with j + kFN / 2 in a lane).
-template <int BN, int WGM, int WGN, int NSA, int NSB, int MODE>
-__device__ __forceinline__ void w8a16_gemm_kernel(const int32_t *counts, const uint16_t *x, const uint8_t *w0,
-                                  const uint8_t *w1, const uint8_t *w2, uint16_t *y,
-                                  uint8_t *ws) {
+// smem: the block's LDS (T::kSmem bytes, 1 KiB aligned). bid / nblocks: the
+// block's index and the block count of this GEMM's part of the grid
+// (default blockIdx.x, gridDim.x). gate(s) runs once the weight ring's
+// first stages are in flight and before any activation load of K-slice s;
+// if it returns false the block waits for its loads into LDS and returns
+// (no activation load, no store, no split-K arrival). THROUGH: the outputs
+// are stored through the XCD's L2 (phases.h), for an output that blocks of
+// the same launch read.
+template <int BN, int WGM, int WGN, int NSA, int NSB, int MODE, bool THROUGH = false, class Gate = NoWait>
+__device__ __forceinline__ void w8a16_gemm_kernel(uint8_t *smem, const int32_t *counts, const uint16_t *x,
+                                                  const uint8_t *w0, const uint8_t *w1, const uint8_t *w2,
+                                                  uint16_t *y, uint8_t *ws, int bid = -1, int nblocks = -1,
+                                                  const Gate &gate = Gate{}) {
   using T = Tile<BN, WGM, WGN, NSA, NSB>;
-  __shared__ __attribute__((aligned(1024))) uint8_t smem[T::kSmem];
   __shared__ int last_block;
   if (!dense_regions_ok<MODE>(w0, w1, w2)) return;
   const WeightHeader &h0 = header_of(w0);
@@ -100,12 +109,17 @@ __device__ __forceinline__ void w8a16_gemm_kernel(const int32_t *counts, const u
   const int ld = MODE == 1 ? nq + nk + static_cast<int>(header_of(w2).rows) : nq;
   const int blocks_n = MODE == 2 ? ld / (BN / 2) : ld / BN;
   if (blocks_n < 1) return;
-  const int S = static_cast<int>(gridDim.x) / blocks_n;
-  if (S < 1) return;  // the geometry rules this out
-  const int cb = static_cast<int>(blockIdx.x) / S;
-  const int s = static_cast<int>(blockIdx.x) - cb * S;
+  const int nb = nblocks < 0 ? static_cast<int>(gridDim.x) : nblocks;
+  const int block = bid < 0 ? static_cast<int>(blockIdx.x) : bid;
+  const int S = nb / blocks_n;
+  // A grid whose split is not 1..KT (the geometry rules it out) stores
+  // nothing in any block: an empty K-slice would never arrive, and its
+  // column block's counter would stay raised for later launches.
+  if (S < 1 || S > KT) return;
+  const int cb = block / S;
+  const int s = block - cb * S;
   const int kt0 = (KT * s) / S, kt1 = (KT * (s + 1)) / S;
-  if (cb >= blocks_n || kt1 <= kt0) return;
+  if (cb >= blocks_n) return;
   const int M = live_rows(counts, T::kBM);
   if (M == 0) return;
 
@@ -200,10 +214,15 @@ __device__ __forceinline__ void w8a16_gemm_kernel(const int32_t *counts, const u
     for (int j = 0; j < T::kFN; ++j) acc[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
 
   const int nkt = kt1 - kt0;
+  if (!a_loader) {
+    for (int i = 0; i < NSB - 1 && i < nkt; ++i) issue_b(i);
+  }
+  if (!gate(s)) {
+    w8a8v3::wait_vmcnt<0>();  // no load may land in LDS after the block ends
+    return;
+  }
   if (a_loader) {
     for (int i = 0; i < NSA - 1 && i < nkt; ++i) issue_a(i);
-  } else {
-    for (int i = 0; i < NSB - 1 && i < nkt; ++i) issue_b(i);
   }
   for (int k = 0; k < nkt; ++k) {
     // This wave's part of stage k has landed once at most the later stages
@@ -253,6 +272,14 @@ __device__ __forceinline__ void w8a16_gemm_kernel(const int32_t *counts, const u
 
   // Epilogue. Lane element (i, j, e) is row wm * kWaveM + 16 i + 4 g + e of
   // slot column 16 (wn kFN + j) + r.
+  auto put = [&](uint16_t *p, float v) {
+    const uint16_t bits = static_cast<uint16_t>(f32_to_bf16(v));
+    if constexpr (THROUGH) {
+      __hip_atomic_store(p, bits, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    } else {
+      *p = bits;
+    }
+  };
   auto store = [&](const f32x4 (&v)[T::kFM][T::kFN]) {
 #pragma unroll
     for (int i = 0; i < T::kFM; ++i)
@@ -268,7 +295,7 @@ __device__ __forceinline__ void w8a16_gemm_kernel(const int32_t *counts, const u
             slot(wn * T::kFN + j, region, tile, ocol);
             const float out = silu_mul(v[i][j][e] * sc[j],
                                        v[i][j + T::kFN / 2][e] * sc[j + T::kFN / 2]);
-            y[static_cast<uint64_t>(m) * ld + ocol + r] = static_cast<uint16_t>(f32_to_bf16(out));
+            put(y + static_cast<uint64_t>(m) * ld + ocol + r, out);
           }
         } else {
 #pragma unroll
@@ -276,8 +303,7 @@ __device__ __forceinline__ void w8a16_gemm_kernel(const int32_t *counts, const u
             const uint8_t *region;
             int tile, ocol;
             slot(wn * T::kFN + j, region, tile, ocol);
-            y[static_cast<uint64_t>(m) * ld + ocol + r] =
-                static_cast<uint16_t>(f32_to_bf16(v[i][j][e] * sc[j]));
+            put(y + static_cast<uint64_t>(m) * ld + ocol + r, v[i][j][e] * sc[j]);
           }
         }
       }
@@ -349,6 +375,78 @@ __device__ __forceinline__ void w8a16_gemm_kernel(const int32_t *counts, const u
   store(sum);
 }
 
+// ---------------------------------------------------------------------------
+// GatedMlp in one launch for profiles of 65..128 rows (model/plan/plan.mbt:
+// 47-59; kernels/reference/mlp.mbt:4-39): the grid's first G1 blocks run the
+// gate/up GEMM above (GU_BN columns per block, one K-slice) into h in the
+// workspace, written through to memory; the other G2 blocks run the down
+// GEMM (DN_BN, split S = G2 / (H / DN_BN)) on h. Down blocks start their
+// weight ring, then wait (phases.h) until the gate/up blocks that write the
+// h columns of their K-slice have counted themselves done: a gate/up block
+// (GU_BN / 2 h-columns, within one 128-column k-tile of the down GEMM) adds
+// to the counter of the slice holding its k-tile, one 128-byte line per
+// slice counter (phases.h). The last down block resets the counters for
+// the next launch unless the error word is set.
+// Workspace: h [128][I] bf16 | the down GEMM's split-K partials and arrival
+// counters | sync (128 S + 256 bytes): slice counter s at +128 s, done at
+// +128 S, error at +128 S + 128 (the last line but one).
+template <int GU_BN, int DN_BN, int WGM, int WGN, int GU_NSA, int GU_NSB, int DN_NSA, int DN_NSB>
+struct GatedMlpGemm {
+  using GU = Tile<GU_BN, WGM, WGN, GU_NSA, GU_NSB>;
+  using DN = Tile<DN_BN, WGM, WGN, DN_NSA, DN_NSB>;
+  static constexpr int kSmem = GU::kSmem > DN::kSmem ? GU::kSmem : DN::kSmem;
+  LF_DEVICE static void run(const int32_t *counts, const uint16_t *x, const uint8_t *wg,
+                            const uint8_t *wu, const uint8_t *wd, uint16_t *y, uint8_t *ws) {
+    __shared__ __attribute__((aligned(1024))) uint8_t smem[kSmem];
+    __shared__ phase::Flag flag;
+    if (!dense_regions_ok<2>(wg, wu, wu) || !dense_regions_ok<0>(wd, wd, wd)) return;
+    const int H = static_cast<int>(header_of(wg).columns), I = static_cast<int>(header_of(wg).rows);
+    if (static_cast<int>(header_of(wd).columns) != I || static_cast<int>(header_of(wd).rows) != H) return;
+    const int g1 = I / (GU_BN / 2);
+    const int g2 = static_cast<int>(gridDim.x) - g1;
+    const int dn_blocks_n = H / DN_BN;
+    if (g1 < 1 || dn_blocks_n < 1 || g2 < dn_blocks_n || g2 % dn_blocks_n != 0) return;
+    const int S = g2 / dn_blocks_n;
+    uint16_t *h = reinterpret_cast<uint16_t *>(ws);
+    uint8_t *ws_down = ws + align256(128ull * I * 2);
+    // (the down GEMM's own workspace size: 256 bytes, unused, without a split)
+    const uint64_t down_bytes =
+        S == 1 ? 256
+               : align256(static_cast<uint64_t>(S) * dn_blocks_n * DN::kWaves * DN::kFM * DN::kFN * 1024) +
+                     align256(static_cast<uint64_t>(dn_blocks_n) * 4);
+    int *sync = reinterpret_cast<int *>(ws_down + down_bytes);
+    int *done = sync + phase::kLineInts * S;
+    int *error = done + phase::kLineInts;
+    const int KT = I >> 7;
+    auto slice_of = [&](int kt) {  // the down K-slice [KT s / S, KT (s + 1) / S) holding k-tile kt
+      int sl = 0;
+      while (sl + 1 < S && (KT * (sl + 1)) / S <= kt) ++sl;
+      return sl;
+    };
+    const int b = static_cast<int>(blockIdx.x);
+    if (b < g1) {
+      w8a16_gemm_kernel<GU_BN, WGM, WGN, GU_NSA, GU_NSB, 2, true>(smem, counts, x, wg, wu, wu, h, ws_down, b,
+                                                                  g1);
+      phase::signal(sync + phase::kLineInts * slice_of(b * (GU_BN / 2) / 128));
+      return;
+    }
+    const auto gate = [&](int sl) {
+      const int target = (KT * (sl + 1) / S - KT * sl / S) * (128 / (GU_BN / 2));
+      return phase::wait_for(sync + phase::kLineInts * sl, target, error, flag);
+    };
+    w8a16_gemm_kernel<DN_BN, WGM, WGN, DN_NSA, DN_NSB, 0>(smem, counts, h, wd, wd, wd, y, ws_down, b - g1, g2,
+                                                          gate);
+    __syncthreads();
+    if (threadIdx.x == 0) {
+      const int before = __hip_atomic_fetch_add(done, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      if (before == g2 - 1 && phase::load_agent(error) == 0) {
+        for (int sl = 0; sl < S; ++sl) phase::store_agent(sync + phase::kLineInts * sl, 0);
+        phase::store_agent(done, 0);
+      }
+    }
+  }
+};
+
 }  // namespace w16g
 
 extern "C" {
@@ -358,20 +456,37 @@ extern "C" {
 #define LF_W16_GEMM_ENTRIES(BN, WGM, WGN, NSA, NSB)                                              \
   __global__ __launch_bounds__(64 * WGM * WGN) void lf_fp8_w8a16_dense_m128_n##BN(               \
       const int32_t *counts, const uint16_t *x, const uint8_t *w, uint16_t *y, uint8_t *ws) {     \
-    w16g::w8a16_gemm_kernel<BN, WGM, WGN, NSA, NSB, 0>(counts, x, w, w, w, y, ws);                \
+    __shared__ __attribute__((aligned(1024))) uint8_t smem[w16g::Tile<BN, WGM, WGN, NSA, NSB>::kSmem]; \
+    w16g::w8a16_gemm_kernel<BN, WGM, WGN, NSA, NSB, 0>(smem, counts, x, w, w, w, y, ws);          \
   }                                                                                              \
   __global__ __launch_bounds__(64 * WGM * WGN) void lf_fp8_w8a16_qkv_m128_n##BN(                 \
       const int32_t *counts, const uint16_t *x, const uint8_t *wq, const uint8_t *wk,            \
       const uint8_t *wv, uint16_t *y, uint8_t *ws) {                                             \
-    w16g::w8a16_gemm_kernel<BN, WGM, WGN, NSA, NSB, 1>(counts, x, wq, wk, wv, y, ws);             \
+    __shared__ __attribute__((aligned(1024))) uint8_t smem[w16g::Tile<BN, WGM, WGN, NSA, NSB>::kSmem]; \
+    w16g::w8a16_gemm_kernel<BN, WGM, WGN, NSA, NSB, 1>(smem, counts, x, wq, wk, wv, y, ws);       \
   }                                                                                              \
   __global__ __launch_bounds__(64 * WGM * WGN) void lf_fp8_w8a16_gate_up_m128_n##BN(             \
       const int32_t *counts, const uint16_t *x, const uint8_t *wg, const uint8_t *wu,            \
       uint16_t *h, uint8_t *ws) {                                                                \
-    w16g::w8a16_gemm_kernel<BN, WGM, WGN, NSA, NSB, 2>(counts, x, wg, wu, wu, h, ws);             \
+    __shared__ __attribute__((aligned(1024))) uint8_t smem[w16g::Tile<BN, WGM, WGN, NSA, NSB>::kSmem]; \
+    w16g::w8a16_gemm_kernel<BN, WGM, WGN, NSA, NSB, 2>(smem, counts, x, wg, wu, wu, h, ws);       \
   }
 
 LF_W16_GEMM_ENTRIES(64, 4, 2, 4, 2)
 LF_W16_GEMM_ENTRIES(128, 4, 2, 2, 4)
+
+// One-launch GatedMlp for profiles of 65..128 rows, any H and I the forms
+// divide: gate/up on the n128 tiles (one K-slice), down on n128 or n64 (the
+// tile and split its own launch would take), operands (counts, x, wg, wu,
+// wd, y, ws).
+#define LF_W16_GEMM_GATED_MLP(DN_BN, DN_NSA, DN_NSB)                                             \
+  __global__ __launch_bounds__(512) void lf_fp8_w8a16_gated_mlp_m128_n128_n##DN_BN(               \
+      const int32_t *counts, const uint16_t *x, const uint8_t *wg, const uint8_t *wu,            \
+      const uint8_t *wd, uint16_t *y, uint8_t *ws) {                                             \
+    w16g::GatedMlpGemm<128, DN_BN, 4, 2, 2, 4, DN_NSA, DN_NSB>::run(counts, x, wg, wu, wd, y, ws); \
+  }
+
+LF_W16_GEMM_GATED_MLP(128, 2, 4)
+LF_W16_GEMM_GATED_MLP(64, 4, 2)
 
 }  // extern "C"

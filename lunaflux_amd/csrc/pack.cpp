@@ -198,7 +198,8 @@ bool w8a16_gemm(int32_t entry, int64_t n, int64_t k, int32_t max_tokens, W8a16Ge
 // One-launch GatedMlp entries (kernels/w8a16.hip, LF_W16_GATED_MLP): the
 // profile's gate/up and down column-group parameters. Workspace: h [16 mt
 // rows][I] bf16, the down kernel's split-K partials and arrival counters,
-// then 256 bytes of slice counters, done counter and error word.
+// then 768 bytes: the slice counters and the done counter and error word,
+// one 128-byte line each (the error word in the last line but one).
 struct W8a16Gated {
   int64_t hidden, inter;
   int mt, waves, down_split;
@@ -223,7 +224,7 @@ int64_t w8a16_gated_workspace(const W8a16Gated &g) {
   const int64_t tiles = g.hidden / 16;
   const int64_t down = align_up(g.down_split * tiles * g.mt * 1024, 256) +
                        align_up(tiles / g.waves * 4, 256);
-  return h + down + 256;
+  return h + down + 768;
 }
 
 // W8A8 tile forms (kernels/projection.hip). Output columns per block: BN
@@ -284,7 +285,9 @@ bool w8a8_tiles(bool gate_up, int64_t n, int64_t k, int32_t max_tokens, W8a8Tile
 // kernels/projection.hip), and the sync area of kernels/phases.h at the
 // start of the workspace.
 constexpr int64_t kQuantBlocks = 256;
-int64_t sync_bytes(int64_t steps, int64_t bands) { return align_up(128 + 4 * steps * bands, 256); }
+// (kernels/phases.h: error word, done counter, then one 128-byte line per
+// band counter)
+int64_t sync_bytes(int64_t steps, int64_t bands) { return 256 + 128 * steps * bands; }
 int64_t quantized_rows_bytes(int64_t rows, int64_t k) {
   return align_up(rows * k, 256) + align_up(rows * 4, 256);
 }
@@ -316,6 +319,30 @@ int64_t w8a8_gated_workspace(const W8a8Gated &g, int64_t hidden, int64_t inter) 
   const int64_t cap = g.gu.bands * g.gu.bm;
   return sync_bytes(3, g.gu.bands) + quantized_rows_bytes(cap, hidden) + align_up(cap * inter * 2, 256) +
          quantized_rows_bytes(cap, inter);
+}
+
+int64_t w8a16_gemm_workspace(const W8a16Gemm &g);
+
+// One-launch W8A16 GatedMlp for profiles of 65..128 rows (kernels/
+// w8a16_gemm.hip, GatedMlpGemm): where the gate/up launch would take the
+// n128 tiles unsplit, the gate/up blocks and the down launch's blocks (its
+// own tile and split) in one grid. Workspace: h [128][I] bf16, the down
+// GEMM's workspace, 256 bytes of count, done counter and error word.
+struct W8a16GatedGemm {
+  W8a16Gemm gu, dn;
+};
+bool w8a16_gated_gemm(int32_t entry, int64_t hidden, int64_t inter, int32_t max_tokens,
+                      W8a16GatedGemm *out) {
+  if (entry != LF_FP8_ENTRY_W8A16_GATED_MLP || max_tokens <= 64 || max_tokens > 128) return false;
+  if (!w8a16_gemm(LF_FP8_ENTRY_W8A16_GATE_UP, inter, hidden, max_tokens, &out->gu) ||
+      !w8a16_gemm(LF_FP8_ENTRY_W8A16_DENSE, hidden, inter, max_tokens, &out->dn)) {
+    return false;
+  }
+  return out->gu.bn == 128 && out->gu.split == 1;
+}
+int64_t w8a16_gated_gemm_workspace(const W8a16GatedGemm &g, int64_t inter) {
+  // sync: one 128-byte line per down K-slice counter, done, error, one spare
+  return align_up(128 * inter * 2, 256) + w8a16_gemm_workspace(g.dn) + 128 * g.dn.split + 256;
 }
 
 int64_t w8a16_gemm_workspace(const W8a16Gemm &g) {
@@ -498,6 +525,11 @@ int64_t lunaflux_fp8_gated_mlp_workspace_bytes(int32_t entry, int64_t hidden, in
     }
     return w8a8_gated_workspace(g, hidden, inter);
   }
+  W8a16GatedGemm gg;
+  if (hidden > 0 && inter > 0 && hidden <= kMaxDim && inter <= kMaxDim && hidden % 128 == 0 &&
+      inter % 128 == 0 && w8a16_gated_gemm(entry, hidden, inter, max_tokens, &gg)) {
+    return w8a16_gated_gemm_workspace(gg, inter);
+  }
   const W8a16Gated *g = w8a16_gated(entry, hidden, inter, max_tokens);
   return g == nullptr ? -1 : w8a16_gated_workspace(*g);
 }
@@ -533,6 +565,17 @@ int32_t lunaflux_fp8_gated_mlp_geometry(int32_t entry, int64_t hidden, int64_t i
     std::memset(symbol, 0, LF_FP8_SYMBOL_BYTES);
     std::snprintf(symbol, LF_FP8_SYMBOL_BYTES, "lf_fp8_w8a8_gated_mlp_%s_%s", w8a8_form_name(g.gu.form),
                   w8a8_form_name(g.dn.form));
+    return LF_OK;
+  }
+  W8a16GatedGemm gg;
+  if (hidden <= kMaxDim && inter <= kMaxDim && hidden % 128 == 0 && inter % 128 == 0 &&
+      w8a16_gated_gemm(entry, hidden, inter, max_tokens, &gg)) {
+    const int64_t blocks = gg.gu.blocks_n + gg.dn.blocks_n * gg.dn.split;
+    if (blocks > INT32_MAX) return LF_INVALID_ARGUMENT;
+    const int32_t values[7] = {static_cast<int32_t>(blocks), 1, 1, 512, 1, 1, 0};
+    std::memcpy(dims, values, sizeof(values));
+    std::memset(symbol, 0, LF_FP8_SYMBOL_BYTES);
+    std::snprintf(symbol, LF_FP8_SYMBOL_BYTES, "lf_fp8_w8a16_gated_mlp_m128_n128_n%d", gg.dn.bn);
     return LF_OK;
   }
   const W8a16Gated *g = w8a16_gated(entry, hidden, inter, max_tokens);

@@ -245,7 +245,7 @@ def test_one_launch_w8a8_geometry_and_workspace():
         assert s1 == s0 + "_aq" and d1.grid == (d0.grid[0] + 256, 1, 1) and d1.block == d0.block
         bm = 128 if s0.endswith("_t128") else 256
         bands = -(-m // bm)
-        sync = -(-(128 + 4 * bands) // 256) * 256
+        sync = 256 + 128 * bands      # error, done, one 128-byte line per band counter
         cap = bands * bm
         assert fp8.w8a8_workspace_bytes(entry, n, k, m) == sync + fp8.act_quant_bytes(cap, k)
     d, s = fp8.launch_geometry(_abi.ENTRY_W8A8_QKV_AQ, 6144, 4096, 2048, qkv_split=(4096, 1024))
@@ -264,10 +264,35 @@ def test_one_launch_w8a8_geometry_and_workspace():
         assert s == sym and d.grid == (512 + gx * bands, 1, 1) and d.block == (256, 1, 1), (s, d.grid)
         bm = 128 if "t128" in sym else 256
         cap = bands * bm
-        sync = -(-(128 + 12 * bands) // 256) * 256
+        sync = 256 + 128 * 3 * bands
         want = sync + fp8.act_quant_bytes(cap, h) + cap * i * 2 + fp8.act_quant_bytes(cap, i)
         assert lib.lunaflux_fp8_gated_mlp_workspace_bytes(_abi.ENTRY_W8A8_GATED_MLP, h, i, m) == want
     assert lib.lunaflux_fp8_gated_mlp_workspace_bytes(_abi.ENTRY_W8A8_GATED_MLP, 4000, 14336, 64) == -1
+
+
+def test_w8a16_gated_mlp_geometry():
+    """One-launch W8A16 GatedMlp: the column-group entries at the Llama-3-8B
+    widths for <= 16 / <= 32 rows; for 65..128 rows the LDS-tiled GEMMs
+    (gate/up n128 unsplit, then the down launch's own tile and split) at any
+    widths where gate/up takes n128 unsplit; none for 33..64 rows."""
+    lib = _abi.lib()
+    e = _abi.ENTRY_W8A16_GATED_MLP
+    d, s = fp8.gated_mlp_geometry(4096, 14336, 32)
+    assert s == "lf_fp8_w8a16_gated_mlp_h4096_i14336_m32" and d.grid == (224 + 256, 1, 1)
+    d, s = fp8.gated_mlp_geometry(4096, 14336, 128)
+    dn_dims, dn_sym = fp8.launch_geometry(_abi.ENTRY_W8A16_DENSE, 4096, 14336, 128)
+    assert dn_sym == "lf_fp8_w8a16_dense_m128_n128"
+    assert s == "lf_fp8_w8a16_gated_mlp_m128_n128_n128" and d.grid == (224 + dn_dims.grid[0], 1, 1)
+    assert d.block == (512, 1, 1)
+    ws = lib.lunaflux_fp8_gated_mlp_workspace_bytes(e, 4096, 14336, 128)
+    split = dn_dims.grid[0] // (4096 // 128)
+    assert ws == (128 * 14336 * 2 + fp8.w8a16_workspace_bytes(_abi.ENTRY_W8A16_DENSE, 4096, 14336, 128)
+                  + 128 * split + 256)       # one 128-byte line per slice counter, done, error
+    assert (lib.lunaflux_fp8_gated_mlp_workspace_bytes(e, 4096, 14336, 32)
+            == 32 * 14336 * 2 + fp8.w8a16_workspace_bytes(_abi.ENTRY_W8A16_DENSE, 4096, 14336, 32) + 768)
+    assert fp8.gated_mlp_geometry(4096, 14336, 64) is None
+    assert fp8.gated_mlp_geometry(1024, 2048, 128) is None   # gate/up would split K
+    assert lib.lunaflux_fp8_gated_mlp_workspace_bytes(e, 4096, 14336, 64) == -1
 
 
 class _FakeWorkspace:

@@ -175,7 +175,7 @@ def test_w8a8_gated_mlp_one_launch(rt, hidden, inter, max_tokens, symbol):
             bm = 128 if "t128_t128" in symbol else 256
             bands = -(-max_tokens // bm)
             cap = bands * bm
-            sync = -(-(128 + 12 * bands) // 256) * 256
+            sync = 256 + 128 * 3 * bands   # error, done, one line per band counter
             xq_bytes = -(-cap * hidden // 256) * 256 + -(-cap * 4 // 256) * 256
             h_gpu = one.workspace.read(np.uint16, (m, inter), sync + xq_bytes)
             hq_at = sync + xq_bytes + -(-cap * inter * 2 // 256) * 256
@@ -228,8 +228,8 @@ def test_aq_sticky_error_and_timeout(rt):
     assert not ws.read(np.uint8, (ws.byte_count,)).any(), "workspace not zero-filled"
     assert np.array_equal(buf.run(one, x), want)
     # (2) band 0's counter can never reach its target: the sync area is
-    # [error, ..., done at int 16, band counters from int 32]
-    ws.copy_from_host(np.array([-(1 << 30)], np.int32), offset=32 * 4)
+    # [error line, done line, one 128-byte line per band counter]
+    ws.copy_from_host(np.array([-(1 << 30)], np.int32), offset=256)
     buf.ya.copy_from_host(np.full(max_tokens * n, SENTINEL, np.uint16))
     with pytest.raises(DeviceError):
         one.launch(rt.stream, synchronous=True)
@@ -239,14 +239,15 @@ def test_aq_sticky_error_and_timeout(rt):
     one.check()
 
 
-def test_w8a16_gated_mlp_sticky_error_and_timeout(rt):
+@pytest.mark.parametrize("max_tokens,m", [(32, 24), (128, 100)])
+def test_w8a16_gated_mlp_sticky_error_and_timeout(rt, max_tokens, m):
     """The same failure path for the one-launch W8A16 GatedMlp: a preset
     error word stores nothing; a slice counter preset far below its target
     makes the down blocks of that slice run out of polls without loading h
     or storing; the binding raises, zero-fills, and the next launch is
     bit-identical to the two launches."""
-    rng = np.random.default_rng(9600)
-    hidden, inter, max_tokens, m = 4096, 14336, 32, 24
+    rng = np.random.default_rng(9600 + max_tokens)
+    hidden, inter = 4096, 14336
     _, _, wg = weight(rt, rng, inter, hidden)
     _, _, wu = weight(rt, rng, inter, hidden)
     _, _, wd = weight(rt, rng, hidden, inter)
@@ -266,8 +267,14 @@ def test_w8a16_gated_mlp_sticky_error_and_timeout(rt):
         one.launch(rt.stream, synchronous=True)
     assert np.all(buf.ya.read(np.uint16, (max_tokens, hidden)) == SENTINEL)
     assert np.array_equal(buf.run(one, x), want)
-    # slice counter 0 sits 128 bytes before the error word
-    ws.copy_from_host(np.array([-(1 << 30)], np.int32), offset=err_at - 128)
+    # slice counter 0 opens the sync area: 768 bytes (four slice lines, done,
+    # error, spare) in the column-group form, 128 S + 256 in the 128-row form
+    if max_tokens == 32:
+        sync = 768
+    else:
+        dn_dims, _ = fp8.launch_geometry(_abi.ENTRY_W8A16_DENSE, hidden, inter, max_tokens)
+        sync = 128 * (dn_dims.grid[0] // (hidden // 128)) + 256
+    ws.copy_from_host(np.array([-(1 << 30)], np.int32), offset=ws.byte_count - sync)
     with pytest.raises(DeviceError):
         one.launch(rt.stream, synchronous=True)
     assert np.array_equal(buf.run(one, x), want)

@@ -279,15 +279,17 @@ def test_silu_gated_mlp(rt, family, m, max_tokens):
     parity(y, ref, label=f"mlp {family} m={m}")
 
 
-@pytest.mark.parametrize("m,max_tokens", [(1, 16), (13, 16), (16, 16), (17, 32), (32, 32), (0, 32)])
+@pytest.mark.parametrize("m,max_tokens", [(1, 16), (13, 16), (16, 16), (17, 32), (32, 32), (0, 32),
+                                          (128, 128), (97, 128), (65, 128)])
 def test_gated_mlp_one_launch(rt, m, max_tokens):
     """The one-launch W8A16 GatedMlp at the Llama-3-8B widths (H 4096, I
     14336): against the oracle on a column sample of y (h rounded to bf16
     between the GEMMs, as the two-launch form keeps it); bit-identical to
-    the two-launch form where both use the same column-group kernels (the
-    32-row profile); three launches on one workspace agree bit for bit (the
-    slice and done counters return to zero) and leave the error word 0;
-    rows past M untouched."""
+    the two-launch form where both use the same kernels (the 32-row profile's
+    column groups, the 128-row profile's LDS-tiled GEMMs); three launches on
+    one workspace agree bit for bit (the slice and done counters return to
+    zero) and leave the error word 0; rows past M untouched; then new inputs
+    on the same workspace."""
     from lunaflux_amd import _abi
     from lunaflux_amd.fp8 import _region
     rng = np.random.default_rng(7300 + m + max_tokens)
@@ -321,7 +323,7 @@ def test_gated_mlp_one_launch(rt, m, max_tokens):
         wdc = deq(qd[cols], sd[cols])
         parity(outs[0][:m][:, cols], o.dense_projection(hb, wdc), k=inter, s_abs=abs_sum(hb, wdc),
                label=f"gated mlp one launch m={m}")
-    if max_tokens == 32:
+    if max_tokens in (32, 128):
         ya.copy_from_host(sentinel)
         two = rt.bind_gated_mlp("w8a16", counts, _region(xa, alignment=256), wg, wu, wd,
                                 _region(ya, alignment=256), max_tokens, one_launch=False)
