@@ -330,6 +330,15 @@ def load_tensor(path: str, tensors: dict, payload_offset: int, name: str) -> np.
 
 # -- FP8 projection weights --------------------------------------------------
 def _fp8_linear(path, tensors, off, prefix, rows=None, columns=None):
+    """Codes and scales of `<prefix>.weight` (F8_E4M3 [N, K], no NaN code)
+    with `<prefix>.weight_scale`: F32, N values (one per output channel) or
+    a single value for the whole tensor held as a rank-1 or rank-2 tensor of
+    one element, broadcast to every channel; or `<prefix>.weight_scale_inv`:
+    F32 [ceil(N / 128), ceil(K / 128)] (128 x 128 blocks). A rank-0 scale
+    tensor never gets here: the metadata validation rejects every rank-0
+    tensor with InvalidRank, as the reference's does (metadata.mbt:63-86;
+    such files need their scalars stored as shape [1]). Scales must be
+    finite and not negative."""
     w = tensors.get(prefix + ".weight")
     if w is None:
         raise SafetensorsError("MissingTensor", detail=prefix + ".weight")
@@ -429,7 +438,8 @@ def bind_llama_fp8(shape: LlamaShape, tensors: dict) -> list:
     norm, q, k, v, o, post-attention norm, gate, up, down; final norm; LM
     head). Projections are F8_E4M3 with one scale tensor each; norms and the
     embedding stay BF16; the LM head may be either. The header must hold
-    exactly these tensors (the reference's exact count, bind.mbt:60-66)."""
+    exactly these tensors: the count is checked first, as the reference's
+    exact count is (bind.mbt:57-63), then each tensor in TensorRef order."""
     h, i, v, kv = shape.hidden, shape.intermediate, shape.vocabulary, shape.kv_width
     plan = [("model.embed_tokens.weight", (v, h), "BF16")]
     for layer in range(shape.layers):
@@ -444,8 +454,17 @@ def bind_llama_fp8(shape: LlamaShape, tensors: dict) -> list:
                  (f"{p}.mlp.up_proj.weight", (i, h), "F8_E4M3"),
                  (f"{p}.mlp.down_proj.weight", (h, i), "F8_E4M3")]
     plan += [("model.norm.weight", (h,), "BF16"), ("lm_head.weight", (v, h), None)]
+    # The count first, as bind.mbt:57-63 does before any per-tensor check:
+    # 3 + 9 L tensors of the dense vocabulary plus one scale tensor per FP8
+    # projection (7 L, and the LM head when it is F8_E4M3). A file holding
+    # anything else (e.g. per-projection input_scale tensors) fails here.
+    head = tensors.get("lm_head.weight")
+    expected = 3 + 9 * shape.layers + 7 * shape.layers + (
+        1 if head is not None and head.dtype == "F8_E4M3" else 0)
+    if len(tensors) != expected:
+        raise LlamaWeightsError("TensorCountMismatch",
+                                detail=f"expected {expected}, found {len(tensors)}")
     bindings = []
-    scale_tensors = 0
     for name, dims, dtype in plan:
         ref = len(bindings)
         t = tensors.get(name)
@@ -467,12 +486,7 @@ def bind_llama_fp8(shape: LlamaShape, tensors: dict) -> list:
                     scale = base + suffix
             if scale is None:
                 raise LlamaWeightsError("MissingTensor", ref, base + ".weight_scale[_inv]")
-            scale_tensors += 1
         bindings.append(TensorBinding(ref, name, want, tuple(dims), scale))
-    expected = 3 + 9 * shape.layers + scale_tensors
-    if len(tensors) != expected:
-        raise LlamaWeightsError("TensorCountMismatch",
-                                detail=f"expected {expected}, found {len(tensors)}")
     return bindings
 
 

@@ -225,6 +225,25 @@ def test_limits(tmp_path):
         assert err.value.kind == "InvalidLimit"
 
 
+def test_rank0_scale_is_rejected_by_metadata_validation(tmp_path):
+    """A scalar (rank-0) weight_scale, the per-tensor form some FP8
+    checkpoints use, fails the metadata validation with InvalidRank, as
+    every rank-0 tensor does in the reference (metadata.mbt:63-86); the same
+    scale stored as shape [1] is admitted and broadcast."""
+    rng = np.random.default_rng(8)
+    q, _ = synth.weight(rng, 16, 128)
+    path = str(tmp_path / "scalar.safetensors")
+    write_safetensors(path, {"w.weight": ("F8_E4M3", q),
+                             "w.weight_scale": ("F32", np.array(0.5, np.float32))})
+    with pytest.raises(checkpoint.SafetensorsError) as err:
+        checkpoint.read_metadata(path)
+    assert err.value.kind == "InvalidRank"
+    write_safetensors(path, {"w.weight": ("F8_E4M3", q),
+                             "w.weight_scale": ("F32", np.array([0.5], np.float32))})
+    _, scales, mode = checkpoint.load_fp8_linear(path, "w")
+    assert mode == fp8.PER_CHANNEL and np.all(scales == np.float32(0.5)) and scales.shape == (16,)
+
+
 def test_scale_shapes_and_values(tmp_path):
     rng = np.random.default_rng(7)
     q, s = synth.weight(rng, 16, 128)
@@ -318,10 +337,28 @@ def test_bind_llama_fp8_in_tensor_ref_order(tmp_path):
     assert b[-1].dtype == "F8_E4M3"
 
 
+def _swap(t, name):
+    """Replaces tensor `name` by an unrelated one: the count stays right."""
+    t.pop(name)
+    t["unrelated"] = ("F32", np.zeros(1, np.float32))
+
+
+def _incomplete_and_misshapen(t):
+    t.pop("model.layers.1.mlp.up_proj.weight_scale")
+    t["model.layers.0.self_attn.k_proj.weight"] = ("F8_E4M3", np.zeros((128, 128), np.uint8))
+
+
 @pytest.mark.parametrize("change,kind", [
-    (lambda t: t.pop("model.layers.1.mlp.up_proj.weight_scale"), "MissingTensor"),
-    (lambda t: t.pop("model.layers.0.self_attn.k_proj.weight"), "MissingTensor"),
+    (lambda t: _swap(t, "model.layers.1.mlp.up_proj.weight_scale"), "MissingTensor"),
+    (lambda t: _swap(t, "model.layers.0.self_attn.k_proj.weight"), "MissingTensor"),
+    (lambda t: t.pop("model.layers.1.mlp.up_proj.weight_scale"), "TensorCountMismatch"),
     (lambda t: t.update({"extra": ("F32", np.zeros(1, np.float32))}), "TensorCountMismatch"),
+    # the count is checked before any tensor (bind.mbt:57-63)
+    (_incomplete_and_misshapen, "TensorCountMismatch"),
+    # activation scales of static-quantized checkpoints are not part of the
+    # bound vocabulary
+    (lambda t: t.update({"model.layers.0.self_attn.q_proj.input_scale":
+                         ("F32", np.ones(1, np.float32))}), "TensorCountMismatch"),
     (lambda t: t.update({"model.norm.weight": ("BF16", np.zeros((1, 128), np.uint16))}),
      "ShapeRankMismatch"),
     (lambda t: t.update({"model.layers.0.self_attn.k_proj.weight":
