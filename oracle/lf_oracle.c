@@ -562,7 +562,7 @@ static void *moe_worker(void *arg) {
         float p = h[i] * dn[i];
         acc = acc + p;
       }
-      ya[n] = acc;
+      ya[n] = (job->transform & 8) ? lfo_bf16_to_f32(lfo_bf16_rne(acc)) : acc;
     }
   }
   free(h);

@@ -161,7 +161,9 @@ int32_t lfo_moe_sort(const int32_t *topk_experts, int32_t tokens, int32_t k,
  *   to bf16 (RNE); bits 1-2 then quantize-dequantize it to e4m3 with the
  *   lfo_quantize_rows formula (1: one scale per row, 2: one scale per 128
  *   columns). 0 keeps the fp32 h_a of the reference MLP (mlp.mbt:27-31).
- *   y_a = h_a Wd_e^T                                     (fp32)
+ *   y_a = h_a Wd_e^T                                     (fp32; bit 3 of
+ *   hidden_transform rounds it to bf16 (RNE), as a device that stores y in
+ *   bf16 between the down GEMM and the combine)
  *   out_t = sum_j w_tj * y_(t,j), j ascending, fp32.
  * out is [tokens, hidden] fp32. */
 int32_t lfo_moe_mlp(const float *x, int32_t tokens, int32_t hidden,

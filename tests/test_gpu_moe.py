@@ -19,7 +19,7 @@ import pytest
 
 import oracle_lib as o
 from lunaflux_amd import synth
-from parity import parity
+from parity import abs_sum, combine, moved_codes_explained, parity, swiglu_midpoint_tol
 
 pytestmark = pytest.mark.gpu
 
@@ -115,10 +115,13 @@ def check_output(x, weights, ex, w, out, block, label, st):
     np.testing.assert_array_equal(st["hq"], hq_ref)
     np.testing.assert_array_equal(st["hs"].reshape(hs_ref.shape[0], -1), hs_ref.reshape(hs_ref.shape[0], -1))
     hr = o.dequantize(hq_ref, hs_ref, mode=mode, group=grp)
+    h_tol = np.zeros(st["h"].shape, np.float64)
     for e in np.unique(experts):
         rows = np.flatnonzero(experts == e)
         xe = xr[tokens[rows]]
-        h_ref[rows] = o.silu_mul_array(o.dense_projection(xe, wg_f[e]), o.dense_projection(xe, wu_f[e]))
+        g, u = o.dense_projection(xe, wg_f[e]), o.dense_projection(xe, wu_f[e])
+        h_ref[rows] = o.silu_mul_array(g, u)
+        h_tol[rows] = swiglu_midpoint_tol(g, u, abs_sum(xe, wg_f[e]), abs_sum(xe, wu_f[e]), xe.shape[1])
         y_ref[rows] = o.dense_projection(hr[rows], wd_f[e])
     # 2. grouped gate/up + SwiGLU
     parity(st["h"], h_ref, label=label + " gate_up")
@@ -131,9 +134,22 @@ def check_output(x, weights, ex, w, out, block, label, st):
     # the combine's arithmetic is defined exactly (products and sums each
     # rounded, ascending j, from 0): bit-identical on the GPU's own y
     np.testing.assert_array_equal(out, o.bf16_round(comb))
-    # end to end against the oracle from the original inputs
-    ref = o.moe_mlp(xr, wg_f, wu_f, wd_f, ex, w, hidden_transform=5 if block else 3, threads=8)
-    parity(out, ref, rel_l2=1e-2, max_abs=0.25, label=label + " end-to-end")
+    # End to end from the original inputs. h is re-quantized to e4m3 between
+    # the GEMMs, and one bf16 ulp of h can move an e4m3 code across its
+    # rounding boundary, so: (a) every code that differs from the oracle's
+    # own (its bf16 h, quantized) must be such a move; (b) the output must
+    # meet the BASELINE bar against the oracle's down and combine (y rounded
+    # to bf16, as the device stores it; the GPU's routing weights, held
+    # within 2e-6 of the oracle's by check_routing) over the GPU's codes,
+    # which are the oracle's except the moved ones; (c) the pure oracle (its
+    # own codes and weights) at the looser bound.
+    hq_o, hs_o = o.quantize_rows(o.bf16_decode(o.bf16_round(h_ref)), group=grp or None)
+    moved = moved_codes_explained(h_ref, st["h"], h_tol, hq_o, st["hq"], hs_o, st["hs"], label)
+    y_gpu_codes = y_ref[st["pos"].reshape(-1, k)]          # [T, k, H] from the GPU's codes
+    parity(out, combine(st["topk_w"], y_gpu_codes), label=label + " end-to-end (GPU h codes)")
+    ref = o.moe_mlp(xr, wg_f, wu_f, wd_f, ex, w, hidden_transform=(5 if block else 3) | 8, threads=8)
+    print(f"{label}: {moved} of {hq_o.size} h codes moved across a rounding boundary", flush=True)
+    parity(out, ref, rel_l2=1e-2, max_abs=0.25, label=label + " end-to-end (oracle h codes)")
 
 
 @pytest.mark.parametrize("t,e,k,mode", [(100, 8, 2, 0), (37, 64, 6, 1), (1, 8, 2, 0), (300, 16, 4, 0),

@@ -20,17 +20,21 @@ At full size the oracle cannot recompute every GEMM in seconds, so:
   block plus random columns: gate/up + SwiGLU from the GPU's quantized
   tokens, down from the GPU's quantized h, at the BASELINE bar;
 * the combine at full size from the GPU's y and routing weights;
-* end to end from the original inputs for a sample of tokens through the
-  oracle's own grouped MLP (lfo_moe_mlp over the experts those tokens use),
-  at the documented end-to-end bound (h is re-quantized to e4m3 between the
-  GEMMs).
+* end to end from the original inputs for 64 sampled tokens (all 32 at
+  T = 32): the oracle's own h codes against the GPU's, every difference a
+  move across an e4m3 rounding boundary (the two bf16 h values within one
+  ulp); the output at the BASELINE bar against the oracle's down and
+  combine (y rounded to bf16, as the device stores it) over the GPU's
+  codes; and at the documented looser bound against lfo_moe_mlp with its
+  own codes.
 """
 import numpy as np
 import pytest
 
 import oracle_lib as o
 from lunaflux_amd import synth
-from parity import abs_sum, parity, swiglu_midpoint_tol
+from parity import (abs_sum, combine, combine_tol, moved_codes_explained, parity,
+                    swiglu_midpoint_tol)
 from test_gpu_moe import check_routing
 
 pytestmark = pytest.mark.gpu
@@ -112,7 +116,7 @@ def run_full(rt, rng, t, e, k, hidden, inter, route_mode, block, logits):
     return x, weights, out, st
 
 
-def check_full(x, weights, out, st, logits, k, route_mode, block, rng, label, e2e_tokens=6):
+def check_full(x, weights, out, st, logits, k, route_mode, block, rng, label, e2e_tokens=64):
     qg, sg, qu, su, qd, sd = weights
     e = logits.shape[1]
     grp, dmode = (128, 1) if block else (None, 0)
@@ -162,21 +166,56 @@ def check_full(x, weights, out, st, logits, k, route_mode, block, rng, label, e2
     # the combine's arithmetic is defined exactly (products and sums each
     # rounded, ascending j, from 0): bit-identical on the GPU's own y
     np.testing.assert_array_equal(out, o.bf16_round(comb))
-    # end to end from the original inputs, for a sample of tokens: the
-    # lightest experts' tokens first, then random ones
+    # End to end from the original inputs, for e2e_tokens sampled tokens
+    # (the lightest experts' tokens first, then random ones). h is
+    # re-quantized to e4m3 between the GEMMs, and one bf16 ulp of h can move
+    # an e4m3 code across its rounding boundary, so: (a) the oracle's own h
+    # codes (its sequential fp32 gate/up, SiLU, bf16 rounding and quantizer:
+    # lfo_moe_mlp's arithmetic) are formed for every sampled assignment, and
+    # every code that differs from the GPU's must be such a move; (b) the
+    # output must meet the BASELINE bar against the oracle's down and combine
+    # (y rounded to bf16, as the device stores it) over the GPU's codes,
+    # which are the oracle's except the moved ones; (c) the pure oracle (its
+    # own codes, lfo_moe_mlp) at the looser bound.
     counts = np.diff(offsets)
     light = [int(tokens[offsets[ee]]) for ee in np.argsort(counts) if counts[ee] > 0][:2]
-    toks = np.unique(np.concatenate([light, rng.choice(ex.shape[0], e2e_tokens - len(light),
-                                                       replace=False)]))
+    n_tok = min(e2e_tokens, ex.shape[0])
+    toks = np.unique(np.concatenate([light, rng.choice(ex.shape[0], n_tok - len(light), replace=False)]))
     used = np.unique(ex[toks])
     remap = np.full(e, -1, np.int32)
     remap[used] = np.arange(len(used))
     wgf = np.stack([dequant_expert(qg[u_], sg[u_], block) for u_ in used])
     wuf = np.stack([dequant_expert(qu[u_], su[u_], block) for u_ in used])
     wdf = np.stack([dequant_expert(qd[u_], sd[u_], block) for u_ in used])
+    pos_of = st["pos"].reshape(-1, k)
+    y_gpu_codes = np.zeros((len(toks), k, hidden), np.float32)
+    y_abs = np.zeros((len(toks), k, hidden), np.float64)
+    moved = codes = 0
+    for ui, ue in enumerate(used):
+        sel = np.argwhere(ex[toks] == ue)          # (index in toks, pick j)
+        xe = xr[toks[sel[:, 0]]]
+        g = o.project_values_mt(xe, wgf[ui], 16)
+        u = o.project_values_mt(xe, wuf[ui], 16)
+        h_o = o.silu_mul_array(g, u)
+        h_tol = swiglu_midpoint_tol(g, u, abs_sum(xe, wgf[ui]), abs_sum(xe, wuf[ui]), hidden)
+        hq_o, hs_o = o.quantize_rows(o.bf16_decode(o.bf16_round(h_o)), group=grp)
+        p = pos_of[toks[sel[:, 0]], sel[:, 1]]
+        moved += moved_codes_explained(h_o, st["h"][p], h_tol, hq_o, st["hq"][p], hs_o, st["hs"][p],
+                                       f"{label} expert {ue}")
+        codes += hq_o.size
+        hr_g = o.dequantize(st["hq"][p], st["hs"][p], mode=dmode, group=grp or 0)
+        y_gpu_codes[sel[:, 0], sel[:, 1]] = o.project_values_mt(hr_g, wdf[ui], 16)
+        y_abs[sel[:, 0], sel[:, 1]] = abs_sum(hr_g, wdf[ui])
+    print(f"{label} end-to-end: {len(toks)} tokens; {moved} of {codes} h codes moved across a "
+          f"rounding boundary", flush=True)
+    # (routing weights: the GPU's, which check_routing holds within 2e-6 of
+    # the oracle's softmax; a one-ulp weight can flip an output rounding)
+    wg_ = st["topk_w"][toks]
+    parity(out[toks], combine(wg_, y_gpu_codes), label=label + " end-to-end (GPU h codes)",
+           value_tol=combine_tol(wg_, y_gpu_codes, y_abs, inter))
     ref = o.moe_mlp(xr[toks], wgf, wuf, wdf, remap[ex[toks]], w[toks],
-                    hidden_transform=5 if block else 3, threads=16)
-    parity(out[toks], ref, rel_l2=1e-2, max_abs=0.25, label=label + " end-to-end")
+                    hidden_transform=(5 if block else 3) | 8, threads=16)
+    parity(out[toks], ref, rel_l2=1e-2, max_abs=0.25, label=label + " end-to-end (oracle h codes)")
     return ex
 
 

@@ -103,3 +103,34 @@ def test_moe_mlp_hidden_quantization_transform():
             q, s = o.quantize_rows(hb, group=group)
             hq = o.dequantize(q, s if group else s, mode=1 if group else 0, group=group or 0)
             np.testing.assert_array_equal(out[tok], o.dense_projection(hq, wd[ex[tok, 0]])[0])
+
+
+def test_moe_mlp_bf16_y_transform():
+    """Bit 3 of hidden_transform rounds each y_a to bf16 before the combine
+    (the device stores y in bf16): the result equals the per-token sum over
+    the k picks of w_tj * bf16(y_a) with y_a from the dense oracle, and
+    differs from the fp32-y result where a rounding changes a sum."""
+    rng = np.random.default_rng(25)
+    t, h, inter, e, k = 5, 32, 24, 4, 2
+    x = rng.standard_normal((t, h)).astype(np.float32)
+    wg = (rng.standard_normal((e, inter, h)) * 0.2).astype(np.float32)
+    wu = (rng.standard_normal((e, inter, h)) * 0.2).astype(np.float32)
+    wd = (rng.standard_normal((e, h, inter)) * 0.2).astype(np.float32)
+    ex, w = o.route_topk(rng.standard_normal((t, e)).astype(np.float32), k, o.ROUTE_TOPK_SOFTMAX)
+    for transform in (8, 9, 11):
+        out = o.moe_mlp(x, wg, wu, wd, ex, w, hidden_transform=transform, threads=2)
+        for tok in range(t):
+            acc = np.zeros(h, np.float32)
+            for j in range(k):
+                _, hid = o.silu_gated_mlp(x[tok:tok + 1], wg[ex[tok, j]], wu[ex[tok, j]], wd[ex[tok, j]],
+                                          return_hidden=True)
+                if transform & 1:
+                    hid = o.bf16_decode(o.bf16_round(hid))
+                if transform & 2:
+                    q, sc = o.quantize_rows(hid)
+                    hid = o.dequantize(q, sc)
+                y = o.bf16_decode(o.bf16_round(o.dense_projection(hid, wd[ex[tok, j]])))[0]
+                acc = (acc + (w[tok, j] * y).astype(np.float32)).astype(np.float32)
+            np.testing.assert_array_equal(out[tok], acc)
+    assert not np.array_equal(o.moe_mlp(x, wg, wu, wd, ex, w, hidden_transform=8),
+                              o.moe_mlp(x, wg, wu, wd, ex, w, hidden_transform=0))
