@@ -169,8 +169,38 @@ enum lf_fp8_entry {
   LF_FP8_ENTRY_W8A8_DENSE_AQ = 11,
   LF_FP8_ENTRY_W8A8_QKV_AQ = 12,
   LF_FP8_ENTRY_W8A8_GATE_UP_AQ = 13,
-  LF_FP8_ENTRY_W8A8_GATED_MLP = 14
+  LF_FP8_ENTRY_W8A8_GATED_MLP = 14,
+  /* Weights with 128 x 128 block scales (LF_FP8_SCALE_BLOCK128), below */
+  LF_FP8_ENTRY_W8A16_DENSE_B128 = 15,
+  LF_FP8_ENTRY_W8A16_QKV_B128 = 16,
+  LF_FP8_ENTRY_W8A16_GATE_UP_B128 = 17,
+  LF_FP8_ENTRY_W8A8_DENSE_B128 = 18,
+  LF_FP8_ENTRY_W8A8_QKV_B128 = 19,
+  LF_FP8_ENTRY_W8A8_GATE_UP_B128 = 20,
+  LF_FP8_ENTRY_W8A8_GATED_MLP_B128 = 21
 };
+
+/* Block-scaled projections (checkpoints whose weights carry weight_scale_inv
+ * 128 x 128 block scales: W = q s[n / 128][k / 128]); N and K multiples of
+ * 128, every Q / K / V width of a QKV operation too.
+ *  W8A16: lf_fp8_w8a16_{dense,qkv,gate_up}_b128_m{16,32,64,128}
+ *      operands and workspace as the per-channel W8A16 entries
+ *      (lunaflux_fp8_w8a16_workspace_bytes with the _B128 entry); the
+ *      column-group form for every profile, each k-tile's products scaled by
+ *      its block scale: y = sum_kt s[n / 128][kt] sum_{k in kt} x_k q_nk.
+ *  W8A8: lf_fp8_w8a8_{dense,qkv,gate_up}_b128 (counts, x, w..., y, ws), one
+ *      launch each: x quantized per token per 128-column group (amax over
+ *      the group, the per-token quantizer's arithmetic) inside the launch,
+ *      then y = sum_kt sa[m][kt] s[n / 128][kt] sum_{k in kt} qa_mk q_nk on
+ *      128 x 128 tiles. ws: lunaflux_fp8_w8a8_workspace_bytes with the _B128
+ *      entry, error word at LF_FP8_AQ_ERROR_OFFSET as for the _AQ entries.
+ *      lf_fp8_w8a8_gated_mlp_b128 (counts, x, wg, wu, wd, y, ws): GatedMlp
+ *      in one launch (group quantizer, gate/up + SwiGLU, group quantizer of
+ *      h, down), lunaflux_fp8_gated_mlp_geometry / _workspace_bytes with
+ *      LF_FP8_ENTRY_W8A8_GATED_MLP_B128.
+ * The geometry functions take the _B128 entries as the per-channel ones;
+ * admission requires block scales for them (and channel scales for every
+ * other dense entry). */
 
 /* One launch per W8A8 operation (the plan binds one AOT entry point per
  * operation, kernels/launch_contract/types.mbt:16-27, and rejects a second
@@ -204,9 +234,10 @@ int64_t lunaflux_fp8_w8a8_workspace_bytes(int32_t entry, int64_t n, int64_t k, i
  * carry the format's magic, version and layout, the shape (rows = N,
  * columns = K, experts; 1 for the dense families) and the format's own
  * offsets, and region_bytes must equal lunaflux_fp8_weight_region_bytes for
- * it. LF_UNSUPPORTED for a valid region with 128 x 128 block scales on a
- * dense, QKV or gate/up entry (their kernels read one scale per output
- * channel; only LF_FP8_ENTRY_GROUPED admits block scales);
+ * it. LF_UNSUPPORTED for a valid region whose scale mode is not the
+ * entry's: block scales on a per-channel dense, QKV, gate/up or GatedMlp
+ * entry (their kernels read one scale per output channel), channel scales
+ * on a _B128 entry (LF_FP8_ENTRY_GROUPED admits both);
  * LF_INVALID_ARGUMENT for anything else that does not hold. The
  * shape-specialized W8A16 entries start streaming weights before they read
  * the header, so this check is what bounds their reads. */

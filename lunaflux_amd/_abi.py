@@ -57,6 +57,13 @@ ENTRY_W8A8_DENSE_AQ = 11
 ENTRY_W8A8_QKV_AQ = 12
 ENTRY_W8A8_GATE_UP_AQ = 13
 ENTRY_W8A8_GATED_MLP = 14
+ENTRY_W8A16_DENSE_B128 = 15
+ENTRY_W8A16_QKV_B128 = 16
+ENTRY_W8A16_GATE_UP_B128 = 17
+ENTRY_W8A8_DENSE_B128 = 18
+ENTRY_W8A8_QKV_B128 = 19
+ENTRY_W8A8_GATE_UP_B128 = 20
+ENTRY_W8A8_GATED_MLP_B128 = 21
 LF_FP8_GATED_MLP_ERROR_OFFSET_FROM_END = 128
 LF_FP8_AQ_ERROR_OFFSET = 0
 

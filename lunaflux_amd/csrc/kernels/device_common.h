@@ -38,6 +38,7 @@ struct WeightHeader {
 
 constexpr uint32_t kWeightMagic = 0x5738464Cu;
 constexpr uint32_t kScalePerChannel = 1u;
+constexpr uint32_t kScaleBlock128 = 2u;
 // Header size = tile_offset of every region written by the host pack.
 constexpr uint64_t kWeightHeaderBytes = 256;
 constexpr int kTileBytes = 2048;
@@ -47,21 +48,19 @@ LF_DEVICE const WeightHeader &header_of(const uint8_t *region) {
   return *reinterpret_cast<const WeightHeader *>(region);
 }
 
-// The dense, QKV and gate/up kernels read one fp32 scale per output channel
-// (s[n] for n < N). A 128 x 128 block-scaled region holds (N/128)(K/128)
-// scales, so those kernels refuse it (and a region without the pack's magic)
-// before any other read; the host admission rejects such a binding with
-// LF_UNSUPPORTED. MODE 1 (QKV) checks all three weights.
-template <int MODE>
+// The per-channel dense, QKV and gate/up kernels read one fp32 scale per
+// output channel (s[n] for n < N); the _b128 kernels read (N/128)(K/128)
+// block scales. Each refuses a region of the other scale mode (and one
+// without the pack's magic) before any other read; the host admission
+// rejects such a binding. MODE 1 (QKV) checks all three weights.
+template <int MODE, uint32_t SCALE = kScalePerChannel>
 LF_DEVICE bool dense_regions_ok(const uint8_t *w0, const uint8_t *w1, const uint8_t *w2) {
-  bool ok = header_of(w0).magic == kWeightMagic && header_of(w0).scale_mode == kScalePerChannel;
+  bool ok = header_of(w0).magic == kWeightMagic && header_of(w0).scale_mode == SCALE;
   if (MODE != 0) {
-    ok = ok && header_of(w1).magic == kWeightMagic &&
-         header_of(w1).scale_mode == kScalePerChannel;
+    ok = ok && header_of(w1).magic == kWeightMagic && header_of(w1).scale_mode == SCALE;
   }
   if (MODE == 1) {
-    ok = ok && header_of(w2).magic == kWeightMagic &&
-         header_of(w2).scale_mode == kScalePerChannel;
+    ok = ok && header_of(w2).magic == kWeightMagic && header_of(w2).scale_mode == SCALE;
   }
   return ok;
 }

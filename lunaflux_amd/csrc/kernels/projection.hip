@@ -519,6 +519,227 @@ __device__ __forceinline__ int w8a8_tiled_kernel(uint8_t *smem, const int32_t *c
 }
 
 // ---------------------------------------------------------------------------
+// Block-scaled W8A8: weights with 128 x 128 block scales (s[N/128][K/128]),
+// activations quantized per 128-column group (the per-group quantizer's
+// codes and scales), so both scales change with the k-tile:
+//   y[m][n] = sum_kt (sa[m][kt] sw[n / 128][kt]) sum_{k in kt} qa[m][k] qw[n][k]
+// in fp32, each k-tile's products folded into the running sum with its two
+// scales (the main loop of w8a8_v3.h with a fold, as the block-scaled
+// grouped GEMM does), no scale in the epilogue. The activation scales are
+// stored k-tile-major (scales_t[kt][cap]: a 128-row tile's scales of one
+// k-tile are 512 contiguous bytes) and arrive with each k-step's operands
+// (one more LDS-direct load per wave, ScaleSide) in a window of NS slots,
+// so K is not limited by LDS; the weight block scales are wave-uniform and
+// read with scalar loads.
+// ---------------------------------------------------------------------------
+LF_DEVICE const float *uniform_f32(const float *p) {
+  return reinterpret_cast<const float *>(w8a8v3::uniform_ptr(reinterpret_cast<const uint8_t *>(p)));
+}
+
+// Per-128-column-group quantizer of rows row0 .. row0 + rows - 1 (a chunk of
+// a one-launch operation): the arithmetic of quantize_groups_wave (16 lanes
+// per group, four groups per wave instruction, loads of eight quads in
+// flight), codes in the row-major act-quant layout and the scale of (row,
+// group g) at scales_t[g cap + row]. Wave gw of nw takes quads gw, gw + nw,
+// ...; THROUGH: stores written through the XCD's L2 (phases.h).
+template <bool THROUGH>
+LF_DEVICE void quantize_group_rows(const uint16_t *x, int K, int row0, int rows, uint8_t *xq,
+                                   float *scales_t, int cap, int gw, int nw) {
+  const int lane = threadIdx.x & 63;
+  const int per_row = K >> 7;
+  const int groups = rows * per_row;
+  const int quads = (groups + 3) >> 2;
+  constexpr int kBatch = 8;
+  for (int q0 = gw; q0 < quads; q0 += kBatch * nw) {
+    uint4 v[kBatch];
+    uint64_t base[kBatch];
+    int sidx[kBatch];
+    bool live[kBatch];
+#pragma unroll
+    for (int b = 0; b < kBatch; ++b) {
+      const int gid = 4 * (q0 + b * nw) + (lane >> 4);
+      live[b] = gid < groups;
+      const int r = live[b] ? gid / per_row : 0, kg = live[b] ? gid - r * per_row : 0;
+      base[b] = static_cast<uint64_t>(row0 + r) * K + kg * 128 + (lane & 15) * 8;
+      sidx[b] = kg * cap + row0 + r;
+      v[b] = live[b] ? *reinterpret_cast<const uint4 *>(x + base[b]) : make_uint4(0u, 0u, 0u, 0u);
+    }
+#pragma unroll
+    for (int b = 0; b < kBatch; ++b) {
+      float amax = bf16x8_amax(v[b], 0.0f);
+      amax = fmaxf(amax, dpp_f32<0xB1>(amax));   // quad_perm [1, 0, 3, 2]
+      amax = fmaxf(amax, dpp_f32<0x4E>(amax));   // quad_perm [2, 3, 0, 1]
+      amax = fmaxf(amax, dpp_f32<0x141>(amax));  // row_half_mirror
+      amax = fmaxf(amax, dpp_f32<0x140>(amax));  // row_mirror
+      const bool zero = amax == 0.0f;
+      const float ratio = zero ? 0.0f : 448.0f / amax;
+      if (live[b]) {
+        const uint2 e = bf16x8_encode(v[b], ratio, zero);
+        store_codes8<THROUGH>(xq + base[b], e.x, e.y);
+        if ((lane & 15) == 0) store_scale<THROUGH>(scales_t + sidx[b], zero ? 0.0f : amax / 448.0f);
+      }
+    }
+  }
+}
+
+// Fold of one k-tile: acc += products x (sa[row][kt] x sw[block][kt]).
+template <class T>
+struct DenseBlockFold {
+  static constexpr bool kActive = true;
+  static constexpr int kBM = T::kWaveM * T::kWgm;
+  const float *win;           // LDS [NS][kBM]: slot kt % NS holds k-tile kt's row scales
+  int wm, lane;
+  const float *sw[T::kFN];    // fragment j: [KT] scales of its 128-column block (wave-uniform)
+  template <class A>
+  LF_DEVICE void operator()(int kt, const A &step, A &acc, int) const {
+    float swk[T::kFN];
+#pragma unroll
+    for (int j = 0; j < T::kFN; ++j) swk[j] = sw[j][kt];
+    const float *sa_k = win + (kt % T::kStages) * kBM;
+#pragma unroll
+    for (int i = 0; i < T::kFM; ++i) {
+#pragma unroll
+      for (int rr = 0; rr < 4; ++rr) {
+        const float sa = sa_k[w8a8v3::acc_row<T>(wm, i, lane, rr)];
+#pragma unroll
+        for (int j = 0; j < T::kFN; ++j) acc[i][j][rr] += step[i][j][rr] * (sa * swk[j]);
+      }
+    }
+  }
+};
+
+// Side load of k-step kt: the tile's kBM activation scales of k-tile kt
+// (scales_t row kt from the tile's first row) into window slot kt % NS,
+// kBM / waves rows per wave (the first 16-byte lanes of one instruction).
+template <class T>
+struct ScaleSide {
+  static constexpr int kIns = 1;
+  static constexpr int kBM = T::kWaveM * T::kWgm;
+  static constexpr int kLanes = kBM / T::kWaves / 4;
+  static_assert(kLanes >= 1 && kLanes <= 64 && kBM % (4 * T::kWaves) == 0, "scale rows per wave");
+  const uint8_t *base;  // scales_t + first row of the tile
+  uint64_t stride;      // bytes per k-tile: cap * 4
+  uint32_t win;         // LDS byte offset of the window
+  LF_DEVICE void issue(int kt, int slot) const {
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const uint32_t part = static_cast<uint32_t>(wave) * kLanes * 16;
+    if (lane < kLanes) {
+      w8a8v3::dma16(w8a8v3::uniform_ptr(base + static_cast<uint64_t>(kt) * stride), part + lane * 16,
+                    win + static_cast<uint32_t>(slot) * kBM * 4 + part);
+    }
+  }
+};
+
+// The block-scaled GEMM on one tile of the 128 x 128 form (4 waves, a block
+// of T's shape): operand mapping, gate and THROUGH as w8a8_tiled_kernel; M
+// live rows of a workspace sized for cap rows (xq [cap, K] codes, scales_t
+// [K / 128][cap]); win: the block's window, T::kStages x BM floats of LDS.
+template <class T, int GROUP, int MODE, bool THROUGH = false, class Gate = Open>
+LF_DEVICE int w8a8_b128_gemm(uint8_t *smem, float *win, int M, const uint8_t *xq, const float *scales_t,
+                             int cap, const uint8_t *w0, const uint8_t *w1, const uint8_t *w2, uint16_t *y,
+                             int bid, const Gate &gate) {
+  constexpr int BM = T::kWaveM * T::kWgm, BN = T::kWaveN * T::kWgn;
+  const WeightHeader &h0 = header_of(w0);
+  const int K = static_cast<int>(h0.columns);
+  const int KT = K >> 7;
+  const int tq = static_cast<int>(h0.rows) >> 4;
+  const int tk = MODE == 1 ? static_cast<int>(header_of(w1).rows) >> 4 : 0;
+  const int ld = dense_ld<MODE>(w0, w1, w2);
+  const int gx = dense_gx<MODE, BN>(ld);
+  int bx, by;
+  if (!w8a8v3::tile_of_block(bid, gx, (M + BM - 1) / BM, GROUP, bx, by)) return -1;
+  const int m0 = by * BM;
+  if (!gate(m0)) return -1;
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int wm = wave / T::kWgn, wn = wave % T::kWgn;
+
+  // Weight tile of block slot s: region, tile index inside it, output column
+  // (the mapping of w8a8_tiled_kernel).
+  auto slot = [&](int s, const uint8_t *&region, int &t, int &ocol) {
+    if (MODE == 2) {
+      const int sw = s / T::kFN, f = s % T::kFN;
+      const bool up = f >= T::kFN / 2;
+      const int col = bx * (BN / 2) + sw * (T::kWaveN / 2) + 16 * (up ? f - T::kFN / 2 : f);
+      region = up ? w1 : w0;
+      t = col >> 4;
+      ocol = col;
+    } else {
+      t = bx * (BN / 16) + s;
+      ocol = t * 16;
+      region = w0;
+      if (MODE == 1) {
+        if (t >= tq + tk) {
+          region = w2;
+          t -= tq + tk;
+        } else if (t >= tq) {
+          region = w1;
+          t -= tq;
+        }
+      }
+    }
+  };
+
+  w8a8v3::Plan<T> plan;
+#pragma unroll
+  for (int q = 0; q < T::kAIns; ++q) {
+    const int tr = w8a8v3::a_load_row<T>(wave, q, lane);
+    const int row = m0 + tr < M ? m0 + tr : M - 1;
+    plan.a[q] = xq + static_cast<uint64_t>(row) * K + w8a8v3::a_load_chunk(tr, lane) * 16;
+  }
+#pragma unroll
+  for (int q = 0; q < T::kBIns; ++q) {
+    const int half = w8a8v3::b_load_half<T>(wave, q);
+    const uint8_t *region;
+    int t, ocol;
+    slot(half >> 1, region, t, ocol);
+    plan.b[q] = expert_tiles(region, 0) + static_cast<uint64_t>(t) * KT * kTileBytes +
+                (half & 1) * 1024 + lane * 16;
+  }
+  DenseBlockFold<T> fold{win, wm, lane, {}};
+  int ocol[T::kFN];
+#pragma unroll
+  for (int j = 0; j < T::kFN; ++j) {
+    const uint8_t *region;
+    int t;
+    slot(wn * T::kFN + j, region, t, ocol[j]);
+    // the 16-column tile t lies in 128-row block t / 8 of its region
+    fold.sw[j] = uniform_f32(expert_scales(region, 0) + static_cast<uint64_t>(t >> 3) * KT);
+  }
+  const ScaleSide<T> side{w8a8v3::uniform_ptr(reinterpret_cast<const uint8_t *>(scales_t + m0)),
+                          static_cast<uint64_t>(cap) * 4, w8a8v3::lds_offset_of(reinterpret_cast<uint8_t *>(win))};
+  f32x4 acc[T::kFM][T::kFN];
+  w8a8v3::mainloop<T, DenseBlockFold<T>, false, ScaleSide<T>>(plan, KT, smem, acc, fold, T::kFM, side);
+
+  const int r = lane & 15;
+#pragma unroll
+  for (int i = 0; i < T::kFM; ++i) {
+#pragma unroll
+    for (int rr = 0; rr < 4; ++rr) {
+      const int m = m0 + w8a8v3::acc_row<T>(wm, i, lane, rr);
+      if (m >= M) continue;
+      uint16_t *yrow = y + static_cast<uint64_t>(m) * ld;
+      auto put = [&](int col, float v) {
+        const uint16_t bits = static_cast<uint16_t>(f32_to_bf16(v));
+        if constexpr (THROUGH) {
+          __hip_atomic_store(yrow + col, bits, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        } else {
+          yrow[col] = bits;
+        }
+      };
+      if (MODE == 2) {
+#pragma unroll
+        for (int j = 0; j < T::kFN / 2; ++j) put(ocol[j] + r, silu_mul(acc[i][j][rr], acc[i][j + T::kFN / 2][rr]));
+      } else {
+#pragma unroll
+        for (int j = 0; j < T::kFN; ++j) put(ocol[j] + r, acc[i][j][rr]);
+      }
+    }
+  }
+  return by;
+}
+
+// ---------------------------------------------------------------------------
 // W8A8 GEMM on the half-step main loop (w8a8_v4.h, 32 x 32 x 64 MFMA): BM x BN
 // block of WGM x WGN waves, NS LDS stages, 1-D grid in the XCD-aware tile
 // order. Operands and epilogues as w8a8_tiled_kernel. Block-local weight tile s
@@ -986,6 +1207,140 @@ LF_DEVICE void w8a8_one_launch(const int32_t *counts, const uint16_t *x, const u
 }
 
 // ---------------------------------------------------------------------------
+// Block-scaled W8A8 operations as one launch each (_b128 entries): the grid
+// is kQuantBlocks per-group quantizer blocks followed by the GEMM's
+// 128 x 128 tiles (4 waves), each tile starting once every chunk of its row
+// band is quantized, as in w8a8_one_launch. Workspace: the sync area (one
+// step of bands counters), codes [cap, K] (cap = bands x 128), then the
+// group scales k-tile-major, [K / 128][cap] fp32 (B128Rows).
+// ---------------------------------------------------------------------------
+using B128Tile = w8a8v3::Tile<128, 128, 2, 2, 2>;
+constexpr int kB128BM = 128;
+
+struct B128Rows {
+  uint8_t *codes;
+  float *scales_t;
+  uint64_t bytes;
+};
+LF_DEVICE B128Rows b128_rows(uint8_t *at, int cap, int K) {
+  const uint64_t codes = align256(static_cast<uint64_t>(cap) * K);
+  const uint64_t scales = align256(static_cast<uint64_t>(K >> 7) * cap * 4);
+  return B128Rows{at, reinterpret_cast<float *>(at + codes), codes + scales};
+}
+
+// Quantizer step: block b (of kQuantBlocks) quantizes chunks b, b +
+// kQuantBlocks, ... of kChunkRows rows (its 4 waves splitting each chunk's
+// groups) and counts each into its band's counter of step `step`.
+LF_DEVICE void b128_quantize(const uint16_t *x, int K, int M, const B128Rows &rows, int cap, int b,
+                             const phase::Sync &sync, int step) {
+  const int chunks = (M + kChunkRows - 1) / kChunkRows;
+  const int wave = static_cast<int>(threadIdx.x) >> 6, nw = static_cast<int>(blockDim.x) >> 6;
+  for (int c = b; c < chunks; c += kQuantBlocks) {
+    const int row0 = c * kChunkRows;
+    const int n = M - row0 < kChunkRows ? M - row0 : kChunkRows;
+    quantize_group_rows<true>(x, K, row0, n, rows.codes, rows.scales_t, cap, wave, nw);
+    phase::signal(sync.band(step, row0 / kB128BM));
+  }
+}
+
+template <int MODE>
+LF_DEVICE void w8a8_b128_one_launch(const int32_t *counts, const uint16_t *x, const uint8_t *w0,
+                                    const uint8_t *w1, const uint8_t *w2, uint16_t *y, uint8_t *ws) {
+  using T = B128Tile;
+  __shared__ __attribute__((aligned(1024))) uint8_t smem[T::kSmem];
+  __shared__ __attribute__((aligned(16))) float win[T::kStages * kB128BM];
+  __shared__ phase::Flag flag;
+  if (!dense_regions_ok<MODE, kScaleBlock128>(w0, w1, w2)) return;
+  const int K = static_cast<int>(header_of(w0).columns);
+  const int gx = dense_gx<MODE, 128>(dense_ld<MODE>(w0, w1, w2));
+  const int blocks = static_cast<int>(gridDim.x) - kQuantBlocks;
+  if (gx <= 0 || blocks <= 0 || blocks % gx != 0 || blockDim.x != T::kThreads) return;
+  const int bands = blocks / gx;
+  const phase::Sync sync{reinterpret_cast<int *>(ws), bands};
+  const int cap = bands * kB128BM;
+  const B128Rows rows = b128_rows(ws + phase::sync_bytes(1, bands), cap, K);
+  const int M = live_rows(counts, cap);
+  const int b = static_cast<int>(blockIdx.x);
+  if (b < kQuantBlocks) {
+    b128_quantize(x, K, M, rows, cap, b, sync, 0);
+    return;
+  }
+  const auto gate = [&](int m0) {
+    const int band = m0 / kB128BM;
+    return phase::wait_for(sync, sync.band(0, band), chunks_in_band(M, band, kB128BM), flag);
+  };
+  w8a8_b128_gemm<T, 4, MODE>(smem, win, M, rows.codes, rows.scales_t, cap, w0, w1, w2, y, b - kQuantBlocks,
+                             gate);
+  phase::finish(sync, blocks, 1, flag);
+}
+
+// The block-scaled GatedMlp in one launch: x -> group quantizer -> gate/up
+// + SwiGLU -> h (bf16) -> group quantizer -> down, four counted steps as in
+// w8a8_gated_mlp (both GEMMs on 128 x 128 tiles). Workspace: sync area
+// (three steps of bands counters), B128Rows of x (K = H), h [cap, I] bf16,
+// B128Rows of h (K = I).
+LF_DEVICE void w8a8_b128_gated_mlp(const int32_t *counts, const uint16_t *x, const uint8_t *wg,
+                                   const uint8_t *wu, const uint8_t *wd, uint16_t *y, uint8_t *ws) {
+  using T = B128Tile;
+  constexpr int BM = kB128BM;
+  __shared__ __attribute__((aligned(1024))) uint8_t smem[T::kSmem];
+  __shared__ __attribute__((aligned(16))) float win[T::kStages * BM];
+  __shared__ phase::Flag flag;
+  if (!dense_regions_ok<2, kScaleBlock128>(wg, wu, wu) || !dense_regions_ok<0, kScaleBlock128>(wd, wd, wd)) {
+    return;
+  }
+  const int H = static_cast<int>(header_of(wg).columns), I = static_cast<int>(header_of(wg).rows);
+  if (static_cast<int>(header_of(wd).columns) != I || static_cast<int>(header_of(wd).rows) != H) return;
+  const int gx1 = dense_gx<2, 128>(I), gx2 = dense_gx<0, 128>(H);
+  const int blocks = static_cast<int>(gridDim.x) - 2 * kQuantBlocks;
+  if (gx1 <= 0 || gx2 <= 0 || blocks <= 0 || blocks % (gx1 + gx2) != 0 || blockDim.x != T::kThreads) return;
+  const int bands = blocks / (gx1 + gx2);
+  const phase::Sync sync{reinterpret_cast<int *>(ws), bands};
+  const int cap = bands * BM;
+  const B128Rows xr = b128_rows(ws + phase::sync_bytes(3, bands), cap, H);
+  uint16_t *h = reinterpret_cast<uint16_t *>(xr.codes + xr.bytes);
+  const B128Rows hr = b128_rows(reinterpret_cast<uint8_t *>(h) + align256(static_cast<uint64_t>(cap) * I * 2),
+                                cap, I);
+  const int M = live_rows(counts, cap);
+  int b = static_cast<int>(blockIdx.x);
+  if (b < kQuantBlocks) {  // step 0: x -> codes and group scales
+    b128_quantize(x, H, M, xr, cap, b, sync, 0);
+    return;
+  }
+  b -= kQuantBlocks;
+  if (b < gx1 * bands) {  // step 1: gate/up + SwiGLU -> h
+    const auto gate = [&](int m0) {
+      const int band = m0 / BM;
+      return phase::wait_for(sync, sync.band(0, band), chunks_in_band(M, band, BM), flag);
+    };
+    const int band = w8a8_b128_gemm<T, 4, 2, true>(smem, win, M, xr.codes, xr.scales_t, cap, wg, wu, wu, h, b,
+                                                   gate);
+    if (band >= 0) phase::signal(sync.band(1, band));
+    return;
+  }
+  b -= gx1 * bands;
+  if (b < kQuantBlocks) {  // step 2: h -> codes and group scales
+    const int chunks = (M + kChunkRows - 1) / kChunkRows;
+    const int wave = static_cast<int>(threadIdx.x) >> 6;
+    for (int c = b; c < chunks; c += kQuantBlocks) {
+      const int row0 = c * kChunkRows, band = row0 / BM;
+      if (!phase::wait_for(sync, sync.band(1, band), gx1, flag)) return;
+      const int n = M - row0 < kChunkRows ? M - row0 : kChunkRows;
+      quantize_group_rows<true>(h, I, row0, n, hr.codes, hr.scales_t, cap, wave, T::kWaves);
+      phase::signal(sync.band(2, band));
+    }
+    return;
+  }
+  b -= kQuantBlocks;
+  const auto gate = [&](int m0) {  // step 3: down
+    const int band = m0 / BM;
+    return phase::wait_for(sync, sync.band(2, band), chunks_in_band(M, band, BM), flag);
+  };
+  w8a8_b128_gemm<T, 4, 0>(smem, win, M, hr.codes, hr.scales_t, cap, wd, wd, wd, y, b, gate);
+  phase::finish(sync, gx2 * bands, 3, flag);
+}
+
+// ---------------------------------------------------------------------------
 // W8A8 GatedMlp in one launch (model/plan/plan.mbt:47-59;
 // kernels/reference/mlp.mbt:4-39): x -> xq (per token) -> gate/up + SwiGLU ->
 // h (bf16) -> hq (per token) -> down -> y, the same arithmetic as the
@@ -1120,6 +1475,29 @@ LF_W8A8_ENTRIES(t128, GemmT128)
 LF_W8A8_GATED_MLP(t256_t256, GemmT256, GemmT256)
 LF_W8A8_GATED_MLP(t256_t256x128, GemmT256, GemmT256x128)
 LF_W8A8_GATED_MLP(t128_t128, GemmT128, GemmT128)
+
+// Block-scaled (128 x 128 weight blocks, 128-column activation groups) W8A8
+// operations, one launch each: (counts, x, w..., y, ws).
+__global__ __launch_bounds__(256) void lf_fp8_w8a8_dense_b128(const int32_t *counts, const uint16_t *x,
+                                                              const uint8_t *w, uint16_t *y, uint8_t *ws) {
+  w8a8_b128_one_launch<0>(counts, x, w, w, w, y, ws);
+}
+__global__ __launch_bounds__(256) void lf_fp8_w8a8_qkv_b128(const int32_t *counts, const uint16_t *x,
+                                                            const uint8_t *wq, const uint8_t *wk,
+                                                            const uint8_t *wv, uint16_t *y, uint8_t *ws) {
+  w8a8_b128_one_launch<1>(counts, x, wq, wk, wv, y, ws);
+}
+__global__ __launch_bounds__(256) void lf_fp8_w8a8_gate_up_b128(const int32_t *counts, const uint16_t *x,
+                                                                const uint8_t *wg, const uint8_t *wu,
+                                                                uint16_t *h, uint8_t *ws) {
+  w8a8_b128_one_launch<2>(counts, x, wg, wu, wu, h, ws);
+}
+__global__ __launch_bounds__(256) void lf_fp8_w8a8_gated_mlp_b128(const int32_t *counts, const uint16_t *x,
+                                                                  const uint8_t *wg, const uint8_t *wu,
+                                                                  const uint8_t *wd, uint16_t *y,
+                                                                  uint8_t *ws) {
+  w8a8_b128_gated_mlp(counts, x, wg, wu, wd, y, ws);
+}
 
 __global__ __launch_bounds__(256) void lf_fp8_act_quant_rows(const int32_t *counts,
                                                              const uint16_t *x,

@@ -225,10 +225,22 @@ LF_DEVICE void group_epilogue(const f32x4 (&acc)[MT][NW], const float (&sc)[NW],
     }
 }
 
+// Block-scaled weights (BLOCK): k-tiles of one slice whose 128 x 128 block
+// scales a block keeps in LDS (the geometry splits K so that a slice has at
+// most this many).
+constexpr int kW16BlockSliceKT = 128;
+
 // MODE 0: dense, 1: qkv (three weights, packed Q|K|V output), 2: gate/up.
 // D: weight k-tiles in flight per wave; XC: k-tiles per activation chunk
 // (D a multiple of XC).
-template <int WAVES, int MT, int MODE, int D, int XC>
+// BLOCK: the weights carry 128 x 128 block scales (s[N/128][K/128]) instead
+// of channel scales. A wave's 16 columns lie in one 128-row block, so each
+// k-tile has one scale per weight: the k-tile's four MFMAs accumulate into
+// a fresh fragment, which is then multiplied by that scale and added to the
+// running sum (y = sum_kt s[nb][kt] sum_{k in kt} x_k q_k, fp32); the
+// epilogue applies no channel scale. The slice's scales are staged in LDS
+// before the main loop.
+template <int WAVES, int MT, int MODE, int D, int XC, bool BLOCK = false>
 __device__ void w8a16_kernel(const int32_t *counts, const uint16_t *x, const uint8_t *w0,
                              const uint8_t *w1, const uint8_t *w2, uint16_t *y, uint8_t *ws) {
   constexpr int NW = MODE == 2 ? 2 : 1;
@@ -236,9 +248,10 @@ __device__ void w8a16_kernel(const int32_t *counts, const uint16_t *x, const uin
   using X = XRing<MT, XC>;
   __shared__ __attribute__((aligned(1024))) uint8_t ring[X::kBytes];
   __shared__ int last_block;
+  __shared__ float bscale[BLOCK ? WAVES * NW * kW16BlockSliceKT : 1];
 
   const WeightHeader &h0 = header_of(w0);
-  if (!dense_regions_ok<MODE>(w0, w1, w2)) return;
+  if (!dense_regions_ok<MODE, BLOCK ? kScaleBlock128 : kScalePerChannel>(w0, w1, w2)) return;
   const int K = static_cast<int>(h0.columns);
   const int KT = K >> 7;
   const int tq = static_cast<int>(h0.rows) >> 4;
@@ -253,7 +266,7 @@ __device__ void w8a16_kernel(const int32_t *counts, const uint16_t *x, const uin
   const int s = static_cast<int>(blockIdx.x) - cg * S;
   const int kt0 = (KT * s) / S, kt1 = (KT * (s + 1)) / S;
   const int nkt = kt1 - kt0;
-  if (cg >= groups || nkt < 1) return;
+  if (cg >= groups || nkt < 1 || (BLOCK && nkt > kW16BlockSliceKT)) return;
   const int M = live_rows(counts, X::kRows);
   if (M == 0) return;
 
@@ -281,10 +294,20 @@ __device__ void w8a16_kernel(const int32_t *counts, const uint16_t *x, const uin
   }
 
   // 0. Channel scales of this lane's column (first: waits for the activation
-  //    loads below never wait for them).
+  //    loads below never wait for them). Block scales: the epilogue's
+  //    multiplier is 1 and the slice's k-tile scales of this wave's block
+  //    (t / 8) go to LDS.
   float sc[NW];
 #pragma unroll
-  for (int i = 0; i < NW; ++i) sc[i] = expert_scales(region[i], 0)[t * 16 + r];
+  for (int i = 0; i < NW; ++i) {
+    if constexpr (BLOCK) {
+      sc[i] = 1.0f;
+      const float *bs = expert_scales(region[i], 0) + static_cast<uint64_t>(t >> 3) * KT + kt0;
+      for (int kl = lane; kl < nkt; kl += 64) bscale[(wave * NW + i) * kW16BlockSliceKT + kl] = bs[kl];
+    } else {
+      sc[i] = expert_scales(region[i], 0)[t * 16 + r];
+    }
+  }
 
   // Activation chunk c (k-tiles c XC .. c XC + XC - 1 of the slice) goes straight
   // into ring buffer c & 1 with global_load_lds: 1 KiB = 4 rows of one k-tile
@@ -351,6 +374,8 @@ __device__ void w8a16_kernel(const int32_t *counts, const uint16_t *x, const uin
         if (c + 1 < chunks) load_chunk(c + 1);
       }
       const uint8_t *buf = ring + ((kl / XC) & 1) * X::kBufferBytes + (d % XC) * X::kKTileBytes;
+      // BLOCK: this k-tile's products, scaled into acc after its 4 MFMAs
+      f32x4 part[BLOCK ? MT : 1][NW];
 #pragma unroll
       for (int j = 0; j < 4; ++j) {
         Frag16 a[MT];
@@ -365,7 +390,30 @@ __device__ void w8a16_kernel(const int32_t *counts, const uint16_t *x, const uin
           const bf16x8 bf = weight_fragment(b[d][i], j);
 #pragma unroll
           for (int mt = 0; mt < MT; ++mt) {
-            acc[mt][i] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a[mt].v, bf, acc[mt][i], 0, 0, 0);
+            if constexpr (BLOCK) {
+              part[mt][i] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
+                  a[mt].v, bf, j == 0 ? f32x4{0.f, 0.f, 0.f, 0.f} : part[mt][i], 0, 0, 0);
+            } else {
+              acc[mt][i] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a[mt].v, bf, acc[mt][i], 0, 0, 0);
+            }
+          }
+        }
+      }
+      if constexpr (BLOCK) {
+#pragma unroll
+        for (int i = 0; i < NW; ++i) {
+          const float sb = bscale[(wave * NW + i) * kW16BlockSliceKT + kl];
+#pragma unroll
+          for (int mt = 0; mt < MT; ++mt) {
+            acc[mt][i] += part[mt][i] * sb;
+            // Keeps these reads of the MFMA results in the MFMAs' basic
+            // block: sunk past the conditional refill below (as the compiler
+            // otherwise does), the first read at the join was issued one
+            // instruction after the last MFMA on the path that skips the
+            // refill, with none of the wait states an MFMA result needs
+            // before a VALU reads it (measured: element 3 of each fragment
+            // varied from launch to launch at 16 rows).
+            asm volatile("" : "+v"(acc[mt][i]));
           }
         }
       }
@@ -1008,6 +1056,28 @@ LF_W8A16_ENTRIES(1, 16, 4, 4)
 LF_W8A16_ENTRIES(2, 32, 4, 4)
 LF_W8A16_ENTRIES(4, 64, 4, 4)
 LF_W8A16_ENTRIES(8, 128, 2, 2)
+
+// The same column-group forms over weights with 128 x 128 block scales.
+#define LF_W8A16_B128_ENTRIES(MT, M, D, XC)                                                     \
+  __global__ __launch_bounds__(LF_W16_WAVES * 64) void lf_fp8_w8a16_dense_b128_m##M(         \
+      const int32_t *counts, const uint16_t *x, const uint8_t *w, uint16_t *y, uint8_t *ws) { \
+    w8a16_kernel<LF_W16_WAVES, MT, 0, D, XC, true>(counts, x, w, w, w, y, ws);               \
+  }                                                                                          \
+  __global__ __launch_bounds__(LF_W16_WAVES * 64) void lf_fp8_w8a16_qkv_b128_m##M(           \
+      const int32_t *counts, const uint16_t *x, const uint8_t *wq, const uint8_t *wk,        \
+      const uint8_t *wv, uint16_t *y, uint8_t *ws) {                                         \
+    w8a16_kernel<LF_W16_WAVES, MT, 1, D, XC, true>(counts, x, wq, wk, wv, y, ws);            \
+  }                                                                                          \
+  __global__ __launch_bounds__(LF_W16_WAVES * 64) void lf_fp8_w8a16_gate_up_b128_m##M(       \
+      const int32_t *counts, const uint16_t *x, const uint8_t *wg, const uint8_t *wu,        \
+      uint16_t *h, uint8_t *ws) {                                                            \
+    w8a16_kernel<LF_W16_WAVES, MT, 2, D, XC, true>(counts, x, wg, wu, wu, h, ws);            \
+  }
+
+LF_W8A16_B128_ENTRIES(1, 16, 4, 4)
+LF_W8A16_B128_ENTRIES(2, 32, 4, 4)
+LF_W8A16_B128_ENTRIES(4, 64, 4, 4)
+LF_W8A16_B128_ENTRIES(8, 128, 2, 2)
 
 #ifndef LF_W16T_WAVES
 #define LF_W16T_WAVES 8

@@ -132,16 +132,26 @@ struct NoFold {
   LF_DEVICE void operator()(int, const A &, A &, int) const {}
 };
 
+// Side loads: Side::kIns more LDS-direct loads per wave and k-step, issued
+// right after the stage's own loads (side.issue(kt, slot), slot = kt % NS)
+// and waited for with them, so what they bring is in LDS when fold(kt)
+// runs and stays there until the k-step's slot is reused NS steps later.
+// NoSide: none.
+struct NoSide {
+  static constexpr int kIns = 0;
+  LF_DEVICE void issue(int, int) const {}
+};
+
 // SKIP: live_fm is how many of this wave's kFM 16-row fragments hold a live
 // row (wave-uniform); a wave with none skips its A reads, MFMAs and folds
 // (its accumulators are never stored). Skipping single fragments cost the
 // block-scaled kernel an occupancy step in registers, so the skip is per
 // wave. Only the grouped GEMMs, whose expert tiles are often partly past the
 // expert's last row, use it.
-template <class T, class Fold = NoFold, bool SKIP = false>
+template <class T, class Fold = NoFold, bool SKIP = false, class Side = NoSide>
 __device__ __forceinline__ void mainloop(const Plan<T> &plan, int KT, uint8_t *smem,
                          f32x4 (&acc)[T::kFM][T::kFN], const Fold &fold = Fold{},
-                         int live_fm = T::kFM) {
+                         int live_fm = T::kFM, const Side &side = Side{}) {
   const int live = __builtin_amdgcn_readfirstlane(live_fm);
   constexpr int NS = T::kStages;
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
@@ -160,6 +170,7 @@ __device__ __forceinline__ void mainloop(const Plan<T> &plan, int KT, uint8_t *s
     for (int q = 0; q < T::kBIns; ++q) {
       dma16(plan.b[q] + kt * kTileBytes, b + b_load_half<T>(wave, q) * 1024);
     }
+    side.issue(kt, kt % NS);
   };
 
 #pragma unroll
@@ -176,7 +187,7 @@ __device__ __forceinline__ void mainloop(const Plan<T> &plan, int KT, uint8_t *s
     // stages are outstanding (completions are counted in issue order).
     const int later = KT - 1 - kt < NS - 2 ? KT - 1 - kt : NS - 2;
     if (later >= NS - 2) {
-      wait_vmcnt<(NS - 2) * T::kIns>();
+      wait_vmcnt<(NS - 2) * (T::kIns + Side::kIns)>();
     } else {
       wait_vmcnt<0>();
     }

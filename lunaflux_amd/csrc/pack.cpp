@@ -92,6 +92,26 @@ bool w8a16_split(int64_t n, int64_t k, int32_t max_tokens, W8a16Split *out) {
   return true;
 }
 
+// Block-scaled W8A16 entries (_B128): the column-group form for every
+// profile (also <= 16 rows), split as above, with at least enough slices
+// that each holds <= 128 k-tiles (the block scales of a slice are staged in
+// LDS, kW16BlockSliceKT in kernels/w8a16.hip).
+bool w8a16_b128_entry(int32_t e) {
+  return e == LF_FP8_ENTRY_W8A16_DENSE_B128 || e == LF_FP8_ENTRY_W8A16_QKV_B128 ||
+         e == LF_FP8_ENTRY_W8A16_GATE_UP_B128;
+}
+bool w8a16_b128_split(int64_t n, int64_t k, int32_t max_tokens, W8a16Split *out) {
+  if (n % 128 != 0 || k % 128 != 0 || !w8a16_split(n, k, max_tokens, out)) return false;
+  const int64_t kt = k / 128, tiles = n / 16;
+  if (out->one_tile) {
+    out->one_tile = false;
+    out->groups = (tiles + kW16Waves - 1) / kW16Waves;
+    out->split = std::min<int64_t>(kt, std::max<int64_t>(1, (512 + out->groups / 2) / out->groups));
+  }
+  out->split = std::max<int64_t>(out->split, (kt + 127) / 128);
+  return out->groups * out->split <= INT32_MAX;
+}
+
 // Shape-specialized W8A16 entries (w8a16.hip, "LF_W16_FIXED_*"): compiled for
 // one input width K (and, for QKV, one Q / K-V split), as AOT entry points
 // are compiled for one model shape. Two forms: one-tile (a block of `waves`
@@ -292,6 +312,24 @@ int64_t quantized_rows_bytes(int64_t rows, int64_t k) {
   return align_up(rows * k, 256) + align_up(rows * 4, 256);
 }
 
+// Block-scaled W8A8 entries (kernels/projection.hip, _b128): 128 x 128 tiles
+// of 4 waves after kQuantBlocks group-quantizer blocks; the quantized rows
+// hold codes [cap, K] then the group scales k-tile-major [K / 128][cap].
+bool w8a8_b128_entry(int32_t e) {
+  return e == LF_FP8_ENTRY_W8A8_DENSE_B128 || e == LF_FP8_ENTRY_W8A8_QKV_B128 ||
+         e == LF_FP8_ENTRY_W8A8_GATE_UP_B128;
+}
+int64_t b128_rows_bytes(int64_t cap, int64_t k) {
+  return align_up(cap * k, 256) + align_up((k / 128) * cap * 4, 256);
+}
+// Row bands of 128 for the profile; false if the shape has no form (widths
+// not multiples of 128, or group-scale indices past int32).
+bool w8a8_b128_bands(int64_t n, int64_t k, int32_t max_tokens, int64_t *bands) {
+  if (n <= 0 || k <= 0 || n % 128 != 0 || k % 128 != 0 || max_tokens <= 0) return false;
+  *bands = (max_tokens + 127) / 128;
+  return (k / 128) * (*bands * 128) < INT32_MAX;
+}
+
 // W8A8 GatedMlp in one launch: both GEMMs on 4-wave blocks of one band
 // height. Gate/up on 256 x 256 tiles where its own launch would take 256-row
 // tiles (down then on 256 x 256, or 256 x 128 where its own launch would
@@ -450,9 +488,11 @@ int32_t lunaflux_fp8_admit_weight(int32_t entry, const uint8_t *region_head, int
                      entry == LF_FP8_ENTRY_W8A16_GATED_MLP || entry == LF_FP8_ENTRY_W8A8_DENSE_AQ ||
                      entry == LF_FP8_ENTRY_W8A8_QKV_AQ || entry == LF_FP8_ENTRY_W8A8_GATE_UP_AQ ||
                      entry == LF_FP8_ENTRY_W8A8_GATED_MLP;
+  const bool block = w8a16_b128_entry(entry) || w8a8_b128_entry(entry) ||
+                     entry == LF_FP8_ENTRY_W8A8_GATED_MLP_B128;
   const bool grouped = entry == LF_FP8_ENTRY_GROUPED;
-  if ((!dense && !grouped) || region_head == nullptr || head_bytes < LF_FP8_HEADER_BYTES ||
-      (dense && experts != 1)) {
+  if ((!dense && !block && !grouped) || region_head == nullptr || head_bytes < LF_FP8_HEADER_BYTES ||
+      ((dense || block) && experts != 1)) {
     return LF_INVALID_ARGUMENT;
   }
   lf_fp8_weight_header h;
@@ -479,6 +519,7 @@ int32_t lunaflux_fp8_admit_weight(int32_t entry, const uint8_t *region_head, int
     return LF_INVALID_ARGUMENT;
   }
   if (dense && mode != LF_FP8_SCALE_PER_CHANNEL) return LF_UNSUPPORTED;
+  if (block && mode != LF_FP8_SCALE_BLOCK128) return LF_UNSUPPORTED;
   return LF_OK;
 }
 
@@ -489,6 +530,16 @@ int64_t lunaflux_fp8_act_quant_bytes(int64_t max_rows, int64_t columns) {
 
 static int64_t w8a16_workspace(int32_t entry, int64_t n, int64_t k, int64_t nq, int64_t nkv,
                                int32_t max_tokens) {
+  if (w8a16_b128_entry(entry)) {
+    W8a16Split sp;
+    if (n <= 0 || k <= 0 || max_tokens <= 0 || n > kMaxDim || k > kMaxDim ||
+        !w8a16_b128_split(n, k, max_tokens, &sp)) {
+      return -1;
+    }
+    if (sp.split == 1) return 256;
+    const int64_t nw = entry == LF_FP8_ENTRY_W8A16_GATE_UP_B128 ? 2 : 1;
+    return align_up(sp.split * (n / 16) * nw * sp.mt * 1024, 256) + align_up(sp.groups * 4, 256);
+  }
   if (entry != LF_FP8_ENTRY_W8A16_DENSE && entry != LF_FP8_ENTRY_W8A16_QKV &&
       entry != LF_FP8_ENTRY_W8A16_GATE_UP) {
     return -1;
@@ -517,6 +568,16 @@ int64_t lunaflux_fp8_w8a16_workspace_bytes(int32_t entry, int64_t n, int64_t k,
 
 int64_t lunaflux_fp8_gated_mlp_workspace_bytes(int32_t entry, int64_t hidden, int64_t inter,
                                                int32_t max_tokens) {
+  if (entry == LF_FP8_ENTRY_W8A8_GATED_MLP_B128) {
+    int64_t bands = 0;
+    if (hidden > kMaxDim || inter > kMaxDim || !w8a8_b128_bands(hidden, inter, max_tokens, &bands) ||
+        !w8a8_b128_bands(inter, hidden, max_tokens, &bands)) {
+      return -1;
+    }
+    const int64_t cap = bands * 128;
+    return sync_bytes(3, bands) + b128_rows_bytes(cap, hidden) + align_up(cap * inter * 2, 256) +
+           b128_rows_bytes(cap, inter);
+  }
   if (entry == LF_FP8_ENTRY_W8A8_GATED_MLP) {
     W8a8Gated g;
     if (hidden <= 0 || inter <= 0 || max_tokens <= 0 || hidden > kMaxDim || inter > kMaxDim ||
@@ -535,6 +596,11 @@ int64_t lunaflux_fp8_gated_mlp_workspace_bytes(int32_t entry, int64_t hidden, in
 }
 
 int64_t lunaflux_fp8_w8a8_workspace_bytes(int32_t entry, int64_t n, int64_t k, int32_t max_tokens) {
+  if (w8a8_b128_entry(entry)) {
+    int64_t bands = 0;
+    if (n > kMaxDim || k > kMaxDim || !w8a8_b128_bands(n, k, max_tokens, &bands)) return -1;
+    return sync_bytes(1, bands) + b128_rows_bytes(bands * 128, k);
+  }
   if ((entry != LF_FP8_ENTRY_W8A8_DENSE_AQ && entry != LF_FP8_ENTRY_W8A8_QKV_AQ &&
        entry != LF_FP8_ENTRY_W8A8_GATE_UP_AQ) ||
       n <= 0 || k <= 0 || k % 128 != 0 || max_tokens <= 0 || n > kMaxDim || k > kMaxDim) {
@@ -550,6 +616,21 @@ int32_t lunaflux_fp8_gated_mlp_geometry(int32_t entry, int64_t hidden, int64_t i
                                         char symbol[LF_FP8_SYMBOL_BYTES]) {
   if (dims == nullptr || symbol == nullptr || hidden <= 0 || inter <= 0 || max_tokens <= 0) {
     return LF_INVALID_ARGUMENT;
+  }
+  if (entry == LF_FP8_ENTRY_W8A8_GATED_MLP_B128) {
+    int64_t bands = 0;
+    if (hidden > kMaxDim || inter > kMaxDim || !w8a8_b128_bands(hidden, inter, max_tokens, &bands) ||
+        !w8a8_b128_bands(inter, hidden, max_tokens, &bands)) {
+      return LF_INVALID_ARGUMENT;
+    }
+    // x quantizer, gate/up tiles (64 h-columns each), h quantizer, down tiles
+    const int64_t blocks = 2 * kQuantBlocks + (inter / 64 + hidden / 128) * bands;
+    if (blocks > INT32_MAX) return LF_INVALID_ARGUMENT;
+    const int32_t values[7] = {static_cast<int32_t>(blocks), 1, 1, 256, 1, 1, 0};
+    std::memcpy(dims, values, sizeof(values));
+    std::memset(symbol, 0, LF_FP8_SYMBOL_BYTES);
+    std::snprintf(symbol, LF_FP8_SYMBOL_BYTES, "lf_fp8_w8a8_gated_mlp_b128");
+    return LF_OK;
   }
   if (entry == LF_FP8_ENTRY_W8A8_GATED_MLP) {
     W8a8Gated g;
@@ -662,6 +743,35 @@ static int32_t launch_geometry(int32_t entry, int64_t n, int64_t k, int64_t nq, 
       bx = 64 * (sp.one_tile ? kW16TileWaves : kW16Waves);
       break;
     }
+    case LF_FP8_ENTRY_W8A16_DENSE_B128:
+    case LF_FP8_ENTRY_W8A16_QKV_B128:
+    case LF_FP8_ENTRY_W8A16_GATE_UP_B128: {
+      W8a16Split sp;
+      if (!w8a16_b128_split(n, k, max_tokens, &sp)) return LF_INVALID_ARGUMENT;
+      const char *op = entry == LF_FP8_ENTRY_W8A16_DENSE_B128 ? "dense"
+                       : entry == LF_FP8_ENTRY_W8A16_QKV_B128 ? "qkv"
+                                                              : "gate_up";
+      std::snprintf(buffer, sizeof(buffer), "lf_fp8_w8a16_%s_b128_m%d", op, 16 * sp.mt);
+      name = buffer;
+      gx = static_cast<int32_t>(sp.groups * sp.split);
+      bx = 64 * kW16Waves;
+      break;
+    }
+    case LF_FP8_ENTRY_W8A8_DENSE_B128:
+    case LF_FP8_ENTRY_W8A8_QKV_B128:
+    case LF_FP8_ENTRY_W8A8_GATE_UP_B128: {
+      int64_t bands = 0;
+      if (!w8a8_b128_bands(n, k, max_tokens, &bands)) return LF_INVALID_ARGUMENT;
+      const bool gate_up = entry == LF_FP8_ENTRY_W8A8_GATE_UP_B128;
+      const int64_t blocks = kQuantBlocks + (gate_up ? n / 64 : n / 128) * bands;
+      if (blocks > INT32_MAX) return LF_INVALID_ARGUMENT;
+      std::snprintf(buffer, sizeof(buffer), "lf_fp8_w8a8_%s_b128",
+                    entry == LF_FP8_ENTRY_W8A8_QKV_B128 ? "qkv" : gate_up ? "gate_up" : "dense");
+      name = buffer;
+      gx = static_cast<int32_t>(blocks);
+      bx = 256;
+      break;
+    }
     case LF_FP8_ENTRY_W8A8_DENSE:
     case LF_FP8_ENTRY_W8A8_QKV:
     case LF_FP8_ENTRY_W8A8_GATE_UP:
@@ -710,8 +820,15 @@ int32_t lunaflux_fp8_qkv_launch_geometry(int32_t entry, int64_t nq, int64_t nkv,
                                          int32_t max_tokens, int32_t dims[7],
                                          char symbol[LF_FP8_SYMBOL_BYTES]) {
   if ((entry != LF_FP8_ENTRY_W8A16_QKV && entry != LF_FP8_ENTRY_W8A8_QKV &&
-       entry != LF_FP8_ENTRY_W8A8_QKV_AQ) || nq <= 0 ||
+       entry != LF_FP8_ENTRY_W8A8_QKV_AQ && entry != LF_FP8_ENTRY_W8A16_QKV_B128 &&
+       entry != LF_FP8_ENTRY_W8A8_QKV_B128) || nq <= 0 ||
       nkv <= 0 || nq > kMaxDim || nkv > kMaxDim) {
+    return LF_INVALID_ARGUMENT;
+  }
+  // block-scaled QKV: every region's 128-row blocks start on a 128-column
+  // boundary of the packed output
+  if ((entry == LF_FP8_ENTRY_W8A16_QKV_B128 || entry == LF_FP8_ENTRY_W8A8_QKV_B128) &&
+      (nq % 128 != 0 || nkv % 128 != 0)) {
     return LF_INVALID_ARGUMENT;
   }
   return launch_geometry(entry, nq + 2 * nkv, k, nq, nkv, max_tokens, dims, symbol);

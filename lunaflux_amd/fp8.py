@@ -33,6 +33,15 @@ from .device import (Allocation, DeviceError, Function, KernelArgument, KernelAr
                      KernelLaunchDimensions, Stream, open_context)
 
 FAMILIES = ("w8a16", "w8a8")
+# The entry of (family, operation) for weights with 128 x 128 block scales.
+_BLOCK_ENTRIES = {
+    ("w8a16", "dense"): _abi.ENTRY_W8A16_DENSE_B128,
+    ("w8a16", "qkv"): _abi.ENTRY_W8A16_QKV_B128,
+    ("w8a16", "gate_up"): _abi.ENTRY_W8A16_GATE_UP_B128,
+    ("w8a8", "dense"): _abi.ENTRY_W8A8_DENSE_B128,
+    ("w8a8", "qkv"): _abi.ENTRY_W8A8_QKV_B128,
+    ("w8a8", "gate_up"): _abi.ENTRY_W8A8_GATE_UP_B128,
+}
 PER_CHANNEL = _abi.LF_FP8_SCALE_PER_CHANNEL
 BLOCK128 = _abi.LF_FP8_SCALE_BLOCK128
 W8A16_MAX_TOKENS = 128
@@ -309,7 +318,10 @@ class ProjectionRuntime:
                qkv_split=None) -> BoundOperation:
         """A W8A16 launch with its split-K workspace (zero-filled once here;
         the kernels leave its arrival counters at zero after every launch)."""
-        nbytes = w8a16_workspace_bytes(entry, n, k, max_tokens, qkv_split)
+        # (the Q / K-V split selects a shape-specialized per-channel entry;
+        # the block-scaled QKV entry is sized by its packed width)
+        nbytes = w8a16_workspace_bytes(entry, n, k, max_tokens,
+                                       qkv_split if entry == _abi.ENTRY_W8A16_QKV else None)
         ws = self.context.allocate(nbytes)
         ws.copy_from_host(np.zeros(nbytes, np.uint8))
         step = self._step(entry, n, k, max_tokens, operands + [_region(ws, alignment=256)],
@@ -351,12 +363,31 @@ class ProjectionRuntime:
         return self._step(_abi.ENTRY_W8A8_DENSE, w.rows, w.columns, max_tokens,
                           [_region(counts, COUNTS_BYTES, alignment=4), xq, w.region, y])
 
+    def _block(self, family: str, op: str, counts: Allocation, weights, operands, n: int, k: int,
+               max_tokens: int, qkv_split=None) -> BoundOperation:
+        """A projection over weights with 128 x 128 block scales: the _B128
+        entry of the family (W8A16: the column-group form with its split-K
+        workspace; W8A8: one launch, the per-128-column-group quantizer
+        inside it)."""
+        entry = _BLOCK_ENTRIES[(family, op)]
+        for w in weights:
+            w.admit(entry)
+        c = _region(counts, COUNTS_BYTES, alignment=4)
+        if family == "w8a16":
+            return self._w8a16(entry, n, k, max_tokens, [c, *operands], qkv_split)
+        return self._w8a8_one_launch(entry, n, k, max_tokens, [c, *operands], qkv_split)
+
     def bind_dense(self, family: str, counts: Allocation, x: KernelArgument, w: Fp8Weight,
                    y: KernelArgument, max_tokens: int, one_launch: bool = True) -> BoundOperation:
         """OutputProjection / down / the vocabulary head. W8A8: one launch
         (the _aq entry quantizes x inside it); one_launch=False binds the
-        act-quant launch and the GEMM-only launch instead (same outputs)."""
+        act-quant launch and the GEMM-only launch instead (same outputs).
+        A weight with 128 x 128 block scales binds the family's _B128 entry
+        (one launch in both families, whatever one_launch says)."""
         _family(family, max_tokens)
+        if w.scale_mode == BLOCK128:
+            return self._block(family, "dense", counts, [w], [x, w.region, y], w.rows, w.columns,
+                               max_tokens)
         w.admit(_abi.ENTRY_W8A16_DENSE if family == "w8a16" else _abi.ENTRY_W8A8_DENSE)
         c = _region(counts, COUNTS_BYTES, alignment=4)
         if family == "w8a16":
@@ -377,11 +408,15 @@ class ProjectionRuntime:
                  wk: Fp8Weight, wv: Fp8Weight, y: KernelArgument, max_tokens: int,
                  one_launch: bool = True) -> BoundOperation:
         _family(family, max_tokens)
-        for w in (wq, wk, wv):
-            w.admit(_abi.ENTRY_W8A16_QKV if family == "w8a16" else _abi.ENTRY_W8A8_QKV)
         if not (wq.columns == wk.columns == wv.columns) or wk.rows != wv.rows:
             raise DeviceError("qkv shapes", _abi.LF_INVALID_ARGUMENT)
         n = wq.rows + wk.rows + wv.rows
+        if wq.scale_mode == BLOCK128 or wk.scale_mode == BLOCK128 or wv.scale_mode == BLOCK128:
+            return self._block(family, "qkv", counts, [wq, wk, wv],
+                               [x, wq.region, wk.region, wv.region, y], n, wq.columns, max_tokens,
+                               qkv_split=(wq.rows, wk.rows))
+        for w in (wq, wk, wv):
+            w.admit(_abi.ENTRY_W8A16_QKV if family == "w8a16" else _abi.ENTRY_W8A8_QKV)
         c = _region(counts, COUNTS_BYTES, alignment=4)
         if family == "w8a16":
             return self._w8a16(_abi.ENTRY_W8A16_QKV, n, wq.columns, max_tokens,
@@ -403,10 +438,13 @@ class ProjectionRuntime:
                      wu: Fp8Weight, h: KernelArgument, max_tokens: int,
                      one_launch: bool = True) -> BoundOperation:
         _family(family, max_tokens)
-        for w in (wg, wu):
-            w.admit(_abi.ENTRY_W8A16_GATE_UP if family == "w8a16" else _abi.ENTRY_W8A8_GATE_UP)
         if wg.rows != wu.rows or wg.columns != wu.columns:
             raise DeviceError("gate/up shapes", _abi.LF_INVALID_ARGUMENT)
+        if wg.scale_mode == BLOCK128 or wu.scale_mode == BLOCK128:
+            return self._block(family, "gate_up", counts, [wg, wu], [x, wg.region, wu.region, h],
+                               wg.rows, wg.columns, max_tokens)
+        for w in (wg, wu):
+            w.admit(_abi.ENTRY_W8A16_GATE_UP if family == "w8a16" else _abi.ENTRY_W8A8_GATE_UP)
         c = _region(counts, COUNTS_BYTES, alignment=4)
         if family == "w8a16":
             return self._w8a16(_abi.ENTRY_W8A16_GATE_UP, wg.rows, wg.columns, max_tokens,
@@ -433,14 +471,23 @@ class ProjectionRuntime:
         two launch steps: gate/up + SwiGLU into a bf16 intermediate, then the
         down projection from it (each W8A8 step then quantizes its input
         inside its own launch, or, with one_launch=False, in a launch of its
-        own). Every form computes the same values."""
+        own). Every form computes the same values. Weights with 128 x 128
+        block scales: W8A8 as one launch (the _B128 GatedMlp entry), W8A16
+        (and W8A8 with one_launch=False) as the two block-scaled launches."""
         if wd.columns != wg.rows or wd.rows != wg.columns:
             raise DeviceError("mlp shapes", _abi.LF_INVALID_ARGUMENT)
         if wg.rows != wu.rows or wg.columns != wu.columns:
             raise DeviceError("gate/up shapes", _abi.LF_INVALID_ARGUMENT)
         _family(family, max_tokens)
-        entry = _abi.ENTRY_W8A16_GATED_MLP if family == "w8a16" else _abi.ENTRY_W8A8_GATED_MLP
-        geometry = gated_mlp_geometry(wg.columns, wg.rows, max_tokens, entry) if one_launch else None
+        modes = {wg.scale_mode, wu.scale_mode, wd.scale_mode}
+        if modes == {BLOCK128}:
+            entry = _abi.ENTRY_W8A8_GATED_MLP_B128 if family == "w8a8" else None
+        elif BLOCK128 in modes:
+            entry = None
+        else:
+            entry = _abi.ENTRY_W8A16_GATED_MLP if family == "w8a16" else _abi.ENTRY_W8A8_GATED_MLP
+        geometry = (gated_mlp_geometry(wg.columns, wg.rows, max_tokens, entry)
+                    if one_launch and entry is not None else None)
         if geometry is not None:
             for w in (wg, wu, wd):
                 w.admit(entry)

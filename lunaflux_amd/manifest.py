@@ -47,6 +47,14 @@ MAX_SYMBOL_BYTES = 128  # the C ABI's bound (include/lunaflux_hip.h)
 # forms (_aq: x and a workspace in place of the quantized rows) are families
 # of their own, since their operand lists differ.
 FAMILIES = (
+    # block-scaled forms first: their symbols share the per-channel prefixes
+    (15, "lf_fp8_w8a16_dense_b128_"),
+    (16, "lf_fp8_w8a16_qkv_b128_"),
+    (17, "lf_fp8_w8a16_gate_up_b128_"),
+    (18, "lf_fp8_w8a8_dense_b128"),
+    (19, "lf_fp8_w8a8_qkv_b128"),
+    (20, "lf_fp8_w8a8_gate_up_b128"),
+    (21, "lf_fp8_w8a8_gated_mlp_b128"),
     (12, "lf_fp8_w8a8_dense_", "_aq"),
     (13, "lf_fp8_w8a8_qkv_", "_aq"),
     (14, "lf_fp8_w8a8_gate_up_", "_aq"),

@@ -48,7 +48,9 @@ def test_code_object_has_every_entry_point():
                    f"lf_fp8_w8a16_qkv_k4096_q4096_kv1024_m{m}" for m in (16, 32)] + [
                    f"lf_fp8_w8a16_{op}_m128_n{bn}" for op in ("dense", "qkv", "gate_up") for bn in (64, 128)] + [
                    f"lf_fp8_w8a16_dense_wide_k4096_m{m}" for m in (16, 32, 128)] + [
-                   "lf_fp8_rms_norm_quant_rows_eps1em5", "lf_fp8_rms_norm_quant_rows_eps1em6"]:
+                   "lf_fp8_rms_norm_quant_rows_eps1em5", "lf_fp8_rms_norm_quant_rows_eps1em6"] + [
+                   f"lf_fp8_w8a16_{op}_b128_m{m}" for op in ("dense", "qkv", "gate_up") for m in (16, 32, 64, 128)] + [
+                   f"lf_fp8_w8a8_{op}_b128" for op in ("dense", "qkv", "gate_up", "gated_mlp")]:
         assert symbol.encode() + b"\0" in image, symbol
 
 
@@ -268,6 +270,77 @@ def test_one_launch_w8a8_geometry_and_workspace():
         want = sync + fp8.act_quant_bytes(cap, h) + cap * i * 2 + fp8.act_quant_bytes(cap, i)
         assert lib.lunaflux_fp8_gated_mlp_workspace_bytes(_abi.ENTRY_W8A8_GATED_MLP, h, i, m) == want
     assert lib.lunaflux_fp8_gated_mlp_workspace_bytes(_abi.ENTRY_W8A8_GATED_MLP, 4000, 14336, 64) == -1
+
+
+def test_block_scaled_geometry_and_workspace():
+    """The _B128 entries. W8A16: the column-group form for every profile
+    (also <= 16 rows), the per-channel split raised so that a slice holds at
+    most 128 k-tiles, the per-channel workspace formula. W8A8: 256 group-
+    quantizer blocks then 128 x 128 tiles (64 h-columns for gate/up), 256
+    threads; workspace = sync area + codes [cap, K] + scales [K/128][cap]
+    (each part 256-aligned). GatedMlp: four steps on 128-row bands."""
+    lib = _abi.lib()
+    al = lambda v: -(-v // 256) * 256  # noqa: E731
+    for entry, op in [(_abi.ENTRY_W8A16_DENSE_B128, "dense"), (_abi.ENTRY_W8A16_QKV_B128, "qkv"),
+                      (_abi.ENTRY_W8A16_GATE_UP_B128, "gate_up")]:
+        for n, k, m, mt in [(4096, 4096, 1, 1), (6144, 4096, 32, 2), (14336, 4096, 64, 4),
+                            (4096, 14336, 128, 8), (1024, 32768, 16, 1)]:
+            d, sym = fp8.launch_geometry(entry, n, k, m)
+            assert sym == f"lf_fp8_w8a16_{op}_b128_m{16 * mt}" and d.block == (256, 1, 1)
+            groups = -(-(n // 16) // 4)
+            assert d.grid[0] % groups == 0
+            split = d.grid[0] // groups
+            kt = k // 128
+            assert 1 <= split <= kt and -(-kt // split) <= 128, (n, k, m, split)
+            nw = 2 if op == "gate_up" else 1
+            want = 256 if split == 1 else al(split * (n // 16) * nw * mt * 1024) + al(groups * 4)
+            assert fp8.w8a16_workspace_bytes(entry, n, k, m) == want
+    # 128-row blocks: N must be a multiple of 128, every QKV width too
+    with pytest.raises(fp8.DeviceError):
+        fp8.launch_geometry(_abi.ENTRY_W8A16_DENSE_B128, 4096 + 64, 4096, 16)
+    with pytest.raises(fp8.DeviceError):
+        fp8.launch_geometry(_abi.ENTRY_W8A8_QKV_B128, 4096 + 2 * 1088, 4096, 256, qkv_split=(4096, 1088))
+    for entry, op, n, k, m in [(_abi.ENTRY_W8A8_DENSE_B128, "dense", 4096, 14336, 2048),
+                               (_abi.ENTRY_W8A8_QKV_B128, "qkv", 6144, 4096, 300),
+                               (_abi.ENTRY_W8A8_GATE_UP_B128, "gate_up", 14336, 4096, 1)]:
+        d, sym = fp8.launch_geometry(entry, n, k, m)
+        bands = -(-m // 128)
+        gx = n // 64 if op == "gate_up" else n // 128
+        assert sym == f"lf_fp8_w8a8_{op}_b128" and d.grid == (256 + gx * bands, 1, 1) and d.block == (256, 1, 1)
+        cap = 128 * bands
+        want = 256 + 128 * bands + al(cap * k) + al((k // 128) * cap * 4)
+        assert fp8.w8a8_workspace_bytes(entry, n, k, m) == want
+    e = _abi.ENTRY_W8A8_GATED_MLP_B128
+    d, sym = fp8.gated_mlp_geometry(4096, 14336, 2048, e)
+    bands, cap = 16, 2048
+    assert sym == "lf_fp8_w8a8_gated_mlp_b128" and d.grid == (512 + (224 + 32) * bands, 1, 1)
+    want = (256 + 128 * 3 * bands + al(cap * 4096) + al(32 * cap * 4) + al(cap * 14336 * 2)
+            + al(cap * 14336) + al(112 * cap * 4))
+    assert lib.lunaflux_fp8_gated_mlp_workspace_bytes(e, 4096, 14336, 2048) == want
+    assert lib.lunaflux_fp8_gated_mlp_workspace_bytes(e, 4096 + 64, 14336, 2048) == -1
+
+
+def test_block_scaled_admission_cpu():
+    """Each entry admits only its own scale mode: LF_UNSUPPORTED across
+    modes, LF_INVALID_ARGUMENT for an expert count on a dense entry."""
+    rng = np.random.default_rng(3)
+    qb, sb = synth.weight(rng, 256, 256, block=128)
+    rb = fp8.pack_weight(qb, sb, fp8.BLOCK128)
+    qc, sc = synth.weight(rng, 256, 256)
+    rc = fp8.pack_weight(qc, sc)
+    block_entries = (_abi.ENTRY_W8A16_DENSE_B128, _abi.ENTRY_W8A16_QKV_B128, _abi.ENTRY_W8A16_GATE_UP_B128,
+                     _abi.ENTRY_W8A8_DENSE_B128, _abi.ENTRY_W8A8_QKV_B128, _abi.ENTRY_W8A8_GATE_UP_B128,
+                     _abi.ENTRY_W8A8_GATED_MLP_B128)
+    for entry in block_entries:
+        fp8.admit_weight(entry, rb[:256], rb.size, 256, 256)
+        with pytest.raises(fp8.DeviceError) as e:
+            fp8.admit_weight(entry, rc[:256], rc.size, 256, 256)
+        assert e.value.status == _abi.LF_UNSUPPORTED
+    for entry in (_abi.ENTRY_W8A16_DENSE, _abi.ENTRY_W8A8_GATE_UP_AQ, _abi.ENTRY_W8A8_GATED_MLP):
+        with pytest.raises(fp8.DeviceError) as e:
+            fp8.admit_weight(entry, rb[:256], rb.size, 256, 256)
+        assert e.value.status == _abi.LF_UNSUPPORTED
+    fp8.admit_weight(_abi.ENTRY_GROUPED, rb[:256], rb.size, 256, 256)
 
 
 def test_w8a16_gated_mlp_geometry():
@@ -556,24 +629,27 @@ def test_admission_of_weight_regions():
         rejected(d, bad, per.size)
 
 
-def test_dense_binds_refuse_block_scaled_weights_before_any_allocation():
-    """A block-scaled region bound to a dense, QKV or gate/up operation is
-    refused by admission (LF_UNSUPPORTED) before anything is allocated or
-    launched, so no device is needed to see it."""
+def test_block_scaled_weights_bind_their_own_entries():
+    """A block-scaled region bound to a dense, QKV or gate/up operation binds
+    the _B128 entry of the family (its admission passes); the per-token
+    GEMM-only W8A8 entry over pre-quantized rows refuses it (LF_UNSUPPORTED)
+    before anything is allocated or launched, so no device is needed."""
     from types import SimpleNamespace
     rng = np.random.default_rng(12)
     q = rng.integers(0, 0x7e, (256, 256), dtype=np.uint8)
     region = fp8.pack_weight(q, np.ones(4, np.float32), fp8.BLOCK128)
     w = fp8.Fp8Weight(SimpleNamespace(byte_count=region.size), 256, 256, 1, fp8.BLOCK128,
                       region[:256].copy())
-    binds = [lambda f: fp8.ProjectionRuntime.bind_dense(None, f, None, None, w, None, 16),
-             lambda f: fp8.ProjectionRuntime.bind_qkv(None, f, None, None, w, w, w, None, 16),
-             lambda f: fp8.ProjectionRuntime.bind_gate_up(None, f, None, None, w, w, None, 16)]
-    for bind in binds:
+    rt = fp8.ProjectionRuntime.__new__(fp8.ProjectionRuntime)
+    rt._w8a16 = lambda entry, *a, **kw: ("w8a16", entry)
+    rt._w8a8_one_launch = lambda entry, *a, **kw: ("w8a8", entry)
+    counts = SimpleNamespace(byte_count=20, ptr=None)
+    binds = {"dense": lambda f: rt.bind_dense(f, counts, None, w, None, 16),
+             "qkv": lambda f: rt.bind_qkv(f, counts, None, w, w, w, None, 16),
+             "gate_up": lambda f: rt.bind_gate_up(f, counts, None, w, w, None, 16)}
+    for op, bind in binds.items():
         for family in fp8.FAMILIES:
-            with pytest.raises(fp8.DeviceError) as err:
-                bind(family)
-            assert err.value.status == _abi.LF_UNSUPPORTED
+            assert bind(family) == (family, fp8._BLOCK_ENTRIES[(family, op)])
     with pytest.raises(fp8.DeviceError) as err:
         fp8.ProjectionRuntime.bind_dense_quantized(None, None, None, w, None, 16)
     assert err.value.status == _abi.LF_UNSUPPORTED

@@ -43,7 +43,11 @@ def test_manifest_describes_every_kernel_of_the_code_object(image):
                          ("lf_moe_route", 9), ("lf_moe_down_t256_b128", 9),
                          ("lf_fp8_w8a16_gated_mlp_h4096_i14336_m32", 10),
                          ("lf_fp8_w8a8_gated_mlp_t256_t256", 11), ("lf_fp8_w8a8_dense_t256_aq", 12),
-                         ("lf_fp8_w8a8_qkv_t128_aq", 13), ("lf_fp8_w8a8_gate_up_t256x128_aq", 14)]:
+                         ("lf_fp8_w8a8_qkv_t128_aq", 13), ("lf_fp8_w8a8_gate_up_t256x128_aq", 14),
+                         ("lf_fp8_w8a16_dense_b128_m16", 15), ("lf_fp8_w8a16_qkv_b128_m128", 16),
+                         ("lf_fp8_w8a16_gate_up_b128_m32", 17), ("lf_fp8_w8a8_dense_b128", 18),
+                         ("lf_fp8_w8a8_qkv_b128", 19), ("lf_fp8_w8a8_gate_up_b128", 20),
+                         ("lf_fp8_w8a8_gated_mlp_b128", 21)]:
         assert symbols[name][0] == family, name
     assert "lf_calibrate_copy" not in symbols          # a benchmark tool, not a plan kernel
     pairs = [(e["family_id"], e["entry_point_id"]) for e in module["entry_points"]]
