@@ -77,7 +77,9 @@ def roofline_kernel():
 class Layer:
     """Device-resident weights of one layer, `rotations` copies each."""
 
-    def __init__(self, rt, seed=1234, rotations=ROTATIONS):
+    def __init__(self, rt, seed=1234, rotations=ROTATIONS, block=False):
+        """block: 128 x 128 block scales (the _b128 entries) instead of
+        per-channel scales."""
         from lunaflux_amd import fp8, synth
         rng = np.random.default_rng(seed)
         t0 = time.time()
@@ -86,10 +88,11 @@ class Layer:
         for name, rows, cols in [("q", NQ, HIDDEN), ("k", NKV, HIDDEN), ("v", NKV, HIDDEN),
                                  ("o", HIDDEN, HIDDEN), ("gate", INTER, HIDDEN),
                                  ("up", INTER, HIDDEN), ("down", HIDDEN, INTER)]:
-            q, s = synth.weight(rng, rows, cols)
-            region = fp8.pack_weight(q, s)
+            q, s = synth.weight(rng, rows, cols, block=128 if block else None)
+            region = fp8.pack_weight(q, s, fp8.BLOCK128 if block else fp8.PER_CHANNEL)
             self.regions[name] = [rt.weight_from_region(region) for _ in range(rotations)]
-        log(f"weights ready ({rotations} copies of one layer) in {time.time() - t0:.1f}s")
+        log(f"weights ready ({rotations} copies of one {'block-scaled ' if block else ''}layer) "
+            f"in {time.time() - t0:.1f}s")
 
     def w(self, name, r):
         return self.regions[name][r % self.rotations]
@@ -225,6 +228,38 @@ class Bench:
         stop.record(stream)
         stop.synchronize()
         return start.elapsed_milliseconds(stop) / launches
+
+
+def block_scaled_bench(rt):
+    """The Llama-3-8B layer on 128 x 128 block-scaled weights (the _b128
+    entries the bindings pick for weight_scale_inv checkpoints): each
+    operation as the plan binds it (one launch; W8A16 GatedMlp as its two
+    block-scaled launches), decode in GB/s of algorithmic bytes (plus the
+    block scales), prefill in TFLOP/s."""
+    layer = Layer(rt, seed=4321, block=True)
+    out = {}
+    for mm, mt, fam in [(1, 16, "w8a16"), (32, 32, "w8a16"), (128, 128, "w8a16"),
+                        (2048, 2048, "w8a8"), (8192, 8192, "w8a8")]:
+        b = Bench(rt, layer, mt, fam)
+        n = 20 if fam == "w8a16" else 5
+        row = {}
+        for c, k, nn, no in call_shapes():
+            p = b.time_kernel(mm, c, n, warmup=2)
+            if fam == "w8a16":
+                byts = call_bytes(mm, k, nn, no) + (nn // 128) * (k // 128) * 4
+                row[c] = {"us": round(p * 1e3, 2), "GB/s": round(byts / (p * 1e-3) / 1e9, 1)}
+            else:
+                tf = call_flops(mm, k, nn) / (p * 1e-3) / 1e12
+                row[c] = {"us": round(p * 1e3, 1), "TFLOP/s": round(tf, 1),
+                          "fp8_frac": round(tf / FP8_PEAK_TFLOPS, 4)}
+        mlp = b.bind_mlp(mm, True)
+        t1 = b.time_ops(mlp, n)
+        row["gated_mlp"] = {"launches": len(mlp[0].steps), "us": round(t1 * 1e3, 1 if fam == "w8a8" else 2)}
+        row["layer_us"] = round(row["qkv"]["us"] + row["o"]["us"] + t1 * 1e3, 2)
+        out[f"{fam} M={mm}"] = row
+        log(f"block-scaled {fam} M={mm}: {row}")
+        del b
+    return out
 
 
 def rms_norm_quant_bench(rt, bench, m, launches=20):
@@ -489,30 +524,49 @@ def pmc_pass():
 
 
 # (M, K, N) of the dense GEMMs pmc_pass_prefill launches, in order.
-PREFILL_PASS_SHAPES = ((8192, INTER, HIDDEN), (8192, HIDDEN, HIDDEN), (3072, HIDDEN, HIDDEN),
-                       (2048, HIDDEN, HIDDEN))
+# (operation, M, K, N): N is the packed QKV width, or I for gate/up (whose
+# GEMM computes 2 I columns)
+PREFILL_PASS_SHAPES = (("down", 8192, INTER, HIDDEN), ("o", 8192, HIDDEN, HIDDEN),
+                       ("qkv", 8192, HIDDEN, NQ + 2 * NKV), ("gate_up", 8192, HIDDEN, INTER),
+                       ("o", 3072, HIDDEN, HIDDEN), ("o", 2048, HIDDEN, HIDDEN),
+                       ("qkv", 2048, HIDDEN, NQ + 2 * NKV), ("gate_up", 2048, HIDDEN, INTER))
+
+
+def prefill_pass_flops(op, m, k, n):
+    return 2 * m * k * (2 * n if op == "gate_up" else n)
 
 
 def pmc_pass_prefill():
-    """Short run for the MFMA-utilisation counter pass: the prefill down GEMM
-    (K=14336 -> N=4096) and o GEMM at M=8192 (256 x 256 tiles, four waves),
-    the o GEMM at M=3072 (192 tiles of 256 x 256: the eight-wave form) and at
-    M=2048 (128 x 128 tiles), 5 launches each after one act-quant."""
+    """Short run for the MFMA-utilisation counter pass: the GEMM-only W8A8
+    entries of all four Llama-3-8B operations at M = 8192 (256 x 256 tiles,
+    four waves), o at M = 3072 (192 tiles of 256 x 256: the eight-wave form)
+    and o, QKV and gate/up at M = 2048 (256 x 128 / eight-wave 256 x 256 /
+    four-wave 256 x 256 tiles), 5 launches each after one act-quant."""
     from lunaflux_amd import fp8, synth
     from lunaflux_amd.fp8 import ProjectionRuntime, _region
     rt = ProjectionRuntime(0)
     rng = np.random.default_rng(6)
-    for m, k, n in PREFILL_PASS_SHAPES:
-        w = rt.weight_from_region(fp8.pack_weight(*synth.weight(rng, n, k)))
+    for opname, m, k, n in PREFILL_PASS_SHAPES:
         x = rt.context.upload(synth.activations(rng, m, k))
-        y = rt.context.allocate(m * n * 2)
-        op = rt.bind_dense("w8a8", rt.step_counts(m, decode=False), _region(x, alignment=256), w,
-                           _region(y, alignment=256), m)
+        c = rt.step_counts(m, decode=False)
+        xr = _region(x, alignment=256)
+        if opname == "qkv":
+            ws = [rt.weight_from_region(fp8.pack_weight(*synth.weight(rng, nn, k))) for nn in (NQ, NKV, NKV)]
+            y = rt.context.allocate(m * n * 2)
+            op = rt.bind_qkv("w8a8", c, xr, *ws, _region(y, alignment=256), m, one_launch=False)
+        elif opname == "gate_up":
+            ws = [rt.weight_from_region(fp8.pack_weight(*synth.weight(rng, n, k))) for _ in range(2)]
+            y = rt.context.allocate(m * n * 2)
+            op = rt.bind_gate_up("w8a8", c, xr, *ws, _region(y, alignment=256), m, one_launch=False)
+        else:
+            w = rt.weight_from_region(fp8.pack_weight(*synth.weight(rng, n, k)))
+            y = rt.context.allocate(m * n * 2)
+            op = rt.bind_dense("w8a8", c, xr, w, _region(y, alignment=256), m, one_launch=False)
         op.steps[0].launch(rt.stream, synchronous=False)
         for _ in range(5):
             op.steps[-1].launch(rt.stream, synchronous=False)
         rt.stream.synchronize()
-        log(f"pmc prefill pass: {op.steps[-1].name} M={m} K={k} N={n} x5")
+        log(f"pmc prefill pass: {op.steps[-1].name} {opname} M={m} K={k} N={n} x5")
 
 
 def pmc_pass_all():
@@ -673,7 +727,7 @@ def summarize_mfma(counter_csv, trace_csv):
     busy = busy cycles / (GRBM_GUI_ACTIVE / 8 XCDs x 1024 SIMDs); clock =
     GRBM_GUI_ACTIVE / 8 / duration."""
     import csv
-    gemm = lambda name: name.startswith("lf_fp8_w8a8_dense")
+    gemm = lambda name: name.startswith("lf_fp8_w8a8_") and not name.endswith("_aq")
     disp = {}
     for r in csv.DictReader(open(counter_csv)):
         if gemm(r["Kernel_Name"]):
@@ -687,7 +741,7 @@ def summarize_mfma(counter_csv, trace_csv):
     lines = ["| Kernel | Shape | Threads | MFMA instructions | MFMA flops (MOPS_F8 x 512) | MFMA busy cycles "
              "| GRBM_GUI_ACTIVE | Duration (trace) | Clock | MFMA busy | Achieved |",
              "|---|---|---|---|---|---|---|---|---|---|---|"]
-    for s, (m, k, n) in enumerate(shapes):
+    for s, (opname, m, k, n) in enumerate(shapes):
         ds = [disp[i] for i in ids[5 * s:5 * s + 5]]
         ts = trace[5 * s:5 * s + 5]
         name = ds[0]["name"]
@@ -698,9 +752,9 @@ def summarize_mfma(counter_csv, trace_csv):
         ins = mean("SQ_INSTS_VALU_MFMA_F8") + mean("SQ_INSTS_VALU_MFMA_F6F4")
         mops = mean("SQ_INSTS_VALU_MFMA_MOPS_F8") * 512
         busy, gui = mean("SQ_VALU_MFMA_BUSY_CYCLES"), mean("GRBM_GUI_ACTIVE")
-        flops = 2 * m * n * k
-        op = "down" if k == INTER else "o"
-        lines.append(f"| {name} | {op}, M={m}, K={k}, N={n} | {ds[0]['wg']} | {ins:.0f} | {mops:.4g} "
+        flops = prefill_pass_flops(opname, m, k, n)
+        shape = f"N={n}" if opname != "gate_up" else f"N=2x{n}"
+        lines.append(f"| {name} | {opname}, M={m}, K={k}, {shape} | {ds[0]['wg']} | {ins:.0f} | {mops:.4g} "
                      f"(= 2MNK {flops:.4g}) | {busy:.4g} | {gui:.4g} | {dur:.1f} us | "
                      f"{gui / 8 / (dur * 1e-6) / 1e9:.2f} GHz | {100 * busy / (gui / 8 * 1024):.0f} % | "
                      f"{flops / dur / 1e6:.0f} TFLOP/s |")
@@ -865,6 +919,7 @@ def main():
             detail["prefill_w8a8"][f"M={mm}"] = row
             log(f"prefill M={mm}: {row}")
             del b, b1
+        detail["block_scaled"] = block_scaled_bench(rt)
         detail["moe"] = {}
         for name, c in MOE_CONFIGS.items():
             detail["moe"][name] = moe_bench(rt, c)
