@@ -357,8 +357,18 @@ int32_t lunaflux_fp8_rms_norm_quant_geometry(float epsilon, int64_t k, int32_t m
  * meaning no launch. Its outputs equal those of the four launches.
  * lf_moe_route does not read x.)
  *  lf_moe_gate_up[_b128|_t256|_t256_b128_q|_gemv](counts, desc, wg, wu, ws)
- *  lf_moe_quant_hidden  (counts, desc, ws)    (not with _t256_b128_q)
- *  lf_moe_down[_b128|_t256|_t256_b128|_gemv]   (counts, desc, wd, ws)
+ *  lf_moe_quant_hidden  (counts, desc, ws)    (not with _t256_b128_q or _t256_aq)
+ *  lf_moe_down[_b128|_t256_aq|_t256_b128|_gemv]   (counts, desc, wd, ws)
+ *  lf_moe_down_t256_aq  (counts, desc, wd, ws, sync)
+ * (_t256_aq: per-channel profiles on 256-row tiles; the hidden quantizer
+ * runs as the first counted step of the down launch: 256 blocks quantize h
+ * per token (the codes and scales of lf_moe_quant_hidden) and each down tile
+ * starts once every row of its 256-row tile is quantized, so the geometry
+ * gives LF_FP8_MOE_QUANT_HIDDEN no launch. sync: the region of the
+ * workspace from lunaflux_fp8_moe_sync_offset to its end, zero-filled once
+ * when allocated (its counters return to zero at the end of every launch;
+ * launches sharing one workspace must not overlap); its first int32 is the
+ * error word of the one-launch entries, LF_FP8_AQ_ERROR_OFFSET.)
  * (_t256: the GEMMs on 256 x 256 tiles, chosen by the launch geometry for
  * profiles that average >= 256 routed rows per expert, _t256_b128 with block
  * scales where both GEMMs have K <= 3072, its gate/up as _t256_b128_q, whose
@@ -410,9 +420,15 @@ int32_t lunaflux_fp8_moe_descriptor(int32_t experts, int32_t top_k,
                                     int32_t route_mode, int64_t hidden,
                                     int64_t inter, int32_t group,
                                     lf_fp8_moe_desc *out);
-/* Workspace bytes for up to max_tokens live tokens; -1 if invalid. */
+/* Workspace bytes for up to max_tokens live tokens (the arrays below for
+ * max_tokens, then the down launch's counter area where it takes one); -1 if
+ * invalid. */
 int64_t lunaflux_fp8_moe_workspace_bytes(const lf_fp8_moe_desc *desc,
                                          int32_t max_tokens);
+/* Byte offset of the counter area (sync operand of lf_moe_down_t256_aq)
+ * inside that workspace: the end of the arrays for max_tokens, so no live
+ * token count moves it; -1 if the profile's down entry takes none. */
+int64_t lunaflux_fp8_moe_sync_offset(const lf_fp8_moe_desc *desc, int32_t max_tokens);
 /* Byte offsets of the workspace arrays for `tokens` live tokens, in order:
  * top-k ids (int32 [T*k]), top-k weights (fp32 [T*k]), sorted assignments
  * (int32 [T*k]), position of each assignment (int32 [T*k]), expert row

@@ -132,6 +132,7 @@ SIGNATURES = {
                                                     ctypes.c_char_p]),
     "lunaflux_fp8_moe_descriptor": (_i32, [_i32, _i32, _i32, _i64, _i64, _i32, _vp]),
     "lunaflux_fp8_moe_workspace_bytes": (_i64, [_vp, _i32]),
+    "lunaflux_fp8_moe_sync_offset": (_i64, [_vp, _i32]),
     "lunaflux_fp8_moe_workspace_layout": (_i32, [_vp, _i32, _i64p]),
     "lunaflux_fp8_moe_launch_geometry": (_i32, [_i32, _vp, _i32, _i32p, ctypes.c_char_p]),
 }

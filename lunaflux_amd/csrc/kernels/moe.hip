@@ -822,9 +822,21 @@ LF_DEVICE float carry_ratio(float s, float &prev) {
 // QUANT (block-scaled gate/up only): the epilogue also quantizes h, writing
 // the hidden quantizer's e4m3 codes and per-128-column scales instead of
 // bf16 h (see the STAGE 0 epilogue below).
-template <int STAGE, bool BLOCK = false, bool QUANT = false>
+// bid: the block's index in the GEMM's part of the grid (blockIdx.x when the
+// GEMM is the whole grid). gate(tile, rows) runs once the tile's expert and
+// rows are known and before any of its activation rows or row scales is
+// read; false: the tile is not computed (AnyTile: every tile runs). A gated
+// tile reads its row scales with agent-scope loads: they were written in
+// the same launch, and a tile's first and last scales share 128-byte lines
+// with its neighbours', which a block of the same XCD may have read earlier.
+struct AnyTile {
+  LF_DEVICE bool operator()(int, int) const { return true; }
+};
+template <int STAGE, bool BLOCK = false, bool QUANT = false, class Gate = AnyTile>
 __device__ __forceinline__ void grouped_gemm_t256(const int32_t *counts, const MoeDesc &d, const uint8_t *w0,
-                                  const uint8_t *w1, uint8_t *ws) {
+                                  const uint8_t *w1, uint8_t *ws, int bid = -1,
+                                  const Gate &gate = Gate{}) {
+  constexpr bool kGated = !std::is_same<Gate, AnyTile>::value;
   static_assert(!QUANT || (STAGE == 0 && BLOCK), "the fused quantizer is the block-scaled gate/up's");
   using T = GemmTile256;
   constexpr int BM = T::kBM;
@@ -848,11 +860,16 @@ __device__ __forceinline__ void grouped_gemm_t256(const int32_t *counts, const M
   if (a_rows * static_cast<uint64_t>(K) >= (uint64_t(1) << 32)) return;
   const int gx = STAGE == 0 ? N / (T::kBN / 2) : N / T::kBN;
   int bx, by;
-  if (!w8a8v3::tile_of_block(gx, tiles[E], tiles[E], bx, by)) return;
+  if (!w8a8v3::tile_of_block(bid < 0 ? static_cast<int>(blockIdx.x) : bid, gx, tiles[E], tiles[E], bx,
+                             by)) {
+    return;
+  }
   const TileExpert te = find_tile_expert(tiles, at<int32_t>(ws, L.offsets), E, by);
   const int e = te.e;
   const int p0 = te.row_begin + (by - te.first_tile) * BM;
   const int pend = te.row_end;
+  // (the tile's live rows: pend is the end of its expert's rows)
+  if (!gate(by, pend - p0 < BM ? pend - p0 : BM)) return;
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int wm = wave / T::kWgn, wn = wave % T::kWgn;
@@ -881,7 +898,14 @@ __device__ __forceinline__ void grouped_gemm_t256(const int32_t *counts, const M
   float sa_mine = 0.0f;
   if constexpr (!BLOCK) {
     const float *row_scales = at<float>(ws, L.hs);
-    if (threadIdx.x < BM) sa_mine = row_scales[p0 + static_cast<int>(threadIdx.x) < pend ? p0 + threadIdx.x : p0];
+    if (threadIdx.x < BM) {
+      const int i = p0 + static_cast<int>(threadIdx.x) < pend ? p0 + threadIdx.x : p0;
+      if constexpr (kGated) {
+        sa_mine = __hip_atomic_load(row_scales + i, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      } else {
+        sa_mine = row_scales[i];
+      }
+    }
   } else {
     // Ratio tables (see BlockRescale256): threads 0..255 one tile row each
     // (its activation scales in token order for gate/up, expert order for
@@ -1112,6 +1136,87 @@ __device__ __forceinline__ void grouped_gemm_t256(const int32_t *counts, const M
       });
     }
   }
+}
+
+// Per-channel profiles on the 256-row tiles (e.g. Mixtral): the hidden
+// quantizer as the first counted step of the down launch
+// (lf_moe_down_t256_aq), so the plan has no lf_moe_quant_hidden launch. Per-
+// token scales need a whole row of h (I columns from every gate/up column
+// block), so the quantizer cannot live in the gate/up epilogue; here
+// kQuantBlocks blocks at the head of the grid quantize h in chunks of
+// kChunkRows rows (one wave per row: the standalone quantizer's code, its
+// stores written through, phases.h) and count each row into the counter of
+// its 256-row tile; a down tile starts its loads once its tile's counter
+// holds the tile's row count. The counters live in the operation's sync
+// area (the fifth operand, at a fixed offset of the workspace: error word,
+// done counter, one 128-byte line per row tile), left at zero by the last
+// down block of every launch.
+LF_DEVICE void moe_down_aq(const int32_t *counts, const MoeDesc &d, const uint8_t *wd, uint8_t *ws,
+                           uint8_t *sync_area) {
+  __shared__ phase::Flag flag;
+  __shared__ int32_t tab[2 * 257];  // row offsets [E + 1], then the 256-row tile prefix [E + 1]
+  __shared__ int row_tile[kChunkRows];
+  const int Tn = live_rows(counts, 1 << 30);
+  if (Tn == 0) return;
+  const MoeLayout L(d, Tn);
+  const int E = d.experts, A = Tn * d.top_k, I = d.inter;
+  const int32_t *offsets = at<int32_t>(ws, L.offsets);
+  const int32_t *tiles = at<int32_t>(ws, L.tiles) + (E + 1);
+  const int b = static_cast<int>(blockIdx.x);
+  if (b < kQuantBlocks) {
+    const phase::Sync sync{reinterpret_cast<int *>(sync_area), 1};
+    for (int i = threadIdx.x; i <= E; i += blockDim.x) {
+      tab[i] = offsets[i];
+      tab[E + 1 + i] = tiles[i];
+    }
+    __syncthreads();
+    const uint16_t *h = at<uint16_t>(ws, L.h);
+    uint8_t *hq = at<uint8_t>(ws, L.hq);
+    float *hs = at<float>(ws, L.hs);
+    const int wave = static_cast<int>(threadIdx.x) >> 6, lane = threadIdx.x & 63;
+    const int chunks = (A + kChunkRows - 1) / kChunkRows;
+    for (int c = b; c < chunks; c += kQuantBlocks) {
+      const int p = c * kChunkRows + wave;
+      if (wave < kChunkRows) {
+        int tile = -1;
+        if (p < A) {
+          const uint64_t off = static_cast<uint64_t>(p) * I;
+          // (the two-pass form above 8192 columns: the register-resident
+          // 16 KiB-row form would push this kernel past its VGPR budget)
+          quantize_row_wave<true, 16>(h + off, I, hq + off, hs + p);
+          // the expert of row p: offsets[e] <= p < offsets[e + 1]
+          int lo = 0, hi = E;
+          while (hi - lo > 1) {
+            const int mid = (lo + hi) >> 1;
+            if (tab[mid] <= p) {
+              lo = mid;
+            } else {
+              hi = mid;
+            }
+          }
+          tile = tab[E + 1 + lo] + ((p - tab[lo]) >> 8);
+        }
+        if (lane == 0) row_tile[wave] = tile;
+      }
+      asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+      __syncthreads();
+      if (threadIdx.x == 0) {
+        for (int w = 0; w < kChunkRows; ++w) {
+          if (row_tile[w] >= 0) {
+            __hip_atomic_fetch_add(sync.band(0, row_tile[w]), 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+          }
+        }
+      }
+      __syncthreads();  // row_tile is rewritten by the next chunk
+    }
+    return;
+  }
+  const phase::Sync sync{reinterpret_cast<int *>(sync_area), tiles[E]};
+  const auto gate = [&](int tile, int rows) {
+    return phase::wait_for(sync, sync.band(0, tile), rows, flag);
+  };
+  grouped_gemm_t256<1, false, false>(counts, d, wd, wd, ws, b - kQuantBlocks, gate);
+  phase::finish(sync, static_cast<int>(gridDim.x) - kQuantBlocks, 1, flag);
 }
 
 // --- grouped GEMV form ------------------------------------------------------------
@@ -1529,6 +1634,17 @@ __global__ __launch_bounds__(512) void lf_moe_down_t256(const int32_t *counts,
   const MoeDesc d = desc_of(desc);
   if (!desc_ok(d) || d.group != 0 || header_of(wd).magic != kWeightMagic) return;
   grouped_gemm_t256<1>(counts, d, wd, wd, ws);
+}
+
+// The same with the hidden quantizer as the launch's first counted step
+// (moe_down_aq): (counts, desc, wd, ws, sync), sync the operation's counter
+// area (lunaflux_fp8_moe_sync_offset), zero-filled once when allocated.
+__global__ __launch_bounds__(512) void lf_moe_down_t256_aq(const int32_t *counts,
+                                                           const int32_t *desc, const uint8_t *wd,
+                                                           uint8_t *ws, uint8_t *sync) {
+  const MoeDesc d = desc_of(desc);
+  if (!desc_ok(d) || d.group != 0 || header_of(wd).magic != kWeightMagic) return;
+  moe_down_aq(counts, d, wd, ws, sync);
 }
 
 // The same on 128 x 128 block scales (rescaled accumulators, see

@@ -898,9 +898,40 @@ int32_t lunaflux_fp8_moe_workspace_layout(const lf_fp8_moe_desc *d, int32_t toke
   return LF_OK;
 }
 
+// Per-channel profiles whose GEMMs run on 256-row tiles take the hidden
+// quantizer into the down launch (lf_moe_down_t256_aq); the same condition
+// as in lunaflux_fp8_moe_launch_geometry.
+static bool moe_tiles256(const lf_fp8_moe_desc *d, int64_t T) {
+  const int64_t A = T * d->top_k;
+  const bool b128 = d->group == 128;
+  return A >= 256 * static_cast<int64_t>(d->experts) && d->inter % 128 == 0 && d->hidden % 256 == 0 &&
+         (!b128 || (d->hidden <= 3072 && d->inter <= 3072)) &&
+         A * std::max<int64_t>(d->hidden, d->inter) < (int64_t(1) << 32);
+}
+static bool moe_gemv(const lf_fp8_moe_desc *d, int64_t T) {
+  return T <= 32 && d->inter % 64 == 0 && d->hidden % 64 == 0;
+}
+static bool moe_down_aq(const lf_fp8_moe_desc *d, int64_t T) {
+  return d->group == 0 && moe_tiles256(d, T) && !moe_gemv(d, T);
+}
+// Its counter area (kernels/phases.h): error word, done counter, one 128-byte
+// line per 256-row tile of the profile (at most A / 256 + E).
+static int64_t moe_sync_bytes(const lf_fp8_moe_desc *d, int64_t T) {
+  return moe_down_aq(d, T) ? 256 + 128 * (T * d->top_k / 256 + d->experts + 1) : 0;
+}
+
 int64_t lunaflux_fp8_moe_workspace_bytes(const lf_fp8_moe_desc *d, int32_t max_tokens) {
   int64_t offsets[13];
   if (max_tokens <= 0 || lunaflux_fp8_moe_workspace_layout(d, max_tokens, offsets) != LF_OK) {
+    return -1;
+  }
+  return offsets[12] + align_up(moe_sync_bytes(d, max_tokens), 256);
+}
+
+int64_t lunaflux_fp8_moe_sync_offset(const lf_fp8_moe_desc *d, int32_t max_tokens) {
+  int64_t offsets[13];
+  if (max_tokens <= 0 || lunaflux_fp8_moe_workspace_layout(d, max_tokens, offsets) != LF_OK ||
+      !moe_down_aq(d, max_tokens)) {
     return -1;
   }
   return offsets[12];
@@ -924,14 +955,15 @@ int32_t lunaflux_fp8_moe_launch_geometry(int32_t entry, const lf_fp8_moe_desc *d
   // table shares the LDS with the stage ring).
   // Their activation rows are addressed by 32-bit offsets into the token
   // and assignment arrays: A rows x max(H, I) < 2^32.
-  const bool t256 = A >= 256 * static_cast<int64_t>(d->experts) && d->inter % 128 == 0 &&
-                    d->hidden % 256 == 0 && (!b128 || (d->hidden <= 3072 && d->inter <= 3072)) &&
-                    A * std::max<int64_t>(d->hidden, d->inter) < (int64_t(1) << 32);
+  const bool t256 = moe_tiles256(d, T);
   const int64_t tiles256 = A / 256 + d->experts;
   // Profiles of at most 32 tokens (every expert <= 32 rows) run the grouped
   // GEMV form: a fixed grid (up to 4 blocks per CU) whose blocks loop over
   // the (expert with rows, 4 consecutive 16-column tiles) items.
-  const bool gemv = T <= 32 && d->inter % 64 == 0 && d->hidden % 64 == 0;
+  const bool gemv = moe_gemv(d, T);
+  // per-channel 256-row tiles: the hidden quantizer is the down launch's
+  // first step (kQuantBlocks blocks ahead of its tiles)
+  const bool down_aq = moe_down_aq(d, T);
   const int64_t kGemvBlocks = 1024;
   int64_t gx = 1, gy = 1;
   int32_t bx = 256;
@@ -992,8 +1024,9 @@ int32_t lunaflux_fp8_moe_launch_geometry(int32_t entry, const lf_fp8_moe_desc *d
       gx = d->inter / 64 * tiles;
       break;
     case LF_FP8_MOE_QUANT_HIDDEN:
-      if (t256 && b128 && !gemv) {
-        // fused into the gate/up epilogue: no launch (empty symbol, zero dims)
+      if ((t256 && b128 && !gemv) || down_aq) {
+        // fused into the gate/up epilogue (block scales) or run as the down
+        // launch's first step (per-token): no launch (empty symbol, zero dims)
         std::memset(dims, 0, 7 * sizeof(int32_t));
         std::memset(symbol, 0, LF_FP8_SYMBOL_BYTES);
         return LF_OK;
@@ -1008,8 +1041,8 @@ int32_t lunaflux_fp8_moe_launch_geometry(int32_t entry, const lf_fp8_moe_desc *d
         break;
       }
       if (t256) {
-        name = b128 ? "lf_moe_down_t256_b128" : "lf_moe_down_t256";
-        gx = d->hidden / 256 * tiles256;
+        name = b128 ? "lf_moe_down_t256_b128" : "lf_moe_down_t256_aq";
+        gx = d->hidden / 256 * tiles256 + (down_aq ? kQuantBlocks : 0);
         bx = 512;
         break;
       }

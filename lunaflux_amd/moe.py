@@ -50,6 +50,14 @@ def workspace_bytes(desc: MoeDescriptor, max_tokens: int) -> int:
     return n
 
 
+def sync_offset(desc: MoeDescriptor, max_tokens: int):
+    """Offset of the down launch's counter area in the workspace, or None
+    where the profile's down entry takes none (lunaflux_fp8_moe_sync_offset).
+    Its first int32 is the error word of the counted waits."""
+    n = _abi.lib().lunaflux_fp8_moe_sync_offset(ctypes.byref(desc), max_tokens)
+    return None if n < 0 else n
+
+
 LAYOUT_FIELDS = ("topk_ids", "topk_w", "sorted", "pos", "offsets", "tiles", "xq", "xs", "h", "hq",
                  "hs", "y", "end")
 
@@ -80,17 +88,25 @@ def bind_moe(rt: ProjectionRuntime, counts, desc: MoeDescriptor, desc_region: Ke
              wd: Fp8Weight, out: KernelArgument, max_tokens: int) -> BoundMoe:
     """Binds one MoE expert-MLP operation to its regions: 8 launch steps,
     fewer where the geometry gives a step an empty symbol (no launch): the
-    hidden quantizer when the gate/up epilogue runs it, and the two sort
-    steps and the token quantizer when the route step's kernel
-    (lf_moe_route_sort, profiles of at most 1024 assignments) does their
-    work."""
+    hidden quantizer when the gate/up epilogue (block scales) or the down
+    launch (lf_moe_down_t256_aq: per-token scales on 256-row tiles, with
+    the workspace's counter area as a fifth operand and its error word read
+    after a synchronous launch) runs it, and the two sort steps and the
+    token quantizer when the route step's kernel (lf_moe_route_sort,
+    profiles of at most 1024 assignments) does their work."""
     e, h, i = desc.experts, desc.hidden, desc.inter
     mode = _abi.LF_FP8_SCALE_BLOCK128 if desc.group == 128 else _abi.LF_FP8_SCALE_PER_CHANNEL
     for w, rows, cols in ((wg, i, h), (wu, i, h), (wd, h, i)):
         if (w.experts, w.rows, w.columns, w.scale_mode) != (e, rows, cols, mode):
             raise DeviceError("moe weight shape", _abi.LF_INVALID_ARGUMENT)
         w.admit(_abi.ENTRY_GROUPED)
-    ws = rt.context.allocate(workspace_bytes(desc, max_tokens))
+    nbytes = workspace_bytes(desc, max_tokens)
+    ws = rt.context.allocate(nbytes)
+    # the counter area of a down launch with the hidden quantizer inside:
+    # zero-filled once here, back at zero after every launch
+    sync_at = sync_offset(desc, max_tokens)
+    if sync_at is not None:
+        ws.copy_from_host(np.zeros(nbytes, np.uint8))
     wsr = _region(ws, alignment=256)
     c = _region(counts, COUNTS_BYTES, alignment=4)
 
@@ -107,10 +123,12 @@ def bind_moe(rt: ProjectionRuntime, counts, desc: MoeDescriptor, desc_region: Ke
         step(_abi.MOE_QUANT_TOKENS, [c, desc_region, x, wsr]),
         step(_abi.MOE_GATE_UP, [c, desc_region, wg.region, wu.region, wsr]),
         step(_abi.MOE_QUANT_HIDDEN, [c, desc_region, wsr]),
-        step(_abi.MOE_DOWN, [c, desc_region, wd.region, wsr]),
+        step(_abi.MOE_DOWN, [c, desc_region, wd.region, wsr]
+             + ([_region(ws, nbytes - sync_at, sync_at, alignment=256)] if sync_at is not None else [])),
         step(_abi.MOE_COMBINE, [c, desc_region, wsr, out]),
     ]
-    return BoundMoe(steps=[s for s in steps if s is not None], workspace=ws, desc=desc)
+    return BoundMoe(steps=[s for s in steps if s is not None], workspace=ws, desc=desc,
+                    error_offset=sync_at)
 
 
 def moe_expert_mlp(rt: ProjectionRuntime, x: np.ndarray, logits: np.ndarray, wg: Fp8Weight,

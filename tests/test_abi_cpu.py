@@ -40,7 +40,7 @@ def test_code_object_has_every_entry_point():
                                                for t in ("t128", "t256", "t256w8", "t256x128")] + ["lf_moe_route", "lf_moe_route_sort", "lf_moe_sort_count", "lf_moe_sort", "lf_moe_quant_tokens",
                    "lf_moe_gate_up", "lf_moe_gate_up_b128", "lf_moe_quant_hidden", "lf_moe_down",
                    "lf_moe_down_b128", "lf_moe_combine", "lf_moe_gate_up_gemv", "lf_moe_down_gemv",
-                   "lf_moe_gate_up_t256_b128", "lf_moe_down_t256_b128"] + [f"lf_fp8_w8a16_{op}_m{m}" for op in ("dense", "qkv", "gate_up")
+                   "lf_moe_gate_up_t256_b128", "lf_moe_down_t256_b128", "lf_moe_down_t256_aq"] + [f"lf_fp8_w8a16_{op}_m{m}" for op in ("dense", "qkv", "gate_up")
                                              for m in (16, 32, 64, 128)] + [
                    f"lf_fp8_w8a16_{op}_m16_t1" for op in ("dense", "qkv", "gate_up")] + [
                    f"lf_fp8_w8a16_dense_k{k}_m{m}" for k in (4096, 14336) for m in (16, 32)] + [
@@ -466,7 +466,8 @@ def test_moe_descriptor_layout_and_geometry():
     raw = d.as_bytes()
     assert raw.size == 32 and bytes(raw[:4]) == b"LMOE"
     lay = moe.workspace_layout(d, 1024)
-    assert lay["end"] == moe.workspace_bytes(d, 1024)
+    # (the workspace adds the down launch's counter area after the arrays)
+    assert lay["end"] == moe.sync_offset(d, 1024) < moe.workspace_bytes(d, 1024)
     a = 1024 * 2
     assert lay["topk_w"] == a * 4 and lay["y"] + a * 4096 * 4 == lay["end"]
     assert all(v % 256 == 0 for v in lay.values())
@@ -476,8 +477,17 @@ def test_moe_descriptor_layout_and_geometry():
     # (128 h-column block, 256-row tile of the tile bound), 8 waves
     assert sym == "lf_moe_gate_up_t256" and dims.grid == (14336 // 128 * (a // 256 + 8), 1, 1)
     assert dims.block == (512, 1, 1)
-    dims, sym = moe.launch_geometry(6, d, 1024)   # down
-    assert sym == "lf_moe_down_t256" and dims.grid == (4096 // 256 * (a // 256 + 8), 1, 1)
+    dims, sym = moe.launch_geometry(6, d, 1024)   # down, the hidden quantizer inside
+    assert sym == "lf_moe_down_t256_aq" and dims.grid == (256 + 4096 // 256 * (a // 256 + 8), 1, 1)
+    dims, sym = moe.launch_geometry(5, d, 1024)   # so no hidden-quantizer launch
+    assert sym == "" and dims.grid == (0, 0, 0)
+    # its counter area: error word, done counter, one line per 256-row tile
+    # of the profile, at the end of the arrays for max_tokens
+    sync_at = moe.sync_offset(d, 1024)
+    assert sync_at == moe.workspace_layout(d, 1024)["end"]
+    assert moe.workspace_bytes(d, 1024) == sync_at + -(-(256 + 128 * (a // 256 + 8 + 1)) // 256) * 256
+    assert moe.sync_offset(d, 512) is None      # 128-row tiles: no counted step
+    assert moe.workspace_bytes(d, 512) == moe.workspace_layout(d, 512)["end"]
     # the 256-row forms take 32-bit activation offsets: assignments x max(H, I)
     # must stay below 2^32 (here from 149,797 tokens at k = 2, I = 14336)
     for t, t256 in ((149796, True), (149797, False)):

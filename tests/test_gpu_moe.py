@@ -270,12 +270,13 @@ def test_moe_t256(rt, t, e, k, hidden, inter, skew, block):
     mode = 1 if block else 0
     desc = moe.moe_descriptor(e, k, mode, hidden, inter, 128 if block else 0)
     suffix = "_b128" if block else ""
-    # block scales: the gate/up epilogue quantizes h (no hidden-quantizer
-    # launch); check_output compares its codes and scales bit for bit with
-    # the quantizer applied to the bf16 h of the unfused kernel
+    # no hidden-quantizer launch: block scales, the gate/up epilogue quantizes
+    # h; per-token scales, the down launch does as its first counted step.
+    # check_output compares the codes and scales bit for bit with the
+    # quantizer applied to the device's bf16 h
     assert moe.launch_geometry(_abi.MOE_GATE_UP, desc, t)[1] == "lf_moe_gate_up_t256" + suffix + ("_q" if block else "")
-    assert moe.launch_geometry(_abi.MOE_QUANT_HIDDEN, desc, t)[1] == ("" if block else "lf_moe_quant_hidden")
-    assert moe.launch_geometry(_abi.MOE_DOWN, desc, t)[1] == "lf_moe_down_t256" + suffix
+    assert moe.launch_geometry(_abi.MOE_QUANT_HIDDEN, desc, t)[1] == ""
+    assert moe.launch_geometry(_abi.MOE_DOWN, desc, t)[1] == "lf_moe_down_t256" + ("_b128" if block else "_aq")
     rng = np.random.default_rng(950 + t + e + block)
     logits = (rng.standard_normal((t, e)) + rng.normal(0, skew, e)).astype(np.float32)
     x, logits, weights, out, st = run_case(rt, rng, t, e, k, hidden, inter, mode, block=block,
@@ -387,3 +388,38 @@ def test_moe_route_sort_one_block(rt, t, e, k, mode, group):
         np.testing.assert_array_equal(results[1]["xq"].reshape(t, hidden), q)
         np.testing.assert_array_equal(results[1]["xs"].view(np.float32).ravel(), np.asarray(sc, np.float32).ravel())
     assert results[1]["offsets"][-1] == t * k
+
+
+def test_moe_down_quantizer_step_sticky_error(rt):
+    """The counted wait of lf_moe_down_t256_aq (the hidden quantizer as the
+    down launch's first step), forced from the host: a row-tile counter
+    preset far below its target runs the down tiles' wait out (every kernel
+    still ends), the binding raises and zero-fills the workspace, and the
+    next launch gives the first launch's output again."""
+    from lunaflux_amd import _abi, moe
+    from lunaflux_amd.device import DeviceError
+    from lunaflux_amd.fp8 import _region
+    e, k, hidden, inter, t = 4, 1, 256, 256, 1024
+    desc = moe.moe_descriptor(e, k, 0, hidden, inter, 0)
+    assert moe.launch_geometry(_abi.MOE_DOWN, desc, t)[1] == "lf_moe_down_t256_aq"
+    rng = np.random.default_rng(977)
+    x = synth.activations(rng, t, hidden)
+    logits = rng.standard_normal((t, e)).astype(np.float32)
+    ws_ = [rt.upload_weight(*expert_weights(rng, e, r, c, False)) for r, c in ((inter, hidden), (inter, hidden),
+                                                                            (hidden, inter))]
+    ctx = rt.context
+    xa, la, da = ctx.upload(x), ctx.upload(logits), ctx.upload(desc.as_bytes())
+    oa = ctx.allocate(t * hidden * 2)
+    op = moe.bind_moe(rt, rt.step_counts(t, decode=False), desc, _region(da, 32, alignment=4),
+                      _region(la, alignment=256), _region(xa, alignment=256), *ws_, _region(oa, alignment=256), t)
+    assert "lf_moe_quant_hidden" not in [s.name for s in op.steps]
+    op.launch(rt.stream, synchronous=True)
+    want = oa.read(np.uint16, (t, hidden))
+    sync_at = moe.sync_offset(desc, t)
+    assert op.error_offset == sync_at
+    op.workspace.copy_from_host(np.array([-(1 << 30)], np.int32), offset=sync_at + 256)
+    with pytest.raises(DeviceError):
+        op.launch(rt.stream, synchronous=True)
+    assert not op.workspace.read(np.uint8, (op.workspace.byte_count,)).any(), "workspace not zero-filled"
+    op.launch(rt.stream, synchronous=True)
+    assert np.array_equal(oa.read(np.uint16, (t, hidden)), want)

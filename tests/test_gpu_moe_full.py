@@ -224,7 +224,8 @@ def test_moe_config4_mixtral_full_shape(rt):
     t, e, k, hidden, inter = 1024, 8, 2, 4096, 14336
     desc = moe.moe_descriptor(e, k, 0, hidden, inter, 0)
     assert moe.launch_geometry(_abi.MOE_GATE_UP, desc, t)[1] == "lf_moe_gate_up_t256"
-    assert moe.launch_geometry(_abi.MOE_DOWN, desc, t)[1] == "lf_moe_down_t256"
+    assert moe.launch_geometry(_abi.MOE_DOWN, desc, t)[1] == "lf_moe_down_t256_aq"
+    assert moe.launch_geometry(_abi.MOE_QUANT_HIDDEN, desc, t)[1] == ""
     rng = np.random.default_rng(40)
     logits = (rng.standard_normal((t, e)) + rng.normal(0, 1.5, e)).astype(np.float32)
     x, weights, out, st = run_full(rt, rng, t, e, k, hidden, inter, 0, False, logits)

@@ -174,7 +174,7 @@ def test_this_builds_expert_mlp_entries():
     the launch steps the geometry gives each profile."""
     for shape, t, want in [
         (MIXTRAL, 1024, ["lf_moe_route", "lf_moe_sort_count", "lf_moe_sort", "lf_moe_quant_tokens",
-                         "lf_moe_gate_up_t256", "lf_moe_quant_hidden", "lf_moe_down_t256", "lf_moe_combine"]),
+                         "lf_moe_gate_up_t256", "lf_moe_down_t256_aq", "lf_moe_combine"]),
         (FINE, 4096, ["lf_moe_route", "lf_moe_sort_count", "lf_moe_sort", "lf_moe_quant_tokens",
                       "lf_moe_gate_up_t256_b128_q", "lf_moe_down_t256_b128", "lf_moe_combine"]),
         (FINE, 32, ["lf_moe_route_sort", "lf_moe_gate_up_gemv", "lf_moe_quant_hidden", "lf_moe_down_gemv",
