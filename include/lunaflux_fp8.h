@@ -358,7 +358,7 @@ int32_t lunaflux_fp8_rms_norm_quant_geometry(float epsilon, int64_t k, int32_t m
  * lf_moe_route does not read x.)
  *  lf_moe_gate_up[_b128|_t256|_t256_b128_q|_gemv](counts, desc, wg, wu, ws)
  *  lf_moe_quant_hidden  (counts, desc, ws)    (not with _t256_b128_q or _t256_aq)
- *  lf_moe_down[_b128|_t256_aq|_t256_b128|_gemv]   (counts, desc, wd, ws)
+ *  lf_moe_down[_b128|_t256_b128|_gemv]   (counts, desc, wd, ws)
  *  lf_moe_down_t256_aq  (counts, desc, wd, ws, sync)
  * (_t256_aq: per-channel profiles on 256-row tiles; the hidden quantizer
  * runs as the first counted step of the down launch: 256 blocks quantize h

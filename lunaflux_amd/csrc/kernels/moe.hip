@@ -1145,17 +1145,77 @@ __device__ __forceinline__ void grouped_gemm_t256(const int32_t *counts, const M
 // block), so the quantizer cannot live in the gate/up epilogue; here
 // kQuantBlocks blocks at the head of the grid quantize h in chunks of
 // kChunkRows rows (one wave per row: the standalone quantizer's code, its
-// stores written through, phases.h) and count each row into the counter of
+// stores written through, phases.h; rows of 8193-16384 columns by wave
+// pairs, two rows a pair) and count each row into the counter of
 // its 256-row tile; a down tile starts its loads once its tile's counter
 // holds the tile's row count. The counters live in the operation's sync
 // area (the fifth operand, at a fixed offset of the workspace: error word,
 // done counter, one 128-byte line per row tile), left at zero by the last
 // down block of every launch.
+// RB rows of h held by S waves in registers (S = 2 for rows of 8193-16384
+// columns, e.g. Mixtral's I = 14336, that the one-wave forms hold only with
+// 32 chunks per lane, past this kernel's register budget): wave part q of
+// the rows holds 16-byte chunks [q per, (q + 1) per) of each of its RB rows
+// as the one-wave form holds a whole row (C chunks per lane and row, every
+// load of the RB rows in flight at once), a row's amax is the max of the S
+// waves' maxima (through red, RB floats per wave in LDS), then each wave
+// encodes its own chunks. A max is exact in any order, so amax, ratio,
+// codes and scale are those of the one-wave forms. Rows p0 .. p0 + RB - 1;
+// those at or past A load and store nothing. Every wave of the block calls
+// it (it holds a block barrier).
+template <int C, int S, int RB>
+LF_DEVICE void quantize_rows_split(const uint16_t *h, int I, int p0, int A, uint8_t *hq, float *hs,
+                                   float *red, int wave) {
+  const int lane = threadIdx.x & 63, part = wave % S;
+  const int chunks = I >> 3, per = (chunks + S - 1) / S;
+  const int c0 = part * per, c1 = c0 + per < chunks ? c0 + per : chunks;
+  u32x4 v[RB][C];
+  static_for<RB>([&](auto b) {
+    const bool live = p0 + b < A;
+    const u32x4 *src = reinterpret_cast<const u32x4 *>(h + static_cast<uint64_t>(live ? p0 + b : 0) * I);
+    static_for<C>([&](auto c) {
+      const int idx = c0 + lane + 64 * c;
+      v[b][c] = (live && idx < c1) ? src[idx] : u32x4{0u, 0u, 0u, 0u};
+    });
+  });
+  static_for<RB>([&](auto b) {
+    float amax = 0.0f;
+    static_for<C>([&](auto c) {
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        amax = fmaxf(amax, fabsf(bf16_to_f32(v[b][c][i] & 0xffffu)));
+        amax = fmaxf(amax, fabsf(bf16_to_f32(v[b][c][i] >> 16)));
+      }
+    });
+    amax = wave_max(amax);
+    if (lane == 0) red[RB * wave + b] = amax;
+  });
+  __syncthreads();
+  static_for<RB>([&](auto b) {
+    float amax = 0.0f;
+#pragma unroll
+    for (int q = 0; q < S; ++q) amax = fmaxf(amax, red[RB * (wave - part + q) + b]);
+    const bool live = p0 + b < A, zero = amax == 0.0f;
+    const float ratio = zero ? 0.0f : 448.0f / amax;
+    static_for<C>([&](auto c) { opaque(v[b][c]); });
+    uint8_t *dst = hq + static_cast<uint64_t>(live ? p0 + b : 0) * I;
+    static_for<C>([&](auto c) {
+      const int idx = c0 + lane + 64 * c;
+      const uint32_t lo = e4m3x4_from_bf16(v[b][c][0], v[b][c][1], ratio);
+      const uint32_t hi = e4m3x4_from_bf16(v[b][c][2], v[b][c][3], ratio);
+      if (live && idx < c1) store_codes8<true>(dst + 8 * idx, zero ? 0u : lo, zero ? 0u : hi);
+    });
+    if (live && part == 0 && lane == 0) store_scale<true>(hs + p0 + b, zero ? 0.0f : amax / 448.0f);
+  });
+}
+
 LF_DEVICE void moe_down_aq(const int32_t *counts, const MoeDesc &d, const uint8_t *wd, uint8_t *ws,
                            uint8_t *sync_area) {
   __shared__ phase::Flag flag;
   __shared__ int32_t tab[2 * 257];  // row offsets [E + 1], then the 256-row tile prefix [E + 1]
-  __shared__ int row_tile[kChunkRows];
+  constexpr int kHeldRows = 64;
+  __shared__ int row_tile[kHeldRows];  // the 256-row tile of each held row (-1: none)
+  __shared__ float red[2 * kChunkRows];  // per-wave row maxima (quantize_rows_split)
   const int Tn = live_rows(counts, 1 << 30);
   if (Tn == 0) return;
   const MoeLayout L(d, Tn);
@@ -1174,40 +1234,68 @@ LF_DEVICE void moe_down_aq(const int32_t *counts, const MoeDesc &d, const uint8_
     uint8_t *hq = at<uint8_t>(ws, L.hq);
     float *hs = at<float>(ws, L.hs);
     const int wave = static_cast<int>(threadIdx.x) >> 6, lane = threadIdx.x & 63;
-    const int chunks = (A + kChunkRows - 1) / kChunkRows;
+    // waves per row (block-uniform): rows of 8193-16384 columns by wave
+    // pairs, each wave holding halves of two rows (up to 14336 columns: 14
+    // chunks per lane and row) or of one (16 chunks); one wave per row else
+    const int S = I > 8192 && I <= 16384 ? 2 : 1;
+    const int RB = S == 2 && I <= 14336 ? 2 : 1;
+    const int R = kChunkRows / S * RB;  // rows per chunk
+    const int first = wave / S * RB;    // this wave's first row in the chunk
+    const int chunks = (A + R - 1) / R;
+    int held = 0;  // rows quantized and not yet counted (block-uniform)
     for (int c = b; c < chunks; c += kQuantBlocks) {
-      const int p = c * kChunkRows + wave;
-      if (wave < kChunkRows) {
-        int tile = -1;
-        if (p < A) {
-          const uint64_t off = static_cast<uint64_t>(p) * I;
-          // (the two-pass form above 8192 columns: the register-resident
-          // 16 KiB-row form would push this kernel past its VGPR budget)
-          quantize_row_wave<true, 16>(h + off, I, hq + off, hs + p);
-          // the expert of row p: offsets[e] <= p < offsets[e + 1]
-          int lo = 0, hi = E;
-          while (hi - lo > 1) {
-            const int mid = (lo + hi) >> 1;
-            if (tab[mid] <= p) {
-              lo = mid;
-            } else {
-              hi = mid;
+      const int p0 = c * R + first;
+      if (RB == 2) {
+        quantize_rows_split<14, 2, 2>(h, I, p0, A, hq, hs, red, wave);
+      } else if (S == 2) {
+        quantize_rows_split<16, 2, 1>(h, I, p0, A, hq, hs, red, wave);
+      } else if (p0 < A) {
+        const uint64_t off = static_cast<uint64_t>(p0) * I;
+        // (the two-pass form above 16384 columns)
+        quantize_row_wave<true, 16>(h + off, I, hq + off, hs + p0);
+      }
+      if (lane == 0 && wave % S == 0) {
+        for (int r = 0; r < RB; ++r) {
+          const int p = p0 + r;
+          int tile = -1;
+          if (p < A) {
+            // the expert of row p: offsets[e] <= p < offsets[e + 1]
+            int lo = 0, hi = E;
+            while (hi - lo > 1) {
+              const int mid = (lo + hi) >> 1;
+              if (tab[mid] <= p) {
+                lo = mid;
+              } else {
+                hi = mid;
+              }
             }
+            tile = tab[E + 1 + lo] + ((p - tab[lo]) >> 8);
           }
-          tile = tab[E + 1 + lo] + ((p - tab[lo]) >> 8);
-        }
-        if (lane == 0) row_tile[wave] = tile;
-      }
-      asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-      __syncthreads();
-      if (threadIdx.x == 0) {
-        for (int w = 0; w < kChunkRows; ++w) {
-          if (row_tile[w] >= 0) {
-            __hip_atomic_fetch_add(sync.band(0, row_tile[w]), 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-          }
+          row_tile[held + first + r] = tile;
         }
       }
-      __syncthreads();  // row_tile is rewritten by the next chunk
+      held += R;
+      // The rows are counted once the block's stores of them have completed,
+      // when the list is full or after the block's last chunk: a down tile
+      // cannot take this CU before this block ends (one block per CU), so
+      // counting chunk by chunk would only put a store wait between chunks.
+      if (held + R > kHeldRows || c + kQuantBlocks >= chunks) {
+        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+        __syncthreads();
+        if (threadIdx.x == 0) {
+          // runs of rows of one tile as one add
+          for (int w = 0; w < held;) {
+            int n = 1;
+            while (w + n < held && row_tile[w + n] == row_tile[w]) ++n;
+            if (row_tile[w] >= 0) {
+              __hip_atomic_fetch_add(sync.band(0, row_tile[w]), n, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            }
+            w += n;
+          }
+        }
+        __syncthreads();  // row_tile is rewritten from the start
+        held = 0;
+      }
     }
     return;
   }
@@ -1628,17 +1716,10 @@ __global__ __launch_bounds__(512) void lf_moe_gate_up_t256(const int32_t *counts
   grouped_gemm_t256<0>(counts, d, wg, wu, ws);
 }
 
-__global__ __launch_bounds__(512) void lf_moe_down_t256(const int32_t *counts,
-                                                        const int32_t *desc, const uint8_t *wd,
-                                                        uint8_t *ws) {
-  const MoeDesc d = desc_of(desc);
-  if (!desc_ok(d) || d.group != 0 || header_of(wd).magic != kWeightMagic) return;
-  grouped_gemm_t256<1>(counts, d, wd, wd, ws);
-}
-
-// The same with the hidden quantizer as the launch's first counted step
-// (moe_down_aq): (counts, desc, wd, ws, sync), sync the operation's counter
-// area (lunaflux_fp8_moe_sync_offset), zero-filled once when allocated.
+// The per-channel down GEMM on 256-row tiles, with the hidden quantizer as
+// the launch's first counted step (moe_down_aq): (counts, desc, wd, ws,
+// sync), sync the operation's counter area (lunaflux_fp8_moe_sync_offset),
+// zero-filled once when allocated.
 __global__ __launch_bounds__(512) void lf_moe_down_t256_aq(const int32_t *counts,
                                                            const int32_t *desc, const uint8_t *wd,
                                                            uint8_t *ws, uint8_t *sync) {
