@@ -942,14 +942,13 @@ __device__ __forceinline__ void w8a16_fixed_group_kernel(const int32_t *counts, 
 // tripled the operation's time.)
 //
 // Measured on MI355X (Llama-3-8B widths, weights rotated past the MALL),
-// this form is slower than the two launches it replaces: 40.2 vs 32.3 us at
-// M = 1 and 44.8 vs 38.6 us at M = 32. Back-to-back launches on one queue
-// cost almost nothing at the boundary, the down part cannot start before
-// the last gate/up block of its slice, and that block's count reaches the
-// polling down blocks 3-5 us after it is issued (per-block timestamps), so
-// the overlap it buys is smaller than the signalling delay. It is built for
-// callers that need the operation as one launch; the plan binds the two
-// launches by default.
+// this form runs as fast as the two launches it replaces at M = 32 (37.1
+// vs 37.2 us) and 3 us behind them at M <= 16 (35.1 vs 32.0 us, where the
+// two-launch path runs down on the faster one-tile form). Back-to-back
+// launches on one queue cost almost nothing at the boundary, and the down
+// part cannot start before the last gate/up block of its slice, so the one
+// launch buys no overlap. It is the plan's entry for the operation (one
+// launch per operation).
 //
 // Blocks are dispatched in index order on each XCD, so every gate/up block
 // has a CU before any down block of its XCD takes one, and gate/up blocks

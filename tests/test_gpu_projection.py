@@ -152,9 +152,9 @@ def test_dense_w8a8(rt, m, k, n, max_tokens):
 @pytest.mark.parametrize("family_op", ["dense", "gate_up"])
 def test_w8a16_split_k_repeated_launches(rt, family_op):
     """The column-group form reduces split-K partials through the workspace
-    and resets its arrival counters at the end of every launch: three
-    launches of one binding (one workspace) must each match the oracle and
-    be bit-identical to each other (the slice sum order is fixed)."""
+    and clears their slots at the end of every launch: three launches of
+    one binding (one workspace) must each match the oracle and be
+    bit-identical to each other (the slice sum order is fixed)."""
     from lunaflux_amd import _abi, fp8
     from lunaflux_amd.fp8 import _region
     rng = np.random.default_rng(7100)
