@@ -183,11 +183,13 @@ enum lf_fp8_entry {
 /* Block-scaled projections (checkpoints whose weights carry weight_scale_inv
  * 128 x 128 block scales: W = q s[n / 128][k / 128]); N and K multiples of
  * 128, every Q / K / V width of a QKV operation too.
- *  W8A16: lf_fp8_w8a16_{dense,qkv,gate_up}_b128_m{16,32,64,128}
- *      operands and workspace as the per-channel W8A16 entries
- *      (lunaflux_fp8_w8a16_workspace_bytes with the _B128 entry); the
- *      column-group form for every profile, each k-tile's products scaled by
- *      its block scale: y = sum_kt s[n / 128][kt] sum_{k in kt} x_k q_nk.
+ *  W8A16: lf_fp8_w8a16_{dense,qkv,gate_up}_b128_m{16,32,64,128} and, for
+ *      profiles of 65..128 rows, lf_fp8_w8a16_{op}_b128_m128_n{64,128}
+ *      (the per-channel entry's LDS-tiled GEMM geometry); operands and
+ *      workspace as the per-channel W8A16 entries
+ *      (lunaflux_fp8_w8a16_workspace_bytes with the _B128 entry); each
+ *      k-tile's products scaled by its block scale:
+ *      y = sum_kt s[n / 128][kt] sum_{k in kt} x_k q_nk.
  *  W8A8: lf_fp8_w8a8_{dense,qkv,gate_up}_b128 (counts, x, w..., y, ws), one
  *      launch each: x quantized per token per 128-column group (amax over
  *      the group, the per-token quantizer's arithmetic) inside the launch,

@@ -91,14 +91,22 @@ LF_DEVICE void wait_ring(int later) {
 // (no activation load, no store, no split-K arrival). THROUGH: the outputs
 // are stored through the XCD's L2 (phases.h), for an output that blocks of
 // the same launch read.
-template <int BN, int WGM, int WGN, int NSA, int NSB, int MODE, bool THROUGH = false, class Gate = NoWait>
+// BLOCK: the weights carry 128 x 128 block scales (s[N/128][K/128]) instead
+// of channel scales. A k-step is one 128-deep scale block and a fragment's
+// 16 columns lie in one 128-row block, so each k-step's MFMAs accumulate
+// into fresh fragments, which are then multiplied by that block's scale
+// (one per wave and fragment, a scalar load) and added to the running sums
+// (y = sum_kt s[nb][kt] sum_{k in kt} x_k q_k, fp32); the epilogue's
+// multiplier is 1.
+template <int BN, int WGM, int WGN, int NSA, int NSB, int MODE, bool THROUGH = false, class Gate = NoWait,
+          bool BLOCK = false>
 __device__ __forceinline__ void w8a16_gemm_kernel(uint8_t *smem, const int32_t *counts, const uint16_t *x,
                                                   const uint8_t *w0, const uint8_t *w1, const uint8_t *w2,
                                                   uint16_t *y, uint8_t *ws, int bid = -1, int nblocks = -1,
                                                   const Gate &gate = Gate{}) {
   using T = Tile<BN, WGM, WGN, NSA, NSB>;
   __shared__ int last_block;
-  if (!dense_regions_ok<MODE>(w0, w1, w2)) return;
+  if (!dense_regions_ok<MODE, BLOCK ? kScaleBlock128 : kScalePerChannel>(w0, w1, w2)) return;
   const WeightHeader &h0 = header_of(w0);
   const int K = static_cast<int>(h0.columns);
   const int KT = K >> 7;
@@ -156,13 +164,22 @@ __device__ __forceinline__ void w8a16_gemm_kernel(uint8_t *smem, const int32_t *
   };
 
   // This lane's channel scales (one per fragment column), requested first.
+  // Block scales: the multiplier is 1, and bs[j] points at the k-step
+  // scales of fragment j's 128-row block from this slice's first k-tile.
   float sc[T::kFN];
+  const float *bs[BLOCK ? T::kFN : 1];
 #pragma unroll
   for (int j = 0; j < T::kFN; ++j) {
     const uint8_t *region;
     int tile, ocol;
     slot(wn * T::kFN + j, region, tile, ocol);
-    sc[j] = expert_scales(region, 0)[tile * 16 + r];
+    if constexpr (BLOCK) {
+      sc[j] = 1.0f;
+      bs[j] = reinterpret_cast<const float *>(w8a8v3::uniform_ptr(reinterpret_cast<const uint8_t *>(
+          expert_scales(region, 0) + static_cast<uint64_t>(tile >> 3) * KT + kt0)));
+    } else {
+      sc[j] = expert_scales(region, 0)[tile * 16 + r];
+    }
   }
 
   // Global sources of this lane's load instructions at k-tile 0: activation
@@ -257,6 +274,13 @@ __device__ __forceinline__ void w8a16_gemm_kernel(uint8_t *smem, const int32_t *
         af[step][i] =
             *reinterpret_cast<const bf16x8 *>(a + row * 256 + ((((g << 2) | step) ^ chunk_swizzle(r)) << 4));
       }
+    // BLOCK: this k-step's products, scaled into acc after its MFMAs
+    f32x4 part[BLOCK ? T::kFM : 1][T::kFN];
+    float sb[BLOCK ? T::kFN : 1];
+    if constexpr (BLOCK) {
+#pragma unroll
+      for (int j = 0; j < T::kFN; ++j) sb[j] = bs[j][k];
+    }
 #pragma unroll
     for (int step = 0; step < 4; ++step) {
 #pragma unroll
@@ -264,9 +288,26 @@ __device__ __forceinline__ void w8a16_gemm_kernel(uint8_t *smem, const int32_t *
         const bf16x8 bf = weight_fragment(bq[j], step);
 #pragma unroll
         for (int i = 0; i < T::kFM; ++i) {
-          acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(af[step][i], bf, acc[i][j], 0, 0, 0);
+          if constexpr (BLOCK) {
+            part[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
+                af[step][i], bf, step == 0 ? f32x4{0.f, 0.f, 0.f, 0.f} : part[i][j], 0, 0, 0);
+          } else {
+            acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(af[step][i], bf, acc[i][j], 0, 0, 0);
+          }
         }
       }
+    }
+    if constexpr (BLOCK) {
+#pragma unroll
+      for (int j = 0; j < T::kFN; ++j)
+#pragma unroll
+        for (int i = 0; i < T::kFM; ++i) {
+          acc[i][j] += part[i][j] * sb[j];
+          // keeps these reads of the MFMA results in the MFMAs' basic block
+          // (a read sunk past a branch has been issued without the wait
+          // states an MFMA result needs: w8a16.hip, BLOCK)
+          asm volatile("" : "+v"(acc[i][j]));
+        }
     }
   }
 
@@ -474,6 +515,32 @@ extern "C" {
 
 LF_W16_GEMM_ENTRIES(64, 4, 2, 4, 2)
 LF_W16_GEMM_ENTRIES(128, 4, 2, 2, 4)
+
+// The same over weights with 128 x 128 block scales:
+// lf_fp8_w8a16_{op}_b128_m128_n{BN}.
+#define LF_W16_GEMM_B128_ENTRIES(BN, WGM, WGN, NSA, NSB)                                         \
+  __global__ __launch_bounds__(64 * WGM * WGN) void lf_fp8_w8a16_dense_b128_m128_n##BN(          \
+      const int32_t *counts, const uint16_t *x, const uint8_t *w, uint16_t *y, uint8_t *ws) {     \
+    __shared__ __attribute__((aligned(1024))) uint8_t smem[w16g::Tile<BN, WGM, WGN, NSA, NSB>::kSmem]; \
+    w16g::w8a16_gemm_kernel<BN, WGM, WGN, NSA, NSB, 0, false, NoWait, true>(smem, counts, x, w, w, w, y, ws); \
+  }                                                                                              \
+  __global__ __launch_bounds__(64 * WGM * WGN) void lf_fp8_w8a16_qkv_b128_m128_n##BN(            \
+      const int32_t *counts, const uint16_t *x, const uint8_t *wq, const uint8_t *wk,            \
+      const uint8_t *wv, uint16_t *y, uint8_t *ws) {                                             \
+    __shared__ __attribute__((aligned(1024))) uint8_t smem[w16g::Tile<BN, WGM, WGN, NSA, NSB>::kSmem]; \
+    w16g::w8a16_gemm_kernel<BN, WGM, WGN, NSA, NSB, 1, false, NoWait, true>(smem, counts, x, wq, wk, wv, y, \
+                                                                            ws);                 \
+  }                                                                                              \
+  __global__ __launch_bounds__(64 * WGM * WGN) void lf_fp8_w8a16_gate_up_b128_m128_n##BN(        \
+      const int32_t *counts, const uint16_t *x, const uint8_t *wg, const uint8_t *wu,            \
+      uint16_t *h, uint8_t *ws) {                                                                \
+    __shared__ __attribute__((aligned(1024))) uint8_t smem[w16g::Tile<BN, WGM, WGN, NSA, NSB>::kSmem]; \
+    w16g::w8a16_gemm_kernel<BN, WGM, WGN, NSA, NSB, 2, false, NoWait, true>(smem, counts, x, wg, wu, wu, h, \
+                                                                            ws);                 \
+  }
+
+LF_W16_GEMM_B128_ENTRIES(64, 4, 2, 4, 2)
+LF_W16_GEMM_B128_ENTRIES(128, 4, 2, 2, 4)
 
 // One-launch GatedMlp for profiles of 65..128 rows, any H and I the forms
 // divide: gate/up on the n128 tiles (one K-slice), down on n128 or n64 (the

@@ -92,13 +92,23 @@ bool w8a16_split(int64_t n, int64_t k, int32_t max_tokens, W8a16Split *out) {
   return true;
 }
 
-// Block-scaled W8A16 entries (_B128): the column-group form for every
-// profile (also <= 16 rows), split as above, with at least enough slices
-// that each holds <= 128 k-tiles (the block scales of a slice are staged in
-// LDS, kW16BlockSliceKT in kernels/w8a16.hip).
+// Block-scaled W8A16 entries (_B128): profiles of 65..128 rows take the
+// LDS-tiled GEMM form with the per-channel entries' tile and split
+// (w8a16_gemm below, the _b128_m128_n{BN} symbols; every block-scaled width
+// is a multiple of 128, so a 16-column fragment lies in one 128-row scale
+// block); every other profile (also <= 16 rows) the column-group form,
+// split as above, with at least enough slices that each holds <= 128
+// k-tiles (the block scales of a slice are staged in LDS, kW16BlockSliceKT
+// in kernels/w8a16.hip).
 bool w8a16_b128_entry(int32_t e) {
   return e == LF_FP8_ENTRY_W8A16_DENSE_B128 || e == LF_FP8_ENTRY_W8A16_QKV_B128 ||
          e == LF_FP8_ENTRY_W8A16_GATE_UP_B128;
+}
+// The per-channel entry whose tile and split rules a block-scaled one shares.
+int32_t w8a16_channel_entry(int32_t e) {
+  return e == LF_FP8_ENTRY_W8A16_DENSE_B128 ? LF_FP8_ENTRY_W8A16_DENSE
+         : e == LF_FP8_ENTRY_W8A16_QKV_B128 ? LF_FP8_ENTRY_W8A16_QKV
+                                             : LF_FP8_ENTRY_W8A16_GATE_UP;
 }
 bool w8a16_b128_split(int64_t n, int64_t k, int32_t max_tokens, W8a16Split *out) {
   if (n % 128 != 0 || k % 128 != 0 || !w8a16_split(n, k, max_tokens, out)) return false;
@@ -536,6 +546,8 @@ static int64_t w8a16_workspace(int32_t entry, int64_t n, int64_t k, int64_t nq, 
         !w8a16_b128_split(n, k, max_tokens, &sp)) {
       return -1;
     }
+    W8a16Gemm gm;
+    if (w8a16_gemm(w8a16_channel_entry(entry), n, k, max_tokens, &gm)) return w8a16_gemm_workspace(gm);
     if (sp.split == 1) return 256;
     const int64_t nw = entry == LF_FP8_ENTRY_W8A16_GATE_UP_B128 ? 2 : 1;
     return align_up(sp.split * (n / 16) * nw * sp.mt * 1024, 256) + align_up(sp.groups * 4, 256);
@@ -751,6 +763,14 @@ static int32_t launch_geometry(int32_t entry, int64_t n, int64_t k, int64_t nq, 
       const char *op = entry == LF_FP8_ENTRY_W8A16_DENSE_B128 ? "dense"
                        : entry == LF_FP8_ENTRY_W8A16_QKV_B128 ? "qkv"
                                                               : "gate_up";
+      W8a16Gemm gm;
+      if (w8a16_gemm(w8a16_channel_entry(entry), n, k, max_tokens, &gm)) {
+        std::snprintf(buffer, sizeof(buffer), "lf_fp8_w8a16_%s_b128_m128_n%d", op, gm.bn);
+        name = buffer;
+        gx = static_cast<int32_t>(gm.blocks_n * gm.split);
+        bx = 512;
+        break;
+      }
       std::snprintf(buffer, sizeof(buffer), "lf_fp8_w8a16_%s_b128_m%d", op, 16 * sp.mt);
       name = buffer;
       gx = static_cast<int32_t>(sp.groups * sp.split);

@@ -273,7 +273,9 @@ def test_one_launch_w8a8_geometry_and_workspace():
 
 
 def test_block_scaled_geometry_and_workspace():
-    """The _B128 entries. W8A16: the column-group form for every profile
+    """The _B128 entries. W8A16: profiles of 65..128 rows the LDS-tiled
+    GEMM form with the per-channel entry's tile, split and workspace (the
+    _b128_m128_n{BN} symbols); the column-group form for every other profile
     (also <= 16 rows), the per-channel split raised so that a slice holds at
     most 128 k-tiles, the per-channel workspace formula. W8A8: 256 group-
     quantizer blocks then 128 x 128 tiles (64 h-columns for gate/up), 256
@@ -281,10 +283,19 @@ def test_block_scaled_geometry_and_workspace():
     (each part 256-aligned). GatedMlp: four steps on 128-row bands."""
     lib = _abi.lib()
     al = lambda v: -(-v // 256) * 256  # noqa: E731
+    channel = {_abi.ENTRY_W8A16_DENSE_B128: _abi.ENTRY_W8A16_DENSE,
+               _abi.ENTRY_W8A16_QKV_B128: _abi.ENTRY_W8A16_QKV,
+               _abi.ENTRY_W8A16_GATE_UP_B128: _abi.ENTRY_W8A16_GATE_UP}
     for entry, op in [(_abi.ENTRY_W8A16_DENSE_B128, "dense"), (_abi.ENTRY_W8A16_QKV_B128, "qkv"),
                       (_abi.ENTRY_W8A16_GATE_UP_B128, "gate_up")]:
+        for n, k, m in [(4096, 14336, 128), (6144, 4096, 100), (4096, 4096, 65), (1024, 32768, 128)]:
+            d, sym = fp8.launch_geometry(entry, n, k, m)
+            d0, sym0 = fp8.launch_geometry(channel[entry], n, k, m)
+            assert sym0.startswith(f"lf_fp8_w8a16_{op}_m128_n"), sym0
+            assert sym == sym0.replace(f"_{op}_", f"_{op}_b128_") and d == d0, (sym, d, sym0, d0)
+            assert fp8.w8a16_workspace_bytes(entry, n, k, m) == fp8.w8a16_workspace_bytes(channel[entry], n, k, m)
         for n, k, m, mt in [(4096, 4096, 1, 1), (6144, 4096, 32, 2), (14336, 4096, 64, 4),
-                            (4096, 14336, 128, 8), (1024, 32768, 16, 1)]:
+                            (1024, 32768, 16, 1)]:
             d, sym = fp8.launch_geometry(entry, n, k, m)
             assert sym == f"lf_fp8_w8a16_{op}_b128_m{16 * mt}" and d.block == (256, 1, 1)
             groups = -(-(n // 16) // 4)
