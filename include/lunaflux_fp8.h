@@ -177,7 +177,8 @@ enum lf_fp8_entry {
   LF_FP8_ENTRY_W8A8_DENSE_B128 = 18,
   LF_FP8_ENTRY_W8A8_QKV_B128 = 19,
   LF_FP8_ENTRY_W8A8_GATE_UP_B128 = 20,
-  LF_FP8_ENTRY_W8A8_GATED_MLP_B128 = 21
+  LF_FP8_ENTRY_W8A8_GATED_MLP_B128 = 21,
+  LF_FP8_ENTRY_W8A16_GATED_MLP_B128 = 22
 };
 
 /* Block-scaled projections (checkpoints whose weights carry weight_scale_inv
@@ -200,6 +201,16 @@ enum lf_fp8_entry {
  *      in one launch (group quantizer, gate/up + SwiGLU, group quantizer of
  *      h, down), lunaflux_fp8_gated_mlp_geometry / _workspace_bytes with
  *      LF_FP8_ENTRY_W8A8_GATED_MLP_B128.
+ *  W8A16 shape-specialized (Llama-3-8B widths, profiles of <= 32 rows, as
+ *      the per-channel ones): lf_fp8_w8a16_{dense,gate_up}_b128_k{K}_mM,
+ *      lf_fp8_w8a16_qkv_b128_k4096_q4096_kv1024_mM (picked by
+ *      lunaflux_fp8_qkv_launch_geometry; without the split,
+ *      lunaflux_fp8_w8a16_workspace_bytes sizes the QKV_B128 workspace for
+ *      every entry of that width). W8A16 GatedMlp in one launch with
+ *      LF_FP8_ENTRY_W8A16_GATED_MLP_B128 (the per-channel one-launch forms:
+ *      lf_fp8_w8a16_gated_mlp_b128_h4096_i14336_m{16,32} and
+ *      lf_fp8_w8a16_gated_mlp_b128_m128_n128_n{64,128}; workspace and error
+ *      word as LF_FP8_ENTRY_W8A16_GATED_MLP).
  * The geometry functions take the _B128 entries as the per-channel ones;
  * admission requires block scales for them (and channel scales for every
  * other dense entry). */

@@ -64,6 +64,7 @@ ENTRY_W8A8_DENSE_B128 = 18
 ENTRY_W8A8_QKV_B128 = 19
 ENTRY_W8A8_GATE_UP_B128 = 20
 ENTRY_W8A8_GATED_MLP_B128 = 21
+ENTRY_W8A16_GATED_MLP_B128 = 22
 LF_FP8_GATED_MLP_ERROR_OFFSET_FROM_END = 128
 LF_FP8_AQ_ERROR_OFFSET = 0
 

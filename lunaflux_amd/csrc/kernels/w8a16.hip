@@ -562,17 +562,36 @@ __device__ __forceinline__ void w8a16_tile_kernel(const int32_t *counts, const u
 // The first 32 header bytes are read in one go and compared without
 // short-circuits, so the scalar loads issue together (a chain of && made the
 // compiler fetch field by field, each after the previous comparison).
-template <int NW, int K>
+template <int NW, int K, uint32_t SCALE = kScalePerChannel>
 LF_DEVICE bool fixed_shape_ok(const uint8_t *const (&region)[NW], int region_rows) {
   uint32_t bad = 0;
 #pragma unroll
   for (int i = 0; i < NW; ++i) {
     const u32x4 *h = reinterpret_cast<const u32x4 *>(region[i]);
     const u32x4 a = h[0], b = h[1];  // magic, version, layout, scale_mode | rows, columns, experts
-    bad |= (a.x ^ kWeightMagic) | (a.w ^ kScalePerChannel) |
+    bad |= (a.x ^ kWeightMagic) | (a.w ^ SCALE) |
            (b.x ^ static_cast<uint32_t>(region_rows)) | (b.y ^ static_cast<uint32_t>(K)) | (b.z ^ 1u);
   }
   return bad == 0;
+}
+
+// Block scales of the specialized forms (BLOCK): the scales of a region
+// follow its tiles (the offset the header gives, computed from the compiled
+// shape so no header read sits before the loads), [rows / 128][K / 128]. A
+// wave's 16-column tile t lies in 128-row block t / 8; lane l of the
+// returned value holds the scale of k-tile kt0 + l for l < n (n <= 64), so
+// k-step k takes it with one readlane.
+template <int K>
+LF_DEVICE float block_scale_lanes(const uint8_t *region, int region_rows, int t, int kt0, int n) {
+  constexpr int KT = K / 128;
+  const float *s = reinterpret_cast<const float *>(region + kWeightHeaderBytes +
+                                                   static_cast<uint64_t>(region_rows) * K) +
+                   static_cast<uint64_t>(t >> 3) * KT + kt0;
+  const int lane = threadIdx.x & 63;
+  return lane < n ? s[lane] : 0.0f;
+}
+LF_DEVICE float lane_value(float v, int l) {
+  return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), l));
 }
 
 // ---------------------------------------------------------------------------
@@ -594,7 +613,11 @@ LF_DEVICE bool fixed_shape_ok(const uint8_t *const (&region)[NW], int region_row
 // refills makes the compiler fall back to vmcnt(0) at every step, which
 // serializes the ring.) The KS partial tiles are summed in LDS in wave order.
 // ---------------------------------------------------------------------------
-template <int K, int KS, int MT, int MODE, int DW, int DX, int NQ = 0, int NKV = 0, int SLOTS = 2>
+// BLOCK: weights with 128 x 128 block scales; each k-tile's MFMAs run into
+// fresh fragments that are multiplied by the k-tile's block scale and added
+// to the sums (the fold of w8a16_kernel's BLOCK form), no channel scale.
+template <int K, int KS, int MT, int MODE, int DW, int DX, int NQ = 0, int NKV = 0, int SLOTS = 2,
+          bool BLOCK = false>
 __device__ __forceinline__ void w8a16_fixed_kernel(const int32_t *counts, const uint16_t *x, const uint8_t *w0,
                                    const uint8_t *w1, const uint8_t *w2, uint16_t *y) {
   constexpr int NW = MODE == 2 ? 2 : 1;
@@ -649,16 +672,22 @@ __device__ __forceinline__ void w8a16_fixed_kernel(const int32_t *counts, const 
   for (int i = 0; i < NW; ++i) strip[i] = region[i] + tile_base;
 
   // Channel scales of the column this thread finishes in the epilogue:
-  // per-channel scales follow the N x K tile block.
+  // per-channel scales follow the N x K tile block. BLOCK: the multiplier is
+  // 1, and bsv[i] holds this wave's KTW k-tile scales, one per lane.
   const int ec = (threadIdx.x >> 2) & 15;
-  float sc[NW];
+  const int kt0 = wave * KTW;
+  float sc[NW], bsv[NW];
 #pragma unroll
   for (int i = 0; i < NW; ++i) {
-    sc[i] = reinterpret_cast<const float *>(
-        region[i] + kWeightHeaderBytes + static_cast<uint64_t>(region_rows) * K)[t * 16 + ec];
+    if constexpr (BLOCK) {
+      sc[i] = 1.0f;
+      bsv[i] = block_scale_lanes<K>(region[i], region_rows, t, kt0, KTW);
+    } else {
+      sc[i] = reinterpret_cast<const float *>(
+          region[i] + kWeightHeaderBytes + static_cast<uint64_t>(region_rows) * K)[t * 16 + ec];
+    }
   }
 
-  const int kt0 = wave * KTW;
   uint4 b[EW][NW][2];
 #pragma unroll
   for (int d = 0; d < EW; ++d) load_tiles<NW>(strip, kt0 + d, lane, b[d]);
@@ -669,7 +698,9 @@ __device__ __forceinline__ void w8a16_fixed_kernel(const int32_t *counts, const 
 
   // A region whose header disagrees with the compiled shape (a wrong weight
   // bound to this entry) counts as no live rows: nothing is stored.
-  const int M = live_rows(counts, 16 * MT) & -static_cast<int>(fixed_shape_ok<NW, K>(region, region_rows));
+  const int M = live_rows(counts, 16 * MT) &
+                -static_cast<int>(fixed_shape_ok<NW, K, BLOCK ? kScaleBlock128 : kScalePerChannel>(
+                    region, region_rows));
   // Activation loads are row-coalesced: instruction q gives lane l row
   // 4 q + l / 16, 16-byte chunk l % 16 of the k-tile (rows past M re-read row
   // M - 1; their outputs are never stored. M == 0 stores nothing).
@@ -704,6 +735,7 @@ __device__ __forceinline__ void w8a16_fixed_kernel(const int32_t *counts, const 
     __builtin_amdgcn_sched_barrier(0);
     if constexpr (k + EX < KTW) load_a(k + EX, a[k % EX]);
     __builtin_amdgcn_sched_barrier(0);
+    f32x4 part[BLOCK ? MT : 1][NW];  // BLOCK: this k-tile's products
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
       bf16x8 af[MT];
@@ -716,7 +748,23 @@ __device__ __forceinline__ void w8a16_fixed_kernel(const int32_t *counts, const 
         const bf16x8 bf = weight_fragment(b[k % EW][i], j);
 #pragma unroll
         for (int mt = 0; mt < MT; ++mt) {
-          acc[mt][i] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(af[mt], bf, acc[mt][i], 0, 0, 0);
+          if constexpr (BLOCK) {
+            part[mt][i] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
+                af[mt], bf, j == 0 ? f32x4{0.f, 0.f, 0.f, 0.f} : part[mt][i], 0, 0, 0);
+          } else {
+            acc[mt][i] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(af[mt], bf, acc[mt][i], 0, 0, 0);
+          }
+        }
+      }
+    }
+    if constexpr (BLOCK) {
+#pragma unroll
+      for (int i = 0; i < NW; ++i) {
+        const float sb = lane_value(bsv[i], k);
+#pragma unroll
+        for (int mt = 0; mt < MT; ++mt) {
+          acc[mt][i] += part[mt][i] * sb;
+          asm volatile("" : "+v"(acc[mt][i]));  // (in the MFMAs' block: w8a16_kernel)
         }
       }
     }
@@ -785,8 +833,9 @@ struct NoWait {
 // with it (down 17.8 -> 18.4 us), so they keep the plain order. The sums
 // run in a different k order, so results differ from the plain order by
 // fp32 rounding.
+// BLOCK: 128 x 128 block scales, folded per k-tile as in w8a16_fixed_kernel.
 template <int K, int S, int WAVES, int MT, int MODE, int DW, int DX, int NQ = 0, int NKV = 0,
-          class Wait = NoWait, bool COHERENT_OUT = false, bool KROT = false>
+          class Wait = NoWait, bool COHERENT_OUT = false, bool KROT = false, bool BLOCK = false>
 __device__ __forceinline__ void w8a16_fixed_group_kernel(const int32_t *counts, const uint16_t *x,
                                          const uint8_t *w0, const uint8_t *w1, const uint8_t *w2,
                                          uint16_t *y, uint8_t *ws, int bid = -1, int nblocks = -1,
@@ -848,11 +897,19 @@ __device__ __forceinline__ void w8a16_fixed_group_kernel(const int32_t *counts, 
   const uint8_t *strip[NW];
 #pragma unroll
   for (int i = 0; i < NW; ++i) strip[i] = region[i] + tile_base;
-  float sc[NW];
+  // BLOCK: the multiplier is 1, and bsv[i] holds this slice's NKT k-tile
+  // scales, one per lane (NKT <= 64).
+  static_assert(!BLOCK || NKT <= 64, "a slice's block scales fit one register");
+  float sc[NW], bsv[NW];
 #pragma unroll
   for (int i = 0; i < NW; ++i) {
-    sc[i] = reinterpret_cast<const float *>(
-        region[i] + kWeightHeaderBytes + static_cast<uint64_t>(region_rows) * K)[t * 16 + r];
+    if constexpr (BLOCK) {
+      sc[i] = 1.0f;
+      bsv[i] = block_scale_lanes<K>(region[i], region_rows, t, kt0, NKT);
+    } else {
+      sc[i] = reinterpret_cast<const float *>(
+          region[i] + kWeightHeaderBytes + static_cast<uint64_t>(region_rows) * K)[t * 16 + r];
+    }
   }
 
   uint4 b[EW][NW][2];
@@ -863,7 +920,9 @@ __device__ __forceinline__ void w8a16_fixed_group_kernel(const int32_t *counts, 
   // A region whose header disagrees with the compiled shape counts as no
   // live rows: nothing is stored, and the block still takes part in the
   // split-K arrival count, so the counters stay consistent.
-  const int M = live_rows(counts, 16 * MT) & -static_cast<int>(fixed_shape_ok<NW, K>(region, region_rows));
+  const int M = live_rows(counts, 16 * MT) &
+                -static_cast<int>(fixed_shape_ok<NW, K, BLOCK ? kScaleBlock128 : kScalePerChannel>(
+                    region, region_rows));
   const uint16_t *xsrc[XPW];
   int xdst[XPW];
 #pragma unroll
@@ -901,6 +960,7 @@ __device__ __forceinline__ void w8a16_fixed_group_kernel(const int32_t *counts, 
     // fragment reads every wave consumed before this barrier.)
     asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
     __builtin_amdgcn_sched_barrier(0);
+    f32x4 part[BLOCK ? MT : 1][NW];  // BLOCK: this k-tile's products
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
       bf16x8 af[MT];
@@ -913,7 +973,23 @@ __device__ __forceinline__ void w8a16_fixed_group_kernel(const int32_t *counts, 
         const bf16x8 bf = weight_fragment(b[k % EW][i], j);
 #pragma unroll
         for (int mt = 0; mt < MT; ++mt) {
-          acc[mt][i] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(af[mt], bf, acc[mt][i], 0, 0, 0);
+          if constexpr (BLOCK) {
+            part[mt][i] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
+                af[mt], bf, j == 0 ? f32x4{0.f, 0.f, 0.f, 0.f} : part[mt][i], 0, 0, 0);
+          } else {
+            acc[mt][i] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(af[mt], bf, acc[mt][i], 0, 0, 0);
+          }
+        }
+      }
+    }
+    if constexpr (BLOCK) {
+#pragma unroll
+      for (int i = 0; i < NW; ++i) {
+        const float sb = lane_value(bsv[i], kr(k));
+#pragma unroll
+        for (int mt = 0; mt < MT; ++mt) {
+          acc[mt][i] += part[mt][i] * sb;
+          asm volatile("" : "+v"(acc[mt][i]));  // (in the MFMAs' block: w8a16_kernel)
         }
       }
     }
@@ -976,8 +1052,9 @@ struct SliceWait {
   }
 };
 
+// BLOCK: all three weights carry 128 x 128 block scales.
 template <int H, int I, int MT, int GU_W, int GU_DW, int GU_DX, int DN_S, int DN_W, int DN_DW,
-          int DN_DX>
+          int DN_DX, bool BLOCK = false>
 struct GatedMlpFixed {
   static constexpr int kG1 = I / 16 / GU_W;
   static constexpr int kG2 = H / 16 / DN_W * DN_S;
@@ -1004,7 +1081,7 @@ struct GatedMlpFixed {
     int *error = sync + 5 * phase::kLineInts;
     const int b = static_cast<int>(blockIdx.x);
     if (b < kG1) {
-      w8a16_fixed_group_kernel<H, 1, GU_W, MT, 2, GU_DW, GU_DX, 0, 0, NoWait, true, true>(
+      w8a16_fixed_group_kernel<H, 1, GU_W, MT, 2, GU_DW, GU_DX, 0, 0, NoWait, true, true, BLOCK>(
           counts, x, wg, wu, wu, h, ws_down, b, kG1);
       asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
       __syncthreads();
@@ -1015,7 +1092,7 @@ struct GatedMlpFixed {
       return;
     }
     const SliceWait wait{sync, kSliceCols / (GU_W * 16), error, &flag};
-    w8a16_fixed_group_kernel<I, DN_S, DN_W, MT, 0, DN_DW, DN_DX, 0, 0, SliceWait>(
+    w8a16_fixed_group_kernel<I, DN_S, DN_W, MT, 0, DN_DW, DN_DX, 0, 0, SliceWait, false, false, BLOCK>(
         counts, h, wd, wd, wd, y, ws_down, b - kG1, kG2, wait);
     if (threadIdx.x == 0) {
       const int before = __hip_atomic_fetch_add(done, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
@@ -1173,5 +1250,61 @@ LF_W16_FIXED_DENSE_WIDE_G(4096, 128, 8, 1, 8, 2, 1)
 
 LF_W16_GATED_MLP(16, 1, 4, 4, 2, 4, 4, 6, 2)
 LF_W16_GATED_MLP(32, 2, 4, 3, 2, 4, 4, 6, 2)
+
+// The specialized entries over weights with 128 x 128 block scales
+// (lf_fp8_w8a16_{op}_b128_k..., lf_fp8_w8a16_gated_mlp_b128_h4096_i14336_mM):
+// the same forms and parameters with the per-k-tile fold.
+#define LF_W16_FIXED_B128_DENSE_T1(KK, M, MT, KS, DW, DX, SLOTS)                                \
+  __global__ __launch_bounds__(KS * 64) void lf_fp8_w8a16_dense_b128_k##KK##_m##M(           \
+      const int32_t *counts, const uint16_t *x, const uint8_t *w, uint16_t *y, uint8_t *) {  \
+    w8a16_fixed_kernel<KK, KS, MT, 0, DW, DX, 0, 0, SLOTS, true>(counts, x, w, w, w, y);      \
+  }
+#define LF_W16_FIXED_B128_QKV_T1(KK, NQ, NKV, M, MT, KS, DW, DX, SLOTS)                         \
+  __global__ __launch_bounds__(KS * 64) void                                                 \
+      lf_fp8_w8a16_qkv_b128_k##KK##_q##NQ##_kv##NKV##_m##M(                                  \
+          const int32_t *counts, const uint16_t *x, const uint8_t *wq, const uint8_t *wk,    \
+          const uint8_t *wv, uint16_t *y, uint8_t *) {                                       \
+    w8a16_fixed_kernel<KK, KS, MT, 1, DW, DX, NQ, NKV, SLOTS, true>(counts, x, wq, wk, wv, y); \
+  }
+#define LF_W16_FIXED_B128_QKV_G(KK, NQ, NKV, M, MT, S, W, DW, DX)                               \
+  __global__ __launch_bounds__(W * 64) void                                                  \
+      lf_fp8_w8a16_qkv_b128_k##KK##_q##NQ##_kv##NKV##_m##M(                                  \
+          const int32_t *counts, const uint16_t *x, const uint8_t *wq, const uint8_t *wk,    \
+          const uint8_t *wv, uint16_t *y, uint8_t *ws) {                                     \
+    w8a16_fixed_group_kernel<KK, S, W, MT, 1, DW, DX, NQ, NKV, NoWait, false, false, true>(    \
+        counts, x, wq, wk, wv, y, ws);                                                       \
+  }
+#define LF_W16_FIXED_B128_DENSE_G(KK, M, MT, S, W, DW, DX)                                      \
+  __global__ __launch_bounds__(W * 64) void lf_fp8_w8a16_dense_b128_k##KK##_m##M(            \
+      const int32_t *counts, const uint16_t *x, const uint8_t *w, uint16_t *y, uint8_t *ws) { \
+    w8a16_fixed_group_kernel<KK, S, W, MT, 0, DW, DX, 0, 0, NoWait, false, false, true>(       \
+        counts, x, w, w, w, y, ws);                                                          \
+  }
+#define LF_W16_FIXED_B128_GATE_UP_G(KK, M, MT, S, W, DW, DX)                                    \
+  __global__ __launch_bounds__(W * 64) void lf_fp8_w8a16_gate_up_b128_k##KK##_m##M(          \
+      const int32_t *counts, const uint16_t *x, const uint8_t *wg, const uint8_t *wu,        \
+      uint16_t *h, uint8_t *ws) {                                                            \
+    w8a16_fixed_group_kernel<KK, S, W, MT, 2, DW, DX, 0, 0, NoWait, false, S == 1, true>(      \
+        counts, x, wg, wu, wu, h, ws);                                                       \
+  }
+#define LF_W16_GATED_MLP_B128(M, MT, GU_W, GU_DW, GU_DX, DN_S, DN_W, DN_DW, DN_DX)                \
+  __global__ __launch_bounds__(64 * GU_W) void lf_fp8_w8a16_gated_mlp_b128_h4096_i14336_m##M(   \
+      const int32_t *counts, const uint16_t *x, const uint8_t *wg, const uint8_t *wu,            \
+      const uint8_t *wd, uint16_t *y, uint8_t *ws) {                                             \
+    static_assert(GU_W == DN_W, "one block size");                                              \
+    GatedMlpFixed<4096, 14336, MT, GU_W, GU_DW, GU_DX, DN_S, DN_W, DN_DW, DN_DX, true>::run(     \
+        counts, x, wg, wu, wd, y, ws);                                                           \
+  }
+
+LF_W16_FIXED_B128_DENSE_T1(4096, 16, 1, 8, 4, 2, 2)
+LF_W16_FIXED_B128_DENSE_T1(4096, 32, 2, 8, 4, 1, 1)
+LF_W16_FIXED_B128_DENSE_T1(14336, 16, 1, 8, 6, 2, 2)
+LF_W16_FIXED_B128_DENSE_G(14336, 32, 2, 4, 4, 6, 2)
+LF_W16_FIXED_B128_QKV_T1(4096, 4096, 1024, 16, 1, 8, 4, 2, 2)
+LF_W16_FIXED_B128_QKV_G(4096, 4096, 1024, 32, 2, 4, 8, 4, 2)
+LF_W16_FIXED_B128_GATE_UP_G(4096, 16, 1, 1, 2, 4, 2)
+LF_W16_FIXED_B128_GATE_UP_G(4096, 32, 2, 1, 4, 3, 2)
+LF_W16_GATED_MLP_B128(16, 1, 4, 4, 2, 4, 4, 6, 2)
+LF_W16_GATED_MLP_B128(32, 2, 4, 3, 2, 4, 4, 6, 2)
 
 }  // extern "C"

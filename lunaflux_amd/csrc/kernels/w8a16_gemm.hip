@@ -431,7 +431,9 @@ __device__ __forceinline__ void w8a16_gemm_kernel(uint8_t *smem, const int32_t *
 // Workspace: h [128][I] bf16 | the down GEMM's split-K partials and arrival
 // counters | sync (128 S + 256 bytes): slice counter s at +128 s, done at
 // +128 S, error at +128 S + 128 (the last line but one).
-template <int GU_BN, int DN_BN, int WGM, int WGN, int GU_NSA, int GU_NSB, int DN_NSA, int DN_NSB>
+// BLOCK: all three weights carry 128 x 128 block scales.
+template <int GU_BN, int DN_BN, int WGM, int WGN, int GU_NSA, int GU_NSB, int DN_NSA, int DN_NSB,
+          bool BLOCK = false>
 struct GatedMlpGemm {
   using GU = Tile<GU_BN, WGM, WGN, GU_NSA, GU_NSB>;
   using DN = Tile<DN_BN, WGM, WGN, DN_NSA, DN_NSB>;
@@ -440,7 +442,8 @@ struct GatedMlpGemm {
                             const uint8_t *wu, const uint8_t *wd, uint16_t *y, uint8_t *ws) {
     __shared__ __attribute__((aligned(1024))) uint8_t smem[kSmem];
     __shared__ phase::Flag flag;
-    if (!dense_regions_ok<2>(wg, wu, wu) || !dense_regions_ok<0>(wd, wd, wd)) return;
+    constexpr uint32_t kScale = BLOCK ? kScaleBlock128 : kScalePerChannel;
+    if (!dense_regions_ok<2, kScale>(wg, wu, wu) || !dense_regions_ok<0, kScale>(wd, wd, wd)) return;
     const int H = static_cast<int>(header_of(wg).columns), I = static_cast<int>(header_of(wg).rows);
     if (static_cast<int>(header_of(wd).columns) != I || static_cast<int>(header_of(wd).rows) != H) return;
     const int g1 = I / (GU_BN / 2);
@@ -466,8 +469,8 @@ struct GatedMlpGemm {
     };
     const int b = static_cast<int>(blockIdx.x);
     if (b < g1) {
-      w8a16_gemm_kernel<GU_BN, WGM, WGN, GU_NSA, GU_NSB, 2, true>(smem, counts, x, wg, wu, wu, h, ws_down, b,
-                                                                  g1);
+      w8a16_gemm_kernel<GU_BN, WGM, WGN, GU_NSA, GU_NSB, 2, true, NoWait, BLOCK>(smem, counts, x, wg, wu, wu,
+                                                                                 h, ws_down, b, g1);
       phase::signal(sync + phase::kLineInts * slice_of(b * (GU_BN / 2) / 128));
       return;
     }
@@ -475,8 +478,8 @@ struct GatedMlpGemm {
       const int target = (KT * (sl + 1) / S - KT * sl / S) * (128 / (GU_BN / 2));
       return phase::wait_for(sync + phase::kLineInts * sl, target, error, flag);
     };
-    w8a16_gemm_kernel<DN_BN, WGM, WGN, DN_NSA, DN_NSB, 0>(smem, counts, h, wd, wd, wd, y, ws_down, b - g1, g2,
-                                                          gate);
+    w8a16_gemm_kernel<DN_BN, WGM, WGN, DN_NSA, DN_NSB, 0, false, decltype(gate), BLOCK>(
+        smem, counts, h, wd, wd, wd, y, ws_down, b - g1, g2, gate);
     __syncthreads();
     if (threadIdx.x == 0) {
       const int before = __hip_atomic_fetch_add(done, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
@@ -555,5 +558,16 @@ LF_W16_GEMM_B128_ENTRIES(128, 4, 2, 2, 4)
 
 LF_W16_GEMM_GATED_MLP(128, 2, 4)
 LF_W16_GEMM_GATED_MLP(64, 4, 2)
+
+// The same over weights with 128 x 128 block scales.
+#define LF_W16_GEMM_GATED_MLP_B128(DN_BN, DN_NSA, DN_NSB)                                        \
+  __global__ __launch_bounds__(512) void lf_fp8_w8a16_gated_mlp_b128_m128_n128_n##DN_BN(          \
+      const int32_t *counts, const uint16_t *x, const uint8_t *wg, const uint8_t *wu,            \
+      const uint8_t *wd, uint16_t *y, uint8_t *ws) {                                             \
+    w16g::GatedMlpGemm<128, DN_BN, 4, 2, 2, 4, DN_NSA, DN_NSB, true>::run(counts, x, wg, wu, wd, y, ws); \
+  }
+
+LF_W16_GEMM_GATED_MLP_B128(128, 2, 4)
+LF_W16_GEMM_GATED_MLP_B128(64, 4, 2)
 
 }  // extern "C"

@@ -153,6 +153,17 @@ constexpr W8a16Fixed kW8a16Fixed[] = {
      "lf_fp8_w8a16_qkv_k4096_q4096_kv1024_m32"},
     {LF_FP8_ENTRY_W8A16_GATE_UP, 4096, 0, 0, 1, true, 2, 1, "lf_fp8_w8a16_gate_up_k4096_m16"},
     {LF_FP8_ENTRY_W8A16_GATE_UP, 4096, 0, 0, 2, true, 4, 1, "lf_fp8_w8a16_gate_up_k4096_m32"},
+    // the same forms over 128 x 128 block-scaled weights (no wide entries)
+    {LF_FP8_ENTRY_W8A16_DENSE_B128, 4096, 0, 0, 1, false, 8, 1, "lf_fp8_w8a16_dense_b128_k4096_m16"},
+    {LF_FP8_ENTRY_W8A16_DENSE_B128, 4096, 0, 0, 2, false, 8, 1, "lf_fp8_w8a16_dense_b128_k4096_m32"},
+    {LF_FP8_ENTRY_W8A16_DENSE_B128, 14336, 0, 0, 1, false, 8, 1, "lf_fp8_w8a16_dense_b128_k14336_m16"},
+    {LF_FP8_ENTRY_W8A16_DENSE_B128, 14336, 0, 0, 2, true, 4, 4, "lf_fp8_w8a16_dense_b128_k14336_m32"},
+    {LF_FP8_ENTRY_W8A16_QKV_B128, 4096, 4096, 1024, 1, false, 8, 1,
+     "lf_fp8_w8a16_qkv_b128_k4096_q4096_kv1024_m16"},
+    {LF_FP8_ENTRY_W8A16_QKV_B128, 4096, 4096, 1024, 2, true, 8, 4,
+     "lf_fp8_w8a16_qkv_b128_k4096_q4096_kv1024_m32"},
+    {LF_FP8_ENTRY_W8A16_GATE_UP_B128, 4096, 0, 0, 1, true, 2, 1, "lf_fp8_w8a16_gate_up_b128_k4096_m16"},
+    {LF_FP8_ENTRY_W8A16_GATE_UP_B128, 4096, 0, 0, 2, true, 4, 1, "lf_fp8_w8a16_gate_up_b128_k4096_m32"},
 };
 
 // The specialized entry for (entry, N, K, Q / K-V split, profile), or null.
@@ -164,7 +175,8 @@ const W8a16Fixed *w8a16_fixed(int32_t entry, int64_t n, int64_t k, int64_t nq, i
   const int mt = max_tokens <= 16 ? 1 : max_tokens <= 32 ? 2 : max_tokens <= 64 ? 4 : 8;
   for (const W8a16Fixed &f : kW8a16Fixed) {
     if (f.entry != entry || f.k != k || f.mt != mt || n < f.min_n) continue;
-    if (entry == LF_FP8_ENTRY_W8A16_QKV && (f.nq != nq || f.nkv != nkv || n != nq + 2 * nkv)) {
+    if ((entry == LF_FP8_ENTRY_W8A16_QKV || entry == LF_FP8_ENTRY_W8A16_QKV_B128) &&
+        (f.nq != nq || f.nkv != nkv || n != nq + 2 * nkv)) {
       continue;
     }
     if (f.group && (n / 16) % f.waves != 0) continue;
@@ -175,7 +187,7 @@ const W8a16Fixed *w8a16_fixed(int32_t entry, int64_t n, int64_t k, int64_t nq, i
 
 int64_t w8a16_fixed_workspace(const W8a16Fixed &f, int64_t n) {
   if (!f.group || f.split == 1) return 256;
-  const int64_t nw = f.entry == LF_FP8_ENTRY_W8A16_GATE_UP ? 2 : 1;
+  const int64_t nw = f.entry == LF_FP8_ENTRY_W8A16_GATE_UP || f.entry == LF_FP8_ENTRY_W8A16_GATE_UP_B128 ? 2 : 1;
   const int64_t groups = n / 16 / f.waves;
   return align_up(f.split * (n / 16) * nw * f.mt * 1024, 256) + align_up(groups * 4, 256);
 }
@@ -234,17 +246,25 @@ struct W8a16Gated {
   int64_t hidden, inter;
   int mt, waves, down_split;
   const char *symbol;
+  bool block = false;  // 128 x 128 block-scaled weights (LF_FP8_ENTRY_W8A16_GATED_MLP_B128)
 };
 constexpr W8a16Gated kW8a16Gated[] = {
     {4096, 14336, 1, 4, 4, "lf_fp8_w8a16_gated_mlp_h4096_i14336_m16"},
     {4096, 14336, 2, 4, 4, "lf_fp8_w8a16_gated_mlp_h4096_i14336_m32"},
+    {4096, 14336, 1, 4, 4, "lf_fp8_w8a16_gated_mlp_b128_h4096_i14336_m16", true},
+    {4096, 14336, 2, 4, 4, "lf_fp8_w8a16_gated_mlp_b128_h4096_i14336_m32", true},
 };
 
+bool w8a16_gated_entry(int32_t entry) {
+  return entry == LF_FP8_ENTRY_W8A16_GATED_MLP || entry == LF_FP8_ENTRY_W8A16_GATED_MLP_B128;
+}
+
 const W8a16Gated *w8a16_gated(int32_t entry, int64_t hidden, int64_t inter, int32_t max_tokens) {
-  if (entry != LF_FP8_ENTRY_W8A16_GATED_MLP || max_tokens <= 0 || max_tokens > 32) return nullptr;
+  if (!w8a16_gated_entry(entry) || max_tokens <= 0 || max_tokens > 32) return nullptr;
   const int mt = max_tokens <= 16 ? 1 : 2;
+  const bool block = entry == LF_FP8_ENTRY_W8A16_GATED_MLP_B128;
   for (const W8a16Gated &g : kW8a16Gated) {
-    if (g.hidden == hidden && g.inter == inter && g.mt == mt) return &g;
+    if (g.hidden == hidden && g.inter == inter && g.mt == mt && g.block == block) return &g;
   }
   return nullptr;
 }
@@ -381,7 +401,7 @@ struct W8a16GatedGemm {
 };
 bool w8a16_gated_gemm(int32_t entry, int64_t hidden, int64_t inter, int32_t max_tokens,
                       W8a16GatedGemm *out) {
-  if (entry != LF_FP8_ENTRY_W8A16_GATED_MLP || max_tokens <= 64 || max_tokens > 128) return false;
+  if (!w8a16_gated_entry(entry) || max_tokens <= 64 || max_tokens > 128) return false;
   if (!w8a16_gemm(LF_FP8_ENTRY_W8A16_GATE_UP, inter, hidden, max_tokens, &out->gu) ||
       !w8a16_gemm(LF_FP8_ENTRY_W8A16_DENSE, hidden, inter, max_tokens, &out->dn)) {
     return false;
@@ -499,7 +519,7 @@ int32_t lunaflux_fp8_admit_weight(int32_t entry, const uint8_t *region_head, int
                      entry == LF_FP8_ENTRY_W8A8_QKV_AQ || entry == LF_FP8_ENTRY_W8A8_GATE_UP_AQ ||
                      entry == LF_FP8_ENTRY_W8A8_GATED_MLP;
   const bool block = w8a16_b128_entry(entry) || w8a8_b128_entry(entry) ||
-                     entry == LF_FP8_ENTRY_W8A8_GATED_MLP_B128;
+                     entry == LF_FP8_ENTRY_W8A8_GATED_MLP_B128 || entry == LF_FP8_ENTRY_W8A16_GATED_MLP_B128;
   const bool grouped = entry == LF_FP8_ENTRY_GROUPED;
   if ((!dense && !block && !grouped) || region_head == nullptr || head_bytes < LF_FP8_HEADER_BYTES ||
       ((dense || block) && experts != 1)) {
@@ -548,9 +568,25 @@ static int64_t w8a16_workspace(int32_t entry, int64_t n, int64_t k, int64_t nq, 
     }
     W8a16Gemm gm;
     if (w8a16_gemm(w8a16_channel_entry(entry), n, k, max_tokens, &gm)) return w8a16_gemm_workspace(gm);
-    if (sp.split == 1) return 256;
+    if (const W8a16Fixed *f = w8a16_fixed(entry, n, k, nq, nkv, max_tokens)) {
+      return w8a16_fixed_workspace(*f, n);
+    }
     const int64_t nw = entry == LF_FP8_ENTRY_W8A16_GATE_UP_B128 ? 2 : 1;
-    return align_up(sp.split * (n / 16) * nw * sp.mt * 1024, 256) + align_up(sp.groups * 4, 256);
+    int64_t need = sp.split == 1 ? 256
+                                 : align_up(sp.split * (n / 16) * nw * sp.mt * 1024, 256) +
+                                       align_up(sp.groups * 4, 256);
+    // QKV without its Q / K-V split: also room for the workspace of any
+    // specialized entry of this width (the geometry, given the split, may
+    // pick one)
+    if (entry == LF_FP8_ENTRY_W8A16_QKV_B128 && nq == 0) {
+      for (const W8a16Fixed &f : kW8a16Fixed) {
+        if (f.entry == entry && n == f.nq + 2 * f.nkv &&
+            w8a16_fixed(entry, n, k, f.nq, f.nkv, max_tokens) == &f) {
+          need = std::max(need, w8a16_fixed_workspace(f, n));
+        }
+      }
+    }
+    return need;
   }
   if (entry != LF_FP8_ENTRY_W8A16_DENSE && entry != LF_FP8_ENTRY_W8A16_QKV &&
       entry != LF_FP8_ENTRY_W8A16_GATE_UP) {
@@ -668,7 +704,8 @@ int32_t lunaflux_fp8_gated_mlp_geometry(int32_t entry, int64_t hidden, int64_t i
     const int32_t values[7] = {static_cast<int32_t>(blocks), 1, 1, 512, 1, 1, 0};
     std::memcpy(dims, values, sizeof(values));
     std::memset(symbol, 0, LF_FP8_SYMBOL_BYTES);
-    std::snprintf(symbol, LF_FP8_SYMBOL_BYTES, "lf_fp8_w8a16_gated_mlp_m128_n128_n%d", gg.dn.bn);
+    std::snprintf(symbol, LF_FP8_SYMBOL_BYTES, "lf_fp8_w8a16_gated_mlp%s_m128_n128_n%d",
+                  entry == LF_FP8_ENTRY_W8A16_GATED_MLP_B128 ? "_b128" : "", gg.dn.bn);
     return LF_OK;
   }
   const W8a16Gated *g = w8a16_gated(entry, hidden, inter, max_tokens);
@@ -769,6 +806,11 @@ static int32_t launch_geometry(int32_t entry, int64_t n, int64_t k, int64_t nq, 
         name = buffer;
         gx = static_cast<int32_t>(gm.blocks_n * gm.split);
         bx = 512;
+        break;
+      }
+      if (const W8a16Fixed *f = w8a16_fixed(entry, n, k, nq, nkv, max_tokens)) {
+        name = f->symbol;
+        w8a16_fixed_geometry(*f, n, &gx, &bx);
         break;
       }
       std::snprintf(buffer, sizeof(buffer), "lf_fp8_w8a16_%s_b128_m%d", op, 16 * sp.mt);

@@ -472,8 +472,9 @@ class ProjectionRuntime:
         down projection from it (each W8A8 step then quantizes its input
         inside its own launch, or, with one_launch=False, in a launch of its
         own). Every form computes the same values. Weights with 128 x 128
-        block scales: W8A8 as one launch (the _B128 GatedMlp entry), W8A16
-        (and W8A8 with one_launch=False) as the two block-scaled launches."""
+        block scales: the _B128 GatedMlp entry of the family (W8A8 any width,
+        W8A16 where its one-launch forms are built), else, or with
+        one_launch=False, the two block-scaled launches."""
         if wd.columns != wg.rows or wd.rows != wg.columns:
             raise DeviceError("mlp shapes", _abi.LF_INVALID_ARGUMENT)
         if wg.rows != wu.rows or wg.columns != wu.columns:
@@ -481,7 +482,7 @@ class ProjectionRuntime:
         _family(family, max_tokens)
         modes = {wg.scale_mode, wu.scale_mode, wd.scale_mode}
         if modes == {BLOCK128}:
-            entry = _abi.ENTRY_W8A8_GATED_MLP_B128 if family == "w8a8" else None
+            entry = _abi.ENTRY_W8A8_GATED_MLP_B128 if family == "w8a8" else _abi.ENTRY_W8A16_GATED_MLP_B128
         elif BLOCK128 in modes:
             entry = None
         else:

@@ -55,6 +55,7 @@ FAMILIES = (
     (19, "lf_fp8_w8a8_qkv_b128"),
     (20, "lf_fp8_w8a8_gate_up_b128"),
     (21, "lf_fp8_w8a8_gated_mlp_b128"),
+    (22, "lf_fp8_w8a16_gated_mlp_b128"),
     (12, "lf_fp8_w8a8_dense_", "_aq"),
     (13, "lf_fp8_w8a8_qkv_", "_aq"),
     (14, "lf_fp8_w8a8_gate_up_", "_aq"),

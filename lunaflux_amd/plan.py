@@ -535,7 +535,7 @@ def fp8_entry(op_kind: OperationKind, shape, family: str, max_tokens: int, paged
         capability = Capability.EXPERT_MLP
     elif op_kind == OperationKind.GATED_MLP:
         entry = (_abi.ENTRY_W8A8_GATED_MLP_B128 if block else _abi.ENTRY_W8A8_GATED_MLP) if family == "w8a8" \
-            else _abi.ENTRY_W8A16_GATED_MLP
+            else (_abi.ENTRY_W8A16_GATED_MLP_B128 if block else _abi.ENTRY_W8A16_GATED_MLP)
         geometry = fp8.gated_mlp_geometry(shape.hidden_size, shape.intermediate_size, max_tokens, entry)
         if geometry is None:
             raise CatalogError("MissingKernel")

@@ -294,7 +294,20 @@ def test_block_scaled_geometry_and_workspace():
             assert sym0.startswith(f"lf_fp8_w8a16_{op}_m128_n"), sym0
             assert sym == sym0.replace(f"_{op}_", f"_{op}_b128_") and d == d0, (sym, d, sym0, d0)
             assert fp8.w8a16_workspace_bytes(entry, n, k, m) == fp8.w8a16_workspace_bytes(channel[entry], n, k, m)
-        for n, k, m, mt in [(4096, 4096, 1, 1), (6144, 4096, 32, 2), (14336, 4096, 64, 4),
+        # the Llama-3-8B shape-specialized forms at <= 32 rows: the per-channel
+        # entry's geometry and workspace under the _b128 symbol
+        for n, k, m, split in [(4096, 4096, 1, None), (4096, 4096, 32, None), (4096, 14336, 16, None),
+                               (4096, 14336, 32, None), (14336, 4096, 8, None), (14336, 4096, 32, None),
+                               (6144, 4096, 16, (4096, 1024)), (6144, 4096, 32, (4096, 1024))]:
+            if (op == "qkv") != (split is not None) or (op == "gate_up") != (n == 14336):
+                continue
+            d, sym = fp8.launch_geometry(entry, n, k, m, split)
+            d0, sym0 = fp8.launch_geometry(channel[entry], n, k, m, split)
+            assert f"_k{k}" in sym0 and sym == sym0.replace(f"_{op}_", f"_{op}_b128_") and d == d0, (sym, sym0)
+            ws0 = fp8.w8a16_workspace_bytes(channel[entry], n, k, m, split)
+            # (QKV: sized without the split for every entry of that width)
+            assert fp8.w8a16_workspace_bytes(entry, n, k, m) >= ws0
+        for n, k, m, mt in [(4096, 2048, 1, 1), (6144, 2048, 32, 2), (14336, 4096, 64, 4),
                             (1024, 32768, 16, 1)]:
             d, sym = fp8.launch_geometry(entry, n, k, m)
             assert sym == f"lf_fp8_w8a16_{op}_b128_m{16 * mt}" and d.block == (256, 1, 1)
@@ -329,6 +342,19 @@ def test_block_scaled_geometry_and_workspace():
             + al(cap * 14336) + al(112 * cap * 4))
     assert lib.lunaflux_fp8_gated_mlp_workspace_bytes(e, 4096, 14336, 2048) == want
     assert lib.lunaflux_fp8_gated_mlp_workspace_bytes(e, 4096 + 64, 14336, 2048) == -1
+    # W8A16 GatedMlp in one launch on block-scaled weights: the per-channel
+    # one-launch forms' geometry and workspace under the _b128 symbols; none
+    # at 33..64 rows or at widths without a form (two launches there)
+    e, e0 = _abi.ENTRY_W8A16_GATED_MLP_B128, _abi.ENTRY_W8A16_GATED_MLP
+    for h, i, m in [(4096, 14336, 1), (4096, 14336, 32), (4096, 14336, 128), (4096, 14336, 100)]:
+        d, sym = fp8.gated_mlp_geometry(h, i, m, e)
+        d0, sym0 = fp8.gated_mlp_geometry(h, i, m, e0)
+        assert sym == sym0.replace("gated_mlp_", "gated_mlp_b128_") and d == d0, (sym, sym0)
+        assert (lib.lunaflux_fp8_gated_mlp_workspace_bytes(e, h, i, m)
+                == lib.lunaflux_fp8_gated_mlp_workspace_bytes(e0, h, i, m))
+    assert fp8.gated_mlp_geometry(4096, 14336, 64, e) is None
+    assert fp8.gated_mlp_geometry(2048, 5632, 32, e) is None
+    assert fp8.gated_mlp_geometry(2048, 5632, 100, e) is None and fp8.gated_mlp_geometry(2048, 5632, 100, e0) is None
 
 
 def test_block_scaled_admission_cpu():

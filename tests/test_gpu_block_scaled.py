@@ -258,6 +258,54 @@ def test_block_scaled_gated_mlp(rt, family, hidden, inter, m, max_tokens):
            label=label + " down")
 
 
+@pytest.mark.parametrize("m,max_tokens", [(1, 16), (24, 32), (100, 128)])
+def test_block_scaled_w8a16_gated_mlp_one_launch(rt, m, max_tokens):
+    """W8A16 GatedMlp on block-scaled weights at the Llama-3-8B widths as one
+    launch (LF_FP8_ENTRY_W8A16_GATED_MLP_B128): rows past M untouched, two
+    launches on one workspace bit-identical, the same bits as the two
+    block-scaled launches where both run the same down form (32 and 128
+    rows; at 16 rows the two-launch down is the one-tile form, whose sum
+    order differs), and the oracle stage by stage on the device's own h
+    (the workspace's first [rows][I] bf16)."""
+    hidden, inter = 4096, 14336
+    rng = np.random.default_rng(14500 + m)
+    (qg, sg), (qu, su) = spread_weight(rng, inter, hidden), spread_weight(rng, inter, hidden)
+    qd, sd = spread_weight(rng, hidden, inter)
+    wg, wu, wd = upload(rt, qg, sg), upload(rt, qu, su), upload(rt, qd, sd)
+    x = spread_activations(rng, m, hidden)
+    xa = rt.context.upload(np.concatenate([x, np.zeros((max_tokens - m, hidden), np.uint16)]))
+    ya = rt.context.allocate(max_tokens * hidden * 2)
+    counts = rt.step_counts(m)
+    xr_, yr_ = _region(xa, alignment=256), _region(ya, alignment=256)
+    one = rt.bind_gated_mlp("w8a16", counts, xr_, wg, wu, wd, yr_, max_tokens)
+    two = rt.bind_gated_mlp("w8a16", counts, xr_, wg, wu, wd, yr_, max_tokens, one_launch=False)
+    assert len(one.steps) == 1 and "gated_mlp_b128" in one.steps[0].name, one.steps
+    assert len(two.steps) == 2
+    outs = []
+    for op in (one, one, two):
+        ya.copy_from_host(np.full(max_tokens * hidden, SENTINEL, np.uint16))
+        op.launch(rt.stream, synchronous=True)
+        outs.append(ya.read(np.uint16, (max_tokens, hidden)))
+        assert np.all(outs[-1][m:] == SENTINEL), "rows past M written"
+    assert np.array_equal(outs[0], outs[1]), "a second launch on the same workspace differs"
+    if max_tokens > 16:
+        assert np.array_equal(outs[0], outs[2])
+    y = outs[0][:m]
+    h_gpu = one.workspace.read(np.uint16, (m, inter))
+    rows, hcols = sample(rng, m, inter, 24, 192)
+    xr = x_ref(x[rows], "w8a16")
+    wgr, wur = deq_rows(qg, sg, hcols), deq_rows(qu, su, hcols)
+    g, u = o.dense_projection(xr, wgr), o.dense_projection(xr, wur)
+    tol = swiglu_midpoint_tol(g, u, abs_sum(xr, wgr), abs_sum(xr, wur), bound_k(hidden))
+    label = f"b128 w8a16 gated mlp one launch m={m}/{max_tokens}"
+    parity(h_gpu[rows][:, hcols], o.silu_mul_array(g, u), label=label + " gate/up", midpoint_tol=tol)
+    hb = o.bf16_decode(h_gpu[rows])
+    _, cols = sample(rng, m, hidden, 24, 128)
+    wdr = deq_rows(qd, sd, cols)
+    parity(y[rows][:, cols], o.dense_projection(hb, wdr), k=bound_k(inter), s_abs=abs_sum(hb, wdr),
+           label=label + " down")
+
+
 def test_block_scaled_admission(rt):
     """A per-channel weight is refused by the block-scaled entries, a
     block-scaled one by the per-channel entries (UNSUPPORTED), and each

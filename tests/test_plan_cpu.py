@@ -201,6 +201,9 @@ def test_this_builds_dense_entries():
     assert P.fp8_entry(OK.GATED_MLP, gm, "w8a8", 2048, digest=DIGEST,
                        scale_mode=_abi.LF_FP8_SCALE_BLOCK128).implementation.family_id == 21
     assert P.fp8_entry(OK.GATED_MLP, gm, "w8a16", 32, digest=DIGEST).implementation.family_id == 10
+    b = P.fp8_entry(OK.GATED_MLP, gm, "w8a16", 32, digest=DIGEST, scale_mode=_abi.LF_FP8_SCALE_BLOCK128)
+    assert b.implementation.family_id == 22 and b.workspace_bytes == _abi.lib().lunaflux_fp8_gated_mlp_workspace_bytes(
+        _abi.ENTRY_W8A16_GATED_MLP_B128, 4096, 14336, 32)
     o = P.ProjectionShape(4096, 4096)
     assert P.fp8_entry(OK.OUTPUT_PROJECTION, o, "w8a8", 2048, digest=DIGEST).implementation.family_id == 12
     assert P.fp8_entry(OK.OUTPUT_PROJECTION, o, "w8a16", 32, digest=DIGEST).implementation.family_id == 3
