@@ -118,6 +118,23 @@ LF_DEVICE void e4m3x4_to_bf16x4(uint32_t word, uint32_t &lo, uint32_t &hi) {
   hi = __builtin_bit_cast(uint32_t, b);
 }
 
+// Carries the last nonzero scale forward: returns the ratio prev / s for a
+// nonzero s (prev <- s), 1 otherwise.
+LF_DEVICE float carry_ratio(float s, float &prev) {
+  if (s == 0.0f) return 1.0f;
+  const float r = prev / s;
+  prev = s;
+  return r;
+}
+
+// A wave-uniform read-only float through the constant address space: a
+// scalar load (lgkm counter, so the vector-memory waits of a hand-counted
+// load ring are not disturbed).
+LF_DEVICE float sload(const float *p, int i) {
+  typedef const __attribute__((address_space(4))) float cfloat;
+  return ((cfloat *)p)[i];
+}
+
 LF_DEVICE float wave_max(float v) {
 #pragma unroll
   for (int offset = 32; offset > 0; offset >>= 1) v = fmaxf(v, __shfl_xor(v, offset));

@@ -810,14 +810,6 @@ struct BlockRescale256 {
   }
 };
 
-// Carries the last nonzero scale forward: returns the ratio prev / s for a
-// nonzero s (prev <- s), 1 otherwise.
-LF_DEVICE float carry_ratio(float s, float &prev) {
-  if (s == 0.0f) return 1.0f;
-  const float r = prev / s;
-  prev = s;
-  return r;
-}
 
 // QUANT (block-scaled gate/up only): the epilogue also quantizes h, writing
 // the hidden quantizer's e4m3 codes and per-128-column scales instead of
@@ -1338,12 +1330,6 @@ LF_DEVICE u32x4 gload16(const uint8_t *base, uint32_t off) {
   typedef const __attribute__((address_space(1))) uint8_t gbyte;
   typedef const __attribute__((address_space(1))) u32x4 gvec;
   return *reinterpret_cast<gvec *>((gbyte *)base + off);
-}
-// A wave-uniform read-only float through the constant address space: a
-// scalar load.
-LF_DEVICE float sload(const float *p, int i) {
-  typedef const __attribute__((address_space(4))) float cfloat;
-  return ((cfloat *)p)[i];
 }
 
 template <int STAGE, bool BLOCK>

@@ -1231,6 +1231,8 @@ LF_DEVICE B128Rows b128_rows(uint8_t *at, int cap, int K) {
 // Quantizer step: block b (of kQuantBlocks) quantizes chunks b, b +
 // kQuantBlocks, ... of kChunkRows rows (its 4 waves splitting each chunk's
 // groups) and counts each into its band's counter of step `step`.
+// BM: the GEMM's band height (the counter a chunk counts into).
+template <int BM = kB128BM>
 LF_DEVICE void b128_quantize(const uint16_t *x, int K, int M, const B128Rows &rows, int cap, int b,
                              const phase::Sync &sync, int step) {
   const int chunks = (M + kChunkRows - 1) / kChunkRows;
@@ -1239,7 +1241,7 @@ LF_DEVICE void b128_quantize(const uint16_t *x, int K, int M, const B128Rows &ro
     const int row0 = c * kChunkRows;
     const int n = M - row0 < kChunkRows ? M - row0 : kChunkRows;
     quantize_group_rows<true>(x, K, row0, n, rows.codes, rows.scales_t, cap, wave, nw);
-    phase::signal(sync.band(step, row0 / kB128BM));
+    phase::signal(sync.band(step, row0 / BM));
   }
 }
 
@@ -1271,6 +1273,291 @@ LF_DEVICE void w8a8_b128_one_launch(const int32_t *counts, const uint16_t *x, co
   };
   w8a8_b128_gemm<T, 4, MODE>(smem, win, M, rows.codes, rows.scales_t, cap, w0, w1, w2, y, b - kQuantBlocks,
                              gate);
+  phase::finish(sync, blocks, 1, flag);
+}
+
+// ---------------------------------------------------------------------------
+// Block-scaled W8A8 on 256 x 256 tiles (the eight-wave half-step loop of
+// w8a8_v4.h with swapped operands, as the block-scaled MoE GEMMs), which
+// the launch geometry picks for profiles of at least 192 such tiles (fewer:
+// the 128 x 128 form above keeps more CUs busy). The accumulators hold
+// acc / sigma_kt with sigma_kt = a[row][kt] w[block][kt] (each scale
+// sequence carries its last nonzero value forward, carry_ratio: a zero scale
+// belongs only to an all-zero group, whose products are zero); before
+// k-tile kt's first MFMA into a column fragment they are multiplied by
+// sigma_{kt-1} / sigma_kt, and the epilogue multiplies by the last sigma.
+// No table of all k-tiles fits beside the 128 KiB stage ring at these K
+// (32-112 k-tiles), so each stage also side-loads its k-tile's activation
+// scales of the tile's 256 rows into a two-slot LDS window, and the weight
+// scales are scalar loads.
+// ---------------------------------------------------------------------------
+using B128V4Tile = w8a8v4::Tile<256, 256, 4, 4, 2>;
+constexpr int kB128V4BM = 256;
+
+// Side loads (w8a8v4 mainloop SIDE): stage s loads the 256 row scales of
+// k-tile s / 2 (1 KiB of scales_t[kt][m0 ..]) into window slot (s / 2) & 1;
+// both stages of a k-tile load the same bytes, so every stage has one load
+// per wave and the waits stay uniform. Wave w loads rows 64 (w % 4) .. + 63,
+// one dword per lane (waves w and w + 4 write the same bytes: a load with
+// only some lanes active, a branch inside the half-step, cost the loop 70-190
+// spilled registers). Slot reuse: k-tile kt + 2's first load is issued after
+// the block barrier of half-step 2 kt + 1, when every wave has read k-tile
+// kt's slot (at the start of half-step 2 kt); the second load of a k-tile
+// rewrites its slot with the same bytes.
+template <class T>
+struct B128V4Side {
+  static constexpr int kIns = 1;
+  const uint8_t *base;  // scales_t + m0 (wave-uniform)
+  uint64_t stride;      // bytes per k-tile: cap * 4
+  uint32_t win;         // LDS byte offset of the window [2][kBM] fp32
+  LF_DEVICE void issue(int s, int) const {
+    static_assert(T::kBM == 256 && T::kWaves == 8, "four waves cover the 256 rows");
+    const int lane = threadIdx.x & 63, part = (static_cast<int>(threadIdx.x) >> 6) & 3;
+    const int kt = s >> 1;
+    w8a8v3::dma4(w8a8v3::uniform_ptr(base + static_cast<uint64_t>(kt) * stride),
+                 static_cast<uint32_t>(64 * part + lane) * 4,
+                 win + static_cast<uint32_t>(kt & 1) * T::kBM * 4 + static_cast<uint32_t>(part) * 256);
+  }
+};
+
+// Rescale (w8a8v4 mainloop RESCALE, swapped layout: lane l holds row
+// row0 + 32 i of fragment i). Part 1: the up fragments of gate/up (column
+// fragments kFN / 2 ..), whose weight block scales are the up weight's.
+// The loop runs on a copy of the functor, so after the last k-tile's
+// begin() the final sigma factors go to LDS (last: the tile's 256 row
+// scales, then two per wave) for the epilogue.
+template <class T, int MODE>
+struct B128V4Rescale {
+  static constexpr int kParts = MODE == 2 ? 2 : 1;
+  typedef const __attribute__((address_space(3))) float *lds_ptr;
+  typedef __attribute__((address_space(3))) float *lds_wptr;
+  lds_ptr win;                 // [2][kBM] row scales (B128V4Side)
+  lds_wptr last;               // [kBM + 2 kWaves]: last nonzero row / block scales
+  int row0;                    // the lane's row of fragment 0 in the tile
+  int KT;
+  const float *sw[kParts];     // this wave's block scales [KT] per part (wave-uniform)
+  float prev_a[T::kFM];        // last nonzero row scale so far (1 before any)
+  float prev_w[kParts];
+  float m[kParts][T::kFM];     // this k-tile's multipliers
+  LF_DEVICE void begin(int kt) {
+    float rw[kParts];
+#pragma unroll
+    for (int p = 0; p < kParts; ++p) rw[p] = carry_ratio(sload(sw[p], kt), prev_w[p]);
+#pragma unroll
+    for (int i = 0; i < T::kFM; ++i) {
+      const float ra = carry_ratio(win[(kt & 1) * T::kBM + row0 + 32 * i], prev_a[i]);
+#pragma unroll
+      for (int p = 0; p < kParts; ++p) m[p][i] = kt == 0 ? 1.0f : ra * rw[p];
+    }
+    if (kt == KT - 1) {
+      // (lanes l and l + 32 hold the same rows: the same values)
+#pragma unroll
+      for (int i = 0; i < T::kFM; ++i) last[row0 + 32 * i] = prev_a[i];
+      const int wave = threadIdx.x >> 6;
+#pragma unroll
+      for (int p = 0; p < kParts; ++p) last[T::kBM + 2 * wave + p] = prev_w[p];
+    }
+  }
+  template <class A>
+  LF_DEVICE void apply(int o, A &acc) {
+    const int p = kParts == 2 && o >= T::kFN / 2 ? 1 : 0;
+#pragma unroll
+    for (int i = 0; i < T::kFM; ++i)
+#pragma unroll
+      for (int e = 0; e < 16; ++e) acc[i][o][e] *= m[p][i];
+  }
+};
+
+// The GEMM on one 256 x 256 tile of M live rows of a workspace sized for
+// cap rows (codes [cap, K], scales_t [K / 128][cap]); operand mapping and
+// gate as w8a8_b128_gemm; win: the block's LDS window (2 x 256 floats), then
+// kBM + 2 kWaves floats for the final scales.
+template <class T, int GROUP, int MODE, bool THROUGH = false, class Gate = Open>
+LF_DEVICE int w8a8_b128_v4_gemm(uint8_t *smem, float *win, int M, const uint8_t *xq, const float *scales_t,
+                                int cap, const uint8_t *w0, const uint8_t *w1, const uint8_t *w2, uint16_t *y,
+                                int bid, const Gate &gate) {
+  constexpr int BM = T::kBM, BN = T::kBN;
+  static_assert(T::kWaveN == 128 && BM == kB128V4BM, "a wave's columns are one 128-column block");
+  const WeightHeader &h0 = header_of(w0);
+  const int K = static_cast<int>(h0.columns);
+  const int KT = K >> 7;
+  const int tq = static_cast<int>(h0.rows) >> 4;
+  const int tk = MODE == 1 ? static_cast<int>(header_of(w1).rows) >> 4 : 0;
+  const int ld = dense_ld<MODE>(w0, w1, w2);
+  const int gx = dense_gx<MODE, BN>(ld);
+  int bx, by;
+  if (!w8a8v3::tile_of_block(bid, gx, (M + BM - 1) / BM, GROUP, bx, by)) return -1;
+  const int m0 = by * BM;
+  // 32-bit activation offsets (below 256 K) need K < 2^24
+  if (K >= (1 << 24)) {
+    poison_tile<MODE, BN>(y, ld, M, m0, BM, bx);
+    return by;
+  }
+  if (!gate(m0)) return -1;
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int wm = wave / T::kWgn, wn = wave % T::kWgn;
+
+  // Weight tile of block-local tile s (the mapping of w8a8_v4_kernel).
+  auto slot = [&](int s, const uint8_t *&region, int &t, int &ocol) {
+    if (MODE == 2) {
+      const int sw = s / (2 * T::kFN), f = s % (2 * T::kFN);
+      const bool up = f >= T::kFN;
+      const int col = bx * (BN / 2) + sw * (T::kWaveN / 2) + 16 * (up ? f - T::kFN : f);
+      region = up ? w1 : w0;
+      t = col >> 4;
+      ocol = col;
+    } else {
+      t = bx * (BN / 16) + s;
+      ocol = t * 16;
+      region = w0;
+      if (MODE == 1) {
+        if (t >= tq + tk) {
+          region = w2;
+          t -= tq + tk;
+        } else if (t >= tq) {
+          region = w1;
+          t -= tq;
+        }
+      }
+    }
+  };
+
+  w8a8v4::Plan<T> plan;
+  plan.a_base = w8a8v3::uniform_ptr(xq + static_cast<uint64_t>(m0) * K);
+#pragma unroll
+  for (int q = 0; q < T::kAIns; ++q) {
+    const int tr = w8a8v4::a_load_row<T>(wave, q, lane);
+    const int row = m0 + tr < M ? tr : M - 1 - m0;
+    plan.a_off[q] = static_cast<uint32_t>(row) * static_cast<uint32_t>(K) + w8a8v4::a_load_slot(tr, lane) * 32;
+  }
+#pragma unroll
+  for (int q = 0; q < T::kBIns; ++q) {
+    const uint8_t *region;
+    int t, ocol;
+    slot(w8a8v4::b_load_tile<T>(wave, q), region, t, ocol);
+    plan.b_base[q] = w8a8v3::uniform_ptr(expert_tiles(region, 0) + static_cast<uint64_t>(t) * KT * kTileBytes);
+  }
+  plan.b_lane = lane * 16;
+
+  // This wave's 128-column block: (gate/up) its 64 gate and 64 up columns
+  // lie in one 128-row block of each weight; (dense, QKV) its 128 columns
+  // are one block of one region (every QKV width is a multiple of 128).
+  typedef const __attribute__((address_space(3))) float *lds_ptr;
+  typedef __attribute__((address_space(3))) float *lds_wptr;
+  float *last = win + 2 * BM;
+  B128V4Rescale<T, MODE> rs;
+  rs.win = (lds_ptr)(win);
+  rs.last = (lds_wptr)(last);
+  rs.row0 = wm * T::kWaveM + (lane & 31);
+  rs.KT = KT;
+#pragma unroll
+  for (int p = 0; p < B128V4Rescale<T, MODE>::kParts; ++p) {
+    const uint8_t *region;
+    int t, ocol;
+    slot(wn * (T::kWaveN / 16) + p * T::kFN, region, t, ocol);
+    rs.sw[p] = reinterpret_cast<const float *>(w8a8v3::uniform_ptr(
+        reinterpret_cast<const uint8_t *>(expert_scales(region, 0) + static_cast<uint64_t>(t >> 3) * KT)));
+    rs.prev_w[p] = 1.0f;
+  }
+#pragma unroll
+  for (int i = 0; i < T::kFM; ++i) rs.prev_a[i] = 1.0f;
+  const B128V4Side<T> side{w8a8v3::uniform_ptr(reinterpret_cast<const uint8_t *>(scales_t + m0)),
+                           static_cast<uint64_t>(cap) * 4,
+                           w8a8v3::lds_offset_of(reinterpret_cast<uint8_t *>(win))};
+  w8a8v4::f32x16 acc[T::kFM][T::kFN];
+  w8a8v4::mainloop<T, false, B128V4Rescale<T, MODE>, true, B128V4Side<T>>(plan, KT, smem, acc, T::kFM, rs,
+                                                                         true, side);
+  // the final sigma factors (this lane wrote its rows' and its wave's)
+  float sa_last[T::kFM], sw_last[B128V4Rescale<T, MODE>::kParts];
+#pragma unroll
+  for (int i = 0; i < T::kFM; ++i) sa_last[i] = last[rs.row0 + 32 * i];
+#pragma unroll
+  for (int p = 0; p < B128V4Rescale<T, MODE>::kParts; ++p) sw_last[p] = last[BM + 2 * wave + p];
+
+  // Epilogue (swapped layout: element 4 g + q of fragment j is column
+  // 32 j + 8 g + 4 (lane / 32) + q): times the last sigma, staged through
+  // LDS one 32-row fragment at a time in 16-byte row chunks.
+  const int rl = lane & 31, c4 = 4 * (lane >> 5);
+  constexpr int kCols = MODE == 2 ? T::kWaveN / 2 : T::kWaveN;
+  using Stage = w8a8v4::StageTile<uint16_t, 32, kCols>;
+  static_assert(Stage::kBytes * T::kWaves <= T::kSmem, "staging fits the stage ring");
+  int col0;
+  {
+    const uint8_t *region;
+    int t;
+    slot(wn * (T::kWaveN / 16), region, t, col0);
+  }
+  col0 = __builtin_amdgcn_readfirstlane(col0);
+  w8a8v4::epilogue_barrier();
+  const Stage st{reinterpret_cast<uint16_t *>(smem + wave * Stage::kBytes)};
+#pragma unroll
+  for (int i = 0; i < T::kFM; ++i) {
+    const float sa = sa_last[i];
+    if constexpr (MODE == 2) {
+#pragma unroll
+      for (int j = 0; j < T::kFN / 2; ++j)
+#pragma unroll
+        for (int g = 0; g < 4; ++g) {
+          uint32_t b[4];
+#pragma unroll
+          for (int q = 0; q < 4; ++q) {
+            const float gv = acc[i][j][4 * g + q] * sa * sw_last[0];
+            const float uv = acc[i][j + T::kFN / 2][4 * g + q] * sa * sw_last[B128V4Rescale<T, MODE>::kParts - 1];
+            b[q] = f32_to_bf16(silu_mul(gv, uv));
+          }
+          st.put4(rl, 32 * j + 8 * g + c4, b);
+        }
+    } else {
+#pragma unroll
+      for (int j = 0; j < T::kFN; ++j)
+#pragma unroll
+        for (int g = 0; g < 4; ++g) {
+          uint32_t b[4];
+#pragma unroll
+          for (int q = 0; q < 4; ++q) b[q] = f32_to_bf16(acc[i][j][4 * g + q] * sa * sw_last[0]);
+          st.put4(rl, 32 * j + 8 * g + c4, b);
+        }
+    }
+    const int mw = m0 + wm * T::kWaveM + 32 * i;
+    st.template flush<THROUGH>(lane, [&](int row) -> uint16_t * {
+      return mw + row < M ? y + static_cast<uint64_t>(mw + row) * ld + col0 : nullptr;
+    });
+  }
+  return by;
+}
+
+// The block-scaled operations in one launch on the 256 x 256 form: as
+// w8a8_b128_one_launch with 256-row bands (cap = bands x 256).
+template <int MODE>
+LF_DEVICE void w8a8_b128_v4_one_launch(const int32_t *counts, const uint16_t *x, const uint8_t *w0,
+                                       const uint8_t *w1, const uint8_t *w2, uint16_t *y, uint8_t *ws) {
+  using T = B128V4Tile;
+  constexpr int BM = kB128V4BM;
+  __shared__ __attribute__((aligned(1024))) uint8_t smem[T::kSmem];
+  __shared__ __attribute__((aligned(16))) float win[2 * BM + BM + 2 * T::kWaves];
+  __shared__ phase::Flag flag;
+  if (!dense_regions_ok<MODE, kScaleBlock128>(w0, w1, w2)) return;
+  const int K = static_cast<int>(header_of(w0).columns);
+  const int gx = dense_gx<MODE, T::kBN>(dense_ld<MODE>(w0, w1, w2));
+  const int blocks = static_cast<int>(gridDim.x) - kQuantBlocks;
+  if (gx <= 0 || blocks <= 0 || blocks % gx != 0 || blockDim.x != T::kThreads) return;
+  const int bands = blocks / gx;
+  const phase::Sync sync{reinterpret_cast<int *>(ws), bands};
+  const int cap = bands * BM;
+  const B128Rows rows = b128_rows(ws + phase::sync_bytes(1, bands), cap, K);
+  const int M = live_rows(counts, cap);
+  const int b = static_cast<int>(blockIdx.x);
+  if (b < kQuantBlocks) {
+    b128_quantize<BM>(x, K, M, rows, cap, b, sync, 0);
+    return;
+  }
+  const auto gate = [&](int m0) {
+    const int band = m0 / BM;
+    return phase::wait_for(sync, sync.band(0, band), chunks_in_band(M, band, BM), flag);
+  };
+  w8a8_b128_v4_gemm<T, 4, MODE>(smem, win, M, rows.codes, rows.scales_t, cap, w0, w1, w2, y,
+                                b - kQuantBlocks, gate);
   phase::finish(sync, blocks, 1, flag);
 }
 
@@ -1491,6 +1778,22 @@ __global__ __launch_bounds__(256) void lf_fp8_w8a8_gate_up_b128(const int32_t *c
                                                                 const uint8_t *wg, const uint8_t *wu,
                                                                 uint16_t *h, uint8_t *ws) {
   w8a8_b128_one_launch<2>(counts, x, wg, wu, wu, h, ws);
+}
+// The same on 256 x 256 tiles (eight waves), for launches of at least 192
+// such tiles (lunaflux_fp8_launch_geometry picks the form).
+__global__ __launch_bounds__(512) void lf_fp8_w8a8_dense_b128_t256(const int32_t *counts, const uint16_t *x,
+                                                                   const uint8_t *w, uint16_t *y, uint8_t *ws) {
+  w8a8_b128_v4_one_launch<0>(counts, x, w, w, w, y, ws);
+}
+__global__ __launch_bounds__(512) void lf_fp8_w8a8_qkv_b128_t256(const int32_t *counts, const uint16_t *x,
+                                                                 const uint8_t *wq, const uint8_t *wk,
+                                                                 const uint8_t *wv, uint16_t *y, uint8_t *ws) {
+  w8a8_b128_v4_one_launch<1>(counts, x, wq, wk, wv, y, ws);
+}
+__global__ __launch_bounds__(512) void lf_fp8_w8a8_gate_up_b128_t256(const int32_t *counts, const uint16_t *x,
+                                                                     const uint8_t *wg, const uint8_t *wu,
+                                                                     uint16_t *h, uint8_t *ws) {
+  w8a8_b128_v4_one_launch<2>(counts, x, wg, wu, wu, h, ws);
 }
 __global__ __launch_bounds__(256) void lf_fp8_w8a8_gated_mlp_b128(const int32_t *counts, const uint16_t *x,
                                                                   const uint8_t *wg, const uint8_t *wu,

@@ -112,6 +112,13 @@ LF_DEVICE void dma16(const uint8_t *base, uint32_t offset, uint32_t lds_offset) 
                : "v"(offset), "s"(base), "s"(__builtin_amdgcn_readfirstlane(lds_offset))
                : "memory", "m0");
 }
+// The same for 4 bytes per lane: lane l's dword lands at lds_offset + 4 l.
+LF_DEVICE void dma4(const uint8_t *base, uint32_t offset, uint32_t lds_offset) {
+  asm volatile("s_mov_b32 m0, %2\n\tglobal_load_lds_dword %0, %1"
+               :
+               : "v"(offset), "s"(base), "s"(__builtin_amdgcn_readfirstlane(lds_offset))
+               : "memory", "m0");
+}
 #pragma clang diagnostic pop
 
 // LDS byte offset of a pointer into a __shared__ array (an address-space

@@ -99,7 +99,8 @@ LF_DEVICE void block_barrier() { asm volatile("s_barrier" ::: "memory"); }
 // RESCALE (block-scaled operands): before the first half-step of k-tile kt,
 // rescale.begin(kt) loads that k-tile's multipliers and rescale.apply(o, acc)
 // multiplies the accumulators of column fragment o right before their first
-// MFMA of the k-tile (NoRescale: per-channel scales, nothing to do).
+// MFMA of the k-tile (NoRescale: per-channel scales, nothing to do). The
+// loop works on its own copy of the functor.
 // a_loads (wave-uniform): whether this wave issues its A loads. A wave loads
 // A rows 16 kAIns wave .. + 16 kAIns - 1; when all of them are past the last
 // live row the caller passes false and the wave issues only its B loads.
@@ -109,6 +110,10 @@ LF_DEVICE void block_barrier() { asm volatile("s_barrier" ::: "memory"); }
 // per loader and per fragment). The rows such a wave would have written keep
 // whatever the LDS held; no MFMA reads them. Each wave counts its own loads
 // (vmcnt), so the waits use kBIns loads per stage for such a wave.
+// SIDE: extra loads of each stage (Side::kIns DMA instructions per wave,
+// e.g. a block-scaled operand's per-k-tile scales into an LDS window),
+// issued after the stage's own loads, so the waits count them
+// (w8a8v3::NoSide: none).
 // SWAP: the MFMAs take the weight fragment as their first operand and the
 // activation fragment as the second, so each accumulator block holds the
 // transposed product: lane l keeps tile row 32 i + l % 32 of fragment i and,
@@ -121,10 +126,12 @@ struct NoRescale {
   LF_DEVICE void apply(int, A &) {}
 };
 
-template <class T, bool SKIP = false, class Rescale = NoRescale, bool SWAP = false>
+template <class T, bool SKIP = false, class Rescale = NoRescale, bool SWAP = false,
+          class Side = w8a8v3::NoSide>
 __device__ __forceinline__ void mainloop(const Plan<T> &plan, int KT, uint8_t *smem,
                          f32x16 (&acc)[T::kFM][T::kFN], int live_fm = T::kFM,
-                         Rescale rescale = Rescale{}, bool a_loads = true) {
+                         Rescale rescale = Rescale{}, bool a_loads = true,
+                         const Side &side = Side{}) {
   static_assert(!SKIP || T::kAIns * 16 == 32, "a loader's rows are one 32-row fragment");
   constexpr int NS = T::kStages;
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
@@ -137,9 +144,9 @@ __device__ __forceinline__ void mainloop(const Plan<T> &plan, int KT, uint8_t *s
   auto wait_stages = [&](auto n_tag) {
     constexpr int N = decltype(n_tag)::value;
     if (a_on) {
-      w8a8v3::wait_vmcnt<N * T::kIns>();
+      w8a8v3::wait_vmcnt<N * (T::kIns + Side::kIns)>();
     } else {
-      w8a8v3::wait_vmcnt<N * T::kBIns>();
+      w8a8v3::wait_vmcnt<N * (T::kBIns + Side::kIns)>();
     }
   };
   const uint32_t smem_base = __builtin_amdgcn_readfirstlane(w8a8v3::lds_offset_of(smem));
@@ -159,6 +166,7 @@ __device__ __forceinline__ void mainloop(const Plan<T> &plan, int KT, uint8_t *s
   auto issue = [&](int s) {
 #pragma unroll
     for (int q = 0; q < T::kIns; ++q) issue_one(s, q);
+    side.issue(s, s % NS);
   };
 
   // LDS byte offsets of this lane's fragment reads inside a stage: A block i
@@ -235,6 +243,7 @@ __device__ __forceinline__ void mainloop(const Plan<T> &plan, int KT, uint8_t *s
       if constexpr (kIssue) {
 #pragma unroll
         for (int q = o * T::kIns / kOuter; q < (o + 1) * T::kIns / kOuter; ++q) issue_one(s + NS - 1, q);
+        if (o == kOuter - 1) side.issue(s + NS - 1, (s + NS - 1) % NS);
       }
     };
     mfma_group(cur, 0);

@@ -359,6 +359,26 @@ bool w8a8_b128_bands(int64_t n, int64_t k, int32_t max_tokens, int64_t *bands) {
   *bands = (max_tokens + 127) / 128;
   return (k / 128) * (*bands * 128) < INT32_MAX;
 }
+// The standalone block-scaled entries also have a 256 x 256 form of 8 waves
+// (_b128_t256, 256-row bands) for profiles of at least kB128T256Tiles such
+// tiles, where the width is a multiple of its tile (256 columns; gate/up:
+// 128 outputs) and activation offsets fit 32 bits (K < 2^24).
+constexpr int64_t kB128T256Tiles = 192;
+struct W8a8B128 {
+  bool t256;
+  int64_t bm, gx, bands;  // band height, column blocks, row bands
+};
+bool w8a8_b128_tiles(bool gate_up, int64_t n, int64_t k, int32_t max_tokens, W8a8B128 *out) {
+  if (n <= 0 || k <= 0 || n % 128 != 0 || k % 128 != 0 || max_tokens <= 0) return false;
+  const int64_t cols256 = gate_up ? 128 : 256;
+  const int64_t tiles256 =
+      n % cols256 == 0 && k < (int64_t(1) << 24) ? (max_tokens + 255) / 256 * (n / cols256) : 0;
+  out->t256 = tiles256 >= kB128T256Tiles;
+  out->bm = out->t256 ? 256 : 128;
+  out->gx = out->t256 ? n / cols256 : n / (cols256 / 2);
+  out->bands = (max_tokens + out->bm - 1) / out->bm;
+  return (k / 128) * (out->bands * out->bm) < INT32_MAX;
+}
 
 // W8A8 GatedMlp in one launch: both GEMMs on 4-wave blocks of one band
 // height. Gate/up on 256 x 256 tiles where its own launch would take 256-row
@@ -645,9 +665,12 @@ int64_t lunaflux_fp8_gated_mlp_workspace_bytes(int32_t entry, int64_t hidden, in
 
 int64_t lunaflux_fp8_w8a8_workspace_bytes(int32_t entry, int64_t n, int64_t k, int32_t max_tokens) {
   if (w8a8_b128_entry(entry)) {
-    int64_t bands = 0;
-    if (n > kMaxDim || k > kMaxDim || !w8a8_b128_bands(n, k, max_tokens, &bands)) return -1;
-    return sync_bytes(1, bands) + b128_rows_bytes(bands * 128, k);
+    W8a8B128 t;
+    if (n > kMaxDim || k > kMaxDim ||
+        !w8a8_b128_tiles(entry == LF_FP8_ENTRY_W8A8_GATE_UP_B128, n, k, max_tokens, &t)) {
+      return -1;
+    }
+    return sync_bytes(1, t.bands) + b128_rows_bytes(t.bands * t.bm, k);
   }
   if ((entry != LF_FP8_ENTRY_W8A8_DENSE_AQ && entry != LF_FP8_ENTRY_W8A8_QKV_AQ &&
        entry != LF_FP8_ENTRY_W8A8_GATE_UP_AQ) ||
@@ -822,16 +845,17 @@ static int32_t launch_geometry(int32_t entry, int64_t n, int64_t k, int64_t nq, 
     case LF_FP8_ENTRY_W8A8_DENSE_B128:
     case LF_FP8_ENTRY_W8A8_QKV_B128:
     case LF_FP8_ENTRY_W8A8_GATE_UP_B128: {
-      int64_t bands = 0;
-      if (!w8a8_b128_bands(n, k, max_tokens, &bands)) return LF_INVALID_ARGUMENT;
       const bool gate_up = entry == LF_FP8_ENTRY_W8A8_GATE_UP_B128;
-      const int64_t blocks = kQuantBlocks + (gate_up ? n / 64 : n / 128) * bands;
+      W8a8B128 t;
+      if (!w8a8_b128_tiles(gate_up, n, k, max_tokens, &t)) return LF_INVALID_ARGUMENT;
+      const int64_t blocks = kQuantBlocks + t.gx * t.bands;
       if (blocks > INT32_MAX) return LF_INVALID_ARGUMENT;
-      std::snprintf(buffer, sizeof(buffer), "lf_fp8_w8a8_%s_b128",
-                    entry == LF_FP8_ENTRY_W8A8_QKV_B128 ? "qkv" : gate_up ? "gate_up" : "dense");
+      std::snprintf(buffer, sizeof(buffer), "lf_fp8_w8a8_%s_b128%s",
+                    entry == LF_FP8_ENTRY_W8A8_QKV_B128 ? "qkv" : gate_up ? "gate_up" : "dense",
+                    t.t256 ? "_t256" : "");
       name = buffer;
       gx = static_cast<int32_t>(blocks);
-      bx = 256;
+      bx = t.t256 ? 512 : 256;
       break;
     }
     case LF_FP8_ENTRY_W8A8_DENSE:

@@ -334,6 +334,30 @@ def test_block_scaled_geometry_and_workspace():
         cap = 128 * bands
         want = 256 + 128 * bands + al(cap * k) + al((k // 128) * cap * 4)
         assert fp8.w8a8_workspace_bytes(entry, n, k, m) == want
+    # the 256 x 256 form from 192 such tiles on (256-row bands, 512
+    # threads), where the width is a multiple of its tile; its workspace
+    # holds cap = 256 x bands rows
+    for entry, op, n, k, m, t256 in [
+            (_abi.ENTRY_W8A8_DENSE_B128, "dense", 4096, 4096, 3072, True),
+            (_abi.ENTRY_W8A8_DENSE_B128, "dense", 4096, 14336, 3000, True),
+            (_abi.ENTRY_W8A8_DENSE_B128, "dense", 4096, 4096, 2816, False),
+            (_abi.ENTRY_W8A8_DENSE_B128, "dense", 4096 + 128, 4096, 8192, False),
+            (_abi.ENTRY_W8A8_QKV_B128, "qkv", 6144, 4096, 2048, True),
+            (_abi.ENTRY_W8A8_QKV_B128, "qkv", 6144, 4096, 1792, False),
+            (_abi.ENTRY_W8A8_GATE_UP_B128, "gate_up", 14336, 4096, 300, True),
+            (_abi.ENTRY_W8A8_GATE_UP_B128, "gate_up", 14336, 4096, 256, False),
+            (_abi.ENTRY_W8A8_GATE_UP_B128, "gate_up", 1408, 4096, 8192, True)]:
+        d, sym = fp8.launch_geometry(entry, n, k, m)
+        bm = 256 if t256 else 128
+        bands = -(-m // bm)
+        gx = n // (bm // 2) if op == "gate_up" else n // bm
+        assert sym == f"lf_fp8_w8a8_{op}_b128" + ("_t256" if t256 else ""), (n, k, m, sym)
+        assert d.grid == (256 + gx * bands, 1, 1) and d.block == (2 * bm, 1, 1)
+        cap = bm * bands
+        want = 256 + 128 * bands + al(cap * k) + al((k // 128) * cap * 4)
+        assert fp8.w8a8_workspace_bytes(entry, n, k, m) == want
+    d, sym = fp8.launch_geometry(_abi.ENTRY_W8A8_QKV_B128, 6144, 4096, 2048, qkv_split=(4096, 1024))
+    assert sym == "lf_fp8_w8a8_qkv_b128_t256" and d.grid == (256 + 24 * 8, 1, 1)
     e = _abi.ENTRY_W8A8_GATED_MLP_B128
     d, sym = fp8.gated_mlp_geometry(4096, 14336, 2048, e)
     bands, cap = 16, 2048

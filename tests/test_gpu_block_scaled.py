@@ -167,22 +167,34 @@ def test_block_scaled_w8a16(rt, op, m, max_tokens):
 
 def w8a8_quantized_rows(bound, m, k, max_tokens):
     """(codes [m, K], scales [m, K / 128]) from the one-launch workspace:
-    sync area (256 + 128 bands bytes), codes [cap, K], scales [K / 128][cap]."""
-    bands = -(-max_tokens // 128)
-    cap = 128 * bands
+    sync area (256 + 128 bands bytes), codes [cap, K], scales [K / 128][cap],
+    with bands of 128 rows (256 on the _t256 form) and cap = bands x height."""
+    height = 256 if bound.steps[0].name.endswith("_t256") else 128
+    bands = -(-max_tokens // height)
+    cap = height * bands
     at = 256 + 128 * bands
     codes = bound.workspace.read(np.uint8, (cap, k), at)[:m]
     st = bound.workspace.read(np.float32, (k // 128, cap), at + -(-cap * k // 256) * 256)
     return codes, np.ascontiguousarray(st[:, :m].T)
 
 
+# (qkv and gate/up at 2048 rows, and every case from 512 rows of gate/up or
+# 3072 rows of o / down on, take the 256 x 256 form; the ragged and
+# single-band cases leave bands without live rows)
+T256 = {("qkv", 2048, 2048), ("gate_up", 2048, 2048), ("o", 4096, 4096), ("down", 3000, 3072),
+        ("gate_up", 700, 1024), ("gate_up", 200, 1024), ("qkv", 1800, 2048)}
+
+
 @pytest.mark.parametrize("op,m,max_tokens", [
     ("qkv", 2048, 2048), ("o", 2048, 2048), ("gate_up", 2048, 2048), ("down", 2048, 2048),
     ("o", 100, 256), ("down", 300, 512), ("qkv", 129, 256), ("gate_up", 1, 128),
+    ("o", 4096, 4096), ("down", 3000, 3072), ("gate_up", 700, 1024), ("gate_up", 200, 1024),
+    ("qkv", 1800, 2048),
 ])
 def test_block_scaled_w8a8(rt, op, m, max_tokens):
     rng = np.random.default_rng(13000 + 7 * m + max_tokens + len(op))
-    y, x, ws, bound = run_op(rt, rng, op, "w8a8", m, max_tokens, zero=(m == 100))
+    y, x, ws, bound = run_op(rt, rng, op, "w8a8", m, max_tokens, zero=m in (100, 700, 1800))
+    assert bound.steps[0].name.endswith("_t256") == ((op, m, max_tokens) in T256), bound.steps[0].name
     k = SHAPES[op][1]
     codes, scales = w8a8_quantized_rows(bound, m, k, max_tokens)
     q_ref, s_ref = o.quantize_rows(o.bf16_decode(x), group=128)
@@ -198,10 +210,13 @@ def test_block_scaled_w8a8(rt, op, m, max_tokens):
 ])
 def test_block_scaled_gated_mlp(rt, family, hidden, inter, m, max_tokens):
     """GatedMlp on block-scaled weights: W8A8 as one launch (four counted
-    steps) against the two block-scaled launches it replaces, bit for bit;
-    W8A16 as those two launches. The oracle checks stage by stage on the
-    device's own bf16 h (read from the workspace): gate/up, the h quantizer
-    (W8A8: codes and scales of the group quantizer), then down."""
+    steps) against the two block-scaled launches it replaces, bit for bit
+    where both run the same tile forms (a standalone launch of 192 or more
+    256 x 256 tiles takes the 256 x 256 form, whose sum order differs; the
+    chain is then checked against the oracle on its own h); W8A16 as those
+    two launches. The oracle checks stage by stage on the device's own bf16
+    h (read from the workspace): gate/up, the h quantizer (W8A8: codes and
+    scales of the group quantizer), then down."""
     rng = np.random.default_rng(14000 + m + hidden)
     (qg, sg), (qu, su) = spread_weight(rng, inter, hidden), spread_weight(rng, inter, hidden)
     qd, sd = spread_weight(rng, hidden, inter)
@@ -222,7 +237,10 @@ def test_block_scaled_gated_mlp(rt, family, hidden, inter, m, max_tokens):
         op.launch(rt.stream, synchronous=True)
         outs.append(ya.read(np.uint16, (max_tokens, hidden)))
         assert np.all(outs[-1][m:] == SENTINEL), "rows past M written"
-    assert np.array_equal(outs[0], outs[1]) and np.array_equal(outs[0], outs[2])
+    assert np.array_equal(outs[0], outs[2])
+    same_forms = not any(st.name.endswith("_t256") for st in two.steps)
+    if same_forms:
+        assert np.array_equal(outs[0], outs[1])
     y = outs[0][:m]
     # the device's h: the one-launch workspace (W8A8: sync area of three
     # steps, then the x rows: codes [cap, H], scales [H / 128][cap]) or the
@@ -240,22 +258,29 @@ def test_block_scaled_gated_mlp(rt, family, hidden, inter, m, max_tokens):
     else:
         h_gpu = two.workspace.read(np.uint16, (m, inter))
     rows, hcols = sample(rng, m, inter, 24, 192)
+    _, cols = sample(rng, m, hidden, 24, 128)
     xr = x_ref(x[rows], family)
     wgr, wur = deq_rows(qg, sg, hcols), deq_rows(qu, su, hcols)
     g, u = o.dense_projection(xr, wgr), o.dense_projection(xr, wur)
     tol = swiglu_midpoint_tol(g, u, abs_sum(xr, wgr), abs_sum(xr, wur), bound_k(hidden))
-    label = f"b128 gated mlp {family} h={hidden} m={m}"
-    parity(h_gpu[rows][:, hcols], o.silu_mul_array(g, u), label=label + " gate/up", midpoint_tol=tol)
-    hb = o.bf16_decode(h_gpu[rows])
-    if family == "w8a8":
-        hq_ref, hs_ref = o.quantize_rows(hb, group=128)
-        np.testing.assert_array_equal(hq_gpu[rows], hq_ref)
-        np.testing.assert_array_equal(hs_gpu[rows], hs_ref.reshape(len(rows), -1))
-        hb = o.dequantize(hq_ref, hs_ref, mode=1, group=128)
-    _, cols = sample(rng, m, hidden, 24, 128)
     wdr = deq_rows(qd, sd, cols)
-    parity(y[rows][:, cols], o.dense_projection(hb, wdr), k=bound_k(inter), s_abs=abs_sum(hb, wdr),
-           label=label + " down")
+
+    def check_stages(h_dev, y_dev, label, hq_dev=None, hs_dev=None):
+        parity(h_dev[rows][:, hcols], o.silu_mul_array(g, u), label=label + " gate/up", midpoint_tol=tol)
+        hb = o.bf16_decode(h_dev[rows])
+        if family == "w8a8":
+            hq_ref, hs_ref = o.quantize_rows(hb, group=128)
+            if hq_dev is not None:
+                np.testing.assert_array_equal(hq_dev[rows], hq_ref)
+                np.testing.assert_array_equal(hs_dev[rows], hs_ref.reshape(len(rows), -1))
+            hb = o.dequantize(hq_ref, hs_ref, mode=1, group=128)
+        parity(y_dev[rows][:, cols], o.dense_projection(hb, wdr), k=bound_k(inter), s_abs=abs_sum(hb, wdr),
+               label=label + " down")
+
+    label = f"b128 gated mlp {family} h={hidden} m={m}"
+    check_stages(h_gpu, y, label, *((hq_gpu, hs_gpu) if family == "w8a8" else ()))
+    if not same_forms:
+        check_stages(two.workspace.read(np.uint16, (m, inter)), outs[1][:m], label + " (two launches)")
 
 
 @pytest.mark.parametrize("m,max_tokens", [(1, 16), (24, 32), (100, 128)])
