@@ -203,7 +203,9 @@ enum lf_fp8_entry {
  *      lf_fp8_w8a8_gated_mlp_b128 (counts, x, wg, wu, wd, y, ws): GatedMlp
  *      in one launch (group quantizer, gate/up + SwiGLU, group quantizer of
  *      h, down), lunaflux_fp8_gated_mlp_geometry / _workspace_bytes with
- *      LF_FP8_ENTRY_W8A8_GATED_MLP_B128.
+ *      LF_FP8_ENTRY_W8A8_GATED_MLP_B128; lf_fp8_w8a8_gated_mlp_b128_t256
+ *      (the same operands, 512 threads) on 256 x 256 tiles where the
+ *      gate/up launch takes them and the hidden width is a multiple of 256.
  *  W8A16 shape-specialized (Llama-3-8B widths, profiles of <= 32 rows, as
  *      the per-channel ones): lf_fp8_w8a16_{dense,gate_up}_b128_k{K}_mM,
  *      lf_fp8_w8a16_qkv_b128_k4096_q4096_kv1024_mM (picked by

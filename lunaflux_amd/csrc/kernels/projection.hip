@@ -1563,22 +1563,42 @@ LF_DEVICE void w8a8_b128_v4_one_launch(const int32_t *counts, const uint16_t *x,
 
 // The block-scaled GatedMlp in one launch: x -> group quantizer -> gate/up
 // + SwiGLU -> h (bf16) -> group quantizer -> down, four counted steps as in
-// w8a8_gated_mlp (both GEMMs on 128 x 128 tiles). Workspace: sync area
-// (three steps of bands counters), B128Rows of x (K = H), h [cap, I] bf16,
-// B128Rows of h (K = I).
+// w8a8_gated_mlp, both GEMMs on 128 x 128 tiles of 4 waves or (WIDE) on
+// 256 x 256 tiles of 8 waves with 256-row bands (every step then runs
+// 512-thread blocks). Workspace: sync area (three steps of bands counters),
+// B128Rows of x (K = H), h [cap, I] bf16, B128Rows of h (K = I).
+template <bool WIDE, int MODE, bool THROUGH, class Gate>
+LF_DEVICE int w8a8_b128_form_gemm(uint8_t *smem, float *win, int M, const B128Rows &rows, int cap,
+                                  const uint8_t *w0, const uint8_t *w1, uint16_t *out, int bid, const Gate &gate) {
+  if constexpr (WIDE) {
+    return w8a8_b128_v4_gemm<B128V4Tile, 4, MODE, THROUGH>(smem, win, M, rows.codes, rows.scales_t, cap, w0, w1,
+                                                           w1, out, bid, gate);
+  } else {
+    return w8a8_b128_gemm<B128Tile, 4, MODE, THROUGH>(smem, win, M, rows.codes, rows.scales_t, cap, w0, w1, w1,
+                                                      out, bid, gate);
+  }
+}
+
+template <bool WIDE>
 LF_DEVICE void w8a8_b128_gated_mlp(const int32_t *counts, const uint16_t *x, const uint8_t *wg,
                                    const uint8_t *wu, const uint8_t *wd, uint16_t *y, uint8_t *ws) {
-  using T = B128Tile;
-  constexpr int BM = kB128BM;
+  using T = std::conditional_t<WIDE, B128V4Tile, B128Tile>;
+  constexpr int BM = WIDE ? kB128V4BM : kB128BM;
+  // (the 256 x 256 form's window: two k-tile slots, then the final scales)
+  constexpr int kWin = WIDE ? 3 * BM + 2 * T::kWaves : T::kStages * BM;
   __shared__ __attribute__((aligned(1024))) uint8_t smem[T::kSmem];
-  __shared__ __attribute__((aligned(16))) float win[T::kStages * BM];
+  __shared__ __attribute__((aligned(16))) float win[kWin];
   __shared__ phase::Flag flag;
   if (!dense_regions_ok<2, kScaleBlock128>(wg, wu, wu) || !dense_regions_ok<0, kScaleBlock128>(wd, wd, wd)) {
     return;
   }
   const int H = static_cast<int>(header_of(wg).columns), I = static_cast<int>(header_of(wg).rows);
   if (static_cast<int>(header_of(wd).columns) != I || static_cast<int>(header_of(wd).rows) != H) return;
-  const int gx1 = dense_gx<2, 128>(I), gx2 = dense_gx<0, 128>(H);
+  int gx1 = dense_gx<2, BM>(I), gx2 = dense_gx<0, BM>(H);  // (square tiles)
+  // (opaque to the optimizer: a range for H or I derived from the checks
+  // below reshapes the 256 x 256 main loop's prologue and tail, whose
+  // schedule then needs more than its 256 registers)
+  asm("" : "+s"(gx1), "+s"(gx2));
   const int blocks = static_cast<int>(gridDim.x) - 2 * kQuantBlocks;
   if (gx1 <= 0 || gx2 <= 0 || blocks <= 0 || blocks % (gx1 + gx2) != 0 || blockDim.x != T::kThreads) return;
   const int bands = blocks / (gx1 + gx2);
@@ -1591,7 +1611,7 @@ LF_DEVICE void w8a8_b128_gated_mlp(const int32_t *counts, const uint16_t *x, con
   const int M = live_rows(counts, cap);
   int b = static_cast<int>(blockIdx.x);
   if (b < kQuantBlocks) {  // step 0: x -> codes and group scales
-    b128_quantize(x, H, M, xr, cap, b, sync, 0);
+    b128_quantize<BM>(x, H, M, xr, cap, b, sync, 0);
     return;
   }
   b -= kQuantBlocks;
@@ -1600,8 +1620,7 @@ LF_DEVICE void w8a8_b128_gated_mlp(const int32_t *counts, const uint16_t *x, con
       const int band = m0 / BM;
       return phase::wait_for(sync, sync.band(0, band), chunks_in_band(M, band, BM), flag);
     };
-    const int band = w8a8_b128_gemm<T, 4, 2, true>(smem, win, M, xr.codes, xr.scales_t, cap, wg, wu, wu, h, b,
-                                                   gate);
+    const int band = w8a8_b128_form_gemm<WIDE, 2, true>(smem, win, M, xr, cap, wg, wu, h, b, gate);
     if (band >= 0) phase::signal(sync.band(1, band));
     return;
   }
@@ -1623,7 +1642,7 @@ LF_DEVICE void w8a8_b128_gated_mlp(const int32_t *counts, const uint16_t *x, con
     const int band = m0 / BM;
     return phase::wait_for(sync, sync.band(2, band), chunks_in_band(M, band, BM), flag);
   };
-  w8a8_b128_gemm<T, 4, 0>(smem, win, M, hr.codes, hr.scales_t, cap, wd, wd, wd, y, b, gate);
+  w8a8_b128_form_gemm<WIDE, 0, false>(smem, win, M, hr, cap, wd, wd, y, b, gate);
   phase::finish(sync, gx2 * bands, 3, flag);
 }
 
@@ -1799,7 +1818,14 @@ __global__ __launch_bounds__(256) void lf_fp8_w8a8_gated_mlp_b128(const int32_t 
                                                                   const uint8_t *wg, const uint8_t *wu,
                                                                   const uint8_t *wd, uint16_t *y,
                                                                   uint8_t *ws) {
-  w8a8_b128_gated_mlp(counts, x, wg, wu, wd, y, ws);
+  w8a8_b128_gated_mlp<false>(counts, x, wg, wu, wd, y, ws);
+}
+// The same on 256 x 256 tiles (eight waves, 256-row bands).
+__global__ __launch_bounds__(512) void lf_fp8_w8a8_gated_mlp_b128_t256(const int32_t *counts,
+                                                                       const uint16_t *x, const uint8_t *wg,
+                                                                       const uint8_t *wu, const uint8_t *wd,
+                                                                       uint16_t *y, uint8_t *ws) {
+  w8a8_b128_gated_mlp<true>(counts, x, wg, wu, wd, y, ws);
 }
 
 __global__ __launch_bounds__(256) void lf_fp8_act_quant_rows(const int32_t *counts,

@@ -380,6 +380,25 @@ bool w8a8_b128_tiles(bool gate_up, int64_t n, int64_t k, int32_t max_tokens, W8a
   return (k / 128) * (out->bands * out->bm) < INT32_MAX;
 }
 
+// Block-scaled W8A8 GatedMlp in one launch: both GEMMs on one band height,
+// 256 x 256 tiles (_t256, 512 threads) where the gate/up launch of the
+// shape takes them and the hidden width is a multiple of 256, else 128 x 128.
+// out: the band height, the gate/up plus down column blocks and the bands.
+bool w8a8_b128_gated(int64_t hidden, int64_t inter, int32_t max_tokens, W8a8B128 *out) {
+  int64_t bands = 0;
+  W8a8B128 up;
+  if (!w8a8_b128_bands(hidden, inter, max_tokens, &bands) || !w8a8_b128_bands(inter, hidden, max_tokens, &bands) ||
+      !w8a8_b128_tiles(true, inter, hidden, max_tokens, &up)) {
+    return false;
+  }
+  out->t256 = up.t256 && hidden % 256 == 0 && inter < (int64_t(1) << 24);
+  out->bm = out->t256 ? 256 : 128;
+  out->gx = inter / (out->bm / 2) + hidden / out->bm;
+  out->bands = (max_tokens + out->bm - 1) / out->bm;
+  const int64_t cap = out->bands * out->bm;
+  return (hidden / 128) * cap < INT32_MAX && (inter / 128) * cap < INT32_MAX;
+}
+
 // W8A8 GatedMlp in one launch: both GEMMs on 4-wave blocks of one band
 // height. Gate/up on 256 x 256 tiles where its own launch would take 256-row
 // tiles (down then on 256 x 256, or 256 x 128 where its own launch would
@@ -637,13 +656,10 @@ int64_t lunaflux_fp8_w8a16_workspace_bytes(int32_t entry, int64_t n, int64_t k,
 int64_t lunaflux_fp8_gated_mlp_workspace_bytes(int32_t entry, int64_t hidden, int64_t inter,
                                                int32_t max_tokens) {
   if (entry == LF_FP8_ENTRY_W8A8_GATED_MLP_B128) {
-    int64_t bands = 0;
-    if (hidden > kMaxDim || inter > kMaxDim || !w8a8_b128_bands(hidden, inter, max_tokens, &bands) ||
-        !w8a8_b128_bands(inter, hidden, max_tokens, &bands)) {
-      return -1;
-    }
-    const int64_t cap = bands * 128;
-    return sync_bytes(3, bands) + b128_rows_bytes(cap, hidden) + align_up(cap * inter * 2, 256) +
+    W8a8B128 g;
+    if (hidden > kMaxDim || inter > kMaxDim || !w8a8_b128_gated(hidden, inter, max_tokens, &g)) return -1;
+    const int64_t cap = g.bands * g.bm;
+    return sync_bytes(3, g.bands) + b128_rows_bytes(cap, hidden) + align_up(cap * inter * 2, 256) +
            b128_rows_bytes(cap, inter);
   }
   if (entry == LF_FP8_ENTRY_W8A8_GATED_MLP) {
@@ -689,18 +705,18 @@ int32_t lunaflux_fp8_gated_mlp_geometry(int32_t entry, int64_t hidden, int64_t i
     return LF_INVALID_ARGUMENT;
   }
   if (entry == LF_FP8_ENTRY_W8A8_GATED_MLP_B128) {
-    int64_t bands = 0;
-    if (hidden > kMaxDim || inter > kMaxDim || !w8a8_b128_bands(hidden, inter, max_tokens, &bands) ||
-        !w8a8_b128_bands(inter, hidden, max_tokens, &bands)) {
+    W8a8B128 g;
+    if (hidden > kMaxDim || inter > kMaxDim || !w8a8_b128_gated(hidden, inter, max_tokens, &g)) {
       return LF_INVALID_ARGUMENT;
     }
-    // x quantizer, gate/up tiles (64 h-columns each), h quantizer, down tiles
-    const int64_t blocks = 2 * kQuantBlocks + (inter / 64 + hidden / 128) * bands;
+    // x quantizer, gate/up tiles (bm / 2 h-columns each), h quantizer, down
+    // tiles
+    const int64_t blocks = 2 * kQuantBlocks + g.gx * g.bands;
     if (blocks > INT32_MAX) return LF_INVALID_ARGUMENT;
-    const int32_t values[7] = {static_cast<int32_t>(blocks), 1, 1, 256, 1, 1, 0};
+    const int32_t values[7] = {static_cast<int32_t>(blocks), 1, 1, static_cast<int32_t>(2 * g.bm), 1, 1, 0};
     std::memcpy(dims, values, sizeof(values));
     std::memset(symbol, 0, LF_FP8_SYMBOL_BYTES);
-    std::snprintf(symbol, LF_FP8_SYMBOL_BYTES, "lf_fp8_w8a8_gated_mlp_b128");
+    std::snprintf(symbol, LF_FP8_SYMBOL_BYTES, "lf_fp8_w8a8_gated_mlp_b128%s", g.t256 ? "_t256" : "");
     return LF_OK;
   }
   if (entry == LF_FP8_ENTRY_W8A8_GATED_MLP) {

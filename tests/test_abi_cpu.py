@@ -358,13 +358,20 @@ def test_block_scaled_geometry_and_workspace():
         assert fp8.w8a8_workspace_bytes(entry, n, k, m) == want
     d, sym = fp8.launch_geometry(_abi.ENTRY_W8A8_QKV_B128, 6144, 4096, 2048, qkv_split=(4096, 1024))
     assert sym == "lf_fp8_w8a8_qkv_b128_t256" and d.grid == (256 + 24 * 8, 1, 1)
+    # block-scaled W8A8 GatedMlp: 128 x 128 tiles, or 256 x 256 ones (256-row
+    # bands, 512 threads) where the gate/up launch takes them and the hidden
+    # width is a multiple of 256
     e = _abi.ENTRY_W8A8_GATED_MLP_B128
-    d, sym = fp8.gated_mlp_geometry(4096, 14336, 2048, e)
-    bands, cap = 16, 2048
-    assert sym == "lf_fp8_w8a8_gated_mlp_b128" and d.grid == (512 + (224 + 32) * bands, 1, 1)
-    want = (256 + 128 * 3 * bands + al(cap * 4096) + al(32 * cap * 4) + al(cap * 14336 * 2)
-            + al(cap * 14336) + al(112 * cap * 4))
-    assert lib.lunaflux_fp8_gated_mlp_workspace_bytes(e, 4096, 14336, 2048) == want
+    for h, i, m, bm in [(4096, 14336, 2048, 256), (4096, 14336, 300, 256), (4096, 14336, 256, 128),
+                        (4096 + 128, 14336, 2048, 128), (512, 1024, 100, 128)]:
+        d, sym = fp8.gated_mlp_geometry(h, i, m, e)
+        bands = -(-m // bm)
+        cap = bm * bands
+        assert sym == "lf_fp8_w8a8_gated_mlp_b128" + ("_t256" if bm == 256 else ""), (h, i, m, sym)
+        assert d.grid == (512 + (i // (bm // 2) + h // bm) * bands, 1, 1) and d.block == (2 * bm, 1, 1)
+        want = (256 + 128 * 3 * bands + al(cap * h) + al(h // 128 * cap * 4) + al(cap * i * 2)
+                + al(cap * i) + al(i // 128 * cap * 4))
+        assert lib.lunaflux_fp8_gated_mlp_workspace_bytes(e, h, i, m) == want
     assert lib.lunaflux_fp8_gated_mlp_workspace_bytes(e, 4096 + 64, 14336, 2048) == -1
     # W8A16 GatedMlp in one launch on block-scaled weights: the per-channel
     # one-launch forms' geometry and workspace under the _b128 symbols; none
