@@ -3,8 +3,12 @@
 //
 // At 128 rows every weight byte feeds 128 rows of MFMA work. A block of 8
 // waves (two per SIMD, so one wave's LDS reads overlap the other's MFMAs)
-// owns a 128-row x BN-column output tile over one K-slice, as a 4 x 2 grid
-// of 32 x BN/2 wave tiles. Each 128-deep k-step needs the activation tile
+// owns a 128-row x BN-column output tile over one K-slice, as a WGM x WGN
+// grid of wave tiles: 2 x 4 tiles of 64 x 32 at BN = 128 (each weight tile
+// converted to bf16 by two waves instead of four: down and qkv at 128 rows
+// 0.4-1.1 us faster than 4 x 2), 4 x 2 tiles of 32 x 32 at BN = 64 (a wave
+// column needs an even count of 16-column fragments for gate/up's pairs).
+// Each 128-deep k-step needs the activation tile
 // (128 rows x 128 bf16 = 32 KiB, an L2 hit: every block reads the same x)
 // and BN / 16 weight tiles (e4m3, 2 KiB each, copied verbatim from the
 // pre-swizzled region; HBM). Both go global -> LDS with global_load_lds
@@ -208,19 +212,31 @@ __device__ __forceinline__ void w8a16_gemm_kernel(uint8_t *smem, const int32_t *
 
   const uint32_t smem_base = __builtin_amdgcn_readfirstlane(w8a8v3::lds_offset_of(smem));
   const uint32_t b_base = smem_base + NSA * T::kAStage;
-  // Stage i (k-tile kt0 + i) into its ring slot.
+  // Step i of the slice runs k-tile kt0 + ktile(i). Unsplit (S == 1): the
+  // k-tiles from (block / 8) mod nkt on, wrapping around. Blocks are
+  // dispatched to the 8 XCDs in turn, so the column blocks sharing one L2
+  // read different k-tiles of x at a time instead of the same few L2
+  // channels (gate/up at 128 rows: 1.1-2.0 us less per launch). Split
+  // launches keep the plain order: their blocks read disjoint slices, and
+  // o at 128 rows (three slices) was 0.2-0.4 us slower rotated.
+  const int nkt = kt1 - kt0;
+  const int rot = S == 1 ? (block >> 3) % nkt : 0;
+  auto ktile = [&](int i) { return i + rot < nkt ? i + rot : i + rot - nkt; };
+  // Stage i (k-tile kt0 + ktile(i)) into its ring slot.
   auto issue_a = [&](int i) {
     const uint32_t dst = smem_base + (i % NSA) * T::kAStage + lw * T::kAIns * 1024;
+    const int kt = kt0 + ktile(i);
 #pragma unroll
     for (int q = 0; q < T::kAIns; ++q) {
-      w8a8v3::dma16(a_src[q] + (kt0 + i) * 256, dst + q * 1024);
+      w8a8v3::dma16(a_src[q] + kt * 256, dst + q * 1024);
     }
   };
   auto issue_b = [&](int i) {
     const uint32_t dst = b_base + (i % NSB) * T::kBStage + lw * T::kBIns * 1024;
+    const int kt = kt0 + ktile(i);
 #pragma unroll
     for (int q = 0; q < T::kBIns; ++q) {
-      w8a8v3::dma16(b_src[q] + static_cast<uint64_t>(kt0 + i) * kTileBytes, dst + q * 1024);
+      w8a8v3::dma16(b_src[q] + static_cast<uint64_t>(kt) * kTileBytes, dst + q * 1024);
     }
   };
 
@@ -230,7 +246,6 @@ __device__ __forceinline__ void w8a16_gemm_kernel(uint8_t *smem, const int32_t *
 #pragma unroll
     for (int j = 0; j < T::kFN; ++j) acc[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
 
-  const int nkt = kt1 - kt0;
   if (!a_loader) {
     for (int i = 0; i < NSB - 1 && i < nkt; ++i) issue_b(i);
   }
@@ -279,7 +294,7 @@ __device__ __forceinline__ void w8a16_gemm_kernel(uint8_t *smem, const int32_t *
     float sb[BLOCK ? T::kFN : 1];
     if constexpr (BLOCK) {
 #pragma unroll
-      for (int j = 0; j < T::kFN; ++j) sb[j] = bs[j][k];
+      for (int j = 0; j < T::kFN; ++j) sb[j] = bs[j][ktile(k)];
     }
 #pragma unroll
     for (int step = 0; step < 4; ++step) {
@@ -517,7 +532,7 @@ extern "C" {
   }
 
 LF_W16_GEMM_ENTRIES(64, 4, 2, 4, 2)
-LF_W16_GEMM_ENTRIES(128, 4, 2, 2, 4)
+LF_W16_GEMM_ENTRIES(128, 2, 4, 2, 4)
 
 // The same over weights with 128 x 128 block scales:
 // lf_fp8_w8a16_{op}_b128_m128_n{BN}.
@@ -543,31 +558,31 @@ LF_W16_GEMM_ENTRIES(128, 4, 2, 2, 4)
   }
 
 LF_W16_GEMM_B128_ENTRIES(64, 4, 2, 4, 2)
-LF_W16_GEMM_B128_ENTRIES(128, 4, 2, 2, 4)
+LF_W16_GEMM_B128_ENTRIES(128, 2, 4, 2, 4)
 
 // One-launch GatedMlp for profiles of 65..128 rows, any H and I the forms
 // divide: gate/up on the n128 tiles (one K-slice), down on n128 or n64 (the
 // tile and split its own launch would take), operands (counts, x, wg, wu,
 // wd, y, ws).
-#define LF_W16_GEMM_GATED_MLP(DN_BN, DN_NSA, DN_NSB)                                             \
+#define LF_W16_GEMM_GATED_MLP(DN_BN, DN_NSA, DN_NSB, WGM, WGN)                                   \
   __global__ __launch_bounds__(512) void lf_fp8_w8a16_gated_mlp_m128_n128_n##DN_BN(               \
       const int32_t *counts, const uint16_t *x, const uint8_t *wg, const uint8_t *wu,            \
       const uint8_t *wd, uint16_t *y, uint8_t *ws) {                                             \
-    w16g::GatedMlpGemm<128, DN_BN, 4, 2, 2, 4, DN_NSA, DN_NSB>::run(counts, x, wg, wu, wd, y, ws); \
+    w16g::GatedMlpGemm<128, DN_BN, WGM, WGN, 2, 4, DN_NSA, DN_NSB>::run(counts, x, wg, wu, wd, y, ws); \
   }
 
-LF_W16_GEMM_GATED_MLP(128, 2, 4)
-LF_W16_GEMM_GATED_MLP(64, 4, 2)
+LF_W16_GEMM_GATED_MLP(128, 2, 4, 2, 4)
+LF_W16_GEMM_GATED_MLP(64, 4, 2, 4, 2)
 
 // The same over weights with 128 x 128 block scales.
-#define LF_W16_GEMM_GATED_MLP_B128(DN_BN, DN_NSA, DN_NSB)                                        \
+#define LF_W16_GEMM_GATED_MLP_B128(DN_BN, DN_NSA, DN_NSB, WGM, WGN)                              \
   __global__ __launch_bounds__(512) void lf_fp8_w8a16_gated_mlp_b128_m128_n128_n##DN_BN(          \
       const int32_t *counts, const uint16_t *x, const uint8_t *wg, const uint8_t *wu,            \
       const uint8_t *wd, uint16_t *y, uint8_t *ws) {                                             \
-    w16g::GatedMlpGemm<128, DN_BN, 4, 2, 2, 4, DN_NSA, DN_NSB, true>::run(counts, x, wg, wu, wd, y, ws); \
+    w16g::GatedMlpGemm<128, DN_BN, WGM, WGN, 2, 4, DN_NSA, DN_NSB, true>::run(counts, x, wg, wu, wd, y, ws); \
   }
 
-LF_W16_GEMM_GATED_MLP_B128(128, 2, 4)
-LF_W16_GEMM_GATED_MLP_B128(64, 4, 2)
+LF_W16_GEMM_GATED_MLP_B128(128, 2, 4, 2, 4)
+LF_W16_GEMM_GATED_MLP_B128(64, 4, 2, 4, 2)
 
 }  // extern "C"
