@@ -1107,6 +1107,13 @@ using GemmT256 = FormV5<w8a8v5::Tile, 4>;
 using GemmT256x128 = FormV5<w8a8v5::TileN128, 4>;
 using GemmT256w8 = FormW8<w8a8v4::Tile<256, 256, 4, 4, 2>, 4>;
 using GemmT128 = FormT128<w8a8v3::Tile<128, 128, 2, 2, 2>, 4>;
+// The same forms in the striped tile order (tile_of_block, group < 0), for
+// the one-launch GatedMlp: every XCD works on the same group of row bands
+// at a time, so the h quantizer and down steps find the first bands
+// complete while gate/up's last tiles still run.
+using GemmT256S = FormV5<w8a8v5::Tile, -4>;
+using GemmT256x128S = FormV5<w8a8v5::TileN128, -4>;
+using GemmT128S = FormT128<w8a8v3::Tile<128, 128, 2, 2, 2>, -4>;
 
 // ---------------------------------------------------------------------------
 // One launch per W8A8 operation. The plan binds each operation to one AOT
@@ -1778,9 +1785,9 @@ LF_W8A8_ENTRIES(t128, GemmT128)
     w8a8_gated_mlp<GU, DN>(counts, x, wg, wu, wd, y, ws);                                      \
   }
 
-LF_W8A8_GATED_MLP(t256_t256, GemmT256, GemmT256)
-LF_W8A8_GATED_MLP(t256_t256x128, GemmT256, GemmT256x128)
-LF_W8A8_GATED_MLP(t128_t128, GemmT128, GemmT128)
+LF_W8A8_GATED_MLP(t256_t256, GemmT256S, GemmT256S)
+LF_W8A8_GATED_MLP(t256_t256x128, GemmT256S, GemmT256x128S)
+LF_W8A8_GATED_MLP(t128_t128, GemmT128S, GemmT128S)
 
 // Block-scaled (128 x 128 weight blocks, 128-column activation groups) W8A8
 // operations, one launch each: (counts, x, w..., y, ws).

@@ -248,9 +248,25 @@ LF_DEVICE int acc_row(int wm, int i, int lane, int rr) {
 // b: the block's index in the GEMM's part of the grid (blockIdx.x when the
 // GEMM is the whole grid; a one-launch operation puts other steps' blocks
 // first, in a multiple of 8 so that b % 8 is still the XCD).
+// group < 0 (striped order, when gx is a multiple of 8): XCD x takes the
+// columns x, x + 8, ... and every XCD walks the same groups of -group row
+// blocks in turn (inside a group: column by column, down its rows), so the
+// first row blocks are done early across the chip instead of every XCD
+// finishing its own rows at the end; a column's row tiles still run on one
+// XCD, back to back.
 LF_DEVICE bool tile_of_block(int b, int gx, int gy, int group, int &bx, int &by) {
   const int tiles = gx * gy;
   if (b >= tiles) return false;
+  if (group < 0 && (gx & 7) == 0) {
+    const int g = -group, cx = gx >> 3, xcd = b & 7, local = b >> 3;
+    const int first = local / (g * cx) * g;
+    const int rows = gy - first < g ? gy - first : g;
+    const int in = local - first * cx;
+    by = first + in % rows;
+    bx = (in / rows) * 8 + xcd;
+    return true;
+  }
+  if (group < 0) group = -group;
   const int xcd = b & 7, local = b >> 3;
   const int base = tiles >> 3, extra = tiles & 7;
   const int t = xcd * base + (xcd < extra ? xcd : extra) + local;
