@@ -356,13 +356,16 @@ def test_block_scaled_admission(rt):
         assert e.value.status == _abi.LF_UNSUPPORTED
 
 
-def test_block_scaled_w8a8_sticky_error(rt):
-    """The counted wait of the block-scaled one-launch entry, forced from the
-    host as for the _aq entries: a band counter preset far below its target
-    runs the wait out, the binding raises and zero-fills its workspace, and
-    the next launch is correct."""
-    rng = np.random.default_rng(15100)
-    k, n, max_tokens, m = 256, 512, 256, 200
+@pytest.mark.parametrize("n,max_tokens,m,symbol", [
+    (512, 256, 200, "lf_fp8_w8a8_dense_b128"), (4096, 3072, 3000, "lf_fp8_w8a8_dense_b128_t256"),
+])
+def test_block_scaled_w8a8_sticky_error(rt, n, max_tokens, m, symbol):
+    """The counted wait of the block-scaled one-launch entry (both tile
+    forms), forced from the host as for the _aq entries: a band counter
+    preset far below its target runs the wait out, the binding raises and
+    zero-fills its workspace, and the next launch is correct."""
+    rng = np.random.default_rng(15100 + n)
+    k = 256
     q, s = spread_weight(rng, n, k)
     w = upload(rt, q, s)
     xa = rt.context.allocate(max_tokens * k * 2)
@@ -371,6 +374,7 @@ def test_block_scaled_w8a8_sticky_error(rt):
     xa.copy_from_host(np.concatenate([x, np.zeros((max_tokens - m, k), np.uint16)]))
     one = rt.bind_dense("w8a8", rt.step_counts(m), _region(xa, alignment=256), w,
                         _region(ya, alignment=256), max_tokens)
+    assert one.steps[0].name == symbol, one.steps[0].name
     one.launch(rt.stream, synchronous=True)
     want = ya.read(np.uint16, (max_tokens, n))
     ws = one.workspace
@@ -381,3 +385,32 @@ def test_block_scaled_w8a8_sticky_error(rt):
     assert not ws.read(np.uint8, (ws.byte_count,)).any(), "workspace not zero-filled"
     one.launch(rt.stream, synchronous=True)
     assert np.array_equal(ya.read(np.uint16, (max_tokens, n))[:m], want[:m])
+
+
+def test_block_scaled_w8a8_gated_mlp_sticky_error(rt):
+    """The same for the block-scaled GatedMlp on 256 x 256 tiles (hidden 256,
+    intermediate 4096, 2048 rows): the x band counter preset far below its
+    target runs the gate/up wait out, every later step's wait sees the error
+    word, the binding raises and zero-fills the workspace, and the next
+    launch gives the first launch's bits."""
+    rng = np.random.default_rng(15200)
+    hidden, inter, max_tokens, m = 256, 4096, 2048, 2000
+    (qg, sg), (qu, su) = spread_weight(rng, inter, hidden), spread_weight(rng, inter, hidden)
+    qd, sd = spread_weight(rng, hidden, inter)
+    wg, wu, wd = upload(rt, qg, sg), upload(rt, qu, su), upload(rt, qd, sd)
+    x = spread_activations(rng, m, hidden)
+    xa = rt.context.upload(np.concatenate([x, np.zeros((max_tokens - m, hidden), np.uint16)]))
+    ya = rt.context.allocate(max_tokens * hidden * 2)
+    one = rt.bind_gated_mlp("w8a8", rt.step_counts(m), _region(xa, alignment=256), wg, wu, wd,
+                            _region(ya, alignment=256), max_tokens)
+    assert len(one.steps) == 1 and one.steps[0].name == "lf_fp8_w8a8_gated_mlp_b128_t256", one.steps
+    one.launch(rt.stream, synchronous=True)
+    want = ya.read(np.uint16, (max_tokens, hidden))
+    ws = one.workspace
+    ws.copy_from_host(np.array([-(1 << 30)], np.int32), offset=256)
+    ya.copy_from_host(np.full(max_tokens * hidden, SENTINEL, np.uint16))
+    with pytest.raises(DeviceError):
+        one.launch(rt.stream, synchronous=True)
+    assert not ws.read(np.uint8, (ws.byte_count,)).any(), "workspace not zero-filled"
+    one.launch(rt.stream, synchronous=True)
+    assert np.array_equal(ya.read(np.uint16, (max_tokens, hidden))[:m], want[:m])
