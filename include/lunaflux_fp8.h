@@ -195,9 +195,11 @@ enum lf_fp8_entry {
  *      launch each: x quantized per token per 128-column group (amax over
  *      the group, the per-token quantizer's arithmetic) inside the launch,
  *      then y = sum_kt sa[m][kt] s[n / 128][kt] sum_{k in kt} qa_mk q_nk on
- *      128 x 128 tiles, or, from 192 tiles of 256 x 256 on (widths multiples
- *      of 256; gate/up: of 128), lf_fp8_w8a8_{op}_b128_t256 on such tiles
- *      (512 threads). ws: lunaflux_fp8_w8a8_workspace_bytes with the _B128
+ *      256-row bands: lf_fp8_w8a8_{op}_b128_t256 (256 x 256 tiles, from 192
+ *      such tiles on; widths multiples of 256, gate/up: of 128) or
+ *      lf_fp8_w8a8_{op}_b128_t256x128 (256 x 128 tiles), 512 threads; for
+ *      K >= 2^24 lf_fp8_w8a8_{op}_b128 on 128 x 128 tiles (256 threads,
+ *      128-row bands). ws: lunaflux_fp8_w8a8_workspace_bytes with the _B128
  *      entry (it follows the form), error word at LF_FP8_AQ_ERROR_OFFSET as
  *      for the _AQ entries.
  *      lf_fp8_w8a8_gated_mlp_b128 (counts, x, wg, wu, wd, y, ws): GatedMlp

@@ -1299,6 +1299,9 @@ LF_DEVICE void w8a8_b128_one_launch(const int32_t *counts, const uint16_t *x, co
 // scales are scalar loads.
 // ---------------------------------------------------------------------------
 using B128V4Tile = w8a8v4::Tile<256, 256, 4, 4, 2>;
+// 256 x 128 tiles: eight waves of 32 x 128 (each wave's columns still one
+// 128-column block), for launches with too few 256 x 256 tiles
+using B128V4TileN128 = w8a8v4::Tile<256, 128, 4, 8, 1>;
 constexpr int kB128V4BM = 256;
 
 // Side loads (w8a8v4 mainloop SIDE): stage s loads the 256 row scales of
@@ -1534,12 +1537,11 @@ LF_DEVICE int w8a8_b128_v4_gemm(uint8_t *smem, float *win, int M, const uint8_t 
   return by;
 }
 
-// The block-scaled operations in one launch on the 256 x 256 form: as
-// w8a8_b128_one_launch with 256-row bands (cap = bands x 256).
-template <int MODE>
+// The block-scaled operations in one launch on the 256 x 256 (or 256 x 128)
+// form: as w8a8_b128_one_launch with 256-row bands (cap = bands x 256).
+template <class T, int MODE>
 LF_DEVICE void w8a8_b128_v4_one_launch(const int32_t *counts, const uint16_t *x, const uint8_t *w0,
                                        const uint8_t *w1, const uint8_t *w2, uint16_t *y, uint8_t *ws) {
-  using T = B128V4Tile;
   constexpr int BM = kB128V4BM;
   __shared__ __attribute__((aligned(1024))) uint8_t smem[T::kSmem];
   __shared__ __attribute__((aligned(16))) float win[2 * BM + BM + 2 * T::kWaves];
@@ -1568,40 +1570,55 @@ LF_DEVICE void w8a8_b128_v4_one_launch(const int32_t *counts, const uint16_t *x,
   phase::finish(sync, blocks, 1, flag);
 }
 
-// The block-scaled GatedMlp in one launch: x -> group quantizer -> gate/up
-// + SwiGLU -> h (bf16) -> group quantizer -> down, four counted steps as in
-// w8a8_gated_mlp, both GEMMs on 128 x 128 tiles of 4 waves or (WIDE) on
-// 256 x 256 tiles of 8 waves with 256-row bands (every step then runs
-// 512-thread blocks). Workspace: sync area (three steps of bands counters),
-// B128Rows of x (K = H), h [cap, I] bf16, B128Rows of h (K = I).
-template <bool WIDE, int MODE, bool THROUGH, class Gate>
+// Block-scaled tile forms of the one-launch GatedMlp: 0 = 128 x 128 (4
+// waves), 2 = 256 x 256 (8 waves). (The 256 x 128 form of the standalone
+// entries is not built here: in this kernel its gate/up step returned
+// nondeterministic values in a few accumulator elements of one column
+// fragment, different rows on every launch, with the cause not found; the
+// standalone 256 x 128 entries measure bit-identical to 256 x 256.)
+template <int FORM>
+struct B128Form {
+  static_assert(FORM == 0 || FORM == 2, "GatedMlp tile forms");
+  using T = std::conditional_t<FORM == 2, B128V4Tile, std::conditional_t<FORM == 1, B128V4TileN128, B128Tile>>;
+  static constexpr int kBM = FORM ? kB128V4BM : kB128BM, kBN = FORM == 2 ? 256 : 128;
+  // LDS scale window: (256-row forms) two k-tile slots, then the final
+  // scales; (128 x 128) one slot per stage
+  static constexpr int kWin = FORM ? 3 * kBM + 2 * T::kWaves : T::kStages * kBM;
+};
+
+template <int FORM, int MODE, bool THROUGH, class Gate>
 LF_DEVICE int w8a8_b128_form_gemm(uint8_t *smem, float *win, int M, const B128Rows &rows, int cap,
                                   const uint8_t *w0, const uint8_t *w1, uint16_t *out, int bid, const Gate &gate) {
-  if constexpr (WIDE) {
-    return w8a8_b128_v4_gemm<B128V4Tile, 4, MODE, THROUGH>(smem, win, M, rows.codes, rows.scales_t, cap, w0, w1,
-                                                           w1, out, bid, gate);
+  if constexpr (FORM != 0) {
+    return w8a8_b128_v4_gemm<typename B128Form<FORM>::T, 4, MODE, THROUGH>(smem, win, M, rows.codes, rows.scales_t,
+                                                                          cap, w0, w1, w1, out, bid, gate);
   } else {
     return w8a8_b128_gemm<B128Tile, 4, MODE, THROUGH>(smem, win, M, rows.codes, rows.scales_t, cap, w0, w1, w1,
                                                       out, bid, gate);
   }
 }
 
-template <bool WIDE>
+// The block-scaled GatedMlp in one launch: x -> group quantizer -> gate/up
+// + SwiGLU -> h (bf16) -> group quantizer -> down, four counted steps as in
+// w8a8_gated_mlp, both GEMMs on one tile form (B128Form; the 256-row forms
+// run 512-thread blocks in every step). Workspace: sync area (three steps
+// of bands counters), B128Rows of x (K = H), h [cap, I] bf16, B128Rows of h
+// (K = I).
+template <int FORM>
 LF_DEVICE void w8a8_b128_gated_mlp(const int32_t *counts, const uint16_t *x, const uint8_t *wg,
                                    const uint8_t *wu, const uint8_t *wd, uint16_t *y, uint8_t *ws) {
-  using T = std::conditional_t<WIDE, B128V4Tile, B128Tile>;
-  constexpr int BM = WIDE ? kB128V4BM : kB128BM;
-  // (the 256 x 256 form's window: two k-tile slots, then the final scales)
-  constexpr int kWin = WIDE ? 3 * BM + 2 * T::kWaves : T::kStages * BM;
+  using F = B128Form<FORM>;
+  using T = typename F::T;
+  constexpr int BM = F::kBM;
   __shared__ __attribute__((aligned(1024))) uint8_t smem[T::kSmem];
-  __shared__ __attribute__((aligned(16))) float win[kWin];
+  __shared__ __attribute__((aligned(16))) float win[F::kWin];
   __shared__ phase::Flag flag;
   if (!dense_regions_ok<2, kScaleBlock128>(wg, wu, wu) || !dense_regions_ok<0, kScaleBlock128>(wd, wd, wd)) {
     return;
   }
   const int H = static_cast<int>(header_of(wg).columns), I = static_cast<int>(header_of(wg).rows);
   if (static_cast<int>(header_of(wd).columns) != I || static_cast<int>(header_of(wd).rows) != H) return;
-  int gx1 = dense_gx<2, BM>(I), gx2 = dense_gx<0, BM>(H);  // (square tiles)
+  int gx1 = dense_gx<2, F::kBN>(I), gx2 = dense_gx<0, F::kBN>(H);
   // (opaque to the optimizer: a range for H or I derived from the checks
   // below reshapes the 256 x 256 main loop's prologue and tail, whose
   // schedule then needs more than its 256 registers)
@@ -1627,7 +1644,7 @@ LF_DEVICE void w8a8_b128_gated_mlp(const int32_t *counts, const uint16_t *x, con
       const int band = m0 / BM;
       return phase::wait_for(sync, sync.band(0, band), chunks_in_band(M, band, BM), flag);
     };
-    const int band = w8a8_b128_form_gemm<WIDE, 2, true>(smem, win, M, xr, cap, wg, wu, h, b, gate);
+    const int band = w8a8_b128_form_gemm<FORM, 2, true>(smem, win, M, xr, cap, wg, wu, h, b, gate);
     if (band >= 0) phase::signal(sync.band(1, band));
     return;
   }
@@ -1649,7 +1666,7 @@ LF_DEVICE void w8a8_b128_gated_mlp(const int32_t *counts, const uint16_t *x, con
     const int band = m0 / BM;
     return phase::wait_for(sync, sync.band(2, band), chunks_in_band(M, band, BM), flag);
   };
-  w8a8_b128_form_gemm<WIDE, 0, false>(smem, win, M, hr, cap, wd, wd, y, b, gate);
+  w8a8_b128_form_gemm<FORM, 0, false>(smem, win, M, hr, cap, wd, wd, y, b, gate);
   phase::finish(sync, gx2 * bands, 3, flag);
 }
 
@@ -1809,30 +1826,49 @@ __global__ __launch_bounds__(256) void lf_fp8_w8a8_gate_up_b128(const int32_t *c
 // such tiles (lunaflux_fp8_launch_geometry picks the form).
 __global__ __launch_bounds__(512) void lf_fp8_w8a8_dense_b128_t256(const int32_t *counts, const uint16_t *x,
                                                                    const uint8_t *w, uint16_t *y, uint8_t *ws) {
-  w8a8_b128_v4_one_launch<0>(counts, x, w, w, w, y, ws);
+  w8a8_b128_v4_one_launch<B128V4Tile, 0>(counts, x, w, w, w, y, ws);
 }
 __global__ __launch_bounds__(512) void lf_fp8_w8a8_qkv_b128_t256(const int32_t *counts, const uint16_t *x,
                                                                  const uint8_t *wq, const uint8_t *wk,
                                                                  const uint8_t *wv, uint16_t *y, uint8_t *ws) {
-  w8a8_b128_v4_one_launch<1>(counts, x, wq, wk, wv, y, ws);
+  w8a8_b128_v4_one_launch<B128V4Tile, 1>(counts, x, wq, wk, wv, y, ws);
 }
 __global__ __launch_bounds__(512) void lf_fp8_w8a8_gate_up_b128_t256(const int32_t *counts, const uint16_t *x,
                                                                      const uint8_t *wg, const uint8_t *wu,
                                                                      uint16_t *h, uint8_t *ws) {
-  w8a8_b128_v4_one_launch<2>(counts, x, wg, wu, wu, h, ws);
+  w8a8_b128_v4_one_launch<B128V4Tile, 2>(counts, x, wg, wu, wu, h, ws);
+}
+// The same on 256 x 128 tiles (eight waves of 32 x 128), where 256 x 256
+// tiles would be too few.
+__global__ __launch_bounds__(512) void lf_fp8_w8a8_dense_b128_t256x128(const int32_t *counts,
+                                                                       const uint16_t *x, const uint8_t *w,
+                                                                       uint16_t *y, uint8_t *ws) {
+  w8a8_b128_v4_one_launch<B128V4TileN128, 0>(counts, x, w, w, w, y, ws);
+}
+__global__ __launch_bounds__(512) void lf_fp8_w8a8_qkv_b128_t256x128(const int32_t *counts, const uint16_t *x,
+                                                                     const uint8_t *wq, const uint8_t *wk,
+                                                                     const uint8_t *wv, uint16_t *y,
+                                                                     uint8_t *ws) {
+  w8a8_b128_v4_one_launch<B128V4TileN128, 1>(counts, x, wq, wk, wv, y, ws);
+}
+__global__ __launch_bounds__(512) void lf_fp8_w8a8_gate_up_b128_t256x128(const int32_t *counts,
+                                                                         const uint16_t *x, const uint8_t *wg,
+                                                                         const uint8_t *wu, uint16_t *h,
+                                                                         uint8_t *ws) {
+  w8a8_b128_v4_one_launch<B128V4TileN128, 2>(counts, x, wg, wu, wu, h, ws);
 }
 __global__ __launch_bounds__(256) void lf_fp8_w8a8_gated_mlp_b128(const int32_t *counts, const uint16_t *x,
                                                                   const uint8_t *wg, const uint8_t *wu,
                                                                   const uint8_t *wd, uint16_t *y,
                                                                   uint8_t *ws) {
-  w8a8_b128_gated_mlp<false>(counts, x, wg, wu, wd, y, ws);
+  w8a8_b128_gated_mlp<0>(counts, x, wg, wu, wd, y, ws);
 }
 // The same on 256 x 256 tiles (eight waves, 256-row bands).
 __global__ __launch_bounds__(512) void lf_fp8_w8a8_gated_mlp_b128_t256(const int32_t *counts,
                                                                        const uint16_t *x, const uint8_t *wg,
                                                                        const uint8_t *wu, const uint8_t *wd,
                                                                        uint16_t *y, uint8_t *ws) {
-  w8a8_b128_gated_mlp<true>(counts, x, wg, wu, wd, y, ws);
+  w8a8_b128_gated_mlp<2>(counts, x, wg, wu, wd, y, ws);
 }
 
 __global__ __launch_bounds__(256) void lf_fp8_act_quant_rows(const int32_t *counts,

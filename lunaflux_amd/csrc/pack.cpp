@@ -359,31 +359,38 @@ bool w8a8_b128_bands(int64_t n, int64_t k, int32_t max_tokens, int64_t *bands) {
   *bands = (max_tokens + 127) / 128;
   return (k / 128) * (*bands * 128) < INT32_MAX;
 }
-// The standalone block-scaled entries also have a 256 x 256 form of 8 waves
-// (_b128_t256, 256-row bands) for profiles of at least kB128T256Tiles such
-// tiles, where the width is a multiple of its tile (256 columns; gate/up:
-// 128 outputs) and activation offsets fit 32 bits (K < 2^24).
+// The standalone block-scaled entries run 256-row bands on 8 waves: 256 x
+// 256 tiles (_b128_t256) for profiles of at least kB128T256Tiles such tiles
+// where the width is a multiple of that tile (256 columns; gate/up: 128
+// outputs), else 256 x 128 tiles (_b128_t256x128; faster than 128 x 128 at
+// every profile measured, 128-8192 rows). Both use 32-bit activation
+// offsets (K < 2^24); past that, 128 x 128 tiles of 4 waves (_b128).
 constexpr int64_t kB128T256Tiles = 192;
 struct W8a8B128 {
-  bool t256;
+  int form;               // 0: 128 x 128, 1: 256 x 128, 2: 256 x 256
   int64_t bm, gx, bands;  // band height, column blocks, row bands
 };
+const char *w8a8_b128_suffix(int form) { return form == 2 ? "_t256" : form == 1 ? "_t256x128" : ""; }
 bool w8a8_b128_tiles(bool gate_up, int64_t n, int64_t k, int32_t max_tokens, W8a8B128 *out) {
   if (n <= 0 || k <= 0 || n % 128 != 0 || k % 128 != 0 || max_tokens <= 0) return false;
   const int64_t cols256 = gate_up ? 128 : 256;
-  const int64_t tiles256 =
-      n % cols256 == 0 && k < (int64_t(1) << 24) ? (max_tokens + 255) / 256 * (n / cols256) : 0;
-  out->t256 = tiles256 >= kB128T256Tiles;
-  out->bm = out->t256 ? 256 : 128;
-  out->gx = out->t256 ? n / cols256 : n / (cols256 / 2);
+  const bool offsets32 = k < (int64_t(1) << 24);
+  const int64_t tiles256 = n % cols256 == 0 && offsets32 ? (max_tokens + 255) / 256 * (n / cols256) : 0;
+  out->form = tiles256 >= kB128T256Tiles ? 2 : offsets32 ? 1 : 0;
+  out->bm = out->form != 0 ? 256 : 128;
+  out->gx = out->form == 2 ? n / cols256 : n / (cols256 / 2);
   out->bands = (max_tokens + out->bm - 1) / out->bm;
   return (k / 128) * (out->bands * out->bm) < INT32_MAX;
 }
 
-// Block-scaled W8A8 GatedMlp in one launch: both GEMMs on one band height,
-// 256 x 256 tiles (_t256, 512 threads) where the gate/up launch of the
-// shape takes them and the hidden width is a multiple of 256, else 128 x 128.
-// out: the band height, the gate/up plus down column blocks and the bands.
+// Block-scaled W8A8 GatedMlp in one launch: both GEMMs on one tile form and
+// band height, 256 x 256 (_t256, 512 threads) where the gate/up launch of
+// the shape takes it and the hidden width is a multiple of 256, else 128 x
+// 128 (no 256 x 128 form here: kernels/projection.hip, B128Form). (Llama-3-
+// 8B widths, one launch: 256 x 256 270.6 / 548.1 us against 288.9 / 659.3
+// on 128 x 128 at 512 / 2048 rows; 128 x 128 ahead at 128 rows.)
+// out: the form, band height, the gate/up plus down column blocks and the
+// bands.
 bool w8a8_b128_gated(int64_t hidden, int64_t inter, int32_t max_tokens, W8a8B128 *out) {
   int64_t bands = 0;
   W8a8B128 up;
@@ -391,9 +398,11 @@ bool w8a8_b128_gated(int64_t hidden, int64_t inter, int32_t max_tokens, W8a8B128
       !w8a8_b128_tiles(true, inter, hidden, max_tokens, &up)) {
     return false;
   }
-  out->t256 = up.t256 && hidden % 256 == 0 && inter < (int64_t(1) << 24);
-  out->bm = out->t256 ? 256 : 128;
-  out->gx = inter / (out->bm / 2) + hidden / out->bm;
+  const bool offsets32 = hidden < (int64_t(1) << 24) && inter < (int64_t(1) << 24);
+  out->form = up.form == 2 && hidden % 256 == 0 && offsets32 ? 2 : 0;
+  out->bm = out->form != 0 ? 256 : 128;
+  const int64_t bn = out->form == 2 ? 256 : 128;
+  out->gx = inter / (bn / 2) + hidden / bn;
   out->bands = (max_tokens + out->bm - 1) / out->bm;
   const int64_t cap = out->bands * out->bm;
   return (hidden / 128) * cap < INT32_MAX && (inter / 128) * cap < INT32_MAX;
@@ -713,10 +722,10 @@ int32_t lunaflux_fp8_gated_mlp_geometry(int32_t entry, int64_t hidden, int64_t i
     // tiles
     const int64_t blocks = 2 * kQuantBlocks + g.gx * g.bands;
     if (blocks > INT32_MAX) return LF_INVALID_ARGUMENT;
-    const int32_t values[7] = {static_cast<int32_t>(blocks), 1, 1, static_cast<int32_t>(2 * g.bm), 1, 1, 0};
+    const int32_t values[7] = {static_cast<int32_t>(blocks), 1, 1, g.form != 0 ? 512 : 256, 1, 1, 0};
     std::memcpy(dims, values, sizeof(values));
     std::memset(symbol, 0, LF_FP8_SYMBOL_BYTES);
-    std::snprintf(symbol, LF_FP8_SYMBOL_BYTES, "lf_fp8_w8a8_gated_mlp_b128%s", g.t256 ? "_t256" : "");
+    std::snprintf(symbol, LF_FP8_SYMBOL_BYTES, "lf_fp8_w8a8_gated_mlp_b128%s", w8a8_b128_suffix(g.form));
     return LF_OK;
   }
   if (entry == LF_FP8_ENTRY_W8A8_GATED_MLP) {
@@ -868,10 +877,10 @@ static int32_t launch_geometry(int32_t entry, int64_t n, int64_t k, int64_t nq, 
       if (blocks > INT32_MAX) return LF_INVALID_ARGUMENT;
       std::snprintf(buffer, sizeof(buffer), "lf_fp8_w8a8_%s_b128%s",
                     entry == LF_FP8_ENTRY_W8A8_QKV_B128 ? "qkv" : gate_up ? "gate_up" : "dense",
-                    t.t256 ? "_t256" : "");
+                    w8a8_b128_suffix(t.form));
       name = buffer;
       gx = static_cast<int32_t>(blocks);
-      bx = t.t256 ? 512 : 256;
+      bx = t.form != 0 ? 512 : 256;
       break;
     }
     case LF_FP8_ENTRY_W8A8_DENSE:

@@ -324,20 +324,15 @@ def test_block_scaled_geometry_and_workspace():
         fp8.launch_geometry(_abi.ENTRY_W8A16_DENSE_B128, 4096 + 64, 4096, 16)
     with pytest.raises(fp8.DeviceError):
         fp8.launch_geometry(_abi.ENTRY_W8A8_QKV_B128, 4096 + 2 * 1088, 4096, 256, qkv_split=(4096, 1088))
-    for entry, op, n, k, m in [(_abi.ENTRY_W8A8_DENSE_B128, "dense", 4096, 14336, 2048),
-                               (_abi.ENTRY_W8A8_QKV_B128, "qkv", 6144, 4096, 300),
-                               (_abi.ENTRY_W8A8_GATE_UP_B128, "gate_up", 14336, 4096, 1)]:
-        d, sym = fp8.launch_geometry(entry, n, k, m)
-        bands = -(-m // 128)
-        gx = n // 64 if op == "gate_up" else n // 128
-        assert sym == f"lf_fp8_w8a8_{op}_b128" and d.grid == (256 + gx * bands, 1, 1) and d.block == (256, 1, 1)
-        cap = 128 * bands
-        want = 256 + 128 * bands + al(cap * k) + al((k // 128) * cap * 4)
-        assert fp8.w8a8_workspace_bytes(entry, n, k, m) == want
-    # the 256 x 256 form from 192 such tiles on (256-row bands, 512
-    # threads), where the width is a multiple of its tile; its workspace
-    # holds cap = 256 x bands rows
+    # 256-row bands of 512 threads: the 256 x 256 form from 192 such tiles
+    # on, where the width is a multiple of its tile, else 256 x 128 (128
+    # columns; gate/up: 64 outputs); the 128 x 128 form (128-row bands, 256
+    # threads) only for K >= 2^24. The workspace holds cap = bands x height
+    # rows.
     for entry, op, n, k, m, t256 in [
+            (_abi.ENTRY_W8A8_DENSE_B128, "dense", 4096, 14336, 2048, False),
+            (_abi.ENTRY_W8A8_QKV_B128, "qkv", 6144, 4096, 300, False),
+            (_abi.ENTRY_W8A8_GATE_UP_B128, "gate_up", 14336, 4096, 1, False),
             (_abi.ENTRY_W8A8_DENSE_B128, "dense", 4096, 4096, 3072, True),
             (_abi.ENTRY_W8A8_DENSE_B128, "dense", 4096, 14336, 3000, True),
             (_abi.ENTRY_W8A8_DENSE_B128, "dense", 4096, 4096, 2816, False),
@@ -348,22 +343,28 @@ def test_block_scaled_geometry_and_workspace():
             (_abi.ENTRY_W8A8_GATE_UP_B128, "gate_up", 14336, 4096, 256, False),
             (_abi.ENTRY_W8A8_GATE_UP_B128, "gate_up", 1408, 4096, 8192, True)]:
         d, sym = fp8.launch_geometry(entry, n, k, m)
-        bm = 256 if t256 else 128
-        bands = -(-m // bm)
-        gx = n // (bm // 2) if op == "gate_up" else n // bm
-        assert sym == f"lf_fp8_w8a8_{op}_b128" + ("_t256" if t256 else ""), (n, k, m, sym)
-        assert d.grid == (256 + gx * bands, 1, 1) and d.block == (2 * bm, 1, 1)
-        cap = bm * bands
+        bands = -(-m // 256)
+        cols = 256 if t256 else 128
+        gx = n // (cols // 2) if op == "gate_up" else n // cols
+        assert sym == f"lf_fp8_w8a8_{op}_b128" + ("_t256" if t256 else "_t256x128"), (n, k, m, sym)
+        assert d.grid == (256 + gx * bands, 1, 1) and d.block == (512, 1, 1)
+        cap = 256 * bands
         want = 256 + 128 * bands + al(cap * k) + al((k // 128) * cap * 4)
         assert fp8.w8a8_workspace_bytes(entry, n, k, m) == want
+    k = 1 << 24  # 32-bit activation offsets no longer fit: 128 x 128 tiles
+    d, sym = fp8.launch_geometry(_abi.ENTRY_W8A8_DENSE_B128, 256, k, 100)
+    assert sym == "lf_fp8_w8a8_dense_b128" and d.grid == (256 + 2, 1, 1) and d.block == (256, 1, 1)
+    assert fp8.w8a8_workspace_bytes(_abi.ENTRY_W8A8_DENSE_B128, 256, k, 100) == (
+        256 + 128 + al(128 * k) + al((k // 128) * 128 * 4))
     d, sym = fp8.launch_geometry(_abi.ENTRY_W8A8_QKV_B128, 6144, 4096, 2048, qkv_split=(4096, 1024))
     assert sym == "lf_fp8_w8a8_qkv_b128_t256" and d.grid == (256 + 24 * 8, 1, 1)
     # block-scaled W8A8 GatedMlp: 128 x 128 tiles, or 256 x 256 ones (256-row
     # bands, 512 threads) where the gate/up launch takes them and the hidden
-    # width is a multiple of 256
+    # width is a multiple of 256 (no 256 x 128 form for it)
     e = _abi.ENTRY_W8A8_GATED_MLP_B128
-    for h, i, m, bm in [(4096, 14336, 2048, 256), (4096, 14336, 300, 256), (4096, 14336, 256, 128),
-                        (4096 + 128, 14336, 2048, 128), (512, 1024, 100, 128)]:
+    for h, i, m, bm in [(4096, 14336, 3072, 256), (4096, 14336, 2048, 256), (4096, 14336, 300, 256),
+                        (4096, 14336, 256, 128), (4096, 2048, 3072, 256), (4096 + 128, 14336, 8192, 128),
+                        (512, 1024, 100, 128)]:
         d, sym = fp8.gated_mlp_geometry(h, i, m, e)
         bands = -(-m // bm)
         cap = bm * bands

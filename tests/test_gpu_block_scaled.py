@@ -168,8 +168,9 @@ def test_block_scaled_w8a16(rt, op, m, max_tokens):
 def w8a8_quantized_rows(bound, m, k, max_tokens):
     """(codes [m, K], scales [m, K / 128]) from the one-launch workspace:
     sync area (256 + 128 bands bytes), codes [cap, K], scales [K / 128][cap],
-    with bands of 128 rows (256 on the _t256 form) and cap = bands x height."""
-    height = 256 if bound.steps[0].name.endswith("_t256") else 128
+    with bands of 128 rows (256 on the 256-row forms, _t256 and _t256x128)
+    and cap = bands x height."""
+    height = 256 if "_t256" in bound.steps[0].name else 128
     bands = -(-max_tokens // height)
     cap = height * bands
     at = 256 + 128 * bands
@@ -179,8 +180,8 @@ def w8a8_quantized_rows(bound, m, k, max_tokens):
 
 
 # (qkv and gate/up at 2048 rows, and every case from 512 rows of gate/up or
-# 3072 rows of o / down on, take the 256 x 256 form; the ragged and
-# single-band cases leave bands without live rows)
+# 3072 rows of o / down on, take the 256 x 256 form, the others the 256 x
+# 128 one; the ragged and single-band cases leave bands without live rows)
 T256 = {("qkv", 2048, 2048), ("gate_up", 2048, 2048), ("o", 4096, 4096), ("down", 3000, 3072),
         ("gate_up", 700, 1024), ("gate_up", 200, 1024), ("qkv", 1800, 2048)}
 
@@ -194,7 +195,8 @@ T256 = {("qkv", 2048, 2048), ("gate_up", 2048, 2048), ("o", 4096, 4096), ("down"
 def test_block_scaled_w8a8(rt, op, m, max_tokens):
     rng = np.random.default_rng(13000 + 7 * m + max_tokens + len(op))
     y, x, ws, bound = run_op(rt, rng, op, "w8a8", m, max_tokens, zero=m in (100, 700, 1800))
-    assert bound.steps[0].name.endswith("_t256") == ((op, m, max_tokens) in T256), bound.steps[0].name
+    form = "_t256" if (op, m, max_tokens) in T256 else "_t256x128"
+    assert bound.steps[0].name.endswith(form), bound.steps[0].name
     k = SHAPES[op][1]
     codes, scales = w8a8_quantized_rows(bound, m, k, max_tokens)
     q_ref, s_ref = o.quantize_rows(o.bf16_decode(x), group=128)
@@ -206,17 +208,17 @@ def test_block_scaled_w8a8(rt, op, m, max_tokens):
 
 @pytest.mark.parametrize("family,hidden,inter,m,max_tokens", [
     ("w8a8", 4096, 14336, 2048, 2048), ("w8a8", 512, 1024, 100, 256), ("w8a8", 4096, 14336, 300, 512),
+    ("w8a8", 4096, 2048, 3000, 3072),
     ("w8a16", 4096, 14336, 32, 32), ("w8a16", 512, 1024, 100, 128),
 ])
 def test_block_scaled_gated_mlp(rt, family, hidden, inter, m, max_tokens):
     """GatedMlp on block-scaled weights: W8A8 as one launch (four counted
     steps; both GEMMs on 256 x 256 tiles where the gate/up launch takes
-    them: the Llama-3-8B widths from 257 rows on) against the two
-    block-scaled launches it replaces, bit for bit where all of them run
-    the same tile form (a standalone launch takes 256 x 256 tiles from 192
-    of them on, the down projection later than gate/up; the chain is
-    otherwise checked against the oracle on its own h); W8A16 as those two
-    launches. The oracle checks stage by stage on the device's own bf16
+    them and the hidden width is a multiple of 256: the Llama-3-8B widths
+    from 257 rows on; else 128 x 128) against the two block-scaled launches
+    it replaces, bit for bit where all of them have 256-row bands (the
+    256 x 256 and 256 x 128 forms compute the same sums), else the chain
+    checked against the oracle on its own h; W8A16 as those two launches. The oracle checks stage by stage on the device's own bf16
     h (read from the workspace): gate/up, the h quantizer (W8A8: codes and
     scales of the group quantizer), then down."""
     rng = np.random.default_rng(14000 + m + hidden)
@@ -242,7 +244,7 @@ def test_block_scaled_gated_mlp(rt, family, hidden, inter, m, max_tokens):
         outs.append(ya.read(np.uint16, (max_tokens, hidden)))
         assert np.all(outs[-1][m:] == SENTINEL), "rows past M written"
     assert np.array_equal(outs[0], outs[2])
-    same_forms = all(st.name.endswith("_t256") == wide for st in two.steps)
+    same_forms = all(("_t256" in st.name) == wide for st in two.steps)
     if same_forms:
         assert np.array_equal(outs[0], outs[1])
     y = outs[0][:m]
@@ -357,7 +359,7 @@ def test_block_scaled_admission(rt):
 
 
 @pytest.mark.parametrize("n,max_tokens,m,symbol", [
-    (512, 256, 200, "lf_fp8_w8a8_dense_b128"), (4096, 3072, 3000, "lf_fp8_w8a8_dense_b128_t256"),
+    (512, 256, 200, "lf_fp8_w8a8_dense_b128_t256x128"), (4096, 3072, 3000, "lf_fp8_w8a8_dense_b128_t256"),
 ])
 def test_block_scaled_w8a8_sticky_error(rt, n, max_tokens, m, symbol):
     """The counted wait of the block-scaled one-launch entry (both tile
@@ -388,13 +390,13 @@ def test_block_scaled_w8a8_sticky_error(rt, n, max_tokens, m, symbol):
 
 
 def test_block_scaled_w8a8_gated_mlp_sticky_error(rt):
-    """The same for the block-scaled GatedMlp on 256 x 256 tiles (hidden 256,
-    intermediate 4096, 2048 rows): the x band counter preset far below its
+    """The same for the block-scaled GatedMlp on 256 x 256 tiles (hidden 4096,
+    intermediate 2048, 3072 rows): the x band counter preset far below its
     target runs the gate/up wait out, every later step's wait sees the error
     word, the binding raises and zero-fills the workspace, and the next
     launch gives the first launch's bits."""
     rng = np.random.default_rng(15200)
-    hidden, inter, max_tokens, m = 256, 4096, 2048, 2000
+    hidden, inter, max_tokens, m = 4096, 2048, 3072, 3000
     (qg, sg), (qu, su) = spread_weight(rng, inter, hidden), spread_weight(rng, inter, hidden)
     qd, sd = spread_weight(rng, hidden, inter)
     wg, wu, wd = upload(rt, qg, sg), upload(rt, qu, su), upload(rt, qd, sd)
@@ -414,3 +416,66 @@ def test_block_scaled_w8a8_gated_mlp_sticky_error(rt):
     assert not ws.read(np.uint8, (ws.byte_count,)).any(), "workspace not zero-filled"
     one.launch(rt.stream, synchronous=True)
     assert np.array_equal(ya.read(np.uint16, (max_tokens, hidden))[:m], want[:m])
+
+
+def al256(v):
+    return -(-v // 256) * 256
+
+
+def direct_b128(rt, symbol, operands, grid, block, ws_bytes):
+    """A one-launch bound by hand (the 128 x 128 forms, which the geometry
+    picks only for K >= 2^24): zero-filled workspace, error word at 0."""
+    from lunaflux_amd.device import KernelArguments, KernelLaunchDimensions
+    from lunaflux_amd.fp8 import BoundOperation, LaunchStep
+    ws = rt.context.allocate(ws_bytes)
+    ws.copy_from_host(np.zeros(ws_bytes, np.uint8))
+    dims = KernelLaunchDimensions.new((grid, 1, 1), (block, 1, 1), 0)
+    step = LaunchStep(rt.function(symbol), dims, KernelArguments(operands + [_region(ws, alignment=256)]), symbol)
+    return BoundOperation([step], workspace=ws, error_offset=_abi.LF_FP8_AQ_ERROR_OFFSET)
+
+
+@pytest.mark.parametrize("op,m,max_tokens", [("o", 300, 384), ("qkv", 129, 256), ("gate_up", 100, 128)])
+def test_block_scaled_w8a8_t128_fallback(rt, op, m, max_tokens):
+    """The 128 x 128 block-scaled entries (lf_fp8_w8a8_{op}_b128, the
+    geometry's form for K >= 2^24), launched with the grid and workspace the
+    geometry would give them (256 quantizer blocks, then column blocks x
+    128-row bands; sync area of one step, codes [cap, K], scales [K / 128]
+    [cap]): codes and scales bit-exact, outputs against the oracle, rows
+    past M untouched, a second launch bit-identical."""
+    from lunaflux_amd.fp8 import COUNTS_BYTES
+    rng = np.random.default_rng(16000 + m + len(op))
+    n, k = SHAPES[op]
+    x = spread_activations(rng, m, k, zero_groups=True)
+    xa = rt.context.upload(np.concatenate([x, np.zeros((max_tokens - m, k), np.uint16)]))
+    ya = rt.context.allocate(max_tokens * n * 2)
+    ya.copy_from_host(np.full(max_tokens * n, SENTINEL, np.uint16))
+    counts = rt.step_counts(m)
+    c = _region(counts, COUNTS_BYTES, alignment=4)
+    if op == "qkv":
+        ws = [spread_weight(rng, nn, k, zero_block=True) for nn in (4096, 1024, 1024)]
+        regions = [upload(rt, q, s).region for q, s in ws]
+        symbol, gx = "lf_fp8_w8a8_qkv_b128", n // 128
+    elif op == "gate_up":
+        ws = [spread_weight(rng, n, k) for _ in range(2)]
+        regions = [upload(rt, q, s).region for q, s in ws]
+        symbol, gx = "lf_fp8_w8a8_gate_up_b128", n // 64
+    else:
+        ws = [spread_weight(rng, n, k)]
+        regions = [upload(rt, *ws[0]).region]
+        symbol, gx = "lf_fp8_w8a8_dense_b128", n // 128
+    bands = -(-max_tokens // 128)
+    cap = 128 * bands
+    ws_bytes = 256 + 128 * bands + al256(cap * k) + al256((k // 128) * cap * 4)
+    bound = direct_b128(rt, symbol, [c, _region(xa, alignment=256), *regions, _region(ya, alignment=256)],
+                        256 + gx * bands, 256, ws_bytes)
+    bound.launch(rt.stream, synchronous=True)
+    y = ya.read(np.uint16, (max_tokens, n))
+    assert np.all(y[m:] == SENTINEL), "rows past M written"
+    bound.launch(rt.stream, synchronous=True)
+    assert np.array_equal(ya.read(np.uint16, (max_tokens, n)), y)
+    codes, scales = w8a8_quantized_rows(bound, m, k, max_tokens)
+    q_ref, s_ref = o.quantize_rows(o.bf16_decode(x), group=128)
+    np.testing.assert_array_equal(codes, q_ref)
+    np.testing.assert_array_equal(scales, s_ref.reshape(m, -1))
+    rows, cols = sample(rng, m, n, 48, 256)
+    check_op(op, "w8a8", y[:m], x, ws, rows, cols, f"b128 t128 w8a8 {op} m={m}/{max_tokens}")
