@@ -479,3 +479,36 @@ def test_block_scaled_w8a8_t128_fallback(rt, op, m, max_tokens):
     np.testing.assert_array_equal(scales, s_ref.reshape(m, -1))
     rows, cols = sample(rng, m, n, 48, 256)
     check_op(op, "w8a8", y[:m], x, ws, rows, cols, f"b128 t128 w8a8 {op} m={m}/{max_tokens}")
+
+
+@pytest.mark.parametrize("op,m,max_tokens", [("o", 2000, 2048), ("gate_up", 200, 256), ("qkv", 1000, 1024),
+                                             ("down", 500, 512)])
+def test_block_scaled_w8a8_256x128_matches_256x256(rt, op, m, max_tokens):
+    """The 256 x 128 entries (which the geometry binds here) against the
+    256 x 256 entry of the same operation launched by hand on the same
+    inputs: both run the same per-element sums (the same k-tile rescales and
+    MFMA order), so the former's launches (two on one workspace, one on a
+    fresh one) must all give the latter's bits."""
+    from lunaflux_amd.fp8 import COUNTS_BYTES
+    rng = np.random.default_rng(17000 + m)
+    y, x, ws, bound = run_op(rt, rng, op, "w8a8", m, max_tokens)
+    assert bound.steps[0].name.endswith("_t256x128"), bound.steps[0].name
+    n, k = SHAPES[op]
+    xa = rt.context.upload(np.concatenate([x, np.zeros((max_tokens - m, k), np.uint16)]))
+    ya = rt.context.allocate(max_tokens * n * 2)
+    c = _region(rt.step_counts(m), COUNTS_BYTES, alignment=4)
+    regions = [upload(rt, q, s).region for q, s in ws]
+    bands = -(-max_tokens // 256)
+    cap = 256 * bands
+    gx = n // 128 if op == "gate_up" else n // 256
+    symbol = "lf_fp8_w8a8_%s_b128_t256" % ("dense" if op in ("o", "down") else op)
+    ws_bytes = 256 + 128 * bands + al256(cap * k) + al256((k // 128) * cap * 4)
+    wide = direct_b128(rt, symbol, [c, _region(xa, alignment=256), *regions, _region(ya, alignment=256)],
+                       256 + gx * bands, 512, ws_bytes)
+    wide.launch(rt.stream, synchronous=True)
+    want = ya.read(np.uint16, (max_tokens, n))[:m]
+    assert np.array_equal(y, want)
+    # (run_op launched twice on its workspace and compared; a fresh bind on
+    # the same inputs)
+    y2 = run_op(rt, np.random.default_rng(17000 + m), op, "w8a8", m, max_tokens)[0]
+    assert np.array_equal(y2, want)
