@@ -587,7 +587,7 @@ extern "C" {
     w16g::w8a16_gemm_kernel<BN, WGM, WGN, NSA, NSB, 2>(smem, counts, x, wg, wu, wu, h, ws);       \
   }
 
-LF_W16_GEMM_ENTRIES(64, 4, 2, 4, 2)
+LF_W16_GEMM_ENTRIES(64, 4, 2, 3, 4)
 LF_W16_GEMM_ENTRIES(128, 2, 4, 2, 4)
 
 // The same over weights with 128 x 128 block scales:
@@ -613,7 +613,7 @@ LF_W16_GEMM_ENTRIES(128, 2, 4, 2, 4)
                                                                             ws);                 \
   }
 
-LF_W16_GEMM_B128_ENTRIES(64, 4, 2, 4, 2)
+LF_W16_GEMM_B128_ENTRIES(64, 4, 2, 3, 4)
 LF_W16_GEMM_B128_ENTRIES(128, 2, 4, 2, 4)
 
 // One-launch GatedMlp for profiles of 65..128 rows, any H and I the forms
@@ -628,7 +628,7 @@ LF_W16_GEMM_B128_ENTRIES(128, 2, 4, 2, 4)
   }
 
 LF_W16_GEMM_GATED_MLP(128, 2, 4, 2, 4)
-LF_W16_GEMM_GATED_MLP(64, 4, 2, 4, 2)
+LF_W16_GEMM_GATED_MLP(64, 3, 4, 4, 2)
 
 // The same over weights with 128 x 128 block scales.
 #define LF_W16_GEMM_GATED_MLP_B128(DN_BN, DN_NSA, DN_NSB, WGM, WGN)                              \
@@ -639,6 +639,6 @@ LF_W16_GEMM_GATED_MLP(64, 4, 2, 4, 2)
   }
 
 LF_W16_GEMM_GATED_MLP_B128(128, 2, 4, 2, 4)
-LF_W16_GEMM_GATED_MLP_B128(64, 4, 2, 4, 2)
+LF_W16_GEMM_GATED_MLP_B128(64, 3, 4, 4, 2)
 
 }  // extern "C"

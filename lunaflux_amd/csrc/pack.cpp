@@ -201,14 +201,18 @@ void w8a16_fixed_geometry(const W8a16Fixed &f, int64_t n, int32_t *gx, int32_t *
 // Profiles of 65..128 rows: the LDS-tiled GEMM (kernels/w8a16_gemm.hip,
 // "lf_fp8_w8a16_{op}_m128_n{BN}"), any K, any N its blocks divide. A block
 // (8 waves) computes 128 rows x BN weight columns (gate/up: BN / 2 gate and
-// BN / 2 up columns) over one of S K-slices. BN 128 with the fewest slices
-// that give >= 192 blocks, if each slice keeps >= 8 k-tiles; else BN 64 the
-// same way; else BN 64 with slices of 8 k-tiles. Measured at M = 128 on the
-// Llama-3-8B shapes (MI355X, >= 512 MB of weight copies rotated so the MALL
-// serves none), against the column-group entries this form replaced:
-// gate/up 48.4 -> 44.8 us (BN 128, S 1), QKV 24.2 -> 21.3 (128, 4), o
-// 21.0 -> 17.8 (64, 3), down 38.6 -> 32.5 (128, 6). Vocabulary-wide dense
-// shapes with a column-group entry keep it.
+// BN / 2 up columns) over one of S K-slices. Among BN 64 and 128 and the
+// splits that keep >= 8 k-tiles per slice, the most blocks up to one per CU
+// (256), the smaller split on a tie (at equal blocks BN 64 has half the
+// slices, so half the partials); with no such choice (more than 256 column
+// blocks even unsplit) BN 128 unsplit. Measured at M = 128 on the
+// Llama-3-8B shapes (MI355X, 24 weight copies rotated so the MALL serves
+// none), each call under several geometries on one box: QKV (64, 2)
+// 18.4-19.2 us against (128, 4) 19.9-21.5, down (64, 4) 28.9-31.0 against
+// (128, 6) 31.3-34.2 and (64, 3) 33.6-36.6, o (64, 4) 14.3-14.9 against
+// (64, 3) 14.4-15.2, gate/up (128, 1) 38.6-40.2 against (64, 1) 55.7-59.5
+// (448 blocks). Vocabulary-wide dense shapes with a column-group entry keep
+// it.
 struct W8a16Gemm {
   int bn;
   int64_t blocks_n, split;
@@ -220,21 +224,30 @@ bool w8a16_gemm(int32_t entry, int64_t n, int64_t k, int32_t max_tokens, W8a16Ge
     return false;
   }
   const int64_t kt = k / 128;
-  constexpr int64_t kMinBlocks = 192, kMinSliceTiles = 8;
-  for (const int bn : {128, 64}) {
+  constexpr int64_t kMaxBlocks = 256, kMinSliceTiles = 8;
+  const int64_t max_split = std::max<int64_t>(1, kt / kMinSliceTiles);
+  W8a16Gemm best{0, 0, 0};
+  for (const int bn : {64, 128}) {
     const int64_t per = entry == LF_FP8_ENTRY_W8A16_GATE_UP ? bn / 2 : bn;
     if (n % per != 0) continue;
     const int64_t blocks = n / per;
-    const int64_t split = std::max<int64_t>(1, (kMinBlocks + blocks - 1) / blocks);
-    if (split <= kt && kt / split >= kMinSliceTiles) {
-      *out = W8a16Gemm{bn, blocks, split};
-      return blocks * split <= INT32_MAX;
-    }
+    const int64_t split = std::min(max_split, std::max<int64_t>(1, kMaxBlocks / blocks));
+    if (blocks * split > kMaxBlocks) continue;
+    // BN 64 first: it keeps a tie (the same block count at half the split)
+    if (blocks * split > best.blocks_n * best.split) best = W8a16Gemm{bn, blocks, split};
   }
-  const int64_t per = entry == LF_FP8_ENTRY_W8A16_GATE_UP ? 32 : 64;
-  if (n % per != 0) return false;
-  *out = W8a16Gemm{64, n / per, std::max<int64_t>(1, kt / kMinSliceTiles)};
-  return out->blocks_n * out->split <= INT32_MAX;
+  if (best.bn == 0) {
+    for (const int bn : {128, 64}) {
+      const int64_t per = entry == LF_FP8_ENTRY_W8A16_GATE_UP ? bn / 2 : bn;
+      if (n % per == 0) {
+        best = W8a16Gemm{bn, n / per, 1};
+        break;
+      }
+    }
+    if (best.bn == 0) return false;
+  }
+  *out = best;
+  return best.blocks_n * best.split <= INT32_MAX;
 }
 
 // One-launch GatedMlp entries (kernels/w8a16.hip, LF_W16_GATED_MLP): the

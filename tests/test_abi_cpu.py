@@ -125,7 +125,7 @@ def test_launch_geometry():
     assert fp8.w8a16_workspace_bytes(_abi.ENTRY_W8A16_DENSE, 4096, 2048, 32) == 8 * 256 * 2 * 1024 + 256
     assert fp8.w8a16_workspace_bytes(_abi.ENTRY_W8A16_QKV, 6144, 4096, 1) == 256
     assert fp8.w8a16_workspace_bytes(_abi.ENTRY_W8A16_GATE_UP, 14336, 2048, 32) == 2 * 896 * 2 * 2 * 1024 + 1024
-    assert fp8.w8a16_workspace_bytes(_abi.ENTRY_W8A16_QKV, 6144, 4096, 128) == 4 * 48 * 8 * 8 * 1024 + 256
+    assert fp8.w8a16_workspace_bytes(_abi.ENTRY_W8A16_QKV, 6144, 4096, 128) == 2 * 96 * 8 * 4 * 1024 + 512
     # Shape-specialized (Llama-3-8B) entries for profiles of <= 32 rows.
     dims, sym = fp8.launch_geometry(_abi.ENTRY_W8A16_DENSE, 4096, 14336, 32)
     assert sym == "lf_fp8_w8a16_dense_k14336_m32" and dims.grid == (64 * 4, 1, 1)
@@ -156,18 +156,24 @@ def test_launch_geometry():
     dims, sym = fp8.launch_geometry(_abi.ENTRY_W8A16_DENSE, 4096, 4096, 64)
     assert sym == "lf_fp8_w8a16_dense_m64"
     # 65..128 rows: the LDS-tiled GEMM, 128 x BN tiles (gate/up blocks cover
-    # BN / 2 h-columns): BN 128 with the fewest K slices giving >= 192
-    # blocks if each slice keeps >= 8 k-tiles, else BN 64 the same way, else
-    # BN 64 with 8-k-tile slices
+    # BN / 2 h-columns): among BN 64 / 128 and the splits keeping >= 8
+    # k-tiles per slice, the most blocks up to 256, the smaller split on a
+    # tie; with more than 256 column blocks unsplit, BN 128 unsplit
     dims, sym = fp8.launch_geometry(_abi.ENTRY_W8A16_DENSE, 4096, 4096, 128)
-    assert sym == "lf_fp8_w8a16_dense_m128_n64" and dims.grid == (64 * 3, 1, 1)
+    assert sym == "lf_fp8_w8a16_dense_m128_n64" and dims.grid == (64 * 4, 1, 1)
     assert dims.block == (512, 1, 1)
     # S x blocks x 8 waves x (2 x BN / 32) 1 KiB fragments + a counter per block
-    assert fp8.w8a16_workspace_bytes(_abi.ENTRY_W8A16_DENSE, 4096, 4096, 128) == 3 * 64 * 8 * 4 * 1024 + 256
+    assert fp8.w8a16_workspace_bytes(_abi.ENTRY_W8A16_DENSE, 4096, 4096, 128) == 4 * 64 * 8 * 4 * 1024 + 256
     dims, sym = fp8.launch_geometry(_abi.ENTRY_W8A16_DENSE, 4096, 14336, 100)
-    assert sym == "lf_fp8_w8a16_dense_m128_n128" and dims.grid == (32 * 6, 1, 1)
+    assert sym == "lf_fp8_w8a16_dense_m128_n64" and dims.grid == (64 * 4, 1, 1)
     dims, sym = fp8.launch_geometry(_abi.ENTRY_W8A16_QKV, 6144, 4096, 128, qkv_split=(4096, 1024))
-    assert sym == "lf_fp8_w8a16_qkv_m128_n128" and dims.grid == (48 * 4, 1, 1)
+    assert sym == "lf_fp8_w8a16_qkv_m128_n64" and dims.grid == (96 * 2, 1, 1)
+    # (a tie: BN 128 x 2 slices and BN 64 unsplit both give 256 blocks)
+    dims, sym = fp8.launch_geometry(_abi.ENTRY_W8A16_GATE_UP, 8192, 2048, 128)
+    assert sym == "lf_fp8_w8a16_gate_up_m128_n64" and dims.grid == (256, 1, 1)
+    # more than 256 column blocks even unsplit: BN 128, no split
+    dims, sym = fp8.launch_geometry(_abi.ENTRY_W8A16_DENSE, 40960, 1024, 128)
+    assert sym == "lf_fp8_w8a16_dense_m128_n128" and dims.grid == (320, 1, 1)
     dims, sym = fp8.launch_geometry(_abi.ENTRY_W8A16_GATE_UP, 14336, 4096, 128)
     assert sym == "lf_fp8_w8a16_gate_up_m128_n128" and dims.grid == (224, 1, 1)
     dims, sym = fp8.launch_geometry(_abi.ENTRY_W8A16_DENSE, 4096, 2048, 65)
@@ -423,11 +429,11 @@ def test_w8a16_gated_mlp_geometry():
     assert s == "lf_fp8_w8a16_gated_mlp_h4096_i14336_m32" and d.grid == (224 + 256, 1, 1)
     d, s = fp8.gated_mlp_geometry(4096, 14336, 128)
     dn_dims, dn_sym = fp8.launch_geometry(_abi.ENTRY_W8A16_DENSE, 4096, 14336, 128)
-    assert dn_sym == "lf_fp8_w8a16_dense_m128_n128"
-    assert s == "lf_fp8_w8a16_gated_mlp_m128_n128_n128" and d.grid == (224 + dn_dims.grid[0], 1, 1)
+    assert dn_sym == "lf_fp8_w8a16_dense_m128_n64"
+    assert s == "lf_fp8_w8a16_gated_mlp_m128_n128_n64" and d.grid == (224 + dn_dims.grid[0], 1, 1)
     assert d.block == (512, 1, 1)
     ws = lib.lunaflux_fp8_gated_mlp_workspace_bytes(e, 4096, 14336, 128)
-    split = dn_dims.grid[0] // (4096 // 128)
+    split = dn_dims.grid[0] // (4096 // 64)
     assert ws == (128 * 14336 * 2 + fp8.w8a16_workspace_bytes(_abi.ENTRY_W8A16_DENSE, 4096, 14336, 128)
                   + 128 * split + 256)       # one 128-byte line per slice counter, done, error
     assert (lib.lunaflux_fp8_gated_mlp_workspace_bytes(e, 4096, 14336, 32)

@@ -272,8 +272,9 @@ def test_w8a16_gated_mlp_sticky_error_and_timeout(rt, max_tokens, m):
     if max_tokens == 32:
         sync = 768
     else:
-        dn_dims, _ = fp8.launch_geometry(_abi.ENTRY_W8A16_DENSE, hidden, inter, max_tokens)
-        sync = 128 * (dn_dims.grid[0] // (hidden // 128)) + 256
+        dn_dims, dn_sym = fp8.launch_geometry(_abi.ENTRY_W8A16_DENSE, hidden, inter, max_tokens)
+        bn = int(dn_sym.rsplit("_n", 1)[1])  # the down GEMM's block width
+        sync = 128 * (dn_dims.grid[0] // (hidden // bn)) + 256
     ws.copy_from_host(np.array([-(1 << 30)], np.int32), offset=ws.byte_count - sync)
     with pytest.raises(DeviceError):
         one.launch(rt.stream, synchronous=True)

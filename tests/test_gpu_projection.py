@@ -461,7 +461,9 @@ def test_w8a16_specialized_entries(rt, op, m, max_tokens):
     ("dense", 24576, 1024, None, 128, 128),     # BN 128 (192 blocks), no split
     ("dense", 1024, 8192, None, 100, 128),      # BN 64, 16 blocks, S 8
     ("qkv", 3072, 4096, (2048, 512), 77, 128),  # BN 64, S 4; blocks straddle Q|K|V
-    ("gate_up", 8192, 2048, None, 128, 128),    # BN 128, S 2 (256 blocks)
+    ("gate_up", 8192, 2048, None, 128, 128),    # BN 64 unsplit (256 blocks; ties BN 128 x 2)
+    ("gate_up", 4096, 4096, None, 100, 128),    # BN 64, S 2 (256 blocks)
+    ("dense", 40960, 1024, None, 128, 128),     # BN 128 unsplit, 320 blocks (> 256 either way)
     ("gate_up", 12288, 4096, None, 90, 96),     # BN 128 (192 blocks)
 ])
 def test_w8a16_gemm_form(rt, op, n, k, qkv_split, m, max_tokens):

@@ -3,7 +3,9 @@ the shape-specialized column-group entries of the Llama-3-8B decode layer
 (down K = 14336 and QKV at 32 rows, four slices), the generic column-group
 form (eight slices, the last block loading seven partials in two batches;
 gate/up with sixteen, two weights per tile), and the 128-row GEMM form
-(three and six slices). Every block stores its partial tile and counts
+(four slices at BN 64, and six at BN 128: a width the launch geometry no
+longer splits, launched directly, as a caller of the entry may). Every
+block stores its partial tile and counts
 itself; the last to arrive sums the S partials in slice order and resets
 the counter. So every launch must match the oracle, be bit-identical to the
 launch before it on the same workspace (the counters back at zero), and
@@ -39,7 +41,8 @@ CASES = [
     ("qkv", 6144, 4096, 32, 27, "lf_fp8_w8a16_qkv_k4096_q4096_kv1024_m32", 4),
     ("dense", 4096, 2048, 32, 17, "lf_fp8_w8a16_dense_m32", 8),
     ("gate_up", 1024, 2048, 32, 30, "lf_fp8_w8a16_gate_up_m32", 16),
-    ("dense", 4096, 4096, 128, 128, "lf_fp8_w8a16_dense_m128_n64", 3),
+    ("dense", 4096, 4096, 128, 128, "lf_fp8_w8a16_dense_m128_n64", 4),
+    ("dense", 4096, 14336, 128, 77, "lf_fp8_w8a16_dense_m128_n64", 4),
     ("dense", 4096, 14336, 128, 77, "lf_fp8_w8a16_dense_m128_n128", 6),
 ]
 
@@ -63,9 +66,24 @@ def test_split_k_exchange(rt, op, n, k, max_tokens, m, symbol, slices):
         bound = rt.bind_dense("w8a16", counts, xr_, ws[0][2], yr_, max_tokens)
         wr = o.dequantize(ws[0][0], ws[0][1])
     step = bound.steps[0]
+    blocks_n = {"lf_fp8_w8a16_dense_m128_n64": n // 64, "lf_fp8_w8a16_dense_m128_n128": n // 128}
+    if step.name != symbol and symbol in blocks_n:
+        # the entry launched directly with `slices` K-slices, on a workspace
+        # of its size: S x blocks x 8 waves x (2 BN / 32) 1 KiB fragments,
+        # then a counter per column block
+        from lunaflux_amd.device import KernelArguments, KernelLaunchDimensions
+        from lunaflux_amd.fp8 import BoundOperation, LaunchStep
+        bn, cb = int(symbol.rsplit("_n", 1)[1]), blocks_n[symbol]
+        al = lambda v: -(-v // 256) * 256
+        nbytes = al(slices * cb * 8 * 2 * (bn // 32) * 1024) + al(cb * 4)
+        wsd = rt.context.allocate(nbytes)
+        wsd.copy_from_host(np.zeros(nbytes, np.uint8))
+        dims = KernelLaunchDimensions.new((cb * slices, 1, 1), (512, 1, 1), 0)
+        args = KernelArguments(step.args.arguments[:-1] + [_region(wsd, alignment=256)])
+        bound = BoundOperation([LaunchStep(rt.function(symbol), dims, args, symbol)], workspace=wsd)
+        step = bound.steps[0]
     assert len(bound.steps) == 1 and step.name == symbol, step.name
     # the grid is column blocks x slices
-    blocks_n = {"lf_fp8_w8a16_dense_m128_n64": n // 64, "lf_fp8_w8a16_dense_m128_n128": n // 128}
     per_block = 16 * (8 if op == "qkv" else 4) if symbol not in blocks_n else None
     cols = blocks_n.get(symbol) or -(-(n // 16) // (per_block // 16))
     assert step.dims.grid[0] == cols * slices, step.dims.grid
