@@ -204,20 +204,25 @@ void w8a16_fixed_geometry(const W8a16Fixed &f, int64_t n, int32_t *gx, int32_t *
 // BN / 2 up columns) over one of S K-slices. Among BN 64 and 128 and the
 // splits that keep >= 8 k-tiles per slice, the most blocks up to one per CU
 // (256), the smaller split on a tie (at equal blocks BN 64 has half the
-// slices, so half the partials); with no such choice (more than 256 column
+// slices, so half the partials; over 128 x 128 block-scaled weights BN 128
+// on a tie, see below); with no such choice (more than 256 column
 // blocks even unsplit) BN 128 unsplit. Measured at M = 128 on the
 // Llama-3-8B shapes (MI355X, 24 weight copies rotated so the MALL serves
 // none), each call under several geometries on one box: QKV (64, 2)
 // 18.4-19.2 us against (128, 4) 19.9-21.5, down (64, 4) 28.9-31.0 against
 // (128, 6) 31.3-34.2 and (64, 3) 33.6-36.6, o (64, 4) 14.3-14.9 against
 // (64, 3) 14.4-15.2, gate/up (128, 1) 38.6-40.2 against (64, 1) 55.7-59.5
-// (448 blocks). Vocabulary-wide dense shapes with a column-group entry keep
-// it.
+// (448 blocks). Block-scaled weights (block = true; the per-k-step scale
+// fold) measured the other way at equal blocks, layer loop A/B: QKV
+// (128, 4) 21.1-21.3 us against (64, 2) 23.3-24.0, down (128, 6) 34.8-36.2
+// against (64, 4) 39.3-40.2, o (64, 4) 16.0-16.4 against (64, 3) 17.9-19.1.
+// Vocabulary-wide dense shapes with a column-group entry keep it.
 struct W8a16Gemm {
   int bn;
   int64_t blocks_n, split;
 };
-bool w8a16_gemm(int32_t entry, int64_t n, int64_t k, int32_t max_tokens, W8a16Gemm *out) {
+bool w8a16_gemm(int32_t entry, int64_t n, int64_t k, int32_t max_tokens, W8a16Gemm *out,
+                bool block = false) {
   if (max_tokens <= 64 || max_tokens > 128 || n <= 0 || k <= 0 || k % 128 != 0) return false;
   if (entry == LF_FP8_ENTRY_W8A16_DENSE && n >= kWideN &&
       w8a16_fixed(entry, n, k, 0, 0, max_tokens) != nullptr) {
@@ -227,13 +232,14 @@ bool w8a16_gemm(int32_t entry, int64_t n, int64_t k, int32_t max_tokens, W8a16Ge
   constexpr int64_t kMaxBlocks = 256, kMinSliceTiles = 8;
   const int64_t max_split = std::max<int64_t>(1, kt / kMinSliceTiles);
   W8a16Gemm best{0, 0, 0};
-  for (const int bn : {64, 128}) {
+  const int order[2] = {block ? 128 : 64, block ? 64 : 128};
+  for (const int bn : order) {
     const int64_t per = entry == LF_FP8_ENTRY_W8A16_GATE_UP ? bn / 2 : bn;
     if (n % per != 0) continue;
     const int64_t blocks = n / per;
     const int64_t split = std::min(max_split, std::max<int64_t>(1, kMaxBlocks / blocks));
     if (blocks * split > kMaxBlocks) continue;
-    // BN 64 first: it keeps a tie (the same block count at half the split)
+    // the first width keeps a tie
     if (blocks * split > best.blocks_n * best.split) best = W8a16Gemm{bn, blocks, split};
   }
   if (best.bn == 0) {
@@ -463,8 +469,9 @@ struct W8a16GatedGemm {
 bool w8a16_gated_gemm(int32_t entry, int64_t hidden, int64_t inter, int32_t max_tokens,
                       W8a16GatedGemm *out) {
   if (!w8a16_gated_entry(entry) || max_tokens <= 64 || max_tokens > 128) return false;
-  if (!w8a16_gemm(LF_FP8_ENTRY_W8A16_GATE_UP, inter, hidden, max_tokens, &out->gu) ||
-      !w8a16_gemm(LF_FP8_ENTRY_W8A16_DENSE, hidden, inter, max_tokens, &out->dn)) {
+  const bool block = entry == LF_FP8_ENTRY_W8A16_GATED_MLP_B128;
+  if (!w8a16_gemm(LF_FP8_ENTRY_W8A16_GATE_UP, inter, hidden, max_tokens, &out->gu, block) ||
+      !w8a16_gemm(LF_FP8_ENTRY_W8A16_DENSE, hidden, inter, max_tokens, &out->dn, block)) {
     return false;
   }
   return out->gu.bn == 128 && out->gu.split == 1;
@@ -628,7 +635,7 @@ static int64_t w8a16_workspace(int32_t entry, int64_t n, int64_t k, int64_t nq, 
       return -1;
     }
     W8a16Gemm gm;
-    if (w8a16_gemm(w8a16_channel_entry(entry), n, k, max_tokens, &gm)) return w8a16_gemm_workspace(gm);
+    if (w8a16_gemm(w8a16_channel_entry(entry), n, k, max_tokens, &gm, true)) return w8a16_gemm_workspace(gm);
     if (const W8a16Fixed *f = w8a16_fixed(entry, n, k, nq, nkv, max_tokens)) {
       return w8a16_fixed_workspace(*f, n);
     }
@@ -862,7 +869,7 @@ static int32_t launch_geometry(int32_t entry, int64_t n, int64_t k, int64_t nq, 
                        : entry == LF_FP8_ENTRY_W8A16_QKV_B128 ? "qkv"
                                                               : "gate_up";
       W8a16Gemm gm;
-      if (w8a16_gemm(w8a16_channel_entry(entry), n, k, max_tokens, &gm)) {
+      if (w8a16_gemm(w8a16_channel_entry(entry), n, k, max_tokens, &gm, true)) {
         std::snprintf(buffer, sizeof(buffer), "lf_fp8_w8a16_%s_b128_m128_n%d", op, gm.bn);
         name = buffer;
         gx = static_cast<int32_t>(gm.blocks_n * gm.split);

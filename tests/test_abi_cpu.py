@@ -280,8 +280,9 @@ def test_one_launch_w8a8_geometry_and_workspace():
 
 def test_block_scaled_geometry_and_workspace():
     """The _B128 entries. W8A16: profiles of 65..128 rows the LDS-tiled
-    GEMM form with the per-channel entry's tile, split and workspace (the
-    _b128_m128_n{BN} symbols); the column-group form for every other profile
+    GEMM form (the _b128_m128_n{BN} symbols) by the per-channel rule (the
+    most blocks up to 256, >= 8 k-tiles per slice) except that a tie goes to
+    BN 128 instead of BN 64; the column-group form for every other profile
     (also <= 16 rows), the per-channel split raised so that a slice holds at
     most 128 k-tiles, the per-channel workspace formula. W8A8: 256 group-
     quantizer blocks then 128 x 128 tiles (64 h-columns for gate/up), 256
@@ -294,12 +295,20 @@ def test_block_scaled_geometry_and_workspace():
                _abi.ENTRY_W8A16_GATE_UP_B128: _abi.ENTRY_W8A16_GATE_UP}
     for entry, op in [(_abi.ENTRY_W8A16_DENSE_B128, "dense"), (_abi.ENTRY_W8A16_QKV_B128, "qkv"),
                       (_abi.ENTRY_W8A16_GATE_UP_B128, "gate_up")]:
-        for n, k, m in [(4096, 14336, 128), (6144, 4096, 100), (4096, 4096, 65), (1024, 32768, 128)]:
-            d, sym = fp8.launch_geometry(entry, n, k, m)
-            d0, sym0 = fp8.launch_geometry(channel[entry], n, k, m)
-            assert sym0.startswith(f"lf_fp8_w8a16_{op}_m128_n"), sym0
-            assert sym == sym0.replace(f"_{op}_", f"_{op}_b128_") and d == d0, (sym, d, sym0, d0)
-            assert fp8.w8a16_workspace_bytes(entry, n, k, m) == fp8.w8a16_workspace_bytes(channel[entry], n, k, m)
+        # (BN, split) block-scaled / per-channel
+        gate_up = op == "gate_up"
+        for n, k, m, want_b, want_c in [
+                (4096, 14336, 128, (128, 4) if gate_up else (128, 8), (64, 2) if gate_up else (64, 4)),
+                (6144, 4096, 100, (128, 2) if gate_up else (128, 4), (64, 1) if gate_up else (64, 2)),
+                (4096, 4096, 65, (128, 4) if gate_up else (64, 4), (64, 2) if gate_up else (64, 4)),
+                (1024, 32768, 128, (128, 16) if gate_up else (128, 32), (64, 8) if gate_up else (64, 16))]:
+            for e, sub, (bn, split) in ((entry, "_b128", want_b), (channel[entry], "", want_c)):
+                d, sym = fp8.launch_geometry(e, n, k, m)
+                blocks = n // (bn // 2 if gate_up else bn)
+                assert sym == f"lf_fp8_w8a16_{op}{sub}_m128_n{bn}" and d.grid == (blocks * split, 1, 1), (sym, d)
+                assert d.block == (512, 1, 1)
+                want = 256 if split == 1 else al(split * blocks * 8 * 2 * (bn // 32) * 1024) + al(blocks * 4)
+                assert fp8.w8a16_workspace_bytes(e, n, k, m) == want, (sym, split)
         # the Llama-3-8B shape-specialized forms at <= 32 rows: the per-channel
         # entry's geometry and workspace under the _b128 symbol
         for n, k, m, split in [(4096, 4096, 1, None), (4096, 4096, 32, None), (4096, 14336, 16, None),
@@ -380,16 +389,27 @@ def test_block_scaled_geometry_and_workspace():
                 + al(cap * i) + al(i // 128 * cap * 4))
         assert lib.lunaflux_fp8_gated_mlp_workspace_bytes(e, h, i, m) == want
     assert lib.lunaflux_fp8_gated_mlp_workspace_bytes(e, 4096 + 64, 14336, 2048) == -1
-    # W8A16 GatedMlp in one launch on block-scaled weights: the per-channel
-    # one-launch forms' geometry and workspace under the _b128 symbols; none
-    # at 33..64 rows or at widths without a form (two launches there)
+    # W8A16 GatedMlp in one launch on block-scaled weights: at <= 32 rows the
+    # per-channel one-launch forms' geometry and workspace under the _b128
+    # symbols; at 65..128 rows the down part takes the block-scaled tie rule
+    # (BN 128 x 8 slices where per-channel takes BN 64 x 4, both 256
+    # blocks); none at 33..64 rows or at widths without a form
     e, e0 = _abi.ENTRY_W8A16_GATED_MLP_B128, _abi.ENTRY_W8A16_GATED_MLP
-    for h, i, m in [(4096, 14336, 1), (4096, 14336, 32), (4096, 14336, 128), (4096, 14336, 100)]:
+    for h, i, m in [(4096, 14336, 1), (4096, 14336, 32)]:
         d, sym = fp8.gated_mlp_geometry(h, i, m, e)
         d0, sym0 = fp8.gated_mlp_geometry(h, i, m, e0)
         assert sym == sym0.replace("gated_mlp_", "gated_mlp_b128_") and d == d0, (sym, sym0)
         assert (lib.lunaflux_fp8_gated_mlp_workspace_bytes(e, h, i, m)
                 == lib.lunaflux_fp8_gated_mlp_workspace_bytes(e0, h, i, m))
+    for h, i, m in [(4096, 14336, 128), (4096, 14336, 100)]:
+        d, sym = fp8.gated_mlp_geometry(h, i, m, e)
+        d0, sym0 = fp8.gated_mlp_geometry(h, i, m, e0)
+        assert sym == "lf_fp8_w8a16_gated_mlp_b128_m128_n128_n128" and d.grid == (224 + 256, 1, 1), sym
+        assert sym0 == "lf_fp8_w8a16_gated_mlp_m128_n128_n64" and d0.grid == (224 + 256, 1, 1), sym0
+        for ee, bn, split in ((e, 128, 8), (e0, 64, 4)):
+            blocks = h // bn
+            down = split * blocks * 8 * 2 * (bn // 32) * 1024 + al(blocks * 4)
+            assert lib.lunaflux_fp8_gated_mlp_workspace_bytes(ee, h, i, m) == 128 * i * 2 + down + 128 * split + 256
     assert fp8.gated_mlp_geometry(4096, 14336, 64, e) is None
     assert fp8.gated_mlp_geometry(2048, 5632, 32, e) is None
     assert fp8.gated_mlp_geometry(2048, 5632, 100, e) is None and fp8.gated_mlp_geometry(2048, 5632, 100, e0) is None
