@@ -186,7 +186,9 @@ enum lf_fp8_entry {
  * 128, every Q / K / V width of a QKV operation too.
  *  W8A16: lf_fp8_w8a16_{dense,qkv,gate_up}_b128_m{16,32,64,128} and, for
  *      profiles of 65..128 rows, lf_fp8_w8a16_{op}_b128_m128_n{64,128}
- *      (the per-channel entry's LDS-tiled GEMM geometry); operands and
+ *      (the per-channel entry's LDS-tiled GEMM geometry rule, except that
+ *      at equal block counts it takes BN 128 where the per-channel entry
+ *      takes BN 64); operands and
  *      workspace as the per-channel W8A16 entries
  *      (lunaflux_fp8_w8a16_workspace_bytes with the _B128 entry); each
  *      k-tile's products scaled by its block scale:
