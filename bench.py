@@ -615,10 +615,31 @@ def summarize_counters(paths):
     import csv
     vals, dur = {}, {}
     for path in paths:
-        for r in csv.DictReader(open(path)):
+        rows = list(csv.DictReader(open(path)))
+        # Decode kernels are launched three times back to back per call, and
+        # at 128 rows o and down run one kernel on one grid: their rows are
+        # told apart by the run of consecutive dispatches they belong to
+        # (run 2 = the second call of that kernel and grid). MoE kernels
+        # recur in every step of an operation and are pooled.
+        run_of, last, runs = {}, None, {}
+        order = sorted({int(r.get("Dispatch_Id") or 0) for r in rows})
+        first = {}
+        for r in rows:
+            first.setdefault(int(r.get("Dispatch_Id") or 0), r)
+        for d in order:
+            r = first[d]
             blocks = int(r.get("Grid_Size_X") or r.get("Grid_Size") or 0) // max(
                 int(r.get("Workgroup_Size_X") or r.get("Workgroup_Size") or 1), 1)
-            key = (r["Kernel_Name"], blocks)
+            k = (r["Kernel_Name"], blocks)
+            if k != last:
+                runs[k] = runs.get(k, 0) + 1
+            last = k
+            run_of[d] = runs[k] if r["Kernel_Name"].startswith("lf_fp8_w8a16") else 1
+        for r in rows:
+            blocks = int(r.get("Grid_Size_X") or r.get("Grid_Size") or 0) // max(
+                int(r.get("Workgroup_Size_X") or r.get("Workgroup_Size") or 1), 1)
+            run = run_of[int(r.get("Dispatch_Id") or 0)]
+            key = (r["Kernel_Name"], blocks if run == 1 else f"{blocks} (call {run})")
             if "Counter_Name" in r:
                 vals.setdefault(key, {}).setdefault(r["Counter_Name"], []).append(
                     float(r["Counter_Value"]))
@@ -641,7 +662,7 @@ def summarize_counters(paths):
            "",
            "| Kernel | Blocks | Duration us | HBM read MB | HBM write MB | MFMA busy | Clock GHz |",
            "|---|---|---|---|---|---|---|"]
-    for key in sorted(set(vals) | set(dur)):
+    for key in sorted(set(vals) | set(dur), key=lambda kk: (kk[0], str(kk[1]))):
         if key[0] == "lf_calibrate_copy":
             continue
         f, w = mean(key, "FETCH_SIZE"), mean(key, "WRITE_SIZE")
